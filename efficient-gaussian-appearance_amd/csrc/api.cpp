@@ -1,0 +1,622 @@
+// C ABI (include/efgs.h): rasterizer configuration, forward / backward orchestration, Adam.
+// Orchestration follows B/rasterization/src/forward.cu:11-246 and backward.cu:8-135 with this build's
+// stages: preprocess (hipRTC) -> per-block counts scan -> index-ordered compaction -> one host read of
+// (V, I) -> depth radix sort -> gathered scan of tile counts -> instance emission -> tile radix sort ->
+// tile ranges -> blend; backward: blend replay -> preprocess backward (per-instance gradient reduction).
+#include "../../include/efgs.h"
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+#include "rtc.h"
+
+namespace efgs {
+
+namespace {
+thread_local std::string t_error;
+}
+
+void set_error(const std::string& msg) { t_error = msg; }
+const char* error_message() { return t_error.c_str(); }
+
+}  // namespace efgs
+
+using namespace efgs;
+
+struct efgs_rasterizer {
+    bool appearance_set = false;
+    int model = 0;
+    int max_degree = 0;
+    int base_act = 0;
+    int res_act = 0;
+    int color_act = 0;
+    bool direction_gradient = false;
+    bool mlp_set = false;
+    int mlp_n_in = 0;
+    int mlp_n_in_padded = 0;
+    int mlp_n_neurons = 0;
+    int mlp_n_hidden = 0;
+    int mlp_n_frequencies = 0;
+    int mlp_sh_mask = 0;
+    int mlp_n_features = 0;
+    bool mlp_base_input = false;
+    uint32_t* host_counters = nullptr;  // pinned, 4 entries
+};
+
+namespace {
+
+constexpr size_t buffer_alignment = 256;
+
+struct Carver {
+    char* base;
+    size_t offset = 0;
+    template <typename T>
+    T* take(uint64_t count) {
+        offset = (offset + buffer_alignment - 1) & ~(buffer_alignment - 1);
+        T* p = base ? reinterpret_cast<T*>(base + offset) : nullptr;
+        offset += sizeof(T) * count;
+        return p;
+    }
+    void* take_bytes(size_t bytes) { return take<char>(bytes); }
+};
+
+struct PrimitiveLayout {
+    uint32_t* n_touched;
+    uint32_t* depth_keys;
+    PrimRecord* records;
+    uint32_t* prim_offset;
+    uint32_t* block_counts;
+    uint32_t* block_offsets;
+    uint32_t* counters;
+    uint32_t* keys_a;
+    uint32_t* vals_a;
+    uint32_t* keys_b;
+    uint32_t* vals_b;
+    uint32_t* offsets;
+    void* scan_scratch;
+    void* sort_scratch;
+    size_t bytes;
+
+    static PrimitiveLayout carve(char* base, uint64_t n) {
+        PrimitiveLayout l;
+        Carver c{base};
+        const uint64_t nn = n > 0 ? n : 1;
+        const uint32_t blocks = div_up(nn, preprocess_block);
+        l.n_touched = c.take<uint32_t>(nn);
+        l.depth_keys = c.take<uint32_t>(nn);
+        l.records = c.take<PrimRecord>(nn);
+        l.prim_offset = c.take<uint32_t>(nn);
+        l.block_counts = c.take<uint32_t>(2ull * blocks);
+        l.block_offsets = c.take<uint32_t>(2ull * blocks);
+        l.counters = c.take<uint32_t>(4);
+        l.keys_a = c.take<uint32_t>(nn);
+        l.vals_a = c.take<uint32_t>(nn);
+        l.keys_b = c.take<uint32_t>(nn);
+        l.vals_b = c.take<uint32_t>(nn);
+        l.offsets = c.take<uint32_t>(nn);
+        l.scan_scratch = c.take_bytes(scan_scratch_bytes(static_cast<uint32_t>(nn)));
+        l.sort_scratch = c.take_bytes(sort_scratch_bytes(static_cast<uint32_t>(nn)));
+        l.bytes = c.offset + buffer_alignment;
+        return l;
+    }
+};
+
+struct TileLayout {
+    uint2* ranges;
+    float* final_T;
+    uint32_t* n_contrib;
+    uint32_t* tile_max;
+    size_t bytes;
+
+    static TileLayout carve(char* base, uint32_t n_tiles) {
+        TileLayout l;
+        Carver c{base};
+        l.ranges = c.take<uint2>(n_tiles);
+        l.final_T = c.take<float>(static_cast<uint64_t>(n_tiles) * tile_pixels);
+        l.n_contrib = c.take<uint32_t>(static_cast<uint64_t>(n_tiles) * tile_pixels);
+        l.tile_max = c.take<uint32_t>(n_tiles);
+        l.bytes = c.offset + buffer_alignment;
+        return l;
+    }
+};
+
+struct InstanceLayout {
+    void* keys_a;
+    void* keys_b;
+    uint32_t* vals_a;
+    uint32_t* vals_b;
+    uint32_t* inst_prim;
+    void* sort_scratch;
+    size_t bytes;
+
+    static InstanceLayout carve(char* base, uint64_t n_instances, int key_bytes) {
+        InstanceLayout l;
+        Carver c{base};
+        const uint64_t ni = n_instances > 0 ? n_instances : 1;
+        l.keys_a = c.take_bytes(key_bytes * ni);
+        l.keys_b = c.take_bytes(key_bytes * ni);
+        l.vals_a = c.take<uint32_t>(ni);
+        l.vals_b = c.take<uint32_t>(ni);
+        l.inst_prim = c.take<uint32_t>(ni);
+        l.sort_scratch = c.take_bytes(sort_scratch_bytes(static_cast<uint32_t>(ni)));
+        l.bytes = c.offset + buffer_alignment;
+        return l;
+    }
+};
+
+int fail(int code, const std::string& msg) {
+    set_error(msg);
+    return code;
+}
+
+int end_bit_of(uint32_t max_key) {
+    int bits = 0;
+    while (bits < 32 && (max_key >> bits) != 0) bits++;
+    return bits;
+}
+
+const char* model_suffix(int model) {
+    switch (model) {
+        case 0: return "precomputed";
+        case 1: return "sh";
+        case 2: return "sv";
+        case 3: return "nasg";
+        case 4: return "nasgabor";
+        case 5: return "neural";
+    }
+    return "unknown";
+}
+
+int n_units_of(const efgs_rasterizer* r, int model) {
+    switch (model) {
+        case 1: return (r->max_degree + 1) * (r->max_degree + 1) - 1;
+        case 2:
+        case 3:
+        case 4: return r->max_degree;
+        case 5: return r->mlp_n_features;
+    }
+    return 0;
+}
+
+// preamble tokens and source files of the preprocess kernel `kind` ("forward" / "backward") for `model`
+void kernel_source(const efgs_rasterizer* r, int model, const char* kind, std::string& name, std::string& preamble,
+                   std::vector<std::string>& files) {
+    name = std::string("preprocess_") + kind + "_" + model_suffix(model);
+    const bool pre = model == 0;
+    preamble = "#define EFGS_KERNEL_NAME " + name + "\n";
+    preamble += "#define EFGS_MODEL " + std::to_string(model) + "\n";
+    preamble += "#define EFGS_BASE_ACT " + std::to_string(pre ? 0 : r->base_act) + "\n";
+    preamble += "#define EFGS_RES_ACT " + std::to_string(pre ? 0 : r->res_act) + "\n";
+    preamble += "#define EFGS_COLOR_ACT " + std::to_string(pre ? 0 : r->color_act) + "\n";
+    preamble += "#define EFGS_N_UNITS " + std::to_string(n_units_of(r, model)) + "u\n";
+    preamble += "#define EFGS_DIRECTION_GRADIENT " + std::string(!pre && r->direction_gradient ? "1" : "0") + "\n";
+    preamble += "#define EFGS_MLP_N_IN " + std::to_string(model == 5 ? r->mlp_n_in : 0) + "u\n";
+    preamble += "#define EFGS_MLP_N_IN_PADDED " + std::to_string(model == 5 ? r->mlp_n_in_padded : 0) + "u\n";
+    preamble += "#define EFGS_MLP_N_NEURONS " + std::to_string(model == 5 ? r->mlp_n_neurons : 0) + "u\n";
+    preamble += "#define EFGS_MLP_N_HIDDEN " + std::to_string(model == 5 ? r->mlp_n_hidden : 0) + "u\n";
+    preamble += "#define EFGS_N_FREQUENCIES " + std::to_string(model == 5 ? r->mlp_n_frequencies : 0) + "u\n";
+    preamble += "#define EFGS_SH_DEGREE_MASK " + std::to_string(model == 5 ? r->mlp_sh_mask : 0) + "u\n";
+    preamble += "#define EFGS_BASE_INPUT " + std::string(model == 5 && r->mlp_base_input ? "1" : "0") + "\n";
+    files = {"efgs_common.h", "efgs_args.h"};
+    switch (model) {
+        case 1: files.push_back("appearance_sh.h"); break;
+        case 2: files.push_back("appearance_sv.h"); break;
+        case 3:
+        case 4: files.push_back("appearance_lobes.h"); break;
+        case 5: files.push_back("appearance_neural.h"); break;
+    }
+    files.push_back(std::string("preprocess_") + kind + ".hip");
+}
+
+bool get_preprocess_kernel(const efgs_rasterizer* r, int model, const char* kind, RtcKernel& k) {
+    std::string name, preamble;
+    std::vector<std::string> files;
+    kernel_source(r, model, kind, name, preamble, files);
+    return rtc_get_kernel(name, preamble, files, k);
+}
+
+int variant_of(const efgs_rasterizer* r, const efgs_primitives* prims) {
+    return prims->precomputed_colors != nullptr ? 0 : r->model;
+}
+
+int check_config(const efgs_rasterizer* r, const efgs_primitives* prims, int variant) {
+    if (variant != 0 && !r->appearance_set) return fail(EFGS_ERR_STATE, "appearance model is not initialized (efgs_set_appearance)");
+    if (variant == 5 && !r->mlp_set) return fail(EFGS_ERR_STATE, "residual mlp is not initialized (efgs_set_residual_mlp)");
+    if (prims->n_primitives < 0 || prims->n_primitives >= (1ll << 31)) return fail(EFGS_ERR_INVALID_ARGUMENT, "n_primitives out of range");
+    if (prims->n_primitives > 0) {
+        if (!prims->means || !prims->scales || !prims->rotations || !prims->opacities)
+            return fail(EFGS_ERR_INVALID_ARGUMENT, "means, scales, rotations and opacities are required");
+        if (variant != 0 && !prims->base_colors) return fail(EFGS_ERR_INVALID_ARGUMENT, "base_colors are required by the appearance model");
+        if (variant != 0 && n_units_of(r, variant) > 0 && !prims->residual_params)
+            return fail(EFGS_ERR_INVALID_ARGUMENT, "residual_params are required by the appearance model");
+        if (variant == 5 && !prims->mlp_weights) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp_weights are required by the neural model");
+    }
+    return EFGS_OK;
+}
+
+CameraArgs camera_args(const efgs_rasterizer* r, const efgs_settings* s, int variant, uint32_t grid_w, uint32_t grid_h) {
+    CameraArgs c;
+    c.w2c = s->w2c;
+    c.cam_position = s->cam_position;
+    c.width = static_cast<uint32_t>(s->width);
+    c.height = static_cast<uint32_t>(s->height);
+    c.grid_w = grid_w;
+    c.grid_h = grid_h;
+    c.focal_x = s->focal_x;
+    c.focal_y = s->focal_y;
+    c.center_x = s->center_x;
+    c.center_y = s->center_y;
+    c.near_plane = s->near_plane;
+    c.far_plane = s->far_plane;
+    int degree = s->render_residual ? s->appearance_degree : 0;
+    if (degree < 0) degree = 0;
+    const int max_deg = variant == 5 ? 0 : r->max_degree;
+    if (variant >= 1 && variant <= 4 && degree > max_deg) degree = max_deg;
+    if (variant == 0) degree = 0;
+    c.degree = static_cast<uint32_t>(degree);
+    c.proper_aa = s->proper_antialiasing ? 1u : 0u;
+    c.render_base = s->render_base ? 1u : 0u;
+    c.pad_ = 0;
+    return c;
+}
+
+bool launch_rtc(const RtcKernel& k, uint32_t blocks, uint32_t threads, void* args, hipStream_t s) {
+    void* params[] = {args};
+    EFGS_HIP_CHECK(hipModuleLaunchKernel(k.function, blocks, 1, 1, threads, 1, 1, 0, s, params, nullptr));
+    return true;
+}
+
+}  // namespace
+
+
+extern "C" {
+
+const char* efgs_last_error(void) { return error_message(); }
+
+int efgs_set_rtc_dirs(const char* cache_dir, const char* kernel_dir) {
+    if (!kernel_dir) return fail(EFGS_ERR_INVALID_ARGUMENT, "kernel_dir is required");
+    rtc_set_dirs(cache_dir ? cache_dir : "", kernel_dir);
+    return EFGS_OK;
+}
+
+int efgs_rasterizer_create(efgs_rasterizer** out) {
+    if (!out) return fail(EFGS_ERR_INVALID_ARGUMENT, "null output pointer");
+    *out = new efgs_rasterizer();
+    return EFGS_OK;
+}
+
+void efgs_rasterizer_destroy(efgs_rasterizer* r) {
+    if (!r) return;
+    if (r->host_counters) (void)hipHostFree(r->host_counters);
+    delete r;
+}
+
+int efgs_set_appearance(efgs_rasterizer* r, int model, int max_degree, int base_act, int residual_act, int color_act, int direction_gradient) {
+    if (!r) return fail(EFGS_ERR_INVALID_ARGUMENT, "null rasterizer");
+    if (model < 1 || model > 5) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid appearance model id");
+    if (base_act < 0 || base_act > 1) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid base activation id");
+    if (residual_act < 0 || residual_act > 2) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid residual activation id");
+    if (color_act < 0 || color_act > 5) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid color activation id");
+    if (max_degree < 0 || (model == 1 && max_degree > 3)) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid max degree (sh supports 0..3)");
+    r->appearance_set = true;
+    r->model = model;
+    r->max_degree = model == 5 ? 0 : max_degree;
+    r->base_act = base_act;
+    r->res_act = residual_act;
+    r->color_act = color_act;
+    r->direction_gradient = direction_gradient != 0;
+    r->mlp_set = false;
+    return EFGS_OK;
+}
+
+int efgs_set_residual_mlp(efgs_rasterizer* r, int n_input_dims, int n_output_dims, int n_neurons, int n_hidden_layers, int hidden_activation,
+                          int base_input, int n_frequencies, int sh_degree_mask) {
+    if (!r) return fail(EFGS_ERR_INVALID_ARGUMENT, "null rasterizer");
+    if (!r->appearance_set || r->model != 5)
+        return fail(EFGS_ERR_STATE, "set_appearance must select the neural appearance model before set_residual_mlp");
+    if (n_output_dims != 3) return fail(EFGS_ERR_INVALID_ARGUMENT, "the residual mlp must have 3 outputs");
+    if (hidden_activation != 1) return fail(EFGS_ERR_INVALID_ARGUMENT, "only ReLU hidden activations are supported");
+    if (n_neurons != 16 && n_neurons != 32 && n_neurons != 64 && n_neurons != 128)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "n_neurons must be 16, 32, 64 or 128");
+    if (n_hidden_layers < 1 || n_hidden_layers > 8) return fail(EFGS_ERR_INVALID_ARGUMENT, "n_hidden_layers must be in 1..8");
+    if (n_frequencies < 0 || n_frequencies > 8) return fail(EFGS_ERR_INVALID_ARGUMENT, "n_frequencies must be in 0..8");
+    if (sh_degree_mask < 0 || sh_degree_mask > 127) return fail(EFGS_ERR_INVALID_ARGUMENT, "sh degrees must lie in 0..6");
+    int n_degree_dims = 0, max_degree = 0;
+    for (int d = 0; d <= 6; d++) {
+        if (sh_degree_mask & (1 << d)) {
+            n_degree_dims += 2 * d + 1;
+            if (d > 0) max_degree++;
+        }
+    }
+    const int per_feature = n_frequencies > 0 ? 2 * n_frequencies : 1;
+    if (n_input_dims <= n_degree_dims || (n_input_dims - n_degree_dims) % per_feature != 0)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "n_input_dims does not match the feature encoding and the sh degrees");
+    const int raw_features = (n_input_dims - n_degree_dims) / per_feature;
+    const int features = raw_features - (base_input ? 3 : 0);
+    if (features < 1) return fail(EFGS_ERR_INVALID_ARGUMENT, "no learned features left for the residual mlp");
+    if (n_input_dims > 128) return fail(EFGS_ERR_INVALID_ARGUMENT, "n_input_dims above 128 is not supported");
+    r->mlp_set = true;
+    r->mlp_n_in = n_input_dims;
+    r->mlp_n_in_padded = (n_input_dims + 15) / 16 * 16;
+    r->mlp_n_neurons = n_neurons;
+    r->mlp_n_hidden = n_hidden_layers;
+    r->mlp_n_frequencies = n_frequencies;
+    r->mlp_sh_mask = sh_degree_mask;
+    r->mlp_n_features = features;
+    r->mlp_base_input = base_input != 0;
+    r->max_degree = max_degree;
+    return EFGS_OK;
+}
+
+int64_t efgs_mlp_param_count(const efgs_rasterizer* r) {
+    if (!r || !r->mlp_set) return 0;
+    const int64_t n = r->mlp_n_neurons;
+    return n * r->mlp_n_in_padded + (r->mlp_n_hidden - 1) * n * n + 16 * n;
+}
+
+int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image, efgs_alloc_fn alloc,
+                 void* alloc_ctx, efgs_frame* frame, void* stream) {
+    if (!r || !prims || !settings || !image || !alloc || !frame) return fail(EFGS_ERR_INVALID_ARGUMENT, "null argument");
+    if (settings->width <= 0 || settings->height <= 0 || settings->width > 65535 || settings->height > 65535)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "image size out of range");
+    if (!settings->w2c || !settings->cam_position || !settings->bg_color) return fail(EFGS_ERR_INVALID_ARGUMENT, "camera tensors are required");
+    const int variant = variant_of(r, prims);
+    if (int c = check_config(r, prims, variant)) return c;
+    if (variant == 5) return fail(EFGS_ERR_STATE, "the neural appearance kernels are not available in this build");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t n = static_cast<uint32_t>(prims->n_primitives);
+    const uint32_t grid_w = div_up(settings->width, tile_width), grid_h = div_up(settings->height, tile_height);
+    const uint32_t n_tiles = grid_w * grid_h;
+    const int key_bytes = n_tiles <= 65535u ? 2 : 4;
+    const int end_bit = end_bit_of(n_tiles - 1);
+    if (!r->host_counters) {
+        if (hipHostMalloc(reinterpret_cast<void**>(&r->host_counters), 4 * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
+            return fail(EFGS_ERR_HIP, "hipHostMalloc of the counter readback buffer failed");
+    }
+
+    const PrimitiveLayout pl0 = PrimitiveLayout::carve(nullptr, n);
+    char* pblob = static_cast<char*>(alloc(alloc_ctx, pl0.bytes));
+    if (!pblob) return fail(EFGS_ERR_ALLOC, "allocation of the primitive buffers failed");
+    const TileLayout tl0 = TileLayout::carve(nullptr, n_tiles);
+    char* tblob = static_cast<char*>(alloc(alloc_ctx, tl0.bytes));
+    if (!tblob) return fail(EFGS_ERR_ALLOC, "allocation of the tile buffers failed");
+    const PrimitiveLayout pl = PrimitiveLayout::carve(pblob, n);
+    const TileLayout tl = TileLayout::carve(tblob, n_tiles);
+    const CameraArgs cam = camera_args(r, settings, variant, grid_w, grid_h);
+
+    if (n > 0) {
+        RtcKernel k;
+        if (!get_preprocess_kernel(r, variant, "forward", k)) return EFGS_ERR_RTC;
+        PreprocessForwardArgs a;
+        std::memset(&a, 0, sizeof(a));
+        a.means = prims->means;
+        a.scales = prims->scales;
+        a.rotations = prims->rotations;
+        a.opacities = prims->opacities;
+        a.precomputed = prims->precomputed_colors;
+        a.base = prims->base_colors;
+        a.residual = prims->residual_params;
+        a.mlp_weights = prims->mlp_weights;
+        a.n_touched = pl.n_touched;
+        a.depth_keys = pl.depth_keys;
+        a.records = pl.records;
+        a.block_counts = pl.block_counts;
+        a.n = n;
+        a.cam = cam;
+        const uint32_t blocks = div_up(n, preprocess_block);
+        if (!launch_rtc(k, blocks, preprocess_block, &a, s)) return EFGS_ERR_HIP;
+        if (!launch_scan_block_counts(pl.block_counts, pl.block_offsets, pl.counters, blocks, s)) return EFGS_ERR_HIP;
+        if (!launch_compact_visible(pl.n_touched, pl.depth_keys, pl.block_offsets, pl.keys_a, pl.vals_a, n, s)) return EFGS_ERR_HIP;
+    } else {
+        if (!launch_fill_u32(pl.counters, 0u, 4, s)) return EFGS_ERR_HIP;
+    }
+    if (hipMemcpyAsync(r->host_counters, pl.counters, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return fail(EFGS_ERR_HIP, std::string("reading the visible/instance counters failed: ") + hipGetErrorString(hipGetLastError()));
+    const uint32_t n_visible = r->host_counters[0];
+    const uint32_t n_instances = r->host_counters[1];
+
+    bool depth_in_b = false;
+    if (!radix_sort_pairs(pl.keys_a, pl.vals_a, pl.keys_b, pl.vals_b, false, n_visible, 4, 32, pl.sort_scratch, &depth_in_b, s))
+        return EFGS_ERR_HIP;
+    const uint32_t* depth_sorted_prims = depth_in_b ? pl.vals_b : pl.vals_a;
+    if (!scan_exclusive(pl.n_touched, depth_sorted_prims, pl.offsets, nullptr, n_visible, pl.scan_scratch, s)) return EFGS_ERR_HIP;
+
+    const InstanceLayout il0 = InstanceLayout::carve(nullptr, n_instances, key_bytes);
+    char* iblob = static_cast<char*>(alloc(alloc_ctx, il0.bytes));
+    if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
+    const InstanceLayout il = InstanceLayout::carve(iblob, n_instances, key_bytes);
+    if (!launch_create_instances(depth_sorted_prims, pl.offsets, pl.n_touched, pl.records, il.keys_a, key_bytes, il.inst_prim, pl.prim_offset,
+                                 pl.counters, grid_w, n_visible, s))
+        return EFGS_ERR_HIP;
+    bool tiles_in_b = false;
+    if (!radix_sort_pairs(il.keys_a, il.vals_a, il.keys_b, il.vals_b, true, n_instances, key_bytes, end_bit, il.sort_scratch, &tiles_in_b, s))
+        return EFGS_ERR_HIP;
+    const void* sorted_keys = tiles_in_b ? il.keys_b : il.keys_a;
+    const uint32_t* sorted_inst = tiles_in_b ? il.vals_b : il.vals_a;
+    if (!launch_tile_ranges(sorted_keys, key_bytes, tl.ranges, n_instances, n_tiles, s)) return EFGS_ERR_HIP;
+
+    BlendForwardArgs b;
+    b.ranges = tl.ranges;
+    b.sorted_inst = sorted_inst;
+    b.inst_prim = il.inst_prim;
+    b.records = pl.records;
+    b.bg = settings->bg_color;
+    b.image = image;
+    b.final_T = tl.final_T;
+    b.n_contrib = tl.n_contrib;
+    b.tile_max = tl.tile_max;
+    b.width = static_cast<uint32_t>(settings->width);
+    b.height = static_cast<uint32_t>(settings->height);
+    b.grid_w = grid_w;
+    b.n_tiles = n_tiles;
+    if (!launch_blend_forward(b, s)) return EFGS_ERR_HIP;
+
+    frame->primitive_buffers = pblob;
+    frame->tile_buffers = tblob;
+    frame->instance_buffers = iblob;
+    frame->n_primitives = n;
+    frame->n_visible = n_visible;
+    frame->n_instances = n_instances;
+    frame->grid_width = static_cast<int32_t>(grid_w);
+    frame->grid_height = static_cast<int32_t>(grid_h);
+    frame->key_bytes = key_bytes;
+    frame->depth_sorted_in_b = depth_in_b ? 1 : 0;
+    frame->tiles_sorted_in_b = tiles_in_b ? 1 : 0;
+    frame->model = variant;
+    return EFGS_OK;
+}
+
+int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, const efgs_frame* frame, const float* image,
+                  const float* grad_image, efgs_gradients* grads, efgs_alloc_fn alloc, void* alloc_ctx, void* stream) {
+    if (!r || !prims || !settings || !frame || !image || !grad_image || !grads || !alloc)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "null argument");
+    const int variant = frame->model;
+    if (variant != variant_of(r, prims)) return fail(EFGS_ERR_INVALID_ARGUMENT, "inputs do not match the forward frame");
+    if (int c = check_config(r, prims, variant)) return c;
+    if (prims->n_primitives != frame->n_primitives) return fail(EFGS_ERR_INVALID_ARGUMENT, "primitive count differs from the forward frame");
+    if (grads->densification_rows != 0 && grads->densification_rows != 2 && grads->densification_rows != 3)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "densification_rows must be 0, 2 or 3");
+    const uint32_t n = static_cast<uint32_t>(frame->n_primitives);
+    if (n == 0) return EFGS_OK;
+    if (!grads->means || !grads->scales || !grads->rotations || !grads->opacities)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "geometry gradient outputs are required");
+    if (variant == 0 && !grads->precomputed_colors) return fail(EFGS_ERR_INVALID_ARGUMENT, "precomputed colour gradient output is required");
+    if (variant != 0 && !grads->base_colors) return fail(EFGS_ERR_INVALID_ARGUMENT, "base colour gradient output is required");
+    if (variant != 0 && n_units_of(r, variant) > 0 && !grads->residual_params)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "residual parameter gradient output is required");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t grid_w = static_cast<uint32_t>(frame->grid_width), grid_h = static_cast<uint32_t>(frame->grid_height);
+    const uint32_t n_tiles = grid_w * grid_h;
+    const uint32_t n_instances = static_cast<uint32_t>(frame->n_instances);
+    const PrimitiveLayout pl = PrimitiveLayout::carve(static_cast<char*>(frame->primitive_buffers), n);
+    const TileLayout tl = TileLayout::carve(static_cast<char*>(frame->tile_buffers), n_tiles);
+    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), n_instances, frame->key_bytes);
+    const uint32_t* sorted_inst = frame->tiles_sorted_in_b ? il.vals_b : il.vals_a;
+
+    const size_t grad_bytes = static_cast<size_t>(n_instances > 0 ? n_instances : 1) * 12 * sizeof(float);
+    float* inst_grads = static_cast<float*>(alloc(alloc_ctx, grad_bytes));
+    if (!inst_grads) return fail(EFGS_ERR_ALLOC, "allocation of the instance gradient buffer failed");
+
+    BlendBackwardArgs b;
+    b.ranges = tl.ranges;
+    b.sorted_inst = sorted_inst;
+    b.inst_prim = il.inst_prim;
+    b.records = pl.records;
+    b.bg = settings->bg_color;
+    b.image = image;
+    b.grad_image = grad_image;
+    b.final_T = tl.final_T;
+    b.n_contrib = tl.n_contrib;
+    b.tile_max = tl.tile_max;
+    b.inst_grads = inst_grads;
+    b.width = static_cast<uint32_t>(settings->width);
+    b.height = static_cast<uint32_t>(settings->height);
+    b.grid_w = grid_w;
+    b.n_tiles = n_tiles;
+    if (!launch_blend_backward(b, s)) return EFGS_ERR_HIP;
+
+    RtcKernel k;
+    if (!get_preprocess_kernel(r, variant, "backward", k)) return EFGS_ERR_RTC;
+    PreprocessBackwardArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.means = prims->means;
+    a.scales = prims->scales;
+    a.rotations = prims->rotations;
+    a.opacities = prims->opacities;
+    a.base = prims->base_colors;
+    a.residual = prims->residual_params;
+    a.mlp_weights = prims->mlp_weights;
+    a.n_touched = pl.n_touched;
+    a.prim_offset = pl.prim_offset;
+    a.records = pl.records;
+    a.inst_grads = inst_grads;
+    a.g_means = grads->means;
+    a.g_scales = grads->scales;
+    a.g_rotations = grads->rotations;
+    a.g_opacities = grads->opacities;
+    a.g_precomputed = grads->precomputed_colors;
+    a.g_base = grads->base_colors;
+    a.g_residual = grads->residual_params;
+    a.densification_info = grads->densification_rows > 0 ? grads->densification_info : nullptr;
+    a.densification_rows = static_cast<uint32_t>(grads->densification_rows);
+    a.n = n;
+    a.cam = camera_args(r, settings, variant, grid_w, grid_h);
+    if (!launch_rtc(k, div_up(n, preprocess_block), preprocess_block, &a, s)) return EFGS_ERR_HIP;
+    return EFGS_OK;
+}
+
+int efgs_adam_step(const efgs_adam_group* groups, int n_groups, void* stream) {
+    if (n_groups < 0 || (n_groups > 0 && !groups)) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid adam groups");
+    std::vector<AdamGroupDevice> dev(static_cast<size_t>(n_groups));
+    for (int g = 0; g < n_groups; g++) {
+        const efgs_adam_group& in = groups[g];
+        if (in.n_lrs < 1 || in.n_lrs > adam_max_lrs) return fail(EFGS_ERR_INVALID_ARGUMENT, "between 1 and 7 learning rates are supported");
+        if (in.step < 1) return fail(EFGS_ERR_INVALID_ARGUMENT, "adam step counts from 1");
+        if (in.n_elements < 0) return fail(EFGS_ERR_INVALID_ARGUMENT, "negative element count");
+        if (in.n_elements > 0 && (!in.grad || !in.param || !in.exp_avg || !in.exp_avg_sq))
+            return fail(EFGS_ERR_INVALID_ARGUMENT, "null adam tensor");
+        AdamGroupDevice& d = dev[g];
+        d.grad = in.grad;
+        d.param = in.param;
+        d.m = in.exp_avg;
+        d.v = in.exp_avg_sq;
+        d.n = static_cast<uint64_t>(in.n_elements);
+        const double bc1_rcp = 1.0 / (1.0 - std::pow(in.beta1, static_cast<double>(in.step)));
+        const double bc2_sqrt_rcp = 1.0 / std::sqrt(1.0 - std::pow(in.beta2, static_cast<double>(in.step)));
+        for (int k = 0; k < adam_max_lrs; k++) d.step_sizes[k] = k < in.n_lrs ? static_cast<float>(in.lrs[k] * bc1_rcp) : 0.0f;
+        d.n_lrs = in.n_lrs;
+        d.beta1 = static_cast<float>(in.beta1);
+        d.beta2 = static_cast<float>(in.beta2);
+        d.eps = static_cast<float>(in.eps);
+        d.bc2_sqrt_rcp = static_cast<float>(bc2_sqrt_rcp);
+        d.first_block = 0;
+    }
+    if (!launch_adam(dev.data(), n_groups, static_cast<hipStream_t>(stream))) return EFGS_ERR_HIP;
+    return EFGS_OK;
+}
+
+int efgs_get_frame_views(const efgs_frame* frame, efgs_frame_views* v) {
+    if (!frame || !v) return fail(EFGS_ERR_INVALID_ARGUMENT, "null argument");
+    const uint32_t n = static_cast<uint32_t>(frame->n_primitives);
+    const uint32_t n_tiles = static_cast<uint32_t>(frame->grid_width) * static_cast<uint32_t>(frame->grid_height);
+    const PrimitiveLayout pl = PrimitiveLayout::carve(static_cast<char*>(frame->primitive_buffers), n);
+    const TileLayout tl = TileLayout::carve(static_cast<char*>(frame->tile_buffers), n_tiles);
+    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), static_cast<uint64_t>(frame->n_instances),
+                                                    frame->key_bytes);
+    v->n_touched = pl.n_touched;
+    v->depth_keys = pl.depth_keys;
+    v->records = reinterpret_cast<const float*>(pl.records);
+    v->depth_sorted_keys = frame->depth_sorted_in_b ? pl.keys_b : pl.keys_a;
+    v->depth_sorted_prims = frame->depth_sorted_in_b ? pl.vals_b : pl.vals_a;
+    v->instance_offsets = pl.offsets;
+    v->tile_sorted_keys = frame->tiles_sorted_in_b ? il.keys_b : il.keys_a;
+    v->tile_sorted_instances = frame->tiles_sorted_in_b ? il.vals_b : il.vals_a;
+    v->instance_primitive = il.inst_prim;
+    v->tile_ranges = reinterpret_cast<const uint32_t*>(tl.ranges);
+    v->final_transmittance = tl.final_T;
+    v->n_contributors = tl.n_contrib;
+    v->counters = pl.counters;
+    return EFGS_OK;
+}
+
+int efgs_precompile(const efgs_rasterizer* r, const char* arch) {
+    if (!r || !arch) return fail(EFGS_ERR_INVALID_ARGUMENT, "null argument");
+    std::vector<int> variants = {0};
+    if (r->appearance_set && (r->model != 5 || r->mlp_set)) variants.push_back(r->model);
+    for (int variant : variants) {
+        if (variant == 5) continue;
+        for (const char* kind : {"forward", "backward"}) {
+            std::string name, preamble;
+            std::vector<std::string> files;
+            kernel_source(r, variant, kind, name, preamble, files);
+            if (!rtc_precompile(name, preamble, files, arch)) return EFGS_ERR_RTC;
+        }
+    }
+    return EFGS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,67 @@
+// Kernel argument blocks of the hipRTC preprocess kernels, shared verbatim by the host launcher and the
+// runtime-compiled device code (plain pointers and scalars, identical layout on both sides).
+#pragma once
+#ifndef EFGS_RTC
+#include <stdint.h>
+#endif
+
+namespace efgs {
+
+struct PrimRecord;
+
+struct CameraArgs {
+    const float* w2c;           // rows 0..2 of the world-to-view transform (row-major, 4 floats per row)
+    const float* cam_position;  // 3 floats
+    uint32_t width, height, grid_w, grid_h;
+    float focal_x, focal_y, center_x, center_y, near_plane, far_plane;
+    uint32_t degree;            // appearance degree used for rendering (0 when the residual is off)
+    uint32_t proper_aa;
+    uint32_t render_base;
+    uint32_t pad_;
+};
+
+struct PreprocessForwardArgs {
+    const float* means;
+    const float* scales;
+    const float* rotations;
+    const float* opacities;
+    const float* precomputed;
+    const float* base;
+    const float* residual;
+    const uint16_t* mlp_weights;  // fp16 bits, flat tcnn layout
+    uint32_t* n_touched;          // (N) 0 for culled primitives
+    uint32_t* depth_keys;         // (N) float bits of the view depth
+    PrimRecord* records;          // (N) written for visible primitives
+    uint32_t* block_counts;       // (2 * blocks) visible count and instance count per block
+    uint32_t n;
+    uint32_t pad_;
+    CameraArgs cam;
+};
+
+struct PreprocessBackwardArgs {
+    const float* means;
+    const float* scales;
+    const float* rotations;
+    const float* opacities;
+    const float* base;
+    const float* residual;
+    const uint16_t* mlp_weights;
+    const uint32_t* n_touched;
+    const uint32_t* prim_offset;     // (N) first emitted instance of each visible primitive
+    const PrimRecord* records;
+    const float* inst_grads;         // (I x 12) per-instance blend gradients, emission order
+    float* g_means;
+    float* g_scales;
+    float* g_rotations;
+    float* g_opacities;
+    float* g_precomputed;
+    float* g_base;
+    float* g_residual;
+    float* g_mlp_partials;           // neural: (blocks x n_params) fp32 per-block weight gradient partials
+    float* densification_info;       // (rows x N) or null
+    uint32_t densification_rows;
+    uint32_t n;
+    CameraArgs cam;
+};
+
+}  // namespace efgs

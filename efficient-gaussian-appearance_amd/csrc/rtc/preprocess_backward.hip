@@ -1,0 +1,203 @@
+// Backward preprocess, runtime-specialised with hipRTC (same preamble and headers as the forward).
+//
+// One thread per primitive. The blend backward leaves one 12-float gradient record per emitted instance
+// (dL/dmean2d xy, dL/dconic xyz, dL/dopacity, dL/dcolor rgb, |dL/dmean2d| xy, pad) at the instance's
+// emission slot; a visible primitive's slots are contiguous, so this kernel reduces them in a fixed order
+// (deterministic, no float atomics), applies the opacity chain, backpropagates the colour through the
+// activations and the appearance model, and the 2D mean and conic through the EWA projection to the 3D mean,
+// log-scales and quaternion. Culled primitives get zero gradients.
+//
+// Reference: B/rasterization/rtc/preprocess_backward.cu:19-404 (the per-primitive part of
+// B/rasterization/include/kernels_backward.cuh:215-230 is folded in here).
+
+namespace efgs {
+
+constexpr uint32_t preprocess_block = 256;
+constexpr uint32_t params_per_unit = EFGS_MODEL == 1 ? 3u : EFGS_MODEL == 2 ? 7u : EFGS_MODEL == 3 ? 8u : EFGS_MODEL == 4 ? 9u : 1u;
+constexpr uint32_t residual_params = EFGS_MODEL == 0 ? 0u : params_per_unit * EFGS_N_UNITS;
+
+__device__ __forceinline__ uint32_t active_residual_params(uint32_t degree) {
+    if (EFGS_MODEL == 1) return 3u * ((degree + 1) * (degree + 1) - 1);
+    if (EFGS_MODEL == 5) return degree > 0 ? residual_params : 0u;
+    return params_per_unit * degree;
+}
+
+}  // namespace efgs
+
+extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
+    using namespace efgs;
+    const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
+    if (p >= a.n) return;
+    const uint32_t touched = a.n_touched[p];
+    const bool contributes = touched > 0;
+
+    if (!contributes) {
+        a.g_means[3 * p] = 0.0f; a.g_means[3 * p + 1] = 0.0f; a.g_means[3 * p + 2] = 0.0f;
+        a.g_scales[3 * p] = 0.0f; a.g_scales[3 * p + 1] = 0.0f; a.g_scales[3 * p + 2] = 0.0f;
+        a.g_rotations[4 * p] = 0.0f; a.g_rotations[4 * p + 1] = 0.0f; a.g_rotations[4 * p + 2] = 0.0f; a.g_rotations[4 * p + 3] = 0.0f;
+        a.g_opacities[p] = 0.0f;
+#if EFGS_MODEL == 0
+        a.g_precomputed[3 * p] = 0.0f; a.g_precomputed[3 * p + 1] = 0.0f; a.g_precomputed[3 * p + 2] = 0.0f;
+#else
+        a.g_base[3 * p] = 0.0f; a.g_base[3 * p + 1] = 0.0f; a.g_base[3 * p + 2] = 0.0f;
+        for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
+#endif
+        return;
+    }
+
+    // reduce this primitive's instance gradient records (emission order)
+    const float4* ig = reinterpret_cast<const float4*>(a.inst_grads) + 3 * static_cast<size_t>(a.prim_offset[p]);
+    float4 s0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = s0, s2 = s0;
+    for (uint32_t k = 0; k < touched; k++) {
+        const float4 t0 = ig[3 * k], t1 = ig[3 * k + 1], t2 = ig[3 * k + 2];
+        s0.x += t0.x; s0.y += t0.y; s0.z += t0.z; s0.w += t0.w;
+        s1.x += t1.x; s1.y += t1.y; s1.z += t1.z; s1.w += t1.w;
+        s2.x += t2.x; s2.y += t2.y; s2.z += t2.z;
+    }
+    const float gmx = s0.x, gmy = s0.y;
+    const float3 gconic = make_float3(s0.z, s0.w, s1.x);
+    const float gop_acc = s1.y;
+    const float3 gcolor = make_float3(s1.z, s1.w, s2.x);
+    const float gabx = s2.y, gaby = s2.z;
+
+    const PrimRecord rec = a.records[p];
+    const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+
+    // colour -> appearance parameters
+    float3 dmean_color = make_float3(0.0f, 0.0f, 0.0f);
+#if EFGS_MODEL == 0
+    a.g_precomputed[3 * p] = gcolor.x; a.g_precomputed[3 * p + 1] = gcolor.y; a.g_precomputed[3 * p + 2] = gcolor.z;
+#else
+    {
+        const float3 color = make_float3(rec.r1.z, rec.r1.w, rec.r2.x);
+        const float3 dpre = make_float3(color_activation_grad<EFGS_COLOR_ACT>(color.x) * gcolor.x,
+                                        color_activation_grad<EFGS_COLOR_ACT>(color.y) * gcolor.y,
+                                        color_activation_grad<EFGS_COLOR_ACT>(color.z) * gcolor.z);
+        if (a.cam.render_base) {
+            a.g_base[3 * p] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p]) * dpre.x;
+            a.g_base[3 * p + 1] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p + 1]) * dpre.y;
+            a.g_base[3 * p + 2] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p + 2]) * dpre.z;
+        } else {
+            a.g_base[3 * p] = 0.0f; a.g_base[3 * p + 1] = 0.0f; a.g_base[3 * p + 2] = 0.0f;
+        }
+        const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
+        float norm_rcp;
+        const float3 d = view_direction(mean, cam, norm_rcp);
+        const float* rp = a.residual + static_cast<size_t>(p) * residual_params;
+        float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
+#if EFGS_MODEL == 1
+        dmean_color = sh_residual_backward<EFGS_RES_ACT>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+#elif EFGS_MODEL == 2
+        dmean_color = sv_residual_backward<EFGS_RES_ACT>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+#elif EFGS_MODEL == 3
+        dmean_color = lobe_residual_backward<EFGS_RES_ACT, false>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+#elif EFGS_MODEL == 4
+        dmean_color = lobe_residual_backward<EFGS_RES_ACT, true>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+#endif
+        for (uint32_t i = active_residual_params(a.cam.degree); i < residual_params; i++) gp[i] = 0.0f;
+    }
+#endif
+
+    // geometry
+    const float* W = a.cam.w2c;
+    const float depth = W[8] * mean.x + W[9] * mean.y + W[10] * mean.z + W[11];
+    const float x = (W[0] * mean.x + W[1] * mean.y + W[2] * mean.z + W[3]) / depth;
+    const float y = (W[4] * mean.x + W[5] * mean.y + W[6] * mean.z + W[7]) / depth;
+    const float v0 = ef_expf(2.0f * a.scales[3 * p]);
+    const float v1 = ef_expf(2.0f * a.scales[3 * p + 1]);
+    const float v2 = ef_expf(2.0f * a.scales[3 * p + 2]);
+    const float qr = a.rotations[4 * p], qx = a.rotations[4 * p + 1], qy = a.rotations[4 * p + 2], qz = a.rotations[4 * p + 3];
+    float qn;
+    const Mat3 R = quaternion_to_rotation(qr, qx, qy, qz, qn);
+    const Mat3 S = {R.m11 * v0, R.m12 * v1, R.m13 * v2, R.m21 * v0, R.m22 * v1, R.m23 * v2, R.m31 * v0, R.m32 * v1, R.m33 * v2};
+    const float c11 = S.m11 * R.m11 + S.m12 * R.m12 + S.m13 * R.m13;
+    const float c12 = S.m11 * R.m21 + S.m12 * R.m22 + S.m13 * R.m23;
+    const float c13 = S.m11 * R.m31 + S.m12 * R.m32 + S.m13 * R.m33;
+    const float c22 = S.m21 * R.m21 + S.m22 * R.m22 + S.m23 * R.m23;
+    const float c23 = S.m21 * R.m31 + S.m22 * R.m32 + S.m23 * R.m33;
+    const float c33 = S.m31 * R.m31 + S.m32 * R.m32 + S.m33 * R.m33;
+    const float wf = static_cast<float>(a.cam.width), hf = static_cast<float>(a.cam.height);
+    const float fx = a.cam.focal_x, fy = a.cam.focal_y, cx = a.cam.center_x, cy = a.cam.center_y;
+    const float cl = (-0.15f * wf - cx) / fx, cr = (1.15f * wf - cx) / fx;
+    const float ct = (-0.15f * hf - cy) / fy, cb = (1.15f * hf - cy) / fy;
+    const float xc = clampf(x, cl, cr), yc = clampf(y, ct, cb);
+    const float j11 = fx / depth, j13 = -j11 * xc, j22 = fy / depth, j23 = -j22 * yc;
+    const float a1x = j11 * W[0] + j13 * W[8], a1y = j11 * W[1] + j13 * W[9], a1z = j11 * W[2] + j13 * W[10];
+    const float a2x = j22 * W[4] + j23 * W[8], a2y = j22 * W[5] + j23 * W[9], a2z = j22 * W[6] + j23 * W[10];
+    const float b1x = a1x * c11 + a1y * c12 + a1z * c13, b1y = a1x * c12 + a1y * c22 + a1z * c23, b1z = a1x * c13 + a1y * c23 + a1z * c33;
+    const float b2x = a2x * c11 + a2y * c12 + a2z * c13, b2y = a2x * c12 + a2y * c22 + a2z * c23, b2z = a2x * c13 + a2y * c23 + a2z * c33;
+    const float a_raw = b1x * a1x + b1y * a1y + b1z * a1z;
+    const float B = b1x * a2x + b1y * a2y + b1z * a2z;
+    const float c_raw = b2x * a2x + b2y * a2y + b2z * a2z;
+    const float ks = a.cam.proper_aa ? dilation_aa : dilation;
+    const float A = a_raw + ks, C = c_raw + ks;
+    const float aa = A * A, bb = B * B, cc = C * C, ac = A * C, ab = A * B, bc = B * C;
+    const float det = ac - bb;
+    const float det_rcp_sq = 1.0f / (det * det);
+    const float dcx = det_rcp_sq * (2.0f * bc * gconic.y - cc * gconic.x - bb * gconic.z);
+    const float dcy = det_rcp_sq * (bc * gconic.x - (ac + bb) * gconic.y + ab * gconic.z);
+    const float dcz = det_rcp_sq * (2.0f * ab * gconic.y - bb * gconic.x - aa * gconic.z);
+
+    // opacity: stored opacity = sigmoid(raw) [* sqrt(det_raw / det) with proper antialiasing]
+    if (a.cam.proper_aa) {
+        const float o = ef_sigmoid(a.opacities[p]);
+        const float rad = fmaxf((a_raw * c_raw - bb) / det, 0.0f);
+        a.g_opacities[p] = gop_acc * sqrtf(rad) * o * (1.0f - o);
+    } else {
+        const float o = rec.r1.y;
+        a.g_opacities[p] = (o - o * o) * gop_acc;
+    }
+
+    const float d11 = a1x * a1x * dcx + 2.0f * a1x * a2x * dcy + a2x * a2x * dcz;
+    const float d12 = a1x * a1y * dcx + (a1x * a2y + a1y * a2x) * dcy + a2x * a2y * dcz;
+    const float d13 = a1x * a1z * dcx + (a1x * a2z + a1z * a2x) * dcy + a2x * a2z * dcz;
+    const float d22 = a1y * a1y * dcx + 2.0f * a1y * a2y * dcy + a2y * a2y * dcz;
+    const float d23 = a1y * a1z * dcx + (a1y * a2z + a1z * a2y) * dcy + a2y * a2z * dcz;
+    const float d33 = a1z * a1z * dcx + 2.0f * a1z * a2z * dcy + a2z * a2z * dcz;
+    const float g1x = 2.0f * (b1x * dcx + b2x * dcy), g1y = 2.0f * (b1y * dcx + b2y * dcy), g1z = 2.0f * (b1z * dcx + b2z * dcy);
+    const float g2x = 2.0f * (b1x * dcy + b2x * dcz), g2y = 2.0f * (b1y * dcy + b2y * dcz), g2z = 2.0f * (b1z * dcy + b2z * dcz);
+    const float dj11 = W[0] * g1x + W[1] * g1y + W[2] * g1z;
+    const float dj22 = W[4] * g2x + W[5] * g2y + W[6] * g2z;
+    const float dj13 = W[8] * g1x + W[9] * g1y + W[10] * g1z;
+    const float dj23 = W[8] * g2x + W[9] * g2y + W[10] * g2z;
+
+    if (a.densification_info != nullptr) {
+        const uint32_t n = a.n;
+        a.densification_info[p] += 1.0f;
+        const float nx = 0.5f * (gmx * wf), ny = 0.5f * (gmy * hf);
+        a.densification_info[n + p] += sqrtf(nx * nx + ny * ny);
+        if (a.densification_rows > 2) {
+            const float ax = 0.5f * (gabx * wf), ay = 0.5f * (gaby * hf);
+            a.densification_info[2 * n + p] += sqrtf(ax * ax + ay * ay);
+        }
+    }
+
+    float mcx = j11 * gmx, mcy = j22 * gmy, mcz = -j11 * x * gmx - j22 * y * gmy;
+    const bool vx = x >= cl && x <= cr, vy = y >= ct && y <= cb;
+    if (vx) mcx -= j11 * dj13 / depth;
+    if (vy) mcy -= j22 * dj23 / depth;
+    const float fxv = 1.0f + static_cast<float>(vx), fyv = 1.0f + static_cast<float>(vy);
+    mcz += (j11 * (fxv * xc * dj13 - dj11) + j22 * (fyv * yc * dj23 - dj22)) / depth;
+    float gx = W[0] * mcx + W[4] * mcy + W[8] * mcz;
+    float gy = W[1] * mcx + W[5] * mcy + W[9] * mcz;
+    float gz = W[2] * mcx + W[6] * mcy + W[10] * mcz;
+    if (EFGS_DIRECTION_GRADIENT) {
+        gx += dmean_color.x;
+        gy += dmean_color.y;
+        gz += dmean_color.z;
+    }
+    a.g_means[3 * p] = gx; a.g_means[3 * p + 1] = gy; a.g_means[3 * p + 2] = gz;
+
+    const float dv0 = R.m11 * R.m11 * d11 + R.m21 * R.m21 * d22 + R.m31 * R.m31 * d33 + 2.0f * (R.m11 * R.m21 * d12 + R.m11 * R.m31 * d13 + R.m21 * R.m31 * d23);
+    const float dv1 = R.m12 * R.m12 * d11 + R.m22 * R.m22 * d22 + R.m32 * R.m32 * d33 + 2.0f * (R.m12 * R.m22 * d12 + R.m12 * R.m32 * d13 + R.m22 * R.m32 * d23);
+    const float dv2 = R.m13 * R.m13 * d11 + R.m23 * R.m23 * d22 + R.m33 * R.m33 * d33 + 2.0f * (R.m13 * R.m23 * d12 + R.m13 * R.m33 * d13 + R.m23 * R.m33 * d23);
+    a.g_scales[3 * p] = 2.0f * v0 * dv0;
+    a.g_scales[3 * p + 1] = 2.0f * v1 * dv1;
+    a.g_scales[3 * p + 2] = 2.0f * v2 * dv2;
+    const Mat3 dR = {
+        2.0f * (S.m11 * d11 + S.m21 * d12 + S.m31 * d13), 2.0f * (S.m12 * d11 + S.m22 * d12 + S.m32 * d13), 2.0f * (S.m13 * d11 + S.m23 * d12 + S.m33 * d13),
+        2.0f * (S.m11 * d12 + S.m21 * d22 + S.m31 * d23), 2.0f * (S.m12 * d12 + S.m22 * d22 + S.m32 * d23), 2.0f * (S.m13 * d12 + S.m23 * d22 + S.m33 * d23),
+        2.0f * (S.m11 * d13 + S.m21 * d23 + S.m31 * d33), 2.0f * (S.m12 * d13 + S.m22 * d23 + S.m32 * d33), 2.0f * (S.m13 * d13 + S.m23 * d23 + S.m33 * d33)};
+    const float4 gq = quaternion_to_rotation_backward(qr, qx, qy, qz, dR);
+    a.g_rotations[4 * p] = gq.x; a.g_rotations[4 * p + 1] = gq.y; a.g_rotations[4 * p + 2] = gq.z; a.g_rotations[4 * p + 3] = gq.w;
+}

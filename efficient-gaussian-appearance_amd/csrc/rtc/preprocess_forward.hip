@@ -1,0 +1,222 @@
+// Forward preprocess, runtime-specialised with hipRTC. The loader prepends a token preamble
+// (EFGS_KERNEL_NAME, EFGS_MODEL, EFGS_BASE_ACT, EFGS_RES_ACT, EFGS_COLOR_ACT, EFGS_N_UNITS, neural MLP shape
+// tokens), efgs_common.h, efgs_args.h and the selected appearance header.
+//
+// One thread per primitive, 256 threads = 4 wave64 per block. Per primitive: view-depth cull, opacity cull,
+// 3D covariance from log-scales and quaternion, EWA projection with the 1.15x clip, dilation and determinant
+// cull, conic, screen bounds clamped to the padded tile grid, exact touched-tile count (first 4 tiles per
+// lane, larger footprints wave-cooperatively 64 tiles per step), activated colour, and the 48-byte record.
+// Each block also writes its visible and instance counts, which a scan turns into deterministic
+// (primitive-index ordered) compaction offsets. No global atomics.
+//
+// Reference: B/rasterization/rtc/preprocess_forward.cu:12-278, preprocess_common.cuh:190-252.
+
+namespace efgs {
+
+constexpr uint32_t preprocess_block = 256;
+constexpr uint32_t n_sequential_tiles = 4;
+constexpr uint32_t params_per_unit = EFGS_MODEL == 1 ? 3u : EFGS_MODEL == 2 ? 7u : EFGS_MODEL == 3 ? 8u : EFGS_MODEL == 4 ? 9u : 1u;
+constexpr uint32_t residual_params = EFGS_MODEL == 0 ? 0u : params_per_unit * EFGS_N_UNITS;
+
+struct Projected {
+    float mean2d_x, mean2d_y, conic_x, conic_y, conic_z, opacity, power_threshold, depth;
+    uint32_t sx0, sx1, sy0, sy1;
+    TileRect tiles;
+    bool visible;
+};
+
+__device__ inline Projected project(const PreprocessForwardArgs& a, uint32_t p, bool active) {
+#pragma clang fp contract(off)
+    Projected r;
+    r.visible = false;
+    r.sx0 = r.sx1 = r.sy0 = r.sy1 = 0;
+    r.tiles = {0, 0, 0, 0};
+    const float* W = a.cam.w2c;
+    const float mx = a.means[3 * p], my = a.means[3 * p + 1], mz = a.means[3 * p + 2];
+    const float depth = W[8] * mx + W[9] * my + W[10] * mz + W[11];
+    r.depth = depth;
+    if (!active || depth < a.cam.near_plane || depth > a.cam.far_plane) return r;
+    float opacity = ef_sigmoid(a.opacities[p]);
+    if (opacity < min_alpha) return r;
+    const float v0 = ef_expf(2.0f * a.scales[3 * p]);
+    const float v1 = ef_expf(2.0f * a.scales[3 * p + 1]);
+    const float v2 = ef_expf(2.0f * a.scales[3 * p + 2]);
+    float qn;
+    const Mat3 R = quaternion_to_rotation(a.rotations[4 * p], a.rotations[4 * p + 1], a.rotations[4 * p + 2], a.rotations[4 * p + 3], qn);
+    if (qn < 1e-8f) return r;
+    const Mat3 S = {R.m11 * v0, R.m12 * v1, R.m13 * v2, R.m21 * v0, R.m22 * v1, R.m23 * v2, R.m31 * v0, R.m32 * v1, R.m33 * v2};
+    const float c11 = S.m11 * R.m11 + S.m12 * R.m12 + S.m13 * R.m13;
+    const float c12 = S.m11 * R.m21 + S.m12 * R.m22 + S.m13 * R.m23;
+    const float c13 = S.m11 * R.m31 + S.m12 * R.m32 + S.m13 * R.m33;
+    const float c22 = S.m21 * R.m21 + S.m22 * R.m22 + S.m23 * R.m23;
+    const float c23 = S.m21 * R.m31 + S.m22 * R.m32 + S.m23 * R.m33;
+    const float c33 = S.m31 * R.m31 + S.m32 * R.m32 + S.m33 * R.m33;
+    const float x = (W[0] * mx + W[1] * my + W[2] * mz + W[3]) / depth;
+    const float y = (W[4] * mx + W[5] * my + W[6] * mz + W[7]) / depth;
+    const float wf = static_cast<float>(a.cam.width), hf = static_cast<float>(a.cam.height);
+    const float fx = a.cam.focal_x, fy = a.cam.focal_y, cx = a.cam.center_x, cy = a.cam.center_y;
+    const float cl = (-0.15f * wf - cx) / fx, cr = (1.15f * wf - cx) / fx;
+    const float ct = (-0.15f * hf - cy) / fy, cb = (1.15f * hf - cy) / fy;
+    const float xc = clampf(x, cl, cr), yc = clampf(y, ct, cb);
+    const float j11 = fx / depth, j13 = -j11 * xc, j22 = fy / depth, j23 = -j22 * yc;
+    const float a1x = j11 * W[0] + j13 * W[8], a1y = j11 * W[1] + j13 * W[9], a1z = j11 * W[2] + j13 * W[10];
+    const float a2x = j22 * W[4] + j23 * W[8], a2y = j22 * W[5] + j23 * W[9], a2z = j22 * W[6] + j23 * W[10];
+    const float b1x = a1x * c11 + a1y * c12 + a1z * c13, b1y = a1x * c12 + a1y * c22 + a1z * c23, b1z = a1x * c13 + a1y * c23 + a1z * c33;
+    const float b2x = a2x * c11 + a2y * c12 + a2z * c13, b2y = a2x * c12 + a2y * c22 + a2z * c23, b2z = a2x * c13 + a2y * c23 + a2z * c33;
+    float vx = b1x * a1x + b1y * a1y + b1z * a1z;
+    const float vy = b1x * a2x + b1y * a2y + b1z * a2z;
+    float vz = b2x * a2x + b2y * a2y + b2z * a2z;
+    const float det_raw = vx * vz - vy * vy;
+    const float ks = a.cam.proper_aa ? dilation_aa : dilation;
+    vx += ks;
+    vz += ks;
+    const float det = vx * vz - vy * vy;
+    if (det < min_cov2d_det) return r;
+    r.conic_x = vz / det;
+    r.conic_y = -vy / det;
+    r.conic_z = vx / det;
+    if (a.cam.proper_aa) {
+        opacity *= sqrtf(fmaxf(det_raw / det, 0.0f));
+        if (opacity < min_alpha) return r;
+    }
+    r.opacity = opacity;
+    r.mean2d_x = x * fx + cx;
+    r.mean2d_y = y * fy + cy;
+    const float pt = power_threshold_of(opacity);
+    r.power_threshold = pt;
+    const float cutoff = 2.0f * pt;
+    const float ex = fmaxf(sqrtf(vx * cutoff) - 0.5f, 0.0f);
+    const float ey = fmaxf(sqrtf(vz * cutoff) - 0.5f, 0.0f);
+    const float pw = static_cast<float>(a.cam.grid_w * tile_width), ph = static_cast<float>(a.cam.grid_h * tile_height);
+    // min(padded, max(0, round_down/up(v))) with the clamp applied before the float-to-int conversion
+    const int bx0 = static_cast<int>(floorf(clampf(r.mean2d_x - ex, -1.0f, pw + 1.0f)));
+    const int bx1 = static_cast<int>(ceilf(clampf(r.mean2d_x + ex, -1.0f, pw + 1.0f)));
+    const int by0 = static_cast<int>(floorf(clampf(r.mean2d_y - ey, -1.0f, ph + 1.0f)));
+    const int by1 = static_cast<int>(ceilf(clampf(r.mean2d_y + ey, -1.0f, ph + 1.0f)));
+    const int ipw = static_cast<int>(a.cam.grid_w * tile_width), iph = static_cast<int>(a.cam.grid_h * tile_height);
+    r.sx0 = static_cast<uint32_t>(min(ipw, max(0, bx0)));
+    r.sx1 = static_cast<uint32_t>(min(ipw, max(0, bx1)));
+    r.sy0 = static_cast<uint32_t>(min(iph, max(0, by0)));
+    r.sy1 = static_cast<uint32_t>(min(iph, max(0, by1)));
+    r.tiles = screen_to_tile_bounds(r.sx0, r.sx1, r.sy0, r.sy1);
+    r.visible = (r.tiles.x1 - r.tiles.x0) * (r.tiles.y1 - r.tiles.y0) > 0;
+    return r;
+}
+
+// exact number of tiles in the tile rectangle that the primitive reaches; every lane of the wave must call it
+__device__ inline uint32_t count_touched_tiles(const Projected& pr, uint32_t lane) {
+#pragma clang fp contract(off)
+    const uint32_t bw = pr.tiles.x1 - pr.tiles.x0;
+    const uint32_t cnt = pr.visible ? bw * (pr.tiles.y1 - pr.tiles.y0) : 0u;
+    const float smx = pr.mean2d_x - 0.5f, smy = pr.mean2d_y - 0.5f;
+    uint32_t touched = 0;
+    for (uint32_t i = 0; i < cnt && i < n_sequential_tiles; i++) {
+        const uint32_t tx = pr.tiles.x0 + i % bw, ty = pr.tiles.y0 + i / bw;
+        touched += will_primitive_contribute(smx, smy, pr.conic_x, pr.conic_y, pr.conic_z, tx, ty, pr.power_threshold) ? 1u : 0u;
+    }
+    uint64_t coop = __ballot(cnt > n_sequential_tiles);
+    while (coop != 0) {
+        const uint32_t src = static_cast<uint32_t>(__ffsll(static_cast<long long>(coop)) - 1);
+        coop &= coop - 1;
+        const uint32_t c_x0 = __shfl(pr.tiles.x0, src), c_y0 = __shfl(pr.tiles.y0, src);
+        const uint32_t c_bw = __shfl(bw, src), c_cnt = __shfl(cnt, src);
+        const float c_mx = __shfl(smx, src), c_my = __shfl(smy, src);
+        const float c_cx = __shfl(pr.conic_x, src), c_cy = __shfl(pr.conic_y, src), c_cz = __shfl(pr.conic_z, src);
+        const float c_pt = __shfl(pr.power_threshold, src);
+        uint32_t hits = 0;
+        for (uint32_t base = n_sequential_tiles; base < c_cnt; base += 64) {
+            const uint32_t i = base + lane;
+            const bool hit = i < c_cnt && will_primitive_contribute(c_mx, c_my, c_cx, c_cy, c_cz, c_x0 + i % c_bw, c_y0 + i / c_bw, c_pt);
+            hits += static_cast<uint32_t>(__popcll(__ballot(hit)));
+        }
+        if (lane == src) touched += hits;
+    }
+    return touched;
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+}  // namespace efgs
+
+extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessForwardArgs a) {
+    using namespace efgs;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t p_raw = blockIdx.x * preprocess_block + threadIdx.x;
+    const bool active = p_raw < a.n;
+    const uint32_t p = active ? p_raw : a.n - 1;
+
+    Projected pr = project(a, p, active);
+    uint32_t touched = count_touched_tiles(pr, lane);
+    bool visible = pr.visible && touched > 0;
+
+    float3 color = make_float3(0.0f, 0.0f, 0.0f);
+    if (visible) {
+#if EFGS_MODEL == 0
+        color = make_float3(a.precomputed[3 * p], a.precomputed[3 * p + 1], a.precomputed[3 * p + 2]);
+#else
+        const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+        const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
+        float norm_rcp;
+        const float3 d = view_direction(mean, cam, norm_rcp);
+        const float* rp = a.residual + static_cast<size_t>(p) * residual_params;
+        float3 res = make_float3(0.0f, 0.0f, 0.0f);
+#if EFGS_MODEL == 1
+        res = sh_residual<EFGS_RES_ACT>(rp, d, a.cam.degree);
+#elif EFGS_MODEL == 2
+        res = sv_residual<EFGS_RES_ACT>(rp, d, a.cam.degree);
+#elif EFGS_MODEL == 3
+        res = lobe_residual<EFGS_RES_ACT, false>(rp, d, a.cam.degree);
+#elif EFGS_MODEL == 4
+        res = lobe_residual<EFGS_RES_ACT, true>(rp, d, a.cam.degree);
+#endif
+        const float b0 = base_activation<EFGS_BASE_ACT>(a.base[3 * p]);
+        const float b1 = base_activation<EFGS_BASE_ACT>(a.base[3 * p + 1]);
+        const float b2 = base_activation<EFGS_BASE_ACT>(a.base[3 * p + 2]);
+        color = make_float3(color_activation<EFGS_COLOR_ACT>(b0 + res.x), color_activation<EFGS_COLOR_ACT>(b1 + res.y),
+                            color_activation<EFGS_COLOR_ACT>(b2 + res.z));
+        if (!a.cam.render_base) {
+            color.x = fabsf(color.x - color_activation<EFGS_COLOR_ACT>(b0));
+            color.y = fabsf(color.y - color_activation<EFGS_COLOR_ACT>(b1));
+            color.z = fabsf(color.z - color_activation<EFGS_COLOR_ACT>(b2));
+        }
+#endif
+    }
+
+    if (!visible) touched = 0;
+    if (active) {
+        a.n_touched[p] = touched;
+        a.depth_keys[p] = __float_as_uint(pr.depth);
+        if (visible) {
+            PrimRecord rec;
+            rec.r0 = make_float4(pr.mean2d_x, pr.mean2d_y, pr.conic_x, pr.conic_y);
+            rec.r1 = make_float4(pr.conic_z, pr.opacity, color.x, color.y);
+            rec.r2 = make_float4(color.z, __uint_as_float(pr.sx0 | (pr.sx1 << 16)), __uint_as_float(pr.sy0 | (pr.sy1 << 16)), 0.0f);
+            a.records[p] = rec;
+        }
+    }
+
+    // per-block visible / instance counts (deterministic compaction offsets come from their scan)
+    __shared__ uint32_t wave_counts[2 * (preprocess_block / 64)];
+    const uint32_t wave_visible = static_cast<uint32_t>(__popcll(__ballot(visible && active)));
+    const uint32_t wave_instances = wave_sum_u32(active ? touched : 0u);
+    if (lane == 0) {
+        wave_counts[2 * wave] = wave_visible;
+        wave_counts[2 * wave + 1] = wave_instances;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t v = 0, i = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < preprocess_block / 64; w++) {
+            v += wave_counts[2 * w];
+            i += wave_counts[2 * w + 1];
+        }
+        a.block_counts[2 * blockIdx.x] = v;
+        a.block_counts[2 * blockIdx.x + 1] = i;
+    }
+}

@@ -1,0 +1,151 @@
+// Device-wide exclusive scan of uint32 on wave64: reduce -> scan of block sums -> block scan with offsets.
+// Used for compaction offsets (gathering per-primitive tile counts in depth order), radix-sort histograms
+// and the per-block preprocess counts. Replaces cub::DeviceScan (B/rasterization/src/forward.cu:107-114,
+// 211-218).
+#include "internal.h"
+
+namespace efgs {
+
+namespace {
+
+__device__ __forceinline__ uint32_t load_value(const uint32_t* in, const uint32_t* idx, uint32_t i) {
+    return idx ? in[idx[i]] : in[i];
+}
+
+// inclusive scan of v over the 64 lanes of a wave (Hillis-Steele with lane shuffles)
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, uint32_t lane) {
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(v, o);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+// exclusive scan over the block's threads; returns the thread's exclusive prefix and the block total
+template <uint32_t BLOCK>
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& total) {
+    __shared__ uint32_t wave_totals[BLOCK / 64];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t inc = wave_inclusive_scan(v, lane);
+    if (lane == 63) wave_totals[wave] = inc;
+    __syncthreads();
+    uint32_t wave_prefix = 0;
+    total = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < BLOCK / 64; w++) {
+        const uint32_t t = wave_totals[w];
+        if (w < wave) wave_prefix += t;
+        total += t;
+    }
+    __syncthreads();
+    return wave_prefix + inc - v;
+}
+
+__global__ __launch_bounds__(scan_block) void scan_reduce_kernel(const uint32_t* in, const uint32_t* idx, uint32_t* block_sums, uint32_t n) {
+    const uint32_t base = blockIdx.x * scan_tile + threadIdx.x * scan_items;
+    uint32_t s = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < scan_items; k++) {
+        const uint32_t i = base + k;
+        if (i < n) s += load_value(in, idx, i);
+    }
+    uint32_t total;
+    block_exclusive_scan<scan_block>(s, total);
+    if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
+}
+
+// single block: exclusive scan of up to 1024 * k block sums in place, total -> *total
+__global__ __launch_bounds__(1024) void scan_block_sums_kernel(uint32_t* sums, uint32_t n, uint32_t* total) {
+    const uint32_t per = (n + 1023) / 1024;
+    const uint32_t base = threadIdx.x * per;
+    uint32_t s = 0;
+    for (uint32_t k = 0; k < per; k++)
+        if (base + k < n) s += sums[base + k];
+    uint32_t block_total;
+    uint32_t prefix = block_exclusive_scan<1024>(s, block_total);
+    for (uint32_t k = 0; k < per; k++) {
+        if (base + k < n) {
+            const uint32_t v = sums[base + k];
+            sums[base + k] = prefix;
+            prefix += v;
+        }
+    }
+    if (threadIdx.x == 0 && total) *total = block_total;
+}
+
+__global__ __launch_bounds__(scan_block) void scan_downsweep_kernel(const uint32_t* in, const uint32_t* idx, const uint32_t* block_offsets,
+                                                                   uint32_t* out, uint32_t n) {
+    const uint32_t base = blockIdx.x * scan_tile + threadIdx.x * scan_items;
+    uint32_t v[scan_items];
+    uint32_t s = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < scan_items; k++) {
+        const uint32_t i = base + k;
+        v[k] = i < n ? load_value(in, idx, i) : 0u;
+        s += v[k];
+    }
+    uint32_t total;
+    uint32_t prefix = block_exclusive_scan<scan_block>(s, total) + block_offsets[blockIdx.x];
+#pragma unroll
+    for (uint32_t k = 0; k < scan_items; k++) {
+        const uint32_t i = base + k;
+        if (i < n) out[i] = prefix;
+        prefix += v[k];
+    }
+}
+
+// one block: offsets of the per-preprocess-block (visible, instance) counts; counters[0] = V, counters[1] = I
+__global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t* counts, uint32_t* offsets, uint32_t* counters, uint32_t n) {
+    const uint32_t per = (n + 1023) / 1024;
+    const uint32_t base = threadIdx.x * per;
+    uint32_t sv = 0, si = 0;
+    for (uint32_t k = 0; k < per; k++) {
+        if (base + k < n) {
+            sv += counts[2 * (base + k)];
+            si += counts[2 * (base + k) + 1];
+        }
+    }
+    uint32_t tv, ti;
+    uint32_t pv = block_exclusive_scan<1024>(sv, tv);
+    uint32_t pi = block_exclusive_scan<1024>(si, ti);
+    for (uint32_t k = 0; k < per; k++) {
+        if (base + k < n) {
+            offsets[2 * (base + k)] = pv;
+            offsets[2 * (base + k) + 1] = pi;
+            pv += counts[2 * (base + k)];
+            pi += counts[2 * (base + k) + 1];
+        }
+    }
+    if (threadIdx.x == 0) {
+        counters[0] = tv;
+        counters[1] = ti;
+        counters[2] = 0;  // instance-emission mismatch counter, see create_instances
+        counters[3] = 0;
+    }
+}
+
+}  // namespace
+
+size_t scan_scratch_bytes(uint32_t n) { return sizeof(uint32_t) * (static_cast<size_t>(div_up(n, scan_tile)) + 64); }
+
+bool scan_exclusive(const uint32_t* in, const uint32_t* idx, uint32_t* out, uint32_t* total, uint32_t n, void* scratch, hipStream_t s) {
+    if (n == 0) {
+        return total ? launch_fill_u32(total, 0u, 1, s) : true;
+    }
+    const uint32_t blocks = div_up(n, scan_tile);
+    uint32_t* sums = static_cast<uint32_t*>(scratch);
+    scan_reduce_kernel<<<blocks, scan_block, 0, s>>>(in, idx, sums, n);
+    scan_block_sums_kernel<<<1, 1024, 0, s>>>(sums, blocks, total);
+    scan_downsweep_kernel<<<blocks, scan_block, 0, s>>>(in, idx, sums, out, n);
+    EFGS_HIP_CHECK(hipGetLastError());
+    return true;
+}
+
+bool launch_scan_block_counts(const uint32_t* block_counts, uint32_t* block_offsets, uint32_t* counters, uint32_t n_blocks, hipStream_t s) {
+    scan_block_counts_kernel<<<1, 1024, 0, s>>>(block_counts, block_offsets, counters, n_blocks);
+    EFGS_HIP_CHECK(hipGetLastError());
+    return true;
+}
+
+}  // namespace efgs

@@ -1,0 +1,13 @@
+"""efgs -- MI355X-native fused-appearance differentiable Gaussian rasterizer.
+
+Drop-in for the reference package's exports (FasterGSVDACudaBackend/__init__.py:14-23): diff_rasterize,
+rasterize, update_pruning_scores, RasterizerSettings, initialize_appearance, initialize_residual_mlp,
+FusedAdam. The compute path is libefgs_hip.so (hand-written HIP kernels for gfx950, hipRTC-specialised
+preprocess); importing without the built library raises ImportError.
+"""
+from .rasterization import (diff_rasterize, rasterize, update_pruning_scores, RasterizerSettings, initialize_appearance,
+                            initialize_residual_mlp)
+from .adam import FusedAdam
+
+__all__ = ['diff_rasterize', 'rasterize', 'update_pruning_scores', 'RasterizerSettings', 'initialize_appearance',
+           'initialize_residual_mlp', 'FusedAdam']

@@ -1,0 +1,287 @@
+"""Python interface of the rasterizer, mirroring the reference bindings
+(FasterGSVDACudaBackend/FasterGSVDACudaBackend/torch_bindings/rasterization.py:1-251): same function names,
+argument meaning and error behaviour, backed by libefgs_hip.so through ctypes.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Any, NamedTuple
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import _lib
+from ._lib import check, lib
+
+APPEARANCE_MODEL_IDS = {'sh': 1, 'sv': 2, 'nasg': 3, 'nasgabor': 4, 'neural': 5}  # 0: internal precomputed-colour variant
+BASE_ACTIVATION_IDS = {'none': 0, 'exp': 1}
+RESIDUAL_ACTIVATION_IDS = {'none': 0, 'tanh': 1, 'softplus': 2}
+COLOR_ACTIVATION_IDS = {'none': 0, 'relu': 1, 'softplus': 2, 'sigmoid': 3, 'hardsigmoid': 4, 'satexp': 5}
+HIDDEN_ACTIVATION_IDS = {'relu': 1}
+
+
+class Rasterizer:
+    """Owns the native rasterizer state (appearance configuration, specialised kernels)."""
+
+    def __init__(self) -> None:
+        h = ctypes.c_void_p()
+        check(lib.efgs_rasterizer_create(ctypes.byref(h)))
+        self.handle = h
+
+    def __del__(self) -> None:
+        if getattr(self, 'handle', None) is not None and lib is not None:
+            lib.efgs_rasterizer_destroy(self.handle)
+            self.handle = None
+
+    def set_appearance(self, model: int, max_degree: int, base_act: int, residual_act: int, color_act: int, direction_gradient: bool) -> None:
+        check(lib.efgs_set_appearance(self.handle, model, max_degree, base_act, residual_act, color_act, int(bool(direction_gradient))))
+
+    def set_residual_mlp(self, n_input_dims: int, n_output_dims: int, n_neurons: int, n_hidden_layers: int, hidden_activation: int,
+                         base_input: bool, n_frequencies: int, sh_degree_mask: int) -> None:
+        check(lib.efgs_set_residual_mlp(self.handle, n_input_dims, n_output_dims, n_neurons, n_hidden_layers, hidden_activation,
+                                        int(bool(base_input)), n_frequencies, sh_degree_mask))
+
+    def mlp_param_count(self) -> int:
+        return int(lib.efgs_mlp_param_count(self.handle))
+
+    def precompile(self, arch: str = 'gfx950') -> None:
+        check(lib.efgs_precompile(self.handle, arch.encode()))
+
+
+# module-level rasterizer instance owning the specialised kernels (as the reference's _rasterizer)
+_rasterizer = Rasterizer()
+
+
+def initialize_appearance(appearance_model: str, max_degree: int, base_activation: str, residual_activation: str,
+                          color_activation: str, direction_gradient: bool) -> None:
+    """Configures the rasterizer's runtime-specialised kernels for the given appearance model."""
+    _rasterizer.set_appearance(APPEARANCE_MODEL_IDS[appearance_model], max_degree, BASE_ACTIVATION_IDS[base_activation],
+                               RESIDUAL_ACTIVATION_IDS[residual_activation], COLOR_ACTIVATION_IDS[color_activation], direction_gradient)
+
+
+def initialize_residual_mlp(n_input_dims: int, n_output_dims: int, encoding_config: dict[str, Any], network_config: dict[str, Any],
+                            base_input: bool, n_frequencies: int, sh_degrees: list[int]) -> None:
+    """Creates the residual MLP from a tinycudann-style configuration (requires initialize_appearance('neural', ...) first).
+
+    Supported: encoding 'Identity', network 'FullyFusedMLP' / 'CutlassMLP' with ReLU hidden layers and 'None' output.
+    """
+    otype = str(encoding_config.get('otype', 'Identity')).lower()
+    if otype != 'identity':
+        raise RuntimeError(f'efgs: unsupported encoding {encoding_config.get("otype")!r} (only Identity)')
+    out_act = str(network_config.get('output_activation', 'None')).lower()
+    if out_act != 'none':
+        raise RuntimeError(f'efgs: unsupported output activation {network_config.get("output_activation")!r}')
+    hidden = str(network_config.get('activation', 'ReLU')).lower()
+    if hidden not in HIDDEN_ACTIVATION_IDS:
+        raise RuntimeError(f'efgs: unsupported hidden activation {network_config.get("activation")!r}')
+    sh_degree_mask = sum(1 << degree for degree in sh_degrees)
+    _rasterizer.set_residual_mlp(n_input_dims, n_output_dims, int(network_config['n_neurons']), int(network_config['n_hidden_layers']),
+                                 HIDDEN_ACTIVATION_IDS[hidden], base_input, n_frequencies, sh_degree_mask)
+
+
+class RasterizerSettings(NamedTuple):
+    w2c: torch.Tensor  # affine transformation from model/world space to view space
+    cam_position: torch.Tensor  # camera position in world space
+    bg_color: torch.Tensor  # background color in RGB format
+    appearance_degree: int  # appearance degree used for rendering
+    width: int  # width of the image plane in pixels
+    height: int  # height of the image plane in pixels
+    focal_x: float  # focal length in x direction in pixels
+    focal_y: float  # focal length in y direction in pixels
+    center_x: float  # x coordinate of the image center in pixels (positive -> right)
+    center_y: float  # y coordinate of the image center in pixels (positive -> down)
+    near_plane: float  # near clipping plane distance
+    far_plane: float  # far clipping plane distance
+    proper_antialiasing: bool  # whether to use proper antialiasing
+    render_base: bool  # whether the view-independent base color contributes to the rendered color
+    render_residual: bool  # whether the view-dependent appearance term contributes (if False, the appearance degree is treated as 0)
+
+    def as_tuple(self) -> tuple:
+        return tuple(self)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return t.data_ptr() if t is not None and t.numel() > 0 else None
+
+
+def _check_param(name: str, t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    if t.numel() == 0:
+        return t
+    if t.dtype != torch.float32:
+        raise ValueError(f'efgs: {name} must be float32, got {t.dtype}')
+    if t.device != device:
+        raise ValueError(f'efgs: {name} is on {t.device}, expected {device}')
+    if not t.is_contiguous():
+        raise ValueError(f'efgs: {name} must be contiguous')
+    return t
+
+
+def _native_settings(s: RasterizerSettings, device: torch.device) -> tuple[_lib.Settings, list[torch.Tensor]]:
+    w2c = s.w2c.detach().to(device=device, dtype=torch.float32).contiguous()
+    if w2c.numel() < 12:
+        raise ValueError('efgs: w2c needs at least 3 rows of 4 entries')
+    cam = s.cam_position.detach().to(device=device, dtype=torch.float32).contiguous()
+    bg = s.bg_color.detach().to(device=device, dtype=torch.float32).contiguous()
+    c = _lib.Settings()
+    c.w2c, c.cam_position, c.bg_color = w2c.data_ptr(), cam.data_ptr(), bg.data_ptr()
+    c.appearance_degree = int(s.appearance_degree)
+    c.width, c.height = int(s.width), int(s.height)
+    c.focal_x, c.focal_y, c.center_x, c.center_y = float(s.focal_x), float(s.focal_y), float(s.center_x), float(s.center_y)
+    c.near_plane, c.far_plane = float(s.near_plane), float(s.far_plane)
+    c.proper_antialiasing = int(bool(s.proper_antialiasing))
+    c.render_base = int(bool(s.render_base))
+    c.render_residual = int(bool(s.render_residual))
+    return c, [w2c, cam, bg]
+
+
+def _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half):
+    p = _lib.Primitives()
+    p.n_primitives = int(means.shape[0])
+    p.means, p.scales, p.rotations, p.opacities = means.data_ptr(), scales.data_ptr(), rotations.data_ptr(), opacities.data_ptr()
+    p.precomputed_colors = _ptr(precomputed_colors)
+    p.base_colors = _ptr(base_colors)
+    p.residual_params = _ptr(residual_params)
+    p.mlp_weights = _ptr(mlp_weights_half)
+    return p
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half, settings):
+    device = means.device
+    if device.type != 'cuda':
+        raise ValueError('efgs: the rasterizer runs on a GPU device')
+    names = ('means', 'scales', 'rotations', 'opacities', 'precomputed_colors', 'base_colors', 'residual_params')
+    for name, t in zip(names, (means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params)):
+        _check_param(name, t, device)
+    with torch.cuda.device(device):
+        cs, keep = _native_settings(settings, device)
+        prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
+        image = torch.empty((3, int(settings.height), int(settings.width)), dtype=torch.float32, device=device)
+        alloc = _lib.TensorAllocator(device)
+        frame = _lib.Frame()
+        check(lib.efgs_forward(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), image.data_ptr(), alloc.fn, None,
+                               ctypes.byref(frame), _stream(device)))
+    return image, frame, alloc.tensors, keep
+
+
+class _Rasterize(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights,
+                densification_info, rasterizer_settings: RasterizerSettings) -> torch.Tensor:
+        mlp_weights_half = mlp_weights.detach().half().contiguous() if mlp_weights.numel() > 0 else torch.empty(0, dtype=torch.float16, device=means.device)
+        image, frame, buffers, _ = _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params,
+                                            mlp_weights_half, rasterizer_settings)
+        ctx.rasterizer_settings = rasterizer_settings
+        ctx.frame = frame
+        ctx.buffers = buffers
+        ctx.mlp_numel = mlp_weights.numel()
+        ctx.save_for_backward(image, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
+        ctx.densification_info = densification_info
+        ctx.mark_non_differentiable(densification_info)
+        return image
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, grad_image: torch.Tensor):
+        image, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half = ctx.saved_tensors
+        device = means.device
+        n = means.shape[0]
+        grad_image = grad_image.contiguous()
+        with torch.cuda.device(device):
+            cs, keep = _native_settings(ctx.rasterizer_settings, device)
+            prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
+            g_means = torch.empty_like(means)
+            g_scales = torch.empty_like(scales)
+            g_rotations = torch.empty_like(rotations)
+            g_opacities = torch.empty_like(opacities)
+            g_pre = torch.empty_like(precomputed_colors)
+            g_base = torch.empty_like(base_colors)
+            g_res = torch.empty_like(residual_params)
+            g_mlp = torch.zeros(ctx.mlp_numel, dtype=torch.float32, device=device)
+            dinfo = ctx.densification_info
+            rows = int(dinfo.shape[0]) if dinfo is not None and dinfo.numel() > 0 else 0
+            if rows:
+                if dinfo.dtype != torch.float32 or not dinfo.is_contiguous() or dinfo.shape[-1] != n or dinfo.device != device:
+                    raise ValueError('efgs: densification_info must be a contiguous float32 (2|3, N) tensor on the rendering device')
+            grads = _lib.Gradients()
+            grads.means, grads.scales, grads.rotations, grads.opacities = (g_means.data_ptr(), g_scales.data_ptr(),
+                                                                           g_rotations.data_ptr(), g_opacities.data_ptr())
+            grads.precomputed_colors = _ptr(g_pre)
+            grads.base_colors = _ptr(g_base)
+            grads.residual_params = _ptr(g_res)
+            grads.mlp_weights = _ptr(g_mlp)
+            grads.densification_info = dinfo.data_ptr() if rows else None
+            grads.densification_rows = rows
+            alloc = _lib.TensorAllocator(device)
+            check(lib.efgs_backward(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), ctypes.byref(ctx.frame), image.data_ptr(),
+                                    grad_image.data_ptr(), ctypes.byref(grads), alloc.fn, None, _stream(device)))
+        return (g_means, g_scales, g_rotations, g_opacities,
+                g_pre if g_pre.numel() > 0 else None,
+                g_base if g_base.numel() > 0 else None,
+                g_res if g_res.numel() > 0 else None,
+                g_mlp if g_mlp.numel() > 0 else None,
+                None, None)
+
+
+def _empty(device: torch.device, dtype=torch.float32) -> torch.Tensor:
+    return torch.empty(0, dtype=dtype, device=device)
+
+
+def diff_rasterize(means: torch.Tensor, scales: torch.Tensor, rotations: torch.Tensor, opacities: torch.Tensor,
+                   densification_info: torch.Tensor, rasterizer_settings: RasterizerSettings,
+                   precomputed_colors: torch.Tensor | None = None, base_colors: torch.Tensor | None = None,
+                   residual_params: torch.Tensor | None = None, mlp_weights: torch.Tensor | None = None) -> torch.Tensor:
+    """Differentiable render (3, H, W); densification_info (0,) or (2|3, N) is updated in place by the backward."""
+    d = means.device
+    return _Rasterize.apply(means, scales, rotations, opacities,
+                            precomputed_colors if precomputed_colors is not None else _empty(d),
+                            base_colors if base_colors is not None else _empty(d),
+                            residual_params if residual_params is not None else _empty(d),
+                            mlp_weights if mlp_weights is not None else _empty(d),
+                            densification_info, rasterizer_settings)
+
+
+@torch.no_grad()
+def rasterize(means: torch.Tensor, scales: torch.Tensor, rotations: torch.Tensor, opacities: torch.Tensor,
+              rasterizer_settings: RasterizerSettings, to_chw: bool, clamp_output: bool,
+              precomputed_colors: torch.Tensor | None = None, base_colors: torch.Tensor | None = None,
+              residual_params: torch.Tensor | None = None, mlp_weights: torch.Tensor | None = None) -> torch.Tensor:
+    """Inference render: (3, H, W) if to_chw else (H, W, 3), optionally clamped to [0, 1]."""
+    d = means.device
+    mlp_half = mlp_weights.detach().half().contiguous() if mlp_weights is not None else _empty(d, torch.float16)
+    image, _, _, _ = _forward(means, scales, rotations, opacities,
+                              precomputed_colors if precomputed_colors is not None else _empty(d),
+                              base_colors if base_colors is not None else _empty(d),
+                              residual_params if residual_params is not None else _empty(d),
+                              mlp_half, rasterizer_settings)
+    if clamp_output:
+        image = image.clamp_(0.0, 1.0)
+    return image if to_chw else image.permute(1, 2, 0).contiguous()
+
+
+def update_pruning_scores(*args, **kwargs):
+    """Speedy-Splat pruning scores are not part of this build (reference: kernels_pruning_scores.cuh)."""
+    raise NotImplementedError('efgs: update_pruning_scores is not implemented in this build')
+
+
+def frame_views(frame: _lib.Frame) -> _lib.FrameViews:
+    """Device pointers into a forward frame's buffers (inspection for parity tests)."""
+    v = _lib.FrameViews()
+    check(lib.efgs_get_frame_views(ctypes.byref(frame), ctypes.byref(v)))
+    return v
+
+
+def forward_with_frame(means, scales, rotations, opacities, rasterizer_settings: RasterizerSettings, precomputed_colors=None,
+                       base_colors=None, residual_params=None, mlp_weights=None):
+    """Forward pass returning (image, frame, buffers): the frame and the buffers that back it, for inspection."""
+    d = means.device
+    mlp_half = mlp_weights.detach().half().contiguous() if mlp_weights is not None else _empty(d, torch.float16)
+    image, frame, buffers, _ = _forward(means, scales, rotations, opacities,
+                                        precomputed_colors if precomputed_colors is not None else _empty(d),
+                                        base_colors if base_colors is not None else _empty(d),
+                                        residual_params if residual_params is not None else _empty(d),
+                                        mlp_half, rasterizer_settings)
+    return image, frame, buffers

@@ -1,0 +1,189 @@
+/*
+ * efgs.h -- C ABI of the MI355X (gfx950) fused-appearance Gaussian rasterizer (libefgs_hip.so).
+ *
+ * Plain pointers, sizes and POD structs only. Every tensor argument is a device pointer to contiguous fp32
+ * data in the reference's layouts (N x k row-major, quaternions (w, x, y, z), opacity logits, CHW images);
+ * `stream` is a hipStream_t. Functions return EFGS_OK or an error code; efgs_last_error() gives the message
+ * of the calling thread's last failure.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository,
+ * B/ = FasterGSVDACudaBackend/FasterGSVDACudaBackend/):
+ *   _C.set_rtc_dirs ............ B/torch_bindings/bindings.cu:14-28, B/rasterization/src/appearance.cu:16-21
+ *   _C.Rasterizer() ............ B/torch_bindings/rasterization.py:8, B/rasterization/include/appearance.h:18-88
+ *   Rasterizer.set_appearance .. B/rasterization/src/appearance.cu:166-179
+ *   Rasterizer.set_residual_mlp  B/rasterization/src/appearance.cu:181-201
+ *   _C.forward ................. B/rasterization/src/rasterization_api.cu:16-123
+ *   _C.backward ................ B/rasterization/src/rasterization_api.cu:125-247
+ *   _C.adam_step ............... B/adam/src/adam.cu:44-87
+ */
+#ifndef EFGS_H
+#define EFGS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    EFGS_OK = 0,
+    EFGS_ERR_INVALID_ARGUMENT = 1,  /* bad id, size or null pointer */
+    EFGS_ERR_STATE = 2,             /* e.g. forward before set_appearance, set_residual_mlp on a non-neural model */
+    EFGS_ERR_HIP = 3,               /* HIP runtime failure */
+    EFGS_ERR_RTC = 4,               /* hipRTC compilation or module load failure */
+    EFGS_ERR_ALLOC = 5              /* the allocation callback returned NULL */
+};
+
+/* appearance model ids (B/torch_bindings/rasterization.py:21-24); 0 is the internal precomputed-colour variant */
+enum { EFGS_MODEL_PRECOMPUTED = 0, EFGS_MODEL_SH = 1, EFGS_MODEL_SV = 2, EFGS_MODEL_NASG = 3, EFGS_MODEL_NASGABOR = 4, EFGS_MODEL_NEURAL = 5 };
+
+typedef struct efgs_rasterizer efgs_rasterizer;
+
+/* Caller-owned device allocation: returns a device pointer of at least `bytes` bytes (256-byte aligned) that
+ * stays valid until the caller releases it. Used for the forward's persistent buffers (kept for the
+ * backward) and for the backward's temporaries. */
+typedef void* (*efgs_alloc_fn)(void* ctx, size_t bytes);
+
+/* Message of the calling thread's last error (empty if none). */
+const char* efgs_last_error(void);
+
+/* Directory for cached hipRTC code objects and directory holding the preprocess kernel sources.
+ * Replaces _C.set_rtc_dirs(cache, include, kernel_dir): B/rasterization/src/appearance.cu:16-21. */
+int efgs_set_rtc_dirs(const char* cache_dir, const char* kernel_dir);
+
+/* Replaces the _C.Rasterizer singleton (B/torch_bindings/rasterization.py:8). */
+int efgs_rasterizer_create(efgs_rasterizer** out);
+void efgs_rasterizer_destroy(efgs_rasterizer* r);
+
+/* Selects the appearance model and activations and invalidates the specialised kernels (compiled lazily).
+ * model 1..5; base_act 0 none / 1 exp; residual_act 0 none / 1 tanh / 2 softplus; color_act 0 none /
+ * 1 relu / 2 softplus / 3 sigmoid / 4 hardsigmoid / 5 satexp. max_degree: SH degree, SV sites, lobes.
+ * Replaces Rasterizer::set_appearance, B/rasterization/src/appearance.cu:166-179. */
+int efgs_set_appearance(efgs_rasterizer* r, int model, int max_degree, int base_act, int residual_act, int color_act,
+                        int direction_gradient);
+
+/* Residual MLP of the neural model: bias-free, hidden_activation 1 = ReLU (the only one supported),
+ * 'None' output activation, tcnn flat parameter layout (row-major [out x in] matrices, input padded to a
+ * multiple of 16, output padded to 16 rows). sh_degree_mask: bit l = SH degree l in the direction encoding.
+ * Requires efgs_set_appearance(model = 5) first.
+ * Replaces Rasterizer::set_residual_mlp, B/rasterization/src/appearance.cu:181-201. */
+int efgs_set_residual_mlp(efgs_rasterizer* r, int n_input_dims, int n_output_dims, int n_neurons, int n_hidden_layers,
+                          int hidden_activation, int base_input, int n_frequencies, int sh_degree_mask);
+
+/* Number of fp16 parameters of the configured residual MLP (0 if none). */
+int64_t efgs_mlp_param_count(const efgs_rasterizer* r);
+
+/* Camera and render settings: RasterizerSettings, B/torch_bindings/rasterization.py:49-83. */
+typedef struct efgs_settings {
+    const float* w2c;            /* device, >= 12 floats: rows 0..2 of the world-to-view matrix, row-major */
+    const float* cam_position;   /* device, 3 floats */
+    const float* bg_color;       /* device, 3 floats */
+    int appearance_degree;
+    int width, height;
+    float focal_x, focal_y, center_x, center_y;
+    float near_plane, far_plane;
+    int proper_antialiasing;
+    int render_base;
+    int render_residual;         /* 0 renders at appearance degree 0 */
+} efgs_settings;
+
+typedef struct efgs_primitives {
+    int64_t n_primitives;
+    const float* means;               /* (N, 3) */
+    const float* scales;              /* (N, 3) log scales */
+    const float* rotations;           /* (N, 4) (w, x, y, z), unnormalised */
+    const float* opacities;           /* (N, 1) logits */
+    const float* precomputed_colors;  /* (N, 3) or NULL; non-NULL selects the precomputed-colour variant */
+    const float* base_colors;         /* (N, 3) or NULL */
+    const float* residual_params;     /* model-specific (N, ...) or NULL */
+    const uint16_t* mlp_weights;      /* fp16 bits, efgs_mlp_param_count entries, neural only */
+} efgs_primitives;
+
+/* Forward state consumed by the backward. The three buffers are caller-owned allocations made through the
+ * callback during efgs_forward; the scalars describe their layout. */
+typedef struct efgs_frame {
+    void* primitive_buffers;
+    void* tile_buffers;
+    void* instance_buffers;
+    int64_t n_primitives;
+    int64_t n_visible;
+    int64_t n_instances;
+    int32_t grid_width, grid_height;
+    int32_t key_bytes;           /* 2 or 4: width of the tile keys */
+    int32_t depth_sorted_in_b;   /* which ping-pong half holds the depth-sorted pairs */
+    int32_t tiles_sorted_in_b;   /* which ping-pong half holds the tile-sorted pairs */
+    int32_t model;               /* variant used (0 = precomputed colours) */
+} efgs_frame;
+
+/* Renders image (device, 3 x H x W fp32, written) and fills *frame. Blocks once on `stream` to read the
+ * visible-primitive and instance counts (the reference does the same, B/rasterization/src/forward.cu:82-86).
+ * Replaces _C.forward, B/rasterization/src/rasterization_api.cu:16-123. */
+int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image,
+                 efgs_alloc_fn alloc, void* alloc_ctx, efgs_frame* frame, void* stream);
+
+typedef struct efgs_gradients {
+    float* means;                 /* (N, 3) written */
+    float* scales;                /* (N, 3) written */
+    float* rotations;             /* (N, 4) written */
+    float* opacities;             /* (N, 1) written */
+    float* precomputed_colors;    /* (N, 3) written, precomputed variant only */
+    float* base_colors;           /* (N, 3) written */
+    float* residual_params;       /* same shape as the parameters, written */
+    float* mlp_weights;           /* fp32, efgs_mlp_param_count entries, written (neural only) */
+    float* densification_info;    /* (rows, N) accumulated in place, or NULL */
+    int densification_rows;       /* 0, 2 or 3 (3 also accumulates the absolute 2D-mean gradient norm) */
+} efgs_gradients;
+
+/* Gradients of the image with respect to all inputs. Stream-ordered, no host synchronisation. `prims`,
+ * `settings` and `image` must be those of the forward that produced `frame`.
+ * Replaces _C.backward, B/rasterization/src/rasterization_api.cu:125-247. */
+int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, const efgs_frame* frame,
+                  const float* image, const float* grad_image, efgs_gradients* grads, efgs_alloc_fn alloc, void* alloc_ctx,
+                  void* stream);
+
+/* One Adam step over several parameter groups in a single launch. lrs: n_lrs (1..7) learning rates cycled
+ * by element index; step counts from 1.
+ * Replaces _C.adam_step (one launch per group), B/adam/src/adam.cu:44-87. */
+typedef struct efgs_adam_group {
+    const float* grad;
+    float* param;
+    float* exp_avg;
+    float* exp_avg_sq;
+    int64_t n_elements;
+    int64_t step;
+    int32_t n_lrs;
+    int32_t pad_;
+    double lrs[7];
+    double beta1, beta2, eps;
+} efgs_adam_group;
+int efgs_adam_step(const efgs_adam_group* groups, int n_groups, void* stream);
+
+/* Device pointers into a frame's buffers, for inspection (no counterpart in the reference: it lets parity
+ * tests compare keys, orders and tile ranges with the CPU oracle). */
+typedef struct efgs_frame_views {
+    const uint32_t* n_touched;        /* (N) 0 = culled */
+    const uint32_t* depth_keys;       /* (N) float bits of the view depth (valid where n_touched > 0) */
+    const float* records;             /* (N x 12) mean2d xy, conic xyz, opacity, rgb, packed bounds, pad */
+    const uint32_t* depth_sorted_keys;   /* (V) */
+    const uint32_t* depth_sorted_prims;  /* (V) */
+    const uint32_t* instance_offsets;    /* (V) exclusive scan of touched tiles in depth order */
+    const void* tile_sorted_keys;        /* (I) key_bytes wide */
+    const uint32_t* tile_sorted_instances; /* (I) emission index of each sorted instance */
+    const uint32_t* instance_primitive;  /* (I) primitive per emission index */
+    const uint32_t* tile_ranges;         /* (T x 2) [start, end) */
+    const float* final_transmittance;    /* (T x 192) per tile, row-major 16 x 12 */
+    const uint32_t* n_contributors;      /* (T x 192) */
+    const uint32_t* counters;            /* (4) V, I, instance-count mismatches, reserved */
+} efgs_frame_views;
+int efgs_get_frame_views(const efgs_frame* frame, efgs_frame_views* views);
+
+/* Compiles the preprocess kernels of the current configuration into the hipRTC cache for `arch` (e.g.
+ * "gfx950") without using a device (no counterpart in the reference; build step). */
+int efgs_precompile(const efgs_rasterizer* r, const char* arch);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EFGS_H */
