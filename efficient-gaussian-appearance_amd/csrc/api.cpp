@@ -28,7 +28,7 @@ using namespace efgs;
 
 struct efgs_rasterizer {
     bool appearance_set = false;
-    int model = 0;
+    int model = -1;  // -1 until efgs_set_appearance
     int max_degree = 0;
     int base_act = 0;
     int res_act = 0;
@@ -218,12 +218,17 @@ bool get_preprocess_kernel(const efgs_rasterizer* r, int model, const char* kind
     return rtc_get_kernel(name, preamble, files, k);
 }
 
+// 0 (precomputed colours) when colours are supplied, else the configured model; -1 if none is configured
 int variant_of(const efgs_rasterizer* r, const efgs_primitives* prims) {
-    return prims->precomputed_colors != nullptr ? 0 : r->model;
+    if (prims->precomputed_colors != nullptr) return 0;
+    return r->appearance_set ? r->model : -1;
 }
 
 int check_config(const efgs_rasterizer* r, const efgs_primitives* prims, int variant) {
-    if (variant != 0 && !r->appearance_set) return fail(EFGS_ERR_STATE, "appearance model is not initialized (efgs_set_appearance)");
+    if (variant < 0 || (variant != 0 && !r->appearance_set))
+        return fail(EFGS_ERR_STATE, "appearance model is not initialized (efgs_set_appearance)");
+    if (variant == 0 && prims->n_primitives > 0 && !prims->precomputed_colors)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "precomputed_colors are required by the precomputed-colour variant");
     if (variant == 5 && !r->mlp_set) return fail(EFGS_ERR_STATE, "residual mlp is not initialized (efgs_set_residual_mlp)");
     if (prims->n_primitives < 0 || prims->n_primitives >= (1ll << 31)) return fail(EFGS_ERR_INVALID_ARGUMENT, "n_primitives out of range");
     if (prims->n_primitives > 0) {

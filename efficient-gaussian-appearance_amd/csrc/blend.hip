@@ -2,7 +2,8 @@
 // one pixel per lane. Gaussians of the tile are staged 192 at a time in LDS; each wave culls a 64-Gaussian
 // chunk against its band with one 64-bit ballot and walks the surviving bits.
 //
-// Forward: front-to-back compositing, alpha = o exp2(min(q, 0)) with the conic pre-scaled by -log2(e)/2,
+// Forward: front-to-back compositing, alpha = o exp2(min(q, 0)) with the conic pre-scaled by -log2(e)/2 and
+// exp2 from ef_exp2f (a fixed operation sequence, so alpha, T and the image are reproducible bit for bit),
 // alpha < 1/255 skipped, stop at T < 1e-4; stores the image, final T and last-contributor index per pixel and
 // the per-tile maximum. No per-bucket checkpoints.
 //
@@ -36,7 +37,7 @@ __device__ __forceinline__ float eval_alpha(float2 xy, float4 co, float pxf, flo
     dx = xy.x - pxf;
     dy = xy.y - pyf;
     const float q = __builtin_fmaf(dx, __builtin_fmaf(co.x, dx, co.y * dy), co.z * dy * dy);
-    G = __builtin_amdgcn_exp2f(fminf(q, 0.0f));
+    G = ef_exp2f(fminf(q, 0.0f));
     return co.w * G;
 }
 

@@ -95,6 +95,24 @@ __device__ inline float ef_logf(float x) {
     return ef * 0.693145752f + (ef * 1.42860677e-06f + log_m);
 }
 
+// 2^x for x <= 0 (the blend's Gaussian factor): x = k + r with k = rint(x) and |r| <= 1/2 (r exact), 2^r by its
+// degree-7 Taylor series in r ln2 evaluated with fused multiply-adds, scaled by 2^k; 0 below -126, where
+// alpha = opacity * 2^x is far under the 1/255 threshold.
+__device__ inline float ef_exp2f(float x) {
+#pragma clang fp contract(off)
+    if (!(x >= -126.0f)) return 0.0f;
+    const float k = __builtin_rintf(x);
+    const float r = x - k;
+    float p = __builtin_fmaf(1.52527338e-05f, r, 1.54035304e-04f);
+    p = __builtin_fmaf(p, r, 1.33335581e-03f);
+    p = __builtin_fmaf(p, r, 9.61812911e-03f);
+    p = __builtin_fmaf(p, r, 5.55041087e-02f);
+    p = __builtin_fmaf(p, r, 2.40226507e-01f);
+    p = __builtin_fmaf(p, r, 6.93147181e-01f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return p * ef_pow2i(static_cast<int>(k));
+}
+
 __device__ __forceinline__ float ef_sigmoid(float x) {
 #pragma clang fp contract(off)
     return 1.0f / (1.0f + ef_expf(-x));

@@ -106,6 +106,30 @@ float ef_logf(float x) {
 }
 
 static float ef_sigmoid(float x) { return 1.0f / (1.0f + ef_expf(-x)); }
+
+/* 2^x for x <= 0: k = rint(x), r = x - k exact, degree-7 Taylor series of 2^r in r ln2 with fused
+ * multiply-adds, scaled by 2^k; 0 below -126. */
+float ef_exp2f(float x) {
+    if (!(x >= -126.0f)) return 0.0f;
+    const float k = rintf(x);
+    const float r = x - k;
+    float p = fmaf(1.52527338e-05f, r, 1.54035304e-04f);
+    p = fmaf(p, r, 1.33335581e-03f);
+    p = fmaf(p, r, 9.61812911e-03f);
+    p = fmaf(p, r, 5.55041087e-02f);
+    p = fmaf(p, r, 2.40226507e-01f);
+    p = fmaf(p, r, 6.93147181e-01f);
+    p = fmaf(p, r, 1.0f);
+    return p * ef_pow2i((int)k);
+}
+
+/* exponent of the exp2-scaled conic (ex, ey, ez) at offset (dx, dy), with two fused multiply-adds: the
+ * contraction nvcc applies to kernels_forward.cuh:124 by default, fixed here so host and device agree */
+static float blend_exponent(float ex, float ey, float ez, float dx, float dy) {
+    return fmaf(dx, fmaf(ex, dx, ey * dy), ez * dy * dy);
+}
+
+
 static float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
 static float saturatef(float x) { return fminf(fmaxf(x, 0.0f), 1.0f); }
 
@@ -560,17 +584,17 @@ void efo_blend_forward(
                 const float* co = conic_opacity + 4 * p;
                 const float ex = -0.5f * log2e * co[0], ey = -log2e * co[1], ez = -0.5f * log2e * co[2];
                 const float dx = mean2d[2 * p] - pxf, dy = mean2d[2 * p + 1] - pyf;
-                const float e = dx * (ex * dx + ey * dy) + ez * dy * dy;
-                const float g = exp2f(fminf(e, 0.0f));
+                const float g = ef_exp2f(fminf(blend_exponent(ex, ey, ez, dx, dy), 0.0f));
                 const float alpha = co[3] * g;
                 if (alpha < K_MIN_ALPHA) continue;
-                for (int c = 0; c < 3; c++) C[c] += T * alpha * color[3 * p + c];
+                const float w = T * alpha;
+                for (int c = 0; c < 3; c++) C[c] = fmaf(w, color[3 * p + c], C[c]);
                 T *= 1.0f - alpha;
                 last = i - r0 + 1;
                 if (T < k_transmittance_threshold) break;
             }
             const int pix = py * width + px;
-            for (int c = 0; c < 3; c++) image[c * n_pixels + pix] = C[c] + T * bg[c];
+            for (int c = 0; c < 3; c++) image[c * n_pixels + pix] = fmaf(T, bg[c], C[c]);
             final_T[pix] = T;
             n_contrib[pix] = last;
         }
@@ -620,8 +644,7 @@ void efo_blend_backward(
                 const float* co = conic_opacity + 4 * p;
                 const float ex = -0.5f * log2e * co[0], ey = -log2e * co[1], ez = -0.5f * log2e * co[2];
                 const float dx = mean2d[2 * p] - pxf, dy = mean2d[2 * p + 1] - pyf;
-                const float e = dx * (ex * dx + ey * dy) + ez * dy * dy;
-                const float G = exp2f(fminf(e, 0.0f));
+                const float G = ef_exp2f(fminf(blend_exponent(ex, ey, ez, dx, dy), 0.0f));
                 const float alpha = co[3] * G;
                 if (alpha < K_MIN_ALPHA) continue;
                 const float w = T * alpha;
@@ -1006,4 +1029,30 @@ void efo_adam_step(int n, const float* grad, float* param, float* m, float* v, i
         m[i] = m1;
         v[i] = m2;
     }
+}
+
+/* ------------------------------------------------------------------------------------------------------ */
+/* helpers exposed for closed-form tests                                                                  */
+/* ------------------------------------------------------------------------------------------------------ */
+
+/* rest-band SH basis values (15) of a unit direction, band order of appearance_sh.cuh:43-61 */
+int efo_sh_rest_basis(const float* dir, int degree, float* out) { return sh_rest_basis(dir, degree, out); }
+
+/* activated residual colour of one primitive for the SH / SV / NASG / NASGabor models */
+void efo_residual(const efo_app* a, const float* params, const float* dir, int degree, float* out) {
+    switch (a->model) {
+        case 1: sh_residual(a, params, dir, degree, out); break;
+        case 2: sv_residual(a, params, dir, degree, out); break;
+        case 3: lobe_residual(a, params, dir, degree, 0, out); break;
+        case 4: lobe_residual(a, params, dir, degree, 1, out); break;
+        default: out[0] = out[1] = out[2] = 0.0f;
+    }
+}
+
+/* alpha of a Gaussian (mean2d, conic, opacity) at pixel centre (px + 0.5, py + 0.5), as the blend computes it */
+float efo_blend_alpha(float mx, float my, float cx, float cy, float cz, float opacity, int px, int py) {
+    const float log2e = 1.44269504089f;
+    const float ex = -0.5f * log2e * cx, ey = -log2e * cy, ez = -0.5f * log2e * cz;
+    const float dx = mx - ((float)px + 0.5f), dy = my - ((float)py + 0.5f);
+    return opacity * ef_exp2f(fminf(blend_exponent(ex, ey, ez, dx, dy), 0.0f));
 }

@@ -71,6 +71,11 @@ def lib() -> ctypes.CDLL:
         _lib.efo_create_instances.restype = ctypes.c_uint32
         _lib.efo_will_primitive_contribute.restype = ctypes.c_int
         _lib.efo_will_primitive_contribute.argtypes = [ctypes.c_float] * 5 + [ctypes.c_uint32] * 2 + [ctypes.c_float]
+        _lib.ef_exp2f.restype = ctypes.c_float
+        _lib.ef_exp2f.argtypes = [ctypes.c_float]
+        _lib.efo_blend_alpha.restype = ctypes.c_float
+        _lib.efo_blend_alpha.argtypes = [ctypes.c_float] * 6 + [ctypes.c_int] * 2
+        _lib.efo_sh_rest_basis.restype = ctypes.c_int
     return _lib
 
 
@@ -629,3 +634,25 @@ def ef_exp(x: float) -> float:
 
 def ef_log(x: float) -> float:
     return lib().ef_logf(ctypes.c_float(x))
+
+
+def ef_exp2(x: float) -> float:
+    return lib().ef_exp2f(ctypes.c_float(x))
+
+
+def blend_alpha(mean2d, conic_opacity, px: int, py: int) -> float:
+    co = conic_opacity
+    return lib().efo_blend_alpha(float(mean2d[0]), float(mean2d[1]), float(co[0]), float(co[1]), float(co[2]), float(co[3]), px, py)
+
+
+def sh_rest_basis(direction, degree: int) -> np.ndarray:
+    out = np.zeros(15, np.float32)
+    d = _f32(direction)
+    n = lib().efo_sh_rest_basis(_p(d), ctypes.c_int(degree), _p(out))
+    return out[:n]
+
+
+def residual(app: 'Appearance', params: np.ndarray, direction, degree: int) -> np.ndarray:
+    out = np.zeros(3, np.float32)
+    lib().efo_residual(ctypes.byref(app.c_struct()), _p(_f32(params).reshape(-1)), _p(_f32(direction)), ctypes.c_int(degree), _p(out))
+    return out

