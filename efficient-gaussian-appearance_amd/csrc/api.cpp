@@ -219,6 +219,30 @@ bool get_preprocess_kernel(const efgs_rasterizer* r, int model, const char* kind
 }
 
 // 0 (precomputed colours) when colours are supplied, else the configured model; -1 if none is configured
+uint32_t mlp_params(const efgs_rasterizer* r) {
+    const uint32_t n = static_cast<uint32_t>(r->mlp_n_neurons);
+    return n * static_cast<uint32_t>(r->mlp_n_in_padded) + static_cast<uint32_t>(r->mlp_n_hidden - 1) * n * n + 16 * n;
+}
+
+// dynamic LDS of the neural preprocess kernels: fp16 weights + 4 per-wave staging areas (forward); the
+// backward reuses the area for the fp32 block reduction of the weight gradients
+uint32_t mlp_smem_forward(const efgs_rasterizer* r) {
+    const uint32_t inp = static_cast<uint32_t>(r->mlp_n_in_padded), nn = static_cast<uint32_t>(r->mlp_n_neurons);
+    const uint32_t maxk = inp > nn ? inp : nn;
+    const uint32_t row = maxk > 2 * inp ? maxk : 2 * inp;
+    const uint32_t weight_bytes = (mlp_params(r) * 2 + 15) / 16 * 16;
+    return weight_bytes + 4 * 64 * row * 2;
+}
+
+uint32_t mlp_smem_backward(const efgs_rasterizer* r) {
+    const uint32_t f = mlp_smem_forward(r), red = mlp_params(r) * 4;
+    return f > red ? f : red;
+}
+
+constexpr uint32_t max_dynamic_lds = 64 * 1024;
+constexpr uint32_t neural_forward_blocks = 1024;
+constexpr uint32_t neural_backward_blocks = 512;
+
 int variant_of(const efgs_rasterizer* r, const efgs_primitives* prims) {
     if (prims->precomputed_colors != nullptr) return 0;
     return r->appearance_set ? r->model : -1;
@@ -238,6 +262,8 @@ int check_config(const efgs_rasterizer* r, const efgs_primitives* prims, int var
         if (variant != 0 && n_units_of(r, variant) > 0 && !prims->residual_params)
             return fail(EFGS_ERR_INVALID_ARGUMENT, "residual_params are required by the appearance model");
         if (variant == 5 && !prims->mlp_weights) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp_weights are required by the neural model");
+        if (variant == 5 && (reinterpret_cast<uintptr_t>(prims->mlp_weights) & 15u) != 0)
+            return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp_weights must be 16-byte aligned");
     }
     return EFGS_OK;
 }
@@ -268,9 +294,9 @@ CameraArgs camera_args(const efgs_rasterizer* r, const efgs_settings* s, int var
     return c;
 }
 
-bool launch_rtc(const RtcKernel& k, uint32_t blocks, uint32_t threads, void* args, hipStream_t s) {
+bool launch_rtc(const RtcKernel& k, uint32_t blocks, uint32_t threads, uint32_t shared_bytes, void* args, hipStream_t s) {
     void* params[] = {args};
-    EFGS_HIP_CHECK(hipModuleLaunchKernel(k.function, blocks, 1, 1, threads, 1, 1, 0, s, params, nullptr));
+    EFGS_HIP_CHECK(hipModuleLaunchKernel(k.function, blocks, 1, 1, threads, 1, 1, shared_bytes, s, params, nullptr));
     return true;
 }
 
@@ -343,6 +369,12 @@ int efgs_set_residual_mlp(efgs_rasterizer* r, int n_input_dims, int n_output_dim
     const int features = raw_features - (base_input ? 3 : 0);
     if (features < 1) return fail(EFGS_ERR_INVALID_ARGUMENT, "no learned features left for the residual mlp");
     if (n_input_dims > 128) return fail(EFGS_ERR_INVALID_ARGUMENT, "n_input_dims above 128 is not supported");
+    efgs_rasterizer probe = *r;
+    probe.mlp_n_in_padded = (n_input_dims + 15) / 16 * 16;
+    probe.mlp_n_neurons = n_neurons;
+    probe.mlp_n_hidden = n_hidden_layers;
+    if (mlp_smem_backward(&probe) > max_dynamic_lds)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "the residual mlp exceeds the 64 KiB LDS budget of the fused kernels");
     r->mlp_set = true;
     r->mlp_n_in = n_input_dims;
     r->mlp_n_in_padded = (n_input_dims + 15) / 16 * 16;
@@ -370,7 +402,6 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     if (!settings->w2c || !settings->cam_position || !settings->bg_color) return fail(EFGS_ERR_INVALID_ARGUMENT, "camera tensors are required");
     const int variant = variant_of(r, prims);
     if (int c = check_config(r, prims, variant)) return c;
-    if (variant == 5) return fail(EFGS_ERR_STATE, "the neural appearance kernels are not available in this build");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint32_t n = static_cast<uint32_t>(prims->n_primitives);
     const uint32_t grid_w = div_up(settings->width, tile_width), grid_h = div_up(settings->height, tile_height);
@@ -411,9 +442,11 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         a.block_counts = pl.block_counts;
         a.n = n;
         a.cam = cam;
-        const uint32_t blocks = div_up(n, preprocess_block);
-        if (!launch_rtc(k, blocks, preprocess_block, &a, s)) return EFGS_ERR_HIP;
-        if (!launch_scan_block_counts(pl.block_counts, pl.block_offsets, pl.counters, blocks, s)) return EFGS_ERR_HIP;
+        const uint32_t chunks = div_up(n, preprocess_block);
+        const uint32_t blocks = variant == 5 ? (chunks < neural_forward_blocks ? chunks : neural_forward_blocks) : chunks;
+        const uint32_t shared = variant == 5 ? mlp_smem_forward(r) : 0u;
+        if (!launch_rtc(k, blocks, preprocess_block, shared, &a, s)) return EFGS_ERR_HIP;
+        if (!launch_scan_block_counts(pl.block_counts, pl.block_offsets, pl.counters, chunks, s)) return EFGS_ERR_HIP;
         if (!launch_compact_visible(pl.n_touched, pl.depth_keys, pl.block_offsets, pl.keys_a, pl.vals_a, n, s)) return EFGS_ERR_HIP;
     } else {
         if (!launch_fill_u32(pl.counters, 0u, 4, s)) return EFGS_ERR_HIP;
@@ -550,7 +583,19 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     a.densification_rows = static_cast<uint32_t>(grads->densification_rows);
     a.n = n;
     a.cam = camera_args(r, settings, variant, grid_w, grid_h);
-    if (!launch_rtc(k, div_up(n, preprocess_block), preprocess_block, &a, s)) return EFGS_ERR_HIP;
+    const uint32_t chunks = div_up(n, preprocess_block);
+    if (variant != 5) {
+        if (!launch_rtc(k, chunks, preprocess_block, 0u, &a, s)) return EFGS_ERR_HIP;
+        return EFGS_OK;
+    }
+    if (!grads->mlp_weights) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp weight gradient output is required");
+    const uint32_t blocks = chunks < neural_backward_blocks ? chunks : neural_backward_blocks;
+    const uint32_t params = mlp_params(r);
+    float* partials = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(blocks) * params * sizeof(float)));
+    if (!partials) return fail(EFGS_ERR_ALLOC, "allocation of the mlp gradient partials failed");
+    a.g_mlp_partials = partials;
+    if (!launch_rtc(k, blocks, preprocess_block, mlp_smem_backward(r), &a, s)) return EFGS_ERR_HIP;
+    if (!launch_reduce_partials(partials, blocks, params, grads->mlp_weights, s)) return EFGS_ERR_HIP;
     return EFGS_OK;
 }
 
@@ -613,7 +658,6 @@ int efgs_precompile(const efgs_rasterizer* r, const char* arch) {
     std::vector<int> variants = {0};
     if (r->appearance_set && (r->model != 5 || r->mlp_set)) variants.push_back(r->model);
     for (int variant : variants) {
-        if (variant == 5) continue;
         for (const char* kind : {"forward", "backward"}) {
             std::string name, preamble;
             std::vector<std::string> files;

@@ -55,6 +55,7 @@ bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_key
 bool launch_create_instances(const uint32_t* sorted_prims, const uint32_t* offsets, const uint32_t* n_touched,
                              const PrimRecord* records, void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* prim_offset,
                              uint32_t* counters, uint32_t grid_w, uint32_t n_visible, hipStream_t s);
+bool launch_reduce_partials(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out, hipStream_t s);
 bool launch_tile_ranges(const void* keys, int key_bytes, uint2* ranges, uint32_t n_instances, uint32_t n_tiles, hipStream_t s);
 
 struct BlendForwardArgs {

@@ -102,6 +102,15 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
     }
 }
 
+// out[i] = sum over blocks b (in order) of partials[b][i]
+__global__ void reduce_partials_kernel(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_params) return;
+    float s = 0.0f;
+    for (uint32_t b = 0; b < n_blocks; b++) s += partials[static_cast<size_t>(b) * n_params + i];
+    out[i] = s;
+}
+
 template <typename KeyT>
 __global__ void tile_ranges_kernel(const KeyT* keys, uint2* ranges, uint32_t n_instances, uint32_t n_tiles) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -143,6 +152,13 @@ bool launch_create_instances(const uint32_t* sorted_prims, const uint32_t* offse
     else
         create_instances_kernel<uint32_t><<<blocks, instance_block, 0, s>>>(sorted_prims, offsets, n_touched, records, static_cast<uint32_t*>(keys),
                                                                            inst_prim, prim_offset, counters, grid_w, n_visible);
+    EFGS_HIP_CHECK(hipGetLastError());
+    return true;
+}
+
+bool launch_reduce_partials(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out, hipStream_t s) {
+    if (n_params == 0) return true;
+    reduce_partials_kernel<<<div_up(n_params, 256), 256, 0, s>>>(partials, n_blocks, n_params, out);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

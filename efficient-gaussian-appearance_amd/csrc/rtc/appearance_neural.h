@@ -1,0 +1,370 @@
+// Neural residual (EFGS_MODEL == 5): a bias-free ReLU MLP over per-Gaussian features (optionally frequency
+// encoded, optionally with the base colour as 3 extra inputs) and the SH degree values of the view
+// direction, evaluated per wave of 64 primitives with fp16 MFMA (v_mfma_f32_16x16x16f16) and fp32
+// accumulation; weights live in LDS in the tcnn flat layout (row-major [out x in] per layer, input padded to
+// a multiple of 16, output padded to 16 rows).
+//
+// Layout: each layer computes H_out^T = W H_in^T with the weights as the A operand and the activations as the
+// B operand, so a 16x16 accumulator tile (lane l: rows 4(l/16)..+3, column l%16) is exactly the B fragment
+// of the next layer's matching k-block: no data movement between layers. Activations are rounded to fp16
+// between layers (as tcnn's half-precision network), the 3 outputs are rounded to fp16.
+//
+// Backward: the forward is recomputed (no stored context). The upstream gradient of the wave is scaled by a
+// power of two so its maximum lies in [256, 512) before the fp16 MFMA chain, and unscaled in fp32. Weight
+// gradients dW = G X accumulate per wave in fp32 registers (operands transposed through LDS), then are reduced
+// across the block's waves in a fixed order.
+//
+// Reference: B/rasterization/rtc/appearance_neural.cuh:17-407 (encoding, SH degree values and their
+// gradient, tcnn eval_model / backward_eval_model at :333, :379); weight layout viewer/export_ngsplat.py:1013-1029.
+#pragma once
+
+namespace efgs {
+
+namespace nn {
+
+constexpr uint32_t IN = EFGS_MLP_N_IN;            // unpadded input width
+constexpr uint32_t INP = EFGS_MLP_N_IN_PADDED;    // padded to a multiple of 16
+constexpr uint32_t NN = EFGS_MLP_N_NEURONS;
+constexpr uint32_t NH = EFGS_MLP_N_HIDDEN;
+constexpr uint32_t NL = NH + 1;                   // weight matrices
+constexpr uint32_t OUTP = 16;
+constexpr uint32_t MAXK = INP > NN ? INP : NN;
+constexpr uint32_t KT = MAXK / 16;
+constexpr uint32_t NT = NN / 16;
+constexpr uint32_t FEATURES = EFGS_N_UNITS;
+constexpr uint32_t RAW_FEATURES = FEATURES + (EFGS_BASE_INPUT ? 3u : 0u);
+constexpr uint32_t ENCODED = EFGS_N_FREQUENCIES == 0 ? RAW_FEATURES : RAW_FEATURES * 2u * EFGS_N_FREQUENCIES;
+constexpr uint32_t PARAMS = NN * INP + (NH - 1) * NN * NN + OUTP * NN;
+constexpr uint32_t STAGE_ROW = MAXK > 2 * INP ? MAXK : 2 * INP;
+constexpr uint32_t STAGE_HALVES = 64 * STAGE_ROW;  // per-wave LDS staging: 64 rows of MAXK halves or INP floats
+constexpr uint32_t WEIGHT_BYTES = (PARAMS * 2 + 15) / 16 * 16;
+
+__device__ constexpr uint32_t lin(uint32_t l) { return l == 0 ? INP : NN; }
+__device__ constexpr uint32_t lout(uint32_t l) { return l == NH ? OUTP : NN; }
+__device__ constexpr uint32_t loff(uint32_t l) { return l == 0 ? 0u : NN * INP + (l - 1) * NN * NN; }
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ f4 f4_zero() { return f4{0.0f, 0.0f, 0.0f, 0.0f}; }
+__device__ __forceinline__ float round_half(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
+__device__ __forceinline__ void wave_sync() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront"); __builtin_amdgcn_wave_barrier(); __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront"); }
+
+// forward-mode dual number (value and d/dx, d/dy, d/dz of the direction) for the SH degree derivatives
+struct D3 {
+    float v, x, y, z;
+};
+__device__ __forceinline__ D3 operator+(D3 a, D3 b) { return {a.v + b.v, a.x + b.x, a.y + b.y, a.z + b.z}; }
+__device__ __forceinline__ D3 operator-(D3 a, D3 b) { return {a.v - b.v, a.x - b.x, a.y - b.y, a.z - b.z}; }
+__device__ __forceinline__ D3 operator-(D3 a) { return {-a.v, -a.x, -a.y, -a.z}; }
+__device__ __forceinline__ D3 operator*(D3 a, D3 b) { return {a.v * b.v, a.x * b.v + a.v * b.x, a.y * b.v + a.v * b.y, a.z * b.v + a.v * b.z}; }
+__device__ __forceinline__ D3 operator*(float s, D3 a) { return {s * a.v, s * a.x, s * a.y, s * a.z}; }
+__device__ __forceinline__ D3 operator*(D3 a, float s) { return s * a; }
+__device__ __forceinline__ D3 operator+(D3 a, float s) { return {a.v + s, a.x, a.y, a.z}; }
+__device__ __forceinline__ D3 operator-(D3 a, float s) { return {a.v - s, a.x, a.y, a.z}; }
+__device__ __forceinline__ D3 operator-(float s, D3 a) { return {s - a.v, -a.x, -a.y, -a.z}; }
+__device__ __forceinline__ float sh_value(float v) { return v; }
+__device__ __forceinline__ float sh_value(D3 v) { return v.v; }
+
+constexpr float sh_c0 = 0.28209479177387814f;
+
+// SH degree values of the direction for the degrees of EFGS_SH_DEGREE_MASK (ascending); degree 0 is never
+// gated, the i-th degree >= 1 is zero unless i < active_degree. emit(index, value) receives every value.
+template <typename T, typename EMIT>
+__device__ inline void sh_degree_values(T x, T y, T z, uint32_t active_degree, EMIT&& emit) {
+    constexpr uint32_t mask = EFGS_SH_DEGREE_MASK;
+    const T xy = x * y, xz = x * z, yz = y * z, x2 = x * x, y2 = y * y, z2 = z * z;
+    const T x4 = x2 * x2, y4 = y2 * y2, z4 = z2 * z2;
+    const T x6 = x4 * x2, y6 = y4 * y2, z6 = z4 * z2;
+    uint32_t o = 0, rank = 0;
+    if (mask & 1u) { emit(o, T{} + sh_c0); o += 1; }
+    if (mask & 2u) {
+        const float m = rank++ < active_degree ? 1.0f : 0.0f;
+        emit(o + 0, m * (-0.48860251190291987f * y)); emit(o + 1, m * (0.48860251190291987f * z)); emit(o + 2, m * (-0.48860251190291987f * x));
+        o += 3;
+    }
+    if (mask & 4u) {
+        const float m = rank++ < active_degree ? 1.0f : 0.0f;
+        emit(o + 0, m * (1.0925484305920792f * xy)); emit(o + 1, m * (-1.0925484305920792f * yz));
+        emit(o + 2, m * (0.94617469575755997f * z2 - 0.31539156525251999f)); emit(o + 3, m * (-1.0925484305920792f * xz));
+        emit(o + 4, m * (0.54627421529603959f * x2 - 0.54627421529603959f * y2));
+        o += 5;
+    }
+    if (mask & 8u) {
+        const float m = rank++ < active_degree ? 1.0f : 0.0f;
+        emit(o + 0, m * (0.59004358992664352f * y * (-3.0f * x2 + y2))); emit(o + 1, m * (2.8906114426405538f * xy * z));
+        emit(o + 2, m * (0.45704579946446572f * y * (1.0f - 5.0f * z2))); emit(o + 3, m * (0.3731763325901154f * z * (5.0f * z2 - 3.0f)));
+        emit(o + 4, m * (0.45704579946446572f * x * (1.0f - 5.0f * z2))); emit(o + 5, m * (1.4453057213202769f * z * (x2 - y2)));
+        emit(o + 6, m * (0.59004358992664352f * x * (-x2 + 3.0f * y2)));
+        o += 7;
+    }
+    if (mask & 16u) {
+        const float m = rank++ < active_degree ? 1.0f : 0.0f;
+        emit(o + 0, m * (2.5033429417967046f * xy * (x2 - y2))); emit(o + 1, m * (1.7701307697799304f * yz * (-3.0f * x2 + y2)));
+        emit(o + 2, m * (0.94617469575756008f * xy * (7.0f * z2 - 1.0f))); emit(o + 3, m * (0.66904654355728921f * yz * (3.0f - 7.0f * z2)));
+        emit(o + 4, m * (-3.1735664074561294f * z2 + 3.7024941420321507f * z4 + 0.31735664074561293f));
+        emit(o + 5, m * (0.66904654355728921f * xz * (3.0f - 7.0f * z2))); emit(o + 6, m * (0.47308734787878004f * (x2 - y2) * (7.0f * z2 - 1.0f)));
+        emit(o + 7, m * (1.7701307697799304f * xz * (-x2 + 3.0f * y2)));
+        emit(o + 8, m * (-3.7550144126950569f * x2 * y2 + 0.62583573544917614f * x4 + 0.62583573544917614f * y4));
+        o += 9;
+    }
+    if (mask & 32u) {
+        const float m = rank++ < active_degree ? 1.0f : 0.0f;
+        emit(o + 0, m * (0.65638205684017015f * y * (10.0f * x2 * y2 - 5.0f * x4 - y4))); emit(o + 1, m * (8.3026492595241645f * xy * z * (x2 - y2)));
+        emit(o + 2, m * (-0.48923829943525038f * y * (3.0f * x2 - y2) * (9.0f * z2 - 1.0f)));
+        emit(o + 3, m * (4.7935367849733241f * xy * z * (3.0f * z2 - 1.0f)));
+        emit(o + 4, m * (0.45294665119569694f * y * (14.0f * z2 - 21.0f * z4 - 1.0f)));
+        emit(o + 5, m * (0.1169503224534236f * z * (-70.0f * z2 + 63.0f * z4 + 15.0f)));
+        emit(o + 6, m * (0.45294665119569694f * x * (14.0f * z2 - 21.0f * z4 - 1.0f)));
+        emit(o + 7, m * (2.3967683924866621f * z * (x2 - y2) * (3.0f * z2 - 1.0f)));
+        emit(o + 8, m * (-0.48923829943525038f * x * (x2 - 3.0f * y2) * (9.0f * z2 - 1.0f)));
+        emit(o + 9, m * (2.0756623148810411f * z * (-6.0f * x2 * y2 + x4 + y4)));
+        emit(o + 10, m * (0.65638205684017015f * x * (10.0f * x2 * y2 - x4 - 5.0f * y4)));
+        o += 11;
+    }
+    if (mask & 64u) {
+        const float m = rank++ < active_degree ? 1.0f : 0.0f;
+        emit(o + 0, m * (1.3663682103838286f * xy * (-10.0f * x2 * y2 + 3.0f * x4 + 3.0f * y4)));
+        emit(o + 1, m * (2.3666191622317521f * yz * (10.0f * x2 * y2 - 5.0f * x4 - y4)));
+        emit(o + 2, m * (2.0182596029148963f * xy * (x2 - y2) * (11.0f * z2 - 1.0f)));
+        emit(o + 3, m * (-0.92120525951492349f * yz * (3.0f * x2 - y2) * (11.0f * z2 - 3.0f)));
+        emit(o + 4, m * (0.92120525951492349f * xy * (-18.0f * z2 + 33.0f * z4 + 1.0f)));
+        emit(o + 5, m * (0.58262136251873131f * yz * (30.0f * z2 - 33.0f * z4 - 5.0f)));
+        emit(o + 6, m * (6.6747662381009842f * z2 - 20.024298714302954f * z4 + 14.684485723822165f * z6 - 0.31784601133814211f));
+        emit(o + 7, m * (0.58262136251873131f * xz * (30.0f * z2 - 33.0f * z4 - 5.0f)));
+        emit(o + 8, m * (0.46060262975746175f * (x2 - y2) * (11.0f * z2 * (3.0f * z2 - 1.0f) - 7.0f * z2 + 1.0f)));
+        emit(o + 9, m * (-0.92120525951492349f * xz * (x2 - 3.0f * y2) * (11.0f * z2 - 3.0f)));
+        emit(o + 10, m * (0.50456490072872406f * (11.0f * z2 - 1.0f) * (-6.0f * x2 * y2 + x4 + y4)));
+        emit(o + 11, m * (2.3666191622317521f * xz * (10.0f * x2 * y2 - x4 - 5.0f * y4)));
+        emit(o + 12, m * (10.247761577878714f * x2 * y4 - 10.247761577878714f * x4 * y2 + 0.6831841051919143f * x6 - 0.6831841051919143f * y6));
+        o += 13;
+    }
+}
+
+// raw feature i of a primitive: learned features, then (with base input) the 3 base values
+__device__ __forceinline__ float raw_feature(const float* feat, const float* base, uint32_t i) {
+    return i < FEATURES ? feat[i] : base[i - FEATURES];
+}
+
+// the lane's MLP input row (INP floats, zero padded): encoded features, then the direction's SH degree values
+__device__ inline void mlp_input(const float* feat, const float* base, float3 d, uint32_t degree, float* x) {
+#pragma unroll
+    for (uint32_t k = 0; k < INP; k++) x[k] = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < RAW_FEATURES; i++) {
+        const float v = raw_feature(feat, base, i);
+        if (EFGS_N_FREQUENCIES == 0) {
+            x[i] = v;
+        } else {
+#pragma unroll
+            for (uint32_t f = 0; f < EFGS_N_FREQUENCIES; f++) {
+                float s, c;
+                sincosf(ldexpf(v, static_cast<int>(f)), &s, &c);
+                x[i * 2 * EFGS_N_FREQUENCIES + 2 * f] = s;
+                x[i * 2 * EFGS_N_FREQUENCIES + 2 * f + 1] = c;
+            }
+        }
+    }
+    sh_degree_values(d.x, d.y, d.z, degree, [&](uint32_t k, float v) { x[ENCODED + k] = v; });
+}
+
+// d(loss)/d(raw feature i) from the input gradient row (frequency encoding chain)
+__device__ inline float feature_grad(float v, const float* dx, uint32_t i) {
+    if (EFGS_N_FREQUENCIES == 0) return dx[i];
+    float g = 0.0f;
+#pragma unroll
+    for (uint32_t f = 0; f < EFGS_N_FREQUENCIES; f++) {
+        float s, c;
+        sincosf(ldexpf(v, static_cast<int>(f)), &s, &c);
+        g += static_cast<float>(1u << f) * (c * dx[i * 2 * EFGS_N_FREQUENCIES + 2 * f] - s * dx[i * 2 * EFGS_N_FREQUENCIES + 2 * f + 1]);
+    }
+    return g;
+}
+
+// d(loss)/d(direction) through the SH degree values (forward-mode duals)
+__device__ inline float3 direction_grad(float3 d, uint32_t degree, const float* dx) {
+    const D3 X{d.x, 1.0f, 0.0f, 0.0f}, Y{d.y, 0.0f, 1.0f, 0.0f}, Z{d.z, 0.0f, 0.0f, 1.0f};
+    float3 g = make_float3(0.0f, 0.0f, 0.0f);
+    sh_degree_values(X, Y, Z, degree, [&](uint32_t k, D3 v) {
+        const float w = dx[ENCODED + k];
+        g.x += w * v.x;
+        g.y += w * v.y;
+        g.z += w * v.z;
+    });
+    return g;
+}
+
+// Per-wave MLP forward. W: the weights in LDS (fp16 bits); stage: this wave's LDS staging; x: the lane's input
+// row. Leaves the input activations of every layer in act (B fragments) and the fp16-rounded outputs in y.
+__device__ inline void mlp_forward(const uint16_t* W, _Float16* stage, const float* x, h4 (&act)[NL][KT][4], float* y, uint32_t lane) {
+    const uint32_t r = lane & 15u, q = lane >> 4;
+#pragma unroll
+    for (uint32_t k = 0; k < INP; k++) stage[lane * MAXK + k] = static_cast<_Float16>(x[k]);
+    wave_sync();
+#pragma unroll
+    for (uint32_t kb = 0; kb < INP / 16; kb++)
+#pragma unroll
+        for (uint32_t cb = 0; cb < 4; cb++) act[0][kb][cb] = *reinterpret_cast<const h4*>(&stage[(cb * 16 + r) * MAXK + kb * 16 + 4 * q]);
+    wave_sync();
+#pragma unroll
+    for (uint32_t l = 0; l < NL; l++) {
+        f4 acc[NT > 1 ? NT : 1][4];
+#pragma unroll
+        for (uint32_t rb = 0; rb < lout(l) / 16; rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = f4_zero();
+#pragma unroll
+        for (uint32_t rb = 0; rb < lout(l) / 16; rb++) {
+#pragma unroll
+            for (uint32_t kb = 0; kb < lin(l) / 16; kb++) {
+                const h4 a = *reinterpret_cast<const h4*>(&W[loff(l) + (rb * 16 + r) * lin(l) + kb * 16 + 4 * q]);
+#pragma unroll
+                for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = mfma(a, act[l][kb][cb], acc[rb][cb]);
+            }
+        }
+        if (l < NH) {
+#pragma unroll
+            for (uint32_t rb = 0; rb < lout(l) / 16; rb++)
+#pragma unroll
+                for (uint32_t cb = 0; cb < 4; cb++) {
+                    const f4 v = acc[rb][cb];
+                    act[l + 1][rb][cb] = h4{static_cast<_Float16>(fmaxf(v[0], 0.0f)), static_cast<_Float16>(fmaxf(v[1], 0.0f)),
+                                            static_cast<_Float16>(fmaxf(v[2], 0.0f)), static_cast<_Float16>(fmaxf(v[3], 0.0f))};
+                }
+        } else {
+            // outputs 0..2 of primitive 16 cb + c sit in lane c of tile cb
+#pragma unroll
+            for (uint32_t o = 0; o < 3; o++) {
+                float v = 0.0f;
+#pragma unroll
+                for (uint32_t cb = 0; cb < 4; cb++) {
+                    const float t = __shfl(acc[0][cb][o], static_cast<int>(r));
+                    if (q == cb) v = t;
+                }
+                y[o] = round_half(v);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Per-wave MLP backward. dy: the lane's gradient of the 3 raw outputs (zero for lanes that do not contribute);
+// act from mlp_forward. Writes the lane's input gradient row dx (INP floats) and adds the wave's weight gradients
+// to dW (fp32 accumulator tiles, lane layout of the D operand).
+__device__ inline void mlp_backward(const uint16_t* W, _Float16* stage, const h4 (&act)[NL][KT][4], const float* dy, float* dx,
+                                    f4 (&dW)[NL][NT > 1 ? NT : 1][KT], uint32_t lane) {
+    const uint32_t r = lane & 15u, q = lane >> 4;
+    const float m = wave_max_f32(fmaxf(fmaxf(fabsf(dy[0]), fabsf(dy[1])), fabsf(dy[2])));
+#pragma unroll
+    for (uint32_t k = 0; k < INP; k++) dx[k] = 0.0f;
+    if (!(m > 0.0f) || !(m < 3.0e38f)) return;  // wave-uniform
+    const int e = max(ilogbf(m), -110);  // keeps the scale 2^(8 - e) finite for denormal maxima
+    const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
+
+    // output-layer gradient tiles (16 outputs x 64 primitives): rows 0..2 live in lanes 0..15
+    h4 g[NT > 1 ? NT : 1][4];
+#pragma unroll
+    for (uint32_t cb = 0; cb < 4; cb++) {
+        float v[3];
+#pragma unroll
+        for (uint32_t j = 0; j < 3; j++) v[j] = __shfl(dy[j] * s, static_cast<int>(cb * 16 + r));
+        g[0][cb] = q == 0 ? h4{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]), static_cast<_Float16>(v[2]), static_cast<_Float16>(0.0f)}
+                          : h4{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
+    }
+
+#pragma unroll
+    for (int li = static_cast<int>(NH); li >= 0; li--) {
+        const uint32_t l = static_cast<uint32_t>(li);
+        constexpr uint32_t stride = 64;  // staging rows are indexed [feature][primitive]
+        // ---- weight gradient dW_l += G_l X_l (operands transposed through LDS) ----
+        h4 ga[NT > 1 ? NT : 1][4];  // A fragments: G_l[out 16 rb + r][prims 16 kb + 4 q .. +3]
+#pragma unroll
+        for (uint32_t rb = 0; rb < lout(l) / 16; rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 4; cb++)
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) stage[(rb * 16 + 4 * q + i) * stride + cb * 16 + r] = g[rb][cb][i];
+        wave_sync();
+#pragma unroll
+        for (uint32_t rb = 0; rb < lout(l) / 16; rb++)
+#pragma unroll
+            for (uint32_t kb = 0; kb < 4; kb++) ga[rb][kb] = *reinterpret_cast<const h4*>(&stage[(rb * 16 + r) * stride + kb * 16 + 4 * q]);
+        wave_sync();
+#pragma unroll
+        for (uint32_t kb = 0; kb < lin(l) / 16; kb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 4; cb++)
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) stage[(kb * 16 + 4 * q + i) * stride + cb * 16 + r] = act[l][kb][cb][i];
+        wave_sync();
+#pragma unroll
+        for (uint32_t rb = 0; rb < lout(l) / 16; rb++) {
+#pragma unroll
+            for (uint32_t cb = 0; cb < lin(l) / 16; cb++) {
+                f4 t = f4_zero();
+#pragma unroll
+                for (uint32_t kb = 0; kb < 4; kb++) {
+                    const h4 b = *reinterpret_cast<const h4*>(&stage[(cb * 16 + r) * stride + kb * 16 + 4 * q]);
+                    t = mfma(ga[rb][kb], b, t);
+                }
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) dW[l][rb][cb][i] = __builtin_fmaf(t[i], inv_s, dW[l][rb][cb][i]);
+            }
+        }
+        wave_sync();
+        // ---- input gradient G_in = W_l^T G_l ----
+        f4 acc[KT][4];
+#pragma unroll
+        for (uint32_t rb = 0; rb < lin(l) / 16; rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = f4_zero();
+#pragma unroll
+        for (uint32_t rb = 0; rb < lin(l) / 16; rb++) {
+#pragma unroll
+            for (uint32_t kb = 0; kb < lout(l) / 16; kb++) {
+                const uint32_t base = loff(l) + (kb * 16 + 4 * q) * lin(l) + rb * 16 + r;
+                const uint16_t w0 = W[base], w1 = W[base + lin(l)], w2 = W[base + 2 * lin(l)], w3 = W[base + 3 * lin(l)];
+                const h4 a = h4{__builtin_bit_cast(_Float16, w0), __builtin_bit_cast(_Float16, w1), __builtin_bit_cast(_Float16, w2),
+                                __builtin_bit_cast(_Float16, w3)};
+#pragma unroll
+                for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = mfma(a, g[kb][cb], acc[rb][cb]);
+            }
+        }
+        if (l > 0) {
+#pragma unroll
+            for (uint32_t rb = 0; rb < lin(l) / 16; rb++)
+#pragma unroll
+                for (uint32_t cb = 0; cb < 4; cb++) {
+                    const h4 xa = act[l][rb][cb];
+                    const f4 v = acc[rb][cb];
+                    g[rb][cb] = h4{static_cast<_Float16>(xa[0] > static_cast<_Float16>(0.0f) ? v[0] : 0.0f),
+                                   static_cast<_Float16>(xa[1] > static_cast<_Float16>(0.0f) ? v[1] : 0.0f),
+                                   static_cast<_Float16>(xa[2] > static_cast<_Float16>(0.0f) ? v[2] : 0.0f),
+                                   static_cast<_Float16>(xa[3] > static_cast<_Float16>(0.0f) ? v[3] : 0.0f)};
+                }
+        } else {
+            // input gradient rows to their lanes through LDS (as floats, 64 x INP)
+            float* fs = reinterpret_cast<float*>(stage);
+#pragma unroll
+            for (uint32_t rb = 0; rb < INP / 16; rb++)
+#pragma unroll
+                for (uint32_t cb = 0; cb < 4; cb++)
+#pragma unroll
+                    for (uint32_t i = 0; i < 4; i++) fs[(cb * 16 + r) * INP + rb * 16 + 4 * q + i] = acc[rb][cb][i] * inv_s;
+            wave_sync();
+#pragma unroll
+            for (uint32_t k = 0; k < INP; k++) dx[k] = fs[lane * INP + k];
+            wave_sync();
+        }
+    }
+}
+
+}  // namespace nn
+
+}  // namespace efgs

@@ -7,6 +7,10 @@
 // activations and the appearance model, and the 2D mean and conic through the EWA projection to the 3D mean,
 // log-scales and quaternion. Culled primitives get zero gradients.
 //
+// The neural variant runs a persistent grid: every wave recomputes the MLP forward for its 64 primitives,
+// backpropagates with fp16 MFMA, keeps its weight gradients in fp32 registers across chunks, and the block
+// sums its four waves in a fixed order into one partial per block (summed over blocks by a separate kernel).
+//
 // Reference: B/rasterization/rtc/preprocess_backward.cu:19-404 (the per-primitive part of
 // B/rasterization/include/kernels_backward.cuh:215-230 is folded in here).
 
@@ -22,30 +26,12 @@ __device__ __forceinline__ uint32_t active_residual_params(uint32_t degree) {
     return params_per_unit * degree;
 }
 
-}  // namespace efgs
+struct InstanceGrads {
+    float gmx, gmy, gcx, gcy, gcz, gop, gr, gg, gb, gax, gay;
+};
 
-extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
-    using namespace efgs;
-    const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
-    if (p >= a.n) return;
-    const uint32_t touched = a.n_touched[p];
-    const bool contributes = touched > 0;
-
-    if (!contributes) {
-        a.g_means[3 * p] = 0.0f; a.g_means[3 * p + 1] = 0.0f; a.g_means[3 * p + 2] = 0.0f;
-        a.g_scales[3 * p] = 0.0f; a.g_scales[3 * p + 1] = 0.0f; a.g_scales[3 * p + 2] = 0.0f;
-        a.g_rotations[4 * p] = 0.0f; a.g_rotations[4 * p + 1] = 0.0f; a.g_rotations[4 * p + 2] = 0.0f; a.g_rotations[4 * p + 3] = 0.0f;
-        a.g_opacities[p] = 0.0f;
-#if EFGS_MODEL == 0
-        a.g_precomputed[3 * p] = 0.0f; a.g_precomputed[3 * p + 1] = 0.0f; a.g_precomputed[3 * p + 2] = 0.0f;
-#else
-        a.g_base[3 * p] = 0.0f; a.g_base[3 * p + 1] = 0.0f; a.g_base[3 * p + 2] = 0.0f;
-        for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
-#endif
-        return;
-    }
-
-    // reduce this primitive's instance gradient records (emission order)
+// sum of a visible primitive's per-instance gradient records, in emission order
+__device__ inline InstanceGrads reduce_instance_grads(const PreprocessBackwardArgs& a, uint32_t p, uint32_t touched) {
     const float4* ig = reinterpret_cast<const float4*>(a.inst_grads) + 3 * static_cast<size_t>(a.prim_offset[p]);
     float4 s0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = s0, s2 = s0;
     for (uint32_t k = 0; k < touched; k++) {
@@ -54,51 +40,44 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         s1.x += t1.x; s1.y += t1.y; s1.z += t1.z; s1.w += t1.w;
         s2.x += t2.x; s2.y += t2.y; s2.z += t2.z;
     }
-    const float gmx = s0.x, gmy = s0.y;
-    const float3 gconic = make_float3(s0.z, s0.w, s1.x);
-    const float gop_acc = s1.y;
-    const float3 gcolor = make_float3(s1.z, s1.w, s2.x);
-    const float gabx = s2.y, gaby = s2.z;
+    return {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w, s2.x, s2.y, s2.z};
+}
 
-    const PrimRecord rec = a.records[p];
-    const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
-
-    // colour -> appearance parameters
-    float3 dmean_color = make_float3(0.0f, 0.0f, 0.0f);
+__device__ inline void zero_primitive(const PreprocessBackwardArgs& a, uint32_t p) {
+    a.g_means[3 * p] = 0.0f; a.g_means[3 * p + 1] = 0.0f; a.g_means[3 * p + 2] = 0.0f;
+    a.g_scales[3 * p] = 0.0f; a.g_scales[3 * p + 1] = 0.0f; a.g_scales[3 * p + 2] = 0.0f;
+    a.g_rotations[4 * p] = 0.0f; a.g_rotations[4 * p + 1] = 0.0f; a.g_rotations[4 * p + 2] = 0.0f; a.g_rotations[4 * p + 3] = 0.0f;
+    a.g_opacities[p] = 0.0f;
 #if EFGS_MODEL == 0
-    a.g_precomputed[3 * p] = gcolor.x; a.g_precomputed[3 * p + 1] = gcolor.y; a.g_precomputed[3 * p + 2] = gcolor.z;
+    a.g_precomputed[3 * p] = 0.0f; a.g_precomputed[3 * p + 1] = 0.0f; a.g_precomputed[3 * p + 2] = 0.0f;
 #else
-    {
-        const float3 color = make_float3(rec.r1.z, rec.r1.w, rec.r2.x);
-        const float3 dpre = make_float3(color_activation_grad<EFGS_COLOR_ACT>(color.x) * gcolor.x,
-                                        color_activation_grad<EFGS_COLOR_ACT>(color.y) * gcolor.y,
-                                        color_activation_grad<EFGS_COLOR_ACT>(color.z) * gcolor.z);
-        if (a.cam.render_base) {
-            a.g_base[3 * p] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p]) * dpre.x;
-            a.g_base[3 * p + 1] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p + 1]) * dpre.y;
-            a.g_base[3 * p + 2] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p + 2]) * dpre.z;
-        } else {
-            a.g_base[3 * p] = 0.0f; a.g_base[3 * p + 1] = 0.0f; a.g_base[3 * p + 2] = 0.0f;
-        }
-        const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
-        float norm_rcp;
-        const float3 d = view_direction(mean, cam, norm_rcp);
-        const float* rp = a.residual + static_cast<size_t>(p) * residual_params;
-        float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
-#if EFGS_MODEL == 1
-        dmean_color = sh_residual_backward<EFGS_RES_ACT>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
-#elif EFGS_MODEL == 2
-        dmean_color = sv_residual_backward<EFGS_RES_ACT>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
-#elif EFGS_MODEL == 3
-        dmean_color = lobe_residual_backward<EFGS_RES_ACT, false>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
-#elif EFGS_MODEL == 4
-        dmean_color = lobe_residual_backward<EFGS_RES_ACT, true>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+    a.g_base[3 * p] = 0.0f; a.g_base[3 * p + 1] = 0.0f; a.g_base[3 * p + 2] = 0.0f;
+    for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
 #endif
-        for (uint32_t i = active_residual_params(a.cam.degree); i < residual_params; i++) gp[i] = 0.0f;
-    }
-#endif
+}
 
-    // geometry
+// colour gradient through the colour activation (reference: recovered from the stored activated colour)
+__device__ __forceinline__ float3 pre_activation_grad(const PrimRecord& rec, const InstanceGrads& g) {
+    return make_float3(color_activation_grad<EFGS_COLOR_ACT>(rec.r1.z) * g.gr, color_activation_grad<EFGS_COLOR_ACT>(rec.r1.w) * g.gg,
+                       color_activation_grad<EFGS_COLOR_ACT>(rec.r2.x) * g.gb);
+}
+
+__device__ __forceinline__ void write_base_grad(const PreprocessBackwardArgs& a, uint32_t p, float3 dpre, float3 extra) {
+    if (a.cam.render_base) {
+        a.g_base[3 * p] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p]) * dpre.x + extra.x;
+        a.g_base[3 * p + 1] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p + 1]) * dpre.y + extra.y;
+        a.g_base[3 * p + 2] = base_activation_grad<EFGS_BASE_ACT>(a.base[3 * p + 2]) * dpre.z + extra.z;
+    } else {
+        a.g_base[3 * p] = extra.x; a.g_base[3 * p + 1] = extra.y; a.g_base[3 * p + 2] = extra.z;
+    }
+}
+
+// 2D mean / conic / opacity gradients through the projection to the 3D mean, log-scales and quaternion
+__device__ inline void geometry_backward(const PreprocessBackwardArgs& a, uint32_t p, const PrimRecord& rec, const InstanceGrads& ig,
+                                         float3 dmean_color) {
+    const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+    const float gmx = ig.gmx, gmy = ig.gmy;
+    const float3 gconic = make_float3(ig.gcx, ig.gcy, ig.gcz);
     const float* W = a.cam.w2c;
     const float depth = W[8] * mean.x + W[9] * mean.y + W[10] * mean.z + W[11];
     const float x = (W[0] * mean.x + W[1] * mean.y + W[2] * mean.z + W[3]) / depth;
@@ -142,10 +121,10 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     if (a.cam.proper_aa) {
         const float o = ef_sigmoid(a.opacities[p]);
         const float rad = fmaxf((a_raw * c_raw - bb) / det, 0.0f);
-        a.g_opacities[p] = gop_acc * sqrtf(rad) * o * (1.0f - o);
+        a.g_opacities[p] = ig.gop * sqrtf(rad) * o * (1.0f - o);
     } else {
         const float o = rec.r1.y;
-        a.g_opacities[p] = (o - o * o) * gop_acc;
+        a.g_opacities[p] = (o - o * o) * ig.gop;
     }
 
     const float d11 = a1x * a1x * dcx + 2.0f * a1x * a2x * dcy + a2x * a2x * dcz;
@@ -167,7 +146,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         const float nx = 0.5f * (gmx * wf), ny = 0.5f * (gmy * hf);
         a.densification_info[n + p] += sqrtf(nx * nx + ny * ny);
         if (a.densification_rows > 2) {
-            const float ax = 0.5f * (gabx * wf), ay = 0.5f * (gaby * hf);
+            const float ax = 0.5f * (ig.gax * wf), ay = 0.5f * (ig.gay * hf);
             a.densification_info[2 * n + p] += sqrtf(ax * ax + ay * ay);
         }
     }
@@ -201,3 +180,159 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     const float4 gq = quaternion_to_rotation_backward(qr, qx, qy, qz, dR);
     a.g_rotations[4 * p] = gq.x; a.g_rotations[4 * p + 1] = gq.y; a.g_rotations[4 * p + 2] = gq.z; a.g_rotations[4 * p + 3] = gq.w;
 }
+
+}  // namespace efgs
+
+#if EFGS_MODEL != 5
+
+extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
+    using namespace efgs;
+    const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
+    if (p >= a.n) return;
+    const uint32_t touched = a.n_touched[p];
+    if (touched == 0) {
+        zero_primitive(a, p);
+        return;
+    }
+    const InstanceGrads ig = reduce_instance_grads(a, p, touched);
+    const PrimRecord rec = a.records[p];
+    float3 dmean_color = make_float3(0.0f, 0.0f, 0.0f);
+#if EFGS_MODEL == 0
+    a.g_precomputed[3 * p] = ig.gr; a.g_precomputed[3 * p + 1] = ig.gg; a.g_precomputed[3 * p + 2] = ig.gb;
+#else
+    {
+        const float3 dpre = pre_activation_grad(rec, ig);
+        write_base_grad(a, p, dpre, make_float3(0.0f, 0.0f, 0.0f));
+        const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+        const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
+        float norm_rcp;
+        const float3 d = view_direction(mean, cam, norm_rcp);
+        const float* rp = a.residual + static_cast<size_t>(p) * residual_params;
+        float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
+#if EFGS_MODEL == 1
+        dmean_color = sh_residual_backward<EFGS_RES_ACT>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+#elif EFGS_MODEL == 2
+        dmean_color = sv_residual_backward<EFGS_RES_ACT>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+#elif EFGS_MODEL == 3
+        dmean_color = lobe_residual_backward<EFGS_RES_ACT, false>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+#elif EFGS_MODEL == 4
+        dmean_color = lobe_residual_backward<EFGS_RES_ACT, true>(rp, dpre, gp, d, norm_rcp, a.cam.degree);
+#endif
+        for (uint32_t i = active_residual_params(a.cam.degree); i < residual_params; i++) gp[i] = 0.0f;
+    }
+#endif
+    geometry_backward(a, p, rec, ig, dmean_color);
+}
+
+#else  // neural
+
+extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
+    using namespace efgs;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint16_t* W = reinterpret_cast<uint16_t*>(smem);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES) + wave * nn::STAGE_HALVES;
+    for (uint32_t i = threadIdx.x; i < nn::PARAMS / 8; i += preprocess_block)
+        reinterpret_cast<uint4*>(W)[i] = reinterpret_cast<const uint4*>(a.mlp_weights)[i];
+    __syncthreads();
+
+    nn::f4 dW[nn::NL][nn::NT > 1 ? nn::NT : 1][nn::KT];
+#pragma unroll
+    for (uint32_t l = 0; l < nn::NL; l++)
+#pragma unroll
+        for (uint32_t rb = 0; rb < (nn::NT > 1 ? nn::NT : 1); rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < nn::KT; cb++) dW[l][rb][cb] = nn::f4_zero();
+
+    const uint32_t degree = a.cam.degree;
+    const uint32_t n_chunks = (a.n + preprocess_block - 1) / preprocess_block;
+    for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
+        const uint32_t p_raw = chunk * preprocess_block + threadIdx.x;
+        const bool valid = p_raw < a.n;
+        const uint32_t p = valid ? p_raw : a.n - 1;
+        const uint32_t touched = valid ? a.n_touched[p] : 0u;
+        const bool contributes = touched > 0;
+
+        InstanceGrads ig = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        PrimRecord rec;
+        rec.r0 = rec.r1 = rec.r2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (contributes) {
+            ig = reduce_instance_grads(a, p, touched);
+            rec = a.records[p];
+        }
+        const float3 dpre = contributes ? pre_activation_grad(rec, ig) : make_float3(0.0f, 0.0f, 0.0f);
+        const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+        const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
+        float norm_rcp;
+        const float3 d = view_direction(mean, cam, norm_rcp);
+        const float* feat = a.residual + static_cast<size_t>(p) * residual_params;
+        float3 dmean_color = make_float3(0.0f, 0.0f, 0.0f);
+        float3 dbase_input = make_float3(0.0f, 0.0f, 0.0f);
+        float dx[nn::INP];
+#pragma unroll
+        for (uint32_t k = 0; k < nn::INP; k++) dx[k] = 0.0f;
+        if (degree > 0) {  // uniform: every lane of every wave runs the MLP
+            float x[nn::INP];
+            nn::mlp_input(feat, a.base + 3 * p, d, degree, x);
+            if (!contributes) {
+#pragma unroll
+                for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
+            }
+            nn::h4 act[nn::NL][nn::KT][4];
+            float y[3];
+            nn::mlp_forward(W, stage, x, act, y, lane);
+            float dy[3];
+            dy[0] = dpre.x * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[0]));
+            dy[1] = dpre.y * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[1]));
+            dy[2] = dpre.z * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[2]));
+            nn::mlp_backward(W, stage, act, dy, dx, dW, lane);
+            if (contributes) {
+                float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
+#pragma unroll
+                for (uint32_t i = 0; i < nn::FEATURES; i++) gp[i] = nn::feature_grad(feat[i], dx, i);
+                if (EFGS_BASE_INPUT) {
+                    dbase_input = make_float3(nn::feature_grad(a.base[3 * p], dx, nn::FEATURES),
+                                              nn::feature_grad(a.base[3 * p + 1], dx, nn::FEATURES + 1),
+                                              nn::feature_grad(a.base[3 * p + 2], dx, nn::FEATURES + 2));
+                }
+                dmean_color = direction_grad_to_mean(nn::direction_grad(d, degree, dx), d, norm_rcp);
+            }
+        }
+        if (valid) {
+            if (!contributes) {
+                zero_primitive(a, p);
+            } else {
+                write_base_grad(a, p, dpre, dbase_input);
+                if (degree == 0)
+                    for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
+                geometry_backward(a, p, rec, ig, dmean_color);
+            }
+        }
+    }
+
+    // block sum of the four waves' weight gradients, in wave order, then one partial per block
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);
+    const uint32_t r = lane & 15u, q = lane >> 4;
+    for (uint32_t w = 0; w < preprocess_block / 64; w++) {
+        if (wave == w) {
+#pragma unroll
+            for (uint32_t l = 0; l < nn::NL; l++)
+#pragma unroll
+                for (uint32_t rb = 0; rb < nn::lout(l) / 16; rb++)
+#pragma unroll
+                    for (uint32_t cb = 0; cb < nn::lin(l) / 16; cb++)
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; i++) {
+                            const uint32_t idx = nn::loff(l) + (rb * 16 + 4 * q + i) * nn::lin(l) + cb * 16 + r;
+                            red[idx] = (w == 0 ? 0.0f : red[idx]) + dW[l][rb][cb][i];
+                        }
+        }
+        __syncthreads();
+    }
+    float* out = a.g_mlp_partials + static_cast<size_t>(blockIdx.x) * nn::PARAMS;
+    for (uint32_t i = threadIdx.x; i < nn::PARAMS; i += preprocess_block) out[i] = red[i];
+}
+
+#endif

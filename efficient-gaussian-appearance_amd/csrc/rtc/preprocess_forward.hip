@@ -6,8 +6,9 @@
 // 3D covariance from log-scales and quaternion, EWA projection with the 1.15x clip, dilation and determinant
 // cull, conic, screen bounds clamped to the padded tile grid, exact touched-tile count (first 4 tiles per
 // lane, larger footprints wave-cooperatively 64 tiles per step), activated colour, and the 48-byte record.
-// Each block also writes its visible and instance counts, which a scan turns into deterministic
-// (primitive-index ordered) compaction offsets. No global atomics.
+// Each 256-primitive chunk also records its visible and instance counts, which a scan turns into
+// deterministic (primitive-index ordered) compaction offsets. No global atomics. The neural variant runs a
+// persistent grid (chunks strided by the grid size) so its MLP weights are staged into LDS once per block.
 //
 // Reference: B/rasterization/rtc/preprocess_forward.cu:12-278, preprocess_common.cuh:190-252.
 
@@ -146,18 +147,29 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t p_raw = blockIdx.x * preprocess_block + threadIdx.x;
-    const bool active = p_raw < a.n;
-    const uint32_t p = active ? p_raw : a.n - 1;
+    __shared__ uint32_t wave_counts[2 * (preprocess_block / 64)];
+#if EFGS_MODEL == 5
+    // residual MLP weights staged once per block; per-wave staging area for operand transposes
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint16_t* W = reinterpret_cast<uint16_t*>(smem);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES) + wave * nn::STAGE_HALVES;
+    for (uint32_t i = threadIdx.x; i < nn::PARAMS / 8; i += preprocess_block)
+        reinterpret_cast<uint4*>(W)[i] = reinterpret_cast<const uint4*>(a.mlp_weights)[i];
+    __syncthreads();
+#endif
+    const uint32_t n_chunks = (a.n + preprocess_block - 1) / preprocess_block;
+    for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
+        const uint32_t p_raw = chunk * preprocess_block + threadIdx.x;
+        const bool active = p_raw < a.n;
+        const uint32_t p = active ? p_raw : a.n - 1;
 
-    Projected pr = project(a, p, active);
-    uint32_t touched = count_touched_tiles(pr, lane);
-    bool visible = pr.visible && touched > 0;
+        Projected pr = project(a, p, active);
+        uint32_t touched = count_touched_tiles(pr, lane);
+        const bool visible = pr.visible && touched > 0;
 
-    float3 color = make_float3(0.0f, 0.0f, 0.0f);
-    if (visible) {
+        float3 color = make_float3(0.0f, 0.0f, 0.0f);
 #if EFGS_MODEL == 0
-        color = make_float3(a.precomputed[3 * p], a.precomputed[3 * p + 1], a.precomputed[3 * p + 2]);
+        if (visible) color = make_float3(a.precomputed[3 * p], a.precomputed[3 * p + 1], a.precomputed[3 * p + 2]);
 #else
         const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
         const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
@@ -165,58 +177,72 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         const float3 d = view_direction(mean, cam, norm_rcp);
         const float* rp = a.residual + static_cast<size_t>(p) * residual_params;
         float3 res = make_float3(0.0f, 0.0f, 0.0f);
-#if EFGS_MODEL == 1
-        res = sh_residual<EFGS_RES_ACT>(rp, d, a.cam.degree);
-#elif EFGS_MODEL == 2
-        res = sv_residual<EFGS_RES_ACT>(rp, d, a.cam.degree);
-#elif EFGS_MODEL == 3
-        res = lobe_residual<EFGS_RES_ACT, false>(rp, d, a.cam.degree);
-#elif EFGS_MODEL == 4
-        res = lobe_residual<EFGS_RES_ACT, true>(rp, d, a.cam.degree);
-#endif
-        const float b0 = base_activation<EFGS_BASE_ACT>(a.base[3 * p]);
-        const float b1 = base_activation<EFGS_BASE_ACT>(a.base[3 * p + 1]);
-        const float b2 = base_activation<EFGS_BASE_ACT>(a.base[3 * p + 2]);
-        color = make_float3(color_activation<EFGS_COLOR_ACT>(b0 + res.x), color_activation<EFGS_COLOR_ACT>(b1 + res.y),
-                            color_activation<EFGS_COLOR_ACT>(b2 + res.z));
-        if (!a.cam.render_base) {
-            color.x = fabsf(color.x - color_activation<EFGS_COLOR_ACT>(b0));
-            color.y = fabsf(color.y - color_activation<EFGS_COLOR_ACT>(b1));
-            color.z = fabsf(color.z - color_activation<EFGS_COLOR_ACT>(b2));
+#if EFGS_MODEL == 5
+        // every lane of every wave runs the MLP (the waves share the block's LDS staging discipline)
+        if (a.cam.degree > 0) {
+            float x[nn::INP];
+            nn::mlp_input(rp, a.base + 3 * p, d, a.cam.degree, x);
+            nn::h4 act[nn::NL][nn::KT][4];
+            float y[3];
+            nn::mlp_forward(W, stage, x, act, y, lane);
+            res = make_float3(residual_activation<EFGS_RES_ACT>(y[0]), residual_activation<EFGS_RES_ACT>(y[1]),
+                              residual_activation<EFGS_RES_ACT>(y[2]));
         }
 #endif
-    }
-
-    if (!visible) touched = 0;
-    if (active) {
-        a.n_touched[p] = touched;
-        a.depth_keys[p] = __float_as_uint(pr.depth);
         if (visible) {
-            PrimRecord rec;
-            rec.r0 = make_float4(pr.mean2d_x, pr.mean2d_y, pr.conic_x, pr.conic_y);
-            rec.r1 = make_float4(pr.conic_z, pr.opacity, color.x, color.y);
-            rec.r2 = make_float4(color.z, __uint_as_float(pr.sx0 | (pr.sx1 << 16)), __uint_as_float(pr.sy0 | (pr.sy1 << 16)), 0.0f);
-            a.records[p] = rec;
+#if EFGS_MODEL == 1
+            res = sh_residual<EFGS_RES_ACT>(rp, d, a.cam.degree);
+#elif EFGS_MODEL == 2
+            res = sv_residual<EFGS_RES_ACT>(rp, d, a.cam.degree);
+#elif EFGS_MODEL == 3
+            res = lobe_residual<EFGS_RES_ACT, false>(rp, d, a.cam.degree);
+#elif EFGS_MODEL == 4
+            res = lobe_residual<EFGS_RES_ACT, true>(rp, d, a.cam.degree);
+#endif
+            const float b0 = base_activation<EFGS_BASE_ACT>(a.base[3 * p]);
+            const float b1 = base_activation<EFGS_BASE_ACT>(a.base[3 * p + 1]);
+            const float b2 = base_activation<EFGS_BASE_ACT>(a.base[3 * p + 2]);
+            color = make_float3(color_activation<EFGS_COLOR_ACT>(b0 + res.x), color_activation<EFGS_COLOR_ACT>(b1 + res.y),
+                                color_activation<EFGS_COLOR_ACT>(b2 + res.z));
+            if (!a.cam.render_base) {
+                color.x = fabsf(color.x - color_activation<EFGS_COLOR_ACT>(b0));
+                color.y = fabsf(color.y - color_activation<EFGS_COLOR_ACT>(b1));
+                color.z = fabsf(color.z - color_activation<EFGS_COLOR_ACT>(b2));
+            }
         }
-    }
+#endif
 
-    // per-block visible / instance counts (deterministic compaction offsets come from their scan)
-    __shared__ uint32_t wave_counts[2 * (preprocess_block / 64)];
-    const uint32_t wave_visible = static_cast<uint32_t>(__popcll(__ballot(visible && active)));
-    const uint32_t wave_instances = wave_sum_u32(active ? touched : 0u);
-    if (lane == 0) {
-        wave_counts[2 * wave] = wave_visible;
-        wave_counts[2 * wave + 1] = wave_instances;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t v = 0, i = 0;
-#pragma unroll
-        for (uint32_t w = 0; w < preprocess_block / 64; w++) {
-            v += wave_counts[2 * w];
-            i += wave_counts[2 * w + 1];
+        if (!visible) touched = 0;
+        if (active) {
+            a.n_touched[p] = touched;
+            a.depth_keys[p] = __float_as_uint(pr.depth);
+            if (visible) {
+                PrimRecord rec;
+                rec.r0 = make_float4(pr.mean2d_x, pr.mean2d_y, pr.conic_x, pr.conic_y);
+                rec.r1 = make_float4(pr.conic_z, pr.opacity, color.x, color.y);
+                rec.r2 = make_float4(color.z, __uint_as_float(pr.sx0 | (pr.sx1 << 16)), __uint_as_float(pr.sy0 | (pr.sy1 << 16)), 0.0f);
+                a.records[p] = rec;
+            }
         }
-        a.block_counts[2 * blockIdx.x] = v;
-        a.block_counts[2 * blockIdx.x + 1] = i;
+
+        // per-chunk visible / instance counts (deterministic compaction offsets come from their scan)
+        const uint32_t wave_visible = static_cast<uint32_t>(__popcll(__ballot(visible && active)));
+        const uint32_t wave_instances = wave_sum_u32(active ? touched : 0u);
+        if (lane == 0) {
+            wave_counts[2 * wave] = wave_visible;
+            wave_counts[2 * wave + 1] = wave_instances;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t v = 0, i = 0;
+#pragma unroll
+            for (uint32_t w = 0; w < preprocess_block / 64; w++) {
+                v += wave_counts[2 * w];
+                i += wave_counts[2 * w + 1];
+            }
+            a.block_counts[2 * chunk] = v;
+            a.block_counts[2 * chunk + 1] = i;
+        }
+        __syncthreads();
     }
 }

@@ -156,6 +156,10 @@ def _forward(means, scales, rotations, opacities, precomputed_colors, base_color
     names = ('means', 'scales', 'rotations', 'opacities', 'precomputed_colors', 'base_colors', 'residual_params')
     for name, t in zip(names, (means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params)):
         _check_param(name, t, device)
+    if mlp_weights_half.numel() > 0:
+        expected = _rasterizer.mlp_param_count()
+        if mlp_weights_half.numel() != expected or mlp_weights_half.device != device:
+            raise ValueError(f'efgs: mlp_weights must hold {expected} parameters on {device}, got {mlp_weights_half.numel()}')
     with torch.cuda.device(device):
         cs, keep = _native_settings(settings, device)
         prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)

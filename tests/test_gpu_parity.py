@@ -1,9 +1,9 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle on identical seeded scenes.
 
 Bars: integer / key / index / range arrays bit-exact; per-primitive projection records (mean2d, conic,
-opacity, bounds) bit-exact (shared decision-path arithmetic); image max-abs <= 1e-4 (fp32 path); gradients
-rel-L2 <= 1e-3; last-contributor indices equal for >= 99.9% of pixels (a Gaussian whose alpha lies within one
-ulp of 1/255 may flip between the GPU's exp2 and libm's).
+opacity, bounds) bit-exact (shared decision-path arithmetic); image max-abs <= 1e-4 (fp32 path, in practice
+bit-exact: the blend shares its exp2 with the oracle) and <= 2e-3 (fp16 neural MLP path); last-contributor
+indices equal (fp32 path); gradients rel-L2 <= 1e-3, including the MLP weight gradients.
 """
 import numpy as np
 import pytest
@@ -14,6 +14,7 @@ from helpers import small_case, rel_l2, configure, torch_inputs, settings, read_
 pytestmark = pytest.mark.gpu
 
 IMAGE_TOL = 1e-4
+IMAGE_TOL_FP16 = 2e-3   # neural: fp16 MLP path
 GRAD_TOL = 1e-3
 
 CASES = {
@@ -31,7 +32,19 @@ CASES = {
     'nasgabor': dict(model='nasgabor', acts=('none', 'tanh', 'softplus')),
     'ragged_image': dict(model='sh', width=50, height=37),
     'dense_2k': dict(model='sh', n=2000, width=96, height=80, scale_shift=1.5),
+    'neural_c3_mlp': dict(model='neural', scale_shift=2.5),
+    'neural_reference_default': dict(model='neural', scale_shift=2.5, acts=('none', 'tanh', 'relu'),
+                                     mlp=dict(n_feature_dims=8, n_frequencies=1, sh_degrees=(0, 1, 2, 3), n_neurons=16,
+                                              n_hidden_layers=2, base_input=False)),
+    'neural_base_input_softplus': dict(model='neural', scale_shift=2.5, acts=('exp', 'softplus', 'satexp'),
+                                       mlp=dict(n_feature_dims=5, n_frequencies=1, sh_degrees=(0, 1, 2, 3), n_neurons=32,
+                                                n_hidden_layers=3, base_input=True)),
+    'neural_degree0': dict(model='neural', scale_shift=2.5, degree=0),
 }
+
+
+def _image_tol(case):
+    return IMAGE_TOL_FP16 if case.get('model') == 'neural' else IMAGE_TOL
 
 
 def _run(case):
@@ -69,7 +82,7 @@ def test_forward_parity(name):
     bx, by = rec[:, 9].view(np.uint32), rec[:, 10].view(np.uint32)
     b = fw.bounds[vis].astype(np.uint32)
     np.testing.assert_array_equal(np.stack([bx & 0xffff, bx >> 16, by & 0xffff, by >> 16], 1), b)
-    np.testing.assert_allclose(rec[:, 6:9], fw.color[vis], rtol=0, atol=1e-5)
+    np.testing.assert_allclose(rec[:, 6:9], fw.color[vis], rtol=0, atol=_image_tol(CASES[name]) / 10 if CASES[name].get('model') != 'neural' else IMAGE_TOL_FP16)
     np.testing.assert_array_equal(read_device(bufs, v.depth_sorted_keys, V, np.uint32), fw.depth_key[fw.depth_sorted])
     np.testing.assert_array_equal(read_device(bufs, v.depth_sorted_prims, V, np.uint32), fw.depth_sorted)
     np.testing.assert_array_equal(read_device(bufs, v.instance_offsets, V, np.uint32), fw.offsets)
@@ -83,12 +96,14 @@ def test_forward_parity(name):
     counters = read_device(bufs, v.counters, 4, np.uint32)
     assert counters[2] == 0, 'instance emission disagreed with the preprocess counts'
     err = np.abs(image.cpu().numpy() - fw.image).max()
-    assert err <= IMAGE_TOL, f'image max-abs {err}'
+    print(f'case {name}: image max-abs {err:.3e}', flush=True)
+    assert err <= _image_tol(CASES[name]), f'image max-abs {err}'
     # per-tile layout (tile, 16 x 12 row-major) -> image layout
     nc = read_device(bufs, v.n_contributors, gw * gh * 192, np.uint32).reshape(gh, gw, 12, 16).transpose(0, 2, 1, 3).reshape(gh * 12, gw * 16)
     nc = nc[:cam.height, :cam.width].reshape(-1)
     mism = np.count_nonzero(nc != fw.n_contrib)
-    assert mism <= max(1, cam.width * cam.height // 1000), f'{mism} last-contributor mismatches'
+    if CASES[name].get('model') != 'neural':
+        assert mism == 0, f'{mism} last-contributor mismatches'
 
 
 @pytest.mark.parametrize('name', list(CASES))
@@ -111,6 +126,8 @@ def test_backward_parity(name):
     torch.cuda.synchronize()
     keys = ['means', 'scales', 'rotations', 'opacities']
     keys += ['precomputed_colors'] if app.model == 'precomputed' else ['base_colors', 'residual_params']
+    if app.model == 'neural':
+        keys.append('mlp_weights')
     for k in keys:
         got = inp[k].grad.cpu().numpy()
         want = ref[k]
