@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Training-step benchmark of the fused-appearance rasterizer on one MI355X.
+
+Workload (default, configuration c3): 1M Gaussians, 1920 x 1080, neural appearance (8 latents + SH degree 1
+direction -> 64 -> 64 -> 3 fp16 MLP, tanh residual, relu colour), synthetic seeded scene. One step =
+diff_rasterize forward, L1 loss against a seeded uniform-noise target, backward, one FusedAdam step over all
+parameter groups (means, scales, rotations, opacities, base colours, latents, MLP weights). Inputs are
+resident in HBM before the timed region.
+
+Output: one JSON line. `value` = W * H / (wall time per full step) in Mpix/s (forward, loss, backward and
+Adam); `fwd_bwd_mpix_s` = W * H / (stream time from the forward's start to the backward's end, Adam
+excluded). `roofline` covers the step's dominant kernel, timed with HIP events that the library records
+around each stage on the stream it launches on (Adam: events around FusedAdam.step on the same stream);
+`stages` lists every stage. `cpu_baseline` times the CPU restatement (oracle/) of one forward + backward of
+the same scene on the host.
+
+  python bench.py [--steps K] [--warmup W] [--config c3|c1|c4_sv|c4_nasg|c4_nasgabor] [--no-cpu-baseline]
+  python bench.py --copy-calibration    # a plain 1 GiB device copy, for scaling rocprofv3 FETCH/WRITE_SIZE
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, 'efficient-gaussian-appearance_amd')
+if PKG not in sys.path:
+    sys.path.insert(0, PKG)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'traffic_c3_neural.txt')
+
+# kernel names (as rocprofv3 lists them) of each timed stage
+STAGE_KERNELS = {
+    'preprocess_forward': 'preprocess_forward_<model>',
+    'compact': 'scan_block_counts_kernel + compact_visible_kernel',
+    'depth_sort': 'sort_histogram_kernel + sort_scatter_kernel (4 passes)',
+    'instance_offsets': 'scan_reduce + scan_block_sums + scan_downsweep',
+    'create_instances': 'create_instances_kernel',
+    'tile_sort': 'sort_histogram_kernel + sort_scatter_kernel (2 passes)',
+    'tile_ranges': 'tile_ranges_kernel',
+    'blend_forward': 'blend_forward_kernel',
+    'blend_backward': 'blend_backward_kernel',
+    'preprocess_backward': 'preprocess_backward_<model>',
+    'mlp_reduce': 'reduce_partials_kernel',
+    'adam': 'adam_kernel',
+}
+
+
+def log(msg: str) -> None:
+    print(f'bench: {msg}', file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split('\n')[0])
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=20)
+    p.add_argument('--warmup', type=int, default=5)
+    p.add_argument('--config', default='c3')
+    p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--copy-calibration', action='store_true')
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------------------------------------
+# algorithmic bytes and flops per launch (compulsory traffic: every input read once, every output written
+# once; radix-pass re-reads and other design-dependent traffic excluded)
+# ---------------------------------------------------------------------------------------------------------
+
+def residual_bytes(model: str, n_units: int) -> int:
+    """Residual parameter bytes per primitive: SH3 45 floats, neural 8 latents, SV 7, NASG 8, NASGabor 9
+    floats per site / lobe."""
+    per_unit = {'sh': 12, 'neural': 4, 'sv': 28, 'nasg': 32, 'nasgabor': 36}[model]
+    return per_unit * n_units
+
+
+def mlp_flops_per_primitive(n_in: int, n_neurons: int, n_hidden: int, n_out: int = 3) -> int:
+    """Unpadded forward FLOPs of the bias-free MLP (2 per multiply-add)."""
+    return 2 * (n_in * n_neurons + (n_hidden - 1) * n_neurons * n_neurons + n_neurons * n_out)
+
+
+def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_fwd_flops: int, adam_elements: int):
+    """(bytes, flops) of one launch of `stage`. Per-unit figures: preprocess N*(60+R) + V*52 split into the
+    preprocess kernel (N*(60+R) + V*44) and the compaction (V*8 key/index pairs); depth sort V*16, offsets
+    scan V*8; instances V*40 + I*6, tile sort I*12, ranges T*8; blend forward I*48 + P*20; blend backward
+    P*32 + I*76; preprocess backward V*(110+R) + N*(56+R); Adam 28 B per element. MLP: forward V*F,
+    backward (input and weight gradients) 2*V*F, F = unpadded forward FLOPs per primitive."""
+    table = {
+        'preprocess_forward': (N * (60 + R) + V * 44, V * mlp_fwd_flops),
+        'compact': (V * 8, 0),
+        'depth_sort': (V * 16, 0),
+        'instance_offsets': (V * 8, 0),
+        'create_instances': (V * 40 + I * 6, 0),
+        'tile_sort': (I * 12, 0),
+        'tile_ranges': (T * 8, 0),
+        'blend_forward': (I * 48 + P * 20, 0),
+        'blend_backward': (P * 32 + I * 76, 0),
+        'preprocess_backward': (V * (110 + R) + N * (56 + R), 2 * V * mlp_fwd_flops),
+        'adam': (28 * adam_elements, 0),
+    }
+    return table.get(stage, (0, 0))
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, if it lists the kernel:
+    lines `traffic <kernel> <fetch_bytes> <write_bytes>` (already scaled by the copy-kernel calibration)."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) == 4 and parts[0] == 'traffic' and parts[1] == kernel:
+                return float(parts[2]) + float(parts[3])
+    return None
+
+
+# ---------------------------------------------------------------------------------------------------------
+# GPU step
+# ---------------------------------------------------------------------------------------------------------
+
+def build_problem(config: str, device):
+    import numpy as np
+    import torch
+    import efgs
+    from efgs.synthetic import make_scene, target_image
+
+    sc = make_scene(config)
+    cam = sc['camera']
+    app = sc['appearance']
+    efgs.initialize_appearance(app['model'], app['max_degree'], app['base_act'], app['res_act'], app['color_act'],
+                               app['direction_gradient'])
+    mlp = app.get('mlp')
+    if mlp is not None:
+        n_in = mlp['n_feature_dims'] + sum(2 * d + 1 for d in mlp['sh_degrees'])
+        efgs.initialize_residual_mlp(n_in, 3, {'otype': 'Identity'},
+                                     {'otype': 'FullyFusedMLP', 'activation': 'ReLU', 'output_activation': 'None',
+                                      'n_neurons': mlp['n_neurons'], 'n_hidden_layers': mlp['n_hidden_layers']},
+                                     mlp['base_input'], mlp['n_frequencies'], list(mlp['sh_degrees']))
+
+    def leaf(a):
+        return torch.tensor(np.ascontiguousarray(a, np.float32), device=device).requires_grad_(True)
+
+    params = dict(means=leaf(sc['means']), scales=leaf(sc['scales']), rotations=leaf(sc['rotations']),
+                  opacities=leaf(sc['opacities']), base_colors=leaf(sc['base_colors']),
+                  residual_params=leaf(sc['residual_params']))
+    if sc['mlp_weights'] is not None:
+        params['mlp_weights'] = leaf(sc['mlp_weights'])
+    degree = app['max_degree'] if app['model'] != 'neural' else 1
+    settings = efgs.RasterizerSettings(
+        w2c=torch.tensor(cam['w2c'], device=device), cam_position=torch.tensor(cam['position'], device=device),
+        bg_color=torch.zeros(3, device=device), appearance_degree=degree, width=cam['width'], height=cam['height'],
+        focal_x=cam['focal_x'], focal_y=cam['focal_y'], center_x=cam['center_x'], center_y=cam['center_y'],
+        near_plane=cam['near_plane'], far_plane=cam['far_plane'], proper_antialiasing=False, render_base=True,
+        render_residual=True)
+    target = torch.tensor(target_image(cam['width'], cam['height']), device=device)
+    # learning rates of the reference's training configurations (3DGS defaults, means scaled by the extent)
+    lrs = dict(means=1.6e-4 * 10.0, scales=5e-3, rotations=1e-3, opacities=2.5e-2, base_colors=2.5e-3,
+               residual_params=2.5e-3, mlp_weights=1e-3)
+    opt = efgs.FusedAdam([{'params': [t], 'lr': lrs[k], 'name': k} for k, t in params.items()], lr=0.0, eps=1e-15)
+    return sc, params, settings, target, opt
+
+
+def gpu_benchmark(args):
+    import torch
+    import efgs
+    from efgs import rasterization as R
+
+    device = torch.device('cuda:0')
+    torch.cuda.set_device(device)
+    sc, params, settings, target, opt = build_problem(args.config, device)
+    empty = torch.empty(0, device=device)
+
+    def step(events=None):
+        if events is not None:
+            events[0].record()
+        img = efgs.diff_rasterize(params['means'], params['scales'], params['rotations'], params['opacities'], empty, settings,
+                                  base_colors=params['base_colors'], residual_params=params['residual_params'],
+                                  mlp_weights=params.get('mlp_weights'))
+        loss = (img - target).abs().mean()
+        loss.backward()
+        if events is not None:
+            events[1].record()
+        opt.step()
+        if events is not None:
+            events[2].record()
+        opt.zero_grad(set_to_none=True)
+        return R.last_frame_counts['n_visible'], R.last_frame_counts['n_instances']
+
+    log(f'scene ready: {sc["means"].shape[0]} Gaussians, {sc["camera"]["width"]}x{sc["camera"]["height"]}, {sc["model"]}')
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f'{args.warmup} warmup steps done')
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    counts = []
+    R._rasterizer.set_stage_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        counts.append(step(events[k]))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    log(f'{args.steps} timed steps done: {wall * 1e3 / args.steps:.3f} ms/step')
+    stage_times = R._rasterizer.stage_times()
+    R._rasterizer.set_stage_timing(False)
+
+    fwd_bwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
+    adam_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    V = sum(c[0] for c in counts) / len(counts)
+    I = sum(c[1] for c in counts) / len(counts)
+    cam = sc['camera']
+    W, H = cam['width'], cam['height']
+    N = sc['means'].shape[0]
+    T = math.ceil(W / 16) * math.ceil(H / 12)
+    app = sc['appearance']
+    model = app['model']
+    mlp = app.get('mlp')
+    if model == 'neural':
+        n_in = mlp['n_feature_dims'] + sum(2 * d + 1 for d in mlp['sh_degrees'])
+        F = mlp_flops_per_primitive(n_in, mlp['n_neurons'], mlp['n_hidden_layers'])
+        R_bytes = residual_bytes(model, mlp['n_feature_dims'])
+    else:
+        F = 0
+        R_bytes = residual_bytes(model, 15 if model == 'sh' else 8)
+    adam_elements = sum(p.numel() for p in params.values())
+    per_stage = {name: (ms / max(n, 1), n) for name, (ms, n) in stage_times.items() if n > 0}
+    per_stage['adam'] = (adam_ms, args.steps)
+    stages = {}
+    for name, (ms, n) in per_stage.items():
+        b, f = algorithmic(name, N, V, I, T, W * H, R_bytes, F, adam_elements)
+        entry = {'ms': round(ms, 5), 'launches': n // args.steps if name != 'adam' else 1}
+        if b:
+            entry['gb_s'] = round(b / (ms * 1e-3) / 1e9, 1)
+            entry['hbm_frac'] = round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        if f:
+            entry['tflop_s'] = round(f / (ms * 1e-3) / 1e12, 2)
+            entry['mfma_frac'] = round(f / (ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4)
+        stages[name] = entry
+
+    kernel_stages = [s for s in per_stage if s not in ('counter_read',)]
+    dominant = max(kernel_stages, key=lambda s: per_stage[s][0])
+    dms = per_stage[dominant][0]
+    b, f = algorithmic(dominant, N, V, I, T, W * H, R_bytes, F, adam_elements)
+    hbm_frac = b / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS if b else 0.0
+    mfma_frac = f / (dms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS if f else 0.0
+    kernel_name = STAGE_KERNELS.get(dominant, dominant).replace('<model>', model)
+    if mfma_frac > hbm_frac:
+        roofline = {'bound': 'mfma', 'achieved': round(f / (dms * 1e-3) / 1e12, 3), 'peak': MFMA_FP16_PEAK_TFLOPS,
+                    'unit': 'TFLOP/s', 'frac': round(mfma_frac, 5)}
+    else:
+        roofline = {'bound': 'hbm', 'achieved': round(b / (dms * 1e-3) / 1e9, 2), 'peak': HBM_PEAK_GBS,
+                    'unit': 'GB/s', 'frac': round(hbm_frac, 5)}
+    roofline['traffic'] = read_traffic(kernel_name)
+    roofline.update({'kernel': kernel_name, 'stage': dominant, 'avg_launch_ms': round(dms, 5),
+                     'algorithmic_bytes': int(b), 'algorithmic_flops': int(f)})
+    ms_per_step = wall * 1e3 / args.steps
+    return dict(W=W, H=H, N=N, V=V, I=I, model=model, ms_per_step=ms_per_step, fwd_bwd_ms=fwd_bwd_ms, adam_ms=adam_ms,
+                roofline=roofline, stages=stages, scene=sc)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# CPU baseline: the C / numpy restatement of the same forward + backward (one iteration, host cores)
+# ---------------------------------------------------------------------------------------------------------
+
+def cpu_baseline(sc: dict) -> dict:
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+    import oracle as O
+    from threadpoolctl import threadpool_limits
+
+    cam0 = sc['camera']
+    app = sc['appearance']
+    W, H = cam0['width'], cam0['height']
+    cam = O.Camera(w2c=cam0['w2c'], position=cam0['position'], width=W, height=H, focal_x=cam0['focal_x'],
+                   focal_y=cam0['focal_y'], center_x=cam0['center_x'], center_y=cam0['center_y'], bg=np.zeros(3, np.float32),
+                   degree=app['max_degree'] if app['model'] != 'neural' else 1, near_plane=cam0['near_plane'],
+                   far_plane=cam0['far_plane'])
+    mlp = O.MLPConfig(**app['mlp']) if app.get('mlp') else None
+    scene = O.Scene(means=sc['means'], scales=sc['scales'], rotations=sc['rotations'], opacities=sc['opacities'],
+                    base_colors=sc['base_colors'], residual_params=sc['residual_params'], mlp_weights=sc['mlp_weights'])
+    oapp = O.Appearance(model=app['model'], base_act=app['base_act'], res_act=app['res_act'], color_act=app['color_act'],
+                        direction_gradient=app['direction_gradient'], max_degree=app['max_degree'], mlp=mlp)
+    O.build()
+    log('cpu baseline: one forward + backward through the CPU restatement')
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        fw = O.render(scene, oapp, cam)
+        grad = np.full(fw.image.shape, 1.0 / fw.image.size, np.float32)
+        O.backward(scene, oapp, cam, fw, grad)
+        seconds = time.perf_counter() - t0
+    return {'value': round(W * H / seconds / 1e6, 5), 'unit': 'Mpix/s', 'cores': 1, 'kind': 'port',
+            'sample': f'one forward + backward of the full {sc["model"]} scene ({sc["means"].shape[0]} Gaussians, {W}x{H}) '
+                      f'through the C/numpy CPU restatement, single thread, no Adam; {seconds:.1f} s'}
+
+
+def copy_calibration() -> None:
+    """A plain device copy of 1 GiB, five times: rocprofv3 FETCH_SIZE / WRITE_SIZE of this command read
+    1 GiB each per dispatch when the counters are exact."""
+    import torch
+    n = (1 << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device='cuda:0')
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_bytes': 4 * n, 'dispatches': 5}))
+
+
+def main() -> None:
+    args = parse_args()
+    world = int(os.environ.get('WORLD_SIZE', '1'))
+    if args.gpus != 1 or world != 1:
+        print(f'bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); '
+              'the rasterizer has no multi-GPU path', file=sys.stderr)
+        sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.steps < 1 or args.warmup < 0:
+        raise SystemExit('bench.py: --steps must be >= 1 and --warmup >= 0')
+    r = gpu_benchmark(args)
+    W, H = r['W'], r['H']
+    value = W * H / (r['ms_per_step'] * 1e-3) / 1e6
+    line = {
+        'metric': 'fwd+bwd Mpix/s @1M Gaussians 1080p (Neural); % HBM/MFMA roofline per kernel',
+        'value': round(value, 3),
+        'unit': 'Mpix/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(r['ms_per_step'], 4),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f32 (f16 MFMA MLP)' if r['model'] == 'neural' else 'f32',
+        'data': 'synthetic',
+        'config': {'workload': f'{args.config}: {r["N"]} Gaussians, {W}x{H}, {r["model"]} appearance, L1 loss, fused Adam',
+                   'n_gaussians': r['N'], 'width': W, 'height': H, 'appearance': r['model'],
+                   'visible': round(r['V']), 'instances': round(r['I'])},
+        'fwd_bwd_mpix_s': round(W * H / (r['fwd_bwd_ms'] * 1e-3) / 1e6, 3),
+        'fwd_bwd_ms': round(r['fwd_bwd_ms'], 4),
+        'adam_ms': round(r['adam_ms'], 4),
+        'roofline': r['roofline'],
+        'stages': r['stages'],
+        'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(r['scene']),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

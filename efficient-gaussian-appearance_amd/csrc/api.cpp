@@ -22,6 +22,102 @@ thread_local std::string t_error;
 void set_error(const std::string& msg) { t_error = msg; }
 const char* error_message() { return t_error.c_str(); }
 
+// Pairs of HIP events around pipeline stages, recorded on the launching stream while enabled; collect()
+// waits for them and folds the elapsed times into per-stage totals. Events are pooled and reused.
+class StageTimer {
+  public:
+    StageTimer() = default;
+    StageTimer(const StageTimer&) = delete;
+    StageTimer& operator=(const StageTimer&) = delete;
+    ~StageTimer() {
+        release(open_);
+        for (const Pair& p : pending_) release(p);
+        for (hipEvent_t e : pool_) (void)hipEventDestroy(e);
+    }
+
+    bool enable(bool on) {
+        if (!collect()) return false;
+        release(open_);
+        open_ = Pair{};
+        enabled_ = on;
+        for (int i = 0; i < EFGS_N_STAGES; i++) {
+            totals_[i] = 0.0;
+            launches_[i] = 0;
+        }
+        return true;
+    }
+
+    void begin(int stage, hipStream_t s) {
+        if (!enabled_) return;
+        release(open_);
+        open_ = Pair{stage, take(), take()};
+        if (!open_.start || !open_.stop || hipEventRecord(open_.start, s) != hipSuccess) {
+            release(open_);
+            open_ = Pair{};
+        }
+    }
+
+    void end(hipStream_t s) {
+        if (!enabled_ || !open_.start) return;
+        if (hipEventRecord(open_.stop, s) == hipSuccess) {
+            pending_.push_back(open_);
+        } else {
+            release(open_);
+        }
+        open_ = Pair{};
+        if (pending_.size() > max_pending) (void)collect();
+    }
+
+    bool collect() {
+        bool ok = true;
+        for (const Pair& p : pending_) {
+            float ms = 0.0f;
+            if (hipEventSynchronize(p.stop) == hipSuccess && hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+                totals_[p.stage] += ms;
+                launches_[p.stage] += 1;
+            } else {
+                ok = false;
+            }
+            release(p);
+        }
+        pending_.clear();
+        if (!ok) set_error("waiting for the stage timing events failed");
+        return ok;
+    }
+
+    double total_ms(int stage) const { return totals_[stage]; }
+    int64_t launches(int stage) const { return launches_[stage]; }
+
+  private:
+    struct Pair {
+        int stage = 0;
+        hipEvent_t start = nullptr;
+        hipEvent_t stop = nullptr;
+    };
+    static constexpr size_t max_pending = 1u << 14;
+
+    hipEvent_t take() {
+        if (!pool_.empty()) {
+            hipEvent_t e = pool_.back();
+            pool_.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        return hipEventCreateWithFlags(&e, hipEventDefault) == hipSuccess ? e : nullptr;
+    }
+    void release(const Pair& p) {
+        if (p.start) pool_.push_back(p.start);
+        if (p.stop) pool_.push_back(p.stop);
+    }
+
+    bool enabled_ = false;
+    Pair open_;
+    std::vector<Pair> pending_;
+    std::vector<hipEvent_t> pool_;
+    double totals_[EFGS_N_STAGES] = {};
+    int64_t launches_[EFGS_N_STAGES] = {};
+};
+
 }  // namespace efgs
 
 using namespace efgs;
@@ -44,6 +140,7 @@ struct efgs_rasterizer {
     int mlp_n_features = 0;
     bool mlp_base_input = false;
     uint32_t* host_counters = nullptr;  // pinned, 4 entries
+    efgs::StageTimer timer;
 };
 
 namespace {
@@ -218,24 +315,29 @@ bool get_preprocess_kernel(const efgs_rasterizer* r, int model, const char* kind
     return rtc_get_kernel(name, preamble, files, k);
 }
 
-// 0 (precomputed colours) when colours are supplied, else the configured model; -1 if none is configured
-uint32_t mlp_params(const efgs_rasterizer* r) {
-    const uint32_t n = static_cast<uint32_t>(r->mlp_n_neurons);
-    return n * static_cast<uint32_t>(r->mlp_n_in_padded) + static_cast<uint32_t>(r->mlp_n_hidden - 1) * n * n + 16 * n;
+struct MlpShape {
+    uint32_t n_in_padded, n_neurons, n_hidden;
+};
+
+MlpShape mlp_shape(const efgs_rasterizer* r) {
+    return MlpShape{static_cast<uint32_t>(r->mlp_n_in_padded), static_cast<uint32_t>(r->mlp_n_neurons), static_cast<uint32_t>(r->mlp_n_hidden)};
 }
+
+// fp16 weight count of the tcnn-flat layout [W0 n x in_pad][W_h n x n]*(L-1)[W_out 16 x n]
+uint32_t mlp_params(const MlpShape& m) { return m.n_neurons * m.n_in_padded + (m.n_hidden - 1) * m.n_neurons * m.n_neurons + 16 * m.n_neurons; }
 
 // dynamic LDS of the neural preprocess kernels: fp16 weights + 4 per-wave staging areas (forward); the
 // backward reuses the area for the fp32 block reduction of the weight gradients
-uint32_t mlp_smem_forward(const efgs_rasterizer* r) {
-    const uint32_t inp = static_cast<uint32_t>(r->mlp_n_in_padded), nn = static_cast<uint32_t>(r->mlp_n_neurons);
+uint32_t mlp_smem_forward(const MlpShape& m) {
+    const uint32_t inp = m.n_in_padded, nn = m.n_neurons;
     const uint32_t maxk = inp > nn ? inp : nn;
     const uint32_t row = maxk > 2 * inp ? maxk : 2 * inp;
-    const uint32_t weight_bytes = (mlp_params(r) * 2 + 15) / 16 * 16;
+    const uint32_t weight_bytes = (mlp_params(m) * 2 + 15) / 16 * 16;
     return weight_bytes + 4 * 64 * row * 2;
 }
 
-uint32_t mlp_smem_backward(const efgs_rasterizer* r) {
-    const uint32_t f = mlp_smem_forward(r), red = mlp_params(r) * 4;
+uint32_t mlp_smem_backward(const MlpShape& m) {
+    const uint32_t f = mlp_smem_forward(m), red = mlp_params(m) * 4;
     return f > red ? f : red;
 }
 
@@ -243,6 +345,7 @@ constexpr uint32_t max_dynamic_lds = 64 * 1024;
 constexpr uint32_t neural_forward_blocks = 1024;
 constexpr uint32_t neural_backward_blocks = 512;
 
+// 0 (precomputed colours) when colours are supplied, else the configured model; -1 if none is configured
 int variant_of(const efgs_rasterizer* r, const efgs_primitives* prims) {
     if (prims->precomputed_colors != nullptr) return 0;
     return r->appearance_set ? r->model : -1;
@@ -369,11 +472,9 @@ int efgs_set_residual_mlp(efgs_rasterizer* r, int n_input_dims, int n_output_dim
     const int features = raw_features - (base_input ? 3 : 0);
     if (features < 1) return fail(EFGS_ERR_INVALID_ARGUMENT, "no learned features left for the residual mlp");
     if (n_input_dims > 128) return fail(EFGS_ERR_INVALID_ARGUMENT, "n_input_dims above 128 is not supported");
-    efgs_rasterizer probe = *r;
-    probe.mlp_n_in_padded = (n_input_dims + 15) / 16 * 16;
-    probe.mlp_n_neurons = n_neurons;
-    probe.mlp_n_hidden = n_hidden_layers;
-    if (mlp_smem_backward(&probe) > max_dynamic_lds)
+    const MlpShape probe{static_cast<uint32_t>((n_input_dims + 15) / 16 * 16), static_cast<uint32_t>(n_neurons),
+                         static_cast<uint32_t>(n_hidden_layers)};
+    if (mlp_smem_backward(probe) > max_dynamic_lds)
         return fail(EFGS_ERR_INVALID_ARGUMENT, "the residual mlp exceeds the 64 KiB LDS budget of the fused kernels");
     r->mlp_set = true;
     r->mlp_n_in = n_input_dims;
@@ -422,6 +523,7 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     const PrimitiveLayout pl = PrimitiveLayout::carve(pblob, n);
     const TileLayout tl = TileLayout::carve(tblob, n_tiles);
     const CameraArgs cam = camera_args(r, settings, variant, grid_w, grid_h);
+    StageTimer& t = r->timer;
 
     if (n > 0) {
         RtcKernel k;
@@ -444,38 +546,54 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         a.cam = cam;
         const uint32_t chunks = div_up(n, preprocess_block);
         const uint32_t blocks = variant == 5 ? (chunks < neural_forward_blocks ? chunks : neural_forward_blocks) : chunks;
-        const uint32_t shared = variant == 5 ? mlp_smem_forward(r) : 0u;
+        const uint32_t shared = variant == 5 ? mlp_smem_forward(mlp_shape(r)) : 0u;
+        t.begin(EFGS_STAGE_PREPROCESS_FORWARD, s);
         if (!launch_rtc(k, blocks, preprocess_block, shared, &a, s)) return EFGS_ERR_HIP;
+        t.end(s);
+        t.begin(EFGS_STAGE_COMPACT, s);
         if (!launch_scan_block_counts(pl.block_counts, pl.block_offsets, pl.counters, chunks, s)) return EFGS_ERR_HIP;
         if (!launch_compact_visible(pl.n_touched, pl.depth_keys, pl.block_offsets, pl.keys_a, pl.vals_a, n, s)) return EFGS_ERR_HIP;
+        t.end(s);
     } else {
         if (!launch_fill_u32(pl.counters, 0u, 4, s)) return EFGS_ERR_HIP;
     }
+    t.begin(EFGS_STAGE_COUNTER_READ, s);
     if (hipMemcpyAsync(r->host_counters, pl.counters, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return fail(EFGS_ERR_HIP, std::string("reading the visible/instance counters failed: ") + hipGetErrorString(hipGetLastError()));
+    t.end(s);
     const uint32_t n_visible = r->host_counters[0];
     const uint32_t n_instances = r->host_counters[1];
 
     bool depth_in_b = false;
+    t.begin(EFGS_STAGE_DEPTH_SORT, s);
     if (!radix_sort_pairs(pl.keys_a, pl.vals_a, pl.keys_b, pl.vals_b, false, n_visible, 4, 32, pl.sort_scratch, &depth_in_b, s))
         return EFGS_ERR_HIP;
+    t.end(s);
     const uint32_t* depth_sorted_prims = depth_in_b ? pl.vals_b : pl.vals_a;
+    t.begin(EFGS_STAGE_INSTANCE_OFFSETS, s);
     if (!scan_exclusive(pl.n_touched, depth_sorted_prims, pl.offsets, nullptr, n_visible, pl.scan_scratch, s)) return EFGS_ERR_HIP;
+    t.end(s);
 
     const InstanceLayout il0 = InstanceLayout::carve(nullptr, n_instances, key_bytes);
     char* iblob = static_cast<char*>(alloc(alloc_ctx, il0.bytes));
     if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
     const InstanceLayout il = InstanceLayout::carve(iblob, n_instances, key_bytes);
+    t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
     if (!launch_create_instances(depth_sorted_prims, pl.offsets, pl.n_touched, pl.records, il.keys_a, key_bytes, il.inst_prim, pl.prim_offset,
                                  pl.counters, grid_w, n_visible, s))
         return EFGS_ERR_HIP;
+    t.end(s);
     bool tiles_in_b = false;
+    t.begin(EFGS_STAGE_TILE_SORT, s);
     if (!radix_sort_pairs(il.keys_a, il.vals_a, il.keys_b, il.vals_b, true, n_instances, key_bytes, end_bit, il.sort_scratch, &tiles_in_b, s))
         return EFGS_ERR_HIP;
+    t.end(s);
     const void* sorted_keys = tiles_in_b ? il.keys_b : il.keys_a;
     const uint32_t* sorted_inst = tiles_in_b ? il.vals_b : il.vals_a;
+    t.begin(EFGS_STAGE_TILE_RANGES, s);
     if (!launch_tile_ranges(sorted_keys, key_bytes, tl.ranges, n_instances, n_tiles, s)) return EFGS_ERR_HIP;
+    t.end(s);
 
     BlendForwardArgs b;
     b.ranges = tl.ranges;
@@ -491,7 +609,9 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     b.height = static_cast<uint32_t>(settings->height);
     b.grid_w = grid_w;
     b.n_tiles = n_tiles;
+    t.begin(EFGS_STAGE_BLEND_FORWARD, s);
     if (!launch_blend_forward(b, s)) return EFGS_ERR_HIP;
+    t.end(s);
 
     frame->primitive_buffers = pblob;
     frame->tile_buffers = tblob;
@@ -555,7 +675,10 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     b.height = static_cast<uint32_t>(settings->height);
     b.grid_w = grid_w;
     b.n_tiles = n_tiles;
+    StageTimer& t = r->timer;
+    t.begin(EFGS_STAGE_BLEND_BACKWARD, s);
     if (!launch_blend_backward(b, s)) return EFGS_ERR_HIP;
+    t.end(s);
 
     RtcKernel k;
     if (!get_preprocess_kernel(r, variant, "backward", k)) return EFGS_ERR_RTC;
@@ -585,17 +708,23 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     a.cam = camera_args(r, settings, variant, grid_w, grid_h);
     const uint32_t chunks = div_up(n, preprocess_block);
     if (variant != 5) {
+        t.begin(EFGS_STAGE_PREPROCESS_BACKWARD, s);
         if (!launch_rtc(k, chunks, preprocess_block, 0u, &a, s)) return EFGS_ERR_HIP;
+        t.end(s);
         return EFGS_OK;
     }
     if (!grads->mlp_weights) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp weight gradient output is required");
     const uint32_t blocks = chunks < neural_backward_blocks ? chunks : neural_backward_blocks;
-    const uint32_t params = mlp_params(r);
+    const uint32_t params = mlp_params(mlp_shape(r));
     float* partials = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(blocks) * params * sizeof(float)));
     if (!partials) return fail(EFGS_ERR_ALLOC, "allocation of the mlp gradient partials failed");
     a.g_mlp_partials = partials;
-    if (!launch_rtc(k, blocks, preprocess_block, mlp_smem_backward(r), &a, s)) return EFGS_ERR_HIP;
+    t.begin(EFGS_STAGE_PREPROCESS_BACKWARD, s);
+    if (!launch_rtc(k, blocks, preprocess_block, mlp_smem_backward(mlp_shape(r)), &a, s)) return EFGS_ERR_HIP;
+    t.end(s);
+    t.begin(EFGS_STAGE_MLP_REDUCE, s);
     if (!launch_reduce_partials(partials, blocks, params, grads->mlp_weights, s)) return EFGS_ERR_HIP;
+    t.end(s);
     return EFGS_OK;
 }
 
@@ -626,6 +755,21 @@ int efgs_adam_step(const efgs_adam_group* groups, int n_groups, void* stream) {
         d.first_block = 0;
     }
     if (!launch_adam(dev.data(), n_groups, static_cast<hipStream_t>(stream))) return EFGS_ERR_HIP;
+    return EFGS_OK;
+}
+
+int efgs_set_stage_timing(efgs_rasterizer* r, int enable) {
+    if (!r) return fail(EFGS_ERR_INVALID_ARGUMENT, "null rasterizer");
+    return r->timer.enable(enable != 0) ? EFGS_OK : EFGS_ERR_HIP;
+}
+
+int efgs_get_stage_times(efgs_rasterizer* r, double* total_ms, int64_t* launches, int n_stages) {
+    if (!r || n_stages < 0 || (n_stages > 0 && (!total_ms || !launches))) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid argument");
+    if (!r->timer.collect()) return EFGS_ERR_HIP;
+    for (int i = 0; i < n_stages; i++) {
+        total_ms[i] = i < EFGS_N_STAGES ? r->timer.total_ms(i) : 0.0;
+        launches[i] = i < EFGS_N_STAGES ? r->timer.launches(i) : 0;
+    }
     return EFGS_OK;
 }
 

@@ -69,7 +69,11 @@ lib = ctypes.CDLL(LIB_PATH)
 
 EXPORTED = ('efgs_last_error', 'efgs_set_rtc_dirs', 'efgs_rasterizer_create', 'efgs_rasterizer_destroy', 'efgs_set_appearance',
             'efgs_set_residual_mlp', 'efgs_mlp_param_count', 'efgs_forward', 'efgs_backward', 'efgs_adam_step',
-            'efgs_get_frame_views', 'efgs_precompile')
+            'efgs_get_frame_views', 'efgs_precompile', 'efgs_set_stage_timing', 'efgs_get_stage_times')
+
+# stage ids of efgs_get_stage_times, in order (include/efgs.h)
+STAGES = ('preprocess_forward', 'compact', 'counter_read', 'depth_sort', 'instance_offsets', 'create_instances', 'tile_sort',
+          'tile_ranges', 'blend_forward', 'blend_backward', 'preprocess_backward', 'mlp_reduce')
 
 lib.efgs_last_error.restype = ctypes.c_char_p
 lib.efgs_last_error.argtypes = []
@@ -88,6 +92,8 @@ lib.efgs_backward.argtypes = [ctypes.c_void_p, ctypes.POINTER(Primitives), ctype
 lib.efgs_adam_step.argtypes = [ctypes.POINTER(AdamGroup), ctypes.c_int, ctypes.c_void_p]
 lib.efgs_get_frame_views.argtypes = [ctypes.POINTER(Frame), ctypes.POINTER(FrameViews)]
 lib.efgs_precompile.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
+lib.efgs_set_stage_timing.argtypes = [ctypes.c_void_p, ctypes.c_int]
+lib.efgs_get_stage_times.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_int]
 
 
 def check(rc: int) -> None:

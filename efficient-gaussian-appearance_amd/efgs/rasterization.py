@@ -47,6 +47,18 @@ class Rasterizer:
     def precompile(self, arch: str = 'gfx950') -> None:
         check(lib.efgs_precompile(self.handle, arch.encode()))
 
+    def set_stage_timing(self, enable: bool) -> None:
+        """Enables (and resets) or disables HIP-event timing of the pipeline stages on their launch stream."""
+        check(lib.efgs_set_stage_timing(self.handle, int(bool(enable))))
+
+    def stage_times(self) -> dict[str, tuple[float, int]]:
+        """Per stage: (summed milliseconds, timed launches) since timing was enabled; waits for the events."""
+        n = len(_lib.STAGES)
+        ms = (ctypes.c_double * n)()
+        cnt = (ctypes.c_int64 * n)()
+        check(lib.efgs_get_stage_times(self.handle, ms, cnt, n))
+        return {name: (float(ms[i]), int(cnt[i])) for i, name in enumerate(_lib.STAGES)}
+
 
 # module-level rasterizer instance owning the specialised kernels (as the reference's _rasterizer)
 _rasterizer = Rasterizer()
@@ -145,6 +157,10 @@ def _native_primitives(means, scales, rotations, opacities, precomputed_colors, 
     return p
 
 
+# primitive, visible-primitive, instance and tile counts of the most recent forward (read back by every forward)
+last_frame_counts: dict[str, int] = {}
+
+
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -168,6 +184,8 @@ def _forward(means, scales, rotations, opacities, precomputed_colors, base_color
         frame = _lib.Frame()
         check(lib.efgs_forward(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), image.data_ptr(), alloc.fn, None,
                                ctypes.byref(frame), _stream(device)))
+    last_frame_counts.update(n_primitives=int(frame.n_primitives), n_visible=int(frame.n_visible),
+                             n_instances=int(frame.n_instances), n_tiles=int(frame.grid_width) * int(frame.grid_height))
     return image, frame, alloc.tensors, keep
 
 

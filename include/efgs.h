@@ -182,6 +182,28 @@ int efgs_get_frame_views(const efgs_frame* frame, efgs_frame_views* views);
  * "gfx950") without using a device (no counterpart in the reference; build step). */
 int efgs_precompile(const efgs_rasterizer* r, const char* arch);
 
+/* Stage timing (no counterpart in the reference: instrumentation for the roofline report). While enabled,
+ * efgs_forward / efgs_backward record a pair of HIP events around each stage on the stream they launch on;
+ * efgs_get_stage_times waits for the recorded events and returns, per stage, the summed milliseconds and
+ * the number of timed launches since timing was (re-)enabled. Enabling again resets the totals. */
+enum {
+    EFGS_STAGE_PREPROCESS_FORWARD = 0, /* hipRTC preprocess (projection, culling, appearance, MLP) */
+    EFGS_STAGE_COMPACT = 1,            /* per-block count scan + index-ordered compaction */
+    EFGS_STAGE_COUNTER_READ = 2,       /* (V, I) device-to-host read and stream synchronisation */
+    EFGS_STAGE_DEPTH_SORT = 3,
+    EFGS_STAGE_INSTANCE_OFFSETS = 4,   /* gathered exclusive scan of the tile counts */
+    EFGS_STAGE_CREATE_INSTANCES = 5,
+    EFGS_STAGE_TILE_SORT = 6,
+    EFGS_STAGE_TILE_RANGES = 7,
+    EFGS_STAGE_BLEND_FORWARD = 8,
+    EFGS_STAGE_BLEND_BACKWARD = 9,
+    EFGS_STAGE_PREPROCESS_BACKWARD = 10,
+    EFGS_STAGE_MLP_REDUCE = 11,        /* reduction of the per-block MLP weight-gradient partials */
+    EFGS_N_STAGES = 12
+};
+int efgs_set_stage_timing(efgs_rasterizer* r, int enable);
+int efgs_get_stage_times(efgs_rasterizer* r, double* total_ms, int64_t* launches, int n_stages);
+
 #ifdef __cplusplus
 }
 #endif
