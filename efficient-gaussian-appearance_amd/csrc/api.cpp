@@ -675,6 +675,7 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     b.height = static_cast<uint32_t>(settings->height);
     b.grid_w = grid_w;
     b.n_tiles = n_tiles;
+    b.abs_grads = grads->densification_rows > 2 ? 1u : 0u;
     StageTimer& t = r->timer;
     t.begin(EFGS_STAGE_BLEND_BACKWARD, s);
     if (!launch_blend_backward(b, s)) return EFGS_ERR_HIP;

@@ -9,9 +9,10 @@
 //
 // Backward: every pixel replays its forward walk (the evaluation below is shared and compiled with
 // -ffp-contract=off, so T and every skip decision are reproduced bit-exactly) and forms the reference's
-// per-pixel terms; the 11 per-Gaussian values are summed over the wave (lanes = pixels), each wave keeps
-// its own LDS slot per Gaussian, and the three band sums are added in a fixed order into one 48-byte record
-// per instance at its emission slot. No float atomics; the result is run-to-run deterministic.
+// per-pixel terms; the 9 per-Gaussian values (11 with the |dL/dmean2d| pair) are summed over the wave
+// (lanes = pixels) with DPP row operations, each wave keeps its own LDS slot per Gaussian, and the three band
+// sums are added in a fixed order into one 48-byte record per instance at its emission slot. No float
+// atomics; the result is run-to-run deterministic.
 //
 // Reference: B/rasterization/include/kernels_forward.cuh:26-166, kernels_backward.cuh:12-231.
 #include "internal.h"
@@ -21,7 +22,6 @@ namespace efgs {
 namespace {
 
 constexpr float log2e = 1.44269504089f;
-constexpr uint32_t grad_values = 11;
 
 struct Staged {
     float2 xy;
@@ -43,12 +43,6 @@ __device__ __forceinline__ float eval_alpha(float2 xy, float4 co, float pxf, flo
 
 __device__ __forceinline__ bool band_overlap(uint2 b, uint32_t bx0, uint32_t bx1, uint32_t by0, uint32_t by1) {
     return (b.x & 0xffffu) < bx1 && bx0 < (b.x >> 16) && (b.y & 0xffffu) < by1 && by0 < (b.y >> 16);
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
@@ -129,13 +123,37 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
     if (tid == 0) a.tile_max[tile] = max(max(s_max[0], s_max[1]), s_max[2]);
 }
 
+// Sum over the wave's 64 lanes, complete in lane 63 (the other lanes hold partial sums). Row shifts by 1, 2,
+// 4 and 8 form 16-lane prefix sums (lane 15 of each row holds its row's sum); the row-15 broadcast adds row 0
+// into row 1 and row 2 into row 3, the row-31 broadcast adds rows 0-1 into rows 2-3. Every step is one
+// full-rate VALU add with a DPP operand; the order is fixed, so the sum is reproducible.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float add_dpp(float v) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+    return v + __int_as_float(moved);
+}
+
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+    v = add_dpp<0x111, 0xf>(v);  // row_shr:1
+    v = add_dpp<0x112, 0xf>(v);  // row_shr:2
+    v = add_dpp<0x114, 0xf>(v);  // row_shr:4
+    v = add_dpp<0x118, 0xf>(v);  // row_shr:8
+    v = add_dpp<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v = add_dpp<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// ABS: also reduce |dL/dmean2d| per pixel (needed only for the third densification row)
+template <bool ABS>
 __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwardArgs a) {
+    constexpr uint32_t n_values = ABS ? 11u : 9u;
+    constexpr uint32_t n_waves = tile_pixels / 64;
     __shared__ float2 s_xy[tile_pixels];
-    __shared__ float4 s_co[tile_pixels];
-    __shared__ float4 s_craw[tile_pixels];
+    __shared__ float4 s_co[tile_pixels];   // raw conic (x, y, z), opacity
     __shared__ float4 s_col[tile_pixels];
     __shared__ uint2 s_b[tile_pixels];
-    __shared__ float s_grad[tile_pixels / 64][tile_pixels][grad_values];
+    __shared__ float4 s_grad4[n_waves * n_values * tile_pixels / 4];
+    float (*s_grad)[n_values][tile_pixels] = reinterpret_cast<float (*)[n_values][tile_pixels]>(s_grad4);
 
     const uint32_t tile = blockIdx.x;
     const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
@@ -176,15 +194,11 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
             e_own = a.sorted_inst[range.x + start + tid];
             const PrimRecord rec = a.records[a.inst_prim[e_own]];
             s_xy[tid] = make_float2(rec.r0.x, rec.r0.y);
-            s_co[tid] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
-            s_craw[tid] = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, 0.0f);
+            s_co[tid] = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
             s_col[tid] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
             s_b[tid] = make_uint2(__float_as_uint(rec.r2.y), __float_as_uint(rec.r2.z));
         }
-#pragma unroll
-        for (uint32_t w = 0; w < tile_pixels / 64; w++)
-#pragma unroll
-            for (uint32_t c = 0; c < grad_values; c++) s_grad[w][tid][c] = 0.0f;
+        for (uint32_t k = tid; k < n_waves * n_values * tile_pixels / 4; k += tile_pixels) s_grad4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         __syncthreads();
         const uint32_t batch_n = min(tile_pixels, n_total - start);
         const uint32_t batch_proc = min(tile_pixels, n_proc - start);
@@ -195,17 +209,17 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
             while (mask != 0) {
                 const uint32_t jj = c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
                 mask &= mask - 1;
-                float v[grad_values];
+                float v[11];
 #pragma unroll
-                for (uint32_t c = 0; c < grad_values; c++) v[c] = 0.0f;
+                for (uint32_t c = 0; c < 11; c++) v[c] = 0.0f;
                 bool contrib = false;
                 if (start + jj < last) {
+                    const float4 cr = s_co[jj];
                     float dx, dy, G;
-                    const float alpha = eval_alpha(s_xy[jj], s_co[jj], pxf, pyf, dx, dy, G);
+                    const float alpha = eval_alpha(s_xy[jj], scale_conic_for_exp2(cr.x, cr.y, cr.z, cr.w), pxf, pyf, dx, dy, G);
                     if (alpha >= min_alpha) {
                         contrib = true;
                         const float4 col = s_col[jj];
-                        const float4 cr = s_craw[jj];
                         const float w = T * alpha;
                         v[6] = w * gr; v[7] = w * gg; v[8] = w * gb;
                         ar -= w * col.x; ag -= w * col.y; ab -= w * col.z;
@@ -226,19 +240,22 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
                     }
                 }
                 if (__ballot(contrib) != 0) {
+                    float sum[n_values];
 #pragma unroll
-                    for (uint32_t c = 0; c < grad_values; c++) {
-                        const float s = wave_sum(v[c]);
-                        if (lane == 0) s_grad[wave][jj][c] = s;
+                    for (uint32_t c = 0; c < n_values; c++) sum[c] = wave_sum_to_lane63(v[c]);
+                    if (lane == 63) {
+#pragma unroll
+                        for (uint32_t c = 0; c < n_values; c++) s_grad[wave][c][jj] = sum[c];
                     }
                 }
             }
         }
         __syncthreads();
         if (tid < batch_n) {
-            float g[grad_values];
+            float g[11];
 #pragma unroll
-            for (uint32_t c = 0; c < grad_values; c++) g[c] = (s_grad[0][tid][c] + s_grad[1][tid][c]) + s_grad[2][tid][c];
+            for (uint32_t c = 0; c < n_values; c++) g[c] = (s_grad[0][c][tid] + s_grad[1][c][tid]) + s_grad[2][c][tid];
+            if (!ABS) g[9] = g[10] = 0.0f;
             float4* out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(e_own);
             out[0] = make_float4(g[0], g[1], g[2], g[3]);
             out[1] = make_float4(g[4], g[5], g[6], g[7]);
@@ -268,7 +285,10 @@ bool launch_blend_forward(const BlendForwardArgs& a, hipStream_t s) {
 
 bool launch_blend_backward(const BlendBackwardArgs& a, hipStream_t s) {
     if (a.n_tiles == 0) return true;
-    blend_backward_kernel<<<a.n_tiles, tile_pixels, 0, s>>>(a);
+    if (a.abs_grads)
+        blend_backward_kernel<true><<<a.n_tiles, tile_pixels, 0, s>>>(a);
+    else
+        blend_backward_kernel<false><<<a.n_tiles, tile_pixels, 0, s>>>(a);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

@@ -85,6 +85,7 @@ struct BlendBackwardArgs {
     const uint32_t* tile_max;
     float* inst_grads;             // (I x 12), emission order
     uint32_t width, height, grid_w, n_tiles;
+    uint32_t abs_grads;            // also reduce |dL/dmean2d| (third densification row)
 };
 bool launch_blend_backward(const BlendBackwardArgs& a, hipStream_t s);
 

@@ -102,13 +102,27 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
     }
 }
 
-// out[i] = sum over blocks b (in order) of partials[b][i]
-__global__ void reduce_partials_kernel(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_params) return;
-    float s = 0.0f;
-    for (uint32_t b = 0; b < n_blocks; b++) s += partials[static_cast<size_t>(b) * n_params + i];
-    out[i] = s;
+// out[i] = sum over blocks b of partials[b][i]. A block covers 64 parameters with 16 groups of 64 lanes;
+// group g sums blocks g, g + 16, ... in order, then the 16 group sums are added in group order (fixed
+// order, reproducible).
+constexpr uint32_t reduce_groups = 16;
+__global__ __launch_bounds__(64 * reduce_groups) void reduce_partials_kernel(const float* partials, uint32_t n_blocks, uint32_t n_params,
+                                                                          float* out) {
+    __shared__ float s_part[reduce_groups][64];
+    const uint32_t lane = threadIdx.x & 63u, g = threadIdx.x >> 6;
+    const uint32_t i = blockIdx.x * 64u + lane;
+    float acc = 0.0f;
+    if (i < n_params) {
+#pragma unroll 4
+        for (uint32_t b = g; b < n_blocks; b += reduce_groups) acc += partials[static_cast<size_t>(b) * n_params + i];
+    }
+    s_part[g][lane] = acc;
+    __syncthreads();
+    if (g == 0 && i < n_params) {
+        float t = s_part[0][lane];
+        for (uint32_t k = 1; k < reduce_groups; k++) t += s_part[k][lane];
+        out[i] = t;
+    }
 }
 
 template <typename KeyT>
@@ -158,7 +172,7 @@ bool launch_create_instances(const uint32_t* sorted_prims, const uint32_t* offse
 
 bool launch_reduce_partials(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out, hipStream_t s) {
     if (n_params == 0) return true;
-    reduce_partials_kernel<<<div_up(n_params, 256), 256, 0, s>>>(partials, n_blocks, n_params, out);
+    reduce_partials_kernel<<<div_up(n_params, 64), 64 * reduce_groups, 0, s>>>(partials, n_blocks, n_params, out);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
