@@ -123,24 +123,62 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
     if (tid == 0) a.tile_max[tile] = max(max(s_max[0], s_max[1]), s_max[2]);
 }
 
-// Sum over the wave's 64 lanes, complete in lane 63 (the other lanes hold partial sums). Row shifts by 1, 2,
-// 4 and 8 form 16-lane prefix sums (lane 15 of each row holds its row's sum); the row-15 broadcast adds row 0
-// into row 1 and row 2 into row 3, the row-31 broadcast adds rows 0-1 into rows 2-3. Every step is one
-// full-rate VALU add with a DPP operand; the order is fixed, so the sum is reproducible.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float add_dpp(float v) {
-    const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
-    return v + __int_as_float(moved);
+// Wave sums of several per-lane values at once ("transposing" reductions). Each exchange step swaps half of
+// the values between lane groups so that every lane keeps fewer values, each summed over more lanes:
+//   permlane32 swap: lanes l and l + 32 exchange, a pair of registers becomes one register holding value
+//                    a in lanes 0-31 and value b in lanes 32-63 (sums over 2 lanes);
+//   permlane16 swap: 16-lane rows 1, 3 of the first register exchange with rows 0, 2 of the second; two such
+//                    registers become one holding four values, one per row (sums over 4 lanes);
+//   row_ror:8      : the two 8-lane halves of a row exchange, two registers become one holding eight
+//                    values, one per half-row (sums over 8 lanes);
+// and plain DPP adds (quad permutations, row_shr) finish the remaining lanes. Every step is a full-rate
+// VALU operation and the order is fixed, so the sums are reproducible.
+template <int CTRL, int ROW_MASK, bool BOUND_CTRL>
+__device__ __forceinline__ float dpp(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xf, BOUND_CTRL));
 }
 
-__device__ __forceinline__ float wave_sum_to_lane63(float v) {
-    v = add_dpp<0x111, 0xf>(v);  // row_shr:1
-    v = add_dpp<0x112, 0xf>(v);  // row_shr:2
-    v = add_dpp<0x114, 0xf>(v);  // row_shr:4
-    v = add_dpp<0x118, 0xf>(v);  // row_shr:8
-    v = add_dpp<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
-    v = add_dpp<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
-    return v;
+// v32 + swapped partner; returns a register with a's pair sums in lanes 0-31 and b's in lanes 32-63
+__device__ __forceinline__ float swap32_add(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// rows (0, 1, 2, 3) of the result: a rows 0+1, b rows 0+1, a rows 2+3, b rows 2+3
+__device__ __forceinline__ float swap16_add(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Eight values -> lanes 8m + 7 (m = 0..7) hold complete sums; value index of lane l: see reduced8_index.
+__device__ __forceinline__ float transpose_reduce8(const float* v, uint32_t lane) {
+    const float w0 = swap32_add(v[0], v[1]), w1 = swap32_add(v[2], v[3]);
+    const float w2 = swap32_add(v[4], v[5]), w3 = swap32_add(v[6], v[7]);
+    // rows of x0: v0, v2, v1, v3; rows of x1: v4, v6, v5, v7 (each summed over the 4 lanes equal mod 16)
+    const float x0 = swap16_add(w0, w1), x1 = swap16_add(w2, w3);
+    const bool hi = (lane & 8u) != 0;
+    const float keep = hi ? x1 : x0, send = hi ? x0 : x1;
+    float y = keep + dpp<0x128, 0xf, false>(0.0f, send);  // row_ror:8
+    y += dpp<0xB1, 0xf, false>(0.0f, y);                    // quad_perm [1, 0, 3, 2]
+    y += dpp<0x4E, 0xf, false>(0.0f, y);                    // quad_perm [2, 3, 0, 1]
+    y += dpp<0x114, 0xf, true>(0.0f, y);                    // row_shr:4; lanes 4-7 / 12-15 of a row complete
+    return y;
+}
+
+__device__ __forceinline__ uint32_t reduced8_index(uint32_t lane) {
+    const uint32_t row = lane >> 4, half = (lane >> 3) & 1u;
+    return 4u * half + ((row & 1u) << 1) + (row >> 1);  // rows 0..3 hold values 0, 2, 1, 3 of the half
+}
+
+// Four values -> lanes 15, 31, 47, 63 hold complete sums of values 0, 2, 1, 3.
+__device__ __forceinline__ float transpose_reduce4(float u0, float u1, float u2, float u3) {
+    const float w0 = swap32_add(u0, u1), w1 = swap32_add(u2, u3);
+    float x = swap16_add(w0, w1);
+    x += dpp<0x111, 0xf, true>(0.0f, x);  // row_shr:1
+    x += dpp<0x112, 0xf, true>(0.0f, x);  // row_shr:2
+    x += dpp<0x114, 0xf, true>(0.0f, x);  // row_shr:4
+    x += dpp<0x118, 0xf, true>(0.0f, x);  // row_shr:8; lane 15 of each row complete
+    return x;
 }
 
 // ABS: also reduce |dL/dmean2d| per pixel (needed only for the third densification row)
@@ -240,12 +278,13 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
                     }
                 }
                 if (__ballot(contrib) != 0) {
-                    float sum[n_values];
-#pragma unroll
-                    for (uint32_t c = 0; c < n_values; c++) sum[c] = wave_sum_to_lane63(v[c]);
-                    if (lane == 63) {
-#pragma unroll
-                        for (uint32_t c = 0; c < n_values; c++) s_grad[wave][c][jj] = sum[c];
+                    const float s8 = transpose_reduce8(v, lane);
+                    const float s4 = transpose_reduce4(v[8], ABS ? v[9] : 0.0f, ABS ? v[10] : 0.0f, 0.0f);
+                    if ((lane & 7u) == 7u) s_grad[wave][reduced8_index(lane)][jj] = s8;
+                    if ((lane & 15u) == 15u) {
+                        const uint32_t row = lane >> 4;
+                        const uint32_t k = 8u + ((row & 1u) << 1) + (row >> 1);  // rows 0..3: values 8, 10, 9, 11
+                        if (k < n_values) s_grad[wave][k][jj] = s4;
                     }
                 }
             }
