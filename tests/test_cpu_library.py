@@ -34,6 +34,7 @@ def test_struct_sizes_match_header_layout():
 
 
 def test_invalid_ids_raise():
+    from efgs import _lib
     from efgs import rasterization as R
     r = R.Rasterizer()
     with pytest.raises(RuntimeError, match='invalid appearance model'):
@@ -47,6 +48,7 @@ def test_invalid_ids_raise():
 
 
 def test_residual_mlp_requires_neural_model():
+    from efgs import _lib
     from efgs import rasterization as R
     r = R.Rasterizer()
     with pytest.raises(RuntimeError, match='neural appearance model before set_residual_mlp'):
@@ -60,6 +62,7 @@ def test_residual_mlp_requires_neural_model():
 
 def test_forward_without_appearance_is_rejected_before_device_work():
     """Regression: an unconfigured rasterizer must not fall back to the precomputed-colour variant."""
+    from efgs import _lib
     from efgs import _lib
     from efgs import rasterization as R
     r = R.Rasterizer()
@@ -77,6 +80,7 @@ def test_forward_without_appearance_is_rejected_before_device_work():
 
 
 def test_precomputed_variant_requires_colours():
+    from efgs import _lib
     from efgs import _lib
     from efgs import rasterization as R
     r = R.Rasterizer()
@@ -103,3 +107,32 @@ def test_adam_validation():
     g.n_lrs = 1
     g.step = 0
     assert _lib.lib.efgs_adam_step(ctypes.byref(g), 1, None) == 1
+
+
+def test_stage_timing_without_launches():
+    """Timing can be enabled and read back without any GPU work: every stage reports zero launches."""
+    from efgs import _lib
+    from efgs import rasterization as R
+    r = R.Rasterizer()
+    r.set_stage_timing(True)
+    times = r.stage_times()
+    assert set(times) == set(_lib.STAGES) and len(_lib.STAGES) == 12
+    assert all(ms == 0.0 and n == 0 for ms, n in times.values())
+    r.set_stage_timing(False)
+
+
+def test_bench_algorithmic_bytes_match_the_c3_budget():
+    """The per-stage algorithmic byte formulas add up to the C3 forward + backward budget (670 MB at
+    V = 699,021 and I = 1,420,415; SURVEY's 675 MB also counts the reference's stored MLP outputs)."""
+    import sys
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    import bench
+    N, V, I, T, P = 1_000_000, 699_021, 1_420_415, 10_800, 1920 * 1080
+    F = bench.mlp_flops_per_primitive(11, 64, 2)
+    assert F == 9_984
+    stages = ['preprocess_forward', 'compact', 'depth_sort', 'instance_offsets', 'create_instances', 'tile_sort',
+              'tile_ranges', 'blend_forward', 'blend_backward', 'preprocess_backward']
+    total = sum(bench.algorithmic(s, N, V, I, T, P, 32, F, 0)[0] for s in stages)
+    assert abs(total / 1e6 - 670.0) < 1.0
+    assert bench.algorithmic('adam', N, V, I, T, P, 32, F, 22_006_144)[0] == 28 * 22_006_144
