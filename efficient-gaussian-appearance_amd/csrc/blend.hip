@@ -181,15 +181,25 @@ __device__ __forceinline__ float transpose_reduce4(float u0, float u1, float u2,
     return x;
 }
 
-// ABS: also reduce |dL/dmean2d| per pixel (needed only for the third densification row)
+// ABS: also reduce |dL/dmean2d| per pixel (needed only for the third densification row).
+//
+// Only alpha has to reproduce the forward bit for bit (it decides which Gaussians a pixel skips); T and the
+// gradient terms use fused multiply-adds and the hardware reciprocal. Per pixel and Gaussian the kernel
+// forms, branch-free (zero for pixels that skip the Gaussian),
+//   h = -alpha dL/dalpha,  dL/dalpha = T (c . g) - (A - g_bg) / max(1 - alpha, eps)
+// with A = (colour still to come) . g, and the wave sums
+//   h dx, h dy, h dx^2, h dx dy, h dy^2, G dL/dalpha, w g_r, w g_g, w g_b   (w = T alpha)
+// from which the instance's record is dL/dmean2d = (C h d summed), dL/dconic = 0.5 (h d d^T summed),
+// dL/dopacity-term = sum G dL/dalpha, dL/dcolour = sum w g.
 template <bool ABS>
 __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwardArgs a) {
     constexpr uint32_t n_values = ABS ? 11u : 9u;
     constexpr uint32_t n_waves = tile_pixels / 64;
     __shared__ float2 s_xy[tile_pixels];
-    __shared__ float4 s_co[tile_pixels];   // raw conic (x, y, z), opacity
+    __shared__ float4 s_co[tile_pixels];    // exp2-scaled conic (x, y, z), opacity
     __shared__ float4 s_col[tile_pixels];
     __shared__ uint2 s_b[tile_pixels];
+    __shared__ float4 s_craw[ABS ? tile_pixels : 1];  // raw conic, for the per-pixel |dL/dmean2d|
     __shared__ float4 s_grad4[n_waves * n_values * tile_pixels / 4];
     float (*s_grad)[n_values][tile_pixels] = reinterpret_cast<float (*)[n_values][tile_pixels]>(s_grad4);
 
@@ -206,8 +216,8 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
     const uint32_t n_total = range.y - range.x;
     const uint32_t n_proc = min(n_total, a.tile_max[tile]);
 
-    // pixel state: upstream gradient, colour still to come after each Gaussian, background term
-    float gr = 0.0f, gg = 0.0f, gb = 0.0f, ar = 0.0f, ag = 0.0f, ab = 0.0f, gac = 0.0f;
+    // pixel state: upstream gradient, (colour still to come) . g, background term
+    float gr = 0.0f, gg = 0.0f, gb = 0.0f, A = 0.0f, gbg = 0.0f;
     uint32_t last = 0;
     if (inside) {
         const uint32_t pix = py * a.width + px;
@@ -216,11 +226,13 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
         const float Tf = a.final_T[slot];
         last = a.n_contrib[slot];
         gr = a.grad_image[pix]; gg = a.grad_image[np + pix]; gb = a.grad_image[2 * np + pix];
-        ar = a.image[pix] - Tf * a.bg[0];
-        ag = a.image[np + pix] - Tf * a.bg[1];
-        ab = a.image[2 * np + pix] - Tf * a.bg[2];
-        gac = Tf * -(gr * a.bg[0] + gg * a.bg[1] + gb * a.bg[2]);
+        const float ar = a.image[pix] - Tf * a.bg[0];
+        const float ag = a.image[np + pix] - Tf * a.bg[1];
+        const float ab = a.image[2 * np + pix] - Tf * a.bg[2];
+        A = __builtin_fmaf(ab, gb, __builtin_fmaf(ag, gg, ar * gr));
+        gbg = Tf * -(gr * a.bg[0] + gg * a.bg[1] + gb * a.bg[2]);
     }
+    const uint32_t wave_last = wave_max_u32(last);  // no pixel of the band uses instances at or after this
     float T = 1.0f;
 
     uint32_t covered = 0;
@@ -228,77 +240,73 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
         __syncthreads();
         const bool own = start + tid < n_total;
         uint32_t e_own = 0;
+        float4 craw = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (own) {
             e_own = a.sorted_inst[range.x + start + tid];
             const PrimRecord rec = a.records[a.inst_prim[e_own]];
+            craw = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, 0.0f);
             s_xy[tid] = make_float2(rec.r0.x, rec.r0.y);
-            s_co[tid] = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
+            s_co[tid] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
             s_col[tid] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
             s_b[tid] = make_uint2(__float_as_uint(rec.r2.y), __float_as_uint(rec.r2.z));
+            if (ABS) s_craw[tid] = craw;
         }
         for (uint32_t k = tid; k < n_waves * n_values * tile_pixels / 4; k += tile_pixels) s_grad4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         __syncthreads();
         const uint32_t batch_n = min(tile_pixels, n_total - start);
-        const uint32_t batch_proc = min(tile_pixels, n_proc - start);
-        for (uint32_t c0 = 0; c0 < batch_proc; c0 += 64) {
+        const uint32_t batch_wave = wave_last > start ? min(min(tile_pixels, n_proc - start), wave_last - start) : 0u;
+        for (uint32_t c0 = 0; c0 < batch_wave; c0 += 64) {
             const uint32_t j = c0 + lane;
-            const bool ov = j < batch_proc && band_overlap(s_b[j], bx0, bx1, by0, by1);
+            const bool ov = j < batch_wave && band_overlap(s_b[j], bx0, bx1, by0, by1);
             uint64_t mask = __ballot(ov);
             while (mask != 0) {
                 const uint32_t jj = c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
                 mask &= mask - 1;
-                float v[11];
-#pragma unroll
-                for (uint32_t c = 0; c < 11; c++) v[c] = 0.0f;
-                bool contrib = false;
-                if (start + jj < last) {
-                    const float4 cr = s_co[jj];
-                    float dx, dy, G;
-                    const float alpha = eval_alpha(s_xy[jj], scale_conic_for_exp2(cr.x, cr.y, cr.z, cr.w), pxf, pyf, dx, dy, G);
-                    if (alpha >= min_alpha) {
-                        contrib = true;
-                        const float4 col = s_col[jj];
-                        const float w = T * alpha;
-                        v[6] = w * gr; v[7] = w * gg; v[8] = w * gb;
-                        ar -= w * col.x; ag -= w * col.y; ab -= w * col.z;
-                        const float oma = 1.0f - alpha;
-                        const float rcp = 1.0f / fmaxf(oma, one_minus_alpha_eps);
-                        const float dadc = (T * col.x - ar * rcp) * gr + (T * col.y - ag * rcp) * gg + (T * col.z - ab * rcp) * gb;
-                        const float dalpha = dadc + gac * rcp;
-                        v[5] = G * dalpha;
-                        const float h = -alpha * dalpha;
-                        v[2] = 0.5f * h * (dx * dx);
-                        v[3] = 0.5f * h * (dx * dy);
-                        v[4] = 0.5f * h * (dy * dy);
-                        v[0] = h * (cr.x * dx + cr.y * dy);
-                        v[1] = h * (cr.y * dx + cr.z * dy);
-                        v[9] = fabsf(v[0]);
-                        v[10] = fabsf(v[1]);
-                        T = T * oma;
-                    }
+                float dx, dy, G;
+                const float alpha = eval_alpha(s_xy[jj], s_co[jj], pxf, pyf, dx, dy, G);
+                const bool contrib = start + jj < last && alpha >= min_alpha;
+                if (__ballot(contrib) == 0) continue;
+                const float ae = contrib ? alpha : 0.0f;
+                const float Ge = contrib ? G : 0.0f;
+                const float4 col = s_col[jj];
+                const float w = T * ae;
+                const float oma = 1.0f - ae;
+                const float rcp = __builtin_amdgcn_rcpf(fmaxf(oma, one_minus_alpha_eps));
+                const float cg = __builtin_fmaf(col.z, gb, __builtin_fmaf(col.y, gg, col.x * gr));
+                A = __builtin_fmaf(-w, cg, A);
+                const float dalpha = __builtin_fmaf(T, cg, -rcp * (A - gbg));
+                const float h = -ae * dalpha;
+                const float hdx = h * dx, hdy = h * dy;
+                float v[8] = {hdx, hdy, hdx * dx, hdx * dy, hdy * dy, Ge * dalpha, w * gr, w * gg};
+                float e1 = 0.0f, e2 = 0.0f;
+                if (ABS) {
+                    const float4 cr = s_craw[jj];
+                    e1 = fabsf(__builtin_fmaf(cr.x, hdx, cr.y * hdy));
+                    e2 = fabsf(__builtin_fmaf(cr.y, hdx, cr.z * hdy));
                 }
-                if (__ballot(contrib) != 0) {
-                    const float s8 = transpose_reduce8(v, lane);
-                    const float s4 = transpose_reduce4(v[8], ABS ? v[9] : 0.0f, ABS ? v[10] : 0.0f, 0.0f);
-                    if ((lane & 7u) == 7u) s_grad[wave][reduced8_index(lane)][jj] = s8;
-                    if ((lane & 15u) == 15u) {
-                        const uint32_t row = lane >> 4;
-                        const uint32_t k = 8u + ((row & 1u) << 1) + (row >> 1);  // rows 0..3: values 8, 10, 9, 11
-                        if (k < n_values) s_grad[wave][k][jj] = s4;
-                    }
+                T = T * oma;
+                const float s8 = transpose_reduce8(v, lane);
+                const float s4 = transpose_reduce4(w * gb, e1, e2, 0.0f);
+                if ((lane & 7u) == 7u) s_grad[wave][reduced8_index(lane)][jj] = s8;
+                if ((lane & 15u) == 15u) {
+                    const uint32_t row = lane >> 4;
+                    const uint32_t k = 8u + ((row & 1u) << 1) + (row >> 1);  // rows 0..3: values 8, 10, 9, 11
+                    if (k < n_values) s_grad[wave][k][jj] = s4;
                 }
             }
         }
         __syncthreads();
         if (tid < batch_n) {
-            float g[11];
+            float r[11];
 #pragma unroll
-            for (uint32_t c = 0; c < n_values; c++) g[c] = (s_grad[0][c][tid] + s_grad[1][c][tid]) + s_grad[2][c][tid];
-            if (!ABS) g[9] = g[10] = 0.0f;
+            for (uint32_t c = 0; c < n_values; c++) r[c] = (s_grad[0][c][tid] + s_grad[1][c][tid]) + s_grad[2][c][tid];
+            if (!ABS) r[9] = r[10] = 0.0f;
+            const float gmx = __builtin_fmaf(craw.x, r[0], craw.y * r[1]);
+            const float gmy = __builtin_fmaf(craw.y, r[0], craw.z * r[1]);
             float4* out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(e_own);
-            out[0] = make_float4(g[0], g[1], g[2], g[3]);
-            out[1] = make_float4(g[4], g[5], g[6], g[7]);
-            out[2] = make_float4(g[8], g[9], g[10], 0.0f);
+            out[0] = make_float4(gmx, gmy, 0.5f * r[2], 0.5f * r[3]);
+            out[1] = make_float4(0.5f * r[4], r[5], r[6], r[7]);
+            out[2] = make_float4(r[8], r[9], r[10], 0.0f);
         }
         covered = min(n_total, start + tile_pixels);
     }

@@ -100,7 +100,8 @@ __device__ inline float ef_logf(float x) {
 // alpha = opacity * 2^x is far under the 1/255 threshold.
 __device__ inline float ef_exp2f(float x) {
 #pragma clang fp contract(off)
-    if (!(x >= -126.0f)) return 0.0f;
+    const bool in_range = x >= -126.0f;  // below: 0 (evaluated branch-free; the polynomial result is discarded)
+    if (!in_range) x = 0.0f;
     const float k = __builtin_rintf(x);
     const float r = x - k;
     float p = __builtin_fmaf(1.52527338e-05f, r, 1.54035304e-04f);
@@ -110,7 +111,7 @@ __device__ inline float ef_exp2f(float x) {
     p = __builtin_fmaf(p, r, 2.40226507e-01f);
     p = __builtin_fmaf(p, r, 6.93147181e-01f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return p * ef_pow2i(static_cast<int>(k));
+    return in_range ? p * ef_pow2i(static_cast<int>(k)) : 0.0f;
 }
 
 __device__ __forceinline__ float ef_sigmoid(float x) {
