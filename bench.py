@@ -47,6 +47,7 @@ STAGE_KERNELS = {
     'blend_forward': 'blend_forward_kernel',
     'blend_backward': 'blend_backward_kernel',
     'preprocess_backward': 'preprocess_backward_<model>',
+    'mlp_backward': 'preprocess_backward_<model>_mlp',
     'mlp_reduce': 'reduce_partials_kernel',
     'adam': 'adam_kernel',
 }
@@ -88,8 +89,10 @@ def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_
     """(bytes, flops) of one launch of `stage`. Per-unit figures: preprocess N*(60+R) + V*52 split into the
     preprocess kernel (N*(60+R) + V*44) and the compaction (V*8 key/index pairs); depth sort V*16, offsets
     scan V*8; instances V*40 + I*6, tile sort I*12, ranges T*8; blend forward I*48 + P*20; blend backward
-    P*32 + I*76; preprocess backward V*(110+R) + N*(56+R); Adam 28 B per element. MLP: forward V*F,
-    backward (input and weight gradients) 2*V*F, F = unpadded forward FLOPs per primitive."""
+    P*32 + I*76; preprocess backward V*(110+R) + N*(56+R), for the neural model split into the geometry
+    kernel (V*110 + N*56 + (N-V)*R: culled primitives' zero latent gradients) and the MLP kernel (V*2R:
+    latents in, latent gradients out); Adam 28 B per element. MLP FLOPs: forward V*F, backward (input and
+    weight gradients, forward recomputed) 2*V*F, F = unpadded forward FLOPs per primitive."""
     table = {
         'preprocess_forward': (N * (60 + R) + V * 44, V * mlp_fwd_flops),
         'compact': (V * 8, 0),
@@ -100,7 +103,9 @@ def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_
         'tile_ranges': (T * 8, 0),
         'blend_forward': (I * 48 + P * 20, 0),
         'blend_backward': (P * 32 + I * 76, 0),
-        'preprocess_backward': (V * (110 + R) + N * (56 + R), 2 * V * mlp_fwd_flops),
+        'preprocess_backward': ((V * 110 + N * 56 + (N - V) * R, 0) if mlp_fwd_flops
+                                else (V * (110 + R) + N * (56 + R), 0)),
+        'mlp_backward': (V * 2 * R, 2 * V * mlp_fwd_flops),
         'adam': (28 * adam_elements, 0),
     }
     return table.get(stage, (0, 0))

@@ -141,6 +141,18 @@ struct efgs_rasterizer {
     bool mlp_base_input = false;
     uint32_t* host_counters = nullptr;  // pinned, 4 entries
     efgs::StageTimer timer;
+    // specialised preprocess kernels of the current configuration, per variant and direction (forward,
+    // backward), for the device they were loaded on; cleared whenever the configuration changes
+    struct KernelSlot {
+        int device = -1;
+        efgs::RtcKernel kernel;
+        hipFunction_t mlp = nullptr;  // neural backward: the MLP kernel of the same module
+    };
+    KernelSlot kernels[6][2];
+    void clear_kernels() {
+        for (auto& v : kernels)
+            for (auto& k : v) k = KernelSlot{};
+    }
 };
 
 namespace {
@@ -308,11 +320,28 @@ void kernel_source(const efgs_rasterizer* r, int model, const char* kind, std::s
     files.push_back(std::string("preprocess_") + kind + ".hip");
 }
 
-bool get_preprocess_kernel(const efgs_rasterizer* r, int model, const char* kind, RtcKernel& k) {
-    std::string name, preamble;
-    std::vector<std::string> files;
-    kernel_source(r, model, kind, name, preamble, files);
-    return rtc_get_kernel(name, preamble, files, k);
+// the specialised preprocess kernel (forward or backward) of `model`, compiled or loaded once per device and
+// configuration; for the neural backward `mlp` receives the MLP kernel of the same module
+bool get_preprocess_kernel(efgs_rasterizer* r, int model, const char* kind, RtcKernel& k, hipFunction_t* mlp = nullptr) {
+    int device = 0;
+    EFGS_HIP_CHECK(hipGetDevice(&device));
+    const bool backward = kind[0] == 'b';
+    efgs_rasterizer::KernelSlot& slot = r->kernels[model][backward ? 1 : 0];
+    if (slot.device != device || !slot.kernel.function) {
+        std::string name, preamble;
+        std::vector<std::string> files;
+        kernel_source(r, model, kind, name, preamble, files);
+        RtcKernel loaded;
+        if (!rtc_get_kernel(name, preamble, files, loaded)) return false;
+        hipFunction_t extra = nullptr;
+        if (backward && model == 5) EFGS_HIP_CHECK(hipModuleGetFunction(&extra, loaded.module, (name + "_mlp").c_str()));
+        slot.kernel = loaded;
+        slot.mlp = extra;
+        slot.device = device;
+    }
+    k = slot.kernel;
+    if (mlp) *mlp = slot.mlp;
+    return true;
 }
 
 struct MlpShape {
@@ -397,10 +426,14 @@ CameraArgs camera_args(const efgs_rasterizer* r, const efgs_settings* s, int var
     return c;
 }
 
-bool launch_rtc(const RtcKernel& k, uint32_t blocks, uint32_t threads, uint32_t shared_bytes, void* args, hipStream_t s) {
+bool launch_function(hipFunction_t f, uint32_t blocks, uint32_t threads, uint32_t shared_bytes, void* args, hipStream_t s) {
     void* params[] = {args};
-    EFGS_HIP_CHECK(hipModuleLaunchKernel(k.function, blocks, 1, 1, threads, 1, 1, shared_bytes, s, params, nullptr));
+    EFGS_HIP_CHECK(hipModuleLaunchKernel(f, blocks, 1, 1, threads, 1, 1, shared_bytes, s, params, nullptr));
     return true;
+}
+
+bool launch_rtc(const RtcKernel& k, uint32_t blocks, uint32_t threads, uint32_t shared_bytes, void* args, hipStream_t s) {
+    return launch_function(k.function, blocks, threads, shared_bytes, args, s);
 }
 
 }  // namespace
@@ -435,6 +468,7 @@ int efgs_set_appearance(efgs_rasterizer* r, int model, int max_degree, int base_
     if (residual_act < 0 || residual_act > 2) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid residual activation id");
     if (color_act < 0 || color_act > 5) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid color activation id");
     if (max_degree < 0 || (model == 1 && max_degree > 3)) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid max degree (sh supports 0..3)");
+    r->clear_kernels();
     r->appearance_set = true;
     r->model = model;
     r->max_degree = model == 5 ? 0 : max_degree;
@@ -476,6 +510,7 @@ int efgs_set_residual_mlp(efgs_rasterizer* r, int n_input_dims, int n_output_dim
                          static_cast<uint32_t>(n_hidden_layers)};
     if (mlp_smem_backward(probe) > max_dynamic_lds)
         return fail(EFGS_ERR_INVALID_ARGUMENT, "the residual mlp exceeds the 64 KiB LDS budget of the fused kernels");
+    r->clear_kernels();
     r->mlp_set = true;
     r->mlp_n_in = n_input_dims;
     r->mlp_n_in_padded = (n_input_dims + 15) / 16 * 16;
@@ -682,7 +717,8 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     t.end(s);
 
     RtcKernel k;
-    if (!get_preprocess_kernel(r, variant, "backward", k)) return EFGS_ERR_RTC;
+    hipFunction_t mlp_kernel = nullptr;
+    if (!get_preprocess_kernel(r, variant, "backward", k, &mlp_kernel)) return EFGS_ERR_RTC;
     PreprocessBackwardArgs a;
     std::memset(&a, 0, sizeof(a));
     a.means = prims->means;
@@ -715,13 +751,23 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
         return EFGS_OK;
     }
     if (!grads->mlp_weights) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp weight gradient output is required");
-    const uint32_t blocks = chunks < neural_backward_blocks ? chunks : neural_backward_blocks;
     const uint32_t params = mlp_params(mlp_shape(r));
+    float* color_grads = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(n) * 4 * sizeof(float)));
+    if (!color_grads) return fail(EFGS_ERR_ALLOC, "allocation of the colour gradient buffer failed");
+    a.color_grads = color_grads;
+    t.begin(EFGS_STAGE_PREPROCESS_BACKWARD, s);
+    if (!launch_rtc(k, chunks, preprocess_block, 0u, &a, s)) return EFGS_ERR_HIP;
+    t.end(s);
+    if (a.cam.degree == 0) {  // the residual is off: no MLP gradient
+        if (!launch_fill_u32(reinterpret_cast<uint32_t*>(grads->mlp_weights), 0u, params, s)) return EFGS_ERR_HIP;
+        return EFGS_OK;
+    }
+    const uint32_t blocks = chunks < neural_backward_blocks ? chunks : neural_backward_blocks;
     float* partials = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(blocks) * params * sizeof(float)));
     if (!partials) return fail(EFGS_ERR_ALLOC, "allocation of the mlp gradient partials failed");
     a.g_mlp_partials = partials;
-    t.begin(EFGS_STAGE_PREPROCESS_BACKWARD, s);
-    if (!launch_rtc(k, blocks, preprocess_block, mlp_smem_backward(mlp_shape(r)), &a, s)) return EFGS_ERR_HIP;
+    t.begin(EFGS_STAGE_MLP_BACKWARD, s);
+    if (!launch_function(mlp_kernel, blocks, preprocess_block, mlp_smem_backward(mlp_shape(r)), &a, s)) return EFGS_ERR_HIP;
     t.end(s);
     t.begin(EFGS_STAGE_MLP_REDUCE, s);
     if (!launch_reduce_partials(partials, blocks, params, grads->mlp_weights, s)) return EFGS_ERR_HIP;

@@ -58,6 +58,7 @@ struct PreprocessBackwardArgs {
     float* g_base;
     float* g_residual;
     float* g_mlp_partials;           // neural: (blocks x n_params) fp32 per-block weight gradient partials
+    float* color_grads;              // neural: (N x 4) dL/d(pre-activation colour), geometry kernel -> MLP kernel
     float* densification_info;       // (rows x N) or null
     uint32_t densification_rows;
     uint32_t n;

@@ -7,9 +7,8 @@
 // activations and the appearance model, and the 2D mean and conic through the EWA projection to the 3D mean,
 // log-scales and quaternion. Culled primitives get zero gradients.
 //
-// The neural variant runs a persistent grid: every wave recomputes the MLP forward for its 64 primitives,
-// backpropagates with fp16 MFMA, keeps its weight gradients in fp32 registers across chunks, and the block
-// sums its four waves in a fixed order into one partial per block (summed over blocks by a separate kernel).
+// The neural variant splits this into two kernels: the same per-primitive geometry part (no MLP state, so it
+// runs at high occupancy) and an MLP kernel on a persistent grid.
 //
 // Reference: B/rasterization/rtc/preprocess_backward.cu:19-404 (the per-primitive part of
 // B/rasterization/include/kernels_backward.cuh:215-230 is folded in here).
@@ -224,9 +223,37 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     geometry_backward(a, p, rec, ig, dmean_color);
 }
 
-#else  // neural
+#else  // neural: a geometry kernel (one thread per primitive) and an MLP kernel
 
+#define EFGS_CAT2(a, b) a##b
+#define EFGS_CAT(a, b) EFGS_CAT2(a, b)
+
+// Everything but the MLP: instance-gradient reduction, colour and base gradients, the projection chain. The
+// gradient with respect to the pre-activation colour is left in color_grads for the MLP kernel, which adds
+// the MLP's view-direction and base-input terms to g_means and g_base and writes the latent gradients.
 extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
+    using namespace efgs;
+    const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
+    if (p >= a.n) return;
+    const uint32_t touched = a.n_touched[p];
+    if (touched == 0) {
+        zero_primitive(a, p);
+        return;
+    }
+    const InstanceGrads ig = reduce_instance_grads(a, p, touched);
+    const PrimRecord rec = a.records[p];
+    const float3 dpre = pre_activation_grad(rec, ig);
+    write_base_grad(a, p, dpre, make_float3(0.0f, 0.0f, 0.0f));
+    if (a.cam.degree == 0)
+        for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
+    geometry_backward(a, p, rec, ig, make_float3(0.0f, 0.0f, 0.0f));
+    reinterpret_cast<float4*>(a.color_grads)[p] = make_float4(dpre.x, dpre.y, dpre.z, 0.0f);
+}
+
+// The MLP backward (launched only when the residual is on). Persistent grid: every wave recomputes the MLP
+// forward for its 64 primitives, backpropagates with fp16 MFMA, keeps its weight gradients in fp32
+// registers across chunks; the block sums its four waves in a fixed order into one partial per block.
+extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _mlp)(efgs::PreprocessBackwardArgs a) {
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
@@ -251,62 +278,42 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         const uint32_t p_raw = chunk * preprocess_block + threadIdx.x;
         const bool valid = p_raw < a.n;
         const uint32_t p = valid ? p_raw : a.n - 1;
-        const uint32_t touched = valid ? a.n_touched[p] : 0u;
-        const bool contributes = touched > 0;
-
-        InstanceGrads ig = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        PrimRecord rec;
-        rec.r0 = rec.r1 = rec.r2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (contributes) {
-            ig = reduce_instance_grads(a, p, touched);
-            rec = a.records[p];
-        }
-        const float3 dpre = contributes ? pre_activation_grad(rec, ig) : make_float3(0.0f, 0.0f, 0.0f);
+        const bool contributes = valid && a.n_touched[p] > 0;
+        if (__ballot(contributes) == 0) continue;  // wave-uniform: nothing to backpropagate
+        const float4 dpre = contributes ? reinterpret_cast<const float4*>(a.color_grads)[p] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
         const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
         float norm_rcp;
         const float3 d = view_direction(mean, cam, norm_rcp);
         const float* feat = a.residual + static_cast<size_t>(p) * residual_params;
-        float3 dmean_color = make_float3(0.0f, 0.0f, 0.0f);
-        float3 dbase_input = make_float3(0.0f, 0.0f, 0.0f);
-        float dx[nn::INP];
+        float x[nn::INP];
+        nn::mlp_input(feat, a.base + 3 * p, d, degree, x);
+        if (!contributes) {
 #pragma unroll
-        for (uint32_t k = 0; k < nn::INP; k++) dx[k] = 0.0f;
-        if (degree > 0) {  // uniform: every lane of every wave runs the MLP
-            float x[nn::INP];
-            nn::mlp_input(feat, a.base + 3 * p, d, degree, x);
-            if (!contributes) {
-#pragma unroll
-                for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
-            }
-            nn::h4 act[nn::NL][nn::KT][4];
-            float y[3];
-            nn::mlp_forward(W, stage, x, act, y, lane);
-            float dy[3];
-            dy[0] = dpre.x * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[0]));
-            dy[1] = dpre.y * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[1]));
-            dy[2] = dpre.z * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[2]));
-            nn::mlp_backward(W, stage, act, dy, dx, dW, lane);
-            if (contributes) {
-                float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
-#pragma unroll
-                for (uint32_t i = 0; i < nn::FEATURES; i++) gp[i] = nn::feature_grad(feat[i], dx, i);
-                if (EFGS_BASE_INPUT) {
-                    dbase_input = make_float3(nn::feature_grad(a.base[3 * p], dx, nn::FEATURES),
-                                              nn::feature_grad(a.base[3 * p + 1], dx, nn::FEATURES + 1),
-                                              nn::feature_grad(a.base[3 * p + 2], dx, nn::FEATURES + 2));
-                }
-                dmean_color = direction_grad_to_mean(nn::direction_grad(d, degree, dx), d, norm_rcp);
-            }
+            for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
         }
-        if (valid) {
-            if (!contributes) {
-                zero_primitive(a, p);
-            } else {
-                write_base_grad(a, p, dpre, dbase_input);
-                if (degree == 0)
-                    for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
-                geometry_backward(a, p, rec, ig, dmean_color);
+        nn::h4 act[nn::NL][nn::KT][4];
+        float y[3];
+        nn::mlp_forward(W, stage, x, act, y, lane);
+        float dy[3];
+        dy[0] = dpre.x * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[0]));
+        dy[1] = dpre.y * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[1]));
+        dy[2] = dpre.z * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[2]));
+        float dx[nn::INP];
+        nn::mlp_backward(W, stage, act, dy, dx, dW, lane);
+        if (contributes) {
+            float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
+#pragma unroll
+            for (uint32_t i = 0; i < nn::FEATURES; i++) gp[i] = nn::feature_grad(feat[i], dx, i);
+            if (EFGS_BASE_INPUT) {
+#pragma unroll
+                for (uint32_t c = 0; c < 3; c++) a.g_base[3 * p + c] += nn::feature_grad(a.base[3 * p + c], dx, nn::FEATURES + c);
+            }
+            if (EFGS_DIRECTION_GRADIENT) {
+                const float3 dm = direction_grad_to_mean(nn::direction_grad(d, degree, dx), d, norm_rcp);
+                a.g_means[3 * p] += dm.x;
+                a.g_means[3 * p + 1] += dm.y;
+                a.g_means[3 * p + 2] += dm.z;
             }
         }
     }

@@ -73,7 +73,7 @@ EXPORTED = ('efgs_last_error', 'efgs_set_rtc_dirs', 'efgs_rasterizer_create', 'e
 
 # stage ids of efgs_get_stage_times, in order (include/efgs.h)
 STAGES = ('preprocess_forward', 'compact', 'counter_read', 'depth_sort', 'instance_offsets', 'create_instances', 'tile_sort',
-          'tile_ranges', 'blend_forward', 'blend_backward', 'preprocess_backward', 'mlp_reduce')
+          'tile_ranges', 'blend_forward', 'blend_backward', 'preprocess_backward', 'mlp_reduce', 'mlp_backward')
 
 lib.efgs_last_error.restype = ctypes.c_char_p
 lib.efgs_last_error.argtypes = []

@@ -199,7 +199,8 @@ enum {
     EFGS_STAGE_BLEND_BACKWARD = 9,
     EFGS_STAGE_PREPROCESS_BACKWARD = 10,
     EFGS_STAGE_MLP_REDUCE = 11,        /* reduction of the per-block MLP weight-gradient partials */
-    EFGS_N_STAGES = 12
+    EFGS_STAGE_MLP_BACKWARD = 12,      /* neural: MLP recompute + backward (EFGS_STAGE_PREPROCESS_BACKWARD is the rest) */
+    EFGS_N_STAGES = 13
 };
 int efgs_set_stage_timing(efgs_rasterizer* r, int enable);
 int efgs_get_stage_times(efgs_rasterizer* r, double* total_ms, int64_t* launches, int n_stages);

@@ -116,7 +116,7 @@ def test_stage_timing_without_launches():
     r = R.Rasterizer()
     r.set_stage_timing(True)
     times = r.stage_times()
-    assert set(times) == set(_lib.STAGES) and len(_lib.STAGES) == 12
+    assert set(times) == set(_lib.STAGES) and len(_lib.STAGES) == 13
     assert all(ms == 0.0 and n == 0 for ms, n in times.values())
     r.set_stage_timing(False)
 
@@ -132,7 +132,7 @@ def test_bench_algorithmic_bytes_match_the_c3_budget():
     F = bench.mlp_flops_per_primitive(11, 64, 2)
     assert F == 9_984
     stages = ['preprocess_forward', 'compact', 'depth_sort', 'instance_offsets', 'create_instances', 'tile_sort',
-              'tile_ranges', 'blend_forward', 'blend_backward', 'preprocess_backward']
+              'tile_ranges', 'blend_forward', 'blend_backward', 'preprocess_backward', 'mlp_backward']
     total = sum(bench.algorithmic(s, N, V, I, T, P, 32, F, 0)[0] for s in stages)
     assert abs(total / 1e6 - 670.0) < 1.0
     assert bench.algorithmic('adam', N, V, I, T, P, 32, F, 22_006_144)[0] == 28 * 22_006_144
