@@ -365,8 +365,17 @@ uint32_t mlp_smem_forward(const MlpShape& m) {
     return weight_bytes + 4 * 64 * row * 2;
 }
 
+// the backward's MLP kernel: W and W^T with rows padded by 4 halves, 4 per-wave staging areas of 64 rows of
+// (n_in_padded + 4) floats; the area is reused for the fp32 block reduction of the weight gradients
 uint32_t mlp_smem_backward(const MlpShape& m) {
-    const uint32_t f = mlp_smem_forward(m), red = mlp_params(m) * 4;
+    uint32_t halves = 0;
+    for (uint32_t l = 0; l <= m.n_hidden; l++) {
+        const uint32_t in = l == 0 ? m.n_in_padded : m.n_neurons;
+        const uint32_t out = l == m.n_hidden ? 16u : m.n_neurons;
+        halves += out * (in + 4) + in * (out + 4);
+    }
+    const uint32_t f = (halves * 2 + 15) / 16 * 16 + 4 * 64 * (m.n_in_padded + 4) * 4;
+    const uint32_t red = mlp_params(m) * 4;
     return f > red ? f : red;
 }
 
@@ -508,7 +517,7 @@ int efgs_set_residual_mlp(efgs_rasterizer* r, int n_input_dims, int n_output_dim
     if (n_input_dims > 128) return fail(EFGS_ERR_INVALID_ARGUMENT, "n_input_dims above 128 is not supported");
     const MlpShape probe{static_cast<uint32_t>((n_input_dims + 15) / 16 * 16), static_cast<uint32_t>(n_neurons),
                          static_cast<uint32_t>(n_hidden_layers)};
-    if (mlp_smem_backward(probe) > max_dynamic_lds)
+    if (mlp_smem_backward(probe) > max_dynamic_lds || mlp_smem_forward(probe) > max_dynamic_lds)
         return fail(EFGS_ERR_INVALID_ARGUMENT, "the residual mlp exceeds the 64 KiB LDS budget of the fused kernels");
     r->clear_kernels();
     r->mlp_set = true;

@@ -39,9 +39,9 @@ constexpr uint32_t STAGE_ROW = MAXK > 2 * INP ? MAXK : 2 * INP;
 constexpr uint32_t STAGE_HALVES = 64 * STAGE_ROW;  // per-wave LDS staging: 64 rows of MAXK halves or INP floats
 constexpr uint32_t WEIGHT_BYTES = (PARAMS * 2 + 15) / 16 * 16;
 
-__device__ constexpr uint32_t lin(uint32_t l) { return l == 0 ? INP : NN; }
-__device__ constexpr uint32_t lout(uint32_t l) { return l == NH ? OUTP : NN; }
-__device__ constexpr uint32_t loff(uint32_t l) { return l == 0 ? 0u : NN * INP + (l - 1) * NN * NN; }
+__host__ __device__ constexpr uint32_t lin(uint32_t l) { return l == 0 ? INP : NN; }
+__host__ __device__ constexpr uint32_t lout(uint32_t l) { return l == NH ? OUTP : NN; }
+__host__ __device__ constexpr uint32_t loff(uint32_t l) { return l == 0 ? 0u : NN * INP + (l - 1) * NN * NN; }
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -360,6 +360,249 @@ __device__ inline void mlp_backward(const uint16_t* W, _Float16* stage, const h4
             wave_sync();
 #pragma unroll
             for (uint32_t k = 0; k < INP; k++) dx[k] = fs[lane * INP + k];
+            wave_sync();
+        }
+    }
+}
+
+// ---- dual-orientation MLP of the backward kernel --------------------------------------------------------
+//
+// Tile sets of a (F x 64 primitives) matrix M held by a wave (lane = r + 16 q):
+//   feature-rows    T[fb][pb]: lane (r, q) holds M[16 fb + 4 q + i][16 pb + r], i = 0..3
+//   primitive-rows  U[pb][fb]: lane (r, q) holds M[16 fb + r][16 pb + 4 q + i]
+// v_mfma_f32_16x16x16f16 takes A as lane (r, q) -> A[r][4 q + i], B as B[4 q + i][r] and returns D as
+// D[4 q + i][r]. So a product's D is a feature-rows or primitive-rows tile as it stands; a feature-rows tile
+// is a B operand with K = features or an A operand holding the block's transpose (rows = primitives,
+// K = features); a primitive-rows tile is a B operand with K = primitives (N = features) or an A operand
+// holding the block itself with K = primitives. Computing every activation and every gradient in both
+// orientations (twice the MFMAs of the forward chain, which are cheap here) feeds every product of the
+// backward, including the weight gradients (contractions over primitives), with no transposes through LDS.
+//
+// LDS holds W_l row-major [out][in] and its transpose [in][out]; rows are padded by 4 halves so that the 16
+// lanes reading 8-byte fragments of 16 consecutive rows fall on distinct banks.
+constexpr uint32_t WPAD = 4;
+__host__ __device__ constexpr uint32_t wrow(uint32_t l) { return lin(l) + WPAD; }
+__host__ __device__ constexpr uint32_t wtrow(uint32_t l) { return lout(l) + WPAD; }
+__host__ __device__ constexpr uint32_t dual_layer_halves(uint32_t l) { return lout(l) * wrow(l) + lin(l) * wtrow(l); }
+__host__ __device__ constexpr uint32_t woff(uint32_t l) {
+    uint32_t o = 0;
+    for (uint32_t k = 0; k < l; k++) o += dual_layer_halves(k);
+    return o;
+}
+__host__ __device__ constexpr uint32_t wtoff(uint32_t l) { return woff(l) + lout(l) * wrow(l); }
+constexpr uint32_t DUAL_WEIGHT_BYTES = (woff(NL) * 2 + 15) / 16 * 16;
+constexpr uint32_t XS = INP + 4;        // staging row of the input / output-gradient rows (halves)
+constexpr uint32_t YS = OUTP + 4;
+constexpr uint32_t FS = INP + 4;        // staging row of the input-gradient rows (floats)
+constexpr uint32_t DUAL_STAGE_BYTES = 64 * FS * 4;  // per wave; also covers 64 rows of XS or YS halves
+
+// copies the flat tcnn-layout weights (fp16 bits) into the padded W / W^T layout (whole block)
+__device__ inline void load_dual_weights(const uint16_t* g, uint16_t* WL, uint32_t tid, uint32_t n_threads) {
+#pragma unroll
+    for (uint32_t l = 0; l < NL; l++) {
+        for (uint32_t idx = tid; idx < lout(l) * lin(l); idx += n_threads) {
+            const uint32_t row = idx / lin(l), col = idx % lin(l);
+            const uint16_t v = g[loff(l) + idx];
+            WL[woff(l) + row * wrow(l) + col] = v;
+            WL[wtoff(l) + col * wtrow(l) + row] = v;
+        }
+    }
+}
+
+__device__ __forceinline__ h4 relu_h4(f4 v) {
+    return h4{static_cast<_Float16>(fmaxf(v[0], 0.0f)), static_cast<_Float16>(fmaxf(v[1], 0.0f)), static_cast<_Float16>(fmaxf(v[2], 0.0f)),
+              static_cast<_Float16>(fmaxf(v[3], 0.0f))};
+}
+
+// v where the activation is positive (ReLU derivative), as fp16
+__device__ __forceinline__ h4 masked_h4(f4 v, h4 act) {
+    const _Float16 z = static_cast<_Float16>(0.0f);
+    return h4{act[0] > z ? static_cast<_Float16>(v[0]) : z, act[1] > z ? static_cast<_Float16>(v[1]) : z,
+              act[2] > z ? static_cast<_Float16>(v[2]) : z, act[3] > z ? static_cast<_Float16>(v[3]) : z};
+}
+
+// ReLU masks of the feature-rows activations, 4 bits per tile (tile fb * 4 + pb), kept once the forward no
+// longer needs the values themselves
+constexpr uint32_t MASK_WORDS = (KT * 4 * 4 + 31) / 32;
+__device__ __forceinline__ uint32_t positive_bits(h4 a) {
+    const _Float16 z = static_cast<_Float16>(0.0f);
+    return (a[0] > z ? 1u : 0u) | (a[1] > z ? 2u : 0u) | (a[2] > z ? 4u : 0u) | (a[3] > z ? 8u : 0u);
+}
+__device__ __forceinline__ h4 masked_h4_bits(f4 v, uint32_t bits) {
+    const _Float16 z = static_cast<_Float16>(0.0f);
+    return h4{(bits & 1u) ? static_cast<_Float16>(v[0]) : z, (bits & 2u) ? static_cast<_Float16>(v[1]) : z,
+              (bits & 4u) ? static_cast<_Float16>(v[2]) : z, (bits & 8u) ? static_cast<_Float16>(v[3]) : z};
+}
+
+// Forward recompute in both orientations. WL: padded W / W^T in LDS; stage: this wave's staging area; x: the
+// lane's input row. U[l]: input activations of layer l as primitive-rows tiles (fp16); Tm[l] (l >= 1): the
+// ReLU masks of the feature-rows tiles; y: the lane's three raw outputs, rounded to fp16 (as mlp_forward).
+__device__ inline void mlp_forward_dual(const _Float16* WL, _Float16* stage, const float* x, uint32_t (&Tm)[NL][MASK_WORDS], h4 (&U)[NL][4][KT],
+                                        float* y, uint32_t lane) {
+    h4 T[NL][KT][4];
+    const uint32_t r = lane & 15u, q = lane >> 4;
+#pragma unroll
+    for (uint32_t k = 0; k < INP; k += 4)
+        *reinterpret_cast<h4*>(&stage[lane * XS + k]) =
+            h4{static_cast<_Float16>(x[k]), static_cast<_Float16>(x[k + 1]), static_cast<_Float16>(x[k + 2]), static_cast<_Float16>(x[k + 3])};
+    wave_sync();
+#pragma unroll
+    for (uint32_t ib = 0; ib < INP / 16; ib++)
+#pragma unroll
+        for (uint32_t pb = 0; pb < 4; pb++) {
+            T[0][ib][pb] = *reinterpret_cast<const h4*>(&stage[(16 * pb + r) * XS + 16 * ib + 4 * q]);
+            U[0][pb][ib] = h4{stage[(16 * pb + 4 * q) * XS + 16 * ib + r], stage[(16 * pb + 4 * q + 1) * XS + 16 * ib + r],
+                              stage[(16 * pb + 4 * q + 2) * XS + 16 * ib + r], stage[(16 * pb + 4 * q + 3) * XS + 16 * ib + r]};
+        }
+    wave_sync();
+    f4 yt[4];
+#pragma unroll
+    for (uint32_t l = 0; l < NL; l++) {
+#pragma unroll
+        for (uint32_t ob = 0; ob < lout(l) / 16; ob++) {
+            h4 wa[KT];
+#pragma unroll
+            for (uint32_t ib = 0; ib < lin(l) / 16; ib++) wa[ib] = *reinterpret_cast<const h4*>(&WL[woff(l) + (16 * ob + r) * wrow(l) + 16 * ib + 4 * q]);
+#pragma unroll
+            for (uint32_t pb = 0; pb < 4; pb++) {
+                f4 t = f4_zero();
+#pragma unroll
+                for (uint32_t ib = 0; ib < lin(l) / 16; ib++) t = mfma(wa[ib], T[l][ib][pb], t);  // H(ob, pb) = sum W(ob, ib) M(ib, pb)
+                if (l < NH) {
+                    T[l + 1][ob][pb] = relu_h4(t);
+                    f4 u = f4_zero();
+#pragma unroll
+                    for (uint32_t ib = 0; ib < lin(l) / 16; ib++) u = mfma(T[l][ib][pb], wa[ib], u);  // H^T(pb, ob) = sum M^T(pb, ib) W^T(ib, ob)
+                    U[l + 1][pb][ob] = relu_h4(u);
+                } else if (ob == 0) {
+                    yt[pb] = t;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one output block in flight: bounds the live accumulators
+        }
+    }
+    // outputs 0..2 of primitive 16 pb + c sit in lane c of output tile pb
+#pragma unroll
+    for (uint32_t o = 0; o < 3; o++) {
+        float v = 0.0f;
+#pragma unroll
+        for (uint32_t pb = 0; pb < 4; pb++) {
+            const float t = __shfl(yt[pb][o], static_cast<int>(r));
+            if (q == pb) v = t;
+        }
+        y[o] = round_half(v);
+    }
+#pragma unroll
+    for (uint32_t l = 1; l < NL; l++) {
+#pragma unroll
+        for (uint32_t w = 0; w < MASK_WORDS; w++) Tm[l][w] = 0u;
+#pragma unroll
+        for (uint32_t fb = 0; fb < lin(l) / 16; fb++)
+#pragma unroll
+            for (uint32_t pb = 0; pb < 4; pb++) {
+                const uint32_t t = fb * 4 + pb;
+                Tm[l][t / 8] |= positive_bits(T[l][fb][pb]) << (4 * (t % 8));
+            }
+    }
+}
+
+// Backward through the MLP from the lanes' output gradients dy (zero for lanes that do not contribute), with
+// Tm / U from mlp_forward_dual. Writes the lane's input gradient row dx (INP floats) and adds the wave's weight
+// gradients to dW (lane layout of the D operand: dW[l][ob][ib][i] = dW_l[16 ob + 4 q + i][16 ib + r]).
+__device__ inline void mlp_backward_dual(const _Float16* WL, _Float16* stage, const uint32_t (&Tm)[NL][MASK_WORDS], const h4 (&U)[NL][4][KT],
+                                         const float* dy, float* dx, f4 (&dW)[NL][NT > 1 ? NT : 1][KT], uint32_t lane) {
+    const uint32_t r = lane & 15u, q = lane >> 4;
+    const float m = wave_max_f32(fmaxf(fmaxf(fabsf(dy[0]), fabsf(dy[1])), fabsf(dy[2])));
+#pragma unroll
+    for (uint32_t k = 0; k < INP; k++) dx[k] = 0.0f;
+    if (!(m > 0.0f) || !(m < 3.0e38f)) return;  // wave-uniform
+    const int e = max(ilogbf(m), -110);  // keeps the scale 2^(8 - e) finite for denormal maxima
+    const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
+
+    // output-layer gradient (16 padded outputs x 64 primitives) in both orientations, through LDS
+    const _Float16 z = static_cast<_Float16>(0.0f);
+    *reinterpret_cast<h4*>(&stage[lane * YS]) = h4{static_cast<_Float16>(dy[0] * s), static_cast<_Float16>(dy[1] * s),
+                                                    static_cast<_Float16>(dy[2] * s), z};
+#pragma unroll
+    for (uint32_t k = 4; k < OUTP; k += 4) *reinterpret_cast<h4*>(&stage[lane * YS + k]) = h4{z, z, z, z};
+    wave_sync();
+    h4 G[KT][4], GT[4][KT];
+#pragma unroll
+    for (uint32_t pb = 0; pb < 4; pb++) {
+        G[0][pb] = *reinterpret_cast<const h4*>(&stage[(16 * pb + r) * YS + 4 * q]);
+        GT[pb][0] = h4{stage[(16 * pb + 4 * q) * YS + r], stage[(16 * pb + 4 * q + 1) * YS + r], stage[(16 * pb + 4 * q + 2) * YS + r],
+                       stage[(16 * pb + 4 * q + 3) * YS + r]};
+    }
+    wave_sync();
+
+#pragma unroll
+    for (int li = static_cast<int>(NH); li >= 0; li--) {
+        const uint32_t l = static_cast<uint32_t>(li);
+        // weight gradient dW_l(ob, ib) += sum_pb dOut(ob, pb) M_l(ib, pb)^T
+#pragma unroll
+        for (uint32_t ob = 0; ob < lout(l) / 16; ob++)
+#pragma unroll
+            for (uint32_t ib = 0; ib < lin(l) / 16; ib++) {
+                f4 t = f4_zero();
+#pragma unroll
+                for (uint32_t pb = 0; pb < 4; pb++) t = mfma(GT[pb][ob], U[l][pb][ib], t);
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) dW[l][ob][ib][i] = __builtin_fmaf(t[i], inv_s, dW[l][ob][ib][i]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        if (l > 0) {
+            // input gradient in both orientations, through the ReLU of layer l's input
+            h4 Gn[KT][4], GTn[4][KT];
+#pragma unroll
+            for (uint32_t ib = 0; ib < lin(l) / 16; ib++) {
+                h4 wt[KT];
+#pragma unroll
+                for (uint32_t ob = 0; ob < lout(l) / 16; ob++)
+                    wt[ob] = *reinterpret_cast<const h4*>(&WL[wtoff(l) + (16 * ib + r) * wtrow(l) + 16 * ob + 4 * q]);
+#pragma unroll
+                for (uint32_t pb = 0; pb < 4; pb++) {
+                    f4 t = f4_zero(), u = f4_zero();
+#pragma unroll
+                    for (uint32_t ob = 0; ob < lout(l) / 16; ob++) {
+                        t = mfma(wt[ob], G[ob][pb], t);   // dIn(ib, pb) = sum W^T(ib, ob) dOut(ob, pb)
+                        u = mfma(G[ob][pb], wt[ob], u);   // dIn^T(pb, ib) = sum dOut^T(pb, ob) W(ob, ib)
+                    }
+                    const uint32_t ti = ib * 4 + pb;
+                    Gn[ib][pb] = masked_h4_bits(t, (Tm[l][ti / 8] >> (4 * (ti % 8))) & 15u);
+                    GTn[pb][ib] = masked_h4(u, U[l][pb][ib]);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // one input block in flight: bounds the live accumulators
+            }
+#pragma unroll
+            for (uint32_t ib = 0; ib < lin(l) / 16; ib++)
+#pragma unroll
+                for (uint32_t pb = 0; pb < 4; pb++) {
+                    G[ib][pb] = Gn[ib][pb];
+                    GT[pb][ib] = GTn[pb][ib];
+                }
+        } else {
+            // input gradient rows (feature-rows tiles, unscaled) to the lanes through LDS
+            float* fs = reinterpret_cast<float*>(stage);
+#pragma unroll
+            for (uint32_t ib = 0; ib < INP / 16; ib++) {
+                h4 wt[KT];
+#pragma unroll
+                for (uint32_t ob = 0; ob < lout(0) / 16; ob++)
+                    wt[ob] = *reinterpret_cast<const h4*>(&WL[wtoff(0) + (16 * ib + r) * wtrow(0) + 16 * ob + 4 * q]);
+#pragma unroll
+                for (uint32_t pb = 0; pb < 4; pb++) {
+                    f4 t = f4_zero();
+#pragma unroll
+                    for (uint32_t ob = 0; ob < lout(0) / 16; ob++) t = mfma(wt[ob], G[ob][pb], t);
+                    *reinterpret_cast<float4*>(&fs[(16 * pb + r) * FS + 16 * ib + 4 * q]) = make_float4(t[0] * inv_s, t[1] * inv_s, t[2] * inv_s, t[3] * inv_s);
+                }
+            }
+            wave_sync();
+#pragma unroll
+            for (uint32_t k = 0; k < INP; k += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(&fs[lane * FS + k]);
+                dx[k] = v.x; dx[k + 1] = v.y; dx[k + 2] = v.z; dx[k + 3] = v.w;
+            }
             wave_sync();
         }
     }

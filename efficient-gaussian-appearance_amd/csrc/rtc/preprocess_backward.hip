@@ -251,17 +251,17 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
 }
 
 // The MLP backward (launched only when the residual is on). Persistent grid: every wave recomputes the MLP
-// forward for its 64 primitives, backpropagates with fp16 MFMA, keeps its weight gradients in fp32
-// registers across chunks; the block sums its four waves in a fixed order into one partial per block.
+// forward for its 64 primitives in both tile orientations, backpropagates with fp16 MFMA without LDS
+// transposes, keeps its weight gradients in fp32 registers across chunks; the block sums its four waves in a
+// fixed order into one partial per block.
 extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _mlp)(efgs::PreprocessBackwardArgs a) {
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     extern __shared__ __align__(16) unsigned char smem[];
-    uint16_t* W = reinterpret_cast<uint16_t*>(smem);
-    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES) + wave * nn::STAGE_HALVES;
-    for (uint32_t i = threadIdx.x; i < nn::PARAMS / 8; i += preprocess_block)
-        reinterpret_cast<uint4*>(W)[i] = reinterpret_cast<const uint4*>(a.mlp_weights)[i];
+    const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES + wave * nn::DUAL_STAGE_BYTES);
+    nn::load_dual_weights(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x, preprocess_block);
     __syncthreads();
 
     nn::f4 dW[nn::NL][nn::NT > 1 ? nn::NT : 1][nn::KT];
@@ -292,15 +292,16 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _ml
 #pragma unroll
             for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
         }
-        nn::h4 act[nn::NL][nn::KT][4];
+        uint32_t Tm[nn::NL][nn::MASK_WORDS];
+        nn::h4 U[nn::NL][4][nn::KT];
         float y[3];
-        nn::mlp_forward(W, stage, x, act, y, lane);
+        nn::mlp_forward_dual(WL, stage, x, Tm, U, y, lane);
         float dy[3];
         dy[0] = dpre.x * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[0]));
         dy[1] = dpre.y * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[1]));
         dy[2] = dpre.z * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[2]));
         float dx[nn::INP];
-        nn::mlp_backward(W, stage, act, dy, dx, dW, lane);
+        nn::mlp_backward_dual(WL, stage, Tm, U, dy, dx, dW, lane);
         if (contributes) {
             float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
 #pragma unroll
