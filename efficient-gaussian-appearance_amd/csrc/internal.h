@@ -23,8 +23,8 @@ void set_error(const std::string& msg);
     } while (0)
 
 constexpr uint32_t sort_block = 256;
-constexpr uint32_t sort_rounds = 4;                     // keys per thread per sort tile
-constexpr uint32_t sort_tile = sort_block * sort_rounds;  // 1024 keys per block
+constexpr uint32_t sort_rounds = 8;                     // keys per thread per sort tile
+constexpr uint32_t sort_tile = sort_block * sort_rounds;  // 2048 keys per block
 constexpr uint32_t sort_bins = 256;                     // 8-bit digits
 constexpr uint32_t scan_block = 256;
 constexpr uint32_t scan_items = 8;

@@ -1,14 +1,22 @@
-// Stable LSD radix sort of (key, value) pairs for wave64, 8-bit digits, 1024 keys per 256-thread block.
-// Per pass: per-block digit histogram -> device exclusive scan in digit-major order -> stable scatter.
-// Within a block, keys are taken in index order (4 rounds of 256); a wave ranks its 64 keys per digit with
-// 64-bit ballots (lanes sharing a digit form a peer mask; rank = peers below the lane), waves are ordered
-// through a per-round digit prefix in LDS. Replaces cub::DeviceRadixSort
-// (B/rasterization/src/forward.cu:88-96 depth keys, :182-190 tile keys).
+// Stable LSD radix sort of (key, value) pairs for wave64, 8-bit digits, 2048 keys per 256-thread block.
+// Per pass (three launches):
+//   histogram : per-block digit counts, counts[digit][block];
+//   row scan  : one block per digit scans its row over the blocks (exclusive) and records the digit total;
+//   scatter   : each block ranks its keys (index order, 8 rounds of 256), places them digit-sorted in LDS,
+//               then writes every digit run to its global position contiguously, so consecutive lanes
+//               store consecutive addresses. Global position = (exclusive scan of the digit totals) + (row
+//               scan of the digit over the previous blocks) + (rank within the block).
+// A wave ranks its 64 keys per digit with 64-bit ballots (lanes sharing a digit form a peer mask; rank =
+// peers below the lane); waves and rounds are ordered through per-digit running counts in LDS, so equal keys
+// keep their input order. Replaces cub::DeviceRadixSort (B/rasterization/src/forward.cu:88-96 depth keys,
+// :182-190 tile keys).
 #include "internal.h"
 
 namespace efgs {
 
 namespace {
+
+constexpr uint32_t sort_waves = sort_block / 64;
 
 // lanes whose 8-bit digit equals this lane's (restricted to valid lanes)
 __device__ __forceinline__ uint64_t match_peers(uint32_t d, bool valid) {
@@ -22,8 +30,27 @@ __device__ __forceinline__ uint64_t match_peers(uint32_t d, bool valid) {
     return peers;
 }
 
+// exclusive scan of one value per thread over a 256-thread block (wave scans with DPP-free shuffles)
+__device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_waves) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) s_waves[wave] = inc;
+    __syncthreads();
+    uint32_t prefix = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < sort_waves; w++)
+        if (w < wave) prefix += s_waves[w];
+    __syncthreads();
+    return prefix + inc - v;
+}
+
 template <typename KeyT>
-__global__ __launch_bounds__(sort_block) void sort_histogram_kernel(const KeyT* keys, uint32_t* hist, uint32_t n, uint32_t shift, uint32_t n_blocks) {
+__global__ __launch_bounds__(sort_block) void sort_histogram_kernel(const KeyT* keys, uint32_t* counts, uint32_t n, uint32_t shift, uint32_t n_blocks) {
     __shared__ uint32_t h[sort_bins];
     const uint32_t lane = threadIdx.x & 63u;
     h[threadIdx.x] = 0;
@@ -39,21 +66,54 @@ __global__ __launch_bounds__(sort_block) void sort_histogram_kernel(const KeyT* 
             atomicAdd(&h[d], static_cast<uint32_t>(__popcll(peers)));
     }
     __syncthreads();
-    hist[threadIdx.x * n_blocks + blockIdx.x] = h[threadIdx.x];
+    counts[threadIdx.x * n_blocks + blockIdx.x] = h[threadIdx.x];
+}
+
+// block d: offsets[d][b] = sum of counts[d][b'] for b' < b, totals[d] = row sum
+__global__ __launch_bounds__(sort_block) void sort_row_scan_kernel(const uint32_t* counts, uint32_t* offsets, uint32_t* totals, uint32_t n_blocks) {
+    __shared__ uint32_t s_waves[sort_waves];
+    const uint32_t d = blockIdx.x;
+    const uint32_t* row = counts + static_cast<size_t>(d) * n_blocks;
+    uint32_t* out = offsets + static_cast<size_t>(d) * n_blocks;
+    const uint32_t per = (n_blocks + sort_block - 1) / sort_block;  // consecutive entries per thread
+    const uint32_t b0 = threadIdx.x * per;
+    uint32_t sum = 0;
+    for (uint32_t k = 0; k < per; k++)
+        if (b0 + k < n_blocks) sum += row[b0 + k];
+    uint32_t run = block_exclusive_scan_256(sum, s_waves);
+    for (uint32_t k = 0; k < per; k++)
+        if (b0 + k < n_blocks) {
+            out[b0 + k] = run;
+            run += row[b0 + k];
+        }
+    if (threadIdx.x == sort_block - 1) totals[d] = run;
 }
 
 template <typename KeyT>
 __global__ __launch_bounds__(sort_block) void sort_scatter_kernel(const KeyT* keys_in, const uint32_t* vals_in, KeyT* keys_out, uint32_t* vals_out,
-                                                                 const uint32_t* offsets, uint32_t n, uint32_t shift, uint32_t n_blocks) {
-    __shared__ uint32_t digit_base[sort_bins];
-    __shared__ uint32_t wave_hist[sort_block / 64][sort_bins];
+                                                                 const uint32_t* counts, const uint32_t* offsets, const uint32_t* totals, uint32_t n,
+                                                                 uint32_t shift, uint32_t n_blocks) {
+    __shared__ KeyT s_key[sort_tile];
+    __shared__ uint32_t s_val[sort_tile];
+    __shared__ uint32_t local_base[sort_bins];   // first slot of each digit in the block's sorted tile
+    __shared__ uint32_t global_base[sort_bins];  // global position of that slot
+    __shared__ uint32_t running[sort_bins];      // keys of each digit placed so far
+    __shared__ uint32_t wave_hist[sort_waves][sort_bins];
+    __shared__ uint32_t s_waves[sort_waves];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint64_t lanes_below = (1ull << lane) - 1ull;
-    digit_base[threadIdx.x] = offsets[threadIdx.x * n_blocks + blockIdx.x];
+    {
+        const uint32_t d = threadIdx.x;
+        const uint32_t lb = block_exclusive_scan_256(counts[d * n_blocks + blockIdx.x], s_waves);
+        const uint32_t digit_start = block_exclusive_scan_256(totals[d], s_waves);
+        local_base[d] = lb;
+        global_base[d] = digit_start + offsets[d * n_blocks + blockIdx.x];
+        running[d] = 0;
+    }
     const uint32_t start = blockIdx.x * sort_tile;
     for (uint32_t r = 0; r < sort_rounds; r++) {
 #pragma unroll
-        for (uint32_t w = 0; w < sort_block / 64; w++) wave_hist[w][threadIdx.x] = 0;
+        for (uint32_t w = 0; w < sort_waves; w++) wave_hist[w][threadIdx.x] = 0;
         __syncthreads();
         const uint32_t i = start + r * sort_block + threadIdx.x;
         const bool valid = i < n;
@@ -69,22 +129,32 @@ __global__ __launch_bounds__(sort_block) void sort_scatter_kernel(const KeyT* ke
         if (valid && rank == 0) wave_hist[wave][d] = static_cast<uint32_t>(__popcll(peers));
         __syncthreads();
         {
-            uint32_t run = digit_base[threadIdx.x];
+            uint32_t run = running[threadIdx.x];
 #pragma unroll
-            for (uint32_t w = 0; w < sort_block / 64; w++) {
+            for (uint32_t w = 0; w < sort_waves; w++) {
                 const uint32_t c = wave_hist[w][threadIdx.x];
                 wave_hist[w][threadIdx.x] = run;
                 run += c;
             }
-            digit_base[threadIdx.x] = run;
+            running[threadIdx.x] = run;
         }
         __syncthreads();
         if (valid) {
-            const uint32_t pos = wave_hist[wave][d] + rank;
-            keys_out[pos] = key;
-            vals_out[pos] = val;
+            const uint32_t slot = local_base[d] + wave_hist[wave][d] + rank;
+            s_key[slot] = key;
+            s_val[slot] = val;
         }
-        __syncthreads();
+        __syncthreads();  // wave_hist is cleared at the top of the next round
+    }
+    const uint32_t tile_n = min(sort_tile, n - start);
+    for (uint32_t k = threadIdx.x; k < tile_n; k += sort_block) {
+        const KeyT key = s_key[k];
+        const uint32_t d = (static_cast<uint32_t>(key) >> shift) & 255u;
+        const uint32_t pos = global_base[d] + (k - local_base[d]);
+        if (pos < n) {
+            keys_out[pos] = key;
+            vals_out[pos] = s_val[k];
+        }
     }
 }
 
@@ -92,8 +162,8 @@ __global__ __launch_bounds__(sort_block) void sort_scatter_kernel(const KeyT* ke
 
 size_t sort_scratch_bytes(uint32_t n) {
     const uint32_t blocks = div_up(n > 0 ? n : 1, sort_tile);
-    const size_t hist = sizeof(uint32_t) * static_cast<size_t>(sort_bins) * blocks;
-    return 2 * ((hist + 255) & ~static_cast<size_t>(255)) + scan_scratch_bytes(sort_bins * blocks);
+    const size_t table = (sizeof(uint32_t) * static_cast<size_t>(sort_bins) * blocks + 255) & ~static_cast<size_t>(255);
+    return 2 * table + sizeof(uint32_t) * sort_bins;
 }
 
 template <typename KeyT>
@@ -102,10 +172,10 @@ static bool sort_impl(KeyT* ka, uint32_t* va, KeyT* kb, uint32_t* vb, bool ident
     *result_in_b = false;
     if (n == 0) return true;
     const uint32_t blocks = div_up(n, sort_tile);
-    const size_t hist_bytes = (sizeof(uint32_t) * static_cast<size_t>(sort_bins) * blocks + 255) & ~static_cast<size_t>(255);
-    uint32_t* hist = static_cast<uint32_t*>(scratch);
-    uint32_t* offsets = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + hist_bytes);
-    void* scan_scratch = static_cast<char*>(scratch) + 2 * hist_bytes;
+    const size_t table = (sizeof(uint32_t) * static_cast<size_t>(sort_bins) * blocks + 255) & ~static_cast<size_t>(255);
+    uint32_t* counts = static_cast<uint32_t*>(scratch);
+    uint32_t* offsets = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + table);
+    uint32_t* totals = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + 2 * table);
     // at least one pass, so identity values are always materialised
     const int passes = end_bit > 0 ? (end_bit + 7) / 8 : 1;
     KeyT* kin = ka;
@@ -115,9 +185,10 @@ static bool sort_impl(KeyT* ka, uint32_t* va, KeyT* kb, uint32_t* vb, bool ident
     bool in_b = false;
     for (int pass = 0; pass < passes; pass++) {
         const uint32_t shift = 8u * static_cast<uint32_t>(pass);
-        sort_histogram_kernel<KeyT><<<blocks, sort_block, 0, s>>>(kin, hist, n, shift, blocks);
-        if (!scan_exclusive(hist, nullptr, offsets, nullptr, sort_bins * blocks, scan_scratch, s)) return false;
-        sort_scatter_kernel<KeyT><<<blocks, sort_block, 0, s>>>(kin, (pass == 0 && identity_vals) ? nullptr : vin, kout, vout, offsets, n, shift, blocks);
+        sort_histogram_kernel<KeyT><<<blocks, sort_block, 0, s>>>(kin, counts, n, shift, blocks);
+        sort_row_scan_kernel<<<sort_bins, sort_block, 0, s>>>(counts, offsets, totals, blocks);
+        sort_scatter_kernel<KeyT><<<blocks, sort_block, 0, s>>>(kin, (pass == 0 && identity_vals) ? nullptr : vin, kout, vout, counts, offsets,
+                                                                totals, n, shift, blocks);
         EFGS_HIP_CHECK(hipGetLastError());
         std::swap(kin, kout);
         std::swap(vin, vout);
