@@ -452,6 +452,19 @@ extern "C" {
 
 const char* efgs_last_error(void) { return error_message(); }
 
+void* efgs_workspace_alloc(void* workspace, size_t bytes) {
+    efgs_workspace* w = static_cast<efgs_workspace*>(workspace);
+    if (!w) return nullptr;
+    const size_t aligned = (bytes + buffer_alignment - 1) & ~(buffer_alignment - 1);
+    w->requested += aligned;
+    if (w->base && w->used + aligned <= w->capacity) {
+        void* p = static_cast<char*>(w->base) + w->used;
+        w->used += aligned;
+        return p;
+    }
+    return w->fallback ? w->fallback(w->fallback_ctx, bytes) : nullptr;
+}
+
 int efgs_set_rtc_dirs(const char* cache_dir, const char* kernel_dir) {
     if (!kernel_dir) return fail(EFGS_ERR_INVALID_ARGUMENT, "kernel_dir is required");
     rtc_set_dirs(cache_dir ? cache_dir : "", kernel_dir);

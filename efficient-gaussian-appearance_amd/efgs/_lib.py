@@ -58,6 +58,11 @@ class AdamGroup(ctypes.Structure):
                 ('beta1', ctypes.c_double), ('beta2', ctypes.c_double), ('eps', ctypes.c_double)]
 
 
+class Workspace(ctypes.Structure):
+    _fields_ = [('base', ctypes.c_void_p), ('capacity', ctypes.c_size_t), ('used', ctypes.c_size_t), ('requested', ctypes.c_size_t),
+                ('fallback', ctypes.c_void_p), ('fallback_ctx', ctypes.c_void_p)]
+
+
 class FrameViews(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in (
         'n_touched', 'depth_keys', 'records', 'depth_sorted_keys', 'depth_sorted_prims', 'instance_offsets',
@@ -69,7 +74,7 @@ lib = ctypes.CDLL(LIB_PATH)
 
 EXPORTED = ('efgs_last_error', 'efgs_set_rtc_dirs', 'efgs_rasterizer_create', 'efgs_rasterizer_destroy', 'efgs_set_appearance',
             'efgs_set_residual_mlp', 'efgs_mlp_param_count', 'efgs_forward', 'efgs_backward', 'efgs_adam_step',
-            'efgs_get_frame_views', 'efgs_precompile', 'efgs_set_stage_timing', 'efgs_get_stage_times')
+            'efgs_get_frame_views', 'efgs_precompile', 'efgs_set_stage_timing', 'efgs_get_stage_times', 'efgs_workspace_alloc')
 
 # stage ids of efgs_get_stage_times, in order (include/efgs.h)
 STAGES = ('preprocess_forward', 'compact', 'counter_read', 'depth_sort', 'instance_offsets', 'create_instances', 'tile_sort',
@@ -93,6 +98,9 @@ lib.efgs_adam_step.argtypes = [ctypes.POINTER(AdamGroup), ctypes.c_int, ctypes.c
 lib.efgs_get_frame_views.argtypes = [ctypes.POINTER(Frame), ctypes.POINTER(FrameViews)]
 lib.efgs_precompile.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
 lib.efgs_set_stage_timing.argtypes = [ctypes.c_void_p, ctypes.c_int]
+lib.efgs_workspace_alloc.restype = ctypes.c_void_p
+lib.efgs_workspace_alloc.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+WORKSPACE_ALLOC = ctypes.cast(lib.efgs_workspace_alloc, ALLOC_FN)  # C function: no Python per allocation
 lib.efgs_get_stage_times.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_int]
 
 
@@ -105,6 +113,34 @@ def check(rc: int) -> None:
 
 os.makedirs(CACHE_DIR, exist_ok=True)
 check(lib.efgs_set_rtc_dirs(CACHE_DIR.encode(), KERNEL_DIR.encode()))
+
+
+class WorkspaceAllocator:
+    """One torch uint8 device tensor per call, carved by the library's C bump allocator; requests beyond it fall
+    back to per-buffer tensors. The region size follows the largest total requested so far (per key), so in
+    steady state a call makes a single allocation and no Python callbacks."""
+
+    _sizes: dict = {}
+
+    def __init__(self, device: torch.device, key: str):
+        self.key = (key, device)
+        capacity = WorkspaceAllocator._sizes.get(self.key, 0)
+        self.region = torch.empty(max(capacity, 256), dtype=torch.uint8, device=device)
+        self.fallback = TensorAllocator(device)
+        self.ws = Workspace(self.region.data_ptr(), capacity, 0, 0, ctypes.cast(self.fallback.fn, ctypes.c_void_p), None)
+        self.fn = WORKSPACE_ALLOC
+        self.ctx = ctypes.cast(ctypes.pointer(self.ws), ctypes.c_void_p)
+
+    @property
+    def tensors(self) -> list:
+        """The tensors backing every buffer handed out (keep them alive as long as the buffers are used)."""
+        return [self.region] + self.fallback.tensors
+
+    def done(self) -> None:
+        """Records the call's total so the next region covers it (with 1/16 headroom)."""
+        need = int(self.ws.requested)
+        if need > WorkspaceAllocator._sizes.get(self.key, 0):
+            WorkspaceAllocator._sizes[self.key] = (need + need // 16 + 255) // 256 * 256
 
 
 class TensorAllocator:

@@ -180,10 +180,11 @@ def _forward(means, scales, rotations, opacities, precomputed_colors, base_color
         cs, keep = _native_settings(settings, device)
         prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
         image = torch.empty((3, int(settings.height), int(settings.width)), dtype=torch.float32, device=device)
-        alloc = _lib.TensorAllocator(device)
+        alloc = _lib.WorkspaceAllocator(device, 'forward')
         frame = _lib.Frame()
-        check(lib.efgs_forward(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), image.data_ptr(), alloc.fn, None,
+        check(lib.efgs_forward(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), image.data_ptr(), alloc.fn, alloc.ctx,
                                ctypes.byref(frame), _stream(device)))
+        alloc.done()
     last_frame_counts.update(n_primitives=int(frame.n_primitives), n_visible=int(frame.n_visible),
                              n_instances=int(frame.n_instances), n_tiles=int(frame.grid_width) * int(frame.grid_height))
     return image, frame, alloc.tensors, keep
@@ -215,14 +216,13 @@ class _Rasterize(torch.autograd.Function):
         with torch.cuda.device(device):
             cs, keep = _native_settings(ctx.rasterizer_settings, device)
             prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
-            g_means = torch.empty_like(means)
-            g_scales = torch.empty_like(scales)
-            g_rotations = torch.empty_like(rotations)
-            g_opacities = torch.empty_like(opacities)
-            g_pre = torch.empty_like(precomputed_colors)
-            g_base = torch.empty_like(base_colors)
-            g_res = torch.empty_like(residual_params)
-            g_mlp = torch.zeros(ctx.mlp_numel, dtype=torch.float32, device=device)
+            # every gradient output is a view of one allocation (each is fully written by the backward)
+            shapes = [means.shape, scales.shape, rotations.shape, opacities.shape, precomputed_colors.shape, base_colors.shape,
+                      residual_params.shape, (ctx.mlp_numel,)]
+            sizes = [int(torch.Size(sh).numel()) for sh in shapes]
+            flat = torch.empty(sum(sizes), dtype=torch.float32, device=device)
+            g_means, g_scales, g_rotations, g_opacities, g_pre, g_base, g_res, g_mlp = (
+                t.view(sh) for t, sh in zip(flat.split(sizes), shapes))
             dinfo = ctx.densification_info
             rows = int(dinfo.shape[0]) if dinfo is not None and dinfo.numel() > 0 else 0
             if rows:
@@ -237,9 +237,10 @@ class _Rasterize(torch.autograd.Function):
             grads.mlp_weights = _ptr(g_mlp)
             grads.densification_info = dinfo.data_ptr() if rows else None
             grads.densification_rows = rows
-            alloc = _lib.TensorAllocator(device)
+            alloc = _lib.WorkspaceAllocator(device, 'backward')
             check(lib.efgs_backward(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), ctypes.byref(ctx.frame), image.data_ptr(),
-                                    grad_image.data_ptr(), ctypes.byref(grads), alloc.fn, None, _stream(device)))
+                                    grad_image.data_ptr(), ctypes.byref(grads), alloc.fn, alloc.ctx, _stream(device)))
+            alloc.done()
         return (g_means, g_scales, g_rotations, g_opacities,
                 g_pre if g_pre.numel() > 0 else None,
                 g_base if g_base.numel() > 0 else None,

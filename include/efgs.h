@@ -45,6 +45,21 @@ typedef struct efgs_rasterizer efgs_rasterizer;
  * backward) and for the backward's temporaries. */
 typedef void* (*efgs_alloc_fn)(void* ctx, size_t bytes);
 
+/* Bump allocator over one caller-provided device region (no counterpart in the reference: it spares callers
+ * a callback per buffer). Pass efgs_workspace_alloc as the efgs_alloc_fn and a workspace as its context: each
+ * request takes the next 256-byte-aligned slice of [base, base + capacity); a request that does not fit goes
+ * to `fallback` (if set) and the slice is left unused. `requested` accumulates the aligned sizes of all
+ * requests, so a caller can size the next call's region. */
+typedef struct efgs_workspace {
+    void* base;               /* device region, 256-byte aligned */
+    size_t capacity;
+    size_t used;              /* bytes handed out from the region */
+    size_t requested;         /* bytes asked for in total (region + fallback) */
+    efgs_alloc_fn fallback;   /* may be NULL: a request that does not fit then fails */
+    void* fallback_ctx;
+} efgs_workspace;
+void* efgs_workspace_alloc(void* workspace, size_t bytes);
+
 /* Message of the calling thread's last error (empty if none). */
 const char* efgs_last_error(void);
 

@@ -136,3 +136,26 @@ def test_bench_algorithmic_bytes_match_the_c3_budget():
     total = sum(bench.algorithmic(s, N, V, I, T, P, 32, F, 0)[0] for s in stages)
     assert abs(total / 1e6 - 670.0) < 1.0
     assert bench.algorithmic('adam', N, V, I, T, P, 32, F, 22_006_144)[0] == 28 * 22_006_144
+
+
+def test_workspace_allocator_bumps_aligns_and_falls_back():
+    """efgs_workspace_alloc hands out 256-byte-aligned slices of the region in order, sends what does not fit to
+    the fallback and counts every request (host-only: no memory is touched)."""
+    from efgs import _lib
+    calls = []
+
+    def fallback(_ctx, nbytes):
+        calls.append(nbytes)
+        return 0x900000
+
+    fb = _lib.ALLOC_FN(fallback)
+    ws = _lib.Workspace(0x100000, 1100, 0, 0, ctypes.cast(fb, ctypes.c_void_p), None)
+    p1 = _lib.lib.efgs_workspace_alloc(ctypes.byref(ws), 10)
+    p2 = _lib.lib.efgs_workspace_alloc(ctypes.byref(ws), 300)
+    p3 = _lib.lib.efgs_workspace_alloc(ctypes.byref(ws), 600)   # 768 aligned: does not fit after 768 used of 1100
+    p4 = _lib.lib.efgs_workspace_alloc(ctypes.byref(ws), 100)   # still fits after p2
+    assert (p1, p2, p3, p4) == (0x100000, 0x100100, 0x900000, 0x100300)
+    assert calls == [600] and ws.used == 1024
+    assert ws.requested == 256 + 512 + 768 + 256
+    empty = _lib.Workspace(None, 0, 0, 0, None, None)
+    assert _lib.lib.efgs_workspace_alloc(ctypes.byref(empty), 8) is None
