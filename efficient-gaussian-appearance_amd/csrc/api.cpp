@@ -355,26 +355,24 @@ MlpShape mlp_shape(const efgs_rasterizer* r) {
 // fp16 weight count of the tcnn-flat layout [W0 n x in_pad][W_h n x n]*(L-1)[W_out 16 x n]
 uint32_t mlp_params(const MlpShape& m) { return m.n_neurons * m.n_in_padded + (m.n_hidden - 1) * m.n_neurons * m.n_neurons + 16 * m.n_neurons; }
 
-// dynamic LDS of the neural preprocess kernels: fp16 weights + 4 per-wave staging areas (forward); the
-// backward reuses the area for the fp32 block reduction of the weight gradients
-uint32_t mlp_smem_forward(const MlpShape& m) {
-    const uint32_t inp = m.n_in_padded, nn = m.n_neurons;
-    const uint32_t maxk = inp > nn ? inp : nn;
-    const uint32_t row = maxk > 2 * inp ? maxk : 2 * inp;
-    const uint32_t weight_bytes = (mlp_params(m) * 2 + 15) / 16 * 16;
-    return weight_bytes + 4 * 64 * row * 2;
-}
-
-// the backward's MLP kernel: W and W^T with rows padded by 4 halves, 4 per-wave staging areas of 64 rows of
-// (n_in_padded + 4) floats; the area is reused for the fp32 block reduction of the weight gradients
-uint32_t mlp_smem_backward(const MlpShape& m) {
+// fp16 weights W_l and W_l^T with rows padded by 4 halves, as laid out by the neural kernels in LDS
+uint32_t mlp_dual_weight_bytes(const MlpShape& m) {
     uint32_t halves = 0;
     for (uint32_t l = 0; l <= m.n_hidden; l++) {
         const uint32_t in = l == 0 ? m.n_in_padded : m.n_neurons;
         const uint32_t out = l == m.n_hidden ? 16u : m.n_neurons;
         halves += out * (in + 4) + in * (out + 4);
     }
-    const uint32_t f = (halves * 2 + 15) / 16 * 16 + 4 * 64 * (m.n_in_padded + 4) * 4;
+    return (halves * 2 + 15) / 16 * 16;
+}
+
+// the forward's neural preprocess kernel: weights + 4 per-wave staging areas of 64 rows of (n_in_padded + 4) halves
+uint32_t mlp_smem_forward(const MlpShape& m) { return mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 2; }
+
+// the backward's MLP kernel: W and W^T with rows padded by 4 halves, 4 per-wave staging areas of 64 rows of
+// (n_in_padded + 4) floats; the area is reused for the fp32 block reduction of the weight gradients
+uint32_t mlp_smem_backward(const MlpShape& m) {
+    const uint32_t f = mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 4;
     const uint32_t red = mlp_params(m) * 4;
     return f > red ? f : red;
 }

@@ -35,9 +35,6 @@ constexpr uint32_t FEATURES = EFGS_N_UNITS;
 constexpr uint32_t RAW_FEATURES = FEATURES + (EFGS_BASE_INPUT ? 3u : 0u);
 constexpr uint32_t ENCODED = EFGS_N_FREQUENCIES == 0 ? RAW_FEATURES : RAW_FEATURES * 2u * EFGS_N_FREQUENCIES;
 constexpr uint32_t PARAMS = NN * INP + (NH - 1) * NN * NN + OUTP * NN;
-constexpr uint32_t STAGE_ROW = MAXK > 2 * INP ? MAXK : 2 * INP;
-constexpr uint32_t STAGE_HALVES = 64 * STAGE_ROW;  // per-wave LDS staging: 64 rows of MAXK halves or INP floats
-constexpr uint32_t WEIGHT_BYTES = (PARAMS * 2 + 15) / 16 * 16;
 
 __host__ __device__ constexpr uint32_t lin(uint32_t l) { return l == 0 ? INP : NN; }
 __host__ __device__ constexpr uint32_t lout(uint32_t l) { return l == NH ? OUTP : NN; }
@@ -195,174 +192,10 @@ __device__ inline float3 direction_grad(float3 d, uint32_t degree, const float* 
     return g;
 }
 
-// Per-wave MLP forward. W: the weights in LDS (fp16 bits); stage: this wave's LDS staging; x: the lane's input
-// row. Leaves the input activations of every layer in act (B fragments) and the fp16-rounded outputs in y.
-__device__ inline void mlp_forward(const uint16_t* W, _Float16* stage, const float* x, h4 (&act)[NL][KT][4], float* y, uint32_t lane) {
-    const uint32_t r = lane & 15u, q = lane >> 4;
-#pragma unroll
-    for (uint32_t k = 0; k < INP; k++) stage[lane * MAXK + k] = static_cast<_Float16>(x[k]);
-    wave_sync();
-#pragma unroll
-    for (uint32_t kb = 0; kb < INP / 16; kb++)
-#pragma unroll
-        for (uint32_t cb = 0; cb < 4; cb++) act[0][kb][cb] = *reinterpret_cast<const h4*>(&stage[(cb * 16 + r) * MAXK + kb * 16 + 4 * q]);
-    wave_sync();
-#pragma unroll
-    for (uint32_t l = 0; l < NL; l++) {
-        f4 acc[NT > 1 ? NT : 1][4];
-#pragma unroll
-        for (uint32_t rb = 0; rb < lout(l) / 16; rb++)
-#pragma unroll
-            for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = f4_zero();
-#pragma unroll
-        for (uint32_t rb = 0; rb < lout(l) / 16; rb++) {
-#pragma unroll
-            for (uint32_t kb = 0; kb < lin(l) / 16; kb++) {
-                const h4 a = *reinterpret_cast<const h4*>(&W[loff(l) + (rb * 16 + r) * lin(l) + kb * 16 + 4 * q]);
-#pragma unroll
-                for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = mfma(a, act[l][kb][cb], acc[rb][cb]);
-            }
-        }
-        if (l < NH) {
-#pragma unroll
-            for (uint32_t rb = 0; rb < lout(l) / 16; rb++)
-#pragma unroll
-                for (uint32_t cb = 0; cb < 4; cb++) {
-                    const f4 v = acc[rb][cb];
-                    act[l + 1][rb][cb] = h4{static_cast<_Float16>(fmaxf(v[0], 0.0f)), static_cast<_Float16>(fmaxf(v[1], 0.0f)),
-                                            static_cast<_Float16>(fmaxf(v[2], 0.0f)), static_cast<_Float16>(fmaxf(v[3], 0.0f))};
-                }
-        } else {
-            // outputs 0..2 of primitive 16 cb + c sit in lane c of tile cb
-#pragma unroll
-            for (uint32_t o = 0; o < 3; o++) {
-                float v = 0.0f;
-#pragma unroll
-                for (uint32_t cb = 0; cb < 4; cb++) {
-                    const float t = __shfl(acc[0][cb][o], static_cast<int>(r));
-                    if (q == cb) v = t;
-                }
-                y[o] = round_half(v);
-            }
-        }
-    }
-}
-
 __device__ __forceinline__ float wave_max_f32(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;
-}
-
-// Per-wave MLP backward. dy: the lane's gradient of the 3 raw outputs (zero for lanes that do not contribute);
-// act from mlp_forward. Writes the lane's input gradient row dx (INP floats) and adds the wave's weight gradients
-// to dW (fp32 accumulator tiles, lane layout of the D operand).
-__device__ inline void mlp_backward(const uint16_t* W, _Float16* stage, const h4 (&act)[NL][KT][4], const float* dy, float* dx,
-                                    f4 (&dW)[NL][NT > 1 ? NT : 1][KT], uint32_t lane) {
-    const uint32_t r = lane & 15u, q = lane >> 4;
-    const float m = wave_max_f32(fmaxf(fmaxf(fabsf(dy[0]), fabsf(dy[1])), fabsf(dy[2])));
-#pragma unroll
-    for (uint32_t k = 0; k < INP; k++) dx[k] = 0.0f;
-    if (!(m > 0.0f) || !(m < 3.0e38f)) return;  // wave-uniform
-    const int e = max(ilogbf(m), -110);  // keeps the scale 2^(8 - e) finite for denormal maxima
-    const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
-
-    // output-layer gradient tiles (16 outputs x 64 primitives): rows 0..2 live in lanes 0..15
-    h4 g[NT > 1 ? NT : 1][4];
-#pragma unroll
-    for (uint32_t cb = 0; cb < 4; cb++) {
-        float v[3];
-#pragma unroll
-        for (uint32_t j = 0; j < 3; j++) v[j] = __shfl(dy[j] * s, static_cast<int>(cb * 16 + r));
-        g[0][cb] = q == 0 ? h4{static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]), static_cast<_Float16>(v[2]), static_cast<_Float16>(0.0f)}
-                          : h4{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f)};
-    }
-
-#pragma unroll
-    for (int li = static_cast<int>(NH); li >= 0; li--) {
-        const uint32_t l = static_cast<uint32_t>(li);
-        constexpr uint32_t stride = 64;  // staging rows are indexed [feature][primitive]
-        // ---- weight gradient dW_l += G_l X_l (operands transposed through LDS) ----
-        h4 ga[NT > 1 ? NT : 1][4];  // A fragments: G_l[out 16 rb + r][prims 16 kb + 4 q .. +3]
-#pragma unroll
-        for (uint32_t rb = 0; rb < lout(l) / 16; rb++)
-#pragma unroll
-            for (uint32_t cb = 0; cb < 4; cb++)
-#pragma unroll
-                for (uint32_t i = 0; i < 4; i++) stage[(rb * 16 + 4 * q + i) * stride + cb * 16 + r] = g[rb][cb][i];
-        wave_sync();
-#pragma unroll
-        for (uint32_t rb = 0; rb < lout(l) / 16; rb++)
-#pragma unroll
-            for (uint32_t kb = 0; kb < 4; kb++) ga[rb][kb] = *reinterpret_cast<const h4*>(&stage[(rb * 16 + r) * stride + kb * 16 + 4 * q]);
-        wave_sync();
-#pragma unroll
-        for (uint32_t kb = 0; kb < lin(l) / 16; kb++)
-#pragma unroll
-            for (uint32_t cb = 0; cb < 4; cb++)
-#pragma unroll
-                for (uint32_t i = 0; i < 4; i++) stage[(kb * 16 + 4 * q + i) * stride + cb * 16 + r] = act[l][kb][cb][i];
-        wave_sync();
-#pragma unroll
-        for (uint32_t rb = 0; rb < lout(l) / 16; rb++) {
-#pragma unroll
-            for (uint32_t cb = 0; cb < lin(l) / 16; cb++) {
-                f4 t = f4_zero();
-#pragma unroll
-                for (uint32_t kb = 0; kb < 4; kb++) {
-                    const h4 b = *reinterpret_cast<const h4*>(&stage[(cb * 16 + r) * stride + kb * 16 + 4 * q]);
-                    t = mfma(ga[rb][kb], b, t);
-                }
-#pragma unroll
-                for (uint32_t i = 0; i < 4; i++) dW[l][rb][cb][i] = __builtin_fmaf(t[i], inv_s, dW[l][rb][cb][i]);
-            }
-        }
-        wave_sync();
-        // ---- input gradient G_in = W_l^T G_l ----
-        f4 acc[KT][4];
-#pragma unroll
-        for (uint32_t rb = 0; rb < lin(l) / 16; rb++)
-#pragma unroll
-            for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = f4_zero();
-#pragma unroll
-        for (uint32_t rb = 0; rb < lin(l) / 16; rb++) {
-#pragma unroll
-            for (uint32_t kb = 0; kb < lout(l) / 16; kb++) {
-                const uint32_t base = loff(l) + (kb * 16 + 4 * q) * lin(l) + rb * 16 + r;
-                const uint16_t w0 = W[base], w1 = W[base + lin(l)], w2 = W[base + 2 * lin(l)], w3 = W[base + 3 * lin(l)];
-                const h4 a = h4{__builtin_bit_cast(_Float16, w0), __builtin_bit_cast(_Float16, w1), __builtin_bit_cast(_Float16, w2),
-                                __builtin_bit_cast(_Float16, w3)};
-#pragma unroll
-                for (uint32_t cb = 0; cb < 4; cb++) acc[rb][cb] = mfma(a, g[kb][cb], acc[rb][cb]);
-            }
-        }
-        if (l > 0) {
-#pragma unroll
-            for (uint32_t rb = 0; rb < lin(l) / 16; rb++)
-#pragma unroll
-                for (uint32_t cb = 0; cb < 4; cb++) {
-                    const h4 xa = act[l][rb][cb];
-                    const f4 v = acc[rb][cb];
-                    g[rb][cb] = h4{static_cast<_Float16>(xa[0] > static_cast<_Float16>(0.0f) ? v[0] : 0.0f),
-                                   static_cast<_Float16>(xa[1] > static_cast<_Float16>(0.0f) ? v[1] : 0.0f),
-                                   static_cast<_Float16>(xa[2] > static_cast<_Float16>(0.0f) ? v[2] : 0.0f),
-                                   static_cast<_Float16>(xa[3] > static_cast<_Float16>(0.0f) ? v[3] : 0.0f)};
-                }
-        } else {
-            // input gradient rows to their lanes through LDS (as floats, 64 x INP)
-            float* fs = reinterpret_cast<float*>(stage);
-#pragma unroll
-            for (uint32_t rb = 0; rb < INP / 16; rb++)
-#pragma unroll
-                for (uint32_t cb = 0; cb < 4; cb++)
-#pragma unroll
-                    for (uint32_t i = 0; i < 4; i++) fs[(cb * 16 + r) * INP + rb * 16 + 4 * q + i] = acc[rb][cb][i] * inv_s;
-            wave_sync();
-#pragma unroll
-            for (uint32_t k = 0; k < INP; k++) dx[k] = fs[lane * INP + k];
-            wave_sync();
-        }
-    }
 }
 
 // ---- dual-orientation MLP of the backward kernel --------------------------------------------------------
@@ -434,11 +267,13 @@ __device__ __forceinline__ h4 masked_h4_bits(f4 v, uint32_t bits) {
               (bits & 4u) ? static_cast<_Float16>(v[2]) : z, (bits & 8u) ? static_cast<_Float16>(v[3]) : z};
 }
 
-// Forward recompute in both orientations. WL: padded W / W^T in LDS; stage: this wave's staging area; x: the
-// lane's input row. U[l]: input activations of layer l as primitive-rows tiles (fp16); Tm[l] (l >= 1): the
-// ReLU masks of the feature-rows tiles; y: the lane's three raw outputs, rounded to fp16 (as mlp_forward).
-__device__ inline void mlp_forward_dual(const _Float16* WL, _Float16* stage, const float* x, uint32_t (&Tm)[NL][MASK_WORDS], h4 (&U)[NL][4][KT],
-                                        float* y, uint32_t lane) {
+// Per-wave MLP forward: fp16 MFMA, fp32 accumulation, activations rounded to fp16 between layers. WL: padded
+// W / W^T in LDS; stage: this wave's staging area; x: the lane's input row; y: the lane's three raw outputs,
+// rounded to fp16. With DUAL (the backward's recompute) it also leaves U[l], the input activations of layer l
+// as primitive-rows tiles, and Tm[l] (l >= 1), the ReLU masks of the feature-rows tiles.
+template <bool DUAL>
+__device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, const float* x, uint32_t (&Tm)[NL][MASK_WORDS], h4 (&U)[NL][4][KT],
+                                         float* y, uint32_t lane) {
     h4 T[NL][KT][4];
     const uint32_t r = lane & 15u, q = lane >> 4;
 #pragma unroll
@@ -451,7 +286,8 @@ __device__ inline void mlp_forward_dual(const _Float16* WL, _Float16* stage, con
 #pragma unroll
         for (uint32_t pb = 0; pb < 4; pb++) {
             T[0][ib][pb] = *reinterpret_cast<const h4*>(&stage[(16 * pb + r) * XS + 16 * ib + 4 * q]);
-            U[0][pb][ib] = h4{stage[(16 * pb + 4 * q) * XS + 16 * ib + r], stage[(16 * pb + 4 * q + 1) * XS + 16 * ib + r],
+            if (DUAL)
+                U[0][pb][ib] = h4{stage[(16 * pb + 4 * q) * XS + 16 * ib + r], stage[(16 * pb + 4 * q + 1) * XS + 16 * ib + r],
                               stage[(16 * pb + 4 * q + 2) * XS + 16 * ib + r], stage[(16 * pb + 4 * q + 3) * XS + 16 * ib + r]};
         }
     wave_sync();
@@ -470,6 +306,7 @@ __device__ inline void mlp_forward_dual(const _Float16* WL, _Float16* stage, con
                 for (uint32_t ib = 0; ib < lin(l) / 16; ib++) t = mfma(wa[ib], T[l][ib][pb], t);  // H(ob, pb) = sum W(ob, ib) M(ib, pb)
                 if (l < NH) {
                     T[l + 1][ob][pb] = relu_h4(t);
+                    if (!DUAL) continue;
                     f4 u = f4_zero();
 #pragma unroll
                     for (uint32_t ib = 0; ib < lin(l) / 16; ib++) u = mfma(T[l][ib][pb], wa[ib], u);  // H^T(pb, ob) = sum M^T(pb, ib) W^T(ib, ob)
@@ -492,6 +329,7 @@ __device__ inline void mlp_forward_dual(const _Float16* WL, _Float16* stage, con
         }
         y[o] = round_half(v);
     }
+    if (!DUAL) return;
 #pragma unroll
     for (uint32_t l = 1; l < NL; l++) {
 #pragma unroll
@@ -507,7 +345,7 @@ __device__ inline void mlp_forward_dual(const _Float16* WL, _Float16* stage, con
 }
 
 // Backward through the MLP from the lanes' output gradients dy (zero for lanes that do not contribute), with
-// Tm / U from mlp_forward_dual. Writes the lane's input gradient row dx (INP floats) and adds the wave's weight
+// Tm / U from mlp_forward_tiles<true>. Writes the lane's input gradient row dx (INP floats) and adds the wave's weight
 // gradients to dW (lane layout of the D operand: dW[l][ob][ib][i] = dW_l[16 ob + 4 q + i][16 ib + r]).
 __device__ inline void mlp_backward_dual(const _Float16* WL, _Float16* stage, const uint32_t (&Tm)[NL][MASK_WORDS], const h4 (&U)[NL][4][KT],
                                          const float* dy, float* dx, f4 (&dW)[NL][NT > 1 ? NT : 1][KT], uint32_t lane) {

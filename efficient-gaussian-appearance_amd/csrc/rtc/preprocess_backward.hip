@@ -295,7 +295,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _ml
         uint32_t Tm[nn::NL][nn::MASK_WORDS];
         nn::h4 U[nn::NL][4][nn::KT];
         float y[3];
-        nn::mlp_forward_dual(WL, stage, x, Tm, U, y, lane);
+        nn::mlp_forward_tiles<true>(WL, stage, x, Tm, U, y, lane);
         float dy[3];
         dy[0] = dpre.x * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[0]));
         dy[1] = dpre.y * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[1]));

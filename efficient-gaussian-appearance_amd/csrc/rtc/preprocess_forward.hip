@@ -149,12 +149,11 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     const uint32_t wave = threadIdx.x >> 6;
     __shared__ uint32_t wave_counts[2 * (preprocess_block / 64)];
 #if EFGS_MODEL == 5
-    // residual MLP weights staged once per block; per-wave staging area for operand transposes
+    // residual MLP weights staged once per block (padded rows); per-wave staging area for the input tiles
     extern __shared__ __align__(16) unsigned char smem[];
-    uint16_t* W = reinterpret_cast<uint16_t*>(smem);
-    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES) + wave * nn::STAGE_HALVES;
-    for (uint32_t i = threadIdx.x; i < nn::PARAMS / 8; i += preprocess_block)
-        reinterpret_cast<uint4*>(W)[i] = reinterpret_cast<const uint4*>(a.mlp_weights)[i];
+    const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES) + wave * 64 * nn::XS;
+    nn::load_dual_weights(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x, preprocess_block);
     __syncthreads();
 #endif
     const uint32_t n_chunks = (a.n + preprocess_block - 1) / preprocess_block;
@@ -178,13 +177,14 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         const float* rp = a.residual + static_cast<size_t>(p) * residual_params;
         float3 res = make_float3(0.0f, 0.0f, 0.0f);
 #if EFGS_MODEL == 5
-        // every lane of every wave runs the MLP (the waves share the block's LDS staging discipline)
-        if (a.cam.degree > 0) {
+        // the wave's 64 lanes run the MLP together (skipped when none of them is visible)
+        if (a.cam.degree > 0 && __ballot(visible) != 0) {
             float x[nn::INP];
             nn::mlp_input(rp, a.base + 3 * p, d, a.cam.degree, x);
-            nn::h4 act[nn::NL][nn::KT][4];
+            uint32_t masks[nn::NL][nn::MASK_WORDS];
+            nn::h4 unused[nn::NL][4][nn::KT];
             float y[3];
-            nn::mlp_forward(W, stage, x, act, y, lane);
+            nn::mlp_forward_tiles<false>(WL, stage, x, masks, unused, y, lane);
             res = make_float3(residual_activation<EFGS_RES_ACT>(y[0]), residual_activation<EFGS_RES_ACT>(y[1]),
                               residual_activation<EFGS_RES_ACT>(y[2]));
         }
