@@ -35,7 +35,8 @@ __global__ __launch_bounds__(adam_block) void adam_kernel(AdamLaunch L) {
         const float m1 = __builtin_fmaf(G.beta1, m - grad, grad);
         const float m2 = __builtin_fmaf(G.beta2, v - g2, g2);
         const float denom = __builtin_fmaf(sqrtf(m2), G.bc2_sqrt_rcp, G.eps);
-        G.param[i] -= G.step_sizes[i % static_cast<uint64_t>(G.n_lrs)] * m1 / denom;
+        const float step = G.n_lrs == 1 ? G.step_sizes[0] : G.step_sizes[i % static_cast<uint64_t>(G.n_lrs)];  // uniform branch
+        G.param[i] -= step * m1 / denom;
         G.m[i] = m1;
         G.v[i] = m2;
     }

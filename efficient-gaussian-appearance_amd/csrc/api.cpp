@@ -139,7 +139,7 @@ struct efgs_rasterizer {
     int mlp_sh_mask = 0;
     int mlp_n_features = 0;
     bool mlp_base_input = false;
-    uint32_t* host_counters = nullptr;  // pinned, 4 entries
+    uint32_t* host_counters = nullptr;  // pinned, n_counters entries
     efgs::StageTimer timer;
     // specialised preprocess kernels of the current configuration, per variant and direction (forward,
     // backward), for the device they were loaded on; cleared whenever the configuration changes
@@ -178,6 +178,7 @@ struct PrimitiveLayout {
     PrimRecord* records;
     uint32_t* prim_offset;
     uint32_t* block_counts;
+    uint32_t* block_key_ranges;
     uint32_t* block_offsets;
     uint32_t* counters;
     uint32_t* keys_a;
@@ -199,8 +200,9 @@ struct PrimitiveLayout {
         l.records = c.take<PrimRecord>(nn);
         l.prim_offset = c.take<uint32_t>(nn);
         l.block_counts = c.take<uint32_t>(2ull * blocks);
+        l.block_key_ranges = c.take<uint32_t>(2ull * blocks);
         l.block_offsets = c.take<uint32_t>(2ull * blocks);
-        l.counters = c.take<uint32_t>(4);
+        l.counters = c.take<uint32_t>(n_counters);
         l.keys_a = c.take<uint32_t>(nn);
         l.vals_a = c.take<uint32_t>(nn);
         l.keys_b = c.take<uint32_t>(nn);
@@ -565,7 +567,7 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     const int key_bytes = n_tiles <= 65535u ? 2 : 4;
     const int end_bit = end_bit_of(n_tiles - 1);
     if (!r->host_counters) {
-        if (hipHostMalloc(reinterpret_cast<void**>(&r->host_counters), 4 * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
+        if (hipHostMalloc(reinterpret_cast<void**>(&r->host_counters), n_counters * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
             return fail(EFGS_ERR_HIP, "hipHostMalloc of the counter readback buffer failed");
     }
 
@@ -597,6 +599,7 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         a.depth_keys = pl.depth_keys;
         a.records = pl.records;
         a.block_counts = pl.block_counts;
+        a.block_key_ranges = pl.block_key_ranges;
         a.n = n;
         a.cam = cam;
         const uint32_t chunks = div_up(n, preprocess_block);
@@ -606,23 +609,24 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (!launch_rtc(k, blocks, preprocess_block, shared, &a, s)) return EFGS_ERR_HIP;
         t.end(s);
         t.begin(EFGS_STAGE_COMPACT, s);
-        if (!launch_scan_block_counts(pl.block_counts, pl.block_offsets, pl.counters, chunks, s)) return EFGS_ERR_HIP;
-        if (!launch_compact_visible(pl.n_touched, pl.depth_keys, pl.block_offsets, pl.keys_a, pl.vals_a, n, s)) return EFGS_ERR_HIP;
+        if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, chunks, s)) return EFGS_ERR_HIP;
+        if (!launch_compact_visible(pl.n_touched, pl.depth_keys, pl.block_offsets, pl.counters, pl.keys_a, pl.vals_a, n, s)) return EFGS_ERR_HIP;
         t.end(s);
     } else {
-        if (!launch_fill_u32(pl.counters, 0u, 4, s)) return EFGS_ERR_HIP;
+        if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
     }
     t.begin(EFGS_STAGE_COUNTER_READ, s);
-    if (hipMemcpyAsync(r->host_counters, pl.counters, 4 * sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+    if (hipMemcpyAsync(r->host_counters, pl.counters, n_counters * sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return fail(EFGS_ERR_HIP, std::string("reading the visible/instance counters failed: ") + hipGetErrorString(hipGetLastError()));
     t.end(s);
     const uint32_t n_visible = r->host_counters[0];
     const uint32_t n_instances = r->host_counters[1];
+    const int depth_end_bit = end_bit_of(r->host_counters[4] - r->host_counters[3]);  // keys are relative to the minimum
 
     bool depth_in_b = false;
     t.begin(EFGS_STAGE_DEPTH_SORT, s);
-    if (!radix_sort_pairs(pl.keys_a, pl.vals_a, pl.keys_b, pl.vals_b, false, n_visible, 4, 32, pl.sort_scratch, &depth_in_b, s))
+    if (!radix_sort_pairs(pl.keys_a, pl.vals_a, pl.keys_b, pl.vals_b, false, n_visible, 4, depth_end_bit, pl.sort_scratch, &depth_in_b, s))
         return EFGS_ERR_HIP;
     t.end(s);
     const uint32_t* depth_sorted_prims = depth_in_b ? pl.vals_b : pl.vals_a;

@@ -13,10 +13,10 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t n) {
     if (i < n) p[i] = value;
 }
 
-// primitive-index-ordered compaction of (depth key, primitive) for the visible primitives
+// primitive-index-ordered compaction of (depth key - min depth key, primitive) for the visible primitives
 __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const uint32_t* n_touched, const uint32_t* depth_keys,
-                                                                          const uint32_t* block_offsets, uint32_t* keys_out,
-                                                                          uint32_t* vals_out, uint32_t n) {
+                                                                          const uint32_t* block_offsets, const uint32_t* counters,
+                                                                          uint32_t* keys_out, uint32_t* vals_out, uint32_t n) {
     __shared__ uint32_t wave_counts[preprocess_block / 64];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
@@ -28,7 +28,7 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
     uint32_t pos = block_offsets[2 * blockIdx.x];
     for (uint32_t w = 0; w < wave; w++) pos += wave_counts[w];
     pos += static_cast<uint32_t>(__popcll(mask & ((1ull << lane) - 1ull)));
-    keys_out[pos] = depth_keys[p];
+    keys_out[pos] = depth_keys[p] - counters[3];
     vals_out[pos] = p;
 }
 
@@ -148,9 +148,10 @@ bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s) {
     return true;
 }
 
-bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_keys, const uint32_t* block_offsets, uint32_t* keys_out,
-                            uint32_t* vals_out, uint32_t n, hipStream_t s) {
-    compact_visible_kernel<<<div_up(n, preprocess_block), preprocess_block, 0, s>>>(n_touched, depth_keys, block_offsets, keys_out, vals_out, n);
+bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_keys, const uint32_t* block_offsets, const uint32_t* counters,
+                            uint32_t* keys_out, uint32_t* vals_out, uint32_t n, hipStream_t s) {
+    compact_visible_kernel<<<div_up(n, preprocess_block), preprocess_block, 0, s>>>(n_touched, depth_keys, block_offsets, counters, keys_out,
+                                                                                     vals_out, n);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

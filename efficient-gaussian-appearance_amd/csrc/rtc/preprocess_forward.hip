@@ -141,13 +141,25 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
     return v;
 }
 
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, static_cast<uint32_t>(__shfl_xor(v, o)));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, o)));
+    return v;
+}
+
 }  // namespace efgs
 
 extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessForwardArgs a) {
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
-    __shared__ uint32_t wave_counts[2 * (preprocess_block / 64)];
+    __shared__ uint32_t wave_counts[4 * (preprocess_block / 64)];
 #if EFGS_MODEL == 5
     // residual MLP weights staged once per block (padded rows); per-wave staging area for the input tiles
     extern __shared__ __align__(16) unsigned char smem[];
@@ -228,20 +240,29 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         // per-chunk visible / instance counts (deterministic compaction offsets come from their scan)
         const uint32_t wave_visible = static_cast<uint32_t>(__popcll(__ballot(visible && active)));
         const uint32_t wave_instances = wave_sum_u32(active ? touched : 0u);
+        const uint32_t key = __float_as_uint(pr.depth);
+        const uint32_t wave_kmin = wave_min_u32(visible && active ? key : 0xffffffffu);
+        const uint32_t wave_kmax = wave_max_u32(visible && active ? key : 0u);
         if (lane == 0) {
-            wave_counts[2 * wave] = wave_visible;
-            wave_counts[2 * wave + 1] = wave_instances;
+            wave_counts[4 * wave] = wave_visible;
+            wave_counts[4 * wave + 1] = wave_instances;
+            wave_counts[4 * wave + 2] = wave_kmin;
+            wave_counts[4 * wave + 3] = wave_kmax;
         }
         __syncthreads();
         if (threadIdx.x == 0) {
-            uint32_t v = 0, i = 0;
+            uint32_t v = 0, i = 0, kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
             for (uint32_t w = 0; w < preprocess_block / 64; w++) {
-                v += wave_counts[2 * w];
-                i += wave_counts[2 * w + 1];
+                v += wave_counts[4 * w];
+                i += wave_counts[4 * w + 1];
+                kmin = min(kmin, wave_counts[4 * w + 2]);
+                kmax = max(kmax, wave_counts[4 * w + 3]);
             }
             a.block_counts[2 * chunk] = v;
             a.block_counts[2 * chunk + 1] = i;
+            a.block_key_ranges[2 * chunk] = kmin;
+            a.block_key_ranges[2 * chunk + 1] = kmax;
         }
         __syncthreads();
     }

@@ -95,17 +95,32 @@ __global__ __launch_bounds__(scan_block) void scan_downsweep_kernel(const uint32
     }
 }
 
-// one block: offsets of the per-preprocess-block (visible, instance) counts; counters[0] = V, counters[1] = I
-__global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t* counts, uint32_t* offsets, uint32_t* counters, uint32_t n) {
+// one block: offsets of the per-preprocess-block (visible, instance) counts; counters[0] = V, counters[1] = I,
+// counters[3] / counters[4] = min / max depth key of the visible primitives
+__global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t* counts, const uint32_t* key_ranges, uint32_t* offsets,
+                                                                 uint32_t* counters, uint32_t n) {
+    __shared__ uint32_t s_range[2 * 16];
     const uint32_t per = (n + 1023) / 1024;
     const uint32_t base = threadIdx.x * per;
-    uint32_t sv = 0, si = 0;
+    uint32_t sv = 0, si = 0, kmin = 0xffffffffu, kmax = 0u;
     for (uint32_t k = 0; k < per; k++) {
         if (base + k < n) {
             sv += counts[2 * (base + k)];
             si += counts[2 * (base + k) + 1];
+            kmin = min(kmin, key_ranges[2 * (base + k)]);
+            kmax = max(kmax, key_ranges[2 * (base + k) + 1]);
         }
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(kmin, o)));
+        kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(kmax, o)));
+    }
+    if ((threadIdx.x & 63u) == 0) {
+        s_range[2 * (threadIdx.x >> 6)] = kmin;
+        s_range[2 * (threadIdx.x >> 6) + 1] = kmax;
+    }
+    __syncthreads();
     uint32_t tv, ti;
     uint32_t pv = block_exclusive_scan<1024>(sv, tv);
     uint32_t pi = block_exclusive_scan<1024>(si, ti);
@@ -118,10 +133,16 @@ __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t*
         }
     }
     if (threadIdx.x == 0) {
+        uint32_t lo = 0xffffffffu, hi = 0u;
+        for (uint32_t w = 0; w < 16; w++) {
+            lo = min(lo, s_range[2 * w]);
+            hi = max(hi, s_range[2 * w + 1]);
+        }
         counters[0] = tv;
         counters[1] = ti;
         counters[2] = 0;  // instance-emission mismatch counter, see create_instances
-        counters[3] = 0;
+        counters[3] = tv > 0 ? lo : 0u;
+        counters[4] = tv > 0 ? hi : 0u;
     }
 }
 
@@ -142,8 +163,9 @@ bool scan_exclusive(const uint32_t* in, const uint32_t* idx, uint32_t* out, uint
     return true;
 }
 
-bool launch_scan_block_counts(const uint32_t* block_counts, uint32_t* block_offsets, uint32_t* counters, uint32_t n_blocks, hipStream_t s) {
-    scan_block_counts_kernel<<<1, 1024, 0, s>>>(block_counts, block_offsets, counters, n_blocks);
+bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters, uint32_t n_blocks,
+                              hipStream_t s) {
+    scan_block_counts_kernel<<<1, 1024, 0, s>>>(block_counts, key_ranges, block_offsets, counters, n_blocks);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

@@ -180,7 +180,7 @@ typedef struct efgs_frame_views {
     const uint32_t* n_touched;        /* (N) 0 = culled */
     const uint32_t* depth_keys;       /* (N) float bits of the view depth (valid where n_touched > 0) */
     const float* records;             /* (N x 12) mean2d xy, conic xyz, opacity, rgb, packed bounds, pad */
-    const uint32_t* depth_sorted_keys;   /* (V) */
+    const uint32_t* depth_sorted_keys;   /* (V) depth keys minus counters[3] (the smallest visible depth key) */
     const uint32_t* depth_sorted_prims;  /* (V) */
     const uint32_t* instance_offsets;    /* (V) exclusive scan of touched tiles in depth order */
     const void* tile_sorted_keys;        /* (I) key_bytes wide */
@@ -189,7 +189,7 @@ typedef struct efgs_frame_views {
     const uint32_t* tile_ranges;         /* (T x 2) [start, end) */
     const float* final_transmittance;    /* (T x 192) per tile, row-major 16 x 12 */
     const uint32_t* n_contributors;      /* (T x 192) */
-    const uint32_t* counters;            /* (4) V, I, instance-count mismatches, reserved */
+    const uint32_t* counters;            /* (8) V, I, instance-count mismatches, min and max visible depth key, reserved */
 } efgs_frame_views;
 int efgs_get_frame_views(const efgs_frame* frame, efgs_frame_views* views);
 

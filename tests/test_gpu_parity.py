@@ -83,7 +83,11 @@ def test_forward_parity(name):
     b = fw.bounds[vis].astype(np.uint32)
     np.testing.assert_array_equal(np.stack([bx & 0xffff, bx >> 16, by & 0xffff, by >> 16], 1), b)
     np.testing.assert_allclose(rec[:, 6:9], fw.color[vis], rtol=0, atol=_image_tol(CASES[name]) / 10 if CASES[name].get('model') != 'neural' else IMAGE_TOL_FP16)
-    np.testing.assert_array_equal(read_device(bufs, v.depth_sorted_keys, V, np.uint32), fw.depth_key[fw.depth_sorted])
+    counters = read_device(bufs, v.counters, 8, np.uint32)
+    if V > 0:
+        assert counters[3] == fw.depth_key[vis].min() and counters[4] == fw.depth_key[vis].max()
+    # sorted keys are stored relative to the smallest visible key (counters[3])
+    np.testing.assert_array_equal(read_device(bufs, v.depth_sorted_keys, V, np.uint32) + counters[3], fw.depth_key[fw.depth_sorted])
     np.testing.assert_array_equal(read_device(bufs, v.depth_sorted_prims, V, np.uint32), fw.depth_sorted)
     np.testing.assert_array_equal(read_device(bufs, v.instance_offsets, V, np.uint32), fw.offsets)
     kt = np.uint16 if frame.key_bytes == 2 else np.uint32
