@@ -292,6 +292,49 @@ int n_units_of(const efgs_rasterizer* r, int model) {
     return 0;
 }
 
+struct MlpShape {
+    uint32_t n_in_padded, n_neurons, n_hidden;
+};
+
+MlpShape mlp_shape(const efgs_rasterizer* r) {
+    return MlpShape{static_cast<uint32_t>(r->mlp_n_in_padded), static_cast<uint32_t>(r->mlp_n_neurons), static_cast<uint32_t>(r->mlp_n_hidden)};
+}
+
+// fp16 weight count of the tcnn-flat layout [W0 n x in_pad][W_h n x n]*(L-1)[W_out 16 x n]
+uint32_t mlp_params(const MlpShape& m) { return m.n_neurons * m.n_in_padded + (m.n_hidden - 1) * m.n_neurons * m.n_neurons + 16 * m.n_neurons; }
+
+// fp16 weights W_l and W_l^T with rows padded by 4 halves, as laid out by the neural kernels in LDS
+uint32_t mlp_dual_weight_bytes(const MlpShape& m) {
+    uint32_t halves = 0;
+    for (uint32_t l = 0; l <= m.n_hidden; l++) {
+        const uint32_t in = l == 0 ? m.n_in_padded : m.n_neurons;
+        const uint32_t out = l == m.n_hidden ? 16u : m.n_neurons;
+        halves += out * (in + 4) + in * (out + 4);
+    }
+    return (halves * 2 + 15) / 16 * 16;
+}
+
+// the forward's neural preprocess kernel: weights + 4 per-wave staging areas of 64 rows of (n_in_padded + 4) halves
+uint32_t mlp_smem_forward(const MlpShape& m) { return mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 2; }
+
+// the backward's MLP kernel: W and W^T with rows padded by 4 halves, 4 per-wave staging areas of 64 rows of
+// (n_in_padded + 4) floats; the area is reused for the fp32 block reduction of the weight gradients
+constexpr uint32_t max_dynamic_lds = 160 * 1024;  // gfx950: 160 KiB of LDS per block
+
+// per-wave LDS store of the hidden layers' primitive-rows input tiles (one 8-byte slot per lane and tile)
+uint32_t mlp_u_store_bytes(const MlpShape& m) { return m.n_hidden * (m.n_neurons / 16) * 4 * 64 * 8; }
+
+uint32_t mlp_smem_backward_base(const MlpShape& m) { return mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 4; }
+
+// the backward's MLP kernel keeps those tiles in LDS when the store fits next to the weights and staging
+bool mlp_u_in_lds(const MlpShape& m) { return mlp_smem_backward_base(m) + 4 * mlp_u_store_bytes(m) <= max_dynamic_lds; }
+
+uint32_t mlp_smem_backward(const MlpShape& m) {
+    const uint32_t f = mlp_smem_backward_base(m) + (mlp_u_in_lds(m) ? 4 * mlp_u_store_bytes(m) : 0u);
+    const uint32_t red = mlp_params(m) * 4;
+    return f > red ? f : red;
+}
+
 // preamble tokens and source files of the preprocess kernel `kind` ("forward" / "backward") for `model`
 void kernel_source(const efgs_rasterizer* r, int model, const char* kind, std::string& name, std::string& preamble,
                    std::vector<std::string>& files) {
@@ -311,6 +354,7 @@ void kernel_source(const efgs_rasterizer* r, int model, const char* kind, std::s
     preamble += "#define EFGS_N_FREQUENCIES " + std::to_string(model == 5 ? r->mlp_n_frequencies : 0) + "u\n";
     preamble += "#define EFGS_SH_DEGREE_MASK " + std::to_string(model == 5 ? r->mlp_sh_mask : 0) + "u\n";
     preamble += "#define EFGS_BASE_INPUT " + std::string(model == 5 && r->mlp_base_input ? "1" : "0") + "\n";
+    preamble += "#define EFGS_MLP_U_LDS " + std::string(model == 5 && mlp_u_in_lds(mlp_shape(r)) ? "1" : "0") + "\n";
     files = {"efgs_common.h", "efgs_args.h"};
     switch (model) {
         case 1: files.push_back("appearance_sh.h"); break;
@@ -346,40 +390,7 @@ bool get_preprocess_kernel(efgs_rasterizer* r, int model, const char* kind, RtcK
     return true;
 }
 
-struct MlpShape {
-    uint32_t n_in_padded, n_neurons, n_hidden;
-};
 
-MlpShape mlp_shape(const efgs_rasterizer* r) {
-    return MlpShape{static_cast<uint32_t>(r->mlp_n_in_padded), static_cast<uint32_t>(r->mlp_n_neurons), static_cast<uint32_t>(r->mlp_n_hidden)};
-}
-
-// fp16 weight count of the tcnn-flat layout [W0 n x in_pad][W_h n x n]*(L-1)[W_out 16 x n]
-uint32_t mlp_params(const MlpShape& m) { return m.n_neurons * m.n_in_padded + (m.n_hidden - 1) * m.n_neurons * m.n_neurons + 16 * m.n_neurons; }
-
-// fp16 weights W_l and W_l^T with rows padded by 4 halves, as laid out by the neural kernels in LDS
-uint32_t mlp_dual_weight_bytes(const MlpShape& m) {
-    uint32_t halves = 0;
-    for (uint32_t l = 0; l <= m.n_hidden; l++) {
-        const uint32_t in = l == 0 ? m.n_in_padded : m.n_neurons;
-        const uint32_t out = l == m.n_hidden ? 16u : m.n_neurons;
-        halves += out * (in + 4) + in * (out + 4);
-    }
-    return (halves * 2 + 15) / 16 * 16;
-}
-
-// the forward's neural preprocess kernel: weights + 4 per-wave staging areas of 64 rows of (n_in_padded + 4) halves
-uint32_t mlp_smem_forward(const MlpShape& m) { return mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 2; }
-
-// the backward's MLP kernel: W and W^T with rows padded by 4 halves, 4 per-wave staging areas of 64 rows of
-// (n_in_padded + 4) floats; the area is reused for the fp32 block reduction of the weight gradients
-uint32_t mlp_smem_backward(const MlpShape& m) {
-    const uint32_t f = mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 4;
-    const uint32_t red = mlp_params(m) * 4;
-    return f > red ? f : red;
-}
-
-constexpr uint32_t max_dynamic_lds = 64 * 1024;
 constexpr uint32_t neural_forward_blocks = 1024;
 constexpr uint32_t neural_backward_blocks = 512;
 
@@ -776,9 +787,11 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     }
     if (!grads->mlp_weights) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp weight gradient output is required");
     const uint32_t params = mlp_params(mlp_shape(r));
-    float* color_grads = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(n) * 4 * sizeof(float)));
+    float* color_grads = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(n) * 4 * sizeof(float) + 256));
     if (!color_grads) return fail(EFGS_ERR_ALLOC, "allocation of the colour gradient buffer failed");
     a.color_grads = color_grads;
+    a.color_grad_max = reinterpret_cast<uint32_t*>(color_grads + static_cast<size_t>(n) * 4);
+    if (!launch_fill_u32(a.color_grad_max, 0u, 1, s)) return EFGS_ERR_HIP;
     t.begin(EFGS_STAGE_PREPROCESS_BACKWARD, s);
     if (!launch_rtc(k, chunks, preprocess_block, 0u, &a, s)) return EFGS_ERR_HIP;
     t.end(s);

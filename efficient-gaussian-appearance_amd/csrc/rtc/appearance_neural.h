@@ -22,6 +22,9 @@ namespace efgs {
 
 namespace nn {
 
+#ifndef EFGS_MLP_U_LDS
+#define EFGS_MLP_U_LDS 0
+#endif
 constexpr uint32_t IN = EFGS_MLP_N_IN;            // unpadded input width
 constexpr uint32_t INP = EFGS_MLP_N_IN_PADDED;    // padded to a multiple of 16
 constexpr uint32_t NN = EFGS_MLP_N_NEURONS;
@@ -192,12 +195,6 @@ __device__ inline float3 direction_grad(float3 d, uint32_t degree, const float* 
     return g;
 }
 
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
 // ---- dual-orientation MLP of the backward kernel --------------------------------------------------------
 //
 // Tile sets of a (F x 64 primitives) matrix M held by a wave (lane = r + 16 q):
@@ -228,6 +225,14 @@ constexpr uint32_t XS = INP + 4;        // staging row of the input / output-gra
 constexpr uint32_t YS = OUTP + 4;
 constexpr uint32_t FS = INP + 4;        // staging row of the input-gradient rows (floats)
 constexpr uint32_t DUAL_STAGE_BYTES = 64 * FS * 4;  // per wave; also covers 64 rows of XS or YS halves
+// With EFGS_MLP_U_LDS the primitive-rows input tiles of the hidden layers (U[1..NH]) wait for the backward in a
+// per-wave LDS store (one 8-byte slot per lane and tile, written and read by the same lane) instead of
+// registers; the host sets it when the store fits the block's LDS.
+constexpr uint32_t U_TILES = (NN / 16) * 4;
+constexpr uint32_t U_STORE_BYTES = EFGS_MLP_U_LDS ? NH * U_TILES * 64 * 8 : 0u;  // per wave
+__device__ __forceinline__ uint32_t u_slot(uint32_t l, uint32_t pb, uint32_t fb, uint32_t lane) {
+    return (((l - 1) * U_TILES + pb * (NN / 16) + fb) * 64 + lane);
+}
 
 // copies the flat tcnn-layout weights (fp16 bits) into the padded W / W^T layout (whole block)
 __device__ inline void load_dual_weights(const uint16_t* g, uint16_t* WL, uint32_t tid, uint32_t n_threads) {
@@ -242,9 +247,11 @@ __device__ inline void load_dual_weights(const uint16_t* g, uint16_t* WL, uint32
     }
 }
 
+// ReLU of an fp32 tile, rounded to fp16 (round to nearest even, then a packed max with zero)
 __device__ __forceinline__ h4 relu_h4(f4 v) {
-    return h4{static_cast<_Float16>(fmaxf(v[0], 0.0f)), static_cast<_Float16>(fmaxf(v[1], 0.0f)), static_cast<_Float16>(fmaxf(v[2], 0.0f)),
-              static_cast<_Float16>(fmaxf(v[3], 0.0f))};
+    const h4 x = __builtin_convertvector(v, h4);
+    return __builtin_elementwise_max(x, h4{static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f), static_cast<_Float16>(0.0f),
+                                           static_cast<_Float16>(0.0f)});
 }
 
 // v where the activation is positive (ReLU derivative), as fp16
@@ -273,7 +280,7 @@ __device__ __forceinline__ h4 masked_h4_bits(f4 v, uint32_t bits) {
 // as primitive-rows tiles, and Tm[l] (l >= 1), the ReLU masks of the feature-rows tiles.
 template <bool DUAL>
 __device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, const float* x, uint32_t (&Tm)[NL][MASK_WORDS], h4 (&U)[NL][4][KT],
-                                         float* y, uint32_t lane) {
+                                         h4* ustore, float* y, uint32_t lane) {
     h4 T[NL][KT][4];
     const uint32_t r = lane & 15u, q = lane >> 4;
 #pragma unroll
@@ -310,7 +317,10 @@ __device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, co
                     f4 u = f4_zero();
 #pragma unroll
                     for (uint32_t ib = 0; ib < lin(l) / 16; ib++) u = mfma(T[l][ib][pb], wa[ib], u);  // H^T(pb, ob) = sum M^T(pb, ib) W^T(ib, ob)
-                    U[l + 1][pb][ob] = relu_h4(u);
+                    if (EFGS_MLP_U_LDS)
+                        ustore[u_slot(l + 1, pb, ob, lane)] = relu_h4(u);
+                    else
+                        U[l + 1][pb][ob] = relu_h4(u);
                 } else if (ob == 0) {
                     yt[pb] = t;
                 }
@@ -345,17 +355,19 @@ __device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, co
 }
 
 // Backward through the MLP from the lanes' output gradients dy (zero for lanes that do not contribute), with
-// Tm / U from mlp_forward_tiles<true>. Writes the lane's input gradient row dx (INP floats) and adds the wave's weight
-// gradients to dW (lane layout of the D operand: dW[l][ob][ib][i] = dW_l[16 ob + 4 q + i][16 ib + r]).
+// Tm / U from mlp_forward_tiles<true>. The gradients run through the fp16 MFMAs scaled by s (a power of two
+// that keeps them in fp16 range; the caller picks it from a bound on |dy| over the whole launch). Writes the
+// lane's input gradient row dx (INP floats, unscaled) and adds the wave's weight gradients, still scaled by s,
+// to dW (MFMA accumulators, lane layout of the D operand: dW[l][ob][ib][i] = s dW_l[16 ob + 4 q + i][16 ib + r]).
 __device__ inline void mlp_backward_dual(const _Float16* WL, _Float16* stage, const uint32_t (&Tm)[NL][MASK_WORDS], const h4 (&U)[NL][4][KT],
-                                         const float* dy, float* dx, f4 (&dW)[NL][NT > 1 ? NT : 1][KT], uint32_t lane) {
+                                         const h4* ustore, const float* dy, float s, float inv_s, float* dx, f4 (&dW)[NL][NT > 1 ? NT : 1][KT],
+                                         uint32_t lane) {
+    // primitive-rows input tile (pb, fb) of layer l
+    auto u_tile = [&](uint32_t l, uint32_t pb, uint32_t fb) -> h4 { return (EFGS_MLP_U_LDS && l > 0) ? ustore[u_slot(l, pb, fb, lane)] : U[l][pb][fb]; };
     const uint32_t r = lane & 15u, q = lane >> 4;
-    const float m = wave_max_f32(fmaxf(fmaxf(fabsf(dy[0]), fabsf(dy[1])), fabsf(dy[2])));
 #pragma unroll
     for (uint32_t k = 0; k < INP; k++) dx[k] = 0.0f;
-    if (!(m > 0.0f) || !(m < 3.0e38f)) return;  // wave-uniform
-    const int e = max(ilogbf(m), -110);  // keeps the scale 2^(8 - e) finite for denormal maxima
-    const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
+    if (__ballot(dy[0] != 0.0f || dy[1] != 0.0f || dy[2] != 0.0f) == 0) return;  // wave-uniform
 
     // output-layer gradient (16 padded outputs x 64 primitives) in both orientations, through LDS
     const _Float16 z = static_cast<_Float16>(0.0f);
@@ -373,77 +385,68 @@ __device__ inline void mlp_backward_dual(const _Float16* WL, _Float16* stage, co
     }
     wave_sync();
 
+    // output layer: dW_NH(0, ib) += sum_pb dY(0, pb) M_NH(ib, pb)^T (dY as primitive-rows A operand)
 #pragma unroll
-    for (int li = static_cast<int>(NH); li >= 0; li--) {
+    for (uint32_t ib = 0; ib < lin(NH) / 16; ib++) {
+#pragma unroll
+        for (uint32_t pb = 0; pb < 4; pb++) dW[NH][0][ib] = mfma(GT[pb][0], u_tile(NH, pb, ib), dW[NH][0][ib]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int li = static_cast<int>(NH); li >= 1; li--) {
         const uint32_t l = static_cast<uint32_t>(li);
-        // weight gradient dW_l(ob, ib) += sum_pb dOut(ob, pb) M_l(ib, pb)^T
+        // input gradient of layer l in both orientations, through the ReLU of its input; each primitive-rows tile
+        // goes straight into layer l-1's weight gradient (dW_{l-1}(ib, jb) += sum_pb dIn(ib, pb) M_{l-1}(jb, pb)^T)
+        h4 Gn[KT][4];
 #pragma unroll
-        for (uint32_t ob = 0; ob < lout(l) / 16; ob++)
+        for (uint32_t ib = 0; ib < lin(l) / 16; ib++) {
+            h4 wt[KT];
 #pragma unroll
-            for (uint32_t ib = 0; ib < lin(l) / 16; ib++) {
-                f4 t = f4_zero();
+            for (uint32_t ob = 0; ob < lout(l) / 16; ob++)
+                wt[ob] = *reinterpret_cast<const h4*>(&WL[wtoff(l) + (16 * ib + r) * wtrow(l) + 16 * ob + 4 * q]);
 #pragma unroll
-                for (uint32_t pb = 0; pb < 4; pb++) t = mfma(GT[pb][ob], U[l][pb][ib], t);
+            for (uint32_t pb = 0; pb < 4; pb++) {
+                f4 t = f4_zero(), u = f4_zero();
 #pragma unroll
-                for (uint32_t i = 0; i < 4; i++) dW[l][ob][ib][i] = __builtin_fmaf(t[i], inv_s, dW[l][ob][ib][i]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        if (l > 0) {
-            // input gradient in both orientations, through the ReLU of layer l's input
-            h4 Gn[KT][4], GTn[4][KT];
-#pragma unroll
-            for (uint32_t ib = 0; ib < lin(l) / 16; ib++) {
-                h4 wt[KT];
-#pragma unroll
-                for (uint32_t ob = 0; ob < lout(l) / 16; ob++)
-                    wt[ob] = *reinterpret_cast<const h4*>(&WL[wtoff(l) + (16 * ib + r) * wtrow(l) + 16 * ob + 4 * q]);
-#pragma unroll
-                for (uint32_t pb = 0; pb < 4; pb++) {
-                    f4 t = f4_zero(), u = f4_zero();
-#pragma unroll
-                    for (uint32_t ob = 0; ob < lout(l) / 16; ob++) {
-                        t = mfma(wt[ob], G[ob][pb], t);   // dIn(ib, pb) = sum W^T(ib, ob) dOut(ob, pb)
-                        u = mfma(G[ob][pb], wt[ob], u);   // dIn^T(pb, ib) = sum dOut^T(pb, ob) W(ob, ib)
-                    }
-                    const uint32_t ti = ib * 4 + pb;
-                    Gn[ib][pb] = masked_h4_bits(t, (Tm[l][ti / 8] >> (4 * (ti % 8))) & 15u);
-                    GTn[pb][ib] = masked_h4(u, U[l][pb][ib]);
+                for (uint32_t ob = 0; ob < lout(l) / 16; ob++) {
+                    t = mfma(wt[ob], G[ob][pb], t);   // dIn(ib, pb) = sum W^T(ib, ob) dOut(ob, pb)
+                    u = mfma(G[ob][pb], wt[ob], u);   // dIn^T(pb, ib) = sum dOut^T(pb, ob) W(ob, ib)
                 }
-                __builtin_amdgcn_sched_barrier(0);  // one input block in flight: bounds the live accumulators
+                const uint32_t ti = ib * 4 + pb;
+                Gn[ib][pb] = masked_h4_bits(t, (Tm[l][ti / 8] >> (4 * (ti % 8))) & 15u);
+                const h4 gt = masked_h4(u, u_tile(l, pb, ib));
+#pragma unroll
+                for (uint32_t jb = 0; jb < lin(l - 1) / 16; jb++) dW[l - 1][ib][jb] = mfma(gt, u_tile(l - 1, pb, jb), dW[l - 1][ib][jb]);
             }
+            __builtin_amdgcn_sched_barrier(0);  // one input block in flight: bounds the live accumulators
+        }
 #pragma unroll
-            for (uint32_t ib = 0; ib < lin(l) / 16; ib++)
+        for (uint32_t ib = 0; ib < lin(l) / 16; ib++)
 #pragma unroll
-                for (uint32_t pb = 0; pb < 4; pb++) {
-                    G[ib][pb] = Gn[ib][pb];
-                    GT[pb][ib] = GTn[pb][ib];
-                }
-        } else {
-            // input gradient rows (feature-rows tiles, unscaled) to the lanes through LDS
-            float* fs = reinterpret_cast<float*>(stage);
+            for (uint32_t pb = 0; pb < 4; pb++) G[ib][pb] = Gn[ib][pb];
+    }
+    // input gradient rows (feature-rows tiles, unscaled) to the lanes through LDS
+    float* fs = reinterpret_cast<float*>(stage);
 #pragma unroll
-            for (uint32_t ib = 0; ib < INP / 16; ib++) {
-                h4 wt[KT];
+    for (uint32_t ib = 0; ib < INP / 16; ib++) {
+        h4 wt[KT];
 #pragma unroll
-                for (uint32_t ob = 0; ob < lout(0) / 16; ob++)
-                    wt[ob] = *reinterpret_cast<const h4*>(&WL[wtoff(0) + (16 * ib + r) * wtrow(0) + 16 * ob + 4 * q]);
+        for (uint32_t ob = 0; ob < lout(0) / 16; ob++) wt[ob] = *reinterpret_cast<const h4*>(&WL[wtoff(0) + (16 * ib + r) * wtrow(0) + 16 * ob + 4 * q]);
 #pragma unroll
-                for (uint32_t pb = 0; pb < 4; pb++) {
-                    f4 t = f4_zero();
+        for (uint32_t pb = 0; pb < 4; pb++) {
+            f4 t = f4_zero();
 #pragma unroll
-                    for (uint32_t ob = 0; ob < lout(0) / 16; ob++) t = mfma(wt[ob], G[ob][pb], t);
-                    *reinterpret_cast<float4*>(&fs[(16 * pb + r) * FS + 16 * ib + 4 * q]) = make_float4(t[0] * inv_s, t[1] * inv_s, t[2] * inv_s, t[3] * inv_s);
-                }
-            }
-            wave_sync();
-#pragma unroll
-            for (uint32_t k = 0; k < INP; k += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(&fs[lane * FS + k]);
-                dx[k] = v.x; dx[k + 1] = v.y; dx[k + 2] = v.z; dx[k + 3] = v.w;
-            }
-            wave_sync();
+            for (uint32_t ob = 0; ob < lout(0) / 16; ob++) t = mfma(wt[ob], G[ob][pb], t);
+            *reinterpret_cast<float4*>(&fs[(16 * pb + r) * FS + 16 * ib + 4 * q]) = make_float4(t[0] * inv_s, t[1] * inv_s, t[2] * inv_s, t[3] * inv_s);
         }
     }
+    wave_sync();
+#pragma unroll
+    for (uint32_t k = 0; k < INP; k += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&fs[lane * FS + k]);
+        dx[k] = v.x; dx[k + 1] = v.y; dx[k + 2] = v.z; dx[k + 3] = v.w;
+    }
+    wave_sync();
 }
 
 }  // namespace nn

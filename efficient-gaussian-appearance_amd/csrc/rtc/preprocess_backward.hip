@@ -233,21 +233,34 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
 // the MLP's view-direction and base-input terms to g_means and g_base and writes the latent gradients.
 extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
     using namespace efgs;
+    __shared__ uint32_t s_max;
+    if (threadIdx.x == 0) s_max = 0u;
+    __syncthreads();
     const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
-    if (p >= a.n) return;
-    const uint32_t touched = a.n_touched[p];
-    if (touched == 0) {
-        zero_primitive(a, p);
-        return;
+    float m = 0.0f;
+    if (p < a.n) {
+        const uint32_t touched = a.n_touched[p];
+        if (touched == 0) {
+            zero_primitive(a, p);
+        } else {
+            const InstanceGrads ig = reduce_instance_grads(a, p, touched);
+            const PrimRecord rec = a.records[p];
+            const float3 dpre = pre_activation_grad(rec, ig);
+            write_base_grad(a, p, dpre, make_float3(0.0f, 0.0f, 0.0f));
+            if (a.cam.degree == 0)
+                for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
+            geometry_backward(a, p, rec, ig, make_float3(0.0f, 0.0f, 0.0f));
+            reinterpret_cast<float4*>(a.color_grads)[p] = make_float4(dpre.x, dpre.y, dpre.z, 0.0f);
+            m = fmaxf(fmaxf(fabsf(dpre.x), fabsf(dpre.y)), fabsf(dpre.z));
+        }
     }
-    const InstanceGrads ig = reduce_instance_grads(a, p, touched);
-    const PrimRecord rec = a.records[p];
-    const float3 dpre = pre_activation_grad(rec, ig);
-    write_base_grad(a, p, dpre, make_float3(0.0f, 0.0f, 0.0f));
-    if (a.cam.degree == 0)
-        for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
-    geometry_backward(a, p, rec, ig, make_float3(0.0f, 0.0f, 0.0f));
-    reinterpret_cast<float4*>(a.color_grads)[p] = make_float4(dpre.x, dpre.y, dpre.z, 0.0f);
+    // bound for the MLP kernel's gradient scale: the residual activations' derivatives are at most 1, so
+    // |dL/d(MLP output)| <= max |dpre|; non-negative float bits order like the floats (integer max)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63u) == 0) atomicMax(&s_max, __float_as_uint(m));
+    __syncthreads();
+    if (threadIdx.x == 0 && s_max != 0u) atomicMax(a.color_grad_max, s_max);
 }
 
 // The MLP backward (launched only when the residual is on). Persistent grid: every wave recomputes the MLP
@@ -261,6 +274,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _ml
     extern __shared__ __align__(16) unsigned char smem[];
     const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
     _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES + wave * nn::DUAL_STAGE_BYTES);
+    nn::h4* ustore = reinterpret_cast<nn::h4*>(smem + nn::DUAL_WEIGHT_BYTES + 4 * nn::DUAL_STAGE_BYTES + wave * nn::U_STORE_BYTES);
     nn::load_dual_weights(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x, preprocess_block);
     __syncthreads();
 
@@ -273,6 +287,12 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _ml
             for (uint32_t cb = 0; cb < nn::KT; cb++) dW[l][rb][cb] = nn::f4_zero();
 
     const uint32_t degree = a.cam.degree;
+    // one gradient scale for the launch: 2^(8 - e) with e the exponent of the largest |dL/d(MLP output)| bound
+    const float gmax = __uint_as_float(*a.color_grad_max);
+    // (scale 1 when the bound is zero or not finite: non-finite gradients then propagate as they are)
+    const bool finite = gmax > 0.0f && gmax < 3.0e38f;
+    const int e = finite ? max(ilogbf(gmax), -110) : 8;  // the clamp keeps 2^(8 - e) finite for denormal maxima
+    const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
     const uint32_t n_chunks = (a.n + preprocess_block - 1) / preprocess_block;
     for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
         const uint32_t p_raw = chunk * preprocess_block + threadIdx.x;
@@ -295,13 +315,13 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _ml
         uint32_t Tm[nn::NL][nn::MASK_WORDS];
         nn::h4 U[nn::NL][4][nn::KT];
         float y[3];
-        nn::mlp_forward_tiles<true>(WL, stage, x, Tm, U, y, lane);
+        nn::mlp_forward_tiles<true>(WL, stage, x, Tm, U, ustore, y, lane);
         float dy[3];
         dy[0] = dpre.x * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[0]));
         dy[1] = dpre.y * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[1]));
         dy[2] = dpre.z * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[2]));
         float dx[nn::INP];
-        nn::mlp_backward_dual(WL, stage, Tm, U, dy, dx, dW, lane);
+        nn::mlp_backward_dual(WL, stage, Tm, U, ustore, dy, s, inv_s, dx, dW, lane);
         if (contributes) {
             float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
 #pragma unroll
@@ -334,7 +354,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _ml
 #pragma unroll
                         for (uint32_t i = 0; i < 4; i++) {
                             const uint32_t idx = nn::loff(l) + (rb * 16 + 4 * q + i) * nn::lin(l) + cb * 16 + r;
-                            red[idx] = (w == 0 ? 0.0f : red[idx]) + dW[l][rb][cb][i];
+                            red[idx] = (w == 0 ? 0.0f : red[idx]) + dW[l][rb][cb][i] * inv_s;
                         }
         }
         __syncthreads();

@@ -196,7 +196,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             uint32_t masks[nn::NL][nn::MASK_WORDS];
             nn::h4 unused[nn::NL][4][nn::KT];
             float y[3];
-            nn::mlp_forward_tiles<false>(WL, stage, x, masks, unused, y, lane);
+            nn::mlp_forward_tiles<false>(WL, stage, x, masks, unused, nullptr, y, lane);
             res = make_float3(residual_activation<EFGS_RES_ACT>(y[0]), residual_activation<EFGS_RES_ACT>(y[1]),
                               residual_activation<EFGS_RES_ACT>(y[2]));
         }
