@@ -267,7 +267,10 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
 // forward for its 64 primitives in both tile orientations, backpropagates with fp16 MFMA without LDS
 // transposes, keeps its weight gradients in fp32 registers across chunks; the block sums its four waves in a
 // fixed order into one partial per block.
-extern "C" __global__ __launch_bounds__(256) void EFGS_CAT(EFGS_KERNEL_NAME, _mlp)(efgs::PreprocessBackwardArgs a) {
+// With the hidden activations in LDS the kernel fits 256 VGPRs: the bound of two waves per SIMD keeps every
+// MFMA result in VGPRs (accumulator registers would cost a move per element before each conversion); the
+// occupancy itself is set by the LDS, one block per CU.
+extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_CAT(EFGS_KERNEL_NAME, _mlp)(efgs::PreprocessBackwardArgs a) {
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
