@@ -321,13 +321,15 @@ uint32_t mlp_smem_forward(const MlpShape& m) { return mlp_dual_weight_bytes(m) +
 // (n_in_padded + 4) floats; the area is reused for the fp32 block reduction of the weight gradients
 constexpr uint32_t max_dynamic_lds = 160 * 1024;  // gfx950: 160 KiB of LDS per block
 
-// per-wave LDS store of the hidden layers' primitive-rows input tiles (one 8-byte slot per lane and tile)
-uint32_t mlp_u_store_bytes(const MlpShape& m) { return m.n_hidden * (m.n_neurons / 16) * 4 * 64 * 8; }
+// per-wave LDS store of hidden layers 2..n_hidden's primitive-rows input tiles (one 8-byte slot per lane and
+// tile; layer 1's are recomputed from the input tiles)
+uint32_t mlp_u_store_bytes(const MlpShape& m) { return (m.n_hidden > 1 ? m.n_hidden - 1 : 0u) * (m.n_neurons / 16) * 4 * 64 * 8; }
 
 uint32_t mlp_smem_backward_base(const MlpShape& m) { return mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 4; }
 
-// the backward's MLP kernel keeps those tiles in LDS when the store fits next to the weights and staging
-bool mlp_u_in_lds(const MlpShape& m) { return mlp_smem_backward_base(m) + 4 * mlp_u_store_bytes(m) <= max_dynamic_lds; }
+// the backward's MLP kernel keeps those tiles out of its registers when two blocks still fit a CU's LDS
+// (the kernel is then built for two waves per SIMD)
+bool mlp_u_in_lds(const MlpShape& m) { return 2 * (mlp_smem_backward_base(m) + 4 * mlp_u_store_bytes(m)) <= max_dynamic_lds; }
 
 uint32_t mlp_smem_backward(const MlpShape& m) {
     const uint32_t f = mlp_smem_backward_base(m) + (mlp_u_in_lds(m) ? 4 * mlp_u_store_bytes(m) : 0u);

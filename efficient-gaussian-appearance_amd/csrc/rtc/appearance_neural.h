@@ -225,13 +225,14 @@ constexpr uint32_t XS = INP + 4;        // staging row of the input / output-gra
 constexpr uint32_t YS = OUTP + 4;
 constexpr uint32_t FS = INP + 4;        // staging row of the input-gradient rows (floats)
 constexpr uint32_t DUAL_STAGE_BYTES = 64 * FS * 4;  // per wave; also covers 64 rows of XS or YS halves
-// With EFGS_MLP_U_LDS the primitive-rows input tiles of the hidden layers (U[1..NH]) wait for the backward in a
-// per-wave LDS store (one 8-byte slot per lane and tile, written and read by the same lane) instead of
-// registers; the host sets it when the store fits the block's LDS.
+// With EFGS_MLP_U_LDS the primitive-rows input tiles of the hidden layers wait for the backward outside the
+// registers: U[1] is recomputed from the staged input tiles where it is used (one MFMA per tile for a 16-wide
+// input), U[2..NH] sit in a per-wave LDS store (one 8-byte slot per lane and tile, written and read by the
+// same lane). The host sets it when the store fits two blocks' LDS per CU.
 constexpr uint32_t U_TILES = (NN / 16) * 4;
-constexpr uint32_t U_STORE_BYTES = EFGS_MLP_U_LDS ? NH * U_TILES * 64 * 8 : 0u;  // per wave
+constexpr uint32_t U_STORE_BYTES = EFGS_MLP_U_LDS ? (NH > 1 ? NH - 1 : 0u) * U_TILES * 64 * 8 : 0u;  // per wave
 __device__ __forceinline__ uint32_t u_slot(uint32_t l, uint32_t pb, uint32_t fb, uint32_t lane) {
-    return (((l - 1) * U_TILES + pb * (NN / 16) + fb) * 64 + lane);
+    return (((l - 2) * U_TILES + pb * (NN / 16) + fb) * 64 + lane);
 }
 
 // copies the flat tcnn-layout weights (fp16 bits) into the padded W / W^T layout (whole block)
@@ -280,7 +281,7 @@ __device__ __forceinline__ h4 masked_h4_bits(f4 v, uint32_t bits) {
 // as primitive-rows tiles, and Tm[l] (l >= 1), the ReLU masks of the feature-rows tiles.
 template <bool DUAL>
 __device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, const float* x, uint32_t (&Tm)[NL][MASK_WORDS], h4 (&U)[NL][4][KT],
-                                         h4* ustore, float* y, uint32_t lane) {
+                                         h4 (&X)[INP / 16][4], h4* ustore, float* y, uint32_t lane) {
     h4 T[NL][KT][4];
     const uint32_t r = lane & 15u, q = lane >> 4;
 #pragma unroll
@@ -313,7 +314,7 @@ __device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, co
                 for (uint32_t ib = 0; ib < lin(l) / 16; ib++) t = mfma(wa[ib], T[l][ib][pb], t);  // H(ob, pb) = sum W(ob, ib) M(ib, pb)
                 if (l < NH) {
                     T[l + 1][ob][pb] = relu_h4(t);
-                    if (!DUAL) continue;
+                    if (!DUAL || (EFGS_MLP_U_LDS && l == 0)) continue;  // U[1] is recomputed where it is used
                     f4 u = f4_zero();
 #pragma unroll
                     for (uint32_t ib = 0; ib < lin(l) / 16; ib++) u = mfma(T[l][ib][pb], wa[ib], u);  // H^T(pb, ob) = sum M^T(pb, ib) W^T(ib, ob)
@@ -341,6 +342,10 @@ __device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, co
     }
     if (!DUAL) return;
 #pragma unroll
+    for (uint32_t ib = 0; ib < INP / 16; ib++)
+#pragma unroll
+        for (uint32_t pb = 0; pb < 4; pb++) X[ib][pb] = T[0][ib][pb];
+#pragma unroll
     for (uint32_t l = 1; l < NL; l++) {
 #pragma unroll
         for (uint32_t w = 0; w < MASK_WORDS; w++) Tm[l][w] = 0u;
@@ -360,10 +365,18 @@ __device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, co
 // lane's input gradient row dx (INP floats, unscaled) and adds the wave's weight gradients, still scaled by s,
 // to dW (MFMA accumulators, lane layout of the D operand: dW[l][ob][ib][i] = s dW_l[16 ob + 4 q + i][16 ib + r]).
 __device__ inline void mlp_backward_dual(const _Float16* WL, _Float16* stage, const uint32_t (&Tm)[NL][MASK_WORDS], const h4 (&U)[NL][4][KT],
-                                         const h4* ustore, const float* dy, float s, float inv_s, float* dx, f4 (&dW)[NL][NT > 1 ? NT : 1][KT],
-                                         uint32_t lane) {
+                                         const h4 (&X)[INP / 16][4], const h4* ustore, const float* dy, float s, float inv_s, float* dx,
+                                         f4 (&dW)[NL][NT > 1 ? NT : 1][KT], uint32_t lane) {
     // primitive-rows input tile (pb, fb) of layer l
-    auto u_tile = [&](uint32_t l, uint32_t pb, uint32_t fb) -> h4 { return (EFGS_MLP_U_LDS && l > 0) ? ustore[u_slot(l, pb, fb, lane)] : U[l][pb][fb]; };
+    auto u_tile = [&](uint32_t l, uint32_t pb, uint32_t fb) -> h4 {
+        if (!EFGS_MLP_U_LDS || l == 0) return U[l][pb][fb];
+        if (l >= 2) return ustore[u_slot(l, pb, fb, lane)];
+        f4 u = f4_zero();  // U[1](pb, fb) = ReLU(sum_ib X^T(pb, ib) W_0^T(ib, fb))
+#pragma unroll
+        for (uint32_t ib = 0; ib < INP / 16; ib++)
+            u = mfma(X[ib][pb], *reinterpret_cast<const h4*>(&WL[woff(0) + (16 * fb + (lane & 15u)) * wrow(0) + 16 * ib + 4 * (lane >> 4)]), u);
+        return relu_h4(u);
+    };
     const uint32_t r = lane & 15u, q = lane >> 4;
 #pragma unroll
     for (uint32_t k = 0; k < INP; k++) dx[k] = 0.0f;

@@ -317,14 +317,15 @@ extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_C
         }
         uint32_t Tm[nn::NL][nn::MASK_WORDS];
         nn::h4 U[nn::NL][4][nn::KT];
+        nn::h4 X[nn::INP / 16][4];
         float y[3];
-        nn::mlp_forward_tiles<true>(WL, stage, x, Tm, U, ustore, y, lane);
+        nn::mlp_forward_tiles<true>(WL, stage, x, Tm, U, X, ustore, y, lane);
         float dy[3];
         dy[0] = dpre.x * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[0]));
         dy[1] = dpre.y * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[1]));
         dy[2] = dpre.z * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[2]));
         float dx[nn::INP];
-        nn::mlp_backward_dual(WL, stage, Tm, U, ustore, dy, s, inv_s, dx, dW, lane);
+        nn::mlp_backward_dual(WL, stage, Tm, U, X, ustore, dy, s, inv_s, dx, dW, lane);
         if (contributes) {
             float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
 #pragma unroll

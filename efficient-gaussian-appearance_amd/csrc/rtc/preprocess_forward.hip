@@ -195,8 +195,9 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             nn::mlp_input(rp, a.base + 3 * p, d, a.cam.degree, x);
             uint32_t masks[nn::NL][nn::MASK_WORDS];
             nn::h4 unused[nn::NL][4][nn::KT];
+            nn::h4 unused_x[nn::INP / 16][4];
             float y[3];
-            nn::mlp_forward_tiles<false>(WL, stage, x, masks, unused, nullptr, y, lane);
+            nn::mlp_forward_tiles<false>(WL, stage, x, masks, unused, unused_x, nullptr, y, lane);
             res = make_float3(residual_activation<EFGS_RES_ACT>(y[0]), residual_activation<EFGS_RES_ACT>(y[1]),
                               residual_activation<EFGS_RES_ACT>(y[2]));
         }
