@@ -789,11 +789,10 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     }
     if (!grads->mlp_weights) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp weight gradient output is required");
     const uint32_t params = mlp_params(mlp_shape(r));
-    float* color_grads = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(n) * 4 * sizeof(float) + 256));
+    float* color_grads = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(n) * 4 * sizeof(float) + static_cast<size_t>(chunks) * 4));
     if (!color_grads) return fail(EFGS_ERR_ALLOC, "allocation of the colour gradient buffer failed");
     a.color_grads = color_grads;
-    a.color_grad_max = reinterpret_cast<uint32_t*>(color_grads + static_cast<size_t>(n) * 4);
-    if (!launch_fill_u32(a.color_grad_max, 0u, 1, s)) return EFGS_ERR_HIP;
+    a.color_grad_max = reinterpret_cast<uint32_t*>(color_grads + static_cast<size_t>(n) * 4);  // one entry per geometry block
     t.begin(EFGS_STAGE_PREPROCESS_BACKWARD, s);
     if (!launch_rtc(k, chunks, preprocess_block, 0u, &a, s)) return EFGS_ERR_HIP;
     t.end(s);

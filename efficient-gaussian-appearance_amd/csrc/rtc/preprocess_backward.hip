@@ -260,7 +260,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if ((threadIdx.x & 63u) == 0) atomicMax(&s_max, __float_as_uint(m));
     __syncthreads();
-    if (threadIdx.x == 0 && s_max != 0u) atomicMax(a.color_grad_max, s_max);
+    if (threadIdx.x == 0) a.color_grad_max[blockIdx.x] = s_max;
 }
 
 // The MLP backward (launched only when the residual is on). Persistent grid: every wave recomputes the MLP
@@ -291,7 +291,21 @@ extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_C
 
     const uint32_t degree = a.cam.degree;
     // one gradient scale for the launch: 2^(8 - e) with e the exponent of the largest |dL/d(MLP output)| bound
-    const float gmax = __uint_as_float(*a.color_grad_max);
+    // (every block reduces the geometry kernel's per-block maxima itself: a few loads per thread)
+    __shared__ uint32_t s_wave_max[preprocess_block / 64];
+    {
+        const uint32_t n_geometry_blocks = (a.n + preprocess_block - 1) / preprocess_block;
+        uint32_t m = 0u;
+        for (uint32_t b = threadIdx.x; b < n_geometry_blocks; b += preprocess_block) m = max(m, a.color_grad_max[b]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o)));
+        if (lane == 0) s_wave_max[wave] = m;
+        __syncthreads();
+    }
+    uint32_t gbits = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < preprocess_block / 64; w++) gbits = max(gbits, s_wave_max[w]);
+    const float gmax = __uint_as_float(gbits);
     // (scale 1 when the bound is zero or not finite: non-finite gradients then propagate as they are)
     const bool finite = gmax > 0.0f && gmax < 3.0e38f;
     const int e = finite ? max(ilogbf(gmax), -110) : 8;  // the clamp keeps 2^(8 - e) finite for denormal maxima
