@@ -92,18 +92,19 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
             while (mask != 0) {
                 const uint32_t jj = c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
                 mask &= mask - 1;
-                if (done) continue;
+                // branch-free: a skipped Gaussian gets weight 0, which leaves C and T bit for bit unchanged
                 float dx, dy, G;
                 const float alpha = eval_alpha(s_xy[jj], s_co[jj], pxf, pyf, dx, dy, G);
-                if (alpha < min_alpha) continue;
-                const float w = T * alpha;
+                const bool take = !done && alpha >= min_alpha;
+                const float a_t = take ? alpha : 0.0f;
+                const float w = T * a_t;
                 const float4 col = s_col[jj];
                 cr = __builtin_fmaf(w, col.x, cr);
                 cg = __builtin_fmaf(w, col.y, cg);
                 cb = __builtin_fmaf(w, col.z, cb);
-                T = T * (1.0f - alpha);
-                last = start + jj + 1;
-                if (T < transmittance_threshold) done = true;
+                T = T * (1.0f - a_t);
+                last = take ? start + jj + 1 : last;
+                done = done || (take && T < transmittance_threshold);
             }
         }
     }

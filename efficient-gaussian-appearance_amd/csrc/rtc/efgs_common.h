@@ -96,12 +96,12 @@ __device__ inline float ef_logf(float x) {
 }
 
 // 2^x for x <= 0 (the blend's Gaussian factor): x = k + r with k = rint(x) and |r| <= 1/2 (r exact), 2^r by its
-// degree-7 Taylor series in r ln2 evaluated with fused multiply-adds, scaled by 2^k; 0 below -126, where
-// alpha = opacity * 2^x is far under the 1/255 threshold.
+// degree-7 Taylor series in r ln2 evaluated with fused multiply-adds, scaled by 2^k. x is first clamped to
+// -127 (NaN too), whose k = -127 gives the scale bits 0 and so the result 0 with no select or branch; alpha =
+// opacity * 2^x is far under the 1/255 threshold there.
 __device__ inline float ef_exp2f(float x) {
 #pragma clang fp contract(off)
-    const bool in_range = x >= -126.0f;  // below: 0 (evaluated branch-free; the polynomial result is discarded)
-    if (!in_range) x = 0.0f;
+    x = __builtin_fmaxf(x, -127.0f);
     const float k = __builtin_rintf(x);
     const float r = x - k;
     float p = __builtin_fmaf(1.52527338e-05f, r, 1.54035304e-04f);
@@ -111,7 +111,7 @@ __device__ inline float ef_exp2f(float x) {
     p = __builtin_fmaf(p, r, 2.40226507e-01f);
     p = __builtin_fmaf(p, r, 6.93147181e-01f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return in_range ? p * ef_pow2i(static_cast<int>(k)) : 0.0f;
+    return p * __uint_as_float(static_cast<uint32_t>(static_cast<int>(k) + 127) << 23);
 }
 
 __device__ __forceinline__ float ef_sigmoid(float x) {

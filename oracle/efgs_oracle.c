@@ -107,10 +107,10 @@ float ef_logf(float x) {
 
 static float ef_sigmoid(float x) { return 1.0f / (1.0f + ef_expf(-x)); }
 
-/* 2^x for x <= 0: k = rint(x), r = x - k exact, degree-7 Taylor series of 2^r in r ln2 with fused
- * multiply-adds, scaled by 2^k; 0 below -126. */
+/* 2^x for x <= 0: x clamped to -127 (NaN too), k = rint(x), r = x - k exact, degree-7 Taylor series of 2^r
+ * in r ln2 with fused multiply-adds, scaled by 2^k built from its exponent bits (k = -127 gives 0). */
 float ef_exp2f(float x) {
-    if (!(x >= -126.0f)) return 0.0f;
+    x = fmaxf(x, -127.0f);
     const float k = rintf(x);
     const float r = x - k;
     float p = fmaf(1.52527338e-05f, r, 1.54035304e-04f);
@@ -120,7 +120,10 @@ float ef_exp2f(float x) {
     p = fmaf(p, r, 2.40226507e-01f);
     p = fmaf(p, r, 6.93147181e-01f);
     p = fmaf(p, r, 1.0f);
-    return p * ef_pow2i((int)k);
+    uint32_t bits = (uint32_t)((int)k + 127) << 23;
+    float scale;
+    memcpy(&scale, &bits, sizeof scale);
+    return p * scale;
 }
 
 /* exponent of the exp2-scaled conic (ex, ey, ez) at offset (dx, dy), with two fused multiply-adds: the

@@ -57,6 +57,10 @@ def test_ef_exp2_accuracy():
     assert O.ef_exp2(0.0) == 1.0
     assert O.ef_exp2(-1.0) == 0.5
     assert O.ef_exp2(-127.0) == 0.0
+    assert O.ef_exp2(-1000.0) == 0.0 and O.ef_exp2(float("nan")) == 0.0 and O.ef_exp2(-math.inf) == 0.0
+    # just below -126: the subnormal 2^x (p in (0.7, 1) times 2^-126), rounded once
+    sub = O.ef_exp2(-126.25)
+    assert 0.0 < sub < 2.0 ** -126 and abs(sub - 2.0 ** -126.25) <= 2.0 ** -149
 
 
 def _dense_max_power(mx, my, cx, cy, cz, tx, ty):
