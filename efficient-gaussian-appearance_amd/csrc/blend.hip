@@ -33,11 +33,13 @@ __device__ __forceinline__ float4 scale_conic_for_exp2(float cx, float cy, float
 }
 
 // alpha of a staged Gaussian at a pixel centre; G receives the Gaussian factor
-__device__ __forceinline__ float eval_alpha(float2 xy, float4 co, float pxf, float pyf, float& dx, float& dy, float& G) {
+// exponent clamped to [-127, 0] with one median-of-three (the same value as min(q, 0) then max(-127) for
+// every finite q)
+__device__ __forceinline__ float eval_alpha(float4 xy, float4 co, float pxf, float pyf, float& dx, float& dy, float& G) {
     dx = xy.x - pxf;
     dy = xy.y - pyf;
     const float q = __builtin_fmaf(dx, __builtin_fmaf(co.x, dx, co.y * dy), co.z * dy * dy);
-    G = ef_exp2f(fminf(q, 0.0f));
+    G = ef_exp2f_clamped(__builtin_amdgcn_fmed3f(q, -127.0f, 0.0f));
     return co.w * G;
 }
 
@@ -52,7 +54,7 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 
 __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForwardArgs a) {
-    __shared__ float2 s_xy[tile_pixels];
+    __shared__ float4 s_xy[tile_pixels];  // (x, y, -, -): the 16-byte stride of s_co and s_col, one LDS address
     __shared__ float4 s_co[tile_pixels];
     __shared__ float4 s_col[tile_pixels];
     __shared__ uint2 s_b[tile_pixels];
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
         if (start + tid < n_total) {
             const uint32_t e = a.sorted_inst[range.x + start + tid];
             const PrimRecord rec = a.records[a.inst_prim[e]];
-            s_xy[tid] = make_float2(rec.r0.x, rec.r0.y);
+            s_xy[tid] = make_float4(rec.r0.x, rec.r0.y, 0.0f, 0.0f);
             s_co[tid] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
             s_col[tid] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
             s_b[tid] = make_uint2(__float_as_uint(rec.r2.y), __float_as_uint(rec.r2.z));
@@ -196,7 +198,7 @@ template <bool ABS>
 __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwardArgs a) {
     constexpr uint32_t n_values = ABS ? 11u : 9u;
     constexpr uint32_t n_waves = tile_pixels / 64;
-    __shared__ float2 s_xy[tile_pixels];
+    __shared__ float4 s_xy[tile_pixels];  // (x, y, -, -): the 16-byte stride of s_co and s_col, one LDS address
     __shared__ float4 s_co[tile_pixels];    // exp2-scaled conic (x, y, z), opacity
     __shared__ float4 s_col[tile_pixels];
     __shared__ uint2 s_b[tile_pixels];
@@ -246,7 +248,7 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
             e_own = a.sorted_inst[range.x + start + tid];
             const PrimRecord rec = a.records[a.inst_prim[e_own]];
             craw = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, 0.0f);
-            s_xy[tid] = make_float2(rec.r0.x, rec.r0.y);
+            s_xy[tid] = make_float4(rec.r0.x, rec.r0.y, 0.0f, 0.0f);
             s_co[tid] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
             s_col[tid] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
             s_b[tid] = make_uint2(__float_as_uint(rec.r2.y), __float_as_uint(rec.r2.z));

@@ -107,18 +107,18 @@ float ef_logf(float x) {
 
 static float ef_sigmoid(float x) { return 1.0f / (1.0f + ef_expf(-x)); }
 
-/* 2^x for x <= 0: x clamped to -127 (NaN too), k = rint(x), r = x - k exact, degree-7 Taylor series of 2^r
- * in r ln2 with fused multiply-adds, scaled by 2^k built from its exponent bits (k = -127 gives 0). */
+/* 2^x for x <= 0: x clamped to -127 (NaN too), k = rint(x), r = x - k exact, 2^r = 1 + r q(r) with q the
+ * degree-5 minimax polynomial (relative error) on [-1/2, 1/2] in Horner form with fused multiply-adds, scaled
+ * by 2^k built from its exponent bits (k = -127 gives 0). */
 float ef_exp2f(float x) {
     x = fmaxf(x, -127.0f);
     const float k = rintf(x);
     const float r = x - k;
-    float p = fmaf(1.52527338e-05f, r, 1.54035304e-04f);
-    p = fmaf(p, r, 1.33335581e-03f);
-    p = fmaf(p, r, 9.61812911e-03f);
-    p = fmaf(p, r, 5.55041087e-02f);
-    p = fmaf(p, r, 2.40226507e-01f);
-    p = fmaf(p, r, 6.93147181e-01f);
+    float p = fmaf(1.546973217e-04f, r, 1.341000083e-03f);
+    p = fmaf(p, r, 9.618030861e-03f);
+    p = fmaf(p, r, 5.550297350e-02f);
+    p = fmaf(p, r, 2.402265072e-01f);
+    p = fmaf(p, r, 6.931472421e-01f);
     p = fmaf(p, r, 1.0f);
     uint32_t bits = (uint32_t)((int)k + 127) << 23;
     float scale;

@@ -53,7 +53,7 @@ def test_ef_exp2_accuracy():
     got = np.array([O.ef_exp2(float(x)) for x in xs[::7]])
     ref = np.exp2(xs[::7].astype(np.float64))
     normal = ref >= 2.0 ** -126
-    assert _ulps(got[normal], ref[normal]).max() <= 1.5
+    assert _ulps(got[normal], ref[normal]).max() <= 1.0  # the minimax polynomial stays under one ulp
     assert O.ef_exp2(0.0) == 1.0
     assert O.ef_exp2(-1.0) == 0.5
     assert O.ef_exp2(-127.0) == 0.0
