@@ -173,15 +173,67 @@ __device__ __forceinline__ uint32_t reduced8_index(uint32_t lane) {
     return 4u * half + ((row & 1u) << 1) + (row >> 1);  // rows 0..3 hold values 0, 2, 1, 3 of the half
 }
 
-// Four values -> lanes 15, 31, 47, 63 hold complete sums of values 0, 2, 1, 3.
-__device__ __forceinline__ float transpose_reduce4(float u0, float u1, float u2, float u3) {
-    const float w0 = swap32_add(u0, u1), w1 = swap32_add(u2, u3);
-    float x = swap16_add(w0, w1);
+// Sixteen values -> every lane of the quad (4 lanes) that holds value k has its complete sum; value index of
+// lane l: see reduced16_index. The eight-value steps, then row_half_mirror (lane i of a half-row exchanges
+// with lane 7 - i) splits each half-row into two quads and two quad permutations finish.
+__device__ __forceinline__ float transpose_reduce16(const float* v, uint32_t lane) {
+    float w[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = swap32_add(v[2 * i], v[2 * i + 1]);
+    // rows of x[k]: v[4k], v[4k + 2], v[4k + 1], v[4k + 3]
+    float x[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) x[k] = swap16_add(w[2 * k], w[2 * k + 1]);
+    const bool hi = (lane & 8u) != 0;  // half-row h of y0 holds x[h], of y1 holds x[2 + h]
+    const float y0 = (hi ? x[1] : x[0]) + dpp<0x128, 0xf, false>(0.0f, hi ? x[0] : x[1]);  // row_ror:8
+    const float y1 = (hi ? x[3] : x[2]) + dpp<0x128, 0xf, false>(0.0f, hi ? x[2] : x[3]);
+    const bool q = (lane & 4u) != 0;  // quad q of each half-row holds y_q
+    float z = (q ? y1 : y0) + dpp<0x141, 0xf, false>(0.0f, q ? y0 : y1);  // row_half_mirror
+    z += dpp<0xB1, 0xf, false>(0.0f, z);  // quad_perm [1, 0, 3, 2]
+    z += dpp<0x4E, 0xf, false>(0.0f, z);  // quad_perm [2, 3, 0, 1]
+    return z;
+}
+
+__device__ __forceinline__ uint32_t reduced16_index(uint32_t lane) {
+    const uint32_t row = lane >> 4, half = (lane >> 3) & 1u, quad = (lane >> 2) & 1u;
+    return 4u * (half + 2u * quad) + ((row & 1u) << 1) + (row >> 1);
+}
+
+// Two values -> lanes 15, 31 hold the complete sum of a, lanes 47, 63 that of b.
+__device__ __forceinline__ float transpose_reduce2(float a, float b) {
+    const float w = swap32_add(a, b);  // a in lanes 0-31, b in lanes 32-63
+    float x = swap16_add(w, w);        // rows 0, 1: a; rows 2, 3: b
     x += dpp<0x111, 0xf, true>(0.0f, x);  // row_shr:1
     x += dpp<0x112, 0xf, true>(0.0f, x);  // row_shr:2
     x += dpp<0x114, 0xf, true>(0.0f, x);  // row_shr:4
     x += dpp<0x118, 0xf, true>(0.0f, x);  // row_shr:8; lane 15 of each row complete
     return x;
+}
+
+// Per pixel: the nine (eleven with ABS) gradient terms of one Gaussian, zero where the pixel skips it, and the
+// pixel's transmittance and remaining-colour state advanced past it (unchanged bit for bit when skipped).
+template <bool ABS>
+__device__ __forceinline__ void pair_terms(bool contrib, float alpha, float G, float dx, float dy, float4 col, float4 craw,
+                                           float gr, float gg, float gb, float gbg, float& T, float& A, float* v,
+                                           float& wgb, float& e1, float& e2) {
+    const float ae = contrib ? alpha : 0.0f;
+    const float Ge = contrib ? G : 0.0f;
+    const float w = T * ae;
+    const float oma = 1.0f - ae;
+    const float rcp = __builtin_amdgcn_rcpf(fmaxf(oma, one_minus_alpha_eps));
+    const float cg = __builtin_fmaf(col.z, gb, __builtin_fmaf(col.y, gg, col.x * gr));
+    A = __builtin_fmaf(-w, cg, A);
+    const float dalpha = __builtin_fmaf(T, cg, -rcp * (A - gbg));
+    const float h = -ae * dalpha;
+    const float hdx = h * dx, hdy = h * dy;
+    v[0] = hdx; v[1] = hdy; v[2] = hdx * dx; v[3] = hdx * dy; v[4] = hdy * dy;
+    v[5] = Ge * dalpha; v[6] = w * gr; v[7] = w * gg;
+    wgb = w * gb;
+    if (ABS) {
+        e1 = fabsf(__builtin_fmaf(craw.x, hdx, craw.y * hdy));
+        e2 = fabsf(__builtin_fmaf(craw.y, hdx, craw.z * hdy));
+    }
+    T = T * oma;
 }
 
 // ABS: also reduce |dL/dmean2d| per pixel (needed only for the third densification row).
@@ -262,39 +314,38 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
             const uint32_t j = c0 + lane;
             const bool ov = j < batch_wave && band_overlap(s_b[j], bx0, bx1, by0, by1);
             uint64_t mask = __ballot(ov);
+            // two Gaussians (a, b) per step share the transposing reductions; with an odd count the last b is
+            // a = b again, skipped by every pixel and not written
             while (mask != 0) {
-                const uint32_t jj = c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
+                const uint32_t ja = c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
                 mask &= mask - 1;
-                float dx, dy, G;
-                const float alpha = eval_alpha(s_xy[jj], s_co[jj], pxf, pyf, dx, dy, G);
-                const bool contrib = start + jj < last && alpha >= min_alpha;
-                if (__ballot(contrib) == 0) continue;
-                const float ae = contrib ? alpha : 0.0f;
-                const float Ge = contrib ? G : 0.0f;
-                const float4 col = s_col[jj];
-                const float w = T * ae;
-                const float oma = 1.0f - ae;
-                const float rcp = __builtin_amdgcn_rcpf(fmaxf(oma, one_minus_alpha_eps));
-                const float cg = __builtin_fmaf(col.z, gb, __builtin_fmaf(col.y, gg, col.x * gr));
-                A = __builtin_fmaf(-w, cg, A);
-                const float dalpha = __builtin_fmaf(T, cg, -rcp * (A - gbg));
-                const float h = -ae * dalpha;
-                const float hdx = h * dx, hdy = h * dy;
-                float v[8] = {hdx, hdy, hdx * dx, hdx * dy, hdy * dy, Ge * dalpha, w * gr, w * gg};
-                float e1 = 0.0f, e2 = 0.0f;
+                const bool has_b = mask != 0;
+                const uint32_t jb = has_b ? c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1) : ja;
+                mask &= mask - 1;
+                float dxa, dya, Ga, dxb, dyb, Gb;
+                const float alpha_a = eval_alpha(s_xy[ja], s_co[ja], pxf, pyf, dxa, dya, Ga);
+                const float alpha_b = eval_alpha(s_xy[jb], s_co[jb], pxf, pyf, dxb, dyb, Gb);
+                const bool contrib_a = start + ja < last && alpha_a >= min_alpha;
+                const bool contrib_b = has_b && start + jb < last && alpha_b >= min_alpha;
+                if (__ballot(contrib_a || contrib_b) == 0) continue;
+                float v[16], wgb_a, wgb_b, e1a = 0.0f, e2a = 0.0f, e1b = 0.0f, e2b = 0.0f;
+                const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                pair_terms<ABS>(contrib_a, alpha_a, Ga, dxa, dya, s_col[ja], ABS ? s_craw[ja] : zero4, gr, gg, gb, gbg, T, A,
+                                v, wgb_a, e1a, e2a);
+                pair_terms<ABS>(contrib_b, alpha_b, Gb, dxb, dyb, s_col[jb], ABS ? s_craw[jb] : zero4, gr, gg, gb, gbg, T, A,
+                                v + 8, wgb_b, e1b, e2b);
+                const float s16 = transpose_reduce16(v, lane);
+                const uint32_t k16 = reduced16_index(lane);
+                if ((lane & 3u) == 3u && (k16 < 8u || has_b)) s_grad[wave][k16 & 7u][k16 < 8u ? ja : jb] = s16;
                 if (ABS) {
-                    const float4 cr = s_craw[jj];
-                    e1 = fabsf(__builtin_fmaf(cr.x, hdx, cr.y * hdy));
-                    e2 = fabsf(__builtin_fmaf(cr.y, hdx, cr.z * hdy));
-                }
-                T = T * oma;
-                const float s8 = transpose_reduce8(v, lane);
-                const float s4 = transpose_reduce4(w * gb, e1, e2, 0.0f);
-                if ((lane & 7u) == 7u) s_grad[wave][reduced8_index(lane)][jj] = s8;
-                if ((lane & 15u) == 15u) {
-                    const uint32_t row = lane >> 4;
-                    const uint32_t k = 8u + ((row & 1u) << 1) + (row >> 1);  // rows 0..3: values 8, 10, 9, 11
-                    if (k < n_values) s_grad[wave][k][jj] = s4;
+                    const float u[8] = {wgb_a, e1a, e2a, wgb_b, e1b, e2b, 0.0f, 0.0f};
+                    const float s8 = transpose_reduce8(u, lane);
+                    const uint32_t k8 = reduced8_index(lane);  // 0-2: values 8-10 of a, 3-5: of b
+                    if ((lane & 7u) == 7u && (k8 < 3u || (k8 < 6u && has_b)))
+                        s_grad[wave][8u + (k8 < 3u ? k8 : k8 - 3u)][k8 < 3u ? ja : jb] = s8;
+                } else {
+                    const float s2 = transpose_reduce2(wgb_a, wgb_b);
+                    if ((lane & 31u) == 15u && (lane < 32u || has_b)) s_grad[wave][8][lane < 32u ? ja : jb] = s2;
                 }
             }
         }
