@@ -186,6 +186,7 @@ struct PrimitiveLayout {
     uint32_t* keys_b;
     uint32_t* vals_b;
     uint32_t* offsets;
+    uint32_t* visible_prims;
     void* scan_scratch;
     void* sort_scratch;
     size_t bytes;
@@ -208,6 +209,7 @@ struct PrimitiveLayout {
         l.keys_b = c.take<uint32_t>(nn);
         l.vals_b = c.take<uint32_t>(nn);
         l.offsets = c.take<uint32_t>(nn);
+        l.visible_prims = c.take<uint32_t>(nn);
         l.scan_scratch = c.take_bytes(scan_scratch_bytes(static_cast<uint32_t>(nn)));
         l.sort_scratch = c.take_bytes(sort_scratch_bytes(static_cast<uint32_t>(nn)));
         l.bytes = c.offset + buffer_alignment;
@@ -623,7 +625,8 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         t.end(s);
         t.begin(EFGS_STAGE_COMPACT, s);
         if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, chunks, s)) return EFGS_ERR_HIP;
-        if (!launch_compact_visible(pl.n_touched, pl.depth_keys, pl.block_offsets, pl.counters, pl.keys_a, pl.vals_a, n, s)) return EFGS_ERR_HIP;
+        if (!launch_compact_visible(pl.n_touched, pl.depth_keys, pl.block_offsets, pl.counters, pl.keys_a, pl.vals_a, pl.visible_prims, n, s))
+            return EFGS_ERR_HIP;
         t.end(s);
     } else {
         if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
@@ -804,6 +807,8 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     float* partials = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(blocks) * params * sizeof(float)));
     if (!partials) return fail(EFGS_ERR_ALLOC, "allocation of the mlp gradient partials failed");
     a.g_mlp_partials = partials;
+    a.visible_prims = pl.visible_prims;
+    a.n_visible = frame->n_visible;
     t.begin(EFGS_STAGE_MLP_BACKWARD, s);
     if (!launch_function(mlp_kernel, blocks, preprocess_block, mlp_smem_backward(mlp_shape(r)), &a, s)) return EFGS_ERR_HIP;
     t.end(s);

@@ -43,6 +43,8 @@ __device__ __forceinline__ float eval_alpha(float4 xy, float4 co, float pxf, flo
     return co.w * G;
 }
 
+__device__ __forceinline__ uint2 rect_of(float4 xy) { return make_uint2(__float_as_uint(xy.z), __float_as_uint(xy.w)); }
+
 __device__ __forceinline__ bool band_overlap(uint2 b, uint32_t bx0, uint32_t bx1, uint32_t by0, uint32_t by1) {
     return (b.x & 0xffffu) < bx1 && bx0 < (b.x >> 16) && (b.y & 0xffffu) < by1 && by0 < (b.y >> 16);
 }
@@ -54,10 +56,10 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 
 __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForwardArgs a) {
-    __shared__ float4 s_xy[tile_pixels];  // (x, y, -, -): the 16-byte stride of s_co and s_col, one LDS address
+    // (x, y, packed pixel rectangle): the 16-byte stride of s_co and s_col, so the pair loads share one address
+    __shared__ float4 s_xy[tile_pixels];
     __shared__ float4 s_co[tile_pixels];
     __shared__ float4 s_col[tile_pixels];
-    __shared__ uint2 s_b[tile_pixels];
     __shared__ uint32_t s_max[tile_pixels / 64];
 
     const uint32_t tile = blockIdx.x;
@@ -80,16 +82,15 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
         if (start + tid < n_total) {
             const uint32_t e = a.sorted_inst[range.x + start + tid];
             const PrimRecord rec = a.records[a.inst_prim[e]];
-            s_xy[tid] = make_float4(rec.r0.x, rec.r0.y, 0.0f, 0.0f);
+            s_xy[tid] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
             s_co[tid] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
             s_col[tid] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
-            s_b[tid] = make_uint2(__float_as_uint(rec.r2.y), __float_as_uint(rec.r2.z));
         }
         __syncthreads();
         const uint32_t batch_n = min(tile_pixels, n_total - start);
         for (uint32_t c0 = 0; c0 < batch_n; c0 += 64) {
             const uint32_t j = c0 + lane;
-            const bool ov = j < batch_n && band_overlap(s_b[j], bx0, bx1, by0, by1);
+            const bool ov = j < batch_n && band_overlap(rect_of(s_xy[j]), bx0, bx1, by0, by1);
             uint64_t mask = __ballot(ov);
             while (mask != 0) {
                 const uint32_t jj = c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
@@ -250,13 +251,16 @@ template <bool ABS>
 __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwardArgs a) {
     constexpr uint32_t n_values = ABS ? 11u : 9u;
     constexpr uint32_t n_waves = tile_pixels / 64;
-    __shared__ float4 s_xy[tile_pixels];  // (x, y, -, -): the 16-byte stride of s_co and s_col, one LDS address
+    // (x, y, packed pixel rectangle): the 16-byte stride of s_co and s_col, so the pair loads share one address
+    __shared__ float4 s_xy[tile_pixels];
     __shared__ float4 s_co[tile_pixels];    // exp2-scaled conic (x, y, z), opacity
     __shared__ float4 s_col[tile_pixels];
-    __shared__ uint2 s_b[tile_pixels];
     __shared__ float4 s_craw[ABS ? tile_pixels : 1];  // raw conic, for the per-pixel |dL/dmean2d|
-    __shared__ float4 s_grad4[n_waves * n_values * tile_pixels / 4];
-    float (*s_grad)[n_values][tile_pixels] = reinterpret_cast<float (*)[n_values][tile_pixels]>(s_grad4);
+    // per wave and value one row of the batch's 192 instances, rows 200 floats apart (8 mod the 64 LDS banks):
+    // the 16 lanes that store a pair's values for instances a and b hit distinct banks
+    constexpr uint32_t grad_row = tile_pixels + 8;
+    __shared__ float4 s_grad4[n_waves * n_values * grad_row / 4];
+    float (*s_grad)[n_values][grad_row] = reinterpret_cast<float (*)[n_values][grad_row]>(s_grad4);
 
     const uint32_t tile = blockIdx.x;
     const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
@@ -300,19 +304,18 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
             e_own = a.sorted_inst[range.x + start + tid];
             const PrimRecord rec = a.records[a.inst_prim[e_own]];
             craw = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, 0.0f);
-            s_xy[tid] = make_float4(rec.r0.x, rec.r0.y, 0.0f, 0.0f);
+            s_xy[tid] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
             s_co[tid] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
             s_col[tid] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
-            s_b[tid] = make_uint2(__float_as_uint(rec.r2.y), __float_as_uint(rec.r2.z));
             if (ABS) s_craw[tid] = craw;
         }
-        for (uint32_t k = tid; k < n_waves * n_values * tile_pixels / 4; k += tile_pixels) s_grad4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (uint32_t k = tid; k < n_waves * n_values * grad_row / 4; k += tile_pixels) s_grad4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         __syncthreads();
         const uint32_t batch_n = min(tile_pixels, n_total - start);
         const uint32_t batch_wave = wave_last > start ? min(min(tile_pixels, n_proc - start), wave_last - start) : 0u;
         for (uint32_t c0 = 0; c0 < batch_wave; c0 += 64) {
             const uint32_t j = c0 + lane;
-            const bool ov = j < batch_wave && band_overlap(s_b[j], bx0, bx1, by0, by1);
+            const bool ov = j < batch_wave && band_overlap(rect_of(s_xy[j]), bx0, bx1, by0, by1);
             uint64_t mask = __ballot(ov);
             // two Gaussians (a, b) per step share the transposing reductions; with an odd count the last b is
             // a = b again, skipped by every pixel and not written

@@ -53,9 +53,10 @@ bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 constexpr uint32_t n_counters = 8;
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
                               uint32_t n_blocks, hipStream_t s);
-// compacted depth keys are stored relative to counters[3] (order preserving; fewer radix passes)
+// compacted depth keys are stored relative to counters[3] (order preserving; fewer radix passes); the
+// primitive indices go to vals_out (sort input) and visible_out (kept in index order)
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_keys, const uint32_t* block_offsets, const uint32_t* counters,
-                            uint32_t* keys_out, uint32_t* vals_out, uint32_t n, hipStream_t s);
+                            uint32_t* keys_out, uint32_t* vals_out, uint32_t* visible_out, uint32_t n, hipStream_t s);
 bool launch_create_instances(const uint32_t* sorted_prims, const uint32_t* offsets, const uint32_t* n_touched,
                              const PrimRecord* records, void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* prim_offset,
                              uint32_t* counters, uint32_t grid_w, uint32_t n_visible, hipStream_t s);

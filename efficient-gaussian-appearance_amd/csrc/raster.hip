@@ -16,7 +16,8 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t n) {
 // primitive-index-ordered compaction of (depth key - min depth key, primitive) for the visible primitives
 __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const uint32_t* n_touched, const uint32_t* depth_keys,
                                                                           const uint32_t* block_offsets, const uint32_t* counters,
-                                                                          uint32_t* keys_out, uint32_t* vals_out, uint32_t n) {
+                                                                          uint32_t* keys_out, uint32_t* vals_out, uint32_t* visible_out,
+                                                                          uint32_t n) {
     __shared__ uint32_t wave_counts[preprocess_block / 64];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
@@ -30,6 +31,7 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
     pos += static_cast<uint32_t>(__popcll(mask & ((1ull << lane) - 1ull)));
     keys_out[pos] = depth_keys[p] - counters[3];
     vals_out[pos] = p;
+    visible_out[pos] = p;  // kept in index order for the backward (the sort overwrites vals_out)
 }
 
 // One thread per visible primitive in depth order: emits (tile key, primitive) for every tile of its tile
@@ -149,9 +151,9 @@ bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s) {
 }
 
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_keys, const uint32_t* block_offsets, const uint32_t* counters,
-                            uint32_t* keys_out, uint32_t* vals_out, uint32_t n, hipStream_t s) {
+                            uint32_t* keys_out, uint32_t* vals_out, uint32_t* visible_out, uint32_t n, hipStream_t s) {
     compact_visible_kernel<<<div_up(n, preprocess_block), preprocess_block, 0, s>>>(n_touched, depth_keys, block_offsets, counters, keys_out,
-                                                                                     vals_out, n);
+                                                                                     vals_out, visible_out, n);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

@@ -61,6 +61,8 @@ struct PreprocessBackwardArgs {
     float* g_mlp_partials;           // neural: (blocks x n_params) fp32 per-block weight gradient partials
     float* color_grads;              // neural: (N x 4) dL/d(pre-activation colour), geometry kernel -> MLP kernel
     uint32_t* color_grad_max;        // neural: per geometry block, max |dL/d(pre-activation colour)| as float bits
+    const uint32_t* visible_prims;   // neural: (V) the visible primitives in index order (the MLP kernel's work list)
+    uint32_t n_visible;
     float* densification_info;       // (rows x N) or null
     uint32_t densification_rows;
     uint32_t n;

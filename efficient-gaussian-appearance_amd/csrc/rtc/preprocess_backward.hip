@@ -310,13 +310,14 @@ extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_C
     const bool finite = gmax > 0.0f && gmax < 3.0e38f;
     const int e = finite ? max(ilogbf(gmax), -110) : 8;  // the clamp keeps 2^(8 - e) finite for denormal maxima
     const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
-    const uint32_t n_chunks = (a.n + preprocess_block - 1) / preprocess_block;
+    // work list: the visible primitives in index order (every other primitive's MLP gradients are zero), so
+    // the MFMA tiles are full and the gathers nearly contiguous
+    const uint32_t n_chunks = (a.n_visible + preprocess_block - 1) / preprocess_block;
     for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
-        const uint32_t p_raw = chunk * preprocess_block + threadIdx.x;
-        const bool valid = p_raw < a.n;
-        const uint32_t p = valid ? p_raw : a.n - 1;
-        const bool contributes = valid && a.n_touched[p] > 0;
-        if (__ballot(contributes) == 0) continue;  // wave-uniform: nothing to backpropagate
+        const uint32_t v_idx = chunk * preprocess_block + threadIdx.x;
+        const bool contributes = v_idx < a.n_visible;
+        if (__ballot(contributes) == 0) continue;  // wave-uniform: the tail of the list
+        const uint32_t p = a.visible_prims[contributes ? v_idx : 0u];
         const float4 dpre = contributes ? reinterpret_cast<const float4*>(a.color_grads)[p] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
         const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
