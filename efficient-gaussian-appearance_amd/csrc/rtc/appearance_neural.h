@@ -235,15 +235,40 @@ __device__ __forceinline__ uint32_t u_slot(uint32_t l, uint32_t pb, uint32_t fb,
     return (((l - 2) * U_TILES + pb * (NN / 16) + fb) * 64 + lane);
 }
 
-// copies the flat tcnn-layout weights (fp16 bits) into the padded W / W^T layout (whole block)
-__device__ inline void load_dual_weights(const uint16_t* g, uint16_t* WL, uint32_t tid, uint32_t n_threads) {
+// copies the flat tcnn-layout weights (fp16 bits, 16-byte aligned) into the padded W / W^T layout (whole
+// block of N_THREADS): 8 weights per 16-byte load, up to 8 loads per thread in flight before the LDS stores.
+// Every layer holds a multiple of 256 weights, so a vector never straddles two layers or two rows.
+template <uint32_t N_THREADS>
+__device__ inline void load_dual_weights(const uint16_t* g, uint16_t* WL, uint32_t tid) {
+    constexpr uint32_t n_vec = PARAMS / 8;
+    constexpr uint32_t batch = 8;
+    const uint4* gv = reinterpret_cast<const uint4*>(g);
+    for (uint32_t v0 = 0; v0 < n_vec; v0 += batch * N_THREADS) {
+        uint4 w[batch];
 #pragma unroll
-    for (uint32_t l = 0; l < NL; l++) {
-        for (uint32_t idx = tid; idx < lout(l) * lin(l); idx += n_threads) {
-            const uint32_t row = idx / lin(l), col = idx % lin(l);
-            const uint16_t v = g[loff(l) + idx];
-            WL[woff(l) + row * wrow(l) + col] = v;
-            WL[wtoff(l) + col * wtrow(l) + row] = v;
+        for (uint32_t k = 0; k < batch; k++) {
+            const uint32_t v = v0 + k * N_THREADS + tid;
+            if (v < n_vec) w[k] = gv[v];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < batch; k++) {
+            const uint32_t v = v0 + k * N_THREADS + tid;
+            if (v >= n_vec) continue;
+            const uint32_t h = 8 * v;
+            const uint16_t e[8] = {static_cast<uint16_t>(w[k].x), static_cast<uint16_t>(w[k].x >> 16), static_cast<uint16_t>(w[k].y),
+                                   static_cast<uint16_t>(w[k].y >> 16), static_cast<uint16_t>(w[k].z), static_cast<uint16_t>(w[k].z >> 16),
+                                   static_cast<uint16_t>(w[k].w), static_cast<uint16_t>(w[k].w >> 16)};
+#pragma unroll
+            for (uint32_t l = 0; l < NL; l++) {
+                if (h < loff(l) || h >= loff(l) + lout(l) * lin(l)) continue;
+                const uint32_t idx = h - loff(l);
+                const uint32_t row = idx / lin(l), col = idx % lin(l);
+#pragma unroll
+                for (uint32_t i = 0; i < 8; i++) {
+                    WL[woff(l) + row * wrow(l) + col + i] = e[i];
+                    WL[wtoff(l) + (col + i) * wtrow(l) + row] = e[i];
+                }
+            }
         }
     }
 }

@@ -278,7 +278,7 @@ extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_C
     const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
     _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES + wave * nn::DUAL_STAGE_BYTES);
     nn::h4* ustore = reinterpret_cast<nn::h4*>(smem + nn::DUAL_WEIGHT_BYTES + 4 * nn::DUAL_STAGE_BYTES + wave * nn::U_STORE_BYTES);
-    nn::load_dual_weights(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x, preprocess_block);
+    nn::load_dual_weights<preprocess_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
     __syncthreads();
 
     nn::f4 dW[nn::NL][nn::NT > 1 ? nn::NT : 1][nn::KT];
@@ -296,7 +296,16 @@ extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_C
     {
         const uint32_t n_geometry_blocks = (a.n + preprocess_block - 1) / preprocess_block;
         uint32_t m = 0u;
-        for (uint32_t b = threadIdx.x; b < n_geometry_blocks; b += preprocess_block) m = max(m, a.color_grad_max[b]);
+        for (uint32_t b0 = 0; b0 < n_geometry_blocks; b0 += 8 * preprocess_block) {  // 8 loads in flight per thread
+            uint32_t v[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++) {
+                const uint32_t b = b0 + k * preprocess_block + threadIdx.x;
+                v[k] = b < n_geometry_blocks ? a.color_grad_max[b] : 0u;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++) m = max(m, v[k]);
+        }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o)));
         if (lane == 0) s_wave_max[wave] = m;

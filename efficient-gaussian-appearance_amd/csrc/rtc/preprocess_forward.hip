@@ -165,7 +165,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     extern __shared__ __align__(16) unsigned char smem[];
     const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
     _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES) + wave * 64 * nn::XS;
-    nn::load_dual_weights(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x, preprocess_block);
+    nn::load_dual_weights<preprocess_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
     __syncthreads();
 #endif
     const uint32_t n_chunks = (a.n + preprocess_block - 1) / preprocess_block;
