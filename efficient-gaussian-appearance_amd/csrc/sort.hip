@@ -2,13 +2,14 @@
 // Per pass (three launches):
 //   histogram : per-block digit counts, counts[digit][block];
 //   row scan  : one block per digit scans its row over the blocks (exclusive) and records the digit total;
-//   scatter   : each block ranks its keys (index order, 8 rounds of 256), places them digit-sorted in LDS,
-//               then writes every digit run to its global position contiguously, so consecutive lanes
+//   scatter   : each wave ranks a contiguous quarter of the block's keys (8 rounds of 64, no block barrier),
+//               the four waves' digit counts are combined once, the keys are placed digit-sorted in LDS,
+//               then every digit run is written to its global position contiguously, so consecutive lanes
 //               store consecutive addresses. Global position = (exclusive scan of the digit totals) + (row
 //               scan of the digit over the previous blocks) + (rank within the block).
 // A wave ranks its 64 keys per digit with 64-bit ballots (lanes sharing a digit form a peer mask; rank =
-// peers below the lane); waves and rounds are ordered through per-digit running counts in LDS, so equal keys
-// keep their input order. Replaces cub::DeviceRadixSort (B/rasterization/src/forward.cu:88-96 depth keys,
+// peers below the lane) against the wave's per-digit running counts in LDS; segments and rounds are in input
+// order, so equal keys keep their input order. Replaces cub::DeviceRadixSort (B/rasterization/src/forward.cu:88-96 depth keys,
 // :182-190 tile keys).
 #include "internal.h"
 
@@ -93,60 +94,75 @@ template <typename KeyT>
 __global__ __launch_bounds__(sort_block) void sort_scatter_kernel(const KeyT* keys_in, const uint32_t* vals_in, KeyT* keys_out, uint32_t* vals_out,
                                                                  const uint32_t* counts, const uint32_t* offsets, const uint32_t* totals, uint32_t n,
                                                                  uint32_t shift, uint32_t n_blocks) {
+    constexpr uint32_t wave_keys = sort_tile / sort_waves;  // each wave ranks a contiguous segment
+    constexpr uint32_t wave_rounds = wave_keys / 64;
     __shared__ KeyT s_key[sort_tile];
     __shared__ uint32_t s_val[sort_tile];
     __shared__ uint32_t local_base[sort_bins];   // first slot of each digit in the block's sorted tile
     __shared__ uint32_t global_base[sort_bins];  // global position of that slot
-    __shared__ uint32_t running[sort_bins];      // keys of each digit placed so far
-    __shared__ uint32_t wave_hist[sort_waves][sort_bins];
+    __shared__ uint32_t wave_count[sort_waves][sort_bins];  // per wave: keys of each digit so far, then the wave's offset
     __shared__ uint32_t s_waves[sort_waves];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint64_t lanes_below = (1ull << lane) - 1ull;
+    const uint32_t start = blockIdx.x * sort_tile + wave * wave_keys;
+    KeyT kr[wave_rounds];
+    uint32_t vr[wave_rounds], slot[wave_rounds];
+#pragma unroll
+    for (uint32_t r = 0; r < wave_rounds; r++) {
+        const uint32_t i = start + r * 64 + lane;
+        kr[r] = 0;
+        vr[r] = 0;
+        if (i < n) {
+            kr[r] = keys_in[i];
+            vr[r] = vals_in ? vals_in[i] : i;
+        }
+    }
+#pragma unroll
+    for (uint32_t w = 0; w < sort_waves; w++) wave_count[w][threadIdx.x] = 0;
     {
         const uint32_t d = threadIdx.x;
-        const uint32_t lb = block_exclusive_scan_256(counts[d * n_blocks + blockIdx.x], s_waves);
+        const uint32_t lb = block_exclusive_scan_256(counts[d * n_blocks + blockIdx.x], s_waves);  // also orders the clears
         const uint32_t digit_start = block_exclusive_scan_256(totals[d], s_waves);
         local_base[d] = lb;
         global_base[d] = digit_start + offsets[d * n_blocks + blockIdx.x];
-        running[d] = 0;
     }
-    const uint32_t start = blockIdx.x * sort_tile;
-    for (uint32_t r = 0; r < sort_rounds; r++) {
+    // wave-local ranking: a wave's LDS reads and writes execute in issue order, so no barrier is needed
+    // between its rounds (every lane of a digit reads the count before the digit's first lane writes it)
+    uint32_t* count = wave_count[wave];
 #pragma unroll
-        for (uint32_t w = 0; w < sort_waves; w++) wave_hist[w][threadIdx.x] = 0;
-        __syncthreads();
-        const uint32_t i = start + r * sort_block + threadIdx.x;
-        const bool valid = i < n;
-        KeyT key = 0;
-        uint32_t val = 0;
-        if (valid) {
-            key = keys_in[i];
-            val = vals_in ? vals_in[i] : i;
-        }
-        const uint32_t d = (static_cast<uint32_t>(key) >> shift) & 255u;
+    for (uint32_t r = 0; r < wave_rounds; r++) {
+        const bool valid = start + r * 64 + lane < n;
+        const uint32_t d = (static_cast<uint32_t>(kr[r]) >> shift) & 255u;
         const uint64_t peers = match_peers(d, valid);
         const uint32_t rank = static_cast<uint32_t>(__popcll(peers & lanes_below));
-        if (valid && rank == 0) wave_hist[wave][d] = static_cast<uint32_t>(__popcll(peers));
-        __syncthreads();
-        {
-            uint32_t run = running[threadIdx.x];
-#pragma unroll
-            for (uint32_t w = 0; w < sort_waves; w++) {
-                const uint32_t c = wave_hist[w][threadIdx.x];
-                wave_hist[w][threadIdx.x] = run;
-                run += c;
-            }
-            running[threadIdx.x] = run;
-        }
-        __syncthreads();
-        if (valid) {
-            const uint32_t slot = local_base[d] + wave_hist[wave][d] + rank;
-            s_key[slot] = key;
-            s_val[slot] = val;
-        }
-        __syncthreads();  // wave_hist is cleared at the top of the next round
+        const uint32_t base = count[d];
+        slot[r] = base + rank;
+        if (valid && rank == 0) count[d] = base + static_cast<uint32_t>(__popcll(peers));
+        __builtin_amdgcn_wave_barrier();  // keeps the next round's reads after this round's writes
     }
-    const uint32_t tile_n = min(sort_tile, n - start);
+    __syncthreads();
+    {
+        const uint32_t d = threadIdx.x;
+        uint32_t run = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < sort_waves; w++) {
+            const uint32_t c = wave_count[w][d];
+            wave_count[w][d] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < wave_rounds; r++) {
+        if (start + r * 64 + lane >= n) continue;
+        const uint32_t d = (static_cast<uint32_t>(kr[r]) >> shift) & 255u;
+        const uint32_t k = local_base[d] + count[d] + slot[r];
+        s_key[k] = kr[r];
+        s_val[k] = vr[r];
+    }
+    __syncthreads();
+    const uint32_t tile_start = blockIdx.x * sort_tile;
+    const uint32_t tile_n = min(sort_tile, n - tile_start);
     for (uint32_t k = threadIdx.x; k < tile_n; k += sort_block) {
         const KeyT key = s_key[k];
         const uint32_t d = (static_cast<uint32_t>(key) >> shift) & 255u;
