@@ -1,6 +1,6 @@
 // Stable LSD radix sort of (key, value) pairs for wave64, 8-bit digits, 2048 keys per 256-thread block.
 // Per pass (three launches):
-//   histogram : per-block digit counts, counts[digit][block];
+//   histogram : per-block digit counts, counts[block][digit] (each block's row contiguous);
 //   row scan  : one block per digit scans its row over the blocks (exclusive) and records the digit total;
 //   scatter   : each wave ranks a contiguous quarter of the block's keys (8 rounds of 64, no block barrier),
 //               the four waves' digit counts are combined once, the keys are placed digit-sorted in LDS,
@@ -67,25 +67,25 @@ __global__ __launch_bounds__(sort_block) void sort_histogram_kernel(const KeyT* 
             atomicAdd(&h[d], static_cast<uint32_t>(__popcll(peers)));
     }
     __syncthreads();
-    counts[threadIdx.x * n_blocks + blockIdx.x] = h[threadIdx.x];
+    counts[blockIdx.x * sort_bins + threadIdx.x] = h[threadIdx.x];
 }
 
-// block d: offsets[d][b] = sum of counts[d][b'] for b' < b, totals[d] = row sum
+// block d: offsets[b][d] = sum of counts[b'][d] for b' < b, totals[d] = column sum
 __global__ __launch_bounds__(sort_block) void sort_row_scan_kernel(const uint32_t* counts, uint32_t* offsets, uint32_t* totals, uint32_t n_blocks) {
     __shared__ uint32_t s_waves[sort_waves];
     const uint32_t d = blockIdx.x;
-    const uint32_t* row = counts + static_cast<size_t>(d) * n_blocks;
-    uint32_t* out = offsets + static_cast<size_t>(d) * n_blocks;
-    const uint32_t per = (n_blocks + sort_block - 1) / sort_block;  // consecutive entries per thread
+    const uint32_t per = (n_blocks + sort_block - 1) / sort_block;  // consecutive blocks per thread
     const uint32_t b0 = threadIdx.x * per;
     uint32_t sum = 0;
     for (uint32_t k = 0; k < per; k++)
-        if (b0 + k < n_blocks) sum += row[b0 + k];
+        if (b0 + k < n_blocks) sum += counts[static_cast<size_t>(b0 + k) * sort_bins + d];
     uint32_t run = block_exclusive_scan_256(sum, s_waves);
     for (uint32_t k = 0; k < per; k++)
         if (b0 + k < n_blocks) {
-            out[b0 + k] = run;
-            run += row[b0 + k];
+            const size_t e = static_cast<size_t>(b0 + k) * sort_bins + d;
+            const uint32_t c = counts[e];
+            offsets[e] = run;
+            run += c;
         }
     if (threadIdx.x == sort_block - 1) totals[d] = run;
 }
@@ -117,14 +117,18 @@ __global__ __launch_bounds__(sort_block) void sort_scatter_kernel(const KeyT* ke
             vr[r] = vals_in ? vals_in[i] : i;
         }
     }
+    // the block's table entries, loaded with the keys before the first barrier (one memory latency)
+    const uint32_t my_count = counts[static_cast<size_t>(blockIdx.x) * sort_bins + threadIdx.x];
+    const uint32_t my_total = totals[threadIdx.x];
+    const uint32_t my_offset = offsets[static_cast<size_t>(blockIdx.x) * sort_bins + threadIdx.x];
 #pragma unroll
     for (uint32_t w = 0; w < sort_waves; w++) wave_count[w][threadIdx.x] = 0;
     {
         const uint32_t d = threadIdx.x;
-        const uint32_t lb = block_exclusive_scan_256(counts[d * n_blocks + blockIdx.x], s_waves);  // also orders the clears
-        const uint32_t digit_start = block_exclusive_scan_256(totals[d], s_waves);
+        const uint32_t lb = block_exclusive_scan_256(my_count, s_waves);  // also orders the clears
+        const uint32_t digit_start = block_exclusive_scan_256(my_total, s_waves);
         local_base[d] = lb;
-        global_base[d] = digit_start + offsets[d * n_blocks + blockIdx.x];
+        global_base[d] = digit_start + my_offset;
     }
     // wave-local ranking: a wave's LDS reads and writes execute in issue order, so no barrier is needed
     // between its rounds (every lane of a digit reads the count before the digit's first lane writes it)
