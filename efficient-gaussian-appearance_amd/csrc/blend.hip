@@ -1,6 +1,9 @@
 // Alpha blending per 16x12 tile: 192 threads = 3 wave64, wave w owns pixel rows 4w..4w+3 (a 16x4 band),
-// one pixel per lane. Gaussians of the tile are staged 192 at a time in LDS; each wave culls a 64-Gaussian
-// chunk against its band with one 64-bit ballot and walks the surviving bits.
+// one pixel per lane (lane l: x = l & 15, y = 4w + (l >> 4)). Each band is split into four 4x4 pixel groups:
+// group g = (l >> 2) & 3 holds lanes 4g..4g+3 of every 16-lane row. Gaussians of the tile are staged in LDS;
+// a 64-Gaussian chunk is culled against the four group rectangles with four 64-bit ballots, and every group
+// walks its own surviving list, in order, one Gaussian per loop step (four Gaussians per wave instruction).
+// Small Gaussians cover few pixels: a 4x4 group wastes far fewer lanes than a 16x4 band would.
 //
 // Forward: front-to-back compositing, alpha = o exp2(min(q, 0)) with the conic pre-scaled by -log2(e)/2 and
 // exp2 from ef_exp2f (a fixed operation sequence, so alpha, T and the image are reproducible bit for bit),
@@ -9,10 +12,10 @@
 //
 // Backward: every pixel replays its forward walk (the evaluation below is shared and compiled with
 // -ffp-contract=off, so T and every skip decision are reproduced bit-exactly) and forms the reference's
-// per-pixel terms; the 9 per-Gaussian values (11 with the |dL/dmean2d| pair) are summed over the wave
-// (lanes = pixels) with DPP row operations, each wave keeps its own LDS slot per Gaussian, and the three band
-// sums are added in a fixed order into one 48-byte record per instance at its emission slot. No float
-// atomics; the result is run-to-run deterministic.
+// per-pixel terms; the 9 per-Gaussian values (11 with the |dL/dmean2d| pair) are summed over each 16-lane
+// group with two permlane swaps and two quad DPP steps, each (wave, group) keeps its own LDS slot per
+// Gaussian, and the twelve group sums are added in a fixed order into one 48-byte record per instance at its
+// emission slot. No float atomics; the result is run-to-run deterministic.
 //
 // Reference: B/rasterization/include/kernels_forward.cuh:26-166, kernels_backward.cuh:12-231.
 #include "internal.h"
@@ -45,34 +48,69 @@ __device__ __forceinline__ float eval_alpha(float4 xy, float4 co, float pxf, flo
 
 __device__ __forceinline__ uint2 rect_of(float4 xy) { return make_uint2(__float_as_uint(xy.z), __float_as_uint(xy.w)); }
 
-__device__ __forceinline__ bool band_overlap(uint2 b, uint32_t bx0, uint32_t bx1, uint32_t by0, uint32_t by1) {
-    return (b.x & 0xffffu) < bx1 && bx0 < (b.x >> 16) && (b.y & 0xffffu) < by1 && by0 < (b.y >> 16);
-}
-
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, o)));
     return v;
 }
 
+// Culls lane's Gaussian (rectangle `rect`, `in` = exists) against the four 4x4 groups of the band whose pixel
+// columns start at bx0 and rows span [by0, by1); m[g] receives the wave's ballot for group g.
+__device__ __forceinline__ void cull_groups(uint2 rect, bool in, uint32_t bx0, uint32_t by0, uint32_t by1, uint64_t (&m)[4]) {
+    const uint32_t rx0 = rect.x & 0xffffu, rx1 = rect.x >> 16, ry0 = rect.y & 0xffffu, ry1 = rect.y >> 16;
+    const bool yov = in && ry0 < by1 && by0 < ry1;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++) {
+        const uint32_t gx0 = bx0 + 4u * k;
+        m[k] = __ballot(yov && rx0 < gx0 + 4u && gx0 < rx1);
+    }
+}
+
+// the value of the lane's own group among four wave-uniform ones
+__device__ __forceinline__ uint32_t pick_group(uint32_t g, uint32_t j0, uint32_t j1, uint32_t j2, uint32_t j3) {
+    return (g & 2u) ? ((g & 1u) ? j3 : j2) : ((g & 1u) ? j1 : j0);
+}
+
+// Writes each group's surviving Gaussians of the chunk, in order, to list[k * list_len + 0 .. n[k]) (entry:
+// base + lane of the Gaussian); n[k] = popcount(m[k]). A group then walks its list with one LDS read per
+// step instead of scanning a 64-bit mask per lane.
+__device__ __forceinline__ void build_group_lists(const uint64_t (&m)[4], uint32_t lane, uint32_t base, uint32_t* list,
+                                                  uint32_t list_len, uint32_t (&n)[4]) {
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++) {
+        const uint32_t lo = static_cast<uint32_t>(m[k]), hi = static_cast<uint32_t>(m[k] >> 32);
+        if ((m[k] >> lane) & 1u) list[k * list_len + __builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u))] = base + lane;
+        n[k] = static_cast<uint32_t>(__popcll(m[k]));
+    }
+}
+
+// orders a wave's LDS accesses around its list writes (lanes read entries other lanes wrote)
+__device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
 __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForwardArgs a) {
+    constexpr uint32_t list_len = 64;
     // (x, y, packed pixel rectangle): the 16-byte stride of s_co and s_col, so the pair loads share one address
     __shared__ float4 s_xy[tile_pixels];
     __shared__ float4 s_co[tile_pixels];
     __shared__ float4 s_col[tile_pixels];
+    __shared__ uint32_t s_list[tile_pixels / 64][4][list_len];  // per wave and group: batch indices to walk
     __shared__ uint32_t s_max[tile_pixels / 64];
 
     const uint32_t tile = blockIdx.x;
     const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t g = (lane >> 2) & 3u;
     const uint32_t px = tx * tile_width + (lane & 15u);
     const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);
     const bool inside = px < a.width && py < a.height;
     const float pxf = static_cast<float>(px) + 0.5f, pyf = static_cast<float>(py) + 0.5f;
-    const uint32_t bx0 = tx * tile_width, bx1 = bx0 + tile_width;
+    const uint32_t bx0 = tx * tile_width;
     const uint32_t by0 = ty * tile_height + wave * 4u, by1 = by0 + 4u;
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
+    const uint32_t* const my_list = &s_list[wave][g][0];
+    // list entries past a group's count are read (and skipped): keep them valid batch indices
+    for (uint32_t k = tid; k < tile_pixels / 64 * 4 * list_len; k += tile_pixels) (&s_list[0][0][0])[k] = 0;
 
     float cr = 0.0f, cg = 0.0f, cb = 0.0f, T = 1.0f;
     uint32_t last = 0;
@@ -89,16 +127,19 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
         __syncthreads();
         const uint32_t batch_n = min(tile_pixels, n_total - start);
         for (uint32_t c0 = 0; c0 < batch_n; c0 += 64) {
-            const uint32_t j = c0 + lane;
-            const bool ov = j < batch_n && band_overlap(rect_of(s_xy[j]), bx0, bx1, by0, by1);
-            uint64_t mask = __ballot(ov);
-            while (mask != 0) {
-                const uint32_t jj = c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
-                mask &= mask - 1;
+            uint64_t m[4];
+            cull_groups(rect_of(s_xy[c0 + lane]), c0 + lane < batch_n, bx0, by0, by1, m);
+            uint32_t n[4];
+            build_group_lists(m, lane, c0, &s_list[wave][0][0], list_len, n);
+            wave_lds_fence();
+            const uint32_t n_max = max(max(n[0], n[1]), max(n[2], n[3]));
+            const uint32_t my_n = pick_group(g, n[0], n[1], n[2], n[3]);
+            for (uint32_t k = 0; k < n_max; k++) {
+                const uint32_t jj = my_list[k];  // past the group's count: a stale entry, skipped
                 // branch-free: a skipped Gaussian gets weight 0, which leaves C and T bit for bit unchanged
                 float dx, dy, G;
                 const float alpha = eval_alpha(s_xy[jj], s_co[jj], pxf, pyf, dx, dy, G);
-                const bool take = !done && alpha >= min_alpha;
+                const bool take = k < my_n && !done && alpha >= min_alpha;
                 const float a_t = take ? alpha : 0.0f;
                 const float w = T * a_t;
                 const float4 col = s_col[jj];
@@ -109,6 +150,7 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
                 last = take ? start + jj + 1 : last;
                 done = done || (take && T < transmittance_threshold);
             }
+            wave_lds_fence();
         }
     }
     const uint32_t slot = tile * tile_pixels + tid;
@@ -127,16 +169,15 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
     if (tid == 0) a.tile_max[tile] = max(max(s_max[0], s_max[1]), s_max[2]);
 }
 
-// Wave sums of several per-lane values at once ("transposing" reductions). Each exchange step swaps half of
-// the values between lane groups so that every lane keeps fewer values, each summed over more lanes:
+// Sums of several per-lane values over each 4x4 pixel group at once ("transposing" reductions). A group's
+// 16 lanes are lanes 4g..4g+3 of the four 16-lane rows. Each exchange step swaps half of the values between
+// lanes so that every lane keeps fewer values, each summed over more lanes of its group:
 //   permlane32 swap: lanes l and l + 32 exchange, a pair of registers becomes one register holding value
-//                    a in lanes 0-31 and value b in lanes 32-63 (sums over 2 lanes);
-//   permlane16 swap: 16-lane rows 1, 3 of the first register exchange with rows 0, 2 of the second; two such
-//                    registers become one holding four values, one per row (sums over 4 lanes);
-//   row_ror:8      : the two 8-lane halves of a row exchange, two registers become one holding eight
-//                    values, one per half-row (sums over 8 lanes);
-// and plain DPP adds (quad permutations, row_shr) finish the remaining lanes. Every step is a full-rate
-// VALU operation and the order is fixed, so the sums are reproducible.
+//                    a in rows 0, 1 and value b in rows 2, 3 (sums over 2 rows);
+//   permlane16 swap: rows 1, 3 of the first register exchange with rows 0, 2 of the second; two such
+//                    registers become one holding four values, one per row (sums over the 4 rows);
+//   quad_perm      : lanes i and i ^ 2 of a row quad exchange, then i and i ^ 1 add (sums over the quad).
+// Every step is a full-rate VALU operation and the order is fixed, so the sums are reproducible.
 template <int CTRL, int ROW_MASK, bool BOUND_CTRL>
 __device__ __forceinline__ float dpp(float old, float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xf, BOUND_CTRL));
@@ -154,61 +195,51 @@ __device__ __forceinline__ float swap16_add(float a, float b) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Eight values -> lanes 8m + 7 (m = 0..7) hold complete sums; value index of lane l: see reduced8_index.
-__device__ __forceinline__ float transpose_reduce8(const float* v, uint32_t lane) {
+// Eight values -> lane (r, i) of a group (row r, quad position i) holds the group sum of value
+// 4 (i >> 1) + {0, 2, 1, 3}[r].
+__device__ __forceinline__ float group_reduce8(const float* v, uint32_t lane) {
     const float w0 = swap32_add(v[0], v[1]), w1 = swap32_add(v[2], v[3]);
     const float w2 = swap32_add(v[4], v[5]), w3 = swap32_add(v[6], v[7]);
-    // rows of x0: v0, v2, v1, v3; rows of x1: v4, v6, v5, v7 (each summed over the 4 lanes equal mod 16)
-    const float x0 = swap16_add(w0, w1), x1 = swap16_add(w2, w3);
-    const bool hi = (lane & 8u) != 0;
-    const float keep = hi ? x1 : x0, send = hi ? x0 : x1;
-    float y = keep + dpp<0x128, 0xf, false>(0.0f, send);  // row_ror:8
-    y += dpp<0xB1, 0xf, false>(0.0f, y);                    // quad_perm [1, 0, 3, 2]
-    y += dpp<0x4E, 0xf, false>(0.0f, y);                    // quad_perm [2, 3, 0, 1]
-    y += dpp<0x114, 0xf, true>(0.0f, y);                    // row_shr:4; lanes 4-7 / 12-15 of a row complete
+    const float x0 = swap16_add(w0, w1), x1 = swap16_add(w2, w3);  // rows: v0, v2, v1, v3 / v4, v6, v5, v7
+    const bool hi = (lane & 2u) != 0;
+    float y = (hi ? x1 : x0) + dpp<0x4E, 0xf, true>(0.0f, hi ? x0 : x1);  // quad_perm [2, 3, 0, 1]
+    y += dpp<0xB1, 0xf, true>(0.0f, y);                                     // quad_perm [1, 0, 3, 2]
     return y;
 }
 
-__device__ __forceinline__ uint32_t reduced8_index(uint32_t lane) {
-    const uint32_t row = lane >> 4, half = (lane >> 3) & 1u;
-    return 4u * half + ((row & 1u) << 1) + (row >> 1);  // rows 0..3 hold values 0, 2, 1, 3 of the half
+__device__ __forceinline__ uint32_t group_reduced8_index(uint32_t lane) {
+    const uint32_t r = lane >> 4;
+    return 4u * ((lane >> 1) & 1u) + ((r & 1u) << 1) + (r >> 1);
 }
 
-// Sixteen values -> every lane of the quad (4 lanes) that holds value k has its complete sum; value index of
-// lane l: see reduced16_index. The eight-value steps, then row_half_mirror (lane i of a half-row exchanges
-// with lane 7 - i) splits each half-row into two quads and two quad permutations finish.
-__device__ __forceinline__ float transpose_reduce16(const float* v, uint32_t lane) {
+// Sixteen values -> lane (r, i) of a group holds the group sum of value 4 m + {0, 2, 1, 3}[r] with
+// m = {0, 2, 1, 3}[i]: values 0-7 on even quad positions, 8-15 on odd ones.
+__device__ __forceinline__ float group_reduce16(const float* v, uint32_t lane) {
     float w[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) w[i] = swap32_add(v[2 * i], v[2 * i + 1]);
-    // rows of x[k]: v[4k], v[4k + 2], v[4k + 1], v[4k + 3]
-    float x[4];
+    float x[4];  // rows of x[m]: v[4m], v[4m + 2], v[4m + 1], v[4m + 3]
 #pragma unroll
-    for (int k = 0; k < 4; k++) x[k] = swap16_add(w[2 * k], w[2 * k + 1]);
-    const bool hi = (lane & 8u) != 0;  // half-row h of y0 holds x[h], of y1 holds x[2 + h]
-    const float y0 = (hi ? x[1] : x[0]) + dpp<0x128, 0xf, false>(0.0f, hi ? x[0] : x[1]);  // row_ror:8
-    const float y1 = (hi ? x[3] : x[2]) + dpp<0x128, 0xf, false>(0.0f, hi ? x[2] : x[3]);
-    const bool q = (lane & 4u) != 0;  // quad q of each half-row holds y_q
-    float z = (q ? y1 : y0) + dpp<0x141, 0xf, false>(0.0f, q ? y0 : y1);  // row_half_mirror
-    z += dpp<0xB1, 0xf, false>(0.0f, z);  // quad_perm [1, 0, 3, 2]
-    z += dpp<0x4E, 0xf, false>(0.0f, z);  // quad_perm [2, 3, 0, 1]
-    return z;
+    for (int m = 0; m < 4; m++) x[m] = swap16_add(w[2 * m], w[2 * m + 1]);
+    const bool h2 = (lane & 2u) != 0;  // quad positions 2, 3 keep x[1] and x[3]
+    const float y0 = (h2 ? x[1] : x[0]) + dpp<0x4E, 0xf, true>(0.0f, h2 ? x[0] : x[1]);  // quad_perm [2, 3, 0, 1]
+    const float y1 = (h2 ? x[3] : x[2]) + dpp<0x4E, 0xf, true>(0.0f, h2 ? x[2] : x[3]);
+    const bool h1 = (lane & 1u) != 0;  // odd positions keep y1
+    return (h1 ? y1 : y0) + dpp<0xB1, 0xf, true>(0.0f, h1 ? y0 : y1);                  // quad_perm [1, 0, 3, 2]
 }
 
-__device__ __forceinline__ uint32_t reduced16_index(uint32_t lane) {
-    const uint32_t row = lane >> 4, half = (lane >> 3) & 1u, quad = (lane >> 2) & 1u;
-    return 4u * (half + 2u * quad) + ((row & 1u) << 1) + (row >> 1);
+__device__ __forceinline__ uint32_t group_reduced16_index(uint32_t lane) {
+    const uint32_t r = lane >> 4, i = lane & 3u;
+    return 4u * (2u * (i & 1u) + (i >> 1)) + ((r & 1u) << 1) + (r >> 1);
 }
 
-// Two values -> lanes 15, 31 hold the complete sum of a, lanes 47, 63 that of b.
-__device__ __forceinline__ float transpose_reduce2(float a, float b) {
-    const float w = swap32_add(a, b);  // a in lanes 0-31, b in lanes 32-63
-    float x = swap16_add(w, w);        // rows 0, 1: a; rows 2, 3: b
-    x += dpp<0x111, 0xf, true>(0.0f, x);  // row_shr:1
-    x += dpp<0x112, 0xf, true>(0.0f, x);  // row_shr:2
-    x += dpp<0x114, 0xf, true>(0.0f, x);  // row_shr:4
-    x += dpp<0x118, 0xf, true>(0.0f, x);  // row_shr:8; lane 15 of each row complete
-    return x;
+// Two values -> rows 0, 1 of a group hold the group sum of a, rows 2, 3 that of b.
+__device__ __forceinline__ float group_reduce2(float a, float b) {
+    float w = swap32_add(a, b);
+    w = swap16_add(w, w);
+    w += dpp<0x4E, 0xf, true>(0.0f, w);
+    w += dpp<0xB1, 0xf, true>(0.0f, w);
+    return w;
 }
 
 // Per pixel: the nine (eleven with ABS) gradient terms of one Gaussian, zero where the pixel skips it, and the
@@ -243,37 +274,71 @@ __device__ __forceinline__ void pair_terms(bool contrib, float alpha, float G, f
 // gradient terms use fused multiply-adds and the hardware reciprocal. Per pixel and Gaussian the kernel
 // forms, branch-free (zero for pixels that skip the Gaussian),
 //   h = -alpha dL/dalpha,  dL/dalpha = T (c . g) - (A - g_bg) / max(1 - alpha, eps)
-// with A = (colour still to come) . g, and the wave sums
+// with A = (colour still to come) . g, and the group sums
 //   h dx, h dy, h dx^2, h dx dy, h dy^2, G dL/dalpha, w g_r, w g_g, w g_b   (w = T alpha)
 // from which the instance's record is dL/dmean2d = (C h d summed), dL/dconic = 0.5 (h d d^T summed),
 // dL/dopacity-term = sum G dL/dalpha, dL/dcolour = sum w g.
+//
+// Each group walks two Gaussians (a, b) of its list per step, so their first eight values share one
+// 16-value reduction and their ninth values a 2-value one; every (wave, group) stores its sums in its own
+// LDS slot per Gaussian (a group visits a Gaussian at most once per batch). Gaussians are staged 32 at a
+// time (double-buffered, the next batch's records fetched into registers while the current one is
+// walked): one block barrier before the walk, one before the combine, which adds the twelve slots of each
+// value in a fixed order and clears them for the next batch. No atomics: the result is run-to-run
+// deterministic.
 template <bool ABS>
 __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwardArgs a) {
     constexpr uint32_t n_values = ABS ? 11u : 9u;
     constexpr uint32_t n_waves = tile_pixels / 64;
-    // (x, y, packed pixel rectangle): the 16-byte stride of s_co and s_col, so the pair loads share one address
-    __shared__ float4 s_xy[tile_pixels];
-    __shared__ float4 s_co[tile_pixels];    // exp2-scaled conic (x, y, z), opacity
-    __shared__ float4 s_col[tile_pixels];
-    __shared__ float4 s_craw[ABS ? tile_pixels : 1];  // raw conic, for the per-pixel |dL/dmean2d|
-    // per wave and value one row of the batch's 192 instances, rows 200 floats apart (8 mod the 64 LDS banks):
-    // the 16 lanes that store a pair's values for instances a and b hit distinct banks
-    constexpr uint32_t grad_row = tile_pixels + 8;
-    __shared__ float4 s_grad4[n_waves * n_values * grad_row / 4];
-    float (*s_grad)[n_values][grad_row] = reinterpret_cast<float (*)[n_values][grad_row]>(s_grad4);
+    constexpr uint32_t batch = 32;
+    constexpr uint32_t list_len = batch;
+    constexpr uint32_t n_slots = n_waves * 4;  // (wave, group) pairs
+    // slots [wave][group][value][instance]; value rows 33 floats apart
+    constexpr uint32_t value_stride = batch + 1;
+    constexpr uint32_t slot_stride = n_values * value_stride;
+    // staged per Gaussian: (x, y, packed rect), exp2-scaled conic + opacity, colour, raw conic
+    __shared__ float4 s_stage[2][batch][4];
+    __shared__ uint32_t s_emit[2][batch];
+    __shared__ uint32_t s_list[n_waves][4][list_len];
+    __shared__ float s_part[n_slots * slot_stride];
 
     const uint32_t tile = blockIdx.x;
     const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t g = (lane >> 2) & 3u;
     const uint32_t px = tx * tile_width + (lane & 15u);
     const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);
     const bool inside = px < a.width && py < a.height;
     const float pxf = static_cast<float>(px) + 0.5f, pyf = static_cast<float>(py) + 0.5f;
-    const uint32_t bx0 = tx * tile_width, bx1 = bx0 + tile_width;
+    const uint32_t bx0 = tx * tile_width;
     const uint32_t by0 = ty * tile_height + wave * 4u, by1 = by0 + 4u;
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
     const uint32_t n_proc = min(n_total, a.tile_max[tile]);
+    const uint32_t* const my_list = &s_list[wave][g][0];
+    // list entries past a group's count are read (and skipped): keep them valid batch indices; slots start at 0
+    for (uint32_t k = tid; k < n_waves * 4 * list_len; k += tile_pixels) (&s_list[0][0][0])[k] = 0;
+    for (uint32_t k = tid; k < n_slots * slot_stride; k += tile_pixels) s_part[k] = 0.0f;
+
+    // where this lane stores after the reductions: every lane one of the 16 main values (even quad positions
+    // Gaussian a, odd ones b); a few lanes one of the extra values (value 8, with ABS also 9 and 10)
+    const uint32_t row = lane >> 4, qpos = lane & 3u;
+    const uint32_t main_b = qpos & 1u;
+    float* const slot = s_part + (wave * 4u + g) * slot_stride;
+    float* const part_main = slot + (group_reduced16_index(lane) & 7u) * value_stride;
+    bool extra_lane;
+    uint32_t extra_b, extra_k;
+    if (ABS) {  // group_reduce8 of (wgb, e1, e2) of a then b: value u = 4 (i >> 1) + {0, 2, 1, 3}[r]
+        const uint32_t u = group_reduced8_index(lane);
+        extra_lane = (qpos & 1u) == 0 && u < 6u;
+        extra_b = u >= 3u ? 1u : 0u;
+        extra_k = 8u + (u >= 3u ? u - 3u : u);
+    } else {    // group_reduce2: rows 0, 1 hold a, rows 2, 3 hold b
+        extra_lane = qpos == 0 && (row == 0 || row == 2);
+        extra_b = row == 2 ? 1u : 0u;
+        extra_k = 8u;
+    }
+    float* const part_extra = slot + extra_k * value_stride;
 
     // pixel state: upstream gradient, (colour still to come) . g, background term
     float gr = 0.0f, gg = 0.0f, gb = 0.0f, A = 0.0f, gbg = 0.0f;
@@ -281,9 +346,9 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
     if (inside) {
         const uint32_t pix = py * a.width + px;
         const uint32_t np = a.width * a.height;
-        const uint32_t slot = tile * tile_pixels + tid;
-        const float Tf = a.final_T[slot];
-        last = a.n_contrib[slot];
+        const uint32_t pslot = tile * tile_pixels + tid;
+        const float Tf = a.final_T[pslot];
+        last = a.n_contrib[pslot];
         gr = a.grad_image[pix]; gg = a.grad_image[np + pix]; gb = a.grad_image[2 * np + pix];
         const float ar = a.image[pix] - Tf * a.bg[0];
         const float ag = a.image[np + pix] - Tf * a.bg[1];
@@ -294,78 +359,117 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
     const uint32_t wave_last = wave_max_u32(last);  // no pixel of the band uses instances at or after this
     float T = 1.0f;
 
-    uint32_t covered = 0;
-    for (uint32_t start = 0; start < n_proc; start += tile_pixels) {
-        __syncthreads();
-        const bool own = start + tid < n_total;
-        uint32_t e_own = 0;
-        float4 craw = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (own) {
-            e_own = a.sorted_inst[range.x + start + tid];
-            const PrimRecord rec = a.records[a.inst_prim[e_own]];
-            craw = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, 0.0f);
-            s_xy[tid] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
-            s_co[tid] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
-            s_col[tid] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
-            if (ABS) s_craw[tid] = craw;
+    // staging threads (lanes 0-31 of wave 0) fetch the record of their instance one batch ahead
+    uint32_t e_next = 0;
+    PrimRecord rec_next{};
+    const auto fetch = [&](uint32_t s) {
+        if (tid < batch && s + tid < n_total) {
+            e_next = a.sorted_inst[range.x + s + tid];
+            rec_next = a.records[a.inst_prim[e_next]];
         }
-        for (uint32_t k = tid; k < n_waves * n_values * grad_row / 4; k += tile_pixels) s_grad4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        __syncthreads();
-        const uint32_t batch_n = min(tile_pixels, n_total - start);
-        const uint32_t batch_wave = wave_last > start ? min(min(tile_pixels, n_proc - start), wave_last - start) : 0u;
-        for (uint32_t c0 = 0; c0 < batch_wave; c0 += 64) {
-            const uint32_t j = c0 + lane;
-            const bool ov = j < batch_wave && band_overlap(rect_of(s_xy[j]), bx0, bx1, by0, by1);
-            uint64_t mask = __ballot(ov);
-            // two Gaussians (a, b) per step share the transposing reductions; with an odd count the last b is
-            // a = b again, skipped by every pixel and not written
-            while (mask != 0) {
-                const uint32_t ja = c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1);
-                mask &= mask - 1;
-                const bool has_b = mask != 0;
-                const uint32_t jb = has_b ? c0 + static_cast<uint32_t>(__ffsll(static_cast<long long>(mask)) - 1) : ja;
-                mask &= mask - 1;
-                float dxa, dya, Ga, dxb, dyb, Gb;
-                const float alpha_a = eval_alpha(s_xy[ja], s_co[ja], pxf, pyf, dxa, dya, Ga);
-                const float alpha_b = eval_alpha(s_xy[jb], s_co[jb], pxf, pyf, dxb, dyb, Gb);
-                const bool contrib_a = start + ja < last && alpha_a >= min_alpha;
-                const bool contrib_b = has_b && start + jb < last && alpha_b >= min_alpha;
-                if (__ballot(contrib_a || contrib_b) == 0) continue;
-                float v[16], wgb_a, wgb_b, e1a = 0.0f, e2a = 0.0f, e1b = 0.0f, e2b = 0.0f;
-                const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                pair_terms<ABS>(contrib_a, alpha_a, Ga, dxa, dya, s_col[ja], ABS ? s_craw[ja] : zero4, gr, gg, gb, gbg, T, A,
-                                v, wgb_a, e1a, e2a);
-                pair_terms<ABS>(contrib_b, alpha_b, Gb, dxb, dyb, s_col[jb], ABS ? s_craw[jb] : zero4, gr, gg, gb, gbg, T, A,
-                                v + 8, wgb_b, e1b, e2b);
-                const float s16 = transpose_reduce16(v, lane);
-                const uint32_t k16 = reduced16_index(lane);
-                if ((lane & 3u) == 3u && (k16 < 8u || has_b)) s_grad[wave][k16 & 7u][k16 < 8u ? ja : jb] = s16;
-                if (ABS) {
-                    const float u[8] = {wgb_a, e1a, e2a, wgb_b, e1b, e2b, 0.0f, 0.0f};
-                    const float s8 = transpose_reduce8(u, lane);
-                    const uint32_t k8 = reduced8_index(lane);  // 0-2: values 8-10 of a, 3-5: of b
-                    if ((lane & 7u) == 7u && (k8 < 3u || (k8 < 6u && has_b)))
-                        s_grad[wave][8u + (k8 < 3u ? k8 : k8 - 3u)][k8 < 3u ? ja : jb] = s8;
-                } else {
-                    const float s2 = transpose_reduce2(wgb_a, wgb_b);
-                    if ((lane & 31u) == 15u && (lane < 32u || has_b)) s_grad[wave][8][lane < 32u ? ja : jb] = s2;
+    };
+    const auto stage = [&](uint32_t s, uint32_t buf) {
+        if (tid < batch && s + tid < n_total) {
+            const PrimRecord& rec = rec_next;
+            float4* st = s_stage[buf][tid];
+            st[0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
+            st[1] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
+            st[2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
+            st[3] = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, 0.0f);
+            s_emit[buf][tid] = e_next;
+        }
+    };
+    if (n_proc > 0) {
+        fetch(0);
+        stage(0, 0);
+        fetch(batch);
+    }
+
+    uint32_t covered = 0;
+    uint32_t buf = 0;
+    for (uint32_t start = 0; start < n_proc; start += batch, buf ^= 1u) {
+        __syncthreads();  // batch staged; the previous combine has read and cleared the slots
+        const uint32_t batch_wave = wave_last > start ? min(min(batch, n_proc - start), wave_last - start) : 0u;
+        uint64_t m[4];
+        cull_groups(rect_of(s_stage[buf][lane & (batch - 1)][0]), lane < batch_wave, bx0, by0, by1, m);
+        uint32_t n[4];
+        build_group_lists(m, lane, 0u, &s_list[wave][0][0], list_len, n);
+        wave_lds_fence();
+        const uint32_t n_max = __builtin_amdgcn_readfirstlane(max(max(n[0], n[1]), max(n[2], n[3])));
+        const uint32_t my_n = pick_group(g, n[0], n[1], n[2], n[3]);
+        // per-lane step bounds: Gaussian a of step k exists if k < my_n, b if k + 1 < my_n
+        const uint32_t n_main = my_n > main_b ? my_n - main_b : 0u;
+        const uint32_t n_extra = extra_lane && my_n > extra_b ? my_n - extra_b : 0u;
+        const uint32_t last_rel = last > start ? last - start : 0u;  // Gaussians j < last_rel are before `last`
+        const float4(*const stg)[4] = s_stage[buf];
+        for (uint32_t k = 0; k < n_max; k += 2) {
+            const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);  // past the count: stale, skipped
+            const uint32_t ja = jab.x, jb = jab.y;
+            float dxa, dya, Ga, dxb, dyb, Gb;
+            const float alpha_a = eval_alpha(stg[ja][0], stg[ja][1], pxf, pyf, dxa, dya, Ga);
+            const float alpha_b = eval_alpha(stg[jb][0], stg[jb][1], pxf, pyf, dxb, dyb, Gb);
+            const bool ca = k < my_n && ja < last_rel && alpha_a >= min_alpha;
+            const bool cb = k + 1 < my_n && jb < last_rel && alpha_b >= min_alpha;
+            float v[16], wgb_a, wgb_b, e1a = 0.0f, e2a = 0.0f, e1b = 0.0f, e2b = 0.0f;
+            const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            pair_terms<ABS>(ca, alpha_a, Ga, dxa, dya, stg[ja][2], ABS ? stg[ja][3] : zero4, gr, gg, gb, gbg, T, A, v, wgb_a,
+                            e1a, e2a);
+            pair_terms<ABS>(cb, alpha_b, Gb, dxb, dyb, stg[jb][2], ABS ? stg[jb][3] : zero4, gr, gg, gb, gbg, T, A, v + 8, wgb_b,
+                            e1b, e2b);
+            const float s16 = group_reduce16(v, lane);
+            if (k < n_main) part_main[main_b ? jb : ja] = s16;
+            float sx;
+            if (ABS) {
+                const float u[8] = {wgb_a, e1a, e2a, wgb_b, e1b, e2b, 0.0f, 0.0f};
+                sx = group_reduce8(u, lane);
+            } else {
+                sx = group_reduce2(wgb_a, wgb_b);
+            }
+            if (k < n_extra) part_extra[extra_b ? jb : ja] = sx;
+        }
+        wave_lds_fence();
+        __syncthreads();  // every group's sums are in its slots
+        // combine: thread (part p, instance j) adds the twelve slots of its two values in a fixed order,
+        // clears them, and writes its 8 bytes of the 48-byte record
+        const uint32_t j = tid & (batch - 1), p = tid / batch;  // p = 0..5: values 2p, 2p + 1
+        const uint32_t batch_n = min(batch, n_total - start);
+        if (j < batch_n) {
+            float r[2] = {0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t c = 0; c < 2; c++) {
+                const uint32_t k = 2u * p + c;
+                if (k < n_values) {
+                    float* src = s_part + k * value_stride + j;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (uint32_t q = 0; q < n_slots; q++) {
+                        acc += src[q * slot_stride];
+                        src[q * slot_stride] = 0.0f;
+                    }
+                    r[c] = acc;
                 }
             }
+            float2* out = reinterpret_cast<float2*>(a.inst_grads) + 6 * static_cast<size_t>(s_emit[buf][j]) + p;
+            float2 o;
+            if (p == 0) {
+                const float4 craw = s_stage[buf][j][3];
+                o = make_float2(__builtin_fmaf(craw.x, r[0], craw.y * r[1]), __builtin_fmaf(craw.y, r[0], craw.z * r[1]));
+            } else if (p == 1) {
+                o = make_float2(0.5f * r[0], 0.5f * r[1]);
+            } else if (p == 2) {
+                o = make_float2(0.5f * r[0], r[1]);
+            } else {
+                o = make_float2(r[0], r[1]);  // zero past the last value
+            }
+            *out = o;
         }
-        __syncthreads();
-        if (tid < batch_n) {
-            float r[11];
-#pragma unroll
-            for (uint32_t c = 0; c < n_values; c++) r[c] = (s_grad[0][c][tid] + s_grad[1][c][tid]) + s_grad[2][c][tid];
-            if (!ABS) r[9] = r[10] = 0.0f;
-            const float gmx = __builtin_fmaf(craw.x, r[0], craw.y * r[1]);
-            const float gmy = __builtin_fmaf(craw.y, r[0], craw.z * r[1]);
-            float4* out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(e_own);
-            out[0] = make_float4(gmx, gmy, 0.5f * r[2], 0.5f * r[3]);
-            out[1] = make_float4(0.5f * r[4], r[5], r[6], r[7]);
-            out[2] = make_float4(r[8], r[9], r[10], 0.0f);
+        covered = min(n_total, start + batch);
+        // stage the next batch into the other buffer (its last readers finished before this batch's first
+        // barrier) and fetch the one after it
+        if (start + batch < n_proc) {
+            stage(start + batch, buf ^ 1u);
+            fetch(start + 2 * batch);
         }
-        covered = min(n_total, start + tile_pixels);
     }
     // instances the tile never reached (after every pixel's last contributor) get zero records
     for (uint32_t k = covered + tid; k < n_total; k += tile_pixels) {
