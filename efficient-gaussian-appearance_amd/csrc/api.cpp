@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <sstream>
 #include <string>
 #include <vector>
 
@@ -149,9 +150,11 @@ struct efgs_rasterizer {
         hipFunction_t mlp = nullptr;  // neural backward: the MLP kernel of the same module
     };
     KernelSlot kernels[6][2];
+    KernelSlot decode;  // standalone neural decode: forward kernel + backward kernel (in `mlp`) of one module
     void clear_kernels() {
         for (auto& v : kernels)
             for (auto& k : v) k = KernelSlot{};
+        decode = KernelSlot{};
     }
 };
 
@@ -368,6 +371,46 @@ void kernel_source(const efgs_rasterizer* r, int model, const char* kind, std::s
         case 5: files.push_back("appearance_neural.h"); break;
     }
     files.push_back(std::string("preprocess_") + kind + ".hip");
+}
+
+// preamble tokens and source files of the standalone neural decode module (the configured MLP and encoding)
+void decode_source(const efgs_rasterizer* r, std::string& name, std::string& preamble, std::vector<std::string>& files) {
+    std::string unused, full;
+    kernel_source(r, 5, "forward", unused, full, files);
+    name = "neural_decode";
+    // the colour activations and the direction-gradient flag do not enter the decode: fixed tokens keep one
+    // cached code object per MLP configuration
+    preamble = "#define EFGS_KERNEL_NAME " + name + "\n";
+    std::istringstream lines(full);
+    std::string line;
+    while (std::getline(lines, line)) {
+        if (line.rfind("#define EFGS_KERNEL_NAME ", 0) == 0) continue;
+        for (const char* token : {"EFGS_BASE_ACT ", "EFGS_RES_ACT ", "EFGS_COLOR_ACT ", "EFGS_DIRECTION_GRADIENT "})
+            if (line.rfind(std::string("#define ") + token, 0) == 0) line = std::string("#define ") + token + "0";
+        preamble += line + "\n";
+    }
+    files.back() = "neural_decode.hip";
+}
+
+bool get_decode_kernels(efgs_rasterizer* r, RtcKernel& forward, hipFunction_t& backward) {
+    int device = 0;
+    EFGS_HIP_CHECK(hipGetDevice(&device));
+    efgs_rasterizer::KernelSlot& slot = r->decode;
+    if (slot.device != device || !slot.kernel.function) {
+        std::string name, preamble;
+        std::vector<std::string> files;
+        decode_source(r, name, preamble, files);
+        RtcKernel loaded;
+        if (!rtc_get_kernel(name, preamble, files, loaded)) return false;
+        hipFunction_t bwd = nullptr;
+        EFGS_HIP_CHECK(hipModuleGetFunction(&bwd, loaded.module, (name + "_backward").c_str()));
+        slot.kernel = loaded;
+        slot.mlp = bwd;
+        slot.device = device;
+    }
+    forward = slot.kernel;
+    backward = slot.mlp;
+    return true;
 }
 
 // the specialised preprocess kernel (forward or backward) of `model`, compiled or loaded once per device and
@@ -887,6 +930,80 @@ int efgs_get_frame_views(const efgs_frame* frame, efgs_frame_views* v) {
     return EFGS_OK;
 }
 
+namespace {
+
+int check_decode(const efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                 const uint16_t* mlp_weights, int degree) {
+    if (!r) return fail(EFGS_ERR_INVALID_ARGUMENT, "null rasterizer");
+    if (!r->appearance_set || r->model != 5 || !r->mlp_set)
+        return fail(EFGS_ERR_STATE, "the neural decode needs the neural model and its residual mlp (efgs_set_residual_mlp)");
+    if (n < 0 || n >= (1ll << 31)) return fail(EFGS_ERR_INVALID_ARGUMENT, "n out of range");
+    if (degree < 0) return fail(EFGS_ERR_INVALID_ARGUMENT, "negative degree");
+    if (n > 0) {
+        if (!dirs || !mlp_weights || (r->mlp_n_features > 0 && !features)) return fail(EFGS_ERR_INVALID_ARGUMENT, "null input");
+        if (r->mlp_base_input && !base) return fail(EFGS_ERR_INVALID_ARGUMENT, "base colours are required with base input");
+        if ((reinterpret_cast<uintptr_t>(mlp_weights) & 15u) != 0) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp_weights must be 16-byte aligned");
+    }
+    return EFGS_OK;
+}
+
+NeuralDecodeArgs decode_args(int64_t n, const float* features, const float* base, const float* dirs, const uint16_t* mlp_weights, int degree) {
+    NeuralDecodeArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.features = features;
+    a.base = base;
+    a.dirs = dirs;
+    a.mlp_weights = mlp_weights;
+    a.n = static_cast<uint32_t>(n);
+    a.degree = static_cast<uint32_t>(degree);
+    return a;
+}
+
+}  // namespace
+
+int efgs_neural_decode_forward(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                               const uint16_t* mlp_weights, int degree, float* out, void* stream) {
+    if (int c = check_decode(r, n, features, base, dirs, mlp_weights, degree)) return c;
+    if (n > 0 && !out) return fail(EFGS_ERR_INVALID_ARGUMENT, "null output");
+    if (n == 0) return EFGS_OK;
+    RtcKernel fwd;
+    hipFunction_t bwd = nullptr;
+    if (!get_decode_kernels(r, fwd, bwd)) return EFGS_ERR_RTC;
+    NeuralDecodeArgs a = decode_args(n, features, base, dirs, mlp_weights, degree);
+    a.out = out;
+    const uint32_t chunks = div_up(static_cast<uint64_t>(n), preprocess_block);
+    const uint32_t blocks = chunks < neural_forward_blocks ? chunks : neural_forward_blocks;
+    if (!launch_rtc(fwd, blocks, preprocess_block, mlp_smem_forward(mlp_shape(r)), &a, static_cast<hipStream_t>(stream))) return EFGS_ERR_HIP;
+    return EFGS_OK;
+}
+
+int efgs_neural_decode_backward(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                                const uint16_t* mlp_weights, int degree, const float* grad_out, float* g_features, float* g_base,
+                                float* g_dirs, float* g_mlp_weights, efgs_alloc_fn alloc, void* alloc_ctx, void* stream) {
+    if (int c = check_decode(r, n, features, base, dirs, mlp_weights, degree)) return c;
+    if (!g_mlp_weights || !alloc) return fail(EFGS_ERR_INVALID_ARGUMENT, "null weight gradient output or allocator");
+    if (n > 0 && (!grad_out || (r->mlp_n_features > 0 && !g_features))) return fail(EFGS_ERR_INVALID_ARGUMENT, "null gradient argument");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t params = mlp_params(mlp_shape(r));
+    if (n == 0) return launch_fill_u32(reinterpret_cast<uint32_t*>(g_mlp_weights), 0u, params, s) ? EFGS_OK : EFGS_ERR_HIP;
+    RtcKernel fwd;
+    hipFunction_t bwd = nullptr;
+    if (!get_decode_kernels(r, fwd, bwd)) return EFGS_ERR_RTC;
+    const uint32_t chunks = div_up(static_cast<uint64_t>(n), preprocess_block);
+    const uint32_t blocks = chunks < neural_backward_blocks ? chunks : neural_backward_blocks;
+    float* partials = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(blocks) * params * sizeof(float)));
+    if (!partials) return fail(EFGS_ERR_ALLOC, "allocation of the mlp gradient partials failed");
+    NeuralDecodeArgs a = decode_args(n, features, base, dirs, mlp_weights, degree);
+    a.grad_out = grad_out;
+    a.g_features = g_features;
+    a.g_base = r->mlp_base_input ? g_base : nullptr;
+    a.g_dirs = g_dirs;
+    a.g_mlp_partials = partials;
+    if (!launch_function(bwd, blocks, preprocess_block, mlp_smem_backward(mlp_shape(r)), &a, s)) return EFGS_ERR_HIP;
+    if (!launch_reduce_partials(partials, blocks, params, g_mlp_weights, s)) return EFGS_ERR_HIP;
+    return EFGS_OK;
+}
+
 int efgs_precompile(const efgs_rasterizer* r, const char* arch) {
     if (!r || !arch) return fail(EFGS_ERR_INVALID_ARGUMENT, "null argument");
     std::vector<int> variants = {0};
@@ -898,6 +1015,12 @@ int efgs_precompile(const efgs_rasterizer* r, const char* arch) {
             kernel_source(r, variant, kind, name, preamble, files);
             if (!rtc_precompile(name, preamble, files, arch)) return EFGS_ERR_RTC;
         }
+    }
+    if (r->appearance_set && r->model == 5 && r->mlp_set) {
+        std::string name, preamble;
+        std::vector<std::string> files;
+        decode_source(r, name, preamble, files);
+        if (!rtc_precompile(name, preamble, files, arch)) return EFGS_ERR_RTC;
     }
     return EFGS_OK;
 }

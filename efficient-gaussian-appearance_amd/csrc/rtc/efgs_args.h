@@ -69,4 +69,19 @@ struct PreprocessBackwardArgs {
     CameraArgs cam;
 };
 
+struct NeuralDecodeArgs {
+    const float* features;           // (N x n_features) learned per-primitive features
+    const float* base;               // (N x 3) base colours (read with base input only)
+    const float* dirs;               // (N x 3) unit view directions
+    const uint16_t* mlp_weights;     // fp16 bits, flat tcnn layout, 16-byte aligned
+    const float* grad_out;           // backward: (N x 3) dL/d(raw MLP output)
+    float* out;                      // forward: (N x 3) raw MLP outputs (fp16-rounded values)
+    float* g_features;               // backward: (N x n_features) written
+    float* g_base;                   // backward: (N x 3) written with base input, or null
+    float* g_dirs;                   // backward: (N x 3) dL/d(direction) through the SH encoding, or null
+    float* g_mlp_partials;           // backward: (blocks x n_params) per-block weight gradient partials
+    uint32_t n;
+    uint32_t degree;                 // active SH degree count of the direction encoding
+};
+
 }  // namespace efgs

@@ -1,0 +1,175 @@
+// Standalone neural decode: the configured residual MLP on per-primitive features and unit view directions,
+// outside the rasterizer (tokens as the neural preprocess kernels: EFGS_KERNEL_NAME, the MLP shape, the
+// feature encoding and the SH degree mask). Inputs are encoded exactly as in the preprocess kernels (frequency
+// encoding of the features, optional base colour input, SH degree values of the direction), so the decode
+// computes the raw MLP outputs that the rasterizer adds (after the residual activation) to the base colour.
+//
+//   EFGS_KERNEL_NAME            forward: out = MLP(x), fp16 MFMA with fp32 accumulation, outputs rounded to
+//                               fp16 (one wave per 64 primitives, persistent grid, weights in LDS)
+//   EFGS_KERNEL_NAME_backward   recomputes the forward in both tile orientations and backpropagates
+//                               grad_out: feature, base-input and direction gradients per primitive, weight
+//                               gradients as one fp32 partial per block (reduced by reduce_partials_kernel)
+//
+// Reference: the tiny-cuda-nn JIT MLP the reference calls per primitive (eval_model / backward_eval_model,
+// B/rasterization/rtc/appearance_neural.cuh:308-407), here as a kernel of its own so that the decode can be
+// measured and tested in isolation.
+#define EFGS_CAT2(a, b) a##b
+#define EFGS_CAT(a, b) EFGS_CAT2(a, b)
+
+namespace efgs {
+constexpr uint32_t decode_block = 256;
+}  // namespace efgs
+
+extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::NeuralDecodeArgs a) {
+    using namespace efgs;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES) + wave * 64 * nn::XS;
+    nn::load_dual_weights<decode_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
+    __syncthreads();
+    const uint32_t n_chunks = (a.n + decode_block - 1) / decode_block;
+    for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
+        const uint32_t p = chunk * decode_block + threadIdx.x;
+        const bool active = p < a.n;
+        if (__ballot(active) == 0) continue;  // wave-uniform: the tail of the last chunk
+        float x[nn::INP];
+        if (active) {
+            const float3 d = make_float3(a.dirs[3 * p], a.dirs[3 * p + 1], a.dirs[3 * p + 2]);
+            nn::mlp_input(a.features + static_cast<size_t>(p) * nn::FEATURES, EFGS_BASE_INPUT ? a.base + 3 * static_cast<size_t>(p) : nullptr,
+                          d, a.degree, x);
+        } else {
+#pragma unroll
+            for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
+        }
+        uint32_t masks[nn::NL][nn::MASK_WORDS];
+        nn::h4 unused[nn::NL][4][nn::KT];
+        nn::h4 unused_x[nn::INP / 16][4];
+        float y[3];
+        nn::mlp_forward_tiles<false>(WL, stage, x, masks, unused, unused_x, nullptr, y, lane);
+        if (active) {
+            a.out[3 * p] = y[0];
+            a.out[3 * p + 1] = y[1];
+            a.out[3 * p + 2] = y[2];
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_CAT(EFGS_KERNEL_NAME, _backward)(efgs::NeuralDecodeArgs a) {
+    using namespace efgs;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES + wave * nn::DUAL_STAGE_BYTES);
+    nn::h4* ustore = reinterpret_cast<nn::h4*>(smem + nn::DUAL_WEIGHT_BYTES + 4 * nn::DUAL_STAGE_BYTES + wave * nn::U_STORE_BYTES);
+    nn::load_dual_weights<decode_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
+
+    nn::f4 dW[nn::NL][nn::NT > 1 ? nn::NT : 1][nn::KT];
+#pragma unroll
+    for (uint32_t l = 0; l < nn::NL; l++)
+#pragma unroll
+        for (uint32_t rb = 0; rb < (nn::NT > 1 ? nn::NT : 1); rb++)
+#pragma unroll
+            for (uint32_t cb = 0; cb < nn::KT; cb++) dW[l][rb][cb] = nn::f4_zero();
+
+    // one gradient scale per block: 2^(8 - e) with e the exponent of the largest |grad_out| among the
+    // block's primitives (its chunks are read once here, 8 loads in flight per thread)
+    const uint32_t n_chunks = (a.n + decode_block - 1) / decode_block;
+    __shared__ float s_wave_max[decode_block / 64];
+    {
+        float m = 0.0f;
+        for (uint32_t c0 = blockIdx.x; c0 < n_chunks; c0 += 8 * gridDim.x) {
+            float v[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++) {
+                const uint32_t c = c0 + k * gridDim.x;
+                const uint32_t p = c * decode_block + threadIdx.x;
+                v[k] = c < n_chunks && p < a.n
+                           ? fmaxf(fmaxf(fabsf(a.grad_out[3 * p]), fabsf(a.grad_out[3 * p + 1])), fabsf(a.grad_out[3 * p + 2]))
+                           : 0.0f;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++) m = fmaxf(m, v[k]);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        if (lane == 0) s_wave_max[wave] = m;
+    }
+    __syncthreads();  // weights staged, wave maxima written
+    float gmax = 0.0f;
+#pragma unroll
+    for (uint32_t w = 0; w < decode_block / 64; w++) gmax = fmaxf(gmax, s_wave_max[w]);
+    // (scale 1 when the bound is zero or not finite: non-finite gradients then propagate as they are)
+    const bool finite = gmax > 0.0f && gmax < 3.0e38f;
+    const int e = finite ? max(ilogbf(gmax), -110) : 8;  // the clamp keeps 2^(8 - e) finite for denormal maxima
+    const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
+
+    for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
+        const uint32_t p = chunk * decode_block + threadIdx.x;
+        const bool active = p < a.n;
+        if (__ballot(active) == 0) continue;  // wave-uniform: the tail of the last chunk
+        const uint32_t pp = active ? p : 0u;
+        const float3 d = make_float3(a.dirs[3 * pp], a.dirs[3 * pp + 1], a.dirs[3 * pp + 2]);
+        const float* feat = a.features + static_cast<size_t>(pp) * nn::FEATURES;
+        const float* base = EFGS_BASE_INPUT ? a.base + 3 * static_cast<size_t>(pp) : nullptr;
+        float x[nn::INP];
+        nn::mlp_input(feat, base, d, a.degree, x);
+        if (!active) {
+#pragma unroll
+            for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
+        }
+        uint32_t Tm[nn::NL][nn::MASK_WORDS];
+        nn::h4 U[nn::NL][4][nn::KT];
+        nn::h4 X[nn::INP / 16][4];
+        float y[3];
+        nn::mlp_forward_tiles<true>(WL, stage, x, Tm, U, X, ustore, y, lane);
+        float dy[3] = {0.0f, 0.0f, 0.0f};
+        if (active) {
+            dy[0] = a.grad_out[3 * p];
+            dy[1] = a.grad_out[3 * p + 1];
+            dy[2] = a.grad_out[3 * p + 2];
+        }
+        float dx[nn::INP];
+        nn::mlp_backward_dual(WL, stage, Tm, U, X, ustore, dy, s, inv_s, dx, dW, lane);
+        if (active) {
+            float* gf = a.g_features + static_cast<size_t>(p) * nn::FEATURES;
+#pragma unroll
+            for (uint32_t i = 0; i < nn::FEATURES; i++) gf[i] = nn::feature_grad(feat[i], dx, i);
+            if (EFGS_BASE_INPUT && a.g_base) {
+#pragma unroll
+                for (uint32_t c = 0; c < 3; c++) a.g_base[3 * p + c] = nn::feature_grad(base[c], dx, nn::FEATURES + c);
+            }
+            if (a.g_dirs) {
+                const float3 gd = nn::direction_grad(d, a.degree, dx);
+                a.g_dirs[3 * p] = gd.x;
+                a.g_dirs[3 * p + 1] = gd.y;
+                a.g_dirs[3 * p + 2] = gd.z;
+            }
+        }
+    }
+
+    // block sum of the four waves' weight gradients, in wave order, then one partial per block
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);
+    const uint32_t r = lane & 15u, q = lane >> 4;
+    for (uint32_t w = 0; w < decode_block / 64; w++) {
+        if (wave == w) {
+#pragma unroll
+            for (uint32_t l = 0; l < nn::NL; l++)
+#pragma unroll
+                for (uint32_t rb = 0; rb < nn::lout(l) / 16; rb++)
+#pragma unroll
+                    for (uint32_t cb = 0; cb < nn::lin(l) / 16; cb++)
+#pragma unroll
+                        for (uint32_t i = 0; i < 4; i++) {
+                            const uint32_t idx = nn::loff(l) + (rb * 16 + 4 * q + i) * nn::lin(l) + cb * 16 + r;
+                            red[idx] = (w == 0 ? 0.0f : red[idx]) + dW[l][rb][cb][i] * inv_s;
+                        }
+        }
+        __syncthreads();
+    }
+    float* out = a.g_mlp_partials + static_cast<size_t>(blockIdx.x) * nn::PARAMS;
+    for (uint32_t i = threadIdx.x; i < nn::PARAMS; i += decode_block) out[i] = red[i];
+}

@@ -74,7 +74,8 @@ lib = ctypes.CDLL(LIB_PATH)
 
 EXPORTED = ('efgs_last_error', 'efgs_set_rtc_dirs', 'efgs_rasterizer_create', 'efgs_rasterizer_destroy', 'efgs_set_appearance',
             'efgs_set_residual_mlp', 'efgs_mlp_param_count', 'efgs_forward', 'efgs_backward', 'efgs_adam_step',
-            'efgs_get_frame_views', 'efgs_precompile', 'efgs_set_stage_timing', 'efgs_get_stage_times', 'efgs_workspace_alloc')
+            'efgs_get_frame_views', 'efgs_precompile', 'efgs_set_stage_timing', 'efgs_get_stage_times', 'efgs_workspace_alloc',
+            'efgs_neural_decode_forward', 'efgs_neural_decode_backward')
 
 # stage ids of efgs_get_stage_times, in order (include/efgs.h)
 STAGES = ('preprocess_forward', 'compact', 'counter_read', 'depth_sort', 'instance_offsets', 'create_instances', 'tile_sort',
@@ -102,6 +103,10 @@ lib.efgs_workspace_alloc.restype = ctypes.c_void_p
 lib.efgs_workspace_alloc.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
 WORKSPACE_ALLOC = ctypes.cast(lib.efgs_workspace_alloc, ALLOC_FN)  # C function: no Python per allocation
 lib.efgs_get_stage_times.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64), ctypes.c_int]
+lib.efgs_neural_decode_forward.argtypes = [ctypes.c_void_p, ctypes.c_int64] + [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p,
+                                                                                                      ctypes.c_void_p]
+lib.efgs_neural_decode_backward.argtypes = ([ctypes.c_void_p, ctypes.c_int64] + [ctypes.c_void_p] * 4 + [ctypes.c_int] +
+                                            [ctypes.c_void_p] * 5 + [ALLOC_FN, ctypes.c_void_p, ctypes.c_void_p])
 
 
 def check(rc: int) -> None:

@@ -285,6 +285,62 @@ def rasterize(means: torch.Tensor, scales: torch.Tensor, rotations: torch.Tensor
     return image if to_chw else image.permute(1, 2, 0).contiguous()
 
 
+class _NeuralDecode(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, features, dirs, mlp_weights, base, degree: int) -> torch.Tensor:
+        device = features.device
+        mlp_half = mlp_weights.detach().half().contiguous()
+        n = int(dirs.shape[0])
+        out = torch.empty((n, 3), dtype=torch.float32, device=device)
+        with torch.cuda.device(device):
+            check(lib.efgs_neural_decode_forward(_rasterizer.handle, n, _ptr(features), _ptr(base), _ptr(dirs), _ptr(mlp_half), int(degree),
+                                                 _ptr(out), _stream(device)))
+        ctx.degree = int(degree)
+        ctx.mlp_numel = mlp_weights.numel()
+        ctx.save_for_backward(features, dirs, mlp_half, base)
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, grad_out: torch.Tensor):
+        features, dirs, mlp_half, base = ctx.saved_tensors
+        device = features.device
+        n = int(dirs.shape[0])
+        grad_out = grad_out.contiguous()
+        g_features = torch.empty_like(features)
+        g_dirs = torch.empty_like(dirs)
+        g_base = torch.empty_like(base)
+        g_mlp = torch.empty(ctx.mlp_numel, dtype=torch.float32, device=device)
+        with torch.cuda.device(device):
+            alloc = _lib.WorkspaceAllocator(device, 'decode')
+            check(lib.efgs_neural_decode_backward(_rasterizer.handle, n, _ptr(features), _ptr(base), _ptr(dirs), _ptr(mlp_half), ctx.degree,
+                                                  _ptr(grad_out), _ptr(g_features), _ptr(g_base), _ptr(g_dirs), _ptr(g_mlp), alloc.fn,
+                                                  alloc.ctx, _stream(device)))
+            alloc.done()
+        return (g_features if features.numel() > 0 else None, g_dirs, g_mlp, g_base if base.numel() > 0 else None, None)
+
+
+def neural_decode(features: torch.Tensor, dirs: torch.Tensor, mlp_weights: torch.Tensor, degree: int = 1,
+                  base_colors: torch.Tensor | None = None) -> torch.Tensor:
+    """Differentiable standalone decode of the configured residual MLP (initialize_residual_mlp): raw outputs
+    (N, 3) for features (N, n_features), unit view directions (N, 3) and the tcnn-flat fp32 master weights
+    (cast to fp16 per call, as in diff_rasterize); degree gates the direction's SH degrees as the appearance
+    degree does in the rasterizer. Gradients flow to the features, the directions, the weights and (with base
+    input) the base colours. No counterpart in the reference's Python API: its tiny-cuda-nn MLP runs only inside
+    the preprocess kernels."""
+    d = features.device
+    if d.type != 'cuda':
+        raise ValueError('efgs: the neural decode runs on a GPU device')
+    base = base_colors if base_colors is not None else _empty(d)
+    for name, t in (('features', features), ('dirs', dirs), ('mlp_weights', mlp_weights), ('base_colors', base)):
+        _check_param(name, t, d)
+    if dirs.dim() != 2 or dirs.shape[1] != 3:
+        raise ValueError('efgs: dirs must be (N, 3)')
+    if mlp_weights.numel() != _rasterizer.mlp_param_count():
+        raise ValueError(f'efgs: mlp_weights must hold {_rasterizer.mlp_param_count()} parameters, got {mlp_weights.numel()}')
+    return _NeuralDecode.apply(features, dirs, mlp_weights, base, degree)
+
+
 def update_pruning_scores(*args, **kwargs):
     """Speedy-Splat pruning scores are not part of this build (reference: kernels_pruning_scores.cuh)."""
     raise NotImplementedError('efgs: update_pruning_scores is not implemented in this build')

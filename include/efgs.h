@@ -174,6 +174,22 @@ typedef struct efgs_adam_group {
 } efgs_adam_group;
 int efgs_adam_step(const efgs_adam_group* groups, int n_groups, void* stream);
 
+/* Standalone neural decode: the configured residual MLP (efgs_set_residual_mlp, model 5) on n primitives'
+ * features (n x n_features, the learned latents), base colours (n x 3, read with base input only) and unit
+ * view directions (n x 3), encoded as in the rasterizer (frequency encoding, SH degree values of the
+ * direction gated by `degree`). Forward writes the raw MLP outputs (n x 3, fp16-rounded values) to `out`.
+ * Backward takes dL/d(outputs) (n x 3) and writes the feature gradients (n x n_features), the base-input
+ * gradients (n x 3, with base input; may be NULL), the direction gradients (n x 3; may be NULL) and the fp32
+ * weight gradients (efgs_mlp_param_count entries); it allocates its per-block partials through `alloc`.
+ * Stream-ordered, no host synchronisation. The reference has no Python entry point for this: it is the
+ * tiny-cuda-nn MLP that B/rasterization/rtc/appearance_neural.cuh:308-407 calls per primitive
+ * (eval_model / backward_eval_model), exposed to measure and test the decode in isolation. */
+int efgs_neural_decode_forward(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                               const uint16_t* mlp_weights, int degree, float* out, void* stream);
+int efgs_neural_decode_backward(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                                const uint16_t* mlp_weights, int degree, const float* grad_out, float* g_features, float* g_base,
+                                float* g_dirs, float* g_mlp_weights, efgs_alloc_fn alloc, void* alloc_ctx, void* stream);
+
 /* Device pointers into a frame's buffers, for inspection (no counterpart in the reference: it lets parity
  * tests compare keys, orders and tile ranges with the CPU oracle). */
 typedef struct efgs_frame_views {

@@ -421,6 +421,48 @@ def frequency_encode_grad(feat: np.ndarray, denc: np.ndarray, n_freq: int) -> np
     return (scale * (np.cos(s) * d[..., 0] - np.sin(s) * d[..., 1])).sum(-1).astype(np.float32)
 
 
+def decode_inputs(features: np.ndarray, base: np.ndarray | None, dirs: np.ndarray, mlp: MLPConfig,
+                  active_degree: int) -> np.ndarray:
+    """MLP input rows of the standalone decode: the rasterizer's encoding (mlp_inputs) with the view
+    directions given instead of derived from means and camera."""
+    n = dirs.shape[0]
+    feats = features.reshape(n, -1).astype(np.float32)
+    if mlp.base_input:
+        feats = np.concatenate([feats, base.astype(np.float32)], axis=1)
+    x = np.concatenate([frequency_encode(feats, mlp.n_frequencies),
+                        sh_degree_encoding(dirs.astype(np.float32), mlp.sh_degrees, active_degree)], axis=1)
+    pad = mlp.n_input_padded - x.shape[1]
+    if pad:
+        x = np.concatenate([x, np.zeros((n, pad), np.float32)], axis=1)
+    return x.astype(np.float32)
+
+
+def neural_decode(features, base, dirs, weights, mlp: MLPConfig, active_degree: int):
+    """Raw MLP outputs (n, 3) of the per-primitive decode (tiny-cuda-nn eval_model as called from
+    B/rasterization/rtc/appearance_neural.cuh:308-339), with the per-layer activations and the matrices."""
+    mats = mlp_matrices(weights, mlp)
+    y, acts = mlp_forward(decode_inputs(features, base, dirs, mlp, active_degree), mats)
+    return y, acts, mats
+
+
+def neural_decode_backward(features, base, dirs, dy, mats, acts, mlp: MLPConfig, active_degree: int) -> dict:
+    """Gradients of the decode (backward_eval_model + encoding chain, B/rasterization/rtc/appearance_neural.cuh:348-407):
+    features (n, n_feature_dims), base (n, 3) with base input, dirs (n, 3) through the SH degree values, and
+    the flat tcnn-layout weight gradients."""
+    n = dirs.shape[0]
+    dx, dW = mlp_backward(dy.astype(np.float32), mats, acts)
+    feats = features.reshape(n, -1).astype(np.float32)
+    raw = np.concatenate([feats, base.astype(np.float32)], 1) if mlp.base_input else feats
+    dfeat = frequency_encode_grad(raw, dx[:, :mlp.n_encoded_feature_dims], mlp.n_frequencies)
+    out = dict(features=dfeat[:, :mlp.n_feature_dims].copy(),
+               weights=np.concatenate([g.reshape(-1) for g in dW]).astype(np.float32),
+               dirs=sh_degree_encoding_grad(dirs.astype(np.float32), dx[:, mlp.n_encoded_feature_dims:mlp.n_input_dims],
+                                            mlp.sh_degrees, active_degree))
+    if mlp.base_input:
+        out['base'] = dfeat[:, mlp.n_feature_dims:mlp.n_feature_dims + 3].copy()
+    return out
+
+
 # ---------------------------------------------------------------------------------------------------------
 # full pipeline
 # ---------------------------------------------------------------------------------------------------------

@@ -257,3 +257,36 @@ def test_forward_state_invariants():
     assert np.all(fw.n_touched <= np.maximum(area, 0))
     # transmittance in [0, 1]; empty tiles show the background
     assert fw.final_T.min() >= 0 and fw.final_T.max() <= 1
+
+
+DECODE_MLPS = {
+    'c2': dict(n_feature_dims=8, n_frequencies=0, sh_degrees=(1,), n_neurons=64, n_hidden_layers=2, base_input=False),
+    'base_freq': dict(n_feature_dims=5, n_frequencies=1, sh_degrees=(0, 1, 2, 3), n_neurons=32, n_hidden_layers=3, base_input=True),
+}
+
+
+@pytest.mark.parametrize('name', list(DECODE_MLPS))
+def test_neural_decode_matches_autograd(name):
+    """The standalone decode statement (encoding + fp16 MLP + their backward) against autograd of the
+    independent torch restatement (straight-through fp16 rounding), in float64."""
+    from efgs.synthetic import xavier_mlp
+    mlp = O.MLPConfig(**DECODE_MLPS[name])
+    rng = np.random.default_rng(11)
+    n = 400
+    feat = rng.normal(0.0, 0.5, size=(n, mlp.n_feature_dims)).astype(np.float32)
+    base = rng.normal(0.0, 0.5, size=(n, 3)).astype(np.float32)
+    d = rng.normal(size=(n, 3)).astype(np.float32)
+    d /= np.linalg.norm(d, axis=1, keepdims=True)
+    w = xavier_mlp(rng, mlp.n_input_dims, mlp.n_neurons, mlp.n_hidden_layers)
+    dy = rng.normal(size=(n, 3)).astype(np.float32)
+    y, acts, mats = O.neural_decode(feat, base, d, w, mlp, 1)
+    ref = O.neural_decode_backward(feat, base, d, dy, mats, acts, mlp, 1)
+    tf, tb, td, tw = (torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (feat, base, d, w))
+    out = TR.neural_residual(tf, tb, td, mlp, TR.mlp_matrices_torch(tw, mlp), 1, 'none')
+    assert np.abs(out.detach().numpy() - y).max() < 2e-3
+    (out * torch.tensor(dy, dtype=torch.float64)).sum().backward()
+    assert rel_l2(ref['features'], tf.grad.numpy()) < 1e-4
+    assert rel_l2(ref['weights'], tw.grad.numpy()) < 1e-4
+    assert rel_l2(ref['dirs'], td.grad.numpy()) < 1e-4
+    if mlp.base_input:
+        assert rel_l2(ref['base'], tb.grad.numpy()) < 1e-4
