@@ -15,6 +15,7 @@ around each stage on the stream it launches on (Adam: events around FusedAdam.st
 the same scene on the host.
 
   python bench.py [--steps K] [--warmup W] [--config c3|c1|c4_sv|c4_nasg|c4_nasgabor] [--no-cpu-baseline]
+  python bench.py --config c2    # the neural decode alone: 1M primitives, forward + backward (latents, weights)
   python bench.py --copy-calibration    # a plain 1 GiB device copy, for scaling rocprofv3 FETCH/WRITE_SIZE
 """
 from __future__ import annotations
@@ -39,11 +40,10 @@ TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'traffic_c3_neural.txt')
 STAGE_KERNELS = {
     'preprocess_forward': 'preprocess_forward_<model>',
     'compact': 'scan_block_counts_kernel + compact_visible_kernel',
-    'depth_sort': 'sort_histogram_kernel + sort_scatter_kernel (4 passes)',
-    'instance_offsets': 'scan_reduce + scan_block_sums + scan_downsweep',
     'create_instances': 'create_instances_kernel',
-    'tile_sort': 'sort_histogram_kernel + sort_scatter_kernel (2 passes)',
-    'tile_ranges': 'tile_ranges_kernel',
+    'tile_offsets': 'tile_offsets_kernel',
+    'tile_buckets': 'tile_buckets_kernel',
+    'tile_sort': 'tile_sort_kernel',
     'blend_forward': 'blend_forward_kernel',
     'blend_backward': 'blend_backward_kernel',
     'preprocess_backward': 'preprocess_backward_<model>',
@@ -87,20 +87,21 @@ def mlp_flops_per_primitive(n_in: int, n_neurons: int, n_hidden: int, n_out: int
 
 def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_fwd_flops: int, adam_elements: int):
     """(bytes, flops) of one launch of `stage`. Per-unit figures: preprocess N*(60+R) + V*52 split into the
-    preprocess kernel (N*(60+R) + V*44) and the compaction (V*8 key/index pairs); depth sort V*16, offsets
-    scan V*8; instances V*40 + I*6, tile sort I*12, ranges T*8; blend forward I*48 + P*20; blend backward
-    P*32 + I*76; preprocess backward V*(110+R) + N*(56+R), for the neural model split into the geometry
-    kernel (V*110 + N*56 + (N-V)*R: culled primitives' zero latent gradients) and the MLP kernel (V*2R:
-    latents in, latent gradients out); Adam 28 B per element. MLP FLOPs: forward V*F, backward (input and
-    weight gradients, forward recomputed) 2*V*F, F = unpadded forward FLOPs per primitive."""
+    preprocess kernel (N*(60+R) + V*44) and the compaction (V*8: visible list and emission offsets); instance
+    emission V*40 + I*6, tile ranges T*8; the ordering by (tile, depth) -- the reference's depth sort and
+    offset scan (V*24) and tile sort (I*12) -- split into the bucketing (I*6: tile key in, emission index
+    out) and the per-tile sort (I*6 + V*24); blend forward I*48 + P*20; blend backward P*32 + I*76;
+    preprocess backward V*(110+R) + N*(56+R), for the neural model split into the geometry kernel
+    (V*110 + N*56 + (N-V)*R: culled primitives' zero latent gradients) and the MLP kernel (V*2R: latents in,
+    latent gradients out); Adam 28 B per element. MLP FLOPs: forward V*F, backward (input and weight
+    gradients, forward recomputed) 2*V*F, F = unpadded forward FLOPs per primitive."""
     table = {
         'preprocess_forward': (N * (60 + R) + V * 44, V * mlp_fwd_flops),
         'compact': (V * 8, 0),
-        'depth_sort': (V * 16, 0),
-        'instance_offsets': (V * 8, 0),
         'create_instances': (V * 40 + I * 6, 0),
-        'tile_sort': (I * 12, 0),
-        'tile_ranges': (T * 8, 0),
+        'tile_offsets': (T * 8, 0),
+        'tile_buckets': (I * 6, 0),
+        'tile_sort': (I * 6 + V * 24, 0),
         'blend_forward': (I * 48 + P * 20, 0),
         'blend_backward': (P * 32 + I * 76, 0),
         'preprocess_backward': ((V * 110 + N * 56 + (N - V) * R, 0) if mlp_fwd_flops
@@ -304,6 +305,110 @@ def cpu_baseline(sc: dict) -> dict:
                       f'through the C/numpy CPU restatement, single thread, no Adam; {seconds:.1f} s'}
 
 
+# ---------------------------------------------------------------------------------------------------------
+# c2: the neural decode in isolation
+# ---------------------------------------------------------------------------------------------------------
+
+def c2_inputs(n: int = 1_000_000, seed: int = 0):
+    """Configuration c2: latents N(0, 0.1) (n, 8), directions normalize(N(0, 1)^3), the 11 -> 64 -> 64 -> 3
+    Xavier fp16 MLP (tcnn flat layout), upstream gradients N(0, 1) (n, 3); draw order as listed."""
+    import numpy as np
+    from efgs.synthetic import NEURAL_MLP, xavier_mlp
+    rng = np.random.default_rng(seed)
+    m = NEURAL_MLP
+    n_in = m['n_feature_dims'] + sum(2 * d + 1 for d in m['sh_degrees'])
+    feat = rng.normal(0.0, 0.1, size=(n, m['n_feature_dims'])).astype(np.float32)
+    d = rng.normal(0.0, 1.0, size=(n, 3)).astype(np.float32)
+    d /= np.maximum(np.linalg.norm(d, axis=1, keepdims=True), 1e-12)
+    w = xavier_mlp(rng, n_in, m['n_neurons'], m['n_hidden_layers'])
+    dy = rng.normal(0.0, 1.0, size=(n, 3)).astype(np.float32)
+    return m, n_in, feat, d.astype(np.float32), w, dy
+
+
+def decode_benchmark(args) -> None:
+    import numpy as np
+    import torch
+    import efgs
+    from efgs.rasterization import neural_decode
+    device = torch.device('cuda:0')
+    torch.cuda.set_device(device)
+    m, n_in, feat, d, w, dy = c2_inputs()
+    n = feat.shape[0]
+    efgs.initialize_appearance('neural', 0, 'none', 'none', 'relu', True)
+    efgs.initialize_residual_mlp(n_in, 3, {'otype': 'Identity'},
+                                 {'otype': 'FullyFusedMLP', 'activation': 'ReLU', 'output_activation': 'None',
+                                  'n_neurons': m['n_neurons'], 'n_hidden_layers': m['n_hidden_layers']},
+                                 m['base_input'], m['n_frequencies'], list(m['sh_degrees']))
+    tf = torch.tensor(feat, device=device, requires_grad=True)
+    td = torch.tensor(d, device=device, requires_grad=True)
+    tw = torch.tensor(w, device=device, requires_grad=True)
+    tdy = torch.tensor(dy, device=device)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record()
+        out = neural_decode(tf, td, tw, 1)
+        if ev is not None:
+            ev[1].record()
+        out.backward(tdy)
+        if ev is not None:
+            ev[2].record()
+        tf.grad = td.grad = tw.grad = None
+
+    log(f'c2: {n} primitives, MLP {n_in} -> {m["n_neurons"]} x {m["n_hidden_layers"]} -> 3')
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(events[k])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    F = mlp_flops_per_primitive(n_in, m['n_neurons'], m['n_hidden_layers'])
+    flops = 3 * F * n                    # forward + backward (input and weight gradients)
+    lat = 4 * m['n_feature_dims']
+    # forward: latents + directions in, outputs out; backward: latents + directions + upstream in, latent and
+    # direction gradients out (156 B per primitive at c2)
+    nbytes = n * ((lat + 12 + 12) + (lat + 12 + 12 + lat + 12))
+    ms = fwd_ms + bwd_ms
+    line = {
+        'metric': 'neural decode fwd+bwd Mprim/s @1M (c2)', 'value': round(n / (ms * 1e-3) / 1e6, 3), 'unit': 'Mprim/s',
+        'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(wall * 1e3 / args.steps, 4),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16 MFMA, f32 accumulation', 'data': 'synthetic',
+        'config': {'workload': f'c2: neural decode of {n} primitives ({n_in} -> {m["n_neurons"]} x {m["n_hidden_layers"]} -> 3), '
+                               'forward + backward w.r.t. latents, directions and weights', 'n_primitives': n},
+        'forward_ms': round(fwd_ms, 5), 'backward_ms': round(bwd_ms, 5),
+        'roofline': {'bound': 'mfma', 'achieved': round(flops / (ms * 1e-3) / 1e12, 3), 'peak': MFMA_FP16_PEAK_TFLOPS,
+                     'unit': 'TFLOP/s', 'frac': round(flops / (ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 5), 'traffic': None,
+                     'kernel': 'neural_decode + neural_decode_backward', 'algorithmic_flops': int(flops),
+                     'algorithmic_bytes': int(nbytes), 'hbm_gb_s': round(nbytes / (ms * 1e-3) / 1e9, 1)},
+        'cpu_baseline': None if args.no_cpu_baseline else decode_cpu_baseline(m, feat, d, w, dy),
+    }
+    print(json.dumps(line), flush=True)
+
+
+def decode_cpu_baseline(m, feat, d, w, dy) -> dict:
+    """The numpy statement of the decode (oracle.neural_decode + its backward) on a 100k-primitive sample."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+    import oracle as O
+    from threadpoolctl import threadpool_limits
+    k = 100_000
+    mlp = O.MLPConfig(**m)
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        y, acts, mats = O.neural_decode(feat[:k], None, d[:k], w, mlp, 1)
+        O.neural_decode_backward(feat[:k], None, d[:k], dy[:k], mats, acts, mlp, 1)
+        seconds = time.perf_counter() - t0
+    return {'value': round(k / seconds / 1e6, 5), 'unit': 'Mprim/s', 'cores': 1, 'kind': 'port',
+            'sample': f'forward + backward of the first {k} c2 primitives through the numpy statement (oracle), one thread; '
+                      f'{seconds:.1f} s'}
+
+
 def copy_calibration() -> None:
     """A plain device copy of 1 GiB, five times: rocprofv3 FETCH_SIZE / WRITE_SIZE of this command read
     1 GiB each per dispatch when the counters are exact."""
@@ -329,6 +434,9 @@ def main() -> None:
         return
     if args.steps < 1 or args.warmup < 0:
         raise SystemExit('bench.py: --steps must be >= 1 and --warmup >= 0')
+    if args.config == 'c2':
+        decode_benchmark(args)
+        return
     r = gpu_benchmark(args)
     W, H = r['W'], r['H']
     value = W * H / (r['ms_per_step'] * 1e-3) / 1e6

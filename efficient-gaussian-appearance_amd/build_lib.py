@@ -21,7 +21,6 @@ SOURCES = [
     ('api.cpp', []),
     ('rtc.cpp', []),
     ('scan.hip', []),
-    ('sort.hip', []),
     ('raster.hip', ['-ffp-contract=off']),
     ('blend.hip', ['-ffp-contract=off']),
     ('adam.hip', ['-ffp-contract=off']),

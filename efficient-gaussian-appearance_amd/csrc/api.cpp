@@ -184,14 +184,7 @@ struct PrimitiveLayout {
     uint32_t* block_key_ranges;
     uint32_t* block_offsets;
     uint32_t* counters;
-    uint32_t* keys_a;
-    uint32_t* vals_a;
-    uint32_t* keys_b;
-    uint32_t* vals_b;
-    uint32_t* offsets;
     uint32_t* visible_prims;
-    void* scan_scratch;
-    void* sort_scratch;
     size_t bytes;
 
     static PrimitiveLayout carve(char* base, uint64_t n) {
@@ -207,14 +200,7 @@ struct PrimitiveLayout {
         l.block_key_ranges = c.take<uint32_t>(2ull * blocks);
         l.block_offsets = c.take<uint32_t>(2ull * blocks);
         l.counters = c.take<uint32_t>(n_counters);
-        l.keys_a = c.take<uint32_t>(nn);
-        l.vals_a = c.take<uint32_t>(nn);
-        l.keys_b = c.take<uint32_t>(nn);
-        l.vals_b = c.take<uint32_t>(nn);
-        l.offsets = c.take<uint32_t>(nn);
         l.visible_prims = c.take<uint32_t>(nn);
-        l.scan_scratch = c.take_bytes(scan_scratch_bytes(static_cast<uint32_t>(nn)));
-        l.sort_scratch = c.take_bytes(sort_scratch_bytes(static_cast<uint32_t>(nn)));
         l.bytes = c.offset + buffer_alignment;
         return l;
     }
@@ -225,6 +211,8 @@ struct TileLayout {
     float* final_T;
     uint32_t* n_contrib;
     uint32_t* tile_max;
+    uint32_t* totals;       // instances per tile
+    uint32_t* tile_start;   // first slot of every tile (the bucket cursor without a count table)
     size_t bytes;
 
     static TileLayout carve(char* base, uint32_t n_tiles) {
@@ -234,30 +222,35 @@ struct TileLayout {
         l.final_T = c.take<float>(static_cast<uint64_t>(n_tiles) * tile_pixels);
         l.n_contrib = c.take<uint32_t>(static_cast<uint64_t>(n_tiles) * tile_pixels);
         l.tile_max = c.take<uint32_t>(n_tiles);
+        l.totals = c.take<uint32_t>(n_tiles);
+        l.tile_start = c.take<uint32_t>(n_tiles);
         l.bytes = c.offset + buffer_alignment;
         return l;
     }
 };
 
 struct InstanceLayout {
-    void* keys_a;
-    void* keys_b;
-    uint32_t* vals_a;
-    uint32_t* vals_b;
-    uint32_t* inst_prim;
-    void* sort_scratch;
+    void* keys;              // tile key per emission slot
+    uint32_t* inst_prim;     // primitive per emission slot
+    uint32_t* local_rank;    // rank of each instance within its histogram segment's slots of its tile
+    uint32_t* table;         // per histogram segment and tile: the tile's count in the earlier segments
+    uint64_t* bucket;        // sort keys grouped by tile (depth key << 32 | emission index)
+    uint32_t* sorted_inst;   // emission slots in (tile, depth, primitive) order
+    void* sorted_keys;       // tile key of every sorted instance
     size_t bytes;
 
-    static InstanceLayout carve(char* base, uint64_t n_instances, int key_bytes) {
+    static InstanceLayout carve(char* base, uint64_t n_instances, int key_bytes, uint32_t n_tiles) {
         InstanceLayout l;
         Carver c{base};
         const uint64_t ni = n_instances > 0 ? n_instances : 1;
-        l.keys_a = c.take_bytes(key_bytes * ni);
-        l.keys_b = c.take_bytes(key_bytes * ni);
-        l.vals_a = c.take<uint32_t>(ni);
-        l.vals_b = c.take<uint32_t>(ni);
+        const TileBinning plan = tile_binning_plan(static_cast<uint32_t>(n_instances), n_tiles);
+        l.keys = c.take_bytes(key_bytes * ni);
         l.inst_prim = c.take<uint32_t>(ni);
-        l.sort_scratch = c.take_bytes(sort_scratch_bytes(static_cast<uint32_t>(ni)));
+        l.local_rank = c.take<uint32_t>(plan.use_table ? ni : 1);
+        l.table = c.take<uint32_t>(plan.use_table ? static_cast<uint64_t>(plan.blocks) * n_tiles : 1);
+        l.bucket = c.take<uint64_t>(ni);
+        l.sorted_inst = c.take<uint32_t>(ni);
+        l.sorted_keys = c.take_bytes(key_bytes * ni);
         l.bytes = c.offset + buffer_alignment;
         return l;
     }
@@ -266,12 +259,6 @@ struct InstanceLayout {
 int fail(int code, const std::string& msg) {
     set_error(msg);
     return code;
-}
-
-int end_bit_of(uint32_t max_key) {
-    int bits = 0;
-    while (bits < 32 && (max_key >> bits) != 0) bits++;
-    return bits;
 }
 
 const char* model_suffix(int model) {
@@ -623,7 +610,6 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     const uint32_t grid_w = div_up(settings->width, tile_width), grid_h = div_up(settings->height, tile_height);
     const uint32_t n_tiles = grid_w * grid_h;
     const int key_bytes = n_tiles <= 65535u ? 2 : 4;
-    const int end_bit = end_bit_of(n_tiles - 1);
     if (!r->host_counters) {
         if (hipHostMalloc(reinterpret_cast<void**>(&r->host_counters), n_counters * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
             return fail(EFGS_ERR_HIP, "hipHostMalloc of the counter readback buffer failed");
@@ -668,8 +654,7 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         t.end(s);
         t.begin(EFGS_STAGE_COMPACT, s);
         if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, chunks, s)) return EFGS_ERR_HIP;
-        if (!launch_compact_visible(pl.n_touched, pl.depth_keys, pl.block_offsets, pl.counters, pl.keys_a, pl.vals_a, pl.visible_prims, n, s))
-            return EFGS_ERR_HIP;
+        if (!launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
         t.end(s);
     } else {
         if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
@@ -681,37 +666,30 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     t.end(s);
     const uint32_t n_visible = r->host_counters[0];
     const uint32_t n_instances = r->host_counters[1];
-    const int depth_end_bit = end_bit_of(r->host_counters[4] - r->host_counters[3]);  // keys are relative to the minimum
 
-    bool depth_in_b = false;
-    t.begin(EFGS_STAGE_DEPTH_SORT, s);
-    if (!radix_sort_pairs(pl.keys_a, pl.vals_a, pl.keys_b, pl.vals_b, false, n_visible, 4, depth_end_bit, pl.sort_scratch, &depth_in_b, s))
-        return EFGS_ERR_HIP;
-    t.end(s);
-    const uint32_t* depth_sorted_prims = depth_in_b ? pl.vals_b : pl.vals_a;
-    t.begin(EFGS_STAGE_INSTANCE_OFFSETS, s);
-    if (!scan_exclusive(pl.n_touched, depth_sorted_prims, pl.offsets, nullptr, n_visible, pl.scan_scratch, s)) return EFGS_ERR_HIP;
-    t.end(s);
-
-    const InstanceLayout il0 = InstanceLayout::carve(nullptr, n_instances, key_bytes);
+    const InstanceLayout il0 = InstanceLayout::carve(nullptr, n_instances, key_bytes, n_tiles);
     char* iblob = static_cast<char*>(alloc(alloc_ctx, il0.bytes));
     if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
-    const InstanceLayout il = InstanceLayout::carve(iblob, n_instances, key_bytes);
+    const InstanceLayout il = InstanceLayout::carve(iblob, n_instances, key_bytes, n_tiles);
+    const TileBinning plan = tile_binning_plan(n_instances, n_tiles);
     t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
-    if (!launch_create_instances(depth_sorted_prims, pl.offsets, pl.n_touched, pl.records, il.keys_a, key_bytes, il.inst_prim, pl.prim_offset,
-                                 pl.counters, grid_w, n_visible, s))
+    if (!launch_create_instances(pl.visible_prims, pl.prim_offset, pl.n_touched, pl.records, il.keys, key_bytes, il.inst_prim, pl.counters, grid_w,
+                                 n_visible, s))
         return EFGS_ERR_HIP;
     t.end(s);
-    bool tiles_in_b = false;
+    t.begin(EFGS_STAGE_TILE_OFFSETS, s);
+    if (!launch_tile_counts(plan, il.keys, key_bytes, n_instances, il.local_rank, il.table, tl.totals, n_tiles, s)) return EFGS_ERR_HIP;
+    if (!launch_tile_offsets(tl.totals, tl.ranges, tl.tile_start, n_tiles, s)) return EFGS_ERR_HIP;
+    t.end(s);
+    t.begin(EFGS_STAGE_TILE_BUCKETS, s);
+    if (!launch_tile_buckets(plan, il.keys, key_bytes, il.inst_prim, pl.depth_keys, il.table, il.local_rank, tl.tile_start, il.bucket, n_instances,
+                             n_tiles, s))
+        return EFGS_ERR_HIP;
+    t.end(s);
     t.begin(EFGS_STAGE_TILE_SORT, s);
-    if (!radix_sort_pairs(il.keys_a, il.vals_a, il.keys_b, il.vals_b, true, n_instances, key_bytes, end_bit, il.sort_scratch, &tiles_in_b, s))
-        return EFGS_ERR_HIP;
+    if (!launch_tile_sort(tl.ranges, il.bucket, il.sorted_inst, il.sorted_keys, key_bytes, n_tiles, s)) return EFGS_ERR_HIP;
     t.end(s);
-    const void* sorted_keys = tiles_in_b ? il.keys_b : il.keys_a;
-    const uint32_t* sorted_inst = tiles_in_b ? il.vals_b : il.vals_a;
-    t.begin(EFGS_STAGE_TILE_RANGES, s);
-    if (!launch_tile_ranges(sorted_keys, key_bytes, tl.ranges, n_instances, n_tiles, s)) return EFGS_ERR_HIP;
-    t.end(s);
+    const uint32_t* sorted_inst = il.sorted_inst;
 
     BlendForwardArgs b;
     b.ranges = tl.ranges;
@@ -740,8 +718,6 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     frame->grid_width = static_cast<int32_t>(grid_w);
     frame->grid_height = static_cast<int32_t>(grid_h);
     frame->key_bytes = key_bytes;
-    frame->depth_sorted_in_b = depth_in_b ? 1 : 0;
-    frame->tiles_sorted_in_b = tiles_in_b ? 1 : 0;
     frame->model = variant;
     return EFGS_OK;
 }
@@ -770,8 +746,8 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     const uint32_t n_instances = static_cast<uint32_t>(frame->n_instances);
     const PrimitiveLayout pl = PrimitiveLayout::carve(static_cast<char*>(frame->primitive_buffers), n);
     const TileLayout tl = TileLayout::carve(static_cast<char*>(frame->tile_buffers), n_tiles);
-    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), n_instances, frame->key_bytes);
-    const uint32_t* sorted_inst = frame->tiles_sorted_in_b ? il.vals_b : il.vals_a;
+    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), n_instances, frame->key_bytes, n_tiles);
+    const uint32_t* sorted_inst = il.sorted_inst;
 
     const size_t grad_bytes = static_cast<size_t>(n_instances > 0 ? n_instances : 1) * 12 * sizeof(float);
     float* inst_grads = static_cast<float*>(alloc(alloc_ctx, grad_bytes));
@@ -913,16 +889,16 @@ int efgs_get_frame_views(const efgs_frame* frame, efgs_frame_views* v) {
     const PrimitiveLayout pl = PrimitiveLayout::carve(static_cast<char*>(frame->primitive_buffers), n);
     const TileLayout tl = TileLayout::carve(static_cast<char*>(frame->tile_buffers), n_tiles);
     const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), static_cast<uint64_t>(frame->n_instances),
-                                                    frame->key_bytes);
+                                                    frame->key_bytes, n_tiles);
     v->n_touched = pl.n_touched;
     v->depth_keys = pl.depth_keys;
     v->records = reinterpret_cast<const float*>(pl.records);
-    v->depth_sorted_keys = frame->depth_sorted_in_b ? pl.keys_b : pl.keys_a;
-    v->depth_sorted_prims = frame->depth_sorted_in_b ? pl.vals_b : pl.vals_a;
-    v->instance_offsets = pl.offsets;
-    v->tile_sorted_keys = frame->tiles_sorted_in_b ? il.keys_b : il.keys_a;
-    v->tile_sorted_instances = frame->tiles_sorted_in_b ? il.vals_b : il.vals_a;
+    v->visible_prims = pl.visible_prims;
+    v->prim_offset = pl.prim_offset;
+    v->instance_keys = il.keys;
     v->instance_primitive = il.inst_prim;
+    v->tile_sorted_keys = il.sorted_keys;
+    v->tile_sorted_instances = il.sorted_inst;
     v->tile_ranges = reinterpret_cast<const uint32_t*>(tl.ranges);
     v->final_transmittance = tl.final_T;
     v->n_contributors = tl.n_contrib;

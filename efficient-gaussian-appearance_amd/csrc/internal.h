@@ -22,30 +22,10 @@ void set_error(const std::string& msg);
         }                                                                                                 \
     } while (0)
 
-constexpr uint32_t sort_block = 256;
-constexpr uint32_t sort_rounds = 8;                     // keys per thread per sort tile
-constexpr uint32_t sort_tile = sort_block * sort_rounds;  // 2048 keys per block
-constexpr uint32_t sort_bins = 256;                     // 8-bit digits
-constexpr uint32_t scan_block = 256;
-constexpr uint32_t scan_items = 8;
-constexpr uint32_t scan_tile = scan_block * scan_items;   // 2048 elements per block
 constexpr uint32_t preprocess_block = 256;
 constexpr uint32_t instance_block = 256;
 
 inline uint32_t div_up(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a + b - 1) / b); }
-
-// ---- device-wide exclusive scan of uint32 (optionally gathering in[idx[i]]) --------------------------------
-size_t scan_scratch_bytes(uint32_t n);
-// out[i] = sum_{k<i} v(k), v(k) = idx ? in[idx[k]] : in[k]; total (if non-null) receives the full sum
-bool scan_exclusive(const uint32_t* in, const uint32_t* idx, uint32_t* out, uint32_t* total, uint32_t n, void* scratch, hipStream_t s);
-
-// ---- stable LSD radix sort of (key, value) pairs ------------------------------------------------------------
-// keys are uint32 or uint16 (key_bytes 4 or 2), values uint32; vals_in == nullptr means values = index.
-// Ping-pongs between (keys_a, vals_a) and (keys_b, vals_b); returns in *result_in_b whether the sorted data
-// ended in the b buffers.
-size_t sort_scratch_bytes(uint32_t n);
-bool radix_sort_pairs(void* keys_a, uint32_t* vals_a, void* keys_b, uint32_t* vals_b, bool identity_vals, uint32_t n,
-                      int key_bytes, int end_bit, void* scratch, bool* result_in_b, hipStream_t s);
 
 // ---- rasterizer stages -------------------------------------------------------------------------------------
 bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
@@ -53,15 +33,40 @@ bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 constexpr uint32_t n_counters = 8;
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
                               uint32_t n_blocks, hipStream_t s);
-// compacted depth keys are stored relative to counters[3] (order preserving; fewer radix passes); the
-// primitive indices go to vals_out (sort input) and visible_out (kept in index order)
-bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_keys, const uint32_t* block_offsets, const uint32_t* counters,
-                            uint32_t* keys_out, uint32_t* vals_out, uint32_t* visible_out, uint32_t n, hipStream_t s);
-bool launch_create_instances(const uint32_t* sorted_prims, const uint32_t* offsets, const uint32_t* n_touched,
-                             const PrimRecord* records, void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* prim_offset,
-                             uint32_t* counters, uint32_t grid_w, uint32_t n_visible, hipStream_t s);
+// visible primitives in index order and their first emission slots (exclusive scan of the tile counts in
+// index order)
+bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,
+                            hipStream_t s);
+// (tile key, primitive) at every emission slot
+bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, const uint32_t* n_touched, const PrimRecord* records,
+                             void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w, uint32_t n_visible,
+                             hipStream_t s);
+// Tile binning: per-tile counts from LDS histograms over fixed segments of the emission slots (a table of
+// per-segment counts, scanned per tile) when the tile count fits the LDS, else from global atomics.
+constexpr size_t tile_hist_max_lds = 64 * 1024;  // default dynamic LDS limit of a launch
+constexpr uint32_t tile_hist_min_segment = 16384;  // emission slots per histogram block (at least)
+constexpr uint32_t tile_hist_max_blocks = 128;
+struct TileBinning {
+    bool use_table;
+    uint32_t blocks;   // histogram blocks (rows of the table)
+    uint32_t segment;  // emission slots per histogram block
+};
+TileBinning tile_binning_plan(uint32_t n_instances, uint32_t n_tiles);
+// totals[t] = instances of tile t; with the table also every instance's rank within its segment's slots of
+// its tile (local_rank) and, per segment, the tile's count in the earlier segments (table)
+bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* local_rank, uint32_t* table,
+                        uint32_t* totals, uint32_t n_tiles, hipStream_t s);
+// per-tile [start, end) ranges and starts from the totals
+bool launch_tile_offsets(const uint32_t* totals, uint2* ranges, uint32_t* tile_start, uint32_t n_tiles, hipStream_t s);
+// every instance's sort key (depth key of its primitive << 32 | emission index) into a slot of its tile's
+// range (without the table, tile_start serves as the atomic cursor and is advanced)
+bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
+                         const uint32_t* table, const uint32_t* local_rank, uint32_t* tile_start, uint64_t* bucket, uint32_t n_instances,
+                         uint32_t n_tiles, hipStream_t s);
+// per tile: keys sorted ascending -> emission indices in sorted_inst, tile id in sorted_keys
+bool launch_tile_sort(const uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes, uint32_t n_tiles,
+                      hipStream_t s);
 bool launch_reduce_partials(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out, hipStream_t s);
-bool launch_tile_ranges(const void* keys, int key_bytes, uint2* ranges, uint32_t n_instances, uint32_t n_tiles, hipStream_t s);
 
 struct BlendForwardArgs {
     const uint2* ranges;

@@ -1,6 +1,18 @@
-// Binning stages between preprocess and blend: deterministic compaction of visible primitives, instance
-// emission in depth order, and per-tile instance ranges. Compiled with -ffp-contract=off: instance emission
-// re-evaluates the tile test of the preprocess and must reproduce its counts exactly.
+// Binning stages between preprocess and blend. The reference orders instances in two global sorts: a
+// 32-bit radix sort of the visible primitives by depth, emission of (tile, primitive) instances in that
+// order, then a stable radix sort by tile. This build reaches the same per-tile order, (depth, primitive
+// index), without a global sort:
+//   compact_visible     visible primitives in index order and each one's first emission slot (exclusive
+//                       scan of the tile counts in index order);
+//   create_instances    one thread per visible primitive (index order): the tile test of the preprocess,
+//                       (tile key, primitive) at the emission slots, per-tile instance counts;
+//   tile_offsets        one block: exclusive scan of the tile counts -> [start, end) per tile, cursors;
+//   tile_buckets        every instance claims a slot of its tile's range (atomic cursor; order arbitrary);
+//   tile_sort           one block per tile sorts its slots by (depth key, emission index) in LDS: keys are
+//                       unique, so the order is a deterministic function of the inputs (the emission index
+//                       increases with the primitive index, so ties in depth keep primitive-index order).
+// Compiled with -ffp-contract=off: instance emission re-evaluates the tile test of the preprocess and must
+// reproduce its counts exactly.
 // Reference: B/rasterization/include/kernels_common.cuh:20-157, B/rasterization/src/forward.cu:82-221.
 #include "internal.h"
 
@@ -13,46 +25,56 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t n) {
     if (i < n) p[i] = value;
 }
 
-// primitive-index-ordered compaction of (depth key - min depth key, primitive) for the visible primitives
-__global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const uint32_t* n_touched, const uint32_t* depth_keys,
-                                                                          const uint32_t* block_offsets, const uint32_t* counters,
-                                                                          uint32_t* keys_out, uint32_t* vals_out, uint32_t* visible_out,
-                                                                          uint32_t n) {
-    __shared__ uint32_t wave_counts[preprocess_block / 64];
+// Primitive-index-ordered compaction of the visible primitives with their first emission slots (the
+// preprocess stored per-block visible and instance counts; block_offsets holds their exclusive scans).
+__global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const uint32_t* n_touched, const uint32_t* block_offsets,
+                                                                          uint32_t* visible_out, uint32_t* prim_offset, uint32_t n) {
+    __shared__ uint32_t wave_counts[preprocess_block / 64][2];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
-    const bool visible = p < n && n_touched[p] > 0;
+    const uint32_t touched = p < n ? n_touched[p] : 0u;
+    const bool visible = touched > 0;
     const uint64_t mask = __ballot(visible);
-    if (lane == 0) wave_counts[wave] = static_cast<uint32_t>(__popcll(mask));
+    uint32_t inc = touched;  // inclusive wave scan of the tile counts
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) {
+        wave_counts[wave][0] = static_cast<uint32_t>(__popcll(mask));
+        wave_counts[wave][1] = inc;
+    }
     __syncthreads();
     if (!visible) return;
-    uint32_t pos = block_offsets[2 * blockIdx.x];
-    for (uint32_t w = 0; w < wave; w++) pos += wave_counts[w];
+    uint32_t pos = block_offsets[2 * blockIdx.x], off = block_offsets[2 * blockIdx.x + 1];
+    for (uint32_t w = 0; w < wave; w++) {
+        pos += wave_counts[w][0];
+        off += wave_counts[w][1];
+    }
     pos += static_cast<uint32_t>(__popcll(mask & ((1ull << lane) - 1ull)));
-    keys_out[pos] = depth_keys[p] - counters[3];
-    vals_out[pos] = p;
-    visible_out[pos] = p;  // kept in index order for the backward (the sort overwrites vals_out)
+    visible_out[pos] = p;
+    prim_offset[p] = off + inc - touched;
 }
 
-// One thread per visible primitive in depth order: emits (tile key, primitive) for every tile of its tile
+// One thread per visible primitive in index order: emits (tile key, primitive) for every tile of its tile
 // rectangle that passes the contribution test, the first 4 tiles per lane and larger footprints
 // wave-cooperatively (64 tiles per step, positions from ballot prefix counts). Emission slots are
-// [offset, offset + n_touched); a count that disagrees with the preprocess is clamped to that range, the
-// remainder padded with an out-of-range key and counted in counters[2].
+// [prim_offset, prim_offset + n_touched); a count that disagrees with the preprocess is clamped to that
+// range, the remainder padded with an out-of-range key (never bucketed) and counted in counters[2].
 template <typename KeyT>
-__global__ __launch_bounds__(instance_block) void create_instances_kernel(const uint32_t* sorted_prims, const uint32_t* offsets,
+__global__ __launch_bounds__(instance_block) void create_instances_kernel(const uint32_t* visible_prims, const uint32_t* prim_offset,
                                                                          const uint32_t* n_touched, const PrimRecord* records,
-                                                                         KeyT* keys, uint32_t* inst_prim, uint32_t* prim_offset,
-                                                                         uint32_t* counters, uint32_t grid_w, uint32_t n_visible) {
+                                                                         KeyT* keys, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w,
+                                                                         uint32_t n_visible) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint64_t lanes_below = (1ull << lane) - 1ull;
     const uint32_t i_raw = blockIdx.x * instance_block + threadIdx.x;
     const bool active = i_raw < n_visible;
     const uint32_t i = active ? i_raw : n_visible - 1;
-    const uint32_t p = sorted_prims[i];
-    const uint32_t off = offsets[i];
+    const uint32_t p = visible_prims[i];
+    const uint32_t off = prim_offset[p];
     const uint32_t n = n_touched[p];
-    if (active) prim_offset[p] = off;
     const PrimRecord rec = records[p];
     const uint32_t bx = __float_as_uint(rec.r2.y), by = __float_as_uint(rec.r2.z);
     const TileRect t = screen_to_tile_bounds(bx & 0xffffu, bx >> 16, by & 0xffffu, by >> 16);
@@ -104,6 +126,197 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
     }
 }
 
+// Per-tile counts without global atomics: block b of tile_hist counts the tiles of emission slots
+// [b seg, (b + 1) seg) in an LDS histogram (ds_add with return gives every instance its rank within the
+// block's slots of its tile, in arbitrary order) and writes its row table[b][tile]; tile_block_scan turns
+// every column into exclusive prefixes over the blocks and the tile totals. Grids too large for an LDS
+// histogram count with global atomics instead (tile_count_global).
+__global__ __launch_bounds__(1024) void tile_hist_kernel(const void* keys_raw, int key_bytes, uint32_t n_instances, uint32_t seg,
+                                                         uint32_t* local_rank, uint32_t* table, uint32_t n_tiles) {
+    extern __shared__ uint32_t hist[];
+    for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) hist[t] = 0;
+    __syncthreads();
+    const uint32_t e0 = blockIdx.x * seg, e1 = min(n_instances, e0 + seg);
+    for (uint32_t e = e0 + threadIdx.x; e < e1; e += 1024) {
+        const uint32_t t = key_bytes == 2 ? static_cast<const uint16_t*>(keys_raw)[e] : static_cast<const uint32_t*>(keys_raw)[e];
+        if (t < n_tiles) local_rank[e] = atomicAdd(&hist[t], 1u);
+    }
+    __syncthreads();
+    uint32_t* row = table + static_cast<size_t>(blockIdx.x) * n_tiles;
+    for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) row[t] = hist[t];
+}
+
+// one thread per tile: table[b][t] <- sum of table[b'][t] over b' < b; totals[t] <- the column sum
+__global__ __launch_bounds__(256) void tile_block_scan_kernel(uint32_t* table, uint32_t n_blocks, uint32_t n_tiles, uint32_t* totals) {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= n_tiles) return;
+    uint32_t run = 0;
+    for (uint32_t b0 = 0; b0 < n_blocks; b0 += 8) {  // 8 loads in flight
+        uint32_t c[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) c[k] = b0 + k < n_blocks ? table[static_cast<size_t>(b0 + k) * n_tiles + t] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) {
+            if (b0 + k < n_blocks) table[static_cast<size_t>(b0 + k) * n_tiles + t] = run;
+            run += c[k];
+        }
+    }
+    totals[t] = run;
+}
+
+template <typename KeyT>
+__global__ __launch_bounds__(256) void tile_count_global_kernel(const KeyT* keys, uint32_t n_instances, uint32_t* totals, uint32_t n_tiles) {
+    const uint32_t e = blockIdx.x * 256u + threadIdx.x;
+    if (e >= n_instances) return;
+    const uint32_t t = static_cast<uint32_t>(keys[e]);
+    if (t < n_tiles) atomicAdd(&totals[t], 1u);
+}
+
+// One block: exclusive scan of the per-tile totals in chunks of 1024 x 8 (carry between chunks) ->
+// ranges[t] = [start, start + count) ((0, 0) for an empty tile, as the reference's zero-filled ranges) and
+// tile_start[t] = start.
+__global__ __launch_bounds__(1024) void tile_offsets_kernel(const uint32_t* counts, uint2* ranges, uint32_t* tile_start, uint32_t n_tiles) {
+    constexpr uint32_t per = 8;
+    __shared__ uint32_t wave_totals[1024 / 64];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t carry = 0;
+    for (uint32_t base = 0; base < n_tiles; base += 1024 * per) {
+        const uint32_t t0 = base + threadIdx.x * per;
+        uint32_t c[per];
+        uint32_t sum = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < per; k++) {
+            c[k] = t0 + k < n_tiles ? counts[t0 + k] : 0u;
+            sum += c[k];
+        }
+        uint32_t inc = sum;
+#pragma unroll
+        for (uint32_t o = 1; o < 64; o <<= 1) {
+            const uint32_t v = __shfl_up(inc, o);
+            if (lane >= o) inc += v;
+        }
+        if (lane == 63) wave_totals[wave] = inc;
+        __syncthreads();
+        uint32_t prefix = carry, total = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < 1024 / 64; w++) {
+            const uint32_t v = wave_totals[w];
+            if (w < wave) prefix += v;
+            total += v;
+        }
+        __syncthreads();
+        prefix += inc - sum;
+#pragma unroll
+        for (uint32_t k = 0; k < per; k++) {
+            if (t0 + k < n_tiles) {
+                ranges[t0 + k] = c[k] > 0 ? make_uint2(prefix, prefix + c[k]) : make_uint2(0u, 0u);
+                tile_start[t0 + k] = prefix;
+            }
+            prefix += c[k];
+        }
+        carry += total;
+    }
+}
+
+// Every emitted instance goes to a slot of its tile's range: start of the tile + the tile's count in the
+// earlier histogram blocks + its rank within its block (with a table), or the next slot of an atomic cursor
+// (without one: tile_start is advanced). The slot receives the instance's sort key, the depth key of its
+// primitive above its emission index.
+template <typename KeyT>
+__global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
+                                                          const uint32_t* table, const uint32_t* local_rank, uint32_t seg,
+                                                          uint32_t* tile_start, uint64_t* bucket, uint32_t n_instances, uint32_t n_tiles) {
+    const uint32_t e = blockIdx.x * 256u + threadIdx.x;
+    if (e >= n_instances) return;
+    const uint32_t t = static_cast<uint32_t>(keys[e]);
+    if (t >= n_tiles) return;
+    const uint64_t key = (static_cast<uint64_t>(depth_keys[inst_prim[e]]) << 32) | e;
+    const uint32_t pos = table ? tile_start[t] + table[static_cast<size_t>(e / seg) * n_tiles + t] + local_rank[e]
+                               : atomicAdd(&tile_start[t], 1u);
+    bucket[pos] = key;
+}
+
+// Ascending bitonic sort of m (a power of two, <= tile_sort_capacity) 64-bit keys in LDS by the whole block.
+constexpr uint32_t tile_sort_block = 128;
+constexpr uint32_t tile_sort_capacity = 2048;
+__device__ __forceinline__ void bitonic_sort_lds(uint64_t* s, uint32_t m) {
+    for (uint32_t k = 2; k <= m; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t i = threadIdx.x; i < m; i += tile_sort_block) {
+                const uint32_t ixj = i ^ j;
+                if (ixj > i) {
+                    const uint64_t a = s[i], b = s[ixj];
+                    if ((a > b) == ((i & k) == 0)) {
+                        s[i] = b;
+                        s[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// number of keys below x in the ascending run [0, n)
+__device__ __forceinline__ uint32_t rank_in(const uint64_t* run, uint32_t n, uint64_t x) {
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (run[mid] < x) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+// One block per tile sorts the keys of its range ascending (keys are unique); the emission indices go to
+// sorted_inst and the tile id to sorted_keys. A tile of more than tile_sort_capacity instances sorts chunks
+// of that size in LDS back into its range, then places every key at (its index in its chunk) + (its rank
+// in each other chunk).
+template <typename KeyT>
+__global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst,
+                                                                   KeyT* sorted_keys) {
+    __shared__ uint64_t s[tile_sort_capacity];
+    const uint32_t tile = blockIdx.x;
+    const uint2 r = ranges[tile];
+    const uint32_t n = r.y - r.x;
+    if (n == 0) return;
+    uint64_t* run = bucket + r.x;
+    if (n <= tile_sort_capacity) {
+        uint32_t m = 2;
+        while (m < n) m <<= 1;
+        for (uint32_t i = threadIdx.x; i < m; i += tile_sort_block) s[i] = i < n ? run[i] : ~0ull;
+        __syncthreads();
+        bitonic_sort_lds(s, m);
+        for (uint32_t i = threadIdx.x; i < n; i += tile_sort_block) {
+            sorted_inst[r.x + i] = static_cast<uint32_t>(s[i]);
+            sorted_keys[r.x + i] = static_cast<KeyT>(tile);
+        }
+        return;
+    }
+    const uint32_t n_chunks = (n + tile_sort_capacity - 1) / tile_sort_capacity;
+    for (uint32_t c = 0; c < n_chunks; c++) {
+        const uint32_t c0 = c * tile_sort_capacity, cn = min(tile_sort_capacity, n - c0);
+        for (uint32_t i = threadIdx.x; i < tile_sort_capacity; i += tile_sort_block) s[i] = i < cn ? run[c0 + i] : ~0ull;
+        __syncthreads();
+        bitonic_sort_lds(s, tile_sort_capacity);
+        for (uint32_t i = threadIdx.x; i < cn; i += tile_sort_block) run[c0 + i] = s[i];
+        __syncthreads();
+    }
+    __threadfence();
+    __syncthreads();
+    for (uint32_t idx = threadIdx.x; idx < n; idx += tile_sort_block) {
+        const uint64_t x = run[idx];
+        const uint32_t c = idx / tile_sort_capacity;
+        uint32_t pos = idx - c * tile_sort_capacity;
+        for (uint32_t o = 0; o < n_chunks; o++) {
+            if (o == c) continue;
+            const uint32_t o0 = o * tile_sort_capacity;
+            pos += rank_in(run + o0, min(tile_sort_capacity, n - o0), x);
+        }
+        sorted_inst[r.x + pos] = static_cast<uint32_t>(x);
+        sorted_keys[r.x + pos] = static_cast<KeyT>(tile);
+    }
+}
+
 // out[i] = sum over blocks b of partials[b][i]. A block covers 64 parameters with 16 groups of 64 lanes;
 // group g sums blocks g, g + 16, ... in order, then the 16 group sums are added in group order (fixed
 // order, reproducible).
@@ -127,20 +340,6 @@ __global__ __launch_bounds__(64 * reduce_groups) void reduce_partials_kernel(con
     }
 }
 
-template <typename KeyT>
-__global__ void tile_ranges_kernel(const KeyT* keys, uint2* ranges, uint32_t n_instances, uint32_t n_tiles) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_instances) return;
-    const uint32_t key = static_cast<uint32_t>(keys[i]);
-    const bool valid = key < n_tiles;
-    const uint32_t prev = i > 0 ? static_cast<uint32_t>(keys[i - 1]) : 0xffffffffu;
-    if (key != prev) {
-        if (prev < n_tiles) ranges[prev].y = i;
-        if (valid) ranges[key].x = i;
-    }
-    if (i == n_instances - 1 && valid) ranges[key].y = n_instances;
-}
-
 }  // namespace
 
 bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s) {
@@ -150,25 +349,89 @@ bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s) {
     return true;
 }
 
-bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* depth_keys, const uint32_t* block_offsets, const uint32_t* counters,
-                            uint32_t* keys_out, uint32_t* vals_out, uint32_t* visible_out, uint32_t n, hipStream_t s) {
-    compact_visible_kernel<<<div_up(n, preprocess_block), preprocess_block, 0, s>>>(n_touched, depth_keys, block_offsets, counters, keys_out,
-                                                                                     vals_out, visible_out, n);
+bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,
+                            hipStream_t s) {
+    if (n == 0) return true;
+    compact_visible_kernel<<<div_up(n, preprocess_block), preprocess_block, 0, s>>>(n_touched, block_offsets, visible_out, prim_offset, n);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
 
-bool launch_create_instances(const uint32_t* sorted_prims, const uint32_t* offsets, const uint32_t* n_touched, const PrimRecord* records,
-                             void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* prim_offset, uint32_t* counters, uint32_t grid_w,
-                             uint32_t n_visible, hipStream_t s) {
+bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, const uint32_t* n_touched, const PrimRecord* records,
+                             void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w, uint32_t n_visible,
+                             hipStream_t s) {
     if (n_visible == 0) return true;
     const uint32_t blocks = div_up(n_visible, instance_block);
     if (key_bytes == 2)
-        create_instances_kernel<uint16_t><<<blocks, instance_block, 0, s>>>(sorted_prims, offsets, n_touched, records, static_cast<uint16_t*>(keys),
-                                                                           inst_prim, prim_offset, counters, grid_w, n_visible);
+        create_instances_kernel<uint16_t><<<blocks, instance_block, 0, s>>>(visible_prims, prim_offset, n_touched, records, static_cast<uint16_t*>(keys),
+                                                                           inst_prim, counters, grid_w, n_visible);
     else
-        create_instances_kernel<uint32_t><<<blocks, instance_block, 0, s>>>(sorted_prims, offsets, n_touched, records, static_cast<uint32_t*>(keys),
-                                                                           inst_prim, prim_offset, counters, grid_w, n_visible);
+        create_instances_kernel<uint32_t><<<blocks, instance_block, 0, s>>>(visible_prims, prim_offset, n_touched, records, static_cast<uint32_t*>(keys),
+                                                                           inst_prim, counters, grid_w, n_visible);
+    EFGS_HIP_CHECK(hipGetLastError());
+    return true;
+}
+
+TileBinning tile_binning_plan(uint32_t n_instances, uint32_t n_tiles) {
+    TileBinning b;
+    b.use_table = n_tiles > 0 && static_cast<size_t>(n_tiles) * 4 <= tile_hist_max_lds;
+    b.blocks = b.use_table ? (n_instances > 0 ? div_up(n_instances, tile_hist_min_segment) : 1u) : 0u;
+    if (b.blocks > tile_hist_max_blocks) b.blocks = tile_hist_max_blocks;
+    b.segment = b.use_table && n_instances > 0 ? div_up(n_instances, b.blocks) : 1u;
+    return b;
+}
+
+bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* local_rank, uint32_t* table,
+                        uint32_t* totals, uint32_t n_tiles, hipStream_t s) {
+    if (n_tiles == 0) return true;
+    if (plan.use_table) {
+        if (n_instances == 0) return launch_fill_u32(totals, 0u, n_tiles, s);
+        tile_hist_kernel<<<plan.blocks, 1024, n_tiles * 4, s>>>(keys, key_bytes, n_instances, plan.segment, local_rank, table, n_tiles);
+        tile_block_scan_kernel<<<div_up(n_tiles, 256), 256, 0, s>>>(table, plan.blocks, n_tiles, totals);
+    } else {
+        if (!launch_fill_u32(totals, 0u, n_tiles, s)) return false;
+        if (n_instances == 0) return true;
+        if (key_bytes == 2)
+            tile_count_global_kernel<uint16_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint16_t*>(keys), n_instances, totals,
+                                                                                       n_tiles);
+        else
+            tile_count_global_kernel<uint32_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint32_t*>(keys), n_instances, totals,
+                                                                                       n_tiles);
+    }
+    EFGS_HIP_CHECK(hipGetLastError());
+    return true;
+}
+
+bool launch_tile_offsets(const uint32_t* totals, uint2* ranges, uint32_t* tile_start, uint32_t n_tiles, hipStream_t s) {
+    if (n_tiles == 0) return true;
+    tile_offsets_kernel<<<1, 1024, 0, s>>>(totals, ranges, tile_start, n_tiles);
+    EFGS_HIP_CHECK(hipGetLastError());
+    return true;
+}
+
+bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
+                         const uint32_t* table, const uint32_t* local_rank, uint32_t* tile_start, uint64_t* bucket, uint32_t n_instances,
+                         uint32_t n_tiles, hipStream_t s) {
+    if (n_instances == 0) return true;
+    const uint32_t blocks = div_up(n_instances, 256);
+    const uint32_t* tab = plan.use_table ? table : nullptr;
+    if (key_bytes == 2)
+        tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, plan.segment,
+                                                            tile_start, bucket, n_instances, n_tiles);
+    else
+        tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, plan.segment,
+                                                            tile_start, bucket, n_instances, n_tiles);
+    EFGS_HIP_CHECK(hipGetLastError());
+    return true;
+}
+
+bool launch_tile_sort(const uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes, uint32_t n_tiles,
+                      hipStream_t s) {
+    if (n_tiles == 0) return true;
+    if (key_bytes == 2)
+        tile_sort_kernel<uint16_t><<<n_tiles, tile_sort_block, 0, s>>>(ranges, bucket, sorted_inst, static_cast<uint16_t*>(sorted_keys));
+    else
+        tile_sort_kernel<uint32_t><<<n_tiles, tile_sort_block, 0, s>>>(ranges, bucket, sorted_inst, static_cast<uint32_t*>(sorted_keys));
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
@@ -176,17 +439,6 @@ bool launch_create_instances(const uint32_t* sorted_prims, const uint32_t* offse
 bool launch_reduce_partials(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out, hipStream_t s) {
     if (n_params == 0) return true;
     reduce_partials_kernel<<<div_up(n_params, 64), 64 * reduce_groups, 0, s>>>(partials, n_blocks, n_params, out);
-    EFGS_HIP_CHECK(hipGetLastError());
-    return true;
-}
-
-bool launch_tile_ranges(const void* keys, int key_bytes, uint2* ranges, uint32_t n_instances, uint32_t n_tiles, hipStream_t s) {
-    if (!launch_fill_u32(reinterpret_cast<uint32_t*>(ranges), 0u, 2ull * n_tiles, s)) return false;
-    if (n_instances == 0) return true;
-    if (key_bytes == 2)
-        tile_ranges_kernel<uint16_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint16_t*>(keys), ranges, n_instances, n_tiles);
-    else
-        tile_ranges_kernel<uint32_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint32_t*>(keys), ranges, n_instances, n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

@@ -1,16 +1,12 @@
-// Device-wide exclusive scan of uint32 on wave64: reduce -> scan of block sums -> block scan with offsets.
-// Used for compaction offsets (gathering per-primitive tile counts in depth order), radix-sort histograms
-// and the per-block preprocess counts. Replaces cub::DeviceScan (B/rasterization/src/forward.cu:107-114,
-// 211-218).
+// Scan of the preprocess's per-block (visible, instance) counts on wave64 (one block): the offsets that the
+// compaction and the instance emission use, the visible and instance totals read back by the host, and the
+// visible depth-key range. Replaces the reference's cub::DeviceScan calls (B/rasterization/src/forward.cu:
+// 107-114) together with the per-block counts the preprocess kernels produce.
 #include "internal.h"
 
 namespace efgs {
 
 namespace {
-
-__device__ __forceinline__ uint32_t load_value(const uint32_t* in, const uint32_t* idx, uint32_t i) {
-    return idx ? in[idx[i]] : in[i];
-}
 
 // inclusive scan of v over the 64 lanes of a wave (Hillis-Steele with lane shuffles)
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, uint32_t lane) {
@@ -40,59 +36,6 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& t
     }
     __syncthreads();
     return wave_prefix + inc - v;
-}
-
-__global__ __launch_bounds__(scan_block) void scan_reduce_kernel(const uint32_t* in, const uint32_t* idx, uint32_t* block_sums, uint32_t n) {
-    const uint32_t base = blockIdx.x * scan_tile + threadIdx.x * scan_items;
-    uint32_t s = 0;
-#pragma unroll
-    for (uint32_t k = 0; k < scan_items; k++) {
-        const uint32_t i = base + k;
-        if (i < n) s += load_value(in, idx, i);
-    }
-    uint32_t total;
-    block_exclusive_scan<scan_block>(s, total);
-    if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
-}
-
-// single block: exclusive scan of up to 1024 * k block sums in place, total -> *total
-__global__ __launch_bounds__(1024) void scan_block_sums_kernel(uint32_t* sums, uint32_t n, uint32_t* total) {
-    const uint32_t per = (n + 1023) / 1024;
-    const uint32_t base = threadIdx.x * per;
-    uint32_t s = 0;
-    for (uint32_t k = 0; k < per; k++)
-        if (base + k < n) s += sums[base + k];
-    uint32_t block_total;
-    uint32_t prefix = block_exclusive_scan<1024>(s, block_total);
-    for (uint32_t k = 0; k < per; k++) {
-        if (base + k < n) {
-            const uint32_t v = sums[base + k];
-            sums[base + k] = prefix;
-            prefix += v;
-        }
-    }
-    if (threadIdx.x == 0 && total) *total = block_total;
-}
-
-__global__ __launch_bounds__(scan_block) void scan_downsweep_kernel(const uint32_t* in, const uint32_t* idx, const uint32_t* block_offsets,
-                                                                   uint32_t* out, uint32_t n) {
-    const uint32_t base = blockIdx.x * scan_tile + threadIdx.x * scan_items;
-    uint32_t v[scan_items];
-    uint32_t s = 0;
-#pragma unroll
-    for (uint32_t k = 0; k < scan_items; k++) {
-        const uint32_t i = base + k;
-        v[k] = i < n ? load_value(in, idx, i) : 0u;
-        s += v[k];
-    }
-    uint32_t total;
-    uint32_t prefix = block_exclusive_scan<scan_block>(s, total) + block_offsets[blockIdx.x];
-#pragma unroll
-    for (uint32_t k = 0; k < scan_items; k++) {
-        const uint32_t i = base + k;
-        if (i < n) out[i] = prefix;
-        prefix += v[k];
-    }
 }
 
 // one block: offsets of the per-preprocess-block (visible, instance) counts; counters[0] = V, counters[1] = I,
@@ -147,21 +90,6 @@ __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t*
 }
 
 }  // namespace
-
-size_t scan_scratch_bytes(uint32_t n) { return sizeof(uint32_t) * (static_cast<size_t>(div_up(n, scan_tile)) + 64); }
-
-bool scan_exclusive(const uint32_t* in, const uint32_t* idx, uint32_t* out, uint32_t* total, uint32_t n, void* scratch, hipStream_t s) {
-    if (n == 0) {
-        return total ? launch_fill_u32(total, 0u, 1, s) : true;
-    }
-    const uint32_t blocks = div_up(n, scan_tile);
-    uint32_t* sums = static_cast<uint32_t*>(scratch);
-    scan_reduce_kernel<<<blocks, scan_block, 0, s>>>(in, idx, sums, n);
-    scan_block_sums_kernel<<<1, 1024, 0, s>>>(sums, blocks, total);
-    scan_downsweep_kernel<<<blocks, scan_block, 0, s>>>(in, idx, sums, out, n);
-    EFGS_HIP_CHECK(hipGetLastError());
-    return true;
-}
 
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters, uint32_t n_blocks,
                               hipStream_t s) {

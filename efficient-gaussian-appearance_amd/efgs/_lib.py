@@ -40,8 +40,7 @@ class Primitives(ctypes.Structure):
 class Frame(ctypes.Structure):
     _fields_ = [('primitive_buffers', ctypes.c_void_p), ('tile_buffers', ctypes.c_void_p), ('instance_buffers', ctypes.c_void_p),
                 ('n_primitives', ctypes.c_int64), ('n_visible', ctypes.c_int64), ('n_instances', ctypes.c_int64),
-                ('grid_width', ctypes.c_int32), ('grid_height', ctypes.c_int32), ('key_bytes', ctypes.c_int32),
-                ('depth_sorted_in_b', ctypes.c_int32), ('tiles_sorted_in_b', ctypes.c_int32), ('model', ctypes.c_int32)]
+                ('grid_width', ctypes.c_int32), ('grid_height', ctypes.c_int32), ('key_bytes', ctypes.c_int32), ('model', ctypes.c_int32)]
 
 
 class Gradients(ctypes.Structure):
@@ -65,9 +64,8 @@ class Workspace(ctypes.Structure):
 
 class FrameViews(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in (
-        'n_touched', 'depth_keys', 'records', 'depth_sorted_keys', 'depth_sorted_prims', 'instance_offsets',
-        'tile_sorted_keys', 'tile_sorted_instances', 'instance_primitive', 'tile_ranges', 'final_transmittance',
-        'n_contributors', 'counters')]
+        'n_touched', 'depth_keys', 'records', 'visible_prims', 'prim_offset', 'instance_keys', 'instance_primitive',
+        'tile_sorted_keys', 'tile_sorted_instances', 'tile_ranges', 'final_transmittance', 'n_contributors', 'counters')]
 
 
 lib = ctypes.CDLL(LIB_PATH)
@@ -78,8 +76,8 @@ EXPORTED = ('efgs_last_error', 'efgs_set_rtc_dirs', 'efgs_rasterizer_create', 'e
             'efgs_neural_decode_forward', 'efgs_neural_decode_backward')
 
 # stage ids of efgs_get_stage_times, in order (include/efgs.h)
-STAGES = ('preprocess_forward', 'compact', 'counter_read', 'depth_sort', 'instance_offsets', 'create_instances', 'tile_sort',
-          'tile_ranges', 'blend_forward', 'blend_backward', 'preprocess_backward', 'mlp_reduce', 'mlp_backward')
+STAGES = ('preprocess_forward', 'compact', 'counter_read', 'create_instances', 'tile_offsets', 'tile_buckets', 'tile_sort',
+          'blend_forward', 'blend_backward', 'preprocess_backward', 'mlp_reduce', 'mlp_backward')
 
 lib.efgs_last_error.restype = ctypes.c_char_p
 lib.efgs_last_error.argtypes = []

@@ -126,8 +126,6 @@ typedef struct efgs_frame {
     int64_t n_instances;
     int32_t grid_width, grid_height;
     int32_t key_bytes;           /* 2 or 4: width of the tile keys */
-    int32_t depth_sorted_in_b;   /* which ping-pong half holds the depth-sorted pairs */
-    int32_t tiles_sorted_in_b;   /* which ping-pong half holds the tile-sorted pairs */
     int32_t model;               /* variant used (0 = precomputed colours) */
 } efgs_frame;
 
@@ -196,12 +194,13 @@ typedef struct efgs_frame_views {
     const uint32_t* n_touched;        /* (N) 0 = culled */
     const uint32_t* depth_keys;       /* (N) float bits of the view depth (valid where n_touched > 0) */
     const float* records;             /* (N x 12) mean2d xy, conic xyz, opacity, rgb, packed bounds, pad */
-    const uint32_t* depth_sorted_keys;   /* (V) depth keys minus counters[3] (the smallest visible depth key) */
-    const uint32_t* depth_sorted_prims;  /* (V) */
-    const uint32_t* instance_offsets;    /* (V) exclusive scan of touched tiles in depth order */
-    const void* tile_sorted_keys;        /* (I) key_bytes wide */
-    const uint32_t* tile_sorted_instances; /* (I) emission index of each sorted instance */
+    const uint32_t* visible_prims;       /* (V) the visible primitives in index order */
+    const uint32_t* prim_offset;         /* (N) first emission slot of each visible primitive (exclusive scan of
+                                            n_touched in index order) */
+    const void* instance_keys;           /* (I) tile key of every emission slot, key_bytes wide */
     const uint32_t* instance_primitive;  /* (I) primitive per emission index */
+    const void* tile_sorted_keys;        /* (I) key_bytes wide: the tile of every sorted instance */
+    const uint32_t* tile_sorted_instances; /* (I) emission index of each instance in (tile, depth, primitive) order */
     const uint32_t* tile_ranges;         /* (T x 2) [start, end) */
     const float* final_transmittance;    /* (T x 192) per tile, row-major 16 x 12 */
     const uint32_t* n_contributors;      /* (T x 192) */
@@ -219,19 +218,18 @@ int efgs_precompile(const efgs_rasterizer* r, const char* arch);
  * the number of timed launches since timing was (re-)enabled. Enabling again resets the totals. */
 enum {
     EFGS_STAGE_PREPROCESS_FORWARD = 0, /* hipRTC preprocess (projection, culling, appearance, MLP) */
-    EFGS_STAGE_COMPACT = 1,            /* per-block count scan + index-ordered compaction */
+    EFGS_STAGE_COMPACT = 1,            /* per-block count scan + index-ordered compaction with emission offsets */
     EFGS_STAGE_COUNTER_READ = 2,       /* (V, I) device-to-host read and stream synchronisation */
-    EFGS_STAGE_DEPTH_SORT = 3,
-    EFGS_STAGE_INSTANCE_OFFSETS = 4,   /* gathered exclusive scan of the tile counts */
-    EFGS_STAGE_CREATE_INSTANCES = 5,
-    EFGS_STAGE_TILE_SORT = 6,
-    EFGS_STAGE_TILE_RANGES = 7,
-    EFGS_STAGE_BLEND_FORWARD = 8,
-    EFGS_STAGE_BLEND_BACKWARD = 9,
-    EFGS_STAGE_PREPROCESS_BACKWARD = 10,
-    EFGS_STAGE_MLP_REDUCE = 11,        /* reduction of the per-block MLP weight-gradient partials */
-    EFGS_STAGE_MLP_BACKWARD = 12,      /* neural: MLP recompute + backward (EFGS_STAGE_PREPROCESS_BACKWARD is the rest) */
-    EFGS_N_STAGES = 13
+    EFGS_STAGE_CREATE_INSTANCES = 3,   /* (tile, primitive) instances at their emission slots, per-tile counts */
+    EFGS_STAGE_TILE_OFFSETS = 4,       /* scan of the per-tile counts: tile ranges */
+    EFGS_STAGE_TILE_BUCKETS = 5,       /* instances into their tiles' ranges */
+    EFGS_STAGE_TILE_SORT = 6,          /* per-tile (depth, primitive) order */
+    EFGS_STAGE_BLEND_FORWARD = 7,
+    EFGS_STAGE_BLEND_BACKWARD = 8,
+    EFGS_STAGE_PREPROCESS_BACKWARD = 9,
+    EFGS_STAGE_MLP_REDUCE = 10,        /* reduction of the per-block MLP weight-gradient partials */
+    EFGS_STAGE_MLP_BACKWARD = 11,      /* neural: MLP recompute + backward (EFGS_STAGE_PREPROCESS_BACKWARD is the rest) */
+    EFGS_N_STAGES = 12
 };
 int efgs_set_stage_timing(efgs_rasterizer* r, int enable);
 int efgs_get_stage_times(efgs_rasterizer* r, double* total_ms, int64_t* launches, int n_stages);

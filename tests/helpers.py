@@ -109,3 +109,19 @@ def read_device(buffers, ptr: int, count: int, dtype) -> np.ndarray:
         if base <= ptr and ptr + nbytes <= base + b.numel():
             return b[ptr - base: ptr - base + nbytes].cpu().numpy().view(dtype).copy()
     raise AssertionError('pointer outside the frame buffers')
+
+
+def check_emission(bufs, v, frame, fw, n: int) -> None:
+    """Index-ordered emission against the oracle: the visible primitives in index order, each one's first
+    emission slot (exclusive scan of the tile counts in index order) and, at the emission slots, every
+    primitive's tiles in ascending order (its tile rectangle in row-major order)."""
+    V, I = int(frame.n_visible), int(frame.n_instances)
+    np.testing.assert_array_equal(read_device(bufs, v.visible_prims, V, np.uint32), fw.visible)
+    counts = fw.n_touched.astype(np.int64)
+    offsets = np.cumsum(counts) - counts
+    vis = fw.n_touched > 0
+    np.testing.assert_array_equal(read_device(bufs, v.prim_offset, n, np.uint32)[vis], offsets[vis])
+    order = np.lexsort((fw.inst_keys, fw.inst_prims))  # by primitive, then tile
+    kt = np.uint16 if frame.key_bytes == 2 else np.uint32
+    np.testing.assert_array_equal(read_device(bufs, v.instance_keys, I, kt).astype(np.uint32), fw.inst_keys[order])
+    np.testing.assert_array_equal(read_device(bufs, v.instance_primitive, I, np.uint32), fw.inst_prims[order])

@@ -28,7 +28,7 @@ def test_struct_sizes_match_header_layout():
     p = ctypes.sizeof(ctypes.c_void_p)
     assert ctypes.sizeof(_lib.Settings) == 3 * p + 3 * 4 + 6 * 4 + 3 * 4
     assert ctypes.sizeof(_lib.Primitives) == 8 + 8 * p
-    assert ctypes.sizeof(_lib.Frame) == 3 * p + 3 * 8 + 6 * 4
+    assert ctypes.sizeof(_lib.Frame) == 3 * p + 3 * 8 + 4 * 4
     assert ctypes.sizeof(_lib.AdamGroup) == 4 * p + 8 + 8 + 4 + 4 + 7 * 8 + 3 * 8
     assert ctypes.sizeof(_lib.FrameViews) == 13 * p
 
@@ -116,7 +116,7 @@ def test_stage_timing_without_launches():
     r = R.Rasterizer()
     r.set_stage_timing(True)
     times = r.stage_times()
-    assert set(times) == set(_lib.STAGES) and len(_lib.STAGES) == 13
+    assert set(times) == set(_lib.STAGES) and len(_lib.STAGES) == 12
     assert all(ms == 0.0 and n == 0 for ms, n in times.values())
     r.set_stage_timing(False)
 
@@ -131,8 +131,8 @@ def test_bench_algorithmic_bytes_match_the_c3_budget():
     N, V, I, T, P = 1_000_000, 699_021, 1_420_415, 10_800, 1920 * 1080
     F = bench.mlp_flops_per_primitive(11, 64, 2)
     assert F == 9_984
-    stages = ['preprocess_forward', 'compact', 'depth_sort', 'instance_offsets', 'create_instances', 'tile_sort',
-              'tile_ranges', 'blend_forward', 'blend_backward', 'preprocess_backward', 'mlp_backward']
+    stages = ['preprocess_forward', 'compact', 'create_instances', 'tile_offsets', 'tile_buckets', 'tile_sort', 'blend_forward',
+              'blend_backward', 'preprocess_backward', 'mlp_backward']
     total = sum(bench.algorithmic(s, N, V, I, T, P, 32, F, 0)[0] for s in stages)
     assert abs(total / 1e6 - 670.0) < 1.0
     assert bench.algorithmic('adam', N, V, I, T, P, 32, F, 22_006_144)[0] == 28 * 22_006_144

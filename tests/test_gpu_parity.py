@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from helpers import small_case, rel_l2, configure, torch_inputs, settings, read_device
+from helpers import small_case, rel_l2, configure, torch_inputs, settings, read_device, check_emission
 
 pytestmark = pytest.mark.gpu
 
@@ -86,10 +86,7 @@ def test_forward_parity(name):
     counters = read_device(bufs, v.counters, 8, np.uint32)
     if V > 0:
         assert counters[3] == fw.depth_key[vis].min() and counters[4] == fw.depth_key[vis].max()
-    # sorted keys are stored relative to the smallest visible key (counters[3])
-    np.testing.assert_array_equal(read_device(bufs, v.depth_sorted_keys, V, np.uint32) + counters[3], fw.depth_key[fw.depth_sorted])
-    np.testing.assert_array_equal(read_device(bufs, v.depth_sorted_prims, V, np.uint32), fw.depth_sorted)
-    np.testing.assert_array_equal(read_device(bufs, v.instance_offsets, V, np.uint32), fw.offsets)
+    check_emission(bufs, v, frame, fw, n)
     kt = np.uint16 if frame.key_bytes == 2 else np.uint32
     np.testing.assert_array_equal(read_device(bufs, v.tile_sorted_keys, I, kt).astype(np.uint32), fw.inst_keys)
     sorted_inst = read_device(bufs, v.tile_sorted_instances, I, np.uint32)
