@@ -236,23 +236,70 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     bucket[pos] = key;
 }
 
-// Ascending bitonic sort of m (a power of two, <= tile_sort_capacity) 64-bit keys in LDS by the whole block.
-constexpr uint32_t tile_sort_block = 128;
-constexpr uint32_t tile_sort_capacity = 2048;
-__device__ __forceinline__ void bitonic_sort_lds(uint64_t* s, uint32_t m) {
-    for (uint32_t k = 2; k <= m; k <<= 1) {
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = threadIdx.x; i < m; i += tile_sort_block) {
-                const uint32_t ixj = i ^ j;
-                if (ixj > i) {
-                    const uint64_t a = s[i], b = s[ixj];
-                    if ((a > b) == ((i & k) == 0)) {
-                        s[i] = b;
-                        s[ixj] = a;
+// orders a wave's own LDS accesses across the steps of a network (the LDS executes a wave's instructions in
+// order; the fence keeps the compiler from moving them)
+__device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
+// Per-tile sort: one wave per tile, four tiles per block, no block barriers. Keys are unique 64-bit values
+// (depth key << 32 | emission index), sorted ascending by bitonic networks:
+//   n <= 256          in registers, four keys per lane (element x = 4 lane + i): exchanges at distance
+//                     j < 4 within a lane, j >= 4 with the lane at xor distance j / 4;
+//   256 < n <= 512    in the wave's LDS slab;
+//   n > 512           chunks of 512 sorted in the slab and written back to the tile's range, then every key
+//                     placed at (its index in its chunk) + (its rank in each other chunk).
+constexpr uint32_t tile_sort_waves = 4;
+constexpr uint32_t tile_sort_block = 64 * tile_sort_waves;
+constexpr uint32_t wave_slab = 512;
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, uint32_t d) {
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(v)), static_cast<int>(d)));
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(v >> 32)), static_cast<int>(d)));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+__device__ __forceinline__ void wave_bitonic_256(uint64_t (&k)[4], uint32_t lane) {
+#pragma unroll
+    for (uint32_t size = 2; size <= 256; size <<= 1) {
+#pragma unroll
+        for (uint32_t j = size >> 1; j > 0; j >>= 1) {
+            if (j >= 4) {
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) {
+                    const uint32_t x = 4u * lane + i;
+                    const uint64_t o = shfl_xor_u64(k[i], j >> 2);
+                    const bool keep_min = ((x & size) == 0) == ((x & j) == 0);
+                    k[i] = keep_min ? (k[i] < o ? k[i] : o) : (k[i] < o ? o : k[i]);
+                }
+            } else {
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) {
+                    if ((i & j) != 0) continue;
+                    const uint32_t x = 4u * lane + i;
+                    const uint64_t a = k[i], b = k[i ^ j];
+                    const bool swap = (a > b) == ((x & size) == 0);
+                    k[i] = swap ? b : a;
+                    k[i ^ j] = swap ? a : b;
+                }
+            }
+        }
+    }
+}
+
+// ascending bitonic sort of m (a power of two, <= wave_slab) keys in the wave's slab
+__device__ inline void wave_bitonic_lds(uint64_t* s, uint32_t m, uint32_t lane) {
+    for (uint32_t size = 2; size <= m; size <<= 1) {
+        for (uint32_t j = size >> 1; j > 0; j >>= 1) {
+            for (uint32_t x = lane; x < m; x += 64) {
+                const uint32_t y = x ^ j;
+                if (y > x) {
+                    const uint64_t a = s[x], b = s[y];
+                    if ((a > b) == ((x & size) == 0)) {
+                        s[x] = b;
+                        s[y] = a;
                     }
                 }
             }
-            __syncthreads();
+            wave_lds_fence();
         }
     }
 }
@@ -267,53 +314,71 @@ __device__ __forceinline__ uint32_t rank_in(const uint64_t* run, uint32_t n, uin
     return lo;
 }
 
-// One block per tile sorts the keys of its range ascending (keys are unique); the emission indices go to
-// sorted_inst and the tile id to sorted_keys. A tile of more than tile_sort_capacity instances sorts chunks
-// of that size in LDS back into its range, then places every key at (its index in its chunk) + (its rank
-// in each other chunk).
 template <typename KeyT>
 __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst,
-                                                                   KeyT* sorted_keys) {
-    __shared__ uint64_t s[tile_sort_capacity];
-    const uint32_t tile = blockIdx.x;
+                                                                   KeyT* sorted_keys, uint32_t n_tiles) {
+    __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t tile = blockIdx.x * tile_sort_waves + wave;
+    if (tile >= n_tiles) return;  // the whole wave (no block barriers below)
     const uint2 r = ranges[tile];
     const uint32_t n = r.y - r.x;
     if (n == 0) return;
     uint64_t* run = bucket + r.x;
-    if (n <= tile_sort_capacity) {
-        uint32_t m = 2;
-        while (m < n) m <<= 1;
-        for (uint32_t i = threadIdx.x; i < m; i += tile_sort_block) s[i] = i < n ? run[i] : ~0ull;
-        __syncthreads();
-        bitonic_sort_lds(s, m);
-        for (uint32_t i = threadIdx.x; i < n; i += tile_sort_block) {
-            sorted_inst[r.x + i] = static_cast<uint32_t>(s[i]);
-            sorted_keys[r.x + i] = static_cast<KeyT>(tile);
+    uint32_t* out = sorted_inst + r.x;
+    KeyT* out_keys = sorted_keys + r.x;
+    if (n <= 256) {
+        uint64_t k[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t x = 4u * lane + i;
+            k[i] = x < n ? run[x] : ~0ull;
+        }
+        wave_bitonic_256(k, lane);
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint32_t x = 4u * lane + i;
+            if (x < n) {
+                out[x] = static_cast<uint32_t>(k[i]);
+                out_keys[x] = static_cast<KeyT>(tile);
+            }
         }
         return;
     }
-    const uint32_t n_chunks = (n + tile_sort_capacity - 1) / tile_sort_capacity;
-    for (uint32_t c = 0; c < n_chunks; c++) {
-        const uint32_t c0 = c * tile_sort_capacity, cn = min(tile_sort_capacity, n - c0);
-        for (uint32_t i = threadIdx.x; i < tile_sort_capacity; i += tile_sort_block) s[i] = i < cn ? run[c0 + i] : ~0ull;
-        __syncthreads();
-        bitonic_sort_lds(s, tile_sort_capacity);
-        for (uint32_t i = threadIdx.x; i < cn; i += tile_sort_block) run[c0 + i] = s[i];
-        __syncthreads();
+    uint64_t* s = s_slab[wave];
+    if (n <= wave_slab) {
+        uint32_t m = 512;
+        while (m < n) m <<= 1;
+        for (uint32_t x = lane; x < m; x += 64) s[x] = x < n ? run[x] : ~0ull;
+        wave_lds_fence();
+        wave_bitonic_lds(s, m, lane);
+        for (uint32_t x = lane; x < n; x += 64) {
+            out[x] = static_cast<uint32_t>(s[x]);
+            out_keys[x] = static_cast<KeyT>(tile);
+        }
+        return;
     }
-    __threadfence();
-    __syncthreads();
-    for (uint32_t idx = threadIdx.x; idx < n; idx += tile_sort_block) {
-        const uint64_t x = run[idx];
-        const uint32_t c = idx / tile_sort_capacity;
-        uint32_t pos = idx - c * tile_sort_capacity;
+    const uint32_t n_chunks = (n + wave_slab - 1) / wave_slab;
+    for (uint32_t c = 0; c < n_chunks; c++) {
+        const uint32_t c0 = c * wave_slab, cn = min(wave_slab, n - c0);
+        for (uint32_t x = lane; x < wave_slab; x += 64) s[x] = x < cn ? run[c0 + x] : ~0ull;
+        wave_lds_fence();
+        wave_bitonic_lds(s, wave_slab, lane);
+        for (uint32_t x = lane; x < cn; x += 64) run[c0 + x] = s[x];
+        wave_lds_fence();
+    }
+    __threadfence();  // the wave reads back the chunks it wrote
+    for (uint32_t idx = lane; idx < n; idx += 64) {
+        const uint64_t key = run[idx];
+        const uint32_t c = idx / wave_slab;
+        uint32_t pos = idx - c * wave_slab;
         for (uint32_t o = 0; o < n_chunks; o++) {
             if (o == c) continue;
-            const uint32_t o0 = o * tile_sort_capacity;
-            pos += rank_in(run + o0, min(tile_sort_capacity, n - o0), x);
+            const uint32_t o0 = o * wave_slab;
+            pos += rank_in(run + o0, min(wave_slab, n - o0), key);
         }
-        sorted_inst[r.x + pos] = static_cast<uint32_t>(x);
-        sorted_keys[r.x + pos] = static_cast<KeyT>(tile);
+        out[pos] = static_cast<uint32_t>(key);
+        out_keys[pos] = static_cast<KeyT>(tile);
     }
 }
 
@@ -429,9 +494,11 @@ bool launch_tile_sort(const uint2* ranges, uint64_t* bucket, uint32_t* sorted_in
                       hipStream_t s) {
     if (n_tiles == 0) return true;
     if (key_bytes == 2)
-        tile_sort_kernel<uint16_t><<<n_tiles, tile_sort_block, 0, s>>>(ranges, bucket, sorted_inst, static_cast<uint16_t*>(sorted_keys));
+        tile_sort_kernel<uint16_t><<<div_up(n_tiles, tile_sort_waves), tile_sort_block, 0, s>>>(ranges, bucket, sorted_inst,
+                                                                                              static_cast<uint16_t*>(sorted_keys), n_tiles);
     else
-        tile_sort_kernel<uint32_t><<<n_tiles, tile_sort_block, 0, s>>>(ranges, bucket, sorted_inst, static_cast<uint32_t*>(sorted_keys));
+        tile_sort_kernel<uint32_t><<<div_up(n_tiles, tile_sort_waves), tile_sort_block, 0, s>>>(ranges, bucket, sorted_inst,
+                                                                                              static_cast<uint32_t*>(sorted_keys), n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

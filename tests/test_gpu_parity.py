@@ -32,6 +32,10 @@ CASES = {
     'nasgabor': dict(model='nasgabor', acts=('none', 'tanh', 'softplus')),
     'ragged_image': dict(model='sh', width=50, height=37),
     'dense_2k': dict(model='sh', n=2000, width=96, height=80, scale_shift=1.5),
+    # tiles of 171-632 and of 716-2549 instances: every path of the per-tile sort (registers, LDS slab,
+    # chunks merged by rank) and many staging batches in the blends
+    'dense_tiles_3k': dict(model='sh', n=3000, scale_shift=2.0),
+    'dense_tiles_12k': dict(model='sh', n=12000, scale_shift=2.0),
     'neural_c3_mlp': dict(model='neural', scale_shift=2.5),
     'neural_reference_default': dict(model='neural', scale_shift=2.5, acts=('none', 'tanh', 'relu'),
                                      mlp=dict(n_feature_dims=8, n_frequencies=1, sh_degrees=(0, 1, 2, 3), n_neurons=16,
