@@ -211,8 +211,11 @@ struct TileLayout {
     float* final_T;
     uint32_t* n_contrib;
     uint32_t* tile_max;
-    uint32_t* totals;       // instances per tile
-    uint32_t* tile_start;   // first slot of every tile (the bucket cursor without a count table)
+    uint32_t* totals;        // instances per tile
+    uint32_t* local_start;   // tile start within its 256-tile block
+    uint32_t* block_sums;    // instances per 256-tile block
+    uint32_t* block_prefix;  // instances of the earlier 256-tile blocks
+    uint32_t* cursor;        // per-tile bucket cursor of the global-atomic path
     size_t bytes;
 
     static TileLayout carve(char* base, uint32_t n_tiles) {
@@ -223,7 +226,10 @@ struct TileLayout {
         l.n_contrib = c.take<uint32_t>(static_cast<uint64_t>(n_tiles) * tile_pixels);
         l.tile_max = c.take<uint32_t>(n_tiles);
         l.totals = c.take<uint32_t>(n_tiles);
-        l.tile_start = c.take<uint32_t>(n_tiles);
+        l.local_start = c.take<uint32_t>(n_tiles);
+        l.block_sums = c.take<uint32_t>(div_up(n_tiles > 0 ? n_tiles : 1, 256));
+        l.block_prefix = c.take<uint32_t>(div_up(n_tiles > 0 ? n_tiles : 1, 256));
+        l.cursor = c.take<uint32_t>(n_tiles);
         l.bytes = c.offset + buffer_alignment;
         return l;
     }
@@ -677,17 +683,16 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
                                  n_visible, s))
         return EFGS_ERR_HIP;
     t.end(s);
+    const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.block_prefix, pl.counters + 5, tl.cursor};
     t.begin(EFGS_STAGE_TILE_OFFSETS, s);
-    if (!launch_tile_counts(plan, il.keys, key_bytes, n_instances, il.local_rank, il.table, tl.totals, n_tiles, s)) return EFGS_ERR_HIP;
-    if (!launch_tile_offsets(tl.totals, tl.ranges, tl.tile_start, n_tiles, s)) return EFGS_ERR_HIP;
+    if (!launch_tile_counts(plan, il.keys, key_bytes, n_instances, il.local_rank, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
     t.end(s);
     t.begin(EFGS_STAGE_TILE_BUCKETS, s);
-    if (!launch_tile_buckets(plan, il.keys, key_bytes, il.inst_prim, pl.depth_keys, il.table, il.local_rank, tl.tile_start, il.bucket, n_instances,
-                             n_tiles, s))
+    if (!launch_tile_buckets(plan, il.keys, key_bytes, il.inst_prim, pl.depth_keys, il.table, il.local_rank, ts, il.bucket, n_instances, n_tiles, s))
         return EFGS_ERR_HIP;
     t.end(s);
     t.begin(EFGS_STAGE_TILE_SORT, s);
-    if (!launch_tile_sort(tl.ranges, il.bucket, il.sorted_inst, il.sorted_keys, key_bytes, n_tiles, s)) return EFGS_ERR_HIP;
+    if (!launch_tile_sort(ts, tl.ranges, il.bucket, il.sorted_inst, il.sorted_keys, key_bytes, n_tiles, s)) return EFGS_ERR_HIP;
     t.end(s);
     const uint32_t* sorted_inst = il.sorted_inst;
 

@@ -29,7 +29,8 @@ inline uint32_t div_up(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a
 
 // ---- rasterizer stages -------------------------------------------------------------------------------------
 bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
-// counters: [0] V, [1] I, [2] instance-emission mismatches, [3] / [4] min / max depth key of the visible set
+// counters: [0] V, [1] I, [2] instance-emission mismatches, [3] / [4] min / max depth key of the visible set,
+// [5] ticket of the tile scan's last block
 constexpr uint32_t n_counters = 8;
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
                               uint32_t n_blocks, hipStream_t s);
@@ -52,20 +53,30 @@ struct TileBinning {
     uint32_t segment;  // emission slots per histogram block
 };
 TileBinning tile_binning_plan(uint32_t n_instances, uint32_t n_tiles);
-// totals[t] = instances of tile t; with the table also every instance's rank within its segment's slots of
-// its tile (local_rank) and, per segment, the tile's count in the earlier segments (table)
+// Tile scan state (tile arena): totals[t] instances of tile t, local_start[t] exclusive scan of the totals
+// within t's 256-tile block, block_prefix[t / 256] the totals of the earlier blocks (tile t starts at
+// block_prefix[t / 256] + local_start[t]), block_sums per 256-tile block, the ticket of the block that scans
+// them (counters[5], zeroed by scan_block_counts), and a per-tile cursor for the global-atomic path.
+struct TileScan {
+    uint32_t* totals;
+    uint32_t* local_start;
+    uint32_t* block_sums;
+    uint32_t* block_prefix;
+    uint32_t* ticket;
+    uint32_t* cursor;
+};
+// per-tile counts (LDS histograms over segments of the emission slots with per-instance ranks and the
+// segment table, or global atomics) and the scan above
 bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* local_rank, uint32_t* table,
-                        uint32_t* totals, uint32_t n_tiles, hipStream_t s);
-// per-tile [start, end) ranges and starts from the totals
-bool launch_tile_offsets(const uint32_t* totals, uint2* ranges, uint32_t* tile_start, uint32_t n_tiles, hipStream_t s);
-// every instance's sort key (depth key of its primitive << 32 | emission index) into a slot of its tile's
-// range (without the table, tile_start serves as the atomic cursor and is advanced)
+                        const TileScan& ts, uint32_t n_tiles, hipStream_t s);
+// every instance's sort key (depth key of its primitive << 32 | emission index) into a slot of its tile's range
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
-                         const uint32_t* table, const uint32_t* local_rank, uint32_t* tile_start, uint64_t* bucket, uint32_t n_instances,
+                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,
                          uint32_t n_tiles, hipStream_t s);
-// per tile: keys sorted ascending -> emission indices in sorted_inst, tile id in sorted_keys
-bool launch_tile_sort(const uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes, uint32_t n_tiles,
-                      hipStream_t s);
+// per tile: [start, end) into ranges and its keys sorted ascending -> emission indices in sorted_inst, tile id
+// in sorted_keys
+bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
+                      uint32_t n_tiles, hipStream_t s);
 bool launch_reduce_partials(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out, hipStream_t s);
 
 struct BlendForwardArgs {

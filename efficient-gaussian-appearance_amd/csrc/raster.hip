@@ -146,22 +146,77 @@ __global__ __launch_bounds__(1024) void tile_hist_kernel(const void* keys_raw, i
     for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) row[t] = hist[t];
 }
 
-// one thread per tile: table[b][t] <- sum of table[b'][t] over b' < b; totals[t] <- the column sum
-__global__ __launch_bounds__(256) void tile_block_scan_kernel(uint32_t* table, uint32_t n_blocks, uint32_t n_tiles, uint32_t* totals) {
+// exclusive scan of one value per thread over a 256-thread block; sum receives the block total
+__device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_waves, uint32_t& sum) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(inc, o);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) s_waves[wave] = inc;
+    __syncthreads();
+    uint32_t prefix = 0;
+    sum = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 4; w++) {
+        const uint32_t x = s_waves[w];
+        if (w < wave) prefix += x;
+        sum += x;
+    }
+    __syncthreads();
+    return prefix + inc - v;
+}
+
+// One thread per tile, 256 tiles per block. With a count table: the tile's column becomes exclusive prefixes
+// over the histogram segments and its sum the tile's total; without one the totals come from the global
+// counts. Then the block's exclusive scan of its totals (local_start) and the block sum; the last block to
+// finish (atomic ticket, zeroed by scan_block_counts) scans the block sums into block_prefix, so the start
+// of tile t is block_prefix[t / 256] + local_start[t].
+__global__ __launch_bounds__(256) void tile_block_scan_kernel(uint32_t* table, uint32_t n_segments, uint32_t n_tiles, uint32_t* totals,
+                                                              uint32_t* local_start, uint32_t* block_sums, uint32_t* block_prefix,
+                                                              uint32_t* ticket) {
+    __shared__ uint32_t s_waves[4];
+    __shared__ bool s_last;
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
-    if (t >= n_tiles) return;
-    uint32_t run = 0;
-    for (uint32_t b0 = 0; b0 < n_blocks; b0 += 8) {  // 8 loads in flight
-        uint32_t c[8];
+    uint32_t count = 0;
+    if (t < n_tiles) {
+        if (table) {
+            for (uint32_t b0 = 0; b0 < n_segments; b0 += 8) {  // 8 loads in flight
+                uint32_t c[8];
 #pragma unroll
-        for (uint32_t k = 0; k < 8; k++) c[k] = b0 + k < n_blocks ? table[static_cast<size_t>(b0 + k) * n_tiles + t] : 0u;
+                for (uint32_t k = 0; k < 8; k++) c[k] = b0 + k < n_segments ? table[static_cast<size_t>(b0 + k) * n_tiles + t] : 0u;
 #pragma unroll
-        for (uint32_t k = 0; k < 8; k++) {
-            if (b0 + k < n_blocks) table[static_cast<size_t>(b0 + k) * n_tiles + t] = run;
-            run += c[k];
+                for (uint32_t k = 0; k < 8; k++) {
+                    if (b0 + k < n_segments) table[static_cast<size_t>(b0 + k) * n_tiles + t] = count;
+                    count += c[k];
+                }
+            }
+            totals[t] = count;
+        } else {
+            count = totals[t];
         }
     }
-    totals[t] = run;
+    uint32_t sum;
+    const uint32_t ex = block_exclusive_scan_256(count, s_waves, sum);
+    if (t < n_tiles) local_start[t] = ex;
+    if (threadIdx.x == 0) block_sums[blockIdx.x] = sum;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(ticket, 1u) == gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();  // every block's sum is visible to the last block
+    uint32_t carry = 0;
+    for (uint32_t base = 0; base < gridDim.x; base += 256) {
+        const uint32_t i = base + threadIdx.x;
+        const uint32_t v = i < gridDim.x ? block_sums[i] : 0u;
+        uint32_t chunk;
+        const uint32_t e = block_exclusive_scan_256(v, s_waves, chunk);
+        if (i < gridDim.x) block_prefix[i] = carry + e;
+        carry += chunk;
+    }
 }
 
 template <typename KeyT>
@@ -172,67 +227,26 @@ __global__ __launch_bounds__(256) void tile_count_global_kernel(const KeyT* keys
     if (t < n_tiles) atomicAdd(&totals[t], 1u);
 }
 
-// One block: exclusive scan of the per-tile totals in chunks of 1024 x 8 (carry between chunks) ->
-// ranges[t] = [start, start + count) ((0, 0) for an empty tile, as the reference's zero-filled ranges) and
-// tile_start[t] = start.
-__global__ __launch_bounds__(1024) void tile_offsets_kernel(const uint32_t* counts, uint2* ranges, uint32_t* tile_start, uint32_t n_tiles) {
-    constexpr uint32_t per = 8;
-    __shared__ uint32_t wave_totals[1024 / 64];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    uint32_t carry = 0;
-    for (uint32_t base = 0; base < n_tiles; base += 1024 * per) {
-        const uint32_t t0 = base + threadIdx.x * per;
-        uint32_t c[per];
-        uint32_t sum = 0;
-#pragma unroll
-        for (uint32_t k = 0; k < per; k++) {
-            c[k] = t0 + k < n_tiles ? counts[t0 + k] : 0u;
-            sum += c[k];
-        }
-        uint32_t inc = sum;
-#pragma unroll
-        for (uint32_t o = 1; o < 64; o <<= 1) {
-            const uint32_t v = __shfl_up(inc, o);
-            if (lane >= o) inc += v;
-        }
-        if (lane == 63) wave_totals[wave] = inc;
-        __syncthreads();
-        uint32_t prefix = carry, total = 0;
-#pragma unroll
-        for (uint32_t w = 0; w < 1024 / 64; w++) {
-            const uint32_t v = wave_totals[w];
-            if (w < wave) prefix += v;
-            total += v;
-        }
-        __syncthreads();
-        prefix += inc - sum;
-#pragma unroll
-        for (uint32_t k = 0; k < per; k++) {
-            if (t0 + k < n_tiles) {
-                ranges[t0 + k] = c[k] > 0 ? make_uint2(prefix, prefix + c[k]) : make_uint2(0u, 0u);
-                tile_start[t0 + k] = prefix;
-            }
-            prefix += c[k];
-        }
-        carry += total;
-    }
+__device__ __forceinline__ uint32_t tile_start_of(const uint32_t* block_prefix, const uint32_t* local_start, uint32_t t) {
+    return block_prefix[t >> 8] + local_start[t];
 }
 
 // Every emitted instance goes to a slot of its tile's range: start of the tile + the tile's count in the
-// earlier histogram blocks + its rank within its block (with a table), or the next slot of an atomic cursor
-// (without one: tile_start is advanced). The slot receives the instance's sort key, the depth key of its
-// primitive above its emission index.
+// earlier histogram segments + its rank within its segment (with a table), or + the next slot of an atomic
+// cursor (without one). The slot receives the instance's sort key, the depth key of its primitive above
+// its emission index.
 template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
                                                           const uint32_t* table, const uint32_t* local_rank, uint32_t seg,
-                                                          uint32_t* tile_start, uint64_t* bucket, uint32_t n_instances, uint32_t n_tiles) {
+                                                          const uint32_t* block_prefix, const uint32_t* local_start, uint32_t* cursor,
+                                                          uint64_t* bucket, uint32_t n_instances, uint32_t n_tiles) {
     const uint32_t e = blockIdx.x * 256u + threadIdx.x;
     if (e >= n_instances) return;
     const uint32_t t = static_cast<uint32_t>(keys[e]);
     if (t >= n_tiles) return;
     const uint64_t key = (static_cast<uint64_t>(depth_keys[inst_prim[e]]) << 32) | e;
-    const uint32_t pos = table ? tile_start[t] + table[static_cast<size_t>(e / seg) * n_tiles + t] + local_rank[e]
-                               : atomicAdd(&tile_start[t], 1u);
+    const uint32_t pos = tile_start_of(block_prefix, local_start, t) +
+                         (table ? table[static_cast<size_t>(e / seg) * n_tiles + t] + local_rank[e] : atomicAdd(&cursor[t], 1u));
     bucket[pos] = key;
 }
 
@@ -315,14 +329,17 @@ __device__ __forceinline__ uint32_t rank_in(const uint64_t* run, uint32_t n, uin
 }
 
 template <typename KeyT>
-__global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst,
-                                                                   KeyT* sorted_keys, uint32_t n_tiles) {
+__global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* totals, const uint32_t* block_prefix,
+                                                                   const uint32_t* local_start, uint2* ranges, uint64_t* bucket,
+                                                                   uint32_t* sorted_inst, KeyT* sorted_keys, uint32_t n_tiles) {
     __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t tile = blockIdx.x * tile_sort_waves + wave;
     if (tile >= n_tiles) return;  // the whole wave (no block barriers below)
-    const uint2 r = ranges[tile];
-    const uint32_t n = r.y - r.x;
+    const uint32_t n = totals[tile];
+    const uint32_t start = tile_start_of(block_prefix, local_start, tile);
+    const uint2 r = n > 0 ? make_uint2(start, start + n) : make_uint2(0u, 0u);  // (0, 0) for an empty tile, as the reference
+    if (lane == 0) ranges[tile] = r;
     if (n == 0) return;
     uint64_t* run = bucket + r.x;
     uint32_t* out = sorted_inst + r.x;
@@ -447,58 +464,54 @@ TileBinning tile_binning_plan(uint32_t n_instances, uint32_t n_tiles) {
 }
 
 bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* local_rank, uint32_t* table,
-                        uint32_t* totals, uint32_t n_tiles, hipStream_t s) {
+                        const TileScan& ts, uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
-    if (plan.use_table) {
-        if (n_instances == 0) return launch_fill_u32(totals, 0u, n_tiles, s);
+    const bool with_table = plan.use_table && n_instances > 0;
+    if (with_table) {
         tile_hist_kernel<<<plan.blocks, 1024, n_tiles * 4, s>>>(keys, key_bytes, n_instances, plan.segment, local_rank, table, n_tiles);
-        tile_block_scan_kernel<<<div_up(n_tiles, 256), 256, 0, s>>>(table, plan.blocks, n_tiles, totals);
     } else {
-        if (!launch_fill_u32(totals, 0u, n_tiles, s)) return false;
-        if (n_instances == 0) return true;
-        if (key_bytes == 2)
-            tile_count_global_kernel<uint16_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint16_t*>(keys), n_instances, totals,
-                                                                                       n_tiles);
-        else
-            tile_count_global_kernel<uint32_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint32_t*>(keys), n_instances, totals,
-                                                                                       n_tiles);
+        if (!launch_fill_u32(ts.totals, 0u, n_tiles, s) || !launch_fill_u32(ts.cursor, 0u, n_tiles, s)) return false;
+        if (n_instances > 0) {
+            if (key_bytes == 2)
+                tile_count_global_kernel<uint16_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint16_t*>(keys), n_instances,
+                                                                                           ts.totals, n_tiles);
+            else
+                tile_count_global_kernel<uint32_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint32_t*>(keys), n_instances,
+                                                                                           ts.totals, n_tiles);
+        }
     }
-    EFGS_HIP_CHECK(hipGetLastError());
-    return true;
-}
-
-bool launch_tile_offsets(const uint32_t* totals, uint2* ranges, uint32_t* tile_start, uint32_t n_tiles, hipStream_t s) {
-    if (n_tiles == 0) return true;
-    tile_offsets_kernel<<<1, 1024, 0, s>>>(totals, ranges, tile_start, n_tiles);
+    tile_block_scan_kernel<<<div_up(n_tiles, 256), 256, 0, s>>>(with_table ? table : nullptr, with_table ? plan.blocks : 0u, n_tiles, ts.totals,
+                                                                  ts.local_start, ts.block_sums, ts.block_prefix, ts.ticket);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
 
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
-                         const uint32_t* table, const uint32_t* local_rank, uint32_t* tile_start, uint64_t* bucket, uint32_t n_instances,
+                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,
                          uint32_t n_tiles, hipStream_t s) {
     if (n_instances == 0) return true;
     const uint32_t blocks = div_up(n_instances, 256);
     const uint32_t* tab = plan.use_table ? table : nullptr;
     if (key_bytes == 2)
         tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, plan.segment,
-                                                            tile_start, bucket, n_instances, n_tiles);
+                                                            ts.block_prefix, ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
     else
         tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, plan.segment,
-                                                            tile_start, bucket, n_instances, n_tiles);
+                                                            ts.block_prefix, ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
 
-bool launch_tile_sort(const uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes, uint32_t n_tiles,
-                      hipStream_t s) {
+bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
+                      uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
+    const uint32_t blocks = div_up(n_tiles, tile_sort_waves);
     if (key_bytes == 2)
-        tile_sort_kernel<uint16_t><<<div_up(n_tiles, tile_sort_waves), tile_sort_block, 0, s>>>(ranges, bucket, sorted_inst,
-                                                                                              static_cast<uint16_t*>(sorted_keys), n_tiles);
+        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_prefix, ts.local_start, ranges, bucket, sorted_inst,
+                                                                     static_cast<uint16_t*>(sorted_keys), n_tiles);
     else
-        tile_sort_kernel<uint32_t><<<div_up(n_tiles, tile_sort_waves), tile_sort_block, 0, s>>>(ranges, bucket, sorted_inst,
-                                                                                              static_cast<uint32_t*>(sorted_keys), n_tiles);
+        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_prefix, ts.local_start, ranges, bucket, sorted_inst,
+                                                                     static_cast<uint32_t*>(sorted_keys), n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

@@ -86,6 +86,7 @@ __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t*
         counters[2] = 0;  // instance-emission mismatch counter, see create_instances
         counters[3] = tv > 0 ? lo : 0u;
         counters[4] = tv > 0 ? hi : 0u;
+        counters[5] = 0;  // ticket of the tile scan's last block
     }
 }
 
