@@ -91,9 +91,10 @@ def test_fused_adam_matches_oracle_bitwise():
     import efgs
     dev = torch.device('cuda:0')
     rng = np.random.default_rng(0)
-    shapes = [(1000, 3), (1000, 8, 7), (6144,)]
-    lrs = [1e-3, [1e-2, 1e-2, 1e-2, 5e-3, 2e-3, 2e-3, 2e-3], 4e-4]
-    betas = [(0.9, 0.999), (0.9, 0.999), (0.9, 0.99)]
+    # an LR list cycling over a trailing dimension of 7, and an odd-sized group with a 3-entry list
+    shapes = [(1000, 3), (1000, 8, 7), (6144,), (1001,)]
+    lrs = [1e-3, [1e-2, 1e-2, 1e-2, 5e-3, 2e-3, 2e-3, 2e-3], 4e-4, [3e-3, 1e-3, 2e-3]]
+    betas = [(0.9, 0.999), (0.9, 0.999), (0.9, 0.99), (0.8, 0.99)]
     params = [torch.tensor(rng.normal(size=s).astype(np.float32), device=dev, requires_grad=True) for s in shapes]
     groups = [{'params': [p], 'lr': lr, 'betas': b} for p, lr, b in zip(params, lrs, betas)]
     opt = efgs.FusedAdam(groups, lr=0.0, eps=1e-15)
