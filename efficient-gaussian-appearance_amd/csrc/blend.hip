@@ -6,9 +6,9 @@
 // Small Gaussians cover few pixels: a 4x4 group wastes far fewer lanes than a 16x4 band would.
 //
 // Forward: front-to-back compositing, alpha = o exp2(min(q, 0)) with the conic pre-scaled by -log2(e)/2 and
-// exp2 from ef_exp2f (a fixed operation sequence, so alpha, T and the image are reproducible bit for bit),
-// alpha < 1/255 skipped, stop at T < 1e-4; stores the image, final T and last-contributor index per pixel and
-// the per-tile maximum. No per-bucket checkpoints.
+// the hardware exp2 (v_exp_f32, as the reference's fast-math exp2f), alpha < 1/255 skipped, stop at
+// T < 1e-4; stores the image, final T and last-contributor index per pixel and the per-tile maximum. No
+// per-bucket checkpoints.
 //
 // Backward: every pixel replays its forward walk (the evaluation below is shared and compiled with
 // -ffp-contract=off, so T and every skip decision are reproduced bit-exactly) and forms the reference's
@@ -35,14 +35,14 @@ __device__ __forceinline__ float4 scale_conic_for_exp2(float cx, float cy, float
     return make_float4(-0.5f * log2e * cx, -log2e * cy, -0.5f * log2e * cz, opacity);
 }
 
-// alpha of a staged Gaussian at a pixel centre; G receives the Gaussian factor
-// exponent clamped to [-127, 0] with one median-of-three (the same value as min(q, 0) then max(-127) for
-// every finite q)
+// alpha of a staged Gaussian at a pixel centre; G receives the Gaussian factor. v_exp_f32 (a quarter-rate
+// instruction: 4 issue slots) replaces an 11-operation polynomial; its result is a fixed function of q, so
+// the backward's replay reproduces the forward's alpha, T and decisions bit for bit.
 __device__ __forceinline__ float eval_alpha(float4 xy, float4 co, float pxf, float pyf, float& dx, float& dy, float& G) {
     dx = xy.x - pxf;
     dy = xy.y - pyf;
     const float q = __builtin_fmaf(dx, __builtin_fmaf(co.x, dx, co.y * dy), co.z * dy * dy);
-    G = ef_exp2f_clamped(__builtin_amdgcn_fmed3f(q, -127.0f, 0.0f));
+    G = __builtin_amdgcn_exp2f(fminf(q, 0.0f));
     return co.w * G;
 }
 

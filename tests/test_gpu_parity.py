@@ -1,15 +1,17 @@
 """GPU parity: the HIP path (through the C ABI) against the CPU oracle on identical seeded scenes.
 
 Bars: integer / key / index / range arrays bit-exact; per-primitive projection records (mean2d, conic,
-opacity, bounds) bit-exact (shared decision-path arithmetic); image max-abs <= 1e-4 (fp32 path, in practice
-bit-exact: the blend shares its exp2 with the oracle) and <= 2e-3 (fp16 neural MLP path); last-contributor
-indices equal (fp32 path); gradients rel-L2 <= 1e-3, including the MLP weight gradients.
+opacity, bounds) bit-exact (shared decision-path arithmetic); image max-abs <= 1e-4 (fp32 path; the blend's
+alpha uses the hardware exp2) and <= 2e-3 (fp16 neural MLP path); last-contributor indices equal up to
+near-threshold decisions (fp32 path: at most 2 + 1e-5 of the pixels); gradients rel-L2 <= 1e-3, including the
+MLP weight gradients.
 """
 import numpy as np
 import pytest
 
 import oracle as O
-from helpers import small_case, rel_l2, configure, torch_inputs, settings, read_device, check_emission
+from helpers import small_case, rel_l2, configure, torch_inputs, settings, read_device, check_emission, \
+    contributor_tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -107,8 +109,11 @@ def test_forward_parity(name):
     nc = read_device(bufs, v.n_contributors, gw * gh * 192, np.uint32).reshape(gh, gw, 12, 16).transpose(0, 2, 1, 3).reshape(gh * 12, gw * 16)
     nc = nc[:cam.height, :cam.width].reshape(-1)
     mism = np.count_nonzero(nc != fw.n_contrib)
+    print(f'case {name}: {mism} last-contributor mismatches of {nc.size}', flush=True)
     if CASES[name].get('model') != 'neural':
-        assert mism == 0, f'{mism} last-contributor mismatches'
+        # alpha uses the hardware exp2 (the oracle a correctly rounded one): a skip or stop decision can flip
+        # where alpha sits within an ulp of 1/255 or T of 1e-4
+        assert mism <= contributor_tolerance(nc.size), f'{mism} last-contributor mismatches'
 
 
 def _check_backward(name, densify_rows):
