@@ -301,36 +301,27 @@ MlpShape mlp_shape(const efgs_rasterizer* r) {
 // fp16 weight count of the tcnn-flat layout [W0 n x in_pad][W_h n x n]*(L-1)[W_out 16 x n]
 uint32_t mlp_params(const MlpShape& m) { return m.n_neurons * m.n_in_padded + (m.n_hidden - 1) * m.n_neurons * m.n_neurons + 16 * m.n_neurons; }
 
-// fp16 weights W_l and W_l^T with rows padded by 4 halves, as laid out by the neural kernels in LDS
-uint32_t mlp_dual_weight_bytes(const MlpShape& m) {
+// fp16 weights W_l and W_l^T with rows padded by 8 halves, as laid out by the neural kernels in LDS
+uint32_t mlp_weight_bytes(const MlpShape& m) {
     uint32_t halves = 0;
     for (uint32_t l = 0; l <= m.n_hidden; l++) {
         const uint32_t in = l == 0 ? m.n_in_padded : m.n_neurons;
         const uint32_t out = l == m.n_hidden ? 16u : m.n_neurons;
-        halves += out * (in + 4) + in * (out + 4);
+        halves += out * (in + 8) + in * (out + 8);
     }
     return (halves * 2 + 15) / 16 * 16;
 }
 
-// the forward's neural preprocess kernel: weights + 4 per-wave staging areas of 64 rows of (n_in_padded + 4) halves
-uint32_t mlp_smem_forward(const MlpShape& m) { return mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 2; }
+// the forward's neural kernels (preprocess, decode): weights + 4 per-wave staging areas of 64 rows of
+// (n_in_padded + 4) halves
+uint32_t mlp_smem_forward(const MlpShape& m) { return mlp_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 2; }
 
-// the backward's MLP kernel: W and W^T with rows padded by 4 halves, 4 per-wave staging areas of 64 rows of
-// (n_in_padded + 4) floats; the area is reused for the fp32 block reduction of the weight gradients
 constexpr uint32_t max_dynamic_lds = 160 * 1024;  // gfx950: 160 KiB of LDS per block
 
-// per-wave LDS store of hidden layers 2..n_hidden's primitive-rows input tiles (one 8-byte slot per lane and
-// tile; layer 1's are recomputed from the input tiles)
-uint32_t mlp_u_store_bytes(const MlpShape& m) { return (m.n_hidden > 1 ? m.n_hidden - 1 : 0u) * (m.n_neurons / 16) * 4 * 64 * 8; }
-
-uint32_t mlp_smem_backward_base(const MlpShape& m) { return mlp_dual_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 4; }
-
-// the backward's MLP kernel keeps those tiles out of its registers when two blocks still fit a CU's LDS
-// (the kernel is then built for two waves per SIMD)
-bool mlp_u_in_lds(const MlpShape& m) { return 2 * (mlp_smem_backward_base(m) + 4 * mlp_u_store_bytes(m)) <= max_dynamic_lds; }
-
+// the backward's MLP kernels (preprocess, decode): weights + 4 per-wave staging areas of 64 rows of
+// (n_in_padded + 4) floats; the whole area is reused for the fp32 block reduction of the weight gradients
 uint32_t mlp_smem_backward(const MlpShape& m) {
-    const uint32_t f = mlp_smem_backward_base(m) + (mlp_u_in_lds(m) ? 4 * mlp_u_store_bytes(m) : 0u);
+    const uint32_t f = mlp_weight_bytes(m) + 4 * 64 * (m.n_in_padded + 4) * 4;
     const uint32_t red = mlp_params(m) * 4;
     return f > red ? f : red;
 }
@@ -354,7 +345,6 @@ void kernel_source(const efgs_rasterizer* r, int model, const char* kind, std::s
     preamble += "#define EFGS_N_FREQUENCIES " + std::to_string(model == 5 ? r->mlp_n_frequencies : 0) + "u\n";
     preamble += "#define EFGS_SH_DEGREE_MASK " + std::to_string(model == 5 ? r->mlp_sh_mask : 0) + "u\n";
     preamble += "#define EFGS_BASE_INPUT " + std::string(model == 5 && r->mlp_base_input ? "1" : "0") + "\n";
-    preamble += "#define EFGS_MLP_U_LDS " + std::string(model == 5 && mlp_u_in_lds(mlp_shape(r)) ? "1" : "0") + "\n";
     files = {"efgs_common.h", "efgs_args.h"};
     switch (model) {
         case 1: files.push_back("appearance_sh.h"); break;

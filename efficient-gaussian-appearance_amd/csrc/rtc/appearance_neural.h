@@ -1,18 +1,20 @@
 // Neural residual (EFGS_MODEL == 5): a bias-free ReLU MLP over per-Gaussian features (optionally frequency
 // encoded, optionally with the base colour as 3 extra inputs) and the SH degree values of the view
-// direction, evaluated per wave of 64 primitives with fp16 MFMA (v_mfma_f32_16x16x16f16) and fp32
-// accumulation; weights live in LDS in the tcnn flat layout (row-major [out x in] per layer, input padded to
-// a multiple of 16, output padded to 16 rows).
+// direction, evaluated per wave of 64 primitives with fp16 MFMA (v_mfma_f32_16x16x32_f16 wherever a
+// contraction spans 32 or more, v_mfma_f32_16x16x16f16 for a trailing 16) and fp32 accumulation; the weights
+// sit in LDS (tcnn flat layout in HBM: row-major [out x in] per layer, input padded to a multiple of 16,
+// output padded to 16 rows).
 //
-// Layout: each layer computes H_out^T = W H_in^T with the weights as the A operand and the activations as the
-// B operand, so a 16x16 accumulator tile (lane l: rows 4(l/16)..+3, column l%16) is exactly the B fragment
-// of the next layer's matching k-block: no data movement between layers. Activations are rounded to fp16
-// between layers (as tcnn's half-precision network), the 3 outputs are rounded to fp16.
+// Each layer computes H_out = W H_in with W as the A operand and the activations as the B operand, so an
+// accumulator tile is the next layer's B fragment as it stands: no data movement between layers.
+// Activations are rounded to fp16 between layers (as tcnn's half-precision network), the 3 outputs are
+// rounded to fp16.
 //
-// Backward: the forward is recomputed (no stored context). The upstream gradient of the wave is scaled by a
-// power of two so its maximum lies in [256, 512) before the fp16 MFMA chain, and unscaled in fp32. Weight
-// gradients dW = G X accumulate per wave in fp32 registers (operands transposed through LDS), then are reduced
-// across the block's waves in a fixed order.
+// Backward: the forward is recomputed (no stored context), per pair of 16-primitive column blocks, with every
+// activation kept in registers until its backward. The upstream gradient is scaled by a power of two before
+// the fp16 MFMA chain and unscaled in fp32. Weight gradients accumulate per wave in fp32 registers, with
+// the operands' transposes taken by MFMA against the identity, then are reduced across the block's waves
+// in a fixed order.
 //
 // Reference: B/rasterization/rtc/appearance_neural.cuh:17-407 (encoding, SH degree values and their
 // gradient, tcnn eval_model / backward_eval_model at :333, :379); weight layout viewer/export_ngsplat.py:1013-1029.
@@ -22,9 +24,6 @@ namespace efgs {
 
 namespace nn {
 
-#ifndef EFGS_MLP_U_LDS
-#define EFGS_MLP_U_LDS 0
-#endif
 constexpr uint32_t IN = EFGS_MLP_N_IN;            // unpadded input width
 constexpr uint32_t INP = EFGS_MLP_N_IN_PADDED;    // padded to a multiple of 16
 constexpr uint32_t NN = EFGS_MLP_N_NEURONS;
@@ -142,6 +141,24 @@ __device__ inline void sh_degree_values(T x, T y, T z, uint32_t active_degree, E
     }
 }
 
+// derivative of the residual activation at the raw MLP output y, for the gradients: tanh' = sech^2 y =
+// 4 e / (1 + e)^2 and softplus(beta 10)' = sigmoid(10 y), from e = exp(-2|y|) resp. exp(-10|y|) (no overflow),
+// with the hardware exp and reciprocal (about 1 ulp each)
+template <int ACT>
+__device__ __forceinline__ float residual_activation_slope(float y) {
+    if (ACT == 1) {
+        const float e = __expf(-2.0f * fabsf(y));
+        const float d = 1.0f + e;
+        return 4.0f * e * __builtin_amdgcn_rcpf(d * d);
+    }
+    if (ACT == 2) {
+        const float e = __expf(-10.0f * fabsf(y));
+        const float t = __builtin_amdgcn_rcpf(1.0f + e);
+        return y >= 0.0f ? t : e * t;
+    }
+    return 1.0f;
+}
+
 // raw feature i of a primitive: learned features, then (with base input) the 3 base values
 __device__ __forceinline__ float raw_feature(const float* feat, const float* base, uint32_t i) {
     return i < FEATURES ? feat[i] : base[i - FEATURES];
@@ -195,51 +212,55 @@ __device__ inline float3 direction_grad(float3 d, uint32_t degree, const float* 
     return g;
 }
 
-// ---- dual-orientation MLP of the backward kernel --------------------------------------------------------
+// ---- MLP tiles ----------------------------------------------------------------------------------------
 //
-// Tile sets of a (F x 64 primitives) matrix M held by a wave (lane = r + 16 q):
-//   feature-rows    T[fb][pb]: lane (r, q) holds M[16 fb + 4 q + i][16 pb + r], i = 0..3
-//   primitive-rows  U[pb][fb]: lane (r, q) holds M[16 fb + r][16 pb + 4 q + i]
-// v_mfma_f32_16x16x16f16 takes A as lane (r, q) -> A[r][4 q + i], B as B[4 q + i][r] and returns D as
-// D[4 q + i][r]. So a product's D is a feature-rows or primitive-rows tile as it stands; a feature-rows tile
-// is a B operand with K = features or an A operand holding the block's transpose (rows = primitives,
-// K = features); a primitive-rows tile is a B operand with K = primitives (N = features) or an A operand
-// holding the block itself with K = primitives. Computing every activation and every gradient in both
-// orientations (twice the MFMAs of the forward chain, which are cheap here) feeds every product of the
-// backward, including the weight gradients (contractions over primitives), with no transposes through LDS.
+// A wave holds a (features x 64 primitives) matrix M as 16 x 16 blocks in one of two orientations
+// (lane = r + 16 q, i = 0..3):
+//   F-tile (feature rows)    lane (r, q) holds M[16 fb + 4 q + i][16 pb + r]
+//   P-tile (primitive rows)  lane (r, q) holds M[16 fb + r][16 pb + 4 q + i]
+// v_mfma_f32_16x16x16f16 reads A as lane (r, q) -> A[r][4 q + i], B as lane (r, q) -> B[4 q + i][r] and returns
+// D[4 q + i][r]. So rows of W (A, from LDS) times F-tiles (B) give F-tiles: the layer chain, forward and
+// backward, contracts over features. The weight gradients contract over primitives: A is a P-tile of the
+// gradient, B a P-tile of the layer input. An F-tile taken as the A operand is the block's transpose, so its
+// product with the identity is the block's P-tile: one MFMA per tile, exact (products x * 1, sums of zeros).
+// v_mfma_f32_16x16x32_f16 (K = 32, same issue cost) takes two K = 16 fragments concatenated on both sides:
+// A's lane (r, q) and B's lane (n, q) then hold the same k's, so every contraction over 32 or more runs
+// at twice the rate of the K = 16 form.
 //
-// LDS holds W_l row-major [out][in] and its transpose [in][out]; rows are padded by 4 halves so that the 16
-// lanes reading 8-byte fragments of 16 consecutive rows fall on distinct banks.
-constexpr uint32_t WPAD = 4;
+// LDS holds W_l row-major [out][in] and W_l^T row-major [in][out]. Within each 32-column group a row stores
+// column 32 j + 16 h + 4 q + i at 32 j + 8 q + 4 h + i, so the two K = 16 fragments a lane concatenates are one
+// 16-byte read (a trailing 16-column group keeps its order). Rows are padded by 8 halves.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ h8 cat(h4 a, h4 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7); }
+
+constexpr uint32_t WPAD = 8;
 __host__ __device__ constexpr uint32_t wrow(uint32_t l) { return lin(l) + WPAD; }
 __host__ __device__ constexpr uint32_t wtrow(uint32_t l) { return lout(l) + WPAD; }
-__host__ __device__ constexpr uint32_t dual_layer_halves(uint32_t l) { return lout(l) * wrow(l) + lin(l) * wtrow(l); }
+__host__ __device__ constexpr uint32_t layer_halves(uint32_t l) { return lout(l) * wrow(l) + lin(l) * wtrow(l); }
 __host__ __device__ constexpr uint32_t woff(uint32_t l) {
     uint32_t o = 0;
-    for (uint32_t k = 0; k < l; k++) o += dual_layer_halves(k);
+    for (uint32_t k = 0; k < l; k++) o += layer_halves(k);
     return o;
 }
 __host__ __device__ constexpr uint32_t wtoff(uint32_t l) { return woff(l) + lout(l) * wrow(l); }
-constexpr uint32_t DUAL_WEIGHT_BYTES = (woff(NL) * 2 + 15) / 16 * 16;
-constexpr uint32_t XS = INP + 4;        // staging row of the input / output-gradient rows (halves)
-constexpr uint32_t YS = OUTP + 4;
+constexpr uint32_t WEIGHT_BYTES = (woff(NL) * 2 + 15) / 16 * 16;
+constexpr uint32_t XS = INP + 4;        // staging row of the input rows (halves)
 constexpr uint32_t FS = INP + 4;        // staging row of the input-gradient rows (floats)
-constexpr uint32_t DUAL_STAGE_BYTES = 64 * FS * 4;  // per wave; also covers 64 rows of XS or YS halves
-// With EFGS_MLP_U_LDS the primitive-rows input tiles of the hidden layers wait for the backward outside the
-// registers: U[1] is recomputed from the staged input tiles where it is used (one MFMA per tile for a 16-wide
-// input), U[2..NH] sit in a per-wave LDS store (one 8-byte slot per lane and tile, written and read by the
-// same lane). The host sets it when the store fits two blocks' LDS per CU.
-constexpr uint32_t U_TILES = (NN / 16) * 4;
-constexpr uint32_t U_STORE_BYTES = EFGS_MLP_U_LDS ? (NH > 1 ? NH - 1 : 0u) * U_TILES * 64 * 8 : 0u;  // per wave
-__device__ __forceinline__ uint32_t u_slot(uint32_t l, uint32_t pb, uint32_t fb, uint32_t lane) {
-    return (((l - 2) * U_TILES + pb * (NN / 16) + fb) * 64 + lane);
+constexpr uint32_t STAGE_BYTES = 64 * FS * 4;  // per wave; covers 64 rows of XS halves and 64 output rows of 16 bytes
+
+// position of column c in a stored row of `width` columns
+__host__ __device__ constexpr uint32_t kpos(uint32_t c, uint32_t width) {
+    return c < width / 32u * 32u ? (c & ~31u) | (((c >> 2) & 3u) << 3) | (((c >> 4) & 1u) << 2) | (c & 3u) : c;
 }
 
-// copies the flat tcnn-layout weights (fp16 bits, 16-byte aligned) into the padded W / W^T layout (whole
-// block of N_THREADS): 8 weights per 16-byte load, up to 8 loads per thread in flight before the LDS stores.
-// Every layer holds a multiple of 256 weights, so a vector never straddles two layers or two rows.
+// copies the flat tcnn-layout weights (fp16 bits, 16-byte aligned) into the W / W^T layout above (whole block
+// of N_THREADS): 8 weights per 16-byte load, up to 8 loads per thread in flight before the LDS stores. Every
+// layer holds a multiple of 256 weights, so a vector never straddles two layers or two rows.
 template <uint32_t N_THREADS>
-__device__ inline void load_dual_weights(const uint16_t* g, uint16_t* WL, uint32_t tid) {
+__device__ inline void load_weights(const uint16_t* g, uint16_t* WL, uint32_t tid) {
     constexpr uint32_t n_vec = PARAMS / 8;
     constexpr uint32_t batch = 8;
     const uint4* gv = reinterpret_cast<const uint4*>(g);
@@ -265,12 +286,47 @@ __device__ inline void load_dual_weights(const uint16_t* g, uint16_t* WL, uint32
                 const uint32_t row = idx / lin(l), col = idx % lin(l);
 #pragma unroll
                 for (uint32_t i = 0; i < 8; i++) {
-                    WL[woff(l) + row * wrow(l) + col + i] = e[i];
-                    WL[wtoff(l) + (col + i) * wtrow(l) + row] = e[i];
+                    WL[woff(l) + row * wrow(l) + kpos(col + i, lin(l))] = e[i];
+                    WL[wtoff(l) + (col + i) * wtrow(l) + kpos(row, lout(l))] = e[i];
                 }
             }
         }
     }
+}
+
+// sum over the kb_count K = 16 blocks of A(row, kb) B(kb): K = 32 pairs, then a trailing K = 16 block. row:
+// the lane's stored row (16-byte aligned); b: B tiles (F-tiles with K = features). Two column blocks share
+// every A fragment read.
+__device__ __forceinline__ void row_times(const _Float16* row, uint32_t kb_count, const h4* b0, const h4* b1, uint32_t q, f4& acc0,
+                                          f4& acc1) {
+#pragma unroll
+    for (uint32_t j = 0; 2 * j + 1 < kb_count; j++) {
+        const h8 a = *reinterpret_cast<const h8*>(row + 32 * j + 8 * q);
+        acc0 = mfma32(a, cat(b0[2 * j], b0[2 * j + 1]), acc0);
+        acc1 = mfma32(a, cat(b1[2 * j], b1[2 * j + 1]), acc1);
+    }
+    if (kb_count & 1u) {
+        const h4 a = *reinterpret_cast<const h4*>(row + 16 * (kb_count - 1) + 4 * q);
+        acc0 = mfma(a, b0[kb_count - 1], acc0);
+        acc1 = mfma(a, b1[kb_count - 1], acc1);
+    }
+}
+__device__ __forceinline__ f4 row_times1(const _Float16* row, uint32_t kb_count, const h4* b, uint32_t q) {
+    f4 acc = f4_zero();
+#pragma unroll
+    for (uint32_t j = 0; 2 * j + 1 < kb_count; j++)
+        acc = mfma32(*reinterpret_cast<const h8*>(row + 32 * j + 8 * q), cat(b[2 * j], b[2 * j + 1]), acc);
+    if (kb_count & 1u) acc = mfma(*reinterpret_cast<const h4*>(row + 16 * (kb_count - 1) + 4 * q), b[kb_count - 1], acc);
+    return acc;
+}
+
+// The lane's row index within a 16-row block, opaque to the compiler: weight-row addresses built from it stay
+// inside the caller's loop as one base plus constants (folded into the LDS instructions' offsets) instead of
+// being hoisted as one register per row
+__device__ __forceinline__ uint32_t opaque_row(uint32_t lane) {
+    uint32_t r = lane & 15u;
+    asm volatile("" : "+v"(r));
+    return r;
 }
 
 // ReLU of an fp32 tile, rounded to fp16 (round to nearest even, then a packed max with zero)
@@ -280,34 +336,36 @@ __device__ __forceinline__ h4 relu_h4(f4 v) {
                                            static_cast<_Float16>(0.0f)});
 }
 
-// v where the activation is positive (ReLU derivative), as fp16
-__device__ __forceinline__ h4 masked_h4(f4 v, h4 act) {
-    const _Float16 z = static_cast<_Float16>(0.0f);
-    return h4{act[0] > z ? static_cast<_Float16>(v[0]) : z, act[1] > z ? static_cast<_Float16>(v[1]) : z,
-              act[2] > z ? static_cast<_Float16>(v[2]) : z, act[3] > z ? static_cast<_Float16>(v[3]) : z};
+// fp16 of v where the ReLU output act is positive, zero elsewhere. act >= 0, so act > 0 exactly when its bits
+// without the sign are nonzero: m = min(bits & 0x7fff, 1) is 1 or 0 per half and multiplies the fp16 bits
+// (three packed integer instructions per pair of values). m comes from inline assembly so that the compiler
+// cannot turn the product back into a compare and a select per value; the product itself stays ordinary code,
+// so the compiler still sees the write that the next MFMA reads and inserts the wait states it needs.
+__device__ __forceinline__ uint32_t relu_mask2(uint32_t act) {
+    uint32_t m;
+    asm("v_and_b32 %0, %1, %2\n\tv_pk_min_u16 %0, %0, %3" : "=&v"(m) : "s"(0x7fff7fffu), "v"(act), "s"(0x00010001u));
+    return m;
+}
+__device__ __forceinline__ h4 relu_grad(f4 v, h4 act) {
+    const u16x4 x = __builtin_bit_cast(u16x4, __builtin_convertvector(v, h4));
+    const uint2 a = __builtin_bit_cast(uint2, act);
+    const u16x4 m = __builtin_bit_cast(u16x4, make_uint2(relu_mask2(a.x), relu_mask2(a.y)));
+    return __builtin_bit_cast(h4, x * m);
 }
 
-// ReLU masks of the feature-rows activations, 4 bits per tile (tile fb * 4 + pb), kept once the forward no
-// longer needs the values themselves
-constexpr uint32_t MASK_WORDS = (KT * 4 * 4 + 31) / 32;
-__device__ __forceinline__ uint32_t positive_bits(h4 a) {
-    const _Float16 z = static_cast<_Float16>(0.0f);
-    return (a[0] > z ? 1u : 0u) | (a[1] > z ? 2u : 0u) | (a[2] > z ? 4u : 0u) | (a[3] > z ? 8u : 0u);
-}
-__device__ __forceinline__ h4 masked_h4_bits(f4 v, uint32_t bits) {
-    const _Float16 z = static_cast<_Float16>(0.0f);
-    return h4{(bits & 1u) ? static_cast<_Float16>(v[0]) : z, (bits & 2u) ? static_cast<_Float16>(v[1]) : z,
-              (bits & 4u) ? static_cast<_Float16>(v[2]) : z, (bits & 8u) ? static_cast<_Float16>(v[3]) : z};
+// identity B operand: lane (r, q) holds I[4 q + i][r]
+__device__ __forceinline__ h4 identity_tile(uint32_t lane) {
+    const uint32_t r = lane & 15u, q = lane >> 4;
+    const _Float16 one = static_cast<_Float16>(1.0f), z = static_cast<_Float16>(0.0f);
+    return h4{4 * q == r ? one : z, 4 * q + 1 == r ? one : z, 4 * q + 2 == r ? one : z, 4 * q + 3 == r ? one : z};
 }
 
-// Per-wave MLP forward: fp16 MFMA, fp32 accumulation, activations rounded to fp16 between layers. WL: padded
-// W / W^T in LDS; stage: this wave's staging area; x: the lane's input row; y: the lane's three raw outputs,
-// rounded to fp16. With DUAL (the backward's recompute) it also leaves U[l], the input activations of layer l
-// as primitive-rows tiles, and Tm[l] (l >= 1), the ReLU masks of the feature-rows tiles.
-template <bool DUAL>
-__device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, const float* x, uint32_t (&Tm)[NL][MASK_WORDS], h4 (&U)[NL][4][KT],
-                                         h4 (&X)[INP / 16][4], h4* ustore, float* y, uint32_t lane) {
-    h4 T[NL][KT][4];
+// P-tile of the block whose F-tile is f
+__device__ __forceinline__ h4 transpose_tile(h4 f, h4 eye) { return __builtin_convertvector(mfma(f, eye, f4_zero()), h4); }
+
+// the lane's input row (INP floats) to fp16 in the staging area, then the F-tiles X[pb][ib] of the wave's four
+// column blocks
+__device__ inline void stage_input_tiles(_Float16* stage, const float* x, h4 (&X)[4][INP / 16], uint32_t lane) {
     const uint32_t r = lane & 15u, q = lane >> 4;
 #pragma unroll
     for (uint32_t k = 0; k < INP; k += 4)
@@ -315,168 +373,156 @@ __device__ inline void mlp_forward_tiles(const _Float16* WL, _Float16* stage, co
             h4{static_cast<_Float16>(x[k]), static_cast<_Float16>(x[k + 1]), static_cast<_Float16>(x[k + 2]), static_cast<_Float16>(x[k + 3])};
     wave_sync();
 #pragma unroll
-    for (uint32_t ib = 0; ib < INP / 16; ib++)
+    for (uint32_t pb = 0; pb < 4; pb++)
 #pragma unroll
-        for (uint32_t pb = 0; pb < 4; pb++) {
-            T[0][ib][pb] = *reinterpret_cast<const h4*>(&stage[(16 * pb + r) * XS + 16 * ib + 4 * q]);
-            if (DUAL)
-                U[0][pb][ib] = h4{stage[(16 * pb + 4 * q) * XS + 16 * ib + r], stage[(16 * pb + 4 * q + 1) * XS + 16 * ib + r],
-                              stage[(16 * pb + 4 * q + 2) * XS + 16 * ib + r], stage[(16 * pb + 4 * q + 3) * XS + 16 * ib + r]};
-        }
+        for (uint32_t ib = 0; ib < INP / 16; ib++) X[pb][ib] = *reinterpret_cast<const h4*>(&stage[(16 * pb + r) * XS + 16 * ib + 4 * q]);
     wave_sync();
-    f4 yt[4];
-#pragma unroll
-    for (uint32_t l = 0; l < NL; l++) {
-#pragma unroll
-        for (uint32_t ob = 0; ob < lout(l) / 16; ob++) {
-            h4 wa[KT];
-#pragma unroll
-            for (uint32_t ib = 0; ib < lin(l) / 16; ib++) wa[ib] = *reinterpret_cast<const h4*>(&WL[woff(l) + (16 * ob + r) * wrow(l) + 16 * ib + 4 * q]);
-#pragma unroll
-            for (uint32_t pb = 0; pb < 4; pb++) {
-                f4 t = f4_zero();
-#pragma unroll
-                for (uint32_t ib = 0; ib < lin(l) / 16; ib++) t = mfma(wa[ib], T[l][ib][pb], t);  // H(ob, pb) = sum W(ob, ib) M(ib, pb)
-                if (l < NH) {
-                    T[l + 1][ob][pb] = relu_h4(t);
-                    if (!DUAL || (EFGS_MLP_U_LDS && l == 0)) continue;  // U[1] is recomputed where it is used
-                    f4 u = f4_zero();
-#pragma unroll
-                    for (uint32_t ib = 0; ib < lin(l) / 16; ib++) u = mfma(T[l][ib][pb], wa[ib], u);  // H^T(pb, ob) = sum M^T(pb, ib) W^T(ib, ob)
-                    if (EFGS_MLP_U_LDS)
-                        ustore[u_slot(l + 1, pb, ob, lane)] = relu_h4(u);
-                    else
-                        U[l + 1][pb][ob] = relu_h4(u);
-                } else if (ob == 0) {
-                    yt[pb] = t;
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);  // one output block in flight: bounds the live accumulators
-        }
-    }
-    // outputs 0..2 of primitive 16 pb + c sit in lane c of output tile pb
-#pragma unroll
-    for (uint32_t o = 0; o < 3; o++) {
-        float v = 0.0f;
-#pragma unroll
-        for (uint32_t pb = 0; pb < 4; pb++) {
-            const float t = __shfl(yt[pb][o], static_cast<int>(r));
-            if (q == pb) v = t;
-        }
-        y[o] = round_half(v);
-    }
-    if (!DUAL) return;
-#pragma unroll
-    for (uint32_t ib = 0; ib < INP / 16; ib++)
-#pragma unroll
-        for (uint32_t pb = 0; pb < 4; pb++) X[ib][pb] = T[0][ib][pb];
-#pragma unroll
-    for (uint32_t l = 1; l < NL; l++) {
-#pragma unroll
-        for (uint32_t w = 0; w < MASK_WORDS; w++) Tm[l][w] = 0u;
-#pragma unroll
-        for (uint32_t fb = 0; fb < lin(l) / 16; fb++)
-#pragma unroll
-            for (uint32_t pb = 0; pb < 4; pb++) {
-                const uint32_t t = fb * 4 + pb;
-                Tm[l][t / 8] |= positive_bits(T[l][fb][pb]) << (4 * (t % 8));
-            }
-    }
 }
 
-// Backward through the MLP from the lanes' output gradients dy (zero for lanes that do not contribute), with
-// Tm / U from mlp_forward_tiles<true>. The gradients run through the fp16 MFMAs scaled by s (a power of two
-// that keeps them in fp16 range; the caller picks it from a bound on |dy| over the whole launch). Writes the
-// lane's input gradient row dx (INP floats, unscaled) and adds the wave's weight gradients, still scaled by s,
-// to dW (MFMA accumulators, lane layout of the D operand: dW[l][ob][ib][i] = s dW_l[16 ob + 4 q + i][16 ib + r]).
-__device__ inline void mlp_backward_dual(const _Float16* WL, _Float16* stage, const uint32_t (&Tm)[NL][MASK_WORDS], const h4 (&U)[NL][4][KT],
-                                         const h4 (&X)[INP / 16][4], const h4* ustore, const float* dy, float s, float inv_s, float* dx,
-                                         f4 (&dW)[NL][NT > 1 ? NT : 1][KT], uint32_t lane) {
-    // primitive-rows input tile (pb, fb) of layer l
-    auto u_tile = [&](uint32_t l, uint32_t pb, uint32_t fb) -> h4 {
-        if (!EFGS_MLP_U_LDS || l == 0) return U[l][pb][fb];
-        if (l >= 2) return ustore[u_slot(l, pb, fb, lane)];
-        f4 u = f4_zero();  // U[1](pb, fb) = ReLU(sum_ib X^T(pb, ib) W_0^T(ib, fb))
+// Per-wave MLP forward: fp16 MFMA, fp32 accumulation, activations rounded to fp16 between layers. WL: the
+// weights in LDS; stage: this wave's staging area; x: the lane's input row; y: the lane's three raw outputs,
+// rounded to fp16. Column blocks of 16 primitives run one after another (the chain is per primitive).
+__device__ inline void mlp_forward(const _Float16* WL, _Float16* stage, const float* x, float* y, uint32_t lane) {
+    const uint32_t r = lane & 15u, q = lane >> 4, ro = opaque_row(lane);
+    h4 X[4][INP / 16];
+    stage_input_tiles(stage, x, X, lane);
+    float* ys = reinterpret_cast<float*>(stage);
 #pragma unroll
-        for (uint32_t ib = 0; ib < INP / 16; ib++)
-            u = mfma(X[ib][pb], *reinterpret_cast<const h4*>(&WL[woff(0) + (16 * fb + (lane & 15u)) * wrow(0) + 16 * ib + 4 * (lane >> 4)]), u);
-        return relu_h4(u);
-    };
-    const uint32_t r = lane & 15u, q = lane >> 4;
+    for (uint32_t pp = 0; pp < 2; pp++) {
+        h4 H[2][NT], Hn[2][NT];
+        f4 yt[2];
 #pragma unroll
-    for (uint32_t k = 0; k < INP; k++) dx[k] = 0.0f;
-    if (__ballot(dy[0] != 0.0f || dy[1] != 0.0f || dy[2] != 0.0f) == 0) return;  // wave-uniform
-
-    // output-layer gradient (16 padded outputs x 64 primitives) in both orientations, through LDS
-    const _Float16 z = static_cast<_Float16>(0.0f);
-    *reinterpret_cast<h4*>(&stage[lane * YS]) = h4{static_cast<_Float16>(dy[0] * s), static_cast<_Float16>(dy[1] * s),
-                                                    static_cast<_Float16>(dy[2] * s), z};
+        for (uint32_t l = 0; l < NL; l++) {
+            const h4* in0 = l == 0 ? X[2 * pp] : H[0];
+            const h4* in1 = l == 0 ? X[2 * pp + 1] : H[1];
 #pragma unroll
-    for (uint32_t k = 4; k < OUTP; k += 4) *reinterpret_cast<h4*>(&stage[lane * YS + k]) = h4{z, z, z, z};
-    wave_sync();
-    h4 G[KT][4], GT[4][KT];
-#pragma unroll
-    for (uint32_t pb = 0; pb < 4; pb++) {
-        G[0][pb] = *reinterpret_cast<const h4*>(&stage[(16 * pb + r) * YS + 4 * q]);
-        GT[pb][0] = h4{stage[(16 * pb + 4 * q) * YS + r], stage[(16 * pb + 4 * q + 1) * YS + r], stage[(16 * pb + 4 * q + 2) * YS + r],
-                       stage[(16 * pb + 4 * q + 3) * YS + r]};
-    }
-    wave_sync();
-
-    // output layer: dW_NH(0, ib) += sum_pb dY(0, pb) M_NH(ib, pb)^T (dY as primitive-rows A operand)
-#pragma unroll
-    for (uint32_t ib = 0; ib < lin(NH) / 16; ib++) {
-#pragma unroll
-        for (uint32_t pb = 0; pb < 4; pb++) dW[NH][0][ib] = mfma(GT[pb][0], u_tile(NH, pb, ib), dW[NH][0][ib]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int li = static_cast<int>(NH); li >= 1; li--) {
-        const uint32_t l = static_cast<uint32_t>(li);
-        // input gradient of layer l in both orientations, through the ReLU of its input; each primitive-rows tile
-        // goes straight into layer l-1's weight gradient (dW_{l-1}(ib, jb) += sum_pb dIn(ib, pb) M_{l-1}(jb, pb)^T)
-        h4 Gn[KT][4];
-#pragma unroll
-        for (uint32_t ib = 0; ib < lin(l) / 16; ib++) {
-            h4 wt[KT];
-#pragma unroll
-            for (uint32_t ob = 0; ob < lout(l) / 16; ob++)
-                wt[ob] = *reinterpret_cast<const h4*>(&WL[wtoff(l) + (16 * ib + r) * wtrow(l) + 16 * ob + 4 * q]);
-#pragma unroll
-            for (uint32_t pb = 0; pb < 4; pb++) {
-                f4 t = f4_zero(), u = f4_zero();
-#pragma unroll
-                for (uint32_t ob = 0; ob < lout(l) / 16; ob++) {
-                    t = mfma(wt[ob], G[ob][pb], t);   // dIn(ib, pb) = sum W^T(ib, ob) dOut(ob, pb)
-                    u = mfma(G[ob][pb], wt[ob], u);   // dIn^T(pb, ib) = sum dOut^T(pb, ob) W(ob, ib)
+            for (uint32_t ob = 0; ob < lout(l) / 16; ob++) {
+                f4 a0 = f4_zero(), a1 = f4_zero();
+                row_times(WL + woff(l) + (16 * ob + ro) * wrow(l), lin(l) / 16, in0, in1, q, a0, a1);
+                if (l < NH) {
+                    Hn[0][ob] = relu_h4(a0);
+                    Hn[1][ob] = relu_h4(a1);
+                } else if (ob == 0) {
+                    yt[0] = a0;
+                    yt[1] = a1;
                 }
-                const uint32_t ti = ib * 4 + pb;
-                Gn[ib][pb] = masked_h4_bits(t, (Tm[l][ti / 8] >> (4 * (ti % 8))) & 15u);
-                const h4 gt = masked_h4(u, u_tile(l, pb, ib));
-#pragma unroll
-                for (uint32_t jb = 0; jb < lin(l - 1) / 16; jb++) dW[l - 1][ib][jb] = mfma(gt, u_tile(l - 1, pb, jb), dW[l - 1][ib][jb]);
             }
-            __builtin_amdgcn_sched_barrier(0);  // one input block in flight: bounds the live accumulators
+            if (l < NH) {
+#pragma unroll
+                for (uint32_t ob = 0; ob < NT; ob++) {
+                    H[0][ob] = Hn[0][ob];
+                    H[1][ob] = Hn[1][ob];
+                }
+            }
         }
+        // outputs 0..3 of primitive 16 pb + r sit in lane r of column block pb's output tile
+        if (q == 0) {
 #pragma unroll
-        for (uint32_t ib = 0; ib < lin(l) / 16; ib++)
-#pragma unroll
-            for (uint32_t pb = 0; pb < 4; pb++) G[ib][pb] = Gn[ib][pb];
+            for (uint32_t b = 0; b < 2; b++)
+                *reinterpret_cast<float4*>(&ys[(16 * (2 * pp + b) + r) * 4]) =
+                    make_float4(round_half(yt[b][0]), round_half(yt[b][1]), round_half(yt[b][2]), 0.0f);
+        }
     }
-    // input gradient rows (feature-rows tiles, unscaled) to the lanes through LDS
+    wave_sync();
+    const float4 v = *reinterpret_cast<const float4*>(&ys[lane * 4]);
+    y[0] = v.x;
+    y[1] = v.y;
+    y[2] = v.z;
+    wave_sync();
+}
+
+// Forward and backward of the wave's 64 primitives in two passes of 32 (a pair of column blocks): the chain is
+// independent per primitive and only the weight gradients sum over primitives, in K = 32 MFMAs over the
+// pair, so every activation of a pass stays in registers until its backward.
+//   x: the lane's input row; g: the lane's gradient with respect to its 3 activated outputs (zero for lanes
+//   that do not contribute); dy_of(y, g): gradient with respect to the raw output y (rounded to fp16) given g;
+//   s / inv_s: the gradient scale, a power of two that keeps the fp16 gradients in range (the caller picks it
+//   from a bound on |dL/dy| over the launch); dx: the lane's input-gradient row (unscaled); dW: weight
+//   gradient accumulators, still scaled by s (D layout: dW[l][ob][ib][i] = s dW_l[16 ob + 4 q + i][16 ib + r]).
+template <typename DY>
+__device__ inline void mlp_train(const _Float16* WL, _Float16* stage, const float* x, const float* g, DY&& dy_of, float s,
+                                 float inv_s, float* dx, f4 (&dW)[NL][NT][KT], uint32_t lane) {
+    const uint32_t r = lane & 15u, q = lane >> 4, ro = opaque_row(lane);
+    const h4 eye = identity_tile(lane);
+    const _Float16 z = static_cast<_Float16>(0.0f);
+    const h4 zero4 = h4{z, z, z, z};
+    h4 X[4][INP / 16];
+    stage_input_tiles(stage, x, X, lane);
     float* fs = reinterpret_cast<float*>(stage);
 #pragma unroll
-    for (uint32_t ib = 0; ib < INP / 16; ib++) {
-        h4 wt[KT];
+    for (uint32_t pp = 0; pp < 2; pp++) {
+        // forward: F[l] = input activations of layer l >= 1 (F-tiles), P[l] = their P-tiles (P[0]: the inputs)
+        h4 F[NL][2][NT], P[NL][2][KT];
+        f4 yt[2];
 #pragma unroll
-        for (uint32_t ob = 0; ob < lout(0) / 16; ob++) wt[ob] = *reinterpret_cast<const h4*>(&WL[wtoff(0) + (16 * ib + r) * wtrow(0) + 16 * ob + 4 * q]);
+        for (uint32_t b = 0; b < 2; b++)
 #pragma unroll
-        for (uint32_t pb = 0; pb < 4; pb++) {
-            f4 t = f4_zero();
+            for (uint32_t ib = 0; ib < INP / 16; ib++) P[0][b][ib] = transpose_tile(X[2 * pp + b][ib], eye);
 #pragma unroll
-            for (uint32_t ob = 0; ob < lout(0) / 16; ob++) t = mfma(wt[ob], G[ob][pb], t);
-            *reinterpret_cast<float4*>(&fs[(16 * pb + r) * FS + 16 * ib + 4 * q]) = make_float4(t[0] * inv_s, t[1] * inv_s, t[2] * inv_s, t[3] * inv_s);
+        for (uint32_t l = 0; l < NL; l++) {
+            const h4* in0 = l == 0 ? X[2 * pp] : F[l][0];
+            const h4* in1 = l == 0 ? X[2 * pp + 1] : F[l][1];
+#pragma unroll
+            for (uint32_t ob = 0; ob < lout(l) / 16; ob++) {
+                f4 a0 = f4_zero(), a1 = f4_zero();
+                row_times(WL + woff(l) + (16 * ob + ro) * wrow(l), lin(l) / 16, in0, in1, q, a0, a1);
+                if (l < NH) {
+                    F[l + 1][0][ob] = relu_h4(a0);
+                    F[l + 1][1][ob] = relu_h4(a1);
+                    P[l + 1][0][ob] = transpose_tile(F[l + 1][0][ob], eye);
+                    P[l + 1][1][ob] = transpose_tile(F[l + 1][1][ob], eye);
+                } else if (ob == 0) {
+                    yt[0] = a0;
+                    yt[1] = a1;
+                }
+            }
         }
+        // output gradient of column block pb: lane r of the output tile holds primitive 16 pb + r's outputs;
+        // rows 3..15 of the output block are padding (zero gradient)
+        h4 G[2][NT], GT[2];
+#pragma unroll
+        for (uint32_t b = 0; b < 2; b++) {
+            const uint32_t src = 16 * (2 * pp + b) + r;
+            const float d0 = dy_of(round_half(yt[b][0]), __shfl(g[0], static_cast<int>(src)));
+            const float d1 = dy_of(round_half(yt[b][1]), __shfl(g[1], static_cast<int>(src)));
+            const float d2 = dy_of(round_half(yt[b][2]), __shfl(g[2], static_cast<int>(src)));
+            G[b][0] = q == 0 ? h4{static_cast<_Float16>(d0 * s), static_cast<_Float16>(d1 * s), static_cast<_Float16>(d2 * s), z} : zero4;
+            GT[b] = transpose_tile(G[b][0], eye);
+        }
+        // backward: dW_NH += dY X_NH^T over the pair, then layer by layer the input gradient (F-tiles, through
+        // the ReLU of the input), its P-tiles and dW_{l-1} += dIn X_{l-1}^T over the pair
+#pragma unroll
+        for (uint32_t ib = 0; ib < lin(NH) / 16; ib++) dW[NH][0][ib] = mfma32(cat(GT[0], GT[1]), cat(P[NH][0][ib], P[NH][1][ib]), dW[NH][0][ib]);
+#pragma unroll
+        for (int li = static_cast<int>(NH); li >= 1; li--) {
+            const uint32_t l = static_cast<uint32_t>(li);
+            h4 Gn[2][NT];
+#pragma unroll
+            for (uint32_t ib = 0; ib < lin(l) / 16; ib++) {
+                f4 a0 = f4_zero(), a1 = f4_zero();
+                row_times(WL + wtoff(l) + (16 * ib + ro) * wtrow(l), lout(l) / 16, G[0], G[1], q, a0, a1);
+                Gn[0][ib] = relu_grad(a0, F[l][0][ib]);
+                Gn[1][ib] = relu_grad(a1, F[l][1][ib]);
+                const h8 gt = cat(transpose_tile(Gn[0][ib], eye), transpose_tile(Gn[1][ib], eye));
+#pragma unroll
+                for (uint32_t jb = 0; jb < lin(l - 1) / 16; jb++) dW[l - 1][ib][jb] = mfma32(gt, cat(P[l - 1][0][jb], P[l - 1][1][jb]), dW[l - 1][ib][jb]);
+            }
+#pragma unroll
+            for (uint32_t ib = 0; ib < NT; ib++) {
+                G[0][ib] = Gn[0][ib];
+                G[1][ib] = Gn[1][ib];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // input gradient rows (F-tiles, unscaled) to the lanes through LDS (the input rows were read already)
+#pragma unroll
+        for (uint32_t ib = 0; ib < INP / 16; ib++) {
+            f4 a0 = f4_zero(), a1 = f4_zero();
+            row_times(WL + wtoff(0) + (16 * ib + ro) * wtrow(0), NT, G[0], G[1], q, a0, a1);
+            *reinterpret_cast<float4*>(&fs[(16 * (2 * pp) + r) * FS + 16 * ib + 4 * q]) = make_float4(a0[0] * inv_s, a0[1] * inv_s, a0[2] * inv_s, a0[3] * inv_s);
+            *reinterpret_cast<float4*>(&fs[(16 * (2 * pp + 1) + r) * FS + 16 * ib + 4 * q]) = make_float4(a1[0] * inv_s, a1[1] * inv_s, a1[2] * inv_s, a1[3] * inv_s);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one pass in flight: bounds the live activations
     }
     wave_sync();
 #pragma unroll

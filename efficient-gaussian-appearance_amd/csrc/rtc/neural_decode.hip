@@ -6,7 +6,7 @@
 //
 //   EFGS_KERNEL_NAME            forward: out = MLP(x), fp16 MFMA with fp32 accumulation, outputs rounded to
 //                               fp16 (one wave per 64 primitives, persistent grid, weights in LDS)
-//   EFGS_KERNEL_NAME_backward   recomputes the forward in both tile orientations and backpropagates
+//   EFGS_KERNEL_NAME_backward   recomputes the forward and backpropagates
 //                               grad_out: feature, base-input and direction gradients per primitive, weight
 //                               gradients as one fp32 partial per block (reduced by reduce_partials_kernel)
 //
@@ -26,8 +26,8 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::NeuralD
     const uint32_t wave = threadIdx.x >> 6;
     extern __shared__ __align__(16) unsigned char smem[];
     const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
-    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES) + wave * 64 * nn::XS;
-    nn::load_dual_weights<decode_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES) + wave * 64 * nn::XS;
+    nn::load_weights<decode_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
     __syncthreads();
     const uint32_t n_chunks = (a.n + decode_block - 1) / decode_block;
     for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
@@ -43,11 +43,8 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::NeuralD
 #pragma unroll
             for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
         }
-        uint32_t masks[nn::NL][nn::MASK_WORDS];
-        nn::h4 unused[nn::NL][4][nn::KT];
-        nn::h4 unused_x[nn::INP / 16][4];
         float y[3];
-        nn::mlp_forward_tiles<false>(WL, stage, x, masks, unused, unused_x, nullptr, y, lane);
+        nn::mlp_forward(WL, stage, x, y, lane);
         if (active) {
             a.out[3 * p] = y[0];
             a.out[3 * p + 1] = y[1];
@@ -56,21 +53,20 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::NeuralD
     }
 }
 
-extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_CAT(EFGS_KERNEL_NAME, _backward)(efgs::NeuralDecodeArgs a) {
+extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, _backward)(efgs::NeuralDecodeArgs a) {
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     extern __shared__ __align__(16) unsigned char smem[];
     const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
-    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES + wave * nn::DUAL_STAGE_BYTES);
-    nn::h4* ustore = reinterpret_cast<nn::h4*>(smem + nn::DUAL_WEIGHT_BYTES + 4 * nn::DUAL_STAGE_BYTES + wave * nn::U_STORE_BYTES);
-    nn::load_dual_weights<decode_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES + wave * nn::STAGE_BYTES);
+    nn::load_weights<decode_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
 
-    nn::f4 dW[nn::NL][nn::NT > 1 ? nn::NT : 1][nn::KT];
+    nn::f4 dW[nn::NL][nn::NT][nn::KT];
 #pragma unroll
     for (uint32_t l = 0; l < nn::NL; l++)
 #pragma unroll
-        for (uint32_t rb = 0; rb < (nn::NT > 1 ? nn::NT : 1); rb++)
+        for (uint32_t rb = 0; rb < nn::NT; rb++)
 #pragma unroll
             for (uint32_t cb = 0; cb < nn::KT; cb++) dW[l][rb][cb] = nn::f4_zero();
 
@@ -120,19 +116,14 @@ extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_C
 #pragma unroll
             for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
         }
-        uint32_t Tm[nn::NL][nn::MASK_WORDS];
-        nn::h4 U[nn::NL][4][nn::KT];
-        nn::h4 X[nn::INP / 16][4];
-        float y[3];
-        nn::mlp_forward_tiles<true>(WL, stage, x, Tm, U, X, ustore, y, lane);
-        float dy[3] = {0.0f, 0.0f, 0.0f};
+        float g[3] = {0.0f, 0.0f, 0.0f};
         if (active) {
-            dy[0] = a.grad_out[3 * p];
-            dy[1] = a.grad_out[3 * p + 1];
-            dy[2] = a.grad_out[3 * p + 2];
+            g[0] = a.grad_out[3 * p];
+            g[1] = a.grad_out[3 * p + 1];
+            g[2] = a.grad_out[3 * p + 2];
         }
         float dx[nn::INP];
-        nn::mlp_backward_dual(WL, stage, Tm, U, X, ustore, dy, s, inv_s, dx, dW, lane);
+        nn::mlp_train(WL, stage, x, g, [](float, float gy) { return gy; }, s, inv_s, dx, dW, lane);
         if (active) {
             float* gf = a.g_features + static_cast<size_t>(p) * nn::FEATURES;
 #pragma unroll

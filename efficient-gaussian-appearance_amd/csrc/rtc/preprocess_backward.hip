@@ -264,28 +264,24 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
 }
 
 // The MLP backward (launched only when the residual is on). Persistent grid: every wave recomputes the MLP
-// forward for its 64 primitives in both tile orientations, backpropagates with fp16 MFMA without LDS
-// transposes, keeps its weight gradients in fp32 registers across chunks; the block sums its four waves in a
-// fixed order into one partial per block.
-// With the hidden activations in LDS the kernel fits 256 VGPRs: the bound of two waves per SIMD keeps every
-// MFMA result in VGPRs (accumulator registers would cost a move per element before each conversion); the
-// occupancy itself is set by the LDS, one block per CU.
-extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_CAT(EFGS_KERNEL_NAME, _mlp)(efgs::PreprocessBackwardArgs a) {
+// forward for its 64 primitives and backpropagates it with fp16 MFMA, keeps its weight gradients in fp32
+// registers across chunks; the block sums its four waves in a fixed order into one partial per block.
+// Two waves per SIMD: the weight-gradient accumulators and one pass's activations fit 256 VGPRs.
+extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, _mlp)(efgs::PreprocessBackwardArgs a) {
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     extern __shared__ __align__(16) unsigned char smem[];
     const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
-    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES + wave * nn::DUAL_STAGE_BYTES);
-    nn::h4* ustore = reinterpret_cast<nn::h4*>(smem + nn::DUAL_WEIGHT_BYTES + 4 * nn::DUAL_STAGE_BYTES + wave * nn::U_STORE_BYTES);
-    nn::load_dual_weights<preprocess_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES + wave * nn::STAGE_BYTES);
+    nn::load_weights<preprocess_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
     __syncthreads();
 
-    nn::f4 dW[nn::NL][nn::NT > 1 ? nn::NT : 1][nn::KT];
+    nn::f4 dW[nn::NL][nn::NT][nn::KT];
 #pragma unroll
     for (uint32_t l = 0; l < nn::NL; l++)
 #pragma unroll
-        for (uint32_t rb = 0; rb < (nn::NT > 1 ? nn::NT : 1); rb++)
+        for (uint32_t rb = 0; rb < nn::NT; rb++)
 #pragma unroll
             for (uint32_t cb = 0; cb < nn::KT; cb++) dW[l][rb][cb] = nn::f4_zero();
 
@@ -339,17 +335,10 @@ extern "C" __global__ __launch_bounds__(256, EFGS_MLP_U_LDS ? 2 : 1) void EFGS_C
 #pragma unroll
             for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
         }
-        uint32_t Tm[nn::NL][nn::MASK_WORDS];
-        nn::h4 U[nn::NL][4][nn::KT];
-        nn::h4 X[nn::INP / 16][4];
-        float y[3];
-        nn::mlp_forward_tiles<true>(WL, stage, x, Tm, U, X, ustore, y, lane);
-        float dy[3];
-        dy[0] = dpre.x * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[0]));
-        dy[1] = dpre.y * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[1]));
-        dy[2] = dpre.z * residual_activation_grad<EFGS_RES_ACT>(residual_activation<EFGS_RES_ACT>(y[2]));
+        const float g[3] = {dpre.x, dpre.y, dpre.z};
         float dx[nn::INP];
-        nn::mlp_backward_dual(WL, stage, Tm, U, X, ustore, dy, s, inv_s, dx, dW, lane);
+        nn::mlp_train(WL, stage, x, g, [](float y, float gy) { return gy * nn::residual_activation_slope<EFGS_RES_ACT>(y); }, s, inv_s, dx,
+                      dW, lane);
         if (contributes) {
             float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
 #pragma unroll

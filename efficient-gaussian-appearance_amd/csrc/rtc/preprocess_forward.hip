@@ -164,8 +164,8 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     // residual MLP weights staged once per block (padded rows); per-wave staging area for the input tiles
     extern __shared__ __align__(16) unsigned char smem[];
     const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
-    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::DUAL_WEIGHT_BYTES) + wave * 64 * nn::XS;
-    nn::load_dual_weights<preprocess_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES) + wave * 64 * nn::XS;
+    nn::load_weights<preprocess_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
     __syncthreads();
 #endif
     const uint32_t n_chunks = (a.n + preprocess_block - 1) / preprocess_block;
@@ -193,11 +193,8 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         if (a.cam.degree > 0 && __ballot(visible) != 0) {
             float x[nn::INP];
             nn::mlp_input(rp, a.base + 3 * p, d, a.cam.degree, x);
-            uint32_t masks[nn::NL][nn::MASK_WORDS];
-            nn::h4 unused[nn::NL][4][nn::KT];
-            nn::h4 unused_x[nn::INP / 16][4];
             float y[3];
-            nn::mlp_forward_tiles<false>(WL, stage, x, masks, unused, unused_x, nullptr, y, lane);
+            nn::mlp_forward(WL, stage, x, y, lane);
             res = make_float3(residual_activation<EFGS_RES_ACT>(y[0]), residual_activation<EFGS_RES_ACT>(y[1]),
                               residual_activation<EFGS_RES_ACT>(y[2]));
         }
