@@ -141,6 +141,11 @@ struct efgs_rasterizer {
     int mlp_n_features = 0;
     bool mlp_base_input = false;
     uint32_t* host_counters = nullptr;  // pinned, n_counters entries
+    hipEvent_t counters_ready = nullptr;  // recorded after the counter readback, on counters_device
+    int counters_device = -1;
+    // instance count of the last forward and the scene size it was for: sizes the next frame's instance
+    // buffers before its counter readback
+    uint32_t instance_hint = 0, hint_primitives = 0, hint_tiles = 0;
     efgs::StageTimer timer;
     // specialised preprocess kernels of the current configuration, per variant and direction (forward,
     // backward), for the device they were loaded on; cleared whenever the configuration changes
@@ -521,6 +526,7 @@ int efgs_rasterizer_create(efgs_rasterizer** out) {
 void efgs_rasterizer_destroy(efgs_rasterizer* r) {
     if (!r) return;
     if (r->host_counters) (void)hipHostFree(r->host_counters);
+    if (r->counters_ready) (void)hipEventDestroy(r->counters_ready);
     delete r;
 }
 
@@ -610,6 +616,16 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (hipHostMalloc(reinterpret_cast<void**>(&r->host_counters), n_counters * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
             return fail(EFGS_ERR_HIP, "hipHostMalloc of the counter readback buffer failed");
     }
+    {
+        int device = 0;
+        EFGS_HIP_CHECK(hipGetDevice(&device));
+        if (r->counters_device != device) {
+            if (r->counters_ready) (void)hipEventDestroy(r->counters_ready);
+            r->counters_ready = nullptr;
+            EFGS_HIP_CHECK(hipEventCreateWithFlags(&r->counters_ready, hipEventDisableTiming));
+            r->counters_device = device;
+        }
+    }
 
     const PrimitiveLayout pl0 = PrimitiveLayout::carve(nullptr, n);
     char* pblob = static_cast<char*>(alloc(alloc_ctx, pl0.bytes));
@@ -650,22 +666,42 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         t.end(s);
         t.begin(EFGS_STAGE_COMPACT, s);
         if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, chunks, s)) return EFGS_ERR_HIP;
-        if (!launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
-        t.end(s);
     } else {
         if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
     }
-    t.begin(EFGS_STAGE_COUNTER_READ, s);
+    // the counters are final after the block scan: read them back while the compaction runs, and size the
+    // instance buffers meanwhile from the previous frame's count (12.5 % headroom) when the scene size matches,
+    // so that neither the allocation nor the compaction sits between the readback and the next launch
     if (hipMemcpyAsync(r->host_counters, pl.counters, n_counters * sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipStreamSynchronize(s) != hipSuccess)
+        hipEventRecord(r->counters_ready, s) != hipSuccess)
+        return fail(EFGS_ERR_HIP, std::string("enqueueing the counter readback failed: ") + hipGetErrorString(hipGetLastError()));
+    if (n > 0) {
+        if (!launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
+        t.end(s);
+    }
+    char* iblob = nullptr;
+    size_t iblob_bytes = 0;
+    if (r->instance_hint > 0 && r->hint_primitives == n && r->hint_tiles == n_tiles) {
+        const uint64_t guess = static_cast<uint64_t>(r->instance_hint) + r->instance_hint / 8 + 1024;
+        iblob_bytes = InstanceLayout::carve(nullptr, guess, key_bytes, n_tiles).bytes;
+        iblob = static_cast<char*>(alloc(alloc_ctx, iblob_bytes));
+        if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
+    }
+    t.begin(EFGS_STAGE_COUNTER_READ, s);
+    if (hipEventSynchronize(r->counters_ready) != hipSuccess)
         return fail(EFGS_ERR_HIP, std::string("reading the visible/instance counters failed: ") + hipGetErrorString(hipGetLastError()));
     t.end(s);
     const uint32_t n_visible = r->host_counters[0];
     const uint32_t n_instances = r->host_counters[1];
+    r->instance_hint = n_instances;
+    r->hint_primitives = n;
+    r->hint_tiles = n_tiles;
 
     const InstanceLayout il0 = InstanceLayout::carve(nullptr, n_instances, key_bytes, n_tiles);
-    char* iblob = static_cast<char*>(alloc(alloc_ctx, il0.bytes));
-    if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
+    if (!iblob || il0.bytes > iblob_bytes) {
+        iblob = static_cast<char*>(alloc(alloc_ctx, il0.bytes));
+        if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
+    }
     const InstanceLayout il = InstanceLayout::carve(iblob, n_instances, key_bytes, n_tiles);
     const TileBinning plan = tile_binning_plan(n_instances, n_tiles);
     t.begin(EFGS_STAGE_CREATE_INSTANCES, s);

@@ -155,7 +155,8 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 
 }  // namespace efgs
 
-extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessForwardArgs a) {
+// four waves per SIMD (128 VGPRs): the neural variant's LDS admits four blocks per CU as well
+extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::PreprocessForwardArgs a) {
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
