@@ -8,8 +8,9 @@ parameter groups (means, scales, rotations, opacities, base colours, latents, ML
 resident in HBM before the timed region.
 
 Output: one JSON line. `value` = W * H / (wall time per full step) in Mpix/s (forward, loss, backward and
-Adam); `fwd_bwd_mpix_s` = W * H / (stream time from the forward's start to the backward's end, Adam
-excluded). `roofline` covers the step's dominant kernel, timed with HIP events that the library records
+Adam); `fwd_bwd_mpix_s` = W * H / (t_fwd + t_bwd), the rasterizer's forward and backward alone (stream time of
+forward + backward with a fixed upstream gradient: no loss, no Adam); `fwd_loss_bwd_ms` = stream time of a
+full step's forward, L1 loss and backward. `roofline` covers the step's dominant kernel, timed with HIP events that the library records
 around each stage on the stream it launches on (Adam: events around FusedAdam.step on the same stream);
 `stages` lists every stage. `cpu_baseline` times the CPU restatement (oracle/) of one forward + backward of
 the same scene on the host.
@@ -212,6 +213,24 @@ def gpu_benchmark(args):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     log(f'{args.steps} timed steps done: {wall * 1e3 / args.steps:.3f} ms/step')
+    # the rasterizer alone (t_fwd + t_bwd): forward and backward with the L1 gradient of one rendered image
+    with torch.no_grad():
+        img0 = efgs.diff_rasterize(params['means'], params['scales'], params['rotations'], params['opacities'], empty, settings,
+                                   base_colors=params['base_colors'], residual_params=params['residual_params'],
+                                   mlp_weights=params.get('mlp_weights'))
+        upstream = torch.sign(img0 - target) / img0.numel()
+    raster_events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    for k in range(args.steps):
+        raster_events[k][0].record()
+        img = efgs.diff_rasterize(params['means'], params['scales'], params['rotations'], params['opacities'], empty, settings,
+                                  base_colors=params['base_colors'], residual_params=params['residual_params'],
+                                  mlp_weights=params.get('mlp_weights'))
+        img.backward(upstream)
+        raster_events[k][1].record()
+        opt.zero_grad(set_to_none=True)
+    torch.cuda.synchronize()
+    raster_ms = sum(e[0].elapsed_time(e[1]) for e in raster_events) / args.steps
+    log(f'{args.steps} forward + backward passes (no loss, no Adam) done: {raster_ms:.3f} ms')
     # per-stage breakdown in a separate pass: the library's stage events add host work to every launch, so
     # the timed steps above run without them
     R._rasterizer.set_stage_timing(True)
@@ -221,7 +240,7 @@ def gpu_benchmark(args):
     R._rasterizer.set_stage_timing(False)
     log(f'{args.steps} steps with stage timing done')
 
-    fwd_bwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
+    fwd_loss_bwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
     adam_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
     V = sum(c[0] for c in counts) / len(counts)
     I = sum(c[1] for c in counts) / len(counts)
@@ -271,7 +290,7 @@ def gpu_benchmark(args):
     roofline.update({'kernel': kernel_name, 'stage': dominant, 'avg_launch_ms': round(dms, 5),
                      'algorithmic_bytes': int(b), 'algorithmic_flops': int(f)})
     ms_per_step = wall * 1e3 / args.steps
-    return dict(W=W, H=H, N=N, V=V, I=I, model=model, ms_per_step=ms_per_step, fwd_bwd_ms=fwd_bwd_ms, adam_ms=adam_ms,
+    return dict(W=W, H=H, N=N, V=V, I=I, model=model, ms_per_step=ms_per_step, fwd_bwd_ms=raster_ms, fwd_loss_bwd_ms=fwd_loss_bwd_ms, adam_ms=adam_ms,
                 roofline=roofline, stages=stages, scene=sc)
 
 
@@ -463,6 +482,7 @@ def main() -> None:
                    'visible': round(r['V']), 'instances': round(r['I'])},
         'fwd_bwd_mpix_s': round(W * H / (r['fwd_bwd_ms'] * 1e-3) / 1e6, 3),
         'fwd_bwd_ms': round(r['fwd_bwd_ms'], 4),
+        'fwd_loss_bwd_ms': round(r['fwd_loss_bwd_ms'], 4),
         'adam_ms': round(r['adam_ms'], 4),
         'roofline': r['roofline'],
         'stages': r['stages'],
