@@ -17,6 +17,7 @@ the same scene on the host.
 
   python bench.py [--steps K] [--warmup W] [--config c3|c1|c4_sv|c4_nasg|c4_nasgabor] [--no-cpu-baseline]
   python bench.py --config c2    # the neural decode alone: 1M primitives, forward + backward (latents, weights)
+  python bench.py --config mcmc  # MCMC densification: add_noise and relocation_adjustment of the 1M c3 Gaussians
   python bench.py --copy-calibration    # a plain 1 GiB device copy, for scaling rocprofv3 FETCH/WRITE_SIZE
 """
 from __future__ import annotations
@@ -433,6 +434,75 @@ def decode_cpu_baseline(m, feat, d, w, dy) -> dict:
                       f'{seconds:.1f} s'}
 
 
+# ---------------------------------------------------------------------------------------------------------
+# mcmc: the densification operators on the c3 scene
+# ---------------------------------------------------------------------------------------------------------
+
+def mcmc_benchmark(args) -> None:
+    """add_noise over all c3 Gaussians (every step of an MCMC schedule) and relocation_adjustment of all of them
+    with 1..5 samples each; HIP events on the launch stream."""
+    import numpy as np
+    import torch
+    import efgs
+    from efgs.synthetic import make_scene
+    device = torch.device('cuda:0')
+    torch.cuda.set_device(device)
+    torch.cuda.manual_seed(0)
+    sc = make_scene('c3')
+    n = sc['means'].shape[0]
+    scales = torch.tensor(sc['scales'], device=device)
+    rotations = torch.tensor(sc['rotations'], device=device)
+    opacities = torch.tensor(sc['opacities'], device=device)
+    means = torch.tensor(sc['means'], device=device)
+    act_o = torch.sigmoid(opacities)
+    act_s = torch.exp(scales)
+    counts = torch.tensor(np.random.default_rng(0).integers(1, 6, n), dtype=torch.int64, device=device)
+    lr = 5e5 * 1.6e-4 * 0.01
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+        for k in range(args.steps):
+            ev[k][0].record()
+            fn()
+            ev[k][1].record()
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in ev) / args.steps
+
+    log(f'mcmc: {n} Gaussians (c3 scene)')
+    noise_ms = timed(lambda: efgs.add_noise(scales, rotations, opacities, means, lr))
+    reloc_ms = timed(lambda: efgs.relocation_adjustment(act_o, act_s, counts))
+    noise_bytes = n * (12 + 16 + 4 + 12 + 12)    # log-scales, quaternion, opacity, mean in; mean out
+    reloc_bytes = n * (4 + 12 + 8 + 4 + 12)      # opacity, scales, count in; opacity, scales out
+    line = {
+        'metric': 'MCMC add_noise Mprim/s @1M Gaussians (c3 scene)', 'value': round(n / (noise_ms * 1e-3) / 1e6, 3), 'unit': 'Mprim/s',
+        'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(noise_ms, 5), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32 (Philox4x32-10 u32)', 'data': 'synthetic',
+        'config': {'workload': f'mcmc: add_noise and relocation_adjustment (1..5 samples) of the {n} c3 Gaussians', 'n_primitives': n},
+        'add_noise_ms': round(noise_ms, 5), 'relocation_ms': round(reloc_ms, 5),
+        'relocation_mprim_s': round(n / (reloc_ms * 1e-3) / 1e6, 3),
+        'roofline': {'bound': 'hbm', 'achieved': round(noise_bytes / (noise_ms * 1e-3) / 1e9, 2), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+                     'frac': round(noise_bytes / (noise_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5), 'traffic': None, 'kernel': 'add_noise_kernel',
+                     'algorithmic_bytes': int(noise_bytes),
+                     'relocation': {'achieved': round(reloc_bytes / (reloc_ms * 1e-3) / 1e9, 2), 'unit': 'GB/s',
+                                    'frac': round(reloc_bytes / (reloc_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
+                                    'algorithmic_bytes': int(reloc_bytes)}},
+        'cpu_baseline': None,
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+        import oracle as O
+        O.build()
+        t0 = time.perf_counter()
+        O.add_noise(sc['scales'], sc['rotations'], sc['opacities'].reshape(-1), sc['means'], lr, 1, 0)
+        seconds = time.perf_counter() - t0
+        line['cpu_baseline'] = {'value': round(n / seconds / 1e6, 5), 'unit': 'Mprim/s', 'cores': 1, 'kind': 'port',
+                                'sample': f'add_noise of all {n} Gaussians through the C restatement (oracle), one thread; '
+                                          f'{seconds:.2f} s'}
+    print(json.dumps(line), flush=True)
+
+
 def copy_calibration() -> None:
     """A plain device copy of 1 GiB, five times: rocprofv3 FETCH_SIZE / WRITE_SIZE of this command read
     1 GiB each per dispatch when the counters are exact."""
@@ -460,6 +530,9 @@ def main() -> None:
         raise SystemExit('bench.py: --steps must be >= 1 and --warmup >= 0')
     if args.config == 'c2':
         decode_benchmark(args)
+        return
+    if args.config == 'mcmc':
+        mcmc_benchmark(args)
         return
     r = gpu_benchmark(args)
     W, H = r['W'], r['H']

@@ -24,6 +24,7 @@ SOURCES = [
     ('raster.hip', ['-ffp-contract=off']),
     ('blend.hip', ['-ffp-contract=off']),
     ('adam.hip', ['-ffp-contract=off']),
+    ('densification.hip', ['-ffp-contract=off']),
 ]
 
 COMMON = ['-O3', '-std=c++17', '-fPIC', '-fhip-fp32-correctly-rounded-divide-sqrt',

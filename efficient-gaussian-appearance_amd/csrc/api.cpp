@@ -898,6 +898,28 @@ int efgs_adam_step(const efgs_adam_group* groups, int n_groups, void* stream) {
     return EFGS_OK;
 }
 
+int efgs_add_noise(int64_t n, const float* raw_scales, const float* raw_rotations, const float* raw_opacities, float* means, float current_lr,
+                   uint64_t seed, uint64_t offset, void* stream) {
+    if (n < 0 || n > static_cast<int64_t>(UINT32_MAX)) return fail(EFGS_ERR_INVALID_ARGUMENT, "primitive count out of range");
+    if (n > 0 && (!raw_scales || !raw_rotations || !raw_opacities || !means)) return fail(EFGS_ERR_INVALID_ARGUMENT, "null tensor");
+    if (offset % 4 != 0) return fail(EFGS_ERR_INVALID_ARGUMENT, "the philox offset must be a multiple of 4");
+    if (!launch_add_noise(raw_scales, raw_rotations, raw_opacities, means, static_cast<uint32_t>(n), current_lr, seed, offset,
+                          static_cast<hipStream_t>(stream)))
+        return EFGS_ERR_HIP;
+    return EFGS_OK;
+}
+
+int efgs_relocation_adjustment(int64_t n, const float* old_opacities, const float* old_scales, const int64_t* n_samples_per_primitive,
+                               float* new_opacities, float* new_scales, void* stream) {
+    if (n < 0 || n > static_cast<int64_t>(UINT32_MAX)) return fail(EFGS_ERR_INVALID_ARGUMENT, "primitive count out of range");
+    if (n > 0 && (!old_opacities || !old_scales || !n_samples_per_primitive || !new_opacities || !new_scales))
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "null tensor");
+    if (!launch_relocation(old_opacities, old_scales, n_samples_per_primitive, new_opacities, new_scales, static_cast<uint32_t>(n),
+                           static_cast<hipStream_t>(stream)))
+        return EFGS_ERR_HIP;
+    return EFGS_OK;
+}
+
 int efgs_set_stage_timing(efgs_rasterizer* r, int enable) {
     if (!r) return fail(EFGS_ERR_INVALID_ARGUMENT, "null rasterizer");
     return r->timer.enable(enable != 0) ? EFGS_OK : EFGS_ERR_HIP;

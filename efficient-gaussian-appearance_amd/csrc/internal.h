@@ -126,4 +126,11 @@ struct AdamGroupDevice {
 };
 bool launch_adam(const AdamGroupDevice* groups, int n_groups, hipStream_t s);
 
+// ---- MCMC densification ---------------------------------------------------------------------------------------
+constexpr uint32_t mcmc_max_samples = 50;  // samples per relocated Gaussian (larger counts are clamped)
+bool launch_add_noise(const float* raw_scales, const float* raw_rotations, const float* raw_opacities, float* means, uint32_t n, float lr,
+                      uint64_t seed, uint64_t offset, hipStream_t s);
+bool launch_relocation(const float* old_opacities, const float* old_scales, const int64_t* n_samples, float* new_opacities, float* new_scales,
+                       uint32_t n, hipStream_t s);
+
 }  // namespace efgs

@@ -2,12 +2,13 @@
 
 Drop-in for the reference package's exports (FasterGSVDACudaBackend/__init__.py:14-23): diff_rasterize,
 rasterize, update_pruning_scores, RasterizerSettings, initialize_appearance, initialize_residual_mlp,
-FusedAdam. The compute path is libefgs_hip.so (hand-written HIP kernels for gfx950, hipRTC-specialised
+FusedAdam, relocation_adjustment, add_noise. The compute path is libefgs_hip.so (hand-written HIP kernels for gfx950, hipRTC-specialised
 preprocess); importing without the built library raises ImportError.
 """
 from .rasterization import (diff_rasterize, rasterize, update_pruning_scores, RasterizerSettings, initialize_appearance,
                             initialize_residual_mlp)
 from .adam import FusedAdam
+from .densification import relocation_adjustment, add_noise
 
 __all__ = ['diff_rasterize', 'rasterize', 'update_pruning_scores', 'RasterizerSettings', 'initialize_appearance',
-           'initialize_residual_mlp', 'FusedAdam']
+           'initialize_residual_mlp', 'FusedAdam', 'relocation_adjustment', 'add_noise']

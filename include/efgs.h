@@ -15,6 +15,8 @@
  *   _C.forward ................. B/rasterization/src/rasterization_api.cu:16-123
  *   _C.backward ................ B/rasterization/src/rasterization_api.cu:125-247
  *   _C.adam_step ............... B/adam/src/adam.cu:44-87
+ *   _C.add_noise ............... B/densification/src/densification_api.cu:40-72
+ *   _C.relocation_adjustment ... B/densification/src/densification_api.cu:13-38
  */
 #ifndef EFGS_H
 #define EFGS_H
@@ -171,6 +173,24 @@ typedef struct efgs_adam_group {
     double beta1, beta2, eps;
 } efgs_adam_group;
 int efgs_adam_step(const efgs_adam_group* groups, int n_groups, void* stream);
+
+/* MCMC noise (3DGS-MCMC): means (n x 3) += current_lr * sigmoid(-(100 sigmoid(raw_opacity) - 0.5)) * Sigma z in
+ * place, Sigma from the log-scales (n x 3) and the unnormalised quaternions (n x 4, w x y z; |q|^2 < 1e-8 leaves
+ * the mean unchanged), z ~ N(0, I) from Philox4x32-10 with key `seed` and counter (offset / 4, primitive
+ * index, 0) through Box-Muller; `offset` must be a multiple of 4 (the caller advances its generator by 4 per
+ * call, as PyTorch's philox_engine_inputs(4)). Stream-ordered.
+ * Replaces _C.add_noise, B/densification/src/densification_api.cu:40-72 (kernel B/densification/include/
+ * kernels_mcmc.cuh:74-144). */
+int efgs_add_noise(int64_t n, const float* raw_scales, const float* raw_rotations, const float* raw_opacities, float* means, float current_lr,
+                   uint64_t seed, uint64_t offset, void* stream);
+
+/* MCMC relocation: for each of n Gaussians split into n_samples_per_primitive (int64, clamped to 1..50)
+ * copies, the new opacity 1 - (1 - o)^(1/n) (n x 1 in, n x 1 out) and the activated scales (n x 3) scaled so
+ * that the copies together keep the original's footprint (Eq. 9 of the paper). Outputs are caller-allocated.
+ * Replaces _C.relocation_adjustment, B/densification/src/densification_api.cu:13-38 (kernel
+ * B/densification/include/kernels_mcmc.cuh:11-56). */
+int efgs_relocation_adjustment(int64_t n, const float* old_opacities, const float* old_scales, const int64_t* n_samples_per_primitive,
+                               float* new_opacities, float* new_scales, void* stream);
 
 /* Standalone neural decode: the configured residual MLP (efgs_set_residual_mlp, model 5) on n primitives'
  * features (n x n_features, the learned latents), base colours (n x 3, read with base input only) and unit

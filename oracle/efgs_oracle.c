@@ -1059,3 +1059,106 @@ float efo_blend_alpha(float mx, float my, float cx, float cy, float cz, float op
     const float dx = mx - ((float)px + 0.5f), dy = my - ((float)py + 0.5f);
     return opacity * ef_exp2f(fminf(blend_exponent(ex, ey, ez, dx, dy), 0.0f));
 }
+
+/* ------------------------------------------------------------------------------------------------------ */
+/* MCMC densification, B/densification/include/kernels_mcmc.cuh:11-146                                    */
+/* ------------------------------------------------------------------------------------------------------ */
+
+/* Philox4x32-10: Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3" (SC 2011), the
+   Random123 philox4x32 generator with 10 rounds. Round: (c0, c1, c2, c3) -> (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2),
+   hi(M0 c0) ^ c3 ^ k1, lo(M0 c0)); the key is bumped by the Weyl constants before every round but the first. */
+void efo_philox4x32_10(const uint32_t* ctr, const uint32_t* key, uint32_t* out) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; r++) {
+        if (r > 0) {
+            k0 += 0x9E3779B9u;
+            k1 += 0xBB67AE85u;
+        }
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1, n3 = (uint32_t)p0;
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* two standard normal samples from two 32-bit words: u = (bits_u + 1/2) 2^-32 in (0, 1], angle bits_v 2 pi 2^-32
+   (kernels_mcmc.cuh:70-77) */
+void efo_box_muller(uint32_t bits_u, uint32_t bits_v, float* z) {
+    const float u = fmaf((float)bits_u, 2.3283064e-10f, 1.1641532e-10f);
+    const float radius = sqrtf(-2.0f * logf(u));
+    const float angle = (float)bits_v * 1.4629181e-9f;
+    z[0] = radius * cosf(angle);
+    z[1] = radius * sinf(angle);
+}
+
+/* means[i] += lr sigmoid(-(100 sigmoid(raw_opacity) - 0.5)) Sigma z (kernels_mcmc.cuh:79-144): Sigma = R diag(e^{2 s})
+   R^T of the normalised quaternion, z from the Philox block with counter (offset / 4, i, 0) and key seed */
+void efo_add_noise(int n, const float* raw_scales, const float* raw_rotations, const float* raw_opacities, float* means, float lr,
+                   uint64_t seed, uint64_t offset) {
+    const uint64_t counter = offset / 4;
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    for (int i = 0; i < n; i++) {
+        const float* q = raw_rotations + 4 * i;
+        const float w = q[0], x = q[1], y = q[2], z = q[3];
+        const float norm_sq = w * w + x * x + y * y + z * z;
+        if (norm_sq < 1e-8f) continue;
+        const float inv = 1.0f / norm_sq;
+        const float R[3][3] = {{1.0f - 2.0f * (y * y + z * z) * inv, 2.0f * (x * y - w * z) * inv, 2.0f * (x * z + w * y) * inv},
+                               {2.0f * (x * y + w * z) * inv, 1.0f - 2.0f * (x * x + z * z) * inv, 2.0f * (y * z - w * x) * inv},
+                               {2.0f * (x * z - w * y) * inv, 2.0f * (y * z + w * x) * inv, 1.0f - 2.0f * (x * x + y * y) * inv}};
+        const float v[3] = {expf(2.0f * raw_scales[3 * i]), expf(2.0f * raw_scales[3 * i + 1]), expf(2.0f * raw_scales[3 * i + 2])};
+        float S[3][3];
+        for (int a = 0; a < 3; a++)
+            for (int b = 0; b < 3; b++) S[a][b] = R[a][0] * v[0] * R[b][0] + R[a][1] * v[1] * R[b][1] + R[a][2] * v[2] * R[b][2];
+        const uint32_t ctr[4] = {(uint32_t)counter, (uint32_t)(counter >> 32), (uint32_t)i, 0u};
+        uint32_t bits[4];
+        efo_philox4x32_10(ctr, key, bits);
+        float zxy[2], zz[2];
+        efo_box_muller(bits[0], bits[1], zxy);
+        efo_box_muller(bits[2], bits[3], zz);
+        const float zv[3] = {zxy[0], zxy[1], zz[0]};
+        const float o = 1.0f / (1.0f + expf(-raw_opacities[i]));
+        const float f = lr * (1.0f / (1.0f + expf(100.0f * o - 0.5f)));
+        for (int a = 0; a < 3; a++) means[3 * i + a] += f * (S[a][0] * zv[0] + S[a][1] * zv[1] + S[a][2] * zv[2]);
+    }
+}
+
+#define EFO_MCMC_MAX_SAMPLES 50
+
+/* c[m][k] = C(m, k) (-1)^k / sqrt(k + 1) in double, rounded to float (kernels_mcmc.cuh:13-26) */
+void efo_relocation_table(float* table) {
+    for (int m = 0; m < EFO_MCMC_MAX_SAMPLES; m++) {
+        double binom = 1.0, sign = 1.0;
+        for (int k = 0; k < EFO_MCMC_MAX_SAMPLES; k++) {
+            if (k > m) {
+                table[m * EFO_MCMC_MAX_SAMPLES + k] = 0.0f;
+                continue;
+            }
+            table[m * EFO_MCMC_MAX_SAMPLES + k] = (float)(binom * sign * (1.0 / sqrt((double)(k + 1))));
+            binom *= (double)(m - k) / (double)(k + 1);
+            sign = -sign;
+        }
+    }
+}
+
+/* kernels_mcmc.cuh:28-56: o' = 1 - (1 - o)^(1/n), scales times o / sum_{m<n} sum_{k<=m} c[m][k] o'^(k+1) */
+void efo_relocation(int n, const float* old_opacities, const float* old_scales, const int64_t* n_samples, float* new_opacities,
+                    float* new_scales) {
+    float table[EFO_MCMC_MAX_SAMPLES * EFO_MCMC_MAX_SAMPLES];
+    efo_relocation_table(table);
+    for (int i = 0; i < n; i++) {
+        const float o = old_opacities[i];
+        const int64_t s = n_samples[i];
+        const int ns = s < 1 ? 1 : (s > EFO_MCMC_MAX_SAMPLES ? EFO_MCMC_MAX_SAMPLES : (int)s);
+        const float o_new = 1.0f - powf(1.0f - o, 1.0f / (float)ns);
+        new_opacities[i] = o_new;
+        float denominator = 0.0f;
+        for (int m = 0; m < ns; m++) {
+            float p = o_new;
+            for (int k = 0; k <= m; k++, p *= o_new) denominator += table[m * EFO_MCMC_MAX_SAMPLES + k] * p;
+        }
+        const float factor = o / denominator;
+        for (int a = 0; a < 3; a++) new_scales[3 * i + a] = factor * old_scales[3 * i + a];
+    }
+}

@@ -76,6 +76,11 @@ def lib() -> ctypes.CDLL:
         _lib.efo_blend_alpha.restype = ctypes.c_float
         _lib.efo_blend_alpha.argtypes = [ctypes.c_float] * 6 + [ctypes.c_int] * 2
         _lib.efo_sh_rest_basis.restype = ctypes.c_int
+        _lib.efo_philox4x32_10.argtypes = [ctypes.c_void_p] * 3
+        _lib.efo_box_muller.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+        _lib.efo_add_noise.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64]
+        _lib.efo_relocation_table.argtypes = [ctypes.c_void_p]
+        _lib.efo_relocation.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
     return _lib
 
 
@@ -698,3 +703,50 @@ def residual(app: 'Appearance', params: np.ndarray, direction, degree: int) -> n
     out = np.zeros(3, np.float32)
     lib().efo_residual(ctypes.byref(app.c_struct()), _p(_f32(params).reshape(-1)), _p(_f32(direction)), ctypes.c_int(degree), _p(out))
     return out
+
+
+# ---------------------------------------------------------------------------------------------------------
+# MCMC densification (B/densification/include/kernels_mcmc.cuh:11-146)
+# ---------------------------------------------------------------------------------------------------------
+
+MCMC_MAX_SAMPLES = 50
+
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    """Philox4x32-10 block (Random123) of the 4-word counter and 2-word key."""
+    c = np.ascontiguousarray(np.asarray(ctr, dtype=np.uint32))
+    k = np.ascontiguousarray(np.asarray(key, dtype=np.uint32))
+    out = np.zeros(4, np.uint32)
+    lib().efo_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def box_muller(bits_u: int, bits_v: int) -> np.ndarray:
+    out = np.zeros(2, np.float32)
+    lib().efo_box_muller(ctypes.c_uint32(bits_u), ctypes.c_uint32(bits_v), _p(out))
+    return out
+
+
+def add_noise(raw_scales, raw_rotations, raw_opacities, means, lr: float, seed: int, offset: int) -> np.ndarray:
+    """New means after the MCMC noise step (the inputs are not modified)."""
+    s, q, o = _f32(raw_scales), _f32(raw_rotations), _f32(raw_opacities)
+    m = _f32(means).copy()
+    n = m.shape[0]
+    lib().efo_add_noise(n, _p(s), _p(q), _p(o), _p(m), ctypes.c_float(lr), ctypes.c_uint64(seed), ctypes.c_uint64(offset))
+    return m
+
+
+def relocation_table() -> np.ndarray:
+    t = np.zeros((MCMC_MAX_SAMPLES, MCMC_MAX_SAMPLES), np.float32)
+    lib().efo_relocation_table(_p(t))
+    return t
+
+
+def relocation_adjustment(old_opacities, old_scales, n_samples) -> tuple[np.ndarray, np.ndarray]:
+    o, s = _f32(old_opacities).reshape(-1), _f32(old_scales)
+    c = np.ascontiguousarray(np.asarray(n_samples, dtype=np.int64).reshape(-1))
+    n = o.shape[0]
+    new_o = np.zeros((n, 1), np.float32)
+    new_s = np.zeros((n, 3), np.float32)
+    lib().efo_relocation(n, _p(o), _p(s), _p(c), _p(new_o), _p(new_s))
+    return new_o, new_s

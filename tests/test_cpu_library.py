@@ -109,6 +109,22 @@ def test_adam_validation():
     assert _lib.lib.efgs_adam_step(ctypes.byref(g), 1, None) == 1
 
 
+def test_densification_validation():
+    """Argument checks of the MCMC entry points happen before any device work: negative counts, null tensors
+    and a Philox offset that is not a multiple of 4 are rejected; empty inputs are accepted."""
+    from efgs import _lib
+    lib = _lib.lib
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.efgs_add_noise(-1, fake, fake, fake, fake, 0.1, 1, 0, None) == 1
+    assert lib.efgs_add_noise(10, None, fake, fake, fake, 0.1, 1, 0, None) == 1
+    assert lib.efgs_add_noise(10, fake, fake, fake, fake, 0.1, 1, 2, None) == 1
+    assert b'multiple of 4' in lib.efgs_last_error()
+    assert lib.efgs_add_noise(0, None, None, None, None, 0.1, 1, 0, None) == 0
+    assert lib.efgs_relocation_adjustment(-1, fake, fake, fake, fake, fake, None) == 1
+    assert lib.efgs_relocation_adjustment(5, fake, fake, None, fake, fake, None) == 1
+    assert lib.efgs_relocation_adjustment(0, None, None, None, None, None, None) == 0
+
+
 def test_stage_timing_without_launches():
     """Timing can be enabled and read back without any GPU work: every stage reports zero launches."""
     from efgs import _lib

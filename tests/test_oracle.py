@@ -290,3 +290,121 @@ def test_neural_decode_matches_autograd(name):
     assert rel_l2(ref['dirs'], td.grad.numpy()) < 1e-4
     if mlp.base_input:
         assert rel_l2(ref['base'], tb.grad.numpy()) < 1e-4
+
+
+# ---------------------------------------------------------------------------------------------------------
+# MCMC densification (B/densification/include/kernels_mcmc.cuh:11-146)
+# ---------------------------------------------------------------------------------------------------------
+
+# Random123 known-answer vectors of philox4x32 with 10 rounds: (counter, key, output)
+PHILOX_KAT = [
+    ([0x00000000] * 4, [0x00000000] * 2, [0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8]),
+    ([0xffffffff] * 4, [0xffffffff] * 2, [0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd]),
+    ([0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344], [0xa4093822, 0x299f31d0], [0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1]),
+]
+
+
+@pytest.mark.parametrize('case', range(len(PHILOX_KAT)))
+def test_philox_known_answers(case):
+    ctr, key, want = PHILOX_KAT[case]
+    np.testing.assert_array_equal(O.philox4x32_10(ctr, key), np.array(want, np.uint32))
+
+
+def test_box_muller_closed_forms_and_moments():
+    """u = 1 (bits 0xffffffff) gives radius 0; u = 2^-33 (bits 0) radius sqrt(66 ln 2); the angle word maps
+    [0, 2^32) onto [0, 2 pi). Samples from consecutive Philox counters have zero mean, unit variance and no
+    correlation between the two outputs (tolerances ~5 standard errors at 40,000 samples)."""
+    np.testing.assert_allclose(O.box_muller(0xffffffff, 12345), [0.0, 0.0], atol=1e-6)
+    r = math.sqrt(66.0 * math.log(2.0))
+    np.testing.assert_allclose(O.box_muller(0, 0), [r, 0.0], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(O.box_muller(0, 1 << 30), [0.0, r], rtol=1e-5, atol=2e-5)  # angle pi / 2
+    np.testing.assert_allclose(O.box_muller(0, 1 << 31), [-r, 0.0], rtol=1e-5, atol=3e-5)  # angle pi
+    z = []
+    for i in range(10000):
+        b = O.philox4x32_10([i, 0, 7, 0], [1234, 5678])
+        z.append(O.box_muller(int(b[0]), int(b[1])))
+        z.append(O.box_muller(int(b[2]), int(b[3])))
+    z = np.array(z, np.float64)
+    n = z.shape[0]
+    assert np.all(np.abs(z.mean(0)) < 5 / math.sqrt(n))
+    assert np.all(np.abs(z.var(0) - 1.0) < 5 * math.sqrt(2.0 / n))
+    assert abs(np.corrcoef(z[:, 0], z[:, 1])[0, 1]) < 5 / math.sqrt(n)
+
+
+def _noise_direct(raw_scales, rot64, raw_opacities, lr, seed, offset):
+    """Expected noise step in float64 from an independent rotation matrix (axis-angle), the oracle's Philox
+    words and Box-Muller samples."""
+    n = raw_scales.shape[0]
+    out = np.zeros((n, 3))
+    for i in range(n):
+        b = O.philox4x32_10([offset // 4 & 0xffffffff, offset // 4 >> 32, i, 0], [seed & 0xffffffff, seed >> 32])
+        zxy, zz = O.box_muller(int(b[0]), int(b[1])), O.box_muller(int(b[2]), int(b[3]))
+        z = np.array([zxy[0], zxy[1], zz[0]], np.float64)
+        R = rot64[i]
+        sigma = R @ np.diag(np.exp(2.0 * raw_scales[i].astype(np.float64))) @ R.T
+        o = 1.0 / (1.0 + math.exp(-float(raw_opacities[i])))
+        f = lr / (1.0 + math.exp(100.0 * o - 0.5))
+        out[i] = f * (sigma @ z)
+    return out
+
+
+def _axis_angle(axis, angle):
+    a = np.asarray(axis, np.float64)
+    a = a / np.linalg.norm(a)
+    K = np.array([[0, -a[2], a[1]], [a[2], 0, -a[0]], [-a[1], a[0], 0]])
+    return np.eye(3) + math.sin(angle) * K + (1 - math.cos(angle)) * K @ K
+
+
+def test_add_noise_against_direct_statement():
+    """Quaternion (w, x, y, z) = (cos(t/2), sin(t/2) axis) scaled by arbitrary factors (the kernel normalises
+    through |q|^2) must give Sigma = R(axis, t) diag(e^{2s}) R^T; a zero quaternion leaves the mean
+    unchanged; the opacity factor follows sigmoid(-(100 o - 0.5))."""
+    rng = np.random.default_rng(3)
+    n = 64
+    axes = rng.normal(size=(n, 3))
+    angles = rng.uniform(-math.pi, math.pi, n)
+    scale = rng.uniform(0.5, 3.0, n)
+    q = np.stack([np.cos(angles / 2), *(np.sin(angles / 2)[None] * (axes / np.linalg.norm(axes, axis=1, keepdims=True)).T)], 1) * scale[:, None]
+    q[5] = 0.0
+    rot = np.stack([_axis_angle(axes[i], angles[i]) for i in range(n)])
+    raw_scales = rng.normal(-2.0, 0.5, (n, 3)).astype(np.float32)
+    raw_op = rng.normal(-5.0, 2.0, n).astype(np.float32)  # a spread of opacity factors (opaque ones get ~0)
+    means = rng.uniform(-3, 3, (n, 3)).astype(np.float32)
+    seed, offset, lr = 0x1234_5678_9abc_def0, 4 * 77, 0.37
+    got = O.add_noise(raw_scales, q.astype(np.float32), raw_op, means, lr, seed, offset) - means.astype(np.float64)
+    want = _noise_direct(raw_scales, rot, raw_op, lr, seed, offset)
+    want[5] = 0.0
+    assert np.all(got[5] == 0.0)
+    assert rel_l2(got, want) < 1e-4
+    # float32 rounding of the mean update: at most one ulp of the mean plus 1e-5 of the step
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=float(np.abs(means).max()) * 2.0 ** -22)
+
+
+def test_relocation_closed_forms():
+    """The coefficient table equals C(m, k) (-1)^k / sqrt(k + 1) (math.comb, float64); one sample keeps the
+    Gaussian (o' = o, scales unchanged); two samples follow o' = 1 - sqrt(1 - o), factor o / (2 o' - o'^2 /
+    sqrt(2)); counts clamp to 1..50; the split opacities compose back, 1 - (1 - o')^n = o."""
+    t = O.relocation_table()
+    want = np.zeros((50, 50))
+    for m in range(50):
+        for k in range(m + 1):
+            want[m, k] = math.comb(m, k) * (-1) ** k / math.sqrt(k + 1)
+    np.testing.assert_allclose(t, want.astype(np.float32), rtol=1e-7, atol=0)
+    o = np.array([0.01, 0.3, 0.5, 0.9, 0.999, 0.3, 0.3], np.float32)
+    s = np.tile(np.array([[0.1, 0.2, 0.05]], np.float32), (7, 1))
+    c = np.array([1, 1, 2, 2, 2, 0, 80], np.int64)
+    no, ns = O.relocation_adjustment(o, s, c)
+    np.testing.assert_allclose(no[:2, 0], o[:2], rtol=1e-6)
+    np.testing.assert_allclose(ns[:2], s[:2], rtol=1e-6)
+    o2 = 1.0 - np.sqrt(1.0 - o[2:5].astype(np.float64))
+    np.testing.assert_allclose(no[2:5, 0], o2, rtol=1e-5)
+    f2 = o[2:5] / (2 * o2 - o2 ** 2 / math.sqrt(2.0))
+    np.testing.assert_allclose(ns[2:5], s[2:5] * f2[:, None], rtol=1e-5)
+    np.testing.assert_allclose(no[5], no[0] * 0 + o[5], rtol=1e-6)  # count 0 clamps to 1
+    o50 = 1.0 - (1.0 - 0.3) ** (1.0 / 50.0)
+    np.testing.assert_allclose(no[6, 0], o50, rtol=1e-4)  # count 80 clamps to 50
+    rng = np.random.default_rng(5)
+    oo = rng.uniform(0.05, 0.99, 500).astype(np.float32)
+    cc = rng.integers(1, 51, 500)
+    no, _ = O.relocation_adjustment(oo, np.ones((500, 3), np.float32), cc)
+    np.testing.assert_allclose(1.0 - (1.0 - no[:, 0].astype(np.float64)) ** cc, oo, rtol=3e-4)
