@@ -10,7 +10,8 @@ resident in HBM before the timed region.
 Output: one JSON line. `value` = W * H / (wall time per full step) in Mpix/s (forward, loss, backward and
 Adam); `fwd_bwd_mpix_s` = W * H / (t_fwd + t_bwd), the rasterizer's forward and backward alone (stream time of
 forward + backward with a fixed upstream gradient: no loss, no Adam); `fwd_loss_bwd_ms` = stream time of a
-full step's forward, L1 loss and backward. `roofline` covers the step's dominant kernel, timed with HIP events that the library records
+full step's forward, L1 loss and backward; `inference_ms` / `inference_fps` = `rasterize` as the reference's
+render_image_benchmark calls it (HWC, clamped, no autograd). `roofline` covers the step's dominant kernel, timed with HIP events that the library records
 around each stage on the stream it launches on (Adam: events around FusedAdam.step on the same stream);
 `stages` lists every stage. `cpu_baseline` times the CPU restatement (oracle/) of one forward + backward of
 the same scene on the host.
@@ -232,6 +233,20 @@ def gpu_benchmark(args):
     torch.cuda.synchronize()
     raster_ms = sum(e[0].elapsed_time(e[1]) for e in raster_events) / args.steps
     log(f'{args.steps} forward + backward passes (no loss, no Adam) done: {raster_ms:.3f} ms')
+    # inference renders as the reference's render_image_benchmark calls them: HWC, clamped, no autograd
+    render_events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    with torch.inference_mode():
+        for k in range(-2, args.steps):
+            if k >= 0:
+                render_events[k][0].record()
+            efgs.rasterize(params['means'], params['scales'], params['rotations'], params['opacities'], settings, False, True,
+                           base_colors=params['base_colors'], residual_params=params['residual_params'],
+                           mlp_weights=params.get('mlp_weights'))
+            if k >= 0:
+                render_events[k][1].record()
+    torch.cuda.synchronize()
+    render_ms = sum(e[0].elapsed_time(e[1]) for e in render_events) / args.steps
+    log(f'{args.steps} inference renders done: {render_ms:.3f} ms')
     # per-stage breakdown in a separate pass: the library's stage events add host work to every launch, so
     # the timed steps above run without them
     R._rasterizer.set_stage_timing(True)
@@ -291,7 +306,7 @@ def gpu_benchmark(args):
     roofline.update({'kernel': kernel_name, 'stage': dominant, 'avg_launch_ms': round(dms, 5),
                      'algorithmic_bytes': int(b), 'algorithmic_flops': int(f)})
     ms_per_step = wall * 1e3 / args.steps
-    return dict(W=W, H=H, N=N, V=V, I=I, model=model, ms_per_step=ms_per_step, fwd_bwd_ms=raster_ms, fwd_loss_bwd_ms=fwd_loss_bwd_ms, adam_ms=adam_ms,
+    return dict(W=W, H=H, N=N, V=V, I=I, model=model, ms_per_step=ms_per_step, fwd_bwd_ms=raster_ms, fwd_loss_bwd_ms=fwd_loss_bwd_ms, adam_ms=adam_ms, render_ms=render_ms,
                 roofline=roofline, stages=stages, scene=sc)
 
 
@@ -556,6 +571,8 @@ def main() -> None:
         'fwd_bwd_mpix_s': round(W * H / (r['fwd_bwd_ms'] * 1e-3) / 1e6, 3),
         'fwd_bwd_ms': round(r['fwd_bwd_ms'], 4),
         'fwd_loss_bwd_ms': round(r['fwd_loss_bwd_ms'], 4),
+        'inference_ms': round(r['render_ms'], 4),
+        'inference_fps': round(1e3 / r['render_ms'], 1),
         'adam_ms': round(r['adam_ms'], 4),
         'roofline': r['roofline'],
         'stages': r['stages'],

@@ -599,9 +599,14 @@ int64_t efgs_mlp_param_count(const efgs_rasterizer* r) {
     return n * r->mlp_n_in_padded + (r->mlp_n_hidden - 1) * n * n + 16 * n;
 }
 
-int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image, efgs_alloc_fn alloc,
-                 void* alloc_ctx, efgs_frame* frame, void* stream) {
-    if (!r || !prims || !settings || !image || !alloc || !frame) return fail(EFGS_ERR_INVALID_ARGUMENT, "null argument");
+namespace {
+
+// The forward pipeline. A training forward (frame != null) keeps the backward state (final T, last contributors,
+// tile maxima) and writes the image CHW; an inference render (frame == null) writes only the image, in CHW or
+// HWC layout, optionally clamped.
+int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image, efgs_alloc_fn alloc,
+                 void* alloc_ctx, efgs_frame* frame, bool hwc, bool clamp, void* stream) {
+    if (!r || !prims || !settings || !image || !alloc) return fail(EFGS_ERR_INVALID_ARGUMENT, "null argument");
     if (settings->width <= 0 || settings->height <= 0 || settings->width > 65535 || settings->height > 65535)
         return fail(EFGS_ERR_INVALID_ARGUMENT, "image size out of range");
     if (!settings->w2c || !settings->cam_position || !settings->bg_color) return fail(EFGS_ERR_INVALID_ARGUMENT, "camera tensors are required");
@@ -736,9 +741,13 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     b.height = static_cast<uint32_t>(settings->height);
     b.grid_w = grid_w;
     b.n_tiles = n_tiles;
+    b.hwc = hwc ? 1u : 0u;
+    b.clamp = clamp ? 1u : 0u;
+    if (!frame) b.final_T = nullptr;
     t.begin(EFGS_STAGE_BLEND_FORWARD, s);
     if (!launch_blend_forward(b, s)) return EFGS_ERR_HIP;
     t.end(s);
+    if (!frame) return EFGS_OK;
 
     frame->primitive_buffers = pblob;
     frame->tile_buffers = tblob;
@@ -751,6 +760,19 @@ int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     frame->key_bytes = key_bytes;
     frame->model = variant;
     return EFGS_OK;
+}
+
+}  // namespace
+
+int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image, efgs_alloc_fn alloc,
+                 void* alloc_ctx, efgs_frame* frame, void* stream) {
+    if (!frame) return fail(EFGS_ERR_INVALID_ARGUMENT, "null frame");
+    return forward_impl(r, prims, settings, image, alloc, alloc_ctx, frame, false, false, stream);
+}
+
+int efgs_render(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image, int to_chw, int clamp_output,
+                efgs_alloc_fn alloc, void* alloc_ctx, void* stream) {
+    return forward_impl(r, prims, settings, image, alloc, alloc_ctx, nullptr, to_chw == 0, clamp_output != 0, stream);
 }
 
 int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, const efgs_frame* frame, const float* image,

@@ -7,8 +7,8 @@
 //
 // Forward: front-to-back compositing, alpha = o exp2(min(q, 0)) with the conic pre-scaled by -log2(e)/2 and
 // the hardware exp2 (v_exp_f32, as the reference's fast-math exp2f), alpha < 1/255 skipped, stop at
-// T < 1e-4; stores the image, final T and last-contributor index per pixel and the per-tile maximum. No
-// per-bucket checkpoints.
+// T < 1e-4; stores the image, final T and last-contributor index per pixel and the per-tile maximum (an
+// inference render stores only the image, in CHW or HWC layout, optionally clamped). No per-bucket checkpoints.
 //
 // Backward: every pixel replays its forward walk (the evaluation below is shared and compiled with
 // -ffp-contract=off, so T and every skip decision are reproduced bit-exactly) and forms the reference's
@@ -156,11 +156,21 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
     const uint32_t slot = tile * tile_pixels + tid;
     if (inside) {
         const uint32_t pix = py * a.width + px;
-        const uint32_t np = a.width * a.height;
-        a.image[pix] = __builtin_fmaf(T, a.bg[0], cr);
-        a.image[np + pix] = __builtin_fmaf(T, a.bg[1], cg);
-        a.image[2 * np + pix] = __builtin_fmaf(T, a.bg[2], cb);
+        float c[3] = {__builtin_fmaf(T, a.bg[0], cr), __builtin_fmaf(T, a.bg[1], cg), __builtin_fmaf(T, a.bg[2], cb)};
+        if (a.clamp) {
+#pragma unroll
+            for (int k = 0; k < 3; k++) c[k] = fminf(fmaxf(c[k], 0.0f), 1.0f);
+        }
+        if (a.hwc) {
+#pragma unroll
+            for (int k = 0; k < 3; k++) a.image[3 * pix + k] = c[k];
+        } else {
+            const uint32_t np = a.width * a.height;
+#pragma unroll
+            for (int k = 0; k < 3; k++) a.image[k * np + pix] = c[k];
+        }
     }
+    if (!a.final_T) return;  // inference render: no backward state (uniform over the block)
     a.final_T[slot] = T;
     a.n_contrib[slot] = last;
     const uint32_t wm = wave_max_u32(last);

@@ -85,11 +85,13 @@ struct BlendForwardArgs {
     const uint32_t* inst_prim;     // primitive per emission index
     const PrimRecord* records;
     const float* bg;
-    float* image;                  // (3, H, W)
-    float* final_T;                // (tiles x 192)
+    float* image;                  // (3, H, W), or (H, W, 3) with hwc
+    float* final_T;                // (tiles x 192); null for an inference render (no backward state)
     uint32_t* n_contrib;           // (tiles x 192)
     uint32_t* tile_max;            // (tiles)
     uint32_t width, height, grid_w, n_tiles;
+    uint32_t hwc;                  // image layout (H, W, 3)
+    uint32_t clamp;                // image clamped to [0, 1] (NaN to 0)
 };
 bool launch_blend_forward(const BlendForwardArgs& a, hipStream_t s);
 

@@ -165,7 +165,7 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half, settings):
+def _check_inputs(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half) -> torch.device:
     device = means.device
     if device.type != 'cuda':
         raise ValueError('efgs: the rasterizer runs on a GPU device')
@@ -176,6 +176,11 @@ def _forward(means, scales, rotations, opacities, precomputed_colors, base_color
         expected = _rasterizer.mlp_param_count()
         if mlp_weights_half.numel() != expected or mlp_weights_half.device != device:
             raise ValueError(f'efgs: mlp_weights must hold {expected} parameters on {device}, got {mlp_weights_half.numel()}')
+    return device
+
+
+def _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half, settings):
+    device = _check_inputs(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
     with torch.cuda.device(device):
         cs, keep = _native_settings(settings, device)
         prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
@@ -272,17 +277,25 @@ def rasterize(means: torch.Tensor, scales: torch.Tensor, rotations: torch.Tensor
               rasterizer_settings: RasterizerSettings, to_chw: bool, clamp_output: bool,
               precomputed_colors: torch.Tensor | None = None, base_colors: torch.Tensor | None = None,
               residual_params: torch.Tensor | None = None, mlp_weights: torch.Tensor | None = None) -> torch.Tensor:
-    """Inference render: (3, H, W) if to_chw else (H, W, 3), optionally clamped to [0, 1]."""
+    """Inference render (B/torch_bindings/rasterization.py:198-224): (3, H, W) if to_chw else (H, W, 3),
+    clamped to [0, 1] if clamp_output; written in that layout by the blend kernel, no backward state."""
     d = means.device
     mlp_half = mlp_weights.detach().half().contiguous() if mlp_weights is not None else _empty(d, torch.float16)
-    image, _, _, _ = _forward(means, scales, rotations, opacities,
-                              precomputed_colors if precomputed_colors is not None else _empty(d),
-                              base_colors if base_colors is not None else _empty(d),
-                              residual_params if residual_params is not None else _empty(d),
-                              mlp_half, rasterizer_settings)
-    if clamp_output:
-        image = image.clamp_(0.0, 1.0)
-    return image if to_chw else image.permute(1, 2, 0).contiguous()
+    pre = precomputed_colors if precomputed_colors is not None else _empty(d)
+    base = base_colors if base_colors is not None else _empty(d)
+    res = residual_params if residual_params is not None else _empty(d)
+    device = _check_inputs(means, scales, rotations, opacities, pre, base, res, mlp_half)
+    h, w = int(rasterizer_settings.height), int(rasterizer_settings.width)
+    with torch.cuda.device(device):
+        cs, keep = _native_settings(rasterizer_settings, device)
+        prims = _native_primitives(means, scales, rotations, opacities, pre, base, res, mlp_half)
+        image = torch.empty((3, h, w) if to_chw else (h, w, 3), dtype=torch.float32, device=device)
+        alloc = _lib.WorkspaceAllocator(device, 'render')
+        check(lib.efgs_render(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), image.data_ptr(), int(bool(to_chw)),
+                              int(bool(clamp_output)), alloc.fn, alloc.ctx, _stream(device)))
+        alloc.done()
+    del keep
+    return image
 
 
 class _NeuralDecode(torch.autograd.Function):

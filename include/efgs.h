@@ -14,6 +14,7 @@
  *   Rasterizer.set_residual_mlp  B/rasterization/src/appearance.cu:181-201
  *   _C.forward ................. B/rasterization/src/rasterization_api.cu:16-123
  *   _C.backward ................ B/rasterization/src/rasterization_api.cu:125-247
+ *   _C.inference ............... B/rasterization/src/rasterization_api.cu:249-335
  *   _C.adam_step ............... B/adam/src/adam.cu:44-87
  *   _C.add_noise ............... B/densification/src/densification_api.cu:40-72
  *   _C.relocation_adjustment ... B/densification/src/densification_api.cu:13-38
@@ -136,6 +137,14 @@ typedef struct efgs_frame {
  * Replaces _C.forward, B/rasterization/src/rasterization_api.cu:16-123. */
 int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image,
                  efgs_alloc_fn alloc, void* alloc_ctx, efgs_frame* frame, void* stream);
+
+/* Inference render: the same pipeline without the backward state. image (device, fp32) is written 3 x H x W
+ * when to_chw != 0, else H x W x 3, clamped to [0, 1] (NaN to 0) when clamp_output != 0. Buffers come from
+ * `alloc` and are dead on return (stream-ordered). One blocking counter read, as efgs_forward.
+ * Replaces _C.inference, B/rasterization/src/rasterization_api.cu:249-335 (kernels
+ * B/rasterization/include/kernels_inference.cuh:11-126). */
+int efgs_render(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image, int to_chw, int clamp_output,
+                efgs_alloc_fn alloc, void* alloc_ctx, void* stream);
 
 typedef struct efgs_gradients {
     float* means;                 /* (N, 3) written */

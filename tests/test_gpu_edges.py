@@ -116,6 +116,8 @@ def test_fused_adam_matches_oracle_bitwise():
 
 
 def test_rasterize_inference_layouts():
+    """efgs_render writes CHW or HWC, clamped or not, in the blend kernel: every combination equals the oracle's
+    image (clamped to [0, 1] where asked) and, unclamped CHW, the training forward's image bit for bit."""
     import torch
     import efgs
     scene, app, cam = small_case(model='sh', n=500)
@@ -123,12 +125,33 @@ def test_rasterize_inference_layouts():
     configure(app)
     inp = torch_inputs(scene, dev)
     st = settings(cam, dev)
-    chw = efgs.rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], st, True, True,
-                         base_colors=inp['base_colors'], residual_params=inp['residual_params'])
-    hwc = efgs.rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], st, False, False,
-                         base_colors=inp['base_colors'], residual_params=inp['residual_params'])
     fw = O.render(scene, app, cam)
-    assert hwc.shape == (cam.height, cam.width, 3)
-    assert np.abs(hwc.cpu().numpy().transpose(2, 0, 1) - fw.image).max() <= 1e-4
-    assert np.abs(chw.cpu().numpy() - np.clip(fw.image, 0, 1)).max() <= 1e-4
-    assert rel_l2(chw.cpu().numpy(), np.clip(fw.image, 0, 1)) < 1e-5
+    imgs = {}
+    for to_chw in (True, False):
+        for clamp in (True, False):
+            img = efgs.rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], st, to_chw, clamp,
+                                 base_colors=inp['base_colors'], residual_params=inp['residual_params'])
+            assert img.shape == ((3, cam.height, cam.width) if to_chw else (cam.height, cam.width, 3))
+            got = img.cpu().numpy() if to_chw else img.cpu().numpy().transpose(2, 0, 1)
+            want = np.clip(fw.image, 0, 1) if clamp else fw.image
+            assert np.abs(got - want).max() <= 1e-4
+            imgs[(to_chw, clamp)] = got
+    assert np.array_equal(imgs[(True, False)], imgs[(False, False)]) and np.array_equal(imgs[(True, True)], imgs[(False, True)])
+    train = efgs.diff_rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], torch.empty(0, device=dev), st,
+                                base_colors=inp['base_colors'], residual_params=inp['residual_params'])
+    assert np.array_equal(train.detach().cpu().numpy(), imgs[(True, False)])
+
+
+def test_rasterize_neural_inference_matches_training_forward():
+    import torch
+    import efgs
+    scene, app, cam = small_case(model='neural', n=800)
+    dev = torch.device('cuda:0')
+    configure(app)
+    inp = torch_inputs(scene, dev)
+    st = settings(cam, dev)
+    hwc = efgs.rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], st, False, True,
+                         base_colors=inp['base_colors'], residual_params=inp['residual_params'], mlp_weights=inp['mlp_weights'])
+    train = efgs.diff_rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], torch.empty(0, device=dev), st,
+                                base_colors=inp['base_colors'], residual_params=inp['residual_params'], mlp_weights=inp['mlp_weights'])
+    assert np.array_equal(hwc.cpu().numpy(), np.clip(train.detach().cpu().numpy(), 0, 1).transpose(1, 2, 0))
