@@ -19,6 +19,7 @@ the same scene on the host.
   python bench.py [--steps K] [--warmup W] [--config c3|c1|c4_sv|c4_nasg|c4_nasgabor] [--no-cpu-baseline]
   python bench.py --config c2    # the neural decode alone: 1M primitives, forward + backward (latents, weights)
   python bench.py --config mcmc  # MCMC densification: add_noise and relocation_adjustment of the 1M c3 Gaussians
+  python bench.py --config pruning  # Speedy-Splat pruning scores of one c3 view
   python bench.py --copy-calibration    # a plain 1 GiB device copy, for scaling rocprofv3 FETCH/WRITE_SIZE
 """
 from __future__ import annotations
@@ -518,6 +519,48 @@ def mcmc_benchmark(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+# ---------------------------------------------------------------------------------------------------------
+# pruning: Speedy-Splat scores of one c3 view
+# ---------------------------------------------------------------------------------------------------------
+
+def pruning_benchmark(args) -> None:
+    """update_pruning_scores over the c3 scene's view (forward pipeline + score pass), HIP events per call."""
+    import torch
+    import efgs
+    device = torch.device('cuda:0')
+    torch.cuda.set_device(device)
+    sc, params, settings, _, _ = build_problem('c3', device)
+    n = sc['means'].shape[0]
+    W, H = sc['camera']['width'], sc['camera']['height']
+    scores = torch.zeros(n, dtype=torch.float32, device=device)
+
+    def call():
+        efgs.update_pruning_scores(scores, params['means'], params['scales'], params['rotations'], params['opacities'], settings,
+                                   base_colors=params['base_colors'], residual_params=params['residual_params'],
+                                   mlp_weights=params.get('mlp_weights'))
+
+    log(f'pruning: {n} Gaussians, {W}x{H}')
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            call()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+        for k in range(args.steps):
+            ev[k][0].record()
+            call()
+            ev[k][1].record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+    line = {
+        'metric': 'Speedy-Splat pruning scores Mpix/s @1M Gaussians 1080p (Neural)', 'value': round(W * H / (ms * 1e-3) / 1e6, 3),
+        'unit': 'Mpix/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(ms, 5), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32 (f16 MFMA MLP)', 'data': 'synthetic',
+        'config': {'workload': f'pruning: update_pruning_scores of one view of the c3 scene ({n} Gaussians, {W}x{H}, neural): '
+                               'forward pipeline + score pass', 'n_gaussians': n, 'width': W, 'height': H},
+        'roofline': None, 'cpu_baseline': None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def copy_calibration() -> None:
     """A plain device copy of 1 GiB, five times: rocprofv3 FETCH_SIZE / WRITE_SIZE of this command read
     1 GiB each per dispatch when the counters are exact."""
@@ -548,6 +591,9 @@ def main() -> None:
         return
     if args.config == 'mcmc':
         mcmc_benchmark(args)
+        return
+    if args.config == 'pruning':
+        pruning_benchmark(args)
         return
     r = gpu_benchmark(args)
     W, H = r['W'], r['H']

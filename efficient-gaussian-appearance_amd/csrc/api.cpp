@@ -920,6 +920,47 @@ int efgs_adam_step(const efgs_adam_group* groups, int n_groups, void* stream) {
     return EFGS_OK;
 }
 
+int efgs_update_pruning_scores(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* scores,
+                               efgs_alloc_fn alloc, void* alloc_ctx, void* stream) {
+    if (!r || !prims || !settings || !alloc || (prims->n_primitives > 0 && !scores)) return fail(EFGS_ERR_INVALID_ARGUMENT, "null argument");
+    if (settings->width <= 0 || settings->height <= 0 || settings->width > 65535 || settings->height > 65535)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "image size out of range");
+    const size_t image_bytes = static_cast<size_t>(settings->width) * static_cast<size_t>(settings->height) * 3 * sizeof(float);
+    float* image = static_cast<float*>(alloc(alloc_ctx, image_bytes));
+    if (!image) return fail(EFGS_ERR_ALLOC, "allocation of the score pass image failed");
+    efgs_frame frame;
+    if (int rc = forward_impl(r, prims, settings, image, alloc, alloc_ctx, &frame, false, false, stream)) return rc;
+    const uint32_t n = static_cast<uint32_t>(frame.n_primitives);
+    if (n == 0 || frame.n_instances == 0) return EFGS_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t grid_w = static_cast<uint32_t>(frame.grid_width), grid_h = static_cast<uint32_t>(frame.grid_height);
+    const uint32_t n_tiles = grid_w * grid_h;
+    const uint32_t n_instances = static_cast<uint32_t>(frame.n_instances);
+    const PrimitiveLayout pl = PrimitiveLayout::carve(static_cast<char*>(frame.primitive_buffers), n);
+    const TileLayout tl = TileLayout::carve(static_cast<char*>(frame.tile_buffers), n_tiles);
+    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame.instance_buffers), n_instances, frame.key_bytes, n_tiles);
+    float* inst_scores = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(n_instances) * sizeof(float)));
+    if (!inst_scores) return fail(EFGS_ERR_ALLOC, "allocation of the instance score buffer failed");
+    BlendBackwardArgs b;
+    std::memset(&b, 0, sizeof(b));
+    b.ranges = tl.ranges;
+    b.sorted_inst = il.sorted_inst;
+    b.inst_prim = il.inst_prim;
+    b.records = pl.records;
+    b.bg = settings->bg_color;
+    b.image = image;
+    b.final_T = tl.final_T;
+    b.n_contrib = tl.n_contrib;
+    b.tile_max = tl.tile_max;
+    b.inst_grads = inst_scores;
+    b.width = static_cast<uint32_t>(settings->width);
+    b.height = static_cast<uint32_t>(settings->height);
+    b.grid_w = grid_w;
+    b.n_tiles = n_tiles;
+    if (!launch_pruning_scores(b, pl.n_touched, pl.prim_offset, scores, n, s)) return EFGS_ERR_HIP;
+    return EFGS_OK;
+}
+
 int efgs_add_noise(int64_t n, const float* raw_scales, const float* raw_rotations, const float* raw_opacities, float* means, float current_lr,
                    uint64_t seed, uint64_t offset, void* stream) {
     if (n < 0 || n > static_cast<int64_t>(UINT32_MAX)) return fail(EFGS_ERR_INVALID_ARGUMENT, "primitive count out of range");

@@ -492,12 +492,153 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
     }
 }
 
+// Speedy-Splat pruning scores: per pixel and contributing Gaussian (o dL/dalpha)^2 for the upstream gradient
+// (1, 1, 1), with dL/dalpha formed as in the backward: T (c . 1) - (A - g_bg) / max(1 - alpha, eps), A = (colour
+// still to come) . 1, g_bg = -T_final (bg . 1). Same replay, 4x4 groups and lists as the backward; each group
+// walks two Gaussians per step and sums their scores over its 16 lanes with one two-value reduction; per batch
+// the twelve (wave, group) slots are added in a fixed order into one float per instance at its emission slot
+// (instances after every pixel's last contributor get 0). No atomics (the reference adds per pixel with float
+// atomics). Reference: B/rasterization/include/kernels_pruning_scores.cuh:11-171.
+__global__ __launch_bounds__(tile_pixels) void blend_scores_kernel(BlendBackwardArgs a) {
+    constexpr uint32_t n_waves = tile_pixels / 64;
+    constexpr uint32_t batch = 32;
+    constexpr uint32_t list_len = batch;
+    constexpr uint32_t n_slots = n_waves * 4;
+    __shared__ float4 s_stage[batch][3];  // (x, y, packed rect), exp2-scaled conic + opacity, colour
+    __shared__ uint32_t s_emit[batch];
+    __shared__ uint32_t s_list[n_waves][4][list_len];
+    __shared__ float s_part[n_slots][batch + 1];
+
+    const uint32_t tile = blockIdx.x;
+    const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t g = (lane >> 2) & 3u;
+    const uint32_t px = tx * tile_width + (lane & 15u);
+    const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);
+    const bool inside = px < a.width && py < a.height;
+    const float pxf = static_cast<float>(px) + 0.5f, pyf = static_cast<float>(py) + 0.5f;
+    const uint32_t bx0 = tx * tile_width;
+    const uint32_t by0 = ty * tile_height + wave * 4u, by1 = by0 + 4u;
+    const uint2 range = a.ranges[tile];
+    const uint32_t n_total = range.y - range.x;
+    const uint32_t n_proc = min(n_total, a.tile_max[tile]);
+    const uint32_t* const my_list = &s_list[wave][g][0];
+    for (uint32_t k = tid; k < n_waves * 4 * list_len; k += tile_pixels) (&s_list[0][0][0])[k] = 0;
+    for (uint32_t k = tid; k < n_slots * (batch + 1); k += tile_pixels) (&s_part[0][0])[k] = 0.0f;
+    // group_reduce2 leaves Gaussian a's sum in rows 0, 1 and b's in rows 2, 3: lane 4g of rows 0 and 2 store
+    const uint32_t row = lane >> 4;
+    const bool store_lane = (lane & 3u) == 0 && (row == 0 || row == 2);
+    const uint32_t store_b = row == 2 ? 1u : 0u;
+    float* const slot = &s_part[wave * 4u + g][0];
+
+    float A = 0.0f, gbg = 0.0f;
+    uint32_t last = 0;
+    if (inside) {
+        const uint32_t pix = py * a.width + px;
+        const uint32_t np = a.width * a.height;
+        const uint32_t pslot = tile * tile_pixels + tid;
+        const float Tf = a.final_T[pslot];
+        last = a.n_contrib[pslot];
+        A = (a.image[pix] - Tf * a.bg[0]) + (a.image[np + pix] - Tf * a.bg[1]) + (a.image[2 * np + pix] - Tf * a.bg[2]);
+        gbg = Tf * -(a.bg[0] + a.bg[1] + a.bg[2]);
+    }
+    const uint32_t wave_last = wave_max_u32(last);
+    float T = 1.0f;
+
+    uint32_t covered = 0;
+    for (uint32_t start = 0; start < n_proc; start += batch) {
+        __syncthreads();  // the previous batch's combine has read the stage and cleared the slots
+        if (tid < batch && start + tid < n_total) {
+            const uint32_t e = a.sorted_inst[range.x + start + tid];
+            const PrimRecord rec = a.records[a.inst_prim[e]];
+            s_stage[tid][0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
+            s_stage[tid][1] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
+            s_stage[tid][2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
+            s_emit[tid] = e;
+        }
+        __syncthreads();
+        const uint32_t batch_wave = wave_last > start ? min(min(batch, n_proc - start), wave_last - start) : 0u;
+        uint64_t m[4];
+        cull_groups(rect_of(s_stage[lane & (batch - 1)][0]), lane < batch_wave, bx0, by0, by1, m);
+        uint32_t n[4];
+        build_group_lists(m, lane, 0u, &s_list[wave][0][0], list_len, n);
+        wave_lds_fence();
+        const uint32_t n_max = __builtin_amdgcn_readfirstlane(max(max(n[0], n[1]), max(n[2], n[3])));
+        const uint32_t my_n = pick_group(g, n[0], n[1], n[2], n[3]);
+        const uint32_t n_store = store_lane && my_n > store_b ? my_n - store_b : 0u;
+        const uint32_t last_rel = last > start ? last - start : 0u;
+        for (uint32_t k = 0; k < n_max; k += 2) {
+            const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);  // past the count: stale, skipped
+            float sc[2];
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) {
+                const uint32_t j = h ? jab.y : jab.x;
+                float dx, dy, G;
+                const float4 co = s_stage[j][1];
+                const float alpha = eval_alpha(s_stage[j][0], co, pxf, pyf, dx, dy, G);
+                const bool contrib = k + h < my_n && j < last_rel && alpha >= min_alpha;
+                const float ae = contrib ? alpha : 0.0f;
+                const float4 col = s_stage[j][2];
+                const float cg = col.x + col.y + col.z;
+                const float oma = 1.0f - ae;
+                const float rcp = __builtin_amdgcn_rcpf(fmaxf(oma, one_minus_alpha_eps));
+                A = __builtin_fmaf(-T * ae, cg, A);
+                const float dg = co.w * __builtin_fmaf(T, cg, -rcp * (A - gbg));
+                sc[h] = contrib ? dg * dg : 0.0f;
+                T = T * oma;
+            }
+            const float sx = group_reduce2(sc[0], sc[1]);
+            if (k < n_store) slot[store_b ? jab.y : jab.x] = sx;
+        }
+        wave_lds_fence();
+        __syncthreads();  // every group's sums are in its slots
+        const uint32_t batch_n = min(batch, n_total - start);
+        if (tid < batch_n) {
+            float acc = 0.0f;
+#pragma unroll
+            for (uint32_t q = 0; q < n_slots; q++) {
+                acc += s_part[q][tid];
+                s_part[q][tid] = 0.0f;
+            }
+            a.inst_grads[s_emit[tid]] = acc;
+        }
+        covered = min(n_total, start + batch);
+    }
+    for (uint32_t k = covered + tid; k < n_total; k += tile_pixels) a.inst_grads[a.sorted_inst[range.x + k]] = 0.0f;
+}
+
+// scores[p] += the primitive's per-instance scores, in emission order (contiguous slots from prim_offset)
+__global__ __launch_bounds__(256) void accumulate_scores_kernel(const uint32_t* n_touched, const uint32_t* prim_offset, const float* inst_scores,
+                                                               float* scores, uint32_t n) {
+    const uint32_t p = blockIdx.x * 256u + threadIdx.x;
+    if (p >= n) return;
+    const uint32_t touched = n_touched[p];
+    if (touched == 0) return;
+    const float* src = inst_scores + prim_offset[p];
+    float sum = 0.0f;
+    for (uint32_t k = 0; k < touched; k++) sum += src[k];
+    scores[p] += sum;
+}
+
 }  // namespace
 
 bool launch_blend_forward(const BlendForwardArgs& a, hipStream_t s) {
     if (a.n_tiles == 0) return true;
     blend_forward_kernel<<<a.n_tiles, tile_pixels, 0, s>>>(a);
     EFGS_HIP_CHECK(hipGetLastError());
+    return true;
+}
+
+bool launch_pruning_scores(const BlendBackwardArgs& a, const uint32_t* n_touched, const uint32_t* prim_offset, float* scores, uint32_t n,
+                           hipStream_t s) {
+    if (a.n_tiles > 0) {
+        blend_scores_kernel<<<a.n_tiles, tile_pixels, 0, s>>>(a);
+        EFGS_HIP_CHECK(hipGetLastError());
+    }
+    if (n > 0) {
+        accumulate_scores_kernel<<<div_up(n, 256), 256, 0, s>>>(n_touched, prim_offset, a.inst_grads, scores, n);
+        EFGS_HIP_CHECK(hipGetLastError());
+    }
     return true;
 }
 

@@ -106,11 +106,15 @@ struct BlendBackwardArgs {
     const float* final_T;
     const uint32_t* n_contrib;
     const uint32_t* tile_max;
-    float* inst_grads;             // (I x 12), emission order
+    float* inst_grads;             // (I x 12), emission order (pruning scores: one float per instance)
     uint32_t width, height, grid_w, n_tiles;
     uint32_t abs_grads;            // also reduce |dL/dmean2d| (third densification row)
 };
 bool launch_blend_backward(const BlendBackwardArgs& a, hipStream_t s);
+// pruning scores of the frame in `a` (grad_image unused): per-instance scores into a.inst_grads, then
+// scores[p] += their per-primitive sums
+bool launch_pruning_scores(const BlendBackwardArgs& a, const uint32_t* n_touched, const uint32_t* prim_offset, float* scores, uint32_t n,
+                           hipStream_t s);
 
 // ---- adam ---------------------------------------------------------------------------------------------------
 constexpr int adam_max_lrs = 7;

@@ -354,9 +354,29 @@ def neural_decode(features: torch.Tensor, dirs: torch.Tensor, mlp_weights: torch
     return _NeuralDecode.apply(features, dirs, mlp_weights, base, degree)
 
 
-def update_pruning_scores(*args, **kwargs):
-    """Speedy-Splat pruning scores are not part of this build (reference: kernels_pruning_scores.cuh)."""
-    raise NotImplementedError('efgs: update_pruning_scores is not implemented in this build')
+@torch.no_grad()
+def update_pruning_scores(scores: torch.Tensor, means: torch.Tensor, scales: torch.Tensor, rotations: torch.Tensor,
+                          opacities: torch.Tensor, rasterizer_settings: RasterizerSettings,
+                          precomputed_colors: torch.Tensor | None = None, base_colors: torch.Tensor | None = None,
+                          residual_params: torch.Tensor | None = None, mlp_weights: torch.Tensor | None = None) -> None:
+    """Speedy-Splat pruning scores of one view (B/torch_bindings/rasterization.py:226-250): scores (N,) float32
+    += per Gaussian the sum over the view's pixels of (o dL/dalpha)^2 for an all-ones image gradient, in place."""
+    d = means.device
+    mlp_half = mlp_weights.detach().half().contiguous() if mlp_weights is not None else _empty(d, torch.float16)
+    pre = precomputed_colors if precomputed_colors is not None else _empty(d)
+    base = base_colors if base_colors is not None else _empty(d)
+    res = residual_params if residual_params is not None else _empty(d)
+    device = _check_inputs(means, scales, rotations, opacities, pre, base, res, mlp_half)
+    if scores.dtype != torch.float32 or scores.device != device or not scores.is_contiguous() or scores.numel() != means.shape[0]:
+        raise ValueError('efgs: scores must be a contiguous float32 tensor of N entries on the rendering device')
+    with torch.cuda.device(device):
+        cs, keep = _native_settings(rasterizer_settings, device)
+        prims = _native_primitives(means, scales, rotations, opacities, pre, base, res, mlp_half)
+        alloc = _lib.WorkspaceAllocator(device, 'scores')
+        check(lib.efgs_update_pruning_scores(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), scores.data_ptr(), alloc.fn,
+                                             alloc.ctx, _stream(device)))
+        alloc.done()
+    del keep
 
 
 def frame_views(frame: _lib.Frame) -> _lib.FrameViews:

@@ -15,6 +15,7 @@
  *   _C.forward ................. B/rasterization/src/rasterization_api.cu:16-123
  *   _C.backward ................ B/rasterization/src/rasterization_api.cu:125-247
  *   _C.inference ............... B/rasterization/src/rasterization_api.cu:249-335
+ *   _C.pruning_scores .......... B/rasterization/src/rasterization_api.cu:337-415
  *   _C.adam_step ............... B/adam/src/adam.cu:44-87
  *   _C.add_noise ............... B/densification/src/densification_api.cu:40-72
  *   _C.relocation_adjustment ... B/densification/src/densification_api.cu:13-38
@@ -182,6 +183,15 @@ typedef struct efgs_adam_group {
     double beta1, beta2, eps;
 } efgs_adam_group;
 int efgs_adam_step(const efgs_adam_group* groups, int n_groups, void* stream);
+
+/* Speedy-Splat pruning scores of one view: scores (device, n_primitives fp32) += per primitive the sum over the
+ * view's pixels of (o dL/dalpha)^2 for the upstream gradient (1, 1, 1) (o the projected opacity; alpha, the
+ * skips and the stop as in the forward). Runs the forward pipeline into a scratch image from `alloc`, then the
+ * score pass; one blocking counter read, as efgs_forward. Deterministic (fixed summation order).
+ * Replaces _C.pruning_scores, B/rasterization/src/rasterization_api.cu:337-415 (kernels
+ * B/rasterization/include/kernels_pruning_scores.cuh:11-171, B/rasterization/src/pruning_scores.cu:11-204). */
+int efgs_update_pruning_scores(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* scores,
+                               efgs_alloc_fn alloc, void* alloc_ctx, void* stream);
 
 /* MCMC noise (3DGS-MCMC): means (n x 3) += current_lr * sigmoid(-(100 sigmoid(raw_opacity) - 0.5)) * Sigma z in
  * place, Sigma from the log-scales (n x 3) and the unnormalised quaternions (n x 4, w x y z; |q|^2 < 1e-8 leaves

@@ -1162,3 +1162,53 @@ void efo_relocation(int n, const float* old_opacities, const float* old_scales, 
         for (int a = 0; a < 3; a++) new_scales[3 * i + a] = factor * old_scales[3 * i + a];
     }
 }
+
+/* ------------------------------------------------------------------------------------------------------ */
+/* pruning scores (Speedy-Splat), B/rasterization/include/kernels_pruning_scores.cuh:11-171               */
+/* ------------------------------------------------------------------------------------------------------ */
+
+/* scores[p] += sum over pixels of (o_p dL/dalpha_p)^2 for the upstream gradient (1, 1, 1): the second pass of
+   the reference replays each pixel's walk with the colour still to come and the final transmittance of the
+   first (here: the forward's image, final T and last contributor). Accumulated in pixel order. */
+void efo_pruning_scores(
+    int width, int height, int grid_w, int grid_h, const uint32_t* ranges, const uint32_t* inst_prims,
+    const float* mean2d, const float* conic_opacity, const float* color, const float* bg,
+    const float* image, const float* final_T, const uint32_t* n_contrib, float* scores)
+{
+    const float log2e = 1.44269504089f;
+    const int n_pixels = width * height;
+    for (int ty = 0; ty < grid_h; ty++) for (int tx = 0; tx < grid_w; tx++) {
+        const uint32_t t = (uint32_t)(ty * grid_w + tx);
+        const uint32_t r0 = ranges[2 * t];
+        for (int ly = 0; ly < EFO_TILE_H; ly++) for (int lx = 0; lx < EFO_TILE_W; lx++) {
+            const int px = tx * EFO_TILE_W + lx, py = ty * EFO_TILE_H + ly;
+            if (px >= width || py >= height) continue;
+            const int pix = py * width + px;
+            const float pxf = (float)px + 0.5f, pyf = (float)py + 0.5f;
+            const float Tf = final_T[pix];
+            float after[3];
+            for (int c = 0; c < 3; c++) after[c] = image[c * n_pixels + pix] - Tf * bg[c];
+            const float grad_alpha_common = Tf * -(bg[0] + bg[1] + bg[2]);
+            float T = 1.0f;
+            const uint32_t last = n_contrib[pix];
+            for (uint32_t k = 0; k < last; k++) {
+                const uint32_t p = inst_prims[r0 + k];
+                const float* co = conic_opacity + 4 * p;
+                const float ex = -0.5f * log2e * co[0], ey = -log2e * co[1], ez = -0.5f * log2e * co[2];
+                const float dx = mean2d[2 * p] - pxf, dy = mean2d[2 * p + 1] - pyf;
+                const float G = ef_exp2f(fminf(blend_exponent(ex, ey, ez, dx, dy), 0.0f));
+                const float alpha = co[3] * G;
+                if (alpha < K_MIN_ALPHA) continue;
+                const float* col = color + 3 * p;
+                for (int c = 0; c < 3; c++) after[c] -= T * alpha * col[c];
+                const float oma = 1.0f - alpha;
+                const float rcp = 1.0f / fmaxf(oma, k_one_minus_alpha_eps);
+                const float dalpha = (T * col[0] - after[0] * rcp) + (T * col[1] - after[1] * rcp) + (T * col[2] - after[2] * rcp) +
+                                     grad_alpha_common * rcp;
+                const float dg = co[3] * dalpha;
+                scores[p] += dg * dg;
+                T *= oma;
+            }
+        }
+    }
+}

@@ -81,6 +81,7 @@ def lib() -> ctypes.CDLL:
         _lib.efo_add_noise.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64]
         _lib.efo_relocation_table.argtypes = [ctypes.c_void_p]
         _lib.efo_relocation.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5
+        _lib.efo_pruning_scores.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 10
     return _lib
 
 
@@ -750,3 +751,19 @@ def relocation_adjustment(old_opacities, old_scales, n_samples) -> tuple[np.ndar
     new_s = np.zeros((n, 3), np.float32)
     lib().efo_relocation(n, _p(o), _p(s), _p(c), _p(new_o), _p(new_s))
     return new_o, new_s
+
+
+# ---------------------------------------------------------------------------------------------------------
+# pruning scores (Speedy-Splat), B/rasterization/include/kernels_pruning_scores.cuh:11-171
+# ---------------------------------------------------------------------------------------------------------
+
+def pruning_scores(cam: Camera, fw: ForwardState, scores: np.ndarray | None = None) -> np.ndarray:
+    """scores (n,) plus, per primitive, the sum over pixels of (o dL/dalpha)^2 for the upstream gradient
+    (1, 1, 1), from a forward state of `render`."""
+    n = fw.n_touched.shape[0]
+    out = np.zeros(n, np.float32) if scores is None else _f32(scores).copy()
+    gw, gh = cam.grid()
+    lib().efo_pruning_scores(cam.width, cam.height, gw, gh, _p(fw.ranges), _p(np.ascontiguousarray(fw.inst_prims)), _p(fw.mean2d),
+                             _p(fw.conic_opacity), _p(fw.color), _p(_f32(cam.bg)), _p(fw.image), _p(fw.final_T), _p(fw.n_contrib),
+                             _p(out))
+    return out

@@ -408,3 +408,90 @@ def test_relocation_closed_forms():
     cc = rng.integers(1, 51, 500)
     no, _ = O.relocation_adjustment(oo, np.ones((500, 3), np.float32), cc)
     np.testing.assert_allclose(1.0 - (1.0 - no[:, 0].astype(np.float64)) ** cc, oo, rtol=3e-4)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# pruning scores (B/rasterization/include/kernels_pruning_scores.cuh:11-171)
+# ---------------------------------------------------------------------------------------------------------
+
+def _single_tile_state(mean2d, conic_opacity, color, bg):
+    """Forward state of one 16 x 12 tile whose instances are the given 2D Gaussians in order."""
+    import ctypes
+    from types import SimpleNamespace
+    k = mean2d.shape[0]
+    W, H = 16, 12
+    ranges = np.array([0, k], np.uint32)
+    inst = np.arange(k, dtype=np.uint32)
+    bounds = np.tile(np.array([0, W, 0, H], np.uint16), (k, 1))
+    image = np.zeros((3, H, W), np.float32)
+    final_T = np.zeros(H * W, np.float32)
+    n_contrib = np.zeros(H * W, np.uint32)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    O.lib().efo_blend_forward(ctypes.c_int(W), ctypes.c_int(H), ctypes.c_int(1), ctypes.c_int(1), p(ranges), p(inst), p(bounds), p(mean2d),
+                              p(conic_opacity), p(color), p(bg), p(image), p(final_T), p(n_contrib))
+    cam = SimpleNamespace(width=W, height=H, bg=bg, grid=lambda: (1, 1))
+    fw = SimpleNamespace(n_touched=np.ones(k, np.uint32), ranges=ranges, inst_prims=inst, mean2d=mean2d, conic_opacity=conic_opacity,
+                         color=color, image=image, final_T=final_T, n_contrib=n_contrib)
+    return cam, fw
+
+
+def _random_2d_gaussians(rng, k):
+    mean2d = rng.uniform([1.0, 1.0], [15.0, 11.0], (k, 2)).astype(np.float32)
+    co = np.zeros((k, 4), np.float32)
+    for i in range(k):
+        a = rng.normal(size=(2, 2))
+        cov = a @ a.T * 4.0 + np.eye(2) * 1.5
+        inv = np.linalg.inv(cov)
+        co[i] = [inv[0, 0], inv[0, 1], inv[1, 1], rng.uniform(0.3, 0.95)]
+    color = rng.uniform(0.0, 1.0, (k, 3)).astype(np.float32)
+    return mean2d, co, color
+
+
+def test_pruning_scores_match_autograd():
+    """The score of a Gaussian is sum over pixels of (dL/dG)^2 (alpha = o G, so o dL/dalpha = dL/dG) for
+    L = sum of the image: autograd through a float64 front-to-back composite of per-pixel Gaussian values,
+    with the float32 walk's skip (alpha < 1/255) and stop (last contributor) decisions."""
+    rng = np.random.default_rng(21)
+    k = 6
+    mean2d, co, color = _random_2d_gaussians(rng, k)
+    bg = np.array([0.2, 0.5, 0.1], np.float32)
+    cam, fw = _single_tile_state(mean2d, co, color, bg)
+    got = O.pruning_scores(cam, fw)
+    log2e = 1.44269504089
+    ys, xs = np.mgrid[0:12, 0:16]
+    px, py = xs.reshape(-1) + 0.5, ys.reshape(-1) + 0.5
+    G = np.zeros((k, px.size))
+    for i in range(k):
+        dx, dy = mean2d[i, 0] - px, mean2d[i, 1] - py
+        q = -0.5 * log2e * (co[i, 0] * dx * dx + 2 * co[i, 1] * dx * dy + co[i, 2] * dy * dy)
+        G[i] = np.exp2(np.minimum(q, 0.0))
+    Gt = torch.tensor(G, dtype=torch.float64, requires_grad=True)
+    total = torch.zeros((), dtype=torch.float64)
+    for pix in range(px.size):
+        T = torch.ones((), dtype=torch.float64)
+        for i in range(int(fw.n_contrib[pix])):
+            a32 = np.float32(co[i, 3]) * np.float32(G[i, pix])
+            if a32 < 1.0 / 255.0:
+                continue
+            alpha = float(co[i, 3]) * Gt[i, pix]
+            total = total + T * alpha * float(color[i].sum())
+            T = T * (1 - alpha)
+        total = total + T * float(bg.sum())
+    total.backward()
+    want = (Gt.grad.numpy() ** 2).sum(1)
+    np.testing.assert_allclose(got, want, rtol=2e-4)
+
+
+def test_pruning_score_single_gaussian_closed_form():
+    """One Gaussian over the tile: the colour still to come after it is zero and T_final = 1 - alpha, so every
+    pixel it reaches scores (o (sum c - sum bg))^2, whatever its Gaussian value."""
+    mean2d = np.array([[8.0, 6.0]], np.float32)
+    co = np.array([[0.3, 0.02, 0.4, 0.7]], np.float32)
+    color = np.array([[0.9, 0.4, 0.3]], np.float32)
+    bg = np.array([0.1, 0.2, 0.3], np.float32)
+    cam, fw = _single_tile_state(mean2d, co, color, bg)
+    n_pix = int((fw.n_contrib == 1).sum())
+    assert 0 < n_pix < 192
+    got = O.pruning_scores(cam, fw)
+    want = n_pix * (0.7 * (color.sum() - bg.sum())) ** 2
+    np.testing.assert_allclose(got, [want], rtol=1e-5)
