@@ -256,8 +256,8 @@ __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOM
 
 // Per-tile sort: one wave per tile, four tiles per block, no block barriers. Keys are unique 64-bit values
 // (depth key << 32 | emission index), sorted ascending by bitonic networks:
-//   n <= 256          in registers, four keys per lane (element x = 4 lane + i): exchanges at distance
-//                     j < 4 within a lane, j >= 4 with the lane at xor distance j / 4;
+//   n <= 64, 128, 256 in registers, K = 1, 2, 4 keys per lane (element x = K lane + i): exchanges at distance
+//                     j < K within a lane, j >= K with the lane at xor distance j / K;
 //   256 < n <= 512    in the wave's LDS slab;
 //   n > 512           chunks of 512 sorted in the slab and written back to the tile's range, then every key
 //                     placed at (its index in its chunk) + (its rank in each other chunk).
@@ -271,30 +271,51 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, uint32_t d) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-__device__ __forceinline__ void wave_bitonic_256(uint64_t (&k)[4], uint32_t lane) {
+template <uint32_t K>
+__device__ __forceinline__ void wave_bitonic(uint64_t (&k)[K], uint32_t lane) {
 #pragma unroll
-    for (uint32_t size = 2; size <= 256; size <<= 1) {
+    for (uint32_t size = 2; size <= 64 * K; size <<= 1) {
 #pragma unroll
         for (uint32_t j = size >> 1; j > 0; j >>= 1) {
-            if (j >= 4) {
+            if (j >= K) {
 #pragma unroll
-                for (uint32_t i = 0; i < 4; i++) {
-                    const uint32_t x = 4u * lane + i;
-                    const uint64_t o = shfl_xor_u64(k[i], j >> 2);
+                for (uint32_t i = 0; i < K; i++) {
+                    const uint32_t x = K * lane + i;
+                    const uint64_t o = shfl_xor_u64(k[i], j / K);
                     const bool keep_min = ((x & size) == 0) == ((x & j) == 0);
                     k[i] = keep_min ? (k[i] < o ? k[i] : o) : (k[i] < o ? o : k[i]);
                 }
             } else {
 #pragma unroll
-                for (uint32_t i = 0; i < 4; i++) {
+                for (uint32_t i = 0; i < K; i++) {
                     if ((i & j) != 0) continue;
-                    const uint32_t x = 4u * lane + i;
+                    const uint32_t x = K * lane + i;
                     const uint64_t a = k[i], b = k[i ^ j];
                     const bool swap = (a > b) == ((x & size) == 0);
                     k[i] = swap ? b : a;
                     k[i ^ j] = swap ? a : b;
                 }
             }
+        }
+    }
+}
+
+// n <= 64 K keys of the tile's run, sorted in registers (K keys per lane, element x = K lane + i), written out
+template <uint32_t K, typename KeyT>
+__device__ __forceinline__ void sort_run_in_registers(const uint64_t* run, uint32_t n, uint32_t* out, KeyT* out_keys, uint32_t tile, uint32_t lane) {
+    uint64_t k[K];
+#pragma unroll
+    for (uint32_t i = 0; i < K; i++) {
+        const uint32_t x = K * lane + i;
+        k[i] = x < n ? run[x] : ~0ull;
+    }
+    wave_bitonic<K>(k, lane);
+#pragma unroll
+    for (uint32_t i = 0; i < K; i++) {
+        const uint32_t x = K * lane + i;
+        if (x < n) {
+            out[x] = static_cast<uint32_t>(k[i]);
+            out_keys[x] = static_cast<KeyT>(tile);
         }
     }
 }
@@ -344,22 +365,16 @@ __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32
     uint64_t* run = bucket + r.x;
     uint32_t* out = sorted_inst + r.x;
     KeyT* out_keys = sorted_keys + r.x;
+    if (n <= 64) {  // wave-uniform size classes: the smallest network that holds the run
+        sort_run_in_registers<1>(run, n, out, out_keys, tile, lane);
+        return;
+    }
+    if (n <= 128) {
+        sort_run_in_registers<2>(run, n, out, out_keys, tile, lane);
+        return;
+    }
     if (n <= 256) {
-        uint64_t k[4];
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
-            const uint32_t x = 4u * lane + i;
-            k[i] = x < n ? run[x] : ~0ull;
-        }
-        wave_bitonic_256(k, lane);
-#pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
-            const uint32_t x = 4u * lane + i;
-            if (x < n) {
-                out[x] = static_cast<uint32_t>(k[i]);
-                out_keys[x] = static_cast<KeyT>(tile);
-            }
-        }
+        sort_run_in_registers<4>(run, n, out, out_keys, tile, lane);
         return;
     }
     uint64_t* s = s_slab[wave];
