@@ -25,6 +25,7 @@ SOURCES = [
     ('blend.hip', ['-ffp-contract=off']),
     ('adam.hip', ['-ffp-contract=off']),
     ('densification.hip', ['-ffp-contract=off']),
+    ('ngsplat.hip', ['-ffp-contract=off']),
 ]
 
 COMMON = ['-O3', '-std=c++17', '-fPIC', '-fhip-fp32-correctly-rounded-divide-sqrt',

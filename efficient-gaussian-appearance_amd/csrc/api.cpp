@@ -1117,4 +1117,149 @@ int efgs_precompile(const efgs_rasterizer* r, const char* arch) {
     return EFGS_OK;
 }
 
+// ---- .ngsplat packing ------------------------------------------------------------------------------------------------
+
+namespace {
+
+struct NgsplatPlan {
+    int payload, n_items, n_values, n_encoded, row_used, n_textures;
+    uint32_t texel_words[ng_max_textures];
+};
+
+int ngsplat_plan(const efgs_ngsplat_input* in, NgsplatPlan& p) {
+    if (!in) return fail(EFGS_ERR_INVALID_ARGUMENT, "null ngsplat input");
+    p.payload = in->payload;
+    p.n_items = in->n_items;
+    p.n_encoded = 0;
+    switch (in->payload) {
+    case EFGS_NGSPLAT_NEURAL_FEATURES:
+    case EFGS_NGSPLAT_NEURAL_BAKED: {
+        if (in->n_items < 0 || in->n_frequencies < 0 || in->n_frequencies > 16) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid neural feature layout");
+        const int raw = in->n_items + (in->base_input ? 3 : 0);
+        p.n_encoded = raw * (in->n_frequencies ? 2 * in->n_frequencies : 1);
+        p.row_used = in->n_items;
+        if (in->payload == EFGS_NGSPLAT_NEURAL_FEATURES) {
+            if (p.n_encoded < 1 || p.n_encoded > 16) return fail(EFGS_ERR_INVALID_ARGUMENT, "stored neural features need 1..16 encoded dims");
+            p.n_values = p.n_encoded;
+        } else {
+            if (in->n_neurons < 1 || in->n_neurons > static_cast<int>(ng_max_baked))
+                return fail(EFGS_ERR_INVALID_ARGUMENT, "a baked layer 0 needs 1..16 neurons");
+            if (p.n_encoded < 1) return fail(EFGS_ERR_INVALID_ARGUMENT, "a baked layer 0 needs encoded features");
+            p.n_values = in->n_neurons;
+        }
+        break;
+    }
+    case EFGS_NGSPLAT_SH:
+        if (in->n_items != 0 && in->n_items != 3 && in->n_items != 8 && in->n_items != 15)
+            return fail(EFGS_ERR_INVALID_ARGUMENT, "SH export needs 0, 3, 8 or 15 coefficients (degrees up to 3)");
+        p.row_used = 3 * in->n_items;
+        p.n_values = 0;
+        break;
+    case EFGS_NGSPLAT_SV:
+        if (in->n_items < 0 || in->n_items > 9) return fail(EFGS_ERR_INVALID_ARGUMENT, "SV export needs at most 9 sites (64 fp16 values)");
+        p.row_used = 7 * in->n_items;
+        p.n_values = 7 * in->n_items;
+        break;
+    case EFGS_NGSPLAT_NASG:
+        if (in->n_items < 0 || in->n_items > 5) return fail(EFGS_ERR_INVALID_ARGUMENT, "NASG export needs at most 5 lobes (64 fp16 values)");
+        p.row_used = 8 * in->n_items;
+        p.n_values = 12 * in->n_items;
+        break;
+    case EFGS_NGSPLAT_NASGABOR:
+        if (in->n_items < 0 || in->n_items > 4) return fail(EFGS_ERR_INVALID_ARGUMENT, "NASGabor export needs at most 4 lobes (64 fp16 values)");
+        p.row_used = 9 * in->n_items;
+        p.n_values = 13 * in->n_items;
+        break;
+    default: return fail(EFGS_ERR_INVALID_ARGUMENT, "unknown ngsplat payload");
+    }
+    if (p.row_used > static_cast<int>(ng_max_row)) return fail(EFGS_ERR_INVALID_ARGUMENT, "more than 63 residual parameters per splat");
+    if (p.row_used > in->residual_row_stride) return fail(EFGS_ERR_INVALID_ARGUMENT, "residual row stride smaller than the parameters read");
+    if (in->residual_act < 0 || in->residual_act > 2) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid residual activation");
+    p.n_textures = ngsplat_texture_plan(p.payload, p.n_items, p.n_values, p.texel_words);
+    return EFGS_OK;
+}
+
+}  // namespace
+
+int efgs_ngsplat_layout(const efgs_ngsplat_input* in, int* n_textures, int* texel_words) {
+    NgsplatPlan p;
+    if (int rc = ngsplat_plan(in, p)) return rc;
+    if (!n_textures || !texel_words) return fail(EFGS_ERR_INVALID_ARGUMENT, "null output");
+    *n_textures = p.n_textures;
+    for (int k = 0; k < static_cast<int>(ng_max_textures); k++) texel_words[k] = k < p.n_textures ? static_cast<int>(p.texel_words[k]) : 0;
+    return EFGS_OK;
+}
+
+int efgs_ngsplat_pack(const efgs_ngsplat_input* in, efgs_ngsplat_output* out, efgs_alloc_fn alloc, void* alloc_ctx, void* stream) {
+    NgsplatPlan p;
+    if (int rc = ngsplat_plan(in, p)) return rc;
+    if (!out || !alloc) return fail(EFGS_ERR_INVALID_ARGUMENT, "null output or allocator");
+    if (in->n < 0 || in->n > (int64_t{1} << 31)) return fail(EFGS_ERR_INVALID_ARGUMENT, "splat count out of range");
+    if (out->capacity < in->n || out->capacity % ng_tex_width != 0 || out->capacity > (int64_t{1} << 31))
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "output capacity must be a multiple of 2048 rows and hold every splat");
+    if (out->capacity > 0 && (!out->splat_words || (p.n_textures > 0 && !out->params)))
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "null output texture");
+    if (in->n > 0 && (!in->means || !in->raw_scales || !in->raw_rotations || !in->raw_opacities || !in->base_colors ||
+                      (p.row_used > 0 && !in->residual_params)))
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "null tensor");
+    if (p.payload == EFGS_NGSPLAT_NEURAL_BAKED && !in->bake_matrix) return fail(EFGS_ERR_INVALID_ARGUMENT, "null layer-0 bake matrix");
+    if ((reinterpret_cast<uintptr_t>(out->splat_words) | reinterpret_cast<uintptr_t>(out->params)) % 16 != 0)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "output textures must be 16-byte aligned");
+    out->n_kept = 0;
+    out->base_offset = 0.0f;
+    out->base_scale = static_cast<float>(1e-6 / 255.0);
+    for (int l = 0; l < 3; l++) out->sh_level_scale[l] = 0.0f;
+    if (out->capacity == 0) return EFGS_OK;
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t capacity = static_cast<uint32_t>(out->capacity);
+    const size_t partial_bytes = static_cast<size_t>(capacity / ng_block) * 8 * sizeof(uint32_t);
+    char* blob = static_cast<char*>(alloc(alloc_ctx, partial_bytes + 256));
+    if (!blob) return fail(EFGS_ERR_ALLOC, "allocation of the ngsplat partials failed");
+    NgsplatArgs a{};
+    a.means = in->means;
+    a.raw_scales = in->raw_scales;
+    a.raw_rotations = in->raw_rotations;
+    a.raw_opacities = in->raw_opacities;
+    a.base_colors = in->base_colors;
+    a.residual_params = in->residual_params;
+    a.bake_matrix = in->bake_matrix;
+    a.bake_bias = in->bake_bias;
+    a.n = static_cast<uint32_t>(in->n);
+    a.row_stride = static_cast<uint32_t>(in->residual_row_stride);
+    a.row_used = static_cast<uint32_t>(p.row_used);
+    a.payload = p.payload;
+    a.n_items = p.n_items;
+    a.n_values = p.n_values;
+    a.n_encoded = p.n_encoded;
+    a.base_input = in->base_input ? 1 : 0;
+    a.n_frequencies = in->n_frequencies;
+    a.residual_act = in->residual_act;
+    a.color_shift = in->color_shift;
+    NgsplatTextures t{};
+    t.splat_words = out->splat_words;
+    t.params = out->params;
+    t.source_index = out->source_index;
+    t.capacity = capacity;
+    t.n_textures = p.n_textures;
+    uint64_t offset = 0;
+    for (int k = 0; k < p.n_textures; k++) {
+        t.texel_words[k] = p.texel_words[k];
+        t.texture_offset[k] = offset;
+        offset += static_cast<uint64_t>(capacity) * p.texel_words[k];
+    }
+    NgsplatStats* stats = reinterpret_cast<NgsplatStats*>(blob + partial_bytes);
+    if (!launch_ngsplat_pack(a, t, reinterpret_cast<uint32_t*>(blob), stats, s)) return EFGS_ERR_HIP;
+    NgsplatStats host;
+    if (hipMemcpyAsync(&host, stats, sizeof(host), hipMemcpyDeviceToHost, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+        return fail(EFGS_ERR_HIP, "reading the ngsplat statistics failed");
+    out->n_kept = host.n_kept;
+    out->base_offset = host.base_offset;
+    out->base_scale = host.base_scale;
+    // levels absent from the export carry scale 0 (degree l's coefficients end at (l + 1)^2 - 1)
+    for (int l = 0; l < 3; l++)
+        out->sh_level_scale[l] = p.payload == EFGS_NGSPLAT_SH && (l + 2) * (l + 2) - 1 <= p.n_items ? host.level_scale[l] : 0.0f;
+    return EFGS_OK;
+}
+
 }  // extern "C"

@@ -139,4 +139,51 @@ bool launch_add_noise(const float* raw_scales, const float* raw_rotations, const
 bool launch_relocation(const float* old_opacities, const float* old_scales, const int64_t* n_samples, float* new_opacities, float* new_scales,
                        uint32_t n, hipStream_t s);
 
+// ---- .ngsplat packing ----------------------------------------------------------------------------------------------
+enum NgsplatPayload { ng_neural_features = 0, ng_neural_baked = 1, ng_sh = 2, ng_sv = 3, ng_nasg = 4, ng_nasgabor = 5 };
+constexpr uint32_t ng_block = 256;          // splats (and output rows) per block
+constexpr uint32_t ng_tex_width = 2048;     // texture width of the format: output rows come in multiples of it
+constexpr uint32_t ng_max_row = 63;         // residual parameters per splat staged in LDS
+constexpr uint32_t ng_max_values = 64;      // fp16 payload values per splat (8 textures of 8)
+constexpr uint32_t ng_max_baked = 16;       // neurons of a baked layer 0
+constexpr uint32_t ng_max_textures = 8;
+struct NgsplatArgs {
+    const float* means;            // N x 3
+    const float* raw_scales;       // N x 3 log scales
+    const float* raw_rotations;    // N x 4 (w, x, y, z), unnormalised
+    const float* raw_opacities;    // N logits
+    const float* base_colors;      // N x 3
+    const float* residual_params;  // N x row_stride; the first row_used floats of each row are read
+    const float* bake_matrix;      // baked neural: n_values x n_encoded, row-major
+    const float* bake_bias;        // baked neural: n_values, or null
+    uint32_t n, row_stride, row_used;
+    int payload;                   // NgsplatPayload
+    int n_items;                   // SH: coefficients exported; SV: sites; NASG / NASGabor: lobes; neural: raw features
+    int n_values;                  // fp16 values per splat (neural, SV, NASG, NASGabor)
+    int n_encoded;                 // neural: encoded feature width
+    int base_input;                // neural: the raw base colours follow the features
+    int n_frequencies;             // neural: frequency encoding (0 = identity)
+    int residual_act;              // SV / NASG / NASGabor: residual activation baked into the colours
+    float color_shift;             // added to the base colour before quantisation
+};
+struct NgsplatTextures {
+    uint32_t* splat_words;         // capacity x 4
+    uint32_t* params;              // payload textures back to back
+    int32_t* source_index;         // capacity, optional
+    uint32_t capacity;             // rows per texture, a multiple of ng_tex_width
+    int n_textures;
+    uint32_t texel_words[ng_max_textures];
+    uint64_t texture_offset[ng_max_textures];  // u32 offset of each payload texture in params
+};
+// device-side result of the statistics pass, copied to the host
+struct NgsplatStats {
+    uint32_t n_kept;
+    float base_offset, base_scale;
+    float level_scale[3];
+};
+// u32 words per payload texture (SH: per level present) for a payload description; returns the texture count
+int ngsplat_texture_plan(int payload, int n_items, int n_values, uint32_t* texel_words);
+// statistics, block prefix and packing; `partials` holds div_up(capacity, ng_block) * 8 u32, `stats` one NgsplatStats
+bool launch_ngsplat_pack(const NgsplatArgs& a, const NgsplatTextures& t, uint32_t* partials, NgsplatStats* stats, hipStream_t s);
+
 }  // namespace efgs

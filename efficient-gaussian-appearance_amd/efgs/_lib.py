@@ -62,6 +62,20 @@ class Workspace(ctypes.Structure):
                 ('fallback', ctypes.c_void_p), ('fallback_ctx', ctypes.c_void_p)]
 
 
+class NgsplatInput(ctypes.Structure):
+    _fields_ = [('n', ctypes.c_int64)] + [(name, ctypes.c_void_p) for name in (
+        'means', 'raw_scales', 'raw_rotations', 'raw_opacities', 'base_colors', 'residual_params')] + [
+        ('residual_row_stride', ctypes.c_int64), ('payload', ctypes.c_int), ('n_items', ctypes.c_int), ('base_input', ctypes.c_int),
+        ('n_frequencies', ctypes.c_int), ('n_neurons', ctypes.c_int), ('residual_act', ctypes.c_int), ('color_shift', ctypes.c_float),
+        ('bake_matrix', ctypes.c_void_p), ('bake_bias', ctypes.c_void_p)]
+
+
+class NgsplatOutput(ctypes.Structure):
+    _fields_ = [('capacity', ctypes.c_int64), ('splat_words', ctypes.c_void_p), ('params', ctypes.c_void_p), ('source_index', ctypes.c_void_p),
+                ('n_kept', ctypes.c_int64), ('base_offset', ctypes.c_float), ('base_scale', ctypes.c_float),
+                ('sh_level_scale', ctypes.c_float * 3)]
+
+
 class FrameViews(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in (
         'n_touched', 'depth_keys', 'records', 'visible_prims', 'prim_offset', 'instance_keys', 'instance_primitive',
@@ -73,7 +87,8 @@ lib = ctypes.CDLL(LIB_PATH)
 EXPORTED = ('efgs_last_error', 'efgs_set_rtc_dirs', 'efgs_rasterizer_create', 'efgs_rasterizer_destroy', 'efgs_set_appearance',
             'efgs_set_residual_mlp', 'efgs_mlp_param_count', 'efgs_forward', 'efgs_backward', 'efgs_adam_step',
             'efgs_get_frame_views', 'efgs_precompile', 'efgs_set_stage_timing', 'efgs_get_stage_times', 'efgs_workspace_alloc',
-            'efgs_neural_decode_forward', 'efgs_neural_decode_backward', 'efgs_add_noise', 'efgs_relocation_adjustment', 'efgs_render', 'efgs_update_pruning_scores')
+            'efgs_neural_decode_forward', 'efgs_neural_decode_backward', 'efgs_add_noise', 'efgs_relocation_adjustment', 'efgs_render', 'efgs_update_pruning_scores',
+            'efgs_ngsplat_layout', 'efgs_ngsplat_pack')
 
 # stage ids of efgs_get_stage_times, in order (include/efgs.h)
 STAGES = ('preprocess_forward', 'compact', 'counter_read', 'create_instances', 'tile_offsets', 'tile_buckets', 'tile_sort',
@@ -111,6 +126,8 @@ lib.efgs_update_pruning_scores.argtypes = [ctypes.c_void_p, ctypes.POINTER(Primi
                                            ctypes.c_void_p, ctypes.c_void_p]
 lib.efgs_add_noise.argtypes = [ctypes.c_int64] + [ctypes.c_void_p] * 4 + [ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p]
 lib.efgs_relocation_adjustment.argtypes = [ctypes.c_int64] + [ctypes.c_void_p] * 5 + [ctypes.c_void_p]
+lib.efgs_ngsplat_layout.argtypes = [ctypes.POINTER(NgsplatInput), ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+lib.efgs_ngsplat_pack.argtypes = [ctypes.POINTER(NgsplatInput), ctypes.POINTER(NgsplatOutput), ALLOC_FN, ctypes.c_void_p, ctypes.c_void_p]
 
 
 def check(rc: int) -> None:

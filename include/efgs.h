@@ -19,6 +19,7 @@
  *   _C.adam_step ............... B/adam/src/adam.cu:44-87
  *   _C.add_noise ............... B/densification/src/densification_api.cu:40-72
  *   _C.relocation_adjustment ... B/densification/src/densification_api.cu:13-38
+ *   .ngsplat per-splat packing . viewer/export_ngsplat.py:311-400, :576-611, :624-765, :1465-1530 (numpy script)
  */
 #ifndef EFGS_H
 #define EFGS_H
@@ -210,6 +211,59 @@ int efgs_add_noise(int64_t n, const float* raw_scales, const float* raw_rotation
  * B/densification/include/kernels_mcmc.cuh:11-56). */
 int efgs_relocation_adjustment(int64_t n, const float* old_opacities, const float* old_scales, const int64_t* n_samples_per_primitive,
                                float* new_opacities, float* new_scales, void* stream);
+
+/* ---- .ngsplat export: the per-splat textures of the WebGL viewer's file format ----
+ * The reference writes the format with a numpy script (viewer/export_ngsplat.py); these entry points are its
+ * per-splat part, run on the device. Splats with sigmoid(raw opacity) < 1/255 are culled, the kept ones are
+ * written in source order. Payload kinds (the per-splat residual textures of each appearance model): */
+enum {
+    EFGS_NGSPLAT_NEURAL_FEATURES = 0,  /* neural, full layout: encoded features as fp16 (1..16 dims) */
+    EFGS_NGSPLAT_NEURAL_BAKED = 1,     /* neural, baked layout: h0_static = bake_matrix . encoded + bake_bias as fp16 */
+    EFGS_NGSPLAT_SH = 2,               /* raw SH coefficients quantised per level (7 / 8 / 6 bits for degrees 1 / 2 / 3) */
+    EFGS_NGSPLAT_SV = 3,               /* spherical Voronoi: unit site, exp temperature, activated colour (7 fp16 per site) */
+    EFGS_NGSPLAT_NASG = 4,             /* NASG: frame x, frame z, 2 lambda, a, N, activated colour (12 fp16 per lobe) */
+    EFGS_NGSPLAT_NASGABOR = 5          /* NASGabor: the NASG layout plus the Gabor frequency (13 fp16 per lobe) */
+};
+typedef struct efgs_ngsplat_input {
+    int64_t n;                         /* splats */
+    const float* means;                /* n x 3 */
+    const float* raw_scales;           /* n x 3 log scales */
+    const float* raw_rotations;        /* n x 4 (w, x, y, z), unnormalised */
+    const float* raw_opacities;        /* n logits */
+    const float* base_colors;          /* n x 3 */
+    const float* residual_params;      /* n rows of residual_row_stride floats (the model's _residual_params) */
+    int64_t residual_row_stride;
+    int payload;                       /* EFGS_NGSPLAT_* */
+    int n_items;                       /* neural: raw features per row; SH: coefficients exported (0, 3, 8 or 15);
+                                          SV: sites (<= 9); NASG: lobes (<= 5); NASGabor: lobes (<= 4) */
+    int base_input;                    /* neural: the raw base colours follow the features */
+    int n_frequencies;                 /* neural: frequency encoding sin / cos (2^f x), f < k (0 = identity) */
+    int n_neurons;                     /* neural baked: rows of bake_matrix (<= 16) */
+    int residual_act;                  /* SV / NASG / NASGabor: 0 none, 1 tanh, 2 softplus (baked into the colours) */
+    float color_shift;                 /* added to the base colour before its rgb8 quantisation */
+    const float* bake_matrix;          /* neural baked, device: n_neurons x encoded width, row-major */
+    const float* bake_bias;            /* neural baked, device: n_neurons, or NULL */
+} efgs_ngsplat_input;
+typedef struct efgs_ngsplat_output {
+    int64_t capacity;                  /* rows of every texture: a multiple of 2048 that is >= n */
+    uint32_t* splat_words;             /* device, capacity x 4 (RGBA32UI), 16-byte aligned */
+    uint32_t* params;                  /* device, the payload textures back to back: texture k holds capacity x
+                                          texel_words[k] u32 (efgs_ngsplat_layout), 16-byte aligned */
+    int32_t* source_index;             /* device, capacity, optional: source splat of each row, -1 past the kept ones */
+    /* written on return */
+    int64_t n_kept;                    /* rows [n_kept, capacity) are zero */
+    float base_offset, base_scale;     /* base pre-activation d = base_offset + code8 * base_scale */
+    float sh_level_scale[3];           /* SH: max |coefficient| per level (the quantisation scale), 0 when absent */
+} efgs_ngsplat_output;
+/* Texture count and u32 words per texel of each payload texture (texel_words: 8 entries).
+ * Replaces the texture planning of viewer/export_ngsplat.py:372-386 and :576-611. */
+int efgs_ngsplat_layout(const efgs_ngsplat_input* in, int* n_textures, int* texel_words);
+/* Culls, quantises and packs the splat and payload textures; one blocking read of the 32-byte statistics. Its
+ * per-block partials come from `alloc`.
+ * Replaces viewer/export_ngsplat.py:1465-1530 (culling, rgb8 base, a8 opacity, layer-0 bake) with the helpers
+ * :311-400 (pack_splat_texture, encode_quat_oct, encode_scales, pack_half_textures), :576-611
+ * (pack_sh_quantized) and :624-765 (SV / NASG / NASGabor payloads). */
+int efgs_ngsplat_pack(const efgs_ngsplat_input* in, efgs_ngsplat_output* out, efgs_alloc_fn alloc, void* alloc_ctx, void* stream);
 
 /* Standalone neural decode: the configured residual MLP (efgs_set_residual_mlp, model 5) on n primitives'
  * features (n x n_features, the learned latents), base colours (n x 3, read with base input only) and unit
