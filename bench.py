@@ -561,6 +561,85 @@ def pruning_benchmark(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+# ---------------------------------------------------------------------------------------------------------
+# .ngsplat export: device packing of a 1M-splat model
+# ---------------------------------------------------------------------------------------------------------
+
+def ngsplat_benchmark(args) -> None:
+    """efgs_ngsplat_pack over a 1M-splat model in the viewer's default neural configuration (8 features, sin / cos
+    encoding, degrees 0..3, 16 neurons: baked layer 0) and in SH degree 3; HIP events around each call on its
+    stream (a call is the statistics, combine and pack kernels plus its blocking 32-byte statistics read)."""
+    import numpy as np
+    import torch
+    from efgs import ngsplat as NG
+    device = torch.device('cuda:0')
+    torch.cuda.set_device(device)
+    from efgs.synthetic import ngsplat_model as make_case
+    n = 1_000_000
+    results = {}
+    for name in ('baked', 'sh3'):
+        m, plan, _ = make_case(name, n=n, seed=9)
+        t = {k: torch.tensor(v, device=device) for k, v in m.items()}
+
+        def call(timing=False):
+            return NG.pack_textures(t['means'], t['raw_scales'], t['raw_rotations'], t['raw_opacities'], t['base_colors'],
+                                    t['residual_params'], plan, timing=timing)
+        for _ in range(args.warmup):
+            out = call()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+        for k in range(args.steps):
+            ev[k][0].record()
+            out = call()
+            ev[k][1].record()
+        torch.cuda.synchronize()
+        ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+        # the kernels alone: HIP events recorded by the library around them, on the launch stream
+        kms = [call(timing=True)['kernel_ms'] for _ in range(args.steps)]
+        stats_ms = sum(k[0] for k in kms) / len(kms)
+        pack_ms = sum(k[1] for k in kms) / len(kms)
+        kept = out['n_kept']
+        row = m['residual_params'].reshape(n, -1).shape[1] if name == 'sh3' else plan['n_items']
+        out_payload = sum(x.shape[1] * 4 for x in out['textures'])
+        # compulsory: every input row read once (mean, log-scales, quaternion, opacity, base, the payload's residual
+        # parameters), every kept row written once (splat words, payload texels, source index)
+        nbytes = n * (12 + 12 + 16 + 4 + 12 + 4 * row) + kept * (16 + out_payload + 4)
+        results[name] = dict(ms=ms, kept=kept, bytes=nbytes, m=m, plan=plan, stats_ms=stats_ms, pack_ms=pack_ms)
+        log(f'ngsplat {name}: {n} splats, kept {kept}, call {ms:.4f} ms, kernels {stats_ms:.4f} + {pack_ms:.4f} ms')
+    r = results['baked']
+    line = {
+        'metric': '.ngsplat export packing Msplat/s @1M Gaussians (neural, baked layer 0)', 'value': round(n / (r['ms'] * 1e-3) / 1e6, 3),
+        'unit': 'Msplat/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(r['ms'], 5),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32 -> u8 / f16 codes', 'data': 'synthetic',
+        'config': {'workload': f'ngsplat: cull, quantise and pack {n} splats (viewer default neural model: 8 features, sin/cos, '
+                               f'degrees 0-3, 16 neurons) and the same model with SH degree 3', 'n_splats': n},
+        'call_note': 'value and ms_per_step time the whole efgs_ngsplat_pack call from Python (ctypes, output allocation, '
+                     'three kernels, the blocking statistics read); the roofline times the kernels alone',
+        'kernel_ms': {'stats_combine': round(r['stats_ms'], 5), 'pack': round(r['pack_ms'], 5)},
+        'sh3_ms': round(results['sh3']['ms'], 5), 'sh3_msplat_s': round(n / (results['sh3']['ms'] * 1e-3) / 1e6, 3),
+        'sh3_kernel_ms': {'stats_combine': round(results['sh3']['stats_ms'], 5), 'pack': round(results['sh3']['pack_ms'], 5)},
+        'roofline': {'bound': 'hbm', 'achieved': round(r['bytes'] / ((r['stats_ms'] + r['pack_ms']) * 1e-3) / 1e9, 2), 'peak': HBM_PEAK_GBS,
+                     'unit': 'GB/s', 'frac': round(r['bytes'] / ((r['stats_ms'] + r['pack_ms']) * 1e-3) / 1e9 / HBM_PEAK_GBS, 5),
+                     'traffic': None, 'kernel': 'ngsplat_stats_kernel + ngsplat_combine_kernel + ngsplat_pack_kernel (HIP events)',
+                     'algorithmic_bytes': int(r['bytes']),
+                     'sh3': {'achieved': round(results['sh3']['bytes'] / ((results['sh3']['stats_ms'] + results['sh3']['pack_ms']) * 1e-3) / 1e9, 2),
+                             'unit': 'GB/s', 'algorithmic_bytes': int(results['sh3']['bytes']),
+                             'frac': round(results['sh3']['bytes'] / ((results['sh3']['stats_ms'] + results['sh3']['pack_ms']) * 1e-3) / 1e9
+                                           / HBM_PEAK_GBS, 5)}},
+        'cpu_baseline': None,
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+        import ngsplat_oracle as ON
+        mm, plan = r['m'], r['plan']
+        t0 = time.perf_counter()
+        ON.export(mm['means'], mm['raw_scales'], mm['raw_rotations'], mm['raw_opacities'], mm['base_colors'], mm['residual_params'], plan)
+        seconds = time.perf_counter() - t0
+        line['cpu_baseline'] = {'value': round(n / seconds / 1e6, 5), 'unit': 'Msplat/s', 'cores': 1, 'kind': 'port',
+                                'sample': f'the numpy restatement of the exporter (oracle/ngsplat_oracle.py) on the same {n}-splat '
+                                          f'neural model; {seconds:.2f} s'}
+    print(json.dumps(line), flush=True)
+
+
 def copy_calibration() -> None:
     """A plain device copy of 1 GiB, five times: rocprofv3 FETCH_SIZE / WRITE_SIZE of this command read
     1 GiB each per dispatch when the counters are exact."""
@@ -594,6 +673,9 @@ def main() -> None:
         return
     if args.config == 'pruning':
         pruning_benchmark(args)
+        return
+    if args.config == 'ngsplat':
+        ngsplat_benchmark(args)
         return
     r = gpu_benchmark(args)
     W, H = r['W'], r['H']

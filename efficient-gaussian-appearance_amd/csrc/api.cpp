@@ -1144,7 +1144,7 @@ int ngsplat_plan(const efgs_ngsplat_input* in, NgsplatPlan& p) {
         } else {
             if (in->n_neurons < 1 || in->n_neurons > static_cast<int>(ng_max_baked))
                 return fail(EFGS_ERR_INVALID_ARGUMENT, "a baked layer 0 needs 1..16 neurons");
-            if (p.n_encoded < 1) return fail(EFGS_ERR_INVALID_ARGUMENT, "a baked layer 0 needs encoded features");
+            if (p.n_encoded < 1 || p.n_encoded > 256) return fail(EFGS_ERR_INVALID_ARGUMENT, "a baked layer 0 needs 1..256 encoded features");
             p.n_values = in->n_neurons;
         }
         break;
@@ -1249,10 +1249,35 @@ int efgs_ngsplat_pack(const efgs_ngsplat_input* in, efgs_ngsplat_output* out, ef
         offset += static_cast<uint64_t>(capacity) * p.texel_words[k];
     }
     NgsplatStats* stats = reinterpret_cast<NgsplatStats*>(blob + partial_bytes);
-    if (!launch_ngsplat_pack(a, t, reinterpret_cast<uint32_t*>(blob), stats, s)) return EFGS_ERR_HIP;
+    hipEvent_t events[3] = {nullptr, nullptr, nullptr};
+    const bool timed = out->kernel_ms != nullptr;
+    auto destroy_events = [&events]() {
+        for (hipEvent_t& e : events)
+            if (e) (void)hipEventDestroy(e);
+    };
+    if (timed)
+        for (hipEvent_t& e : events)
+            if (hipEventCreate(&e) != hipSuccess) {
+                destroy_events();
+                return fail(EFGS_ERR_HIP, "creating the ngsplat timing events failed");
+            }
+    if (!launch_ngsplat_pack(a, t, reinterpret_cast<uint32_t*>(blob), stats, timed ? events : nullptr, s)) {
+        destroy_events();
+        return EFGS_ERR_HIP;
+    }
     NgsplatStats host;
-    if (hipMemcpyAsync(&host, stats, sizeof(host), hipMemcpyDeviceToHost, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+    if (hipMemcpyAsync(&host, stats, sizeof(host), hipMemcpyDeviceToHost, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
+        destroy_events();
         return fail(EFGS_ERR_HIP, "reading the ngsplat statistics failed");
+    }
+    if (timed) {
+        float ms0 = 0.0f, ms1 = 0.0f;
+        const bool ok = hipEventElapsedTime(&ms0, events[0], events[1]) == hipSuccess && hipEventElapsedTime(&ms1, events[1], events[2]) == hipSuccess;
+        destroy_events();
+        if (!ok) return fail(EFGS_ERR_HIP, "reading the ngsplat timing events failed");
+        out->kernel_ms[0] = ms0;
+        out->kernel_ms[1] = ms1;
+    }
     out->n_kept = host.n_kept;
     out->base_offset = host.base_offset;
     out->base_scale = host.base_scale;

@@ -183,7 +183,9 @@ struct NgsplatStats {
 };
 // u32 words per payload texture (SH: per level present) for a payload description; returns the texture count
 int ngsplat_texture_plan(int payload, int n_items, int n_values, uint32_t* texel_words);
-// statistics, block prefix and packing; `partials` holds div_up(capacity, ng_block) * 8 u32, `stats` one NgsplatStats
-bool launch_ngsplat_pack(const NgsplatArgs& a, const NgsplatTextures& t, uint32_t* partials, NgsplatStats* stats, hipStream_t s);
+// statistics, block prefix and packing; `partials` holds div_up(capacity, ng_block) * 8 u32, `stats` one NgsplatStats;
+// `events` (optional, three) are recorded before the statistics kernel, before and after the pack kernel
+bool launch_ngsplat_pack(const NgsplatArgs& a, const NgsplatTextures& t, uint32_t* partials, NgsplatStats* stats, hipEvent_t* events,
+                         hipStream_t s);
 
 }  // namespace efgs

@@ -134,20 +134,66 @@ __global__ __launch_bounds__(ng_block) void ngsplat_stats_kernel(NgsplatArgs a, 
         }
     }
     float level[3] = {0.0f, 0.0f, 0.0f};
-    if (a.payload == ng_sh && i0 < a.n) {
+    if (a.payload == ng_sh && i0 < a.n && a.row_used == a.row_stride && (reinterpret_cast<uintptr_t>(a.residual_params) & 15u) == 0 &&
+        a.row_used >= 4) {
+        // whole rows, 16-byte aligned: the block's rows are one contiguous run read as float4 (element k of a float4
+        // at flat position p belongs to row (p + k) / used, column (p + k) % used)
+        s_keep[tid] = keep ? 1u : 0u;
+        __syncthreads();
+        const uint32_t rows = min(ng_block, a.n - i0);
+        const uint32_t used = a.row_used, total = rows * used;
+        const float* src = a.residual_params + static_cast<size_t>(i0) * used;
+        const uint32_t step = 4 * ng_block, dr = step / used, dc = step - dr * used;
+        uint32_t r = (4 * tid) / used, col = 4 * tid - r * used;
+#pragma unroll 4
+        for (uint32_t p = 4 * tid; p < total; p += step) {
+            float4 v4;
+            if (p + 4 <= total) {
+                v4 = *reinterpret_cast<const float4*>(src + p);
+            } else {
+                v4.x = src[p];
+                v4.y = p + 1 < total ? src[p + 1] : 0.0f;
+                v4.z = p + 2 < total ? src[p + 2] : 0.0f;
+                v4.w = 0.0f;
+            }
+            const float vals[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t ck = col + k, wrap = ck >= used ? 1u : 0u;
+                const uint32_t cc = ck - wrap * used, rr = r + wrap;
+                const float v = rr < rows && s_keep[rr] ? fabsf(vals[k]) : 0.0f;
+                const uint32_t c = cc / 3;
+                level[0] = c < 3 ? fmaxf(level[0], v) : level[0];
+                level[1] = c >= 3 && c < 8 ? fmaxf(level[1], v) : level[1];
+                level[2] = c >= 8 ? fmaxf(level[2], v) : level[2];
+            }
+            col += dc;
+            r += dr;
+            const bool wrap = col >= used;
+            col = wrap ? col - used : col;
+            r = wrap ? r + 1 : r;
+        }
+    } else if (a.payload == ng_sh && i0 < a.n) {
         s_keep[tid] = keep ? 1u : 0u;
         __syncthreads();
         const uint32_t rows = min(ng_block, a.n - i0);
         const uint32_t used = a.row_used;
         const float* src = a.residual_params + static_cast<size_t>(i0) * a.row_stride;
-        for (uint32_t p = tid; p < rows * used; p += ng_block) {
-            const uint32_t r = p / used, col = p - r * used;
-            if (!s_keep[r]) continue;
-            const float v = fabsf(src[static_cast<size_t>(r) * a.row_stride + col]);
+        // flat sweep over the rows' first `used` floats (branch-free, unrolled: several loads in flight)
+        const uint32_t total = rows * used, dr = ng_block / used, dc = ng_block - dr * used;
+        uint32_t r = tid / used, col = tid - r * used;
+#pragma unroll 8
+        for (uint32_t p = tid; p < total; p += ng_block) {
+            const float v = s_keep[r] ? fabsf(src[static_cast<size_t>(r) * a.row_stride + col]) : 0.0f;
             const uint32_t c = col / 3;
-            if (c < 3) level[0] = fmaxf(level[0], v);
-            else if (c < 8) level[1] = fmaxf(level[1], v);
-            else level[2] = fmaxf(level[2], v);
+            level[0] = c < 3 ? fmaxf(level[0], v) : level[0];
+            level[1] = c >= 3 && c < 8 ? fmaxf(level[1], v) : level[1];
+            level[2] = c >= 8 ? fmaxf(level[2], v) : level[2];
+            col += dc;
+            r += dr;
+            const bool wrap = col >= used;
+            col = wrap ? col - used : col;
+            r = wrap ? r + 1 : r;
         }
     }
     const uint32_t count = static_cast<uint32_t>(__popcll(__ballot(keep)));
@@ -274,7 +320,7 @@ __device__ __forceinline__ float ng_encoded(const float* row, float3 base, int n
 
 // fp16 payload values of one splat (neural features / baked layer 0, SV sites, NASG / NASGabor lobes)
 template <int PAYLOAD>
-__device__ __forceinline__ void ng_values(const NgsplatArgs& a, const float* row, float3 base, float (&v)[ng_max_values]) {
+__device__ __forceinline__ void ng_values(const NgsplatArgs& a, const float* row, float3 base, const float* bake, float (&v)[ng_max_values]) {
     if (PAYLOAD == ng_neural_features) {
 #pragma unroll
         for (int j = 0; j < 16; j++)
@@ -285,9 +331,15 @@ __device__ __forceinline__ void ng_values(const NgsplatArgs& a, const float* row
         for (int o = 0; o < static_cast<int>(ng_max_baked); o++) h[o] = 0.0f;
         for (int j = 0; j < a.n_encoded; j++) {
             const float e = ng_encoded(row, base, a.n_items, a.n_frequencies, j);
+            const float4* m = reinterpret_cast<const float4*>(bake + j * ng_max_baked);
 #pragma unroll
-            for (int o = 0; o < static_cast<int>(ng_max_baked); o++)
-                if (o < a.n_values) h[o] = fmaf(e, a.bake_matrix[o * a.n_encoded + j], h[o]);
+            for (int q = 0; q < static_cast<int>(ng_max_baked) / 4; q++) {
+                const float4 w = m[q];
+                h[4 * q + 0] = fmaf(e, w.x, h[4 * q + 0]);
+                h[4 * q + 1] = fmaf(e, w.y, h[4 * q + 1]);
+                h[4 * q + 2] = fmaf(e, w.z, h[4 * q + 2]);
+                h[4 * q + 3] = fmaf(e, w.w, h[4 * q + 3]);
+            }
         }
 #pragma unroll
         for (int o = 0; o < static_cast<int>(ng_max_baked); o++)
@@ -366,13 +418,28 @@ __global__ __launch_bounds__(ng_block) void ngsplat_pack_kernel(NgsplatArgs a, N
     const uint64_t ballot = __ballot(keep);
     if (lane == 0) s_wave[wave] = static_cast<uint32_t>(__popcll(ballot));
     // the block's residual rows into LDS (stride row_used | 1 keeps consecutive rows in different banks)
-    const uint32_t ld = a.row_used | 1u;
-    if (a.row_used && i0 < a.n) {
+    const uint32_t used = a.row_used, ld = used | 1u;
+    if (used && i0 < a.n) {
         const uint32_t rows = min(ng_block, a.n - i0);
         const float* src = a.residual_params + static_cast<size_t>(i0) * a.row_stride;
-        for (uint32_t p = tid; p < rows * a.row_used; p += ng_block) {
-            const uint32_t r = p / a.row_used, col = p - r * a.row_used;
+        const uint32_t total = rows * used, dr = ng_block / used, dc = ng_block - dr * used;
+        uint32_t r = tid / used, col = tid - r * used;
+#pragma unroll 8
+        for (uint32_t p = tid; p < total; p += ng_block) {
             s_rows[r * ld + col] = src[static_cast<size_t>(r) * a.row_stride + col];
+            col += dc;
+            r += dr;
+            const bool wrap = col >= used;
+            col = wrap ? col - used : col;
+            r = wrap ? r + 1 : r;
+        }
+    }
+    // baked layer 0: the matrix transposed into LDS after the rows (column j of all neurons is 16 consecutive floats)
+    float* s_bake = s_rows + (used ? ng_block * ld : 0u);
+    if (PAYLOAD == ng_neural_baked) {
+        for (uint32_t p = tid; p < static_cast<uint32_t>(a.n_encoded) * ng_max_baked; p += ng_block) {
+            const uint32_t j = p / ng_max_baked, o = p % ng_max_baked;
+            s_bake[p] = o < static_cast<uint32_t>(a.n_values) ? a.bake_matrix[o * a.n_encoded + j] : 0.0f;
         }
     }
     __syncthreads();
@@ -415,10 +482,15 @@ __global__ __launch_bounds__(ng_block) void ngsplat_pack_kernel(NgsplatArgs a, N
             const float qmax = static_cast<float>((1 << (bits - 1)) - 1);
             const uint32_t mask = (1u << bits) - 1u;
             const float scale = st.level_scale[l];
+            // c / scale correctly rounded from the correctly rounded reciprocal and one FMA correction (Markstein)
+            const float inv = 1.0f / scale;
             uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int f = 0; f < 3 * ng_level_width[l]; f++) {
-                const float c = fminf(fmaxf(rintf(x[3 * ng_level_offset[l] + f] / scale * qmax), -qmax), qmax);
+                const float c0 = x[3 * ng_level_offset[l] + f];
+                const float q0 = c0 * inv;
+                const float quot = fmaf(fmaf(-q0, scale, c0), inv, q0);
+                const float c = fminf(fmaxf(rintf(quot * qmax), -qmax), qmax);
                 const uint32_t code = static_cast<uint32_t>(static_cast<int32_t>(c)) & mask;
                 const int bit = bits * f, word = bit >> 5, shift = bit & 31;
                 w[word] |= code << shift;
@@ -432,7 +504,7 @@ __global__ __launch_bounds__(ng_block) void ngsplat_pack_kernel(NgsplatArgs a, N
         float v[ng_max_values];
 #pragma unroll
         for (int j = 0; j < static_cast<int>(ng_max_values); j++) v[j] = 0.0f;
-        ng_values<PAYLOAD>(a, x, make_float3(base[0], base[1], base[2]), v);
+        ng_values<PAYLOAD>(a, x, make_float3(base[0], base[1], base[2]), s_bake, v);
 #pragma unroll
         for (int k = 0; k < static_cast<int>(ng_max_textures); k++) {
             if (k >= t.n_textures) break;
@@ -460,13 +532,17 @@ int ngsplat_texture_plan(int payload, int n_items, int n_values, uint32_t* texel
     return n;
 }
 
-bool launch_ngsplat_pack(const NgsplatArgs& a, const NgsplatTextures& t, uint32_t* partials, NgsplatStats* stats, hipStream_t s) {
+bool launch_ngsplat_pack(const NgsplatArgs& a, const NgsplatTextures& t, uint32_t* partials, NgsplatStats* stats, hipEvent_t* events,
+                         hipStream_t s) {
     const uint32_t blocks = t.capacity / ng_block;
+    if (events) EFGS_HIP_CHECK(hipEventRecord(events[0], s));
     ngsplat_stats_kernel<<<blocks, ng_block, 0, s>>>(a, partials);
     EFGS_HIP_CHECK(hipGetLastError());
     ngsplat_combine_kernel<<<1, 1024, 0, s>>>(partials, blocks, stats);
     EFGS_HIP_CHECK(hipGetLastError());
-    const size_t lds = a.row_used ? sizeof(float) * ng_block * (a.row_used | 1u) : 0;
+    if (events) EFGS_HIP_CHECK(hipEventRecord(events[1], s));
+    const size_t lds = sizeof(float) * (a.row_used ? ng_block * (a.row_used | 1u) : 0) +
+                       (a.payload == ng_neural_baked ? sizeof(float) * a.n_encoded * ng_max_baked : 0);
     switch (a.payload) {
     case ng_neural_features: ngsplat_pack_kernel<ng_neural_features><<<blocks, ng_block, lds, s>>>(a, t, partials, stats); break;
     case ng_neural_baked: ngsplat_pack_kernel<ng_neural_baked><<<blocks, ng_block, lds, s>>>(a, t, partials, stats); break;
@@ -477,6 +553,7 @@ bool launch_ngsplat_pack(const NgsplatArgs& a, const NgsplatTextures& t, uint32_
     default: set_error("unknown ngsplat payload"); return false;
     }
     EFGS_HIP_CHECK(hipGetLastError());
+    if (events) EFGS_HIP_CHECK(hipEventRecord(events[2], s));
     return true;
 }
 

@@ -72,7 +72,7 @@ class NgsplatInput(ctypes.Structure):
 
 class NgsplatOutput(ctypes.Structure):
     _fields_ = [('capacity', ctypes.c_int64), ('splat_words', ctypes.c_void_p), ('params', ctypes.c_void_p), ('source_index', ctypes.c_void_p),
-                ('n_kept', ctypes.c_int64), ('base_offset', ctypes.c_float), ('base_scale', ctypes.c_float),
+                ('kernel_ms', ctypes.POINTER(ctypes.c_float)), ('n_kept', ctypes.c_int64), ('base_offset', ctypes.c_float), ('base_scale', ctypes.c_float),
                 ('sh_level_scale', ctypes.c_float * 3)]
 
 

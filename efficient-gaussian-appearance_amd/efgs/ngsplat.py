@@ -212,10 +212,11 @@ def _device_f32(name: str, t, device: torch.device, shape_tail: tuple[int, ...] 
 
 
 def pack_textures(means: torch.Tensor, raw_scales: torch.Tensor, raw_rotations: torch.Tensor, raw_opacities: torch.Tensor,
-                  base_colors: torch.Tensor, residual_params: torch.Tensor, plan: dict[str, Any]) -> dict[str, Any]:
+                  base_colors: torch.Tensor, residual_params: torch.Tensor, plan: dict[str, Any], timing: bool = False) -> dict[str, Any]:
     """Culls, quantises and packs the splat and payload textures on the device (efgs_ngsplat_pack). Returns the
     kept count, the statistics and device tensors: splat_words (P, 4) and the payload textures (P, words) as
-    uint32 bit patterns in int32 tensors, source_index (P,), with P = 2048 * ceil(kept / 2048)."""
+    uint32 bit patterns in int32 tensors, source_index (P,), with P = 2048 * ceil(kept / 2048); with `timing`, the
+    milliseconds of the statistics + combine kernels and of the pack kernel (HIP events) as kernel_ms."""
     device = means.device
     n = means.shape[0]
     means = _device_f32('means', means, device, (3,))
@@ -240,15 +241,15 @@ def pack_textures(means: torch.Tensor, raw_scales: torch.Tensor, raw_rotations: 
     inp.n_neurons = plan['n_neurons']
     inp.residual_act = plan['residual_act']
     inp.color_shift = plan['color_shift']
-    keep_alive = []
     if plan['bake_matrix'] is not None:
-        m = torch.from_numpy(plan['bake_matrix']).to(device)
-        keep_alive.append(m)
+        # the layer-0 bake on the device, uploaded once per plan and device
+        cache = plan.setdefault('_device_bake', {})
+        if device not in cache:
+            cache[device] = (torch.from_numpy(plan['bake_matrix']).to(device),
+                             torch.from_numpy(plan['bake_bias']).to(device) if plan['bake_bias'] is not None else None)
+        m, b = cache[device]
         inp.bake_matrix = m.data_ptr()
-        if plan['bake_bias'] is not None:
-            b = torch.from_numpy(plan['bake_bias']).to(device)
-            keep_alive.append(b)
-            inp.bake_bias = b.data_ptr()
+        inp.bake_bias = b.data_ptr() if b is not None else None
     n_textures = ctypes.c_int()
     texel_words = (ctypes.c_int * 8)()
     check(lib.efgs_ngsplat_layout(ctypes.byref(inp), ctypes.byref(n_textures), texel_words))
@@ -262,6 +263,8 @@ def pack_textures(means: torch.Tensor, raw_scales: torch.Tensor, raw_rotations: 
     out.splat_words = splat_words.data_ptr()
     out.params = params.data_ptr() if params is not None else None
     out.source_index = source_index.data_ptr()
+    kernel_ms = (ctypes.c_float * 2)()
+    out.kernel_ms = kernel_ms if timing else None
     with torch.cuda.device(device):
         alloc = WorkspaceAllocator(device, 'ngsplat')
         check(lib.efgs_ngsplat_pack(ctypes.byref(inp), ctypes.byref(out), alloc.fn, alloc.ctx, torch.cuda.current_stream(device).cuda_stream))
@@ -274,7 +277,8 @@ def pack_textures(means: torch.Tensor, raw_scales: torch.Tensor, raw_rotations: 
         offset += capacity * w
     return dict(n_kept=n_kept, base_offset=float(out.base_offset), base_scale=float(out.base_scale),
                 sh_level_scales=[float(out.sh_level_scale[i]) for i in range(3)] if plan['payload'] == SH else None,
-                splat_words=splat_words[:rows], textures=textures, source_index=source_index[:rows])
+                splat_words=splat_words[:rows], textures=textures, source_index=source_index[:rows],
+                kernel_ms=(float(kernel_ms[0]), float(kernel_ms[1])) if timing else None)
 
 
 def camera_hint(kept_means: np.ndarray, test_cameras: np.ndarray | None = None, center=None, up=None, distance=None):

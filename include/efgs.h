@@ -250,6 +250,8 @@ typedef struct efgs_ngsplat_output {
     uint32_t* params;                  /* device, the payload textures back to back: texture k holds capacity x
                                           texel_words[k] u32 (efgs_ngsplat_layout), 16-byte aligned */
     int32_t* source_index;             /* device, capacity, optional: source splat of each row, -1 past the kept ones */
+    float* kernel_ms;                  /* host, optional (2 floats): milliseconds of the statistics + combine kernels and
+                                          of the pack kernel, from HIP events on the stream */
     /* written on return */
     int64_t n_kept;                    /* rows [n_kept, capacity) are zero */
     float base_offset, base_scale;     /* base pre-activation d = base_offset + code8 * base_scale */

@@ -17,7 +17,8 @@ import numpy as np
 import pytest
 
 import ngsplat_oracle as ON
-from test_ngsplat_oracle import make_case, NEURAL_CASES, OTHER_CASES
+from efgs.synthetic import NGSPLAT_NEURAL_CASES as NEURAL_CASES, NGSPLAT_OTHER_CASES as OTHER_CASES
+from efgs.synthetic import ngsplat_model as make_case
 
 pytestmark = pytest.mark.gpu
 

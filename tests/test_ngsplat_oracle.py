@@ -22,49 +22,9 @@ import numpy as np
 import pytest
 
 from efgs import ngsplat as NG
+from efgs.synthetic import NGSPLAT_NEURAL_CASES as NEURAL_CASES, NGSPLAT_OTHER_CASES as OTHER_CASES, mlp_flat
+from efgs.synthetic import ngsplat_model as make_case
 import ngsplat_oracle as ON
-
-NEURAL_CASES = {
-    # encoded 16 = 8 features x (sin, cos); degrees 0..3: 48 inputs; 16 neurons -> baked (the viewer's default model)
-    'baked': dict(n_features=8, n_frequencies=1, sh_degrees=[0, 1, 2, 3], n_neurons=16, n_hidden_layers=2, base_input=False),
-    # 32 neurons exceed the baked cache -> stored features + full layer 0 (16 + 1 + 15 = 32 inputs)
-    'full': dict(n_features=8, n_frequencies=1, sh_degrees=[0, 1, 2, 3], n_neurons=32, n_hidden_layers=2, base_input=False),
-    # raw base colours appended to 5 features, identity encoding, no constant input, input padded 20 -> 32
-    'base_input': dict(n_features=5, n_frequencies=0, sh_degrees=[1, 2], n_neurons=16, n_hidden_layers=3, base_input=True),
-}
-OTHER_CASES = {'sh3': ('sh', (15, 3)), 'sh1': ('sh', (3, 3)), 'sv7': ('sv', (7, 7)), 'nasg1': ('nasg', (1, 8)), 'nasg5': ('nasg', (5, 8)),
-               'nasgabor2': ('nasgabor', (2, 9))}
-
-
-def mlp_flat(rng, n_in, n_neurons, n_hidden_layers, scale=0.4):
-    n_in_pad = -(-n_in // 16) * 16
-    size = n_in_pad * n_neurons + (n_hidden_layers - 1) * n_neurons * n_neurons + 16 * n_neurons
-    return rng.normal(0.0, scale, size).astype(np.float16)
-
-
-def make_case(name: str, n: int = 3000, seed: int = 0, residual_act: str = 'tanh', color_act: str = 'relu', base_act: str = 'none'):
-    """A random model and its export plan for one of the named configurations."""
-    rng = np.random.default_rng(seed)
-    m = dict(means=rng.normal(0.0, 3.0, (n, 3)).astype(np.float32), raw_scales=rng.normal(-4.0, 1.5, (n, 3)).astype(np.float32),
-             raw_rotations=rng.normal(size=(n, 4)).astype(np.float32), raw_opacities=rng.normal(-2.0, 3.0, (n, 1)).astype(np.float32),
-             base_colors=rng.normal(0.0, 0.4, (n, 3)).astype(np.float32))
-    cfg = dict(base_activation=base_act, residual_activation=residual_act, color_activation=color_act)
-    mlp = None
-    if name in NEURAL_CASES:
-        c = NEURAL_CASES[name]
-        cfg.update(appearance_type='neural', n_frequencies=c['n_frequencies'], sh_degrees=c['sh_degrees'], n_neurons=c['n_neurons'],
-                   n_hidden_layers=c['n_hidden_layers'], base_input=c['base_input'])
-        m['residual_params'] = rng.normal(0.0, 0.5, (n, c['n_features'])).astype(np.float32)
-        enc = (c['n_features'] + (3 if c['base_input'] else 0)) * (2 * c['n_frequencies'] if c['n_frequencies'] else 1)
-        n_in = enc + sum(2 * d + 1 for d in c['sh_degrees'])
-        mlp = mlp_flat(rng, n_in, c['n_neurons'], c['n_hidden_layers'])
-    else:
-        model, shape = OTHER_CASES[name]
-        cfg['appearance_type'] = model
-        m['residual_params'] = rng.normal(0.0, 0.6, (n,) + shape).astype(np.float32)
-    plan = NG.plan_export(cfg, m['residual_params'].shape, mlp)
-    return m, plan, mlp
-
 
 def _export(m, plan):
     return ON.export(m['means'], m['raw_scales'], m['raw_rotations'], m['raw_opacities'], m['base_colors'], m['residual_params'], plan)
