@@ -4,6 +4,7 @@ argument meaning and error behaviour, backed by libefgs_hip.so through ctypes.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import Any, NamedTuple
 
@@ -209,49 +210,81 @@ class _Rasterize(torch.autograd.Function):
         ctx.save_for_backward(image, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
         ctx.densification_info = densification_info
         ctx.mark_non_differentiable(densification_info)
+        # the backward's host-side state is built here, while the GPU still runs the forward, so that the
+        # backward only launches
+        ctx.prepared = _prepare_backward(ctx, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params,
+                                         mlp_weights_half, densification_info, rasterizer_settings) if any(ctx.needs_input_grad) else None
         return image
 
     @staticmethod
     @once_differentiable
     def backward(ctx: Any, grad_image: torch.Tensor):
-        image, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half = ctx.saved_tensors
-        device = means.device
-        n = means.shape[0]
+        saved = ctx.saved_tensors  # unpacking checks that no saved tensor was modified in place
+        image = saved[0]
+        # a second backward of the same graph (retain_graph) gets fresh outputs: the first call's may now be .grad
+        prep = ctx.prepared or _prepare_backward(ctx, *saved[1:], ctx.densification_info, ctx.rasterizer_settings)
+        ctx.prepared = None
+        device = image.device
         grad_image = grad_image.contiguous()
-        with torch.cuda.device(device):
-            cs, keep = _native_settings(ctx.rasterizer_settings, device)
-            prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
-            # every gradient output is a view of one allocation (each is fully written by the backward)
-            shapes = [means.shape, scales.shape, rotations.shape, opacities.shape, precomputed_colors.shape, base_colors.shape,
-                      residual_params.shape, (ctx.mlp_numel,)]
-            sizes = [int(torch.Size(sh).numel()) for sh in shapes]
-            flat = torch.empty(sum(sizes), dtype=torch.float32, device=device)
-            g_means, g_scales, g_rotations, g_opacities, g_pre, g_base, g_res, g_mlp = (
-                t.view(sh) for t, sh in zip(flat.split(sizes), shapes))
-            dinfo = ctx.densification_info
-            rows = int(dinfo.shape[0]) if dinfo is not None and dinfo.numel() > 0 else 0
-            if rows:
-                if dinfo.dtype != torch.float32 or not dinfo.is_contiguous() or dinfo.shape[-1] != n or dinfo.device != device:
-                    raise ValueError('efgs: densification_info must be a contiguous float32 (2|3, N) tensor on the rendering device')
-            grads = _lib.Gradients()
-            grads.means, grads.scales, grads.rotations, grads.opacities = (g_means.data_ptr(), g_scales.data_ptr(),
-                                                                           g_rotations.data_ptr(), g_opacities.data_ptr())
-            grads.precomputed_colors = _ptr(g_pre)
-            grads.base_colors = _ptr(g_base)
-            grads.residual_params = _ptr(g_res)
-            grads.mlp_weights = _ptr(g_mlp)
-            grads.densification_info = dinfo.data_ptr() if rows else None
-            grads.densification_rows = rows
-            alloc = _lib.WorkspaceAllocator(device, 'backward')
-            check(lib.efgs_backward(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), ctypes.byref(ctx.frame), image.data_ptr(),
-                                    grad_image.data_ptr(), ctypes.byref(grads), alloc.fn, alloc.ctx, _stream(device)))
-            alloc.done()
+        if grad_image.shape != image.shape or grad_image.dtype != torch.float32 or grad_image.device != device:
+            raise ValueError('efgs: the image gradient must be a float32 tensor of the image\'s shape on its device')
+        with _on_device(device):
+            check(lib.efgs_backward(_rasterizer.handle, ctypes.byref(prep.prims), ctypes.byref(prep.settings), ctypes.byref(ctx.frame),
+                                    image.data_ptr(), grad_image.data_ptr(), ctypes.byref(prep.grads), prep.alloc.fn, prep.alloc.ctx,
+                                    _stream(device)))
+            prep.alloc.done()
+        g_means, g_scales, g_rotations, g_opacities, g_pre, g_base, g_res, g_mlp = prep.outputs
         return (g_means, g_scales, g_rotations, g_opacities,
                 g_pre if g_pre.numel() > 0 else None,
                 g_base if g_base.numel() > 0 else None,
                 g_res if g_res.numel() > 0 else None,
                 g_mlp if g_mlp.numel() > 0 else None,
                 None, None)
+
+
+class _PreparedBackward(NamedTuple):
+    settings: Any       # _lib.Settings
+    keep: list          # tensors the settings point to
+    prims: Any          # _lib.Primitives
+    grads: Any          # _lib.Gradients, pointing into `outputs`
+    outputs: tuple      # gradient tensors, views of one allocation
+    alloc: Any          # _lib.WorkspaceAllocator of the backward
+
+
+def _on_device(device: torch.device):
+    """torch.cuda.device(device) unless it is already current (entering the context costs host time)."""
+    return contextlib.nullcontext() if torch.cuda.current_device() == device.index else torch.cuda.device(device)
+
+
+def _prepare_backward(ctx, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half,
+                      dinfo, settings) -> _PreparedBackward:
+    """Native structs, gradient outputs (every gradient is a view of one allocation, each fully written by the
+    backward) and the workspace of the backward of this forward."""
+    device = means.device
+    n = means.shape[0]
+    rows = int(dinfo.shape[0]) if dinfo is not None and dinfo.numel() > 0 else 0
+    if rows and (dinfo.dtype != torch.float32 or not dinfo.is_contiguous() or dinfo.shape[-1] != n or dinfo.device != device):
+        raise ValueError('efgs: densification_info must be a contiguous float32 (2|3, N) tensor on the rendering device')
+    with _on_device(device):
+        cs, keep = _native_settings(settings, device)
+        prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
+        shapes = [means.shape, scales.shape, rotations.shape, opacities.shape, precomputed_colors.shape, base_colors.shape,
+                  residual_params.shape, (ctx.mlp_numel,)]
+        sizes = [int(torch.Size(sh).numel()) for sh in shapes]
+        flat = torch.empty(sum(sizes), dtype=torch.float32, device=device)
+        outputs = tuple(t.view(sh) for t, sh in zip(flat.split(sizes), shapes))
+        g_means, g_scales, g_rotations, g_opacities, g_pre, g_base, g_res, g_mlp = outputs
+        grads = _lib.Gradients()
+        grads.means, grads.scales, grads.rotations, grads.opacities = (g_means.data_ptr(), g_scales.data_ptr(), g_rotations.data_ptr(),
+                                                                       g_opacities.data_ptr())
+        grads.precomputed_colors = _ptr(g_pre)
+        grads.base_colors = _ptr(g_base)
+        grads.residual_params = _ptr(g_res)
+        grads.mlp_weights = _ptr(g_mlp)
+        grads.densification_info = dinfo.data_ptr() if rows else None
+        grads.densification_rows = rows
+        alloc = _lib.WorkspaceAllocator(device, 'backward')
+    return _PreparedBackward(cs, keep, prims, grads, outputs, alloc)
 
 
 def _empty(device: torch.device, dtype=torch.float32) -> torch.Tensor:

@@ -155,3 +155,30 @@ def test_rasterize_neural_inference_matches_training_forward():
     train = efgs.diff_rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], torch.empty(0, device=dev), st,
                                 base_colors=inp['base_colors'], residual_params=inp['residual_params'], mlp_weights=inp['mlp_weights'])
     assert np.array_equal(hwc.cpu().numpy(), np.clip(train.detach().cpu().numpy(), 0, 1).transpose(1, 2, 0))
+
+def test_backward_twice_through_a_retained_graph():
+    """The backward's outputs are prepared during the forward; a second backward of the same graph
+    (retain_graph) gets fresh outputs, so the gradients the first one produced stay intact."""
+    import torch
+    import efgs
+    scene, app, cam = small_case(model='neural', n=400)
+    dev = torch.device('cuda:0')
+    configure(app)
+    inp = torch_inputs(scene, dev, requires_grad=True)
+    img = efgs.diff_rasterize(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], torch.empty(0, device=dev),
+                              settings(cam, dev), base_colors=inp['base_colors'], residual_params=inp['residual_params'],
+                              mlp_weights=inp['mlp_weights'])
+    g = torch.randn_like(img)
+    img.backward(g, retain_graph=True)
+    first = {k: v.grad.clone() for k, v in inp.items() if v is not None and v.grad is not None}
+    held = {k: v.grad for k, v in inp.items() if v is not None and v.grad is not None}
+    for v in inp.values():
+        if v is not None:
+            v.grad = None
+    img.backward(g)
+    torch.cuda.synchronize()
+    assert set(first) == {'means', 'scales', 'rotations', 'opacities', 'base_colors', 'residual_params', 'mlp_weights'}
+    for k in first:
+        assert torch.equal(inp[k].grad, first[k]), k
+        assert torch.equal(held[k], first[k]), k  # the first call's tensors were not written again
+        assert inp[k].grad.data_ptr() != held[k].data_ptr(), k
