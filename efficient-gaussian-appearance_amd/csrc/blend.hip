@@ -134,8 +134,9 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
             wave_lds_fence();
             const uint32_t n_max = max(max(n[0], n[1]), max(n[2], n[3]));
             const uint32_t my_n = pick_group(g, n[0], n[1], n[2], n[3]);
-            for (uint32_t k = 0; k < n_max; k++) {
-                const uint32_t jj = my_list[k];  // past the group's count: a stale entry, skipped
+            // two Gaussians of the group's list per step (list_len is even, so entry k + 1 exists; past the
+            // group's count it is a stale entry, skipped)
+            const auto walk = [&](uint32_t k, uint32_t jj) {
                 // branch-free: a skipped Gaussian gets weight 0, which leaves C and T bit for bit unchanged
                 float dx, dy, G;
                 const float alpha = eval_alpha(s_xy[jj], s_co[jj], pxf, pyf, dx, dy, G);
@@ -149,6 +150,11 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
                 T = T * (1.0f - a_t);
                 last = take ? start + jj + 1 : last;
                 done = done || (take && T < transmittance_threshold);
+            };
+            for (uint32_t k = 0; k < n_max; k += 2) {
+                const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);
+                walk(k, jab.x);
+                walk(k + 1, jab.y);
             }
             wave_lds_fence();
         }
