@@ -29,17 +29,42 @@ struct InstanceGrads {
     float gmx, gmy, gcx, gcy, gcz, gop, gr, gg, gb, gax, gay;
 };
 
-// sum of a visible primitive's per-instance gradient records, in emission order
-__device__ inline InstanceGrads reduce_instance_grads(const PreprocessBackwardArgs& a, uint32_t p, uint32_t touched) {
-    const float4* ig = reinterpret_cast<const float4*>(a.inst_grads) + 3 * static_cast<size_t>(a.prim_offset[p]);
+__device__ __forceinline__ void add_record(float4& s0, float4& s1, float4& s2, float4 t0, float4 t1, float4 t2) {
+    s0.x += t0.x; s0.y += t0.y; s0.z += t0.z; s0.w += t0.w;
+    s1.x += t1.x; s1.y += t1.y; s1.z += t1.z; s1.w += t1.w;
+    s2.x += t2.x; s2.y += t2.y; s2.z += t2.z;
+}
+
+// sum of a visible primitive's per-instance gradient records (starting at emission slot `offset`), in
+// emission order; two records are fetched per step so their loads are in flight together
+__device__ inline InstanceGrads reduce_instance_grads(const PreprocessBackwardArgs& a, uint32_t offset, uint32_t touched) {
+    const float4* ig = reinterpret_cast<const float4*>(a.inst_grads) + 3 * static_cast<size_t>(offset);
     float4 s0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = s0, s2 = s0;
-    for (uint32_t k = 0; k < touched; k++) {
+    uint32_t k = 0;
+    for (; k + 2 <= touched; k += 2) {
         const float4 t0 = ig[3 * k], t1 = ig[3 * k + 1], t2 = ig[3 * k + 2];
-        s0.x += t0.x; s0.y += t0.y; s0.z += t0.z; s0.w += t0.w;
-        s1.x += t1.x; s1.y += t1.y; s1.z += t1.z; s1.w += t1.w;
-        s2.x += t2.x; s2.y += t2.y; s2.z += t2.z;
+        const float4 u0 = ig[3 * k + 3], u1 = ig[3 * k + 4], u2 = ig[3 * k + 5];
+        add_record(s0, s1, s2, t0, t1, t2);
+        add_record(s0, s1, s2, u0, u1, u2);
     }
+    if (k < touched) add_record(s0, s1, s2, ig[3 * k], ig[3 * k + 1], ig[3 * k + 2]);
     return {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w, s2.x, s2.y, s2.z};
+}
+
+// a primitive's parameters, loaded before its instance records are summed so that every load is in flight at once
+struct GeometryInputs {
+    float3 mean, log_scale;
+    float4 rotation;
+    float raw_opacity;
+};
+
+__device__ __forceinline__ GeometryInputs load_geometry(const PreprocessBackwardArgs& a, uint32_t p) {
+    GeometryInputs g;
+    g.mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+    g.log_scale = make_float3(a.scales[3 * p], a.scales[3 * p + 1], a.scales[3 * p + 2]);
+    g.rotation = make_float4(a.rotations[4 * p], a.rotations[4 * p + 1], a.rotations[4 * p + 2], a.rotations[4 * p + 3]);
+    g.raw_opacity = a.cam.proper_aa ? a.opacities[p] : 0.0f;
+    return g;
 }
 
 __device__ inline void zero_primitive(const PreprocessBackwardArgs& a, uint32_t p) {
@@ -72,19 +97,19 @@ __device__ __forceinline__ void write_base_grad(const PreprocessBackwardArgs& a,
 }
 
 // 2D mean / conic / opacity gradients through the projection to the 3D mean, log-scales and quaternion
-__device__ inline void geometry_backward(const PreprocessBackwardArgs& a, uint32_t p, const PrimRecord& rec, const InstanceGrads& ig,
-                                         float3 dmean_color) {
-    const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+__device__ inline void geometry_backward(const PreprocessBackwardArgs& a, uint32_t p, const PrimRecord& rec, const GeometryInputs& gi,
+                                         const InstanceGrads& ig, float3 dmean_color) {
+    const float3 mean = gi.mean;
     const float gmx = ig.gmx, gmy = ig.gmy;
     const float3 gconic = make_float3(ig.gcx, ig.gcy, ig.gcz);
     const float* W = a.cam.w2c;
     const float depth = W[8] * mean.x + W[9] * mean.y + W[10] * mean.z + W[11];
     const float x = (W[0] * mean.x + W[1] * mean.y + W[2] * mean.z + W[3]) / depth;
     const float y = (W[4] * mean.x + W[5] * mean.y + W[6] * mean.z + W[7]) / depth;
-    const float v0 = ef_expf(2.0f * a.scales[3 * p]);
-    const float v1 = ef_expf(2.0f * a.scales[3 * p + 1]);
-    const float v2 = ef_expf(2.0f * a.scales[3 * p + 2]);
-    const float qr = a.rotations[4 * p], qx = a.rotations[4 * p + 1], qy = a.rotations[4 * p + 2], qz = a.rotations[4 * p + 3];
+    const float v0 = ef_expf(2.0f * gi.log_scale.x);
+    const float v1 = ef_expf(2.0f * gi.log_scale.y);
+    const float v2 = ef_expf(2.0f * gi.log_scale.z);
+    const float qr = gi.rotation.x, qx = gi.rotation.y, qy = gi.rotation.z, qz = gi.rotation.w;
     float qn;
     const Mat3 R = quaternion_to_rotation(qr, qx, qy, qz, qn);
     const Mat3 S = {R.m11 * v0, R.m12 * v1, R.m13 * v2, R.m21 * v0, R.m22 * v1, R.m23 * v2, R.m31 * v0, R.m32 * v1, R.m33 * v2};
@@ -118,7 +143,7 @@ __device__ inline void geometry_backward(const PreprocessBackwardArgs& a, uint32
 
     // opacity: stored opacity = sigmoid(raw) [* sqrt(det_raw / det) with proper antialiasing]
     if (a.cam.proper_aa) {
-        const float o = ef_sigmoid(a.opacities[p]);
+        const float o = ef_sigmoid(gi.raw_opacity);
         const float rad = fmaxf((a_raw * c_raw - bb) / det, 0.0f);
         a.g_opacities[p] = ig.gop * sqrtf(rad) * o * (1.0f - o);
     } else {
@@ -189,12 +214,14 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
     if (p >= a.n) return;
     const uint32_t touched = a.n_touched[p];
+    const uint32_t offset = a.prim_offset[p];
     if (touched == 0) {
         zero_primitive(a, p);
         return;
     }
-    const InstanceGrads ig = reduce_instance_grads(a, p, touched);
     const PrimRecord rec = a.records[p];
+    const GeometryInputs gi = load_geometry(a, p);
+    const InstanceGrads ig = reduce_instance_grads(a, offset, touched);
     float3 dmean_color = make_float3(0.0f, 0.0f, 0.0f);
 #if EFGS_MODEL == 0
     a.g_precomputed[3 * p] = ig.gr; a.g_precomputed[3 * p + 1] = ig.gg; a.g_precomputed[3 * p + 2] = ig.gb;
@@ -202,10 +229,9 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     {
         const float3 dpre = pre_activation_grad(rec, ig);
         write_base_grad(a, p, dpre, make_float3(0.0f, 0.0f, 0.0f));
-        const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
         const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
         float norm_rcp;
-        const float3 d = view_direction(mean, cam, norm_rcp);
+        const float3 d = view_direction(gi.mean, cam, norm_rcp);
         const float* rp = a.residual + static_cast<size_t>(p) * residual_params;
         float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
 #if EFGS_MODEL == 1
@@ -220,7 +246,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         for (uint32_t i = active_residual_params(a.cam.degree); i < residual_params; i++) gp[i] = 0.0f;
     }
 #endif
-    geometry_backward(a, p, rec, ig, dmean_color);
+    geometry_backward(a, p, rec, gi, ig, dmean_color);
 }
 
 #else  // neural: a geometry kernel (one thread per primitive) and an MLP kernel
@@ -240,16 +266,18 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     float m = 0.0f;
     if (p < a.n) {
         const uint32_t touched = a.n_touched[p];
+        const uint32_t offset = a.prim_offset[p];
         if (touched == 0) {
             zero_primitive(a, p);
         } else {
-            const InstanceGrads ig = reduce_instance_grads(a, p, touched);
             const PrimRecord rec = a.records[p];
+            const GeometryInputs gi = load_geometry(a, p);
+            const InstanceGrads ig = reduce_instance_grads(a, offset, touched);
             const float3 dpre = pre_activation_grad(rec, ig);
             write_base_grad(a, p, dpre, make_float3(0.0f, 0.0f, 0.0f));
             if (a.cam.degree == 0)
                 for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
-            geometry_backward(a, p, rec, ig, make_float3(0.0f, 0.0f, 0.0f));
+            geometry_backward(a, p, rec, gi, ig, make_float3(0.0f, 0.0f, 0.0f));
             reinterpret_cast<float4*>(a.color_grads)[p] = make_float4(dpre.x, dpre.y, dpre.z, 0.0f);
             m = fmaxf(fmaxf(fabsf(dpre.x), fabsf(dpre.y)), fabsf(dpre.z));
         }
