@@ -367,6 +367,55 @@ def cpu_baseline(sc: dict) -> dict:
                       f'through the C/numpy CPU restatement, single thread, no Adam; {seconds:.1f} s'}
 
 
+def cpu_unfused_appearance(sc: dict) -> dict:
+    """The reference's unfused PyTorch appearance evaluation (USE_FUSED_APPEARANCE false: AppearanceModel.forward,
+    Appearance/Base.py:83-108 with the per-model residual_colors) on the host CPU, as its restatement in
+    oracle/torch_ref.py: BASELINE configuration c0 (10k Gaussians, SH degree 3, colour sigmoid(base + residual(dir)),
+    forward) and the c3 scene's neural appearance (1M Gaussians, MLP with fp16-rounded weights, forward + backward
+    with respect to base, latents and weights)."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, 'oracle'))
+    import oracle as O
+    import torch_ref as TR
+    threads = torch.get_num_threads()
+    out = {'cores': threads, 'kind': 'reference (unfused appearance, restated in torch)'}
+    # c0: 10k Gaussians seen from a pinhole camera at the origin; DC ~ N(0, 0.5), higher bands ~ N(0, 0.05)
+    rng = np.random.default_rng(0)
+    n0 = 10_000
+    means = torch.tensor(rng.uniform(-2.0, 2.0, (n0, 3)) + np.array([0.0, 0.0, 5.0]), dtype=torch.float32)
+    base = torch.tensor(rng.normal(0.0, 0.5, (n0, 3)), dtype=torch.float32)
+    rest = torch.tensor(rng.normal(0.0, 0.05, (n0, 15, 3)), dtype=torch.float32)
+    app0 = O.Appearance(model='sh', base_act='none', res_act='none', color_act='sigmoid', direction_gradient=False, max_degree=3, mlp=None)
+    cam0 = torch.zeros(3)
+    reps = 50
+    TR.appearance_colors(means, cam0, base, rest, app0, 3)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        TR.appearance_colors(means, cam0, base, rest, app0, 3)
+    c0_s = (time.perf_counter() - t0) / reps
+    out['c0'] = {'value': round(n0 / c0_s / 1e6, 4), 'unit': 'Mprim/s', 'ms': round(c0_s * 1e3, 4),
+                 'sample': f'{n0} Gaussians, SH degree 3 (48 coefficients), sigmoid colour, forward, {reps} repetitions'}
+    # c3: the scene's neural appearance, forward + backward
+    app = sc['appearance']
+    mlp = O.MLPConfig(**app['mlp'])
+    oapp = O.Appearance(model='neural', base_act=app['base_act'], res_act=app['res_act'], color_act=app['color_act'],
+                        direction_gradient=app['direction_gradient'], max_degree=app['max_degree'], mlp=mlp)
+    m = torch.tensor(sc['means'])
+    b = torch.tensor(sc['base_colors']).requires_grad_(True)
+    r = torch.tensor(sc['residual_params']).requires_grad_(True)
+    w = torch.tensor(sc['mlp_weights']).requires_grad_(True)
+    cam = torch.tensor(np.asarray(sc['camera']['position'], np.float32))
+    t0 = time.perf_counter()
+    colors = TR.appearance_colors(m, cam, b, r, oapp, 1, mats=TR.mlp_matrices_torch(w, mlp))
+    colors.sum().backward()
+    c3_s = time.perf_counter() - t0
+    n3 = m.shape[0]
+    out['c3_neural'] = {'value': round(n3 / c3_s / 1e6, 4), 'unit': 'Mprim/s', 'ms': round(c3_s * 1e3, 2),
+                        'sample': f'{n3} Gaussians of the c3 scene, neural appearance (MLP 11-64-64-3), forward + backward'}
+    return out
+
+
 # ---------------------------------------------------------------------------------------------------------
 # c2: the neural decode in isolation
 # ---------------------------------------------------------------------------------------------------------
@@ -727,6 +776,8 @@ def main() -> None:
         'stages': r['stages'],
         'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(r['scene']),
     }
+    if not args.no_cpu_baseline and r['model'] == 'neural':
+        line['cpu_unfused_appearance'] = cpu_unfused_appearance(r['scene'])
     print(json.dumps(line), flush=True)
 
 
