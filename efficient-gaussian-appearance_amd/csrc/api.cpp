@@ -243,7 +243,6 @@ struct TileLayout {
 struct InstanceLayout {
     void* keys;              // tile key per emission slot
     uint32_t* inst_prim;     // primitive per emission slot
-    uint32_t* inst_depth;    // depth key of the primitive per emission slot (read in order by the bucket scatter)
     uint32_t* local_rank;    // rank of each instance within its histogram segment's slots of its tile
     uint32_t* table;         // per histogram segment and tile: the tile's count in the earlier segments
     uint64_t* bucket;        // sort keys grouped by tile (depth key << 32 | emission index)
@@ -258,7 +257,6 @@ struct InstanceLayout {
         const TileBinning plan = tile_binning_plan(static_cast<uint32_t>(n_instances), n_tiles);
         l.keys = c.take_bytes(key_bytes * ni);
         l.inst_prim = c.take<uint32_t>(ni);
-        l.inst_depth = c.take<uint32_t>(ni);
         l.local_rank = c.take<uint32_t>(plan.use_table ? ni : 1);
         l.table = c.take<uint32_t>(plan.use_table ? static_cast<uint64_t>(plan.blocks) * n_tiles : 1);
         l.bucket = c.take<uint64_t>(ni);
@@ -712,8 +710,8 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     const InstanceLayout il = InstanceLayout::carve(iblob, n_instances, key_bytes, n_tiles);
     const TileBinning plan = tile_binning_plan(n_instances, n_tiles);
     t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
-    if (!launch_create_instances(pl.visible_prims, pl.prim_offset, pl.n_touched, pl.records, pl.depth_keys, il.keys, key_bytes, il.inst_prim,
-                                 il.inst_depth, pl.counters, grid_w, n_visible, s))
+    if (!launch_create_instances(pl.visible_prims, pl.prim_offset, pl.n_touched, pl.records, il.keys, key_bytes, il.inst_prim, pl.counters, grid_w,
+                                 n_visible, s))
         return EFGS_ERR_HIP;
     t.end(s);
     const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.block_prefix, pl.counters + 5, tl.cursor};
@@ -721,7 +719,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     if (!launch_tile_counts(plan, il.keys, key_bytes, n_instances, il.local_rank, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
     t.end(s);
     t.begin(EFGS_STAGE_TILE_BUCKETS, s);
-    if (!launch_tile_buckets(plan, il.keys, key_bytes, il.inst_depth, il.table, il.local_rank, ts, il.bucket, n_instances, n_tiles, s))
+    if (!launch_tile_buckets(plan, il.keys, key_bytes, il.inst_prim, pl.depth_keys, il.table, il.local_rank, ts, il.bucket, n_instances, n_tiles, s))
         return EFGS_ERR_HIP;
     t.end(s);
     t.begin(EFGS_STAGE_TILE_SORT, s);

@@ -38,10 +38,10 @@ bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_
 // index order)
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,
                             hipStream_t s);
-// (tile key, primitive, primitive's depth key) at every emission slot
+// (tile key, primitive) at every emission slot
 bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, const uint32_t* n_touched, const PrimRecord* records,
-                             const uint32_t* depth_keys, void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* inst_depth, uint32_t* counters,
-                             uint32_t grid_w, uint32_t n_visible, hipStream_t s);
+                             void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w, uint32_t n_visible,
+                             hipStream_t s);
 // Tile binning: per-tile counts from LDS histograms over fixed segments of the emission slots (a table of
 // per-segment counts, scanned per tile) when the tile count fits the LDS, else from global atomics.
 constexpr size_t tile_hist_max_lds = 64 * 1024;  // default dynamic LDS limit of a launch
@@ -70,7 +70,8 @@ struct TileScan {
 bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* local_rank, uint32_t* table,
                         const TileScan& ts, uint32_t n_tiles, hipStream_t s);
 // every instance's sort key (depth key of its primitive << 32 | emission index) into a slot of its tile's range
-bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_depth, const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,
+bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
+                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,
                          uint32_t n_tiles, hipStream_t s);
 // per tile: [start, end) into ranges and its keys sorted ascending -> emission indices in sorted_inst, tile id
 // in sorted_keys

@@ -65,8 +65,7 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
 template <typename KeyT>
 __global__ __launch_bounds__(instance_block) void create_instances_kernel(const uint32_t* visible_prims, const uint32_t* prim_offset,
                                                                          const uint32_t* n_touched, const PrimRecord* records,
-                                                                         const uint32_t* depth_keys, KeyT* keys, uint32_t* inst_prim,
-                                                                         uint32_t* inst_depth, uint32_t* counters, uint32_t grid_w,
+                                                                         KeyT* keys, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w,
                                                                          uint32_t n_visible) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint64_t lanes_below = (1ull << lane) - 1ull;
@@ -77,7 +76,6 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
     const uint32_t off = prim_offset[p];
     const uint32_t n = n_touched[p];
     const PrimRecord rec = records[p];
-    const uint32_t dk = depth_keys[p];
     const uint32_t bx = __float_as_uint(rec.r2.y), by = __float_as_uint(rec.r2.z);
     const TileRect t = screen_to_tile_bounds(bx & 0xffffu, bx >> 16, by & 0xffffu, by >> 16);
     const uint32_t bw = t.x1 - t.x0;
@@ -92,7 +90,6 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
             if (k < n) {
                 keys[off + k] = static_cast<KeyT>(ty * grid_w + tx);
                 inst_prim[off + k] = p;
-                inst_depth[off + k] = dk;
             }
             k++;
         }
@@ -102,7 +99,7 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
         const uint32_t src = static_cast<uint32_t>(__ffsll(static_cast<long long>(coop)) - 1);
         coop &= coop - 1;
         const uint32_t c_x0 = __shfl(t.x0, src), c_y0 = __shfl(t.y0, src), c_bw = __shfl(bw, src), c_cnt = __shfl(cnt, src);
-        const uint32_t c_off = __shfl(off, src), c_n = __shfl(n, src), c_p = __shfl(p, src), c_dk = __shfl(dk, src);
+        const uint32_t c_off = __shfl(off, src), c_n = __shfl(n, src), c_p = __shfl(p, src);
         const float c_mx = __shfl(smx, src), c_my = __shfl(smy, src);
         const float c_cx = __shfl(cx, src), c_cy = __shfl(cy, src), c_cz = __shfl(cz, src), c_pt = __shfl(pt, src);
         uint32_t c_k = __shfl(k, src);
@@ -115,7 +112,6 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
             if (hit && pos < c_n) {
                 keys[c_off + pos] = static_cast<KeyT>(ty * grid_w + tx);
                 inst_prim[c_off + pos] = c_p;
-                inst_depth[c_off + pos] = c_dk;
             }
             c_k += static_cast<uint32_t>(__popcll(m));
         }
@@ -125,7 +121,6 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
         for (uint32_t j = (k < n ? k : n); j < n; j++) {
             keys[off + j] = static_cast<KeyT>(~static_cast<KeyT>(0));
             inst_prim[off + j] = p;
-            inst_depth[off + j] = dk;
         }
         atomicAdd(&counters[2], 1u);
     }
@@ -241,7 +236,7 @@ __device__ __forceinline__ uint32_t tile_start_of(const uint32_t* block_prefix, 
 // cursor (without one). The slot receives the instance's sort key, the depth key of its primitive above
 // its emission index.
 template <typename KeyT>
-__global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_depth,
+__global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
                                                           const uint32_t* table, const uint32_t* local_rank, uint32_t seg,
                                                           const uint32_t* block_prefix, const uint32_t* local_start, uint32_t* cursor,
                                                           uint64_t* bucket, uint32_t n_instances, uint32_t n_tiles) {
@@ -249,7 +244,7 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     if (e >= n_instances) return;
     const uint32_t t = static_cast<uint32_t>(keys[e]);
     if (t >= n_tiles) return;
-    const uint64_t key = (static_cast<uint64_t>(inst_depth[e]) << 32) | e;
+    const uint64_t key = (static_cast<uint64_t>(depth_keys[inst_prim[e]]) << 32) | e;
     const uint32_t pos = tile_start_of(block_prefix, local_start, t) +
                          (table ? table[static_cast<size_t>(e / seg) * n_tiles + t] + local_rank[e] : atomicAdd(&cursor[t], 1u));
     bucket[pos] = key;
@@ -460,18 +455,16 @@ bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_off
 }
 
 bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, const uint32_t* n_touched, const PrimRecord* records,
-                             const uint32_t* depth_keys, void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* inst_depth, uint32_t* counters,
-                             uint32_t grid_w, uint32_t n_visible, hipStream_t s) {
+                             void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w, uint32_t n_visible,
+                             hipStream_t s) {
     if (n_visible == 0) return true;
     const uint32_t blocks = div_up(n_visible, instance_block);
     if (key_bytes == 2)
-        create_instances_kernel<uint16_t><<<blocks, instance_block, 0, s>>>(visible_prims, prim_offset, n_touched, records, depth_keys,
-                                                                           static_cast<uint16_t*>(keys), inst_prim, inst_depth, counters, grid_w,
-                                                                           n_visible);
+        create_instances_kernel<uint16_t><<<blocks, instance_block, 0, s>>>(visible_prims, prim_offset, n_touched, records, static_cast<uint16_t*>(keys),
+                                                                           inst_prim, counters, grid_w, n_visible);
     else
-        create_instances_kernel<uint32_t><<<blocks, instance_block, 0, s>>>(visible_prims, prim_offset, n_touched, records, depth_keys,
-                                                                           static_cast<uint32_t*>(keys), inst_prim, inst_depth, counters, grid_w,
-                                                                           n_visible);
+        create_instances_kernel<uint32_t><<<blocks, instance_block, 0, s>>>(visible_prims, prim_offset, n_touched, records, static_cast<uint32_t*>(keys),
+                                                                           inst_prim, counters, grid_w, n_visible);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
@@ -508,16 +501,17 @@ bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes
     return true;
 }
 
-bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_depth, const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,
+bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
+                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,
                          uint32_t n_tiles, hipStream_t s) {
     if (n_instances == 0) return true;
     const uint32_t blocks = div_up(n_instances, 256);
     const uint32_t* tab = plan.use_table ? table : nullptr;
     if (key_bytes == 2)
-        tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_depth, tab, local_rank, plan.segment,
+        tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, plan.segment,
                                                             ts.block_prefix, ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
     else
-        tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_depth, tab, local_rank, plan.segment,
+        tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, plan.segment,
                                                             ts.block_prefix, ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
