@@ -183,14 +183,19 @@ __global__ __launch_bounds__(256) void tile_block_scan_kernel(uint32_t* table, u
     uint32_t count = 0;
     if (t < n_tiles) {
         if (table) {
-            for (uint32_t b0 = 0; b0 < n_segments; b0 += 8) {  // 8 loads in flight
-                uint32_t c[8];
+            // 32 loads in flight (addresses clamped to the last segment, so every load is unconditional): the
+            // grid is small (one thread per tile), so the column walk is bound by load latency
+            constexpr uint32_t in_flight = 32;
+            for (uint32_t b0 = 0; b0 < n_segments; b0 += in_flight) {
+                uint32_t c[in_flight];
 #pragma unroll
-                for (uint32_t k = 0; k < 8; k++) c[k] = b0 + k < n_segments ? table[static_cast<size_t>(b0 + k) * n_tiles + t] : 0u;
+                for (uint32_t k = 0; k < in_flight; k++) c[k] = table[static_cast<size_t>(min(b0 + k, n_segments - 1)) * n_tiles + t];
 #pragma unroll
-                for (uint32_t k = 0; k < 8; k++) {
-                    if (b0 + k < n_segments) table[static_cast<size_t>(b0 + k) * n_tiles + t] = count;
-                    count += c[k];
+                for (uint32_t k = 0; k < in_flight; k++) {
+                    if (b0 + k < n_segments) {
+                        table[static_cast<size_t>(b0 + k) * n_tiles + t] = count;
+                        count += c[k];
+                    }
                 }
             }
             totals[t] = count;
