@@ -1175,6 +1175,11 @@ int ngsplat_plan(const efgs_ngsplat_input* in, NgsplatPlan& p) {
     if (p.row_used > static_cast<int>(ng_max_row)) return fail(EFGS_ERR_INVALID_ARGUMENT, "more than 63 residual parameters per splat");
     if (p.row_used > in->residual_row_stride) return fail(EFGS_ERR_INVALID_ARGUMENT, "residual row stride smaller than the parameters read");
     if (in->residual_act < 0 || in->residual_act > 2) return fail(EFGS_ERR_INVALID_ARGUMENT, "invalid residual activation");
+    // the pack kernel stages 256 rows (stride row_used | 1) and, for a baked layer 0, the transposed matrix in LDS
+    const size_t lds = sizeof(float) * ((p.row_used ? static_cast<size_t>(ng_block) * (static_cast<uint32_t>(p.row_used) | 1u) : 0) +
+                                        (p.payload == EFGS_NGSPLAT_NEURAL_BAKED ? static_cast<size_t>(p.n_encoded) * ng_max_baked : 0));
+    if (lds > 65536)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "the per-splat parameters and the baked layer 0 need more than 64 KB of LDS per block");
     p.n_textures = ngsplat_texture_plan(p.payload, p.n_items, p.n_values, p.texel_words);
     return EFGS_OK;
 }

@@ -175,3 +175,34 @@ def test_workspace_allocator_bumps_aligns_and_falls_back():
     assert ws.requested == 256 + 512 + 768 + 256
     empty = _lib.Workspace(None, 0, 0, 0, None, None)
     assert _lib.lib.efgs_workspace_alloc(ctypes.byref(empty), 8) is None
+
+
+def test_ngsplat_layout_validation():
+    """efgs_ngsplat_layout plans the payload textures and rejects layouts the pack kernel cannot stage (host-side
+    checks: no GPU work)."""
+    import ctypes
+    from efgs import _lib
+    inp = _lib.NgsplatInput()
+    n_tex, words = ctypes.c_int(), (ctypes.c_int * 8)()
+
+    def plan(**kw):
+        for k, v in kw.items():
+            setattr(inp, k, v)
+        rc = _lib.lib.efgs_ngsplat_layout(ctypes.byref(inp), ctypes.byref(n_tex), words)
+        return rc, n_tex.value, list(words)[:n_tex.value]
+    assert plan(payload=2, n_items=15, residual_row_stride=45) == (0, 3, [2, 4, 4])   # SH degree 3: 7 / 8 / 6-bit levels
+    assert plan(payload=2, n_items=8, residual_row_stride=45) == (0, 2, [2, 4])
+    assert plan(payload=2, n_items=0, residual_row_stride=45) == (0, 0, [])
+    assert plan(payload=3, n_items=7, residual_row_stride=49)[:2] == (0, 7)          # SV: 49 fp16 values -> 7 textures
+    assert plan(payload=4, n_items=5, residual_row_stride=40)[:2] == (0, 8)          # NASG: 60 values
+    assert plan(payload=1, n_items=8, n_frequencies=1, n_neurons=16, residual_row_stride=8)[:2] == (0, 2)
+    for bad in (dict(payload=2, n_items=5, residual_row_stride=45),                   # incomplete SH degree
+                dict(payload=4, n_items=6, residual_row_stride=48),                   # 72 values > 64
+                dict(payload=0, n_items=20, n_frequencies=0, residual_row_stride=20), # stored features > 16
+                dict(payload=1, n_items=8, n_frequencies=1, n_neurons=20, residual_row_stride=8),
+                dict(payload=3, n_items=7, residual_row_stride=10),                   # stride below the parameters read
+                dict(payload=1, n_items=63, n_frequencies=2, n_neurons=16, residual_row_stride=63),  # > 64 KB of LDS
+                dict(payload=9, n_items=1, residual_row_stride=1)):
+        inp.payload, inp.n_items, inp.n_frequencies, inp.n_neurons, inp.residual_row_stride = 0, 0, 0, 0, 0
+        rc, _, _ = plan(**bad)
+        assert rc == 1, bad
