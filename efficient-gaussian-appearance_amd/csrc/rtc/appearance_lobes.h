@@ -50,7 +50,7 @@ __device__ inline float3 lobe_residual(const float* p, float3 d, uint32_t lobes)
         const float vzc = clampf(vz, -lobe_pole_limit, lobe_pole_limit);
         const float K = 0.5f * (vzc + 1.0f);
         const float Ke = lobe_eps + an * vx * vx / (1.0f - vzc * vzc);
-        const float E = powf(K, Ke);
+        const float E = expf(Ke * logf(K));  // K^Ke (K in (0, 1], Ke > 0)
         const float N = lambda * sqrtf(1.0f + an) / (lobe_two_pi * (1.0f + lobe_eps_norm - expf(-2.0f * lambda)));
         const float P = expf(2.0f * lambda * (E * K - 1.0f));
         float G = 1.0f;
@@ -84,13 +84,19 @@ __device__ inline float3 lobe_residual_backward(const float* p, float3 gc, float
         const float vzc = clampf(vz, -lobe_pole_limit, lobe_pole_limit);
         const float K = 0.5f * (vzc + 1.0f);
         const float om = 1.0f - vzc * vzc;
-        const float Ke = lobe_eps + an * vx * vx / om;
-        const float E = powf(K, Ke);
-        const float nd = lobe_two_pi * (1.0f + lobe_eps_norm - expf(-2.0f * lambda));
-        const float N = lambda * sqrtf(1.0f + an) / nd;
-        const float G = GABOR ? 0.5f * (1.0f + cosf(k * vx)) : 1.0f;
-        const float P = expf(2.0f * lambda * (E * K - 1.0f));
+        const float rom = 1.0f / om;
+        const float Ke = lobe_eps + an * vx * vx * rom;
         const float logK = logf(K);
+        const float E = expf(Ke * logK);  // K^Ke (K in (0, 1], Ke > 0)
+        const float em2l = expf(-2.0f * lambda);
+        const float nd = lobe_two_pi * (1.0f + lobe_eps_norm - em2l);
+        const float rnd = 1.0f / nd;
+        const float s1a = sqrtf(1.0f + an);
+        const float N = lambda * s1a * rnd;
+        float skv = 0.0f, ckv = 1.0f;
+        if (GABOR) sincosf(k * vx, &skv, &ckv);
+        const float G = GABOR ? 0.5f * (1.0f + ckv) : 1.0f;
+        const float P = expf(2.0f * lambda * (E * K - 1.0f));
         const bool valid = fabsf(vz) < lobe_pole_limit;
         const float pdf = vz >= lobe_pole_limit ? 1.0f : (valid ? P * E * G * N : 0.0f);
         gp[wo] = gc.x * pdf * residual_activation_grad<RES_ACT>(w0);
@@ -98,23 +104,21 @@ __device__ inline float3 lobe_residual_backward(const float* p, float3 gc, float
         gp[wo + 2] = gc.z * pdf * residual_activation_grad<RES_ACT>(w2);
         const float gpdf = valid ? (gc.x * w0 + gc.y * w1 + gc.z * w2) : 0.0f;
         const float dP_dl = P * 2.0f * (E * K - 1.0f);
-        const float s1a = sqrtf(1.0f + an);
-        const float dN_dl = (s1a * nd - lambda * s1a * 2.0f * lobe_two_pi * expf(-2.0f * lambda)) / (nd * nd);
+        const float dN_dl = (s1a * nd - lambda * s1a * 2.0f * lobe_two_pi * em2l) * (rnd * rnd);
         gp[3] = lu >= lobe_shape_limit ? 0.0f : gpdf * (dP_dl * E * G * N + P * E * G * dN_dl) * lambda;
-        const float dE_da = E * logK * (vx * vx / om);
+        const float dE_da = E * logK * (vx * vx * rom);
         const float dP_da = P * 2.0f * lambda * K * dE_da;
-        const float dN_da = (lambda / (2.0f * s1a)) / nd;
+        const float dN_da = lambda * rnd / (2.0f * s1a);
         gp[4] = au >= lobe_shape_limit ? 0.0f : gpdf * (dP_da * E * G * N + P * dE_da * G * N + P * E * G * dN_da) * an;
         float dG_dvx = 0.0f;
         if (GABOR) {
-            const float skv = sinf(k * vx);
             gp[5] = gpdf * (P * E * (-0.5f * skv * vx) * N) * lobe_freq_scale * (1.0f - tk * tk);
             dG_dvx = -0.5f * skv * k;
         }
-        const float dE_dvx = E * logK * (2.0f * an * vx / om);
+        const float dE_dvx = E * logK * (2.0f * an * vx * rom);
         const float dP_dvx = P * 2.0f * lambda * K * dE_dvx;
         const float gvx = gpdf * (dP_dvx * E * G * N + P * dE_dvx * G * N + P * E * dG_dvx * N);
-        const float dKe_dvz = an * vx * vx * 2.0f * vz / (om * om);
+        const float dKe_dvz = an * vx * vx * 2.0f * vz * (rom * rom);
         const float dE_dvz = E * (Ke / K) * 0.5f + E * logK * dKe_dvz;
         const float dP_dvz = P * 2.0f * lambda * (K * dE_dvz + E * 0.5f);
         const float gvz = gpdf * (dP_dvz * E * G * N + P * dE_dvz * G * N);
