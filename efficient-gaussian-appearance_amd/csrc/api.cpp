@@ -350,7 +350,7 @@ void kernel_source(const efgs_rasterizer* r, int model, const char* kind, std::s
     preamble += "#define EFGS_N_FREQUENCIES " + std::to_string(model == 5 ? r->mlp_n_frequencies : 0) + "u\n";
     preamble += "#define EFGS_SH_DEGREE_MASK " + std::to_string(model == 5 ? r->mlp_sh_mask : 0) + "u\n";
     preamble += "#define EFGS_BASE_INPUT " + std::string(model == 5 && r->mlp_base_input ? "1" : "0") + "\n";
-    files = {"efgs_common.h", "efgs_args.h"};
+    files = {"efgs_common.h", "efgs_args.h", "residual_rows.h"};
     switch (model) {
         case 1: files.push_back("appearance_sh.h"); break;
         case 2: files.push_back("appearance_sv.h"); break;

@@ -16,8 +16,6 @@
 namespace efgs {
 
 constexpr uint32_t preprocess_block = 256;
-constexpr uint32_t params_per_unit = EFGS_MODEL == 1 ? 3u : EFGS_MODEL == 2 ? 7u : EFGS_MODEL == 3 ? 8u : EFGS_MODEL == 4 ? 9u : 1u;
-constexpr uint32_t residual_params = EFGS_MODEL == 0 ? 0u : params_per_unit * EFGS_N_UNITS;
 
 __device__ __forceinline__ uint32_t active_residual_params(uint32_t degree) {
     if (EFGS_MODEL == 1) return 3u * ((degree + 1) * (degree + 1) - 1);
@@ -211,6 +209,60 @@ __device__ inline void geometry_backward(const PreprocessBackwardArgs& a, uint32
 
 extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
     using namespace efgs;
+#if EFGS_MODEL != 0
+    if constexpr (staged_rows) {
+        __shared__ float s_rows[preprocess_block * row_ld];
+        const uint32_t p0 = blockIdx.x * preprocess_block, p = p0 + threadIdx.x;
+        const bool active = p < a.n;
+        const uint32_t touched = active ? a.n_touched[p] : 0u;
+        const uint32_t offset = active ? a.prim_offset[p] : 0u;
+        const bool work = touched > 0;
+        PrimRecord rec{};
+        GeometryInputs gi{};
+        InstanceGrads ig{};
+        float3 dpre = make_float3(0.0f, 0.0f, 0.0f), d = dpre, dmean_color = dpre;
+        float norm_rcp = 0.0f;
+        if (work) {
+            rec = a.records[p];
+            gi = load_geometry(a, p);
+            ig = reduce_instance_grads(a, offset, touched);
+            dpre = pre_activation_grad(rec, ig);
+            write_base_grad(a, p, dpre, make_float3(0.0f, 0.0f, 0.0f));
+            const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
+            d = view_direction(gi.mean, cam, norm_rcp);
+        }
+        const uint32_t rows = p0 < a.n ? min(preprocess_block, a.n - p0) : 0u;
+        float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
+        for (uint32_t pass = 0; pass < n_passes; pass++) {
+            const uint32_t u0 = pass * pass_units;
+            const uint32_t nu = min(pass_units, static_cast<uint32_t>(EFGS_N_UNITS) - u0);
+            if (pass > 0) __syncthreads();  // every thread has read the previous pass's rows
+            stage_residual_rows<preprocess_block>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
+            __syncthreads();
+            if (work) {
+                const float* row = s_rows + threadIdx.x * row_ld;
+#if EFGS_MODEL == 1
+                dmean_color = sh_residual_backward<EFGS_RES_ACT>(row, dpre, gp, d, norm_rcp, a.cam.degree);
+#elif EFGS_MODEL == 2
+                dmean_color = sv_residual_backward<EFGS_RES_ACT>(row, dpre, gp, d, norm_rcp, a.cam.degree);
+#else
+                const uint32_t na = a.cam.degree > u0 ? min(nu, a.cam.degree - u0) : 0u;
+                const float3 dm = lobe_residual_backward<EFGS_RES_ACT, EFGS_MODEL == 4>(row, dpre, gp + u0 * params_per_unit, d, norm_rcp, na);
+                dmean_color.x += dm.x;
+                dmean_color.y += dm.y;
+                dmean_color.z += dm.z;
+#endif
+            }
+        }
+        if (work) {
+            for (uint32_t i = active_residual_params(a.cam.degree); i < residual_params; i++) gp[i] = 0.0f;
+            geometry_backward(a, p, rec, gi, ig, dmean_color);
+        } else if (active) {
+            zero_primitive(a, p);
+        }
+        return;
+    }
+#endif
     const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
     if (p >= a.n) return;
     const uint32_t touched = a.n_touched[p];

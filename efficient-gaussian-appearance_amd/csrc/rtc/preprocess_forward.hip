@@ -16,8 +16,6 @@ namespace efgs {
 
 constexpr uint32_t preprocess_block = 256;
 constexpr uint32_t n_sequential_tiles = 4;
-constexpr uint32_t params_per_unit = EFGS_MODEL == 1 ? 3u : EFGS_MODEL == 2 ? 7u : EFGS_MODEL == 3 ? 8u : EFGS_MODEL == 4 ? 9u : 1u;
-constexpr uint32_t residual_params = EFGS_MODEL == 0 ? 0u : params_per_unit * EFGS_N_UNITS;
 
 struct Projected {
     float mean2d_x, mean2d_y, conic_x, conic_y, conic_z, opacity, power_threshold, depth;
@@ -161,6 +159,12 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     __shared__ uint32_t wave_counts[4 * (preprocess_block / 64)];
+#if EFGS_MODEL >= 1 && EFGS_MODEL <= 4
+    // the forward stages its rows only for the lobe models: SH and SV read each row once and keep more waves per
+    // SIMD without the LDS
+    constexpr bool staged_forward = staged_rows && (EFGS_MODEL == 3 || EFGS_MODEL == 4);
+    __shared__ float s_rows[staged_forward ? preprocess_block * row_ld : 1];
+#endif
 #if EFGS_MODEL == 5
     // residual MLP weights staged once per block (padded rows); per-wave staging area for the input tiles
     extern __shared__ __align__(16) unsigned char smem[];
@@ -200,7 +204,33 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
                               residual_activation<EFGS_RES_ACT>(y[2]));
         }
 #endif
-        if (visible) {
+#if EFGS_MODEL >= 1 && EFGS_MODEL <= 4
+        if constexpr (staged_forward) {
+            // the chunk's rows through LDS (the previous chunk ended at a block barrier), one pass per unit range
+            const uint32_t p0 = chunk * preprocess_block;
+            const uint32_t rows = min(preprocess_block, a.n - p0);
+            for (uint32_t pass = 0; pass < n_passes; pass++) {
+                const uint32_t u0 = pass * pass_units;
+                const uint32_t nu = min(pass_units, static_cast<uint32_t>(EFGS_N_UNITS) - u0);
+                if (pass > 0) __syncthreads();  // every thread has read the previous pass's rows
+                stage_residual_rows<preprocess_block>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
+                __syncthreads();
+                if (visible) {
+                    const float* row = s_rows + threadIdx.x * row_ld;
+#if EFGS_MODEL == 1
+                    res = sh_residual<EFGS_RES_ACT>(row, d, a.cam.degree);
+#elif EFGS_MODEL == 2
+                    res = sv_residual<EFGS_RES_ACT>(row, d, a.cam.degree);
+#else
+                    const uint32_t na = a.cam.degree > u0 ? min(nu, a.cam.degree - u0) : 0u;
+                    const float3 r = lobe_residual<EFGS_RES_ACT, EFGS_MODEL == 4>(row, d, na);
+                    res.x += r.x;
+                    res.y += r.y;
+                    res.z += r.z;
+#endif
+                }
+            }
+        } else if (visible) {
 #if EFGS_MODEL == 1
             res = sh_residual<EFGS_RES_ACT>(rp, d, a.cam.degree);
 #elif EFGS_MODEL == 2
@@ -210,6 +240,9 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
 #elif EFGS_MODEL == 4
             res = lobe_residual<EFGS_RES_ACT, true>(rp, d, a.cam.degree);
 #endif
+        }
+#endif
+        if (visible) {
             const float b0 = base_activation<EFGS_BASE_ACT>(a.base[3 * p]);
             const float b1 = base_activation<EFGS_BASE_ACT>(a.base[3 * p + 1]);
             const float b2 = base_activation<EFGS_BASE_ACT>(a.base[3 * p + 2]);

@@ -1,0 +1,39 @@
+// Per-primitive residual parameters of the preprocess kernels: their count and the LDS staging of a block's rows.
+#pragma once
+
+namespace efgs {
+
+// floats per appearance unit (SH coefficient rgb, SV site, NASG lobe, NASGabor lobe) and per primitive
+constexpr uint32_t params_per_unit = EFGS_MODEL == 1 ? 3u : EFGS_MODEL == 2 ? 7u : EFGS_MODEL == 3 ? 8u : EFGS_MODEL == 4 ? 9u : 1u;
+constexpr uint32_t residual_params = EFGS_MODEL == 0 ? 0u : params_per_unit * EFGS_N_UNITS;
+
+// Residual rows of a block staged through LDS with coalesced loads (a thread's own row is 45-72 floats apart from
+// its neighbours', so direct per-thread reads spread every load instruction of a wave over 64 cache lines). Whole
+// units per pass: SH (coefficients) and SV (sites: the softmax needs them all) in one pass, lobes in passes of at
+// most 40 floats; a layout that does not fit reads its rows directly.
+constexpr uint32_t stage_max_floats = EFGS_MODEL == 1 || EFGS_MODEL == 2 ? 63u : 40u;
+constexpr uint32_t stage_units_fit = params_per_unit > 0 ? stage_max_floats / params_per_unit : 0u;
+constexpr uint32_t pass_units = EFGS_MODEL == 1 || EFGS_MODEL == 2 ? EFGS_N_UNITS
+                                                                   : (stage_units_fit < EFGS_N_UNITS ? stage_units_fit : EFGS_N_UNITS);
+constexpr bool staged_rows = EFGS_MODEL != 0 && EFGS_N_UNITS > 0 && pass_units > 0 && pass_units * params_per_unit <= stage_max_floats;
+constexpr uint32_t row_ld = (pass_units * params_per_unit) | 1u;
+constexpr uint32_t n_passes = pass_units > 0 ? (EFGS_N_UNITS + pass_units - 1) / pass_units : 0u;
+
+// rows [p0, p0 + rows), floats [f0, f0 + floats) of each, into s[r * row_ld + c] by the BLOCK threads of the block;
+// (r, c) advance by (BLOCK / floats, BLOCK % floats) per step, eight loads in flight
+template <uint32_t BLOCK>
+__device__ __forceinline__ void stage_residual_rows(const float* residual, uint32_t p0, uint32_t rows, uint32_t f0, uint32_t floats, float* s) {
+    const uint32_t total = rows * floats, dr = BLOCK / floats, dc = BLOCK - dr * floats;
+    uint32_t r = threadIdx.x / floats, c = threadIdx.x - r * floats;
+#pragma unroll 8
+    for (uint32_t i = threadIdx.x; i < total; i += BLOCK) {
+        s[r * row_ld + c] = residual[static_cast<size_t>(p0 + r) * residual_params + f0 + c];
+        c += dc;
+        r += dr;
+        const bool wrap = c >= floats;
+        c = wrap ? c - floats : c;
+        r = wrap ? r + 1 : r;
+    }
+}
+
+}  // namespace efgs
