@@ -65,7 +65,7 @@ __device__ __forceinline__ GeometryInputs load_geometry(const PreprocessBackward
     return g;
 }
 
-__device__ inline void zero_primitive(const PreprocessBackwardArgs& a, uint32_t p) {
+__device__ inline void zero_primitive(const PreprocessBackwardArgs& a, uint32_t p, bool residual = true) {
     a.g_means[3 * p] = 0.0f; a.g_means[3 * p + 1] = 0.0f; a.g_means[3 * p + 2] = 0.0f;
     a.g_scales[3 * p] = 0.0f; a.g_scales[3 * p + 1] = 0.0f; a.g_scales[3 * p + 2] = 0.0f;
     a.g_rotations[4 * p] = 0.0f; a.g_rotations[4 * p + 1] = 0.0f; a.g_rotations[4 * p + 2] = 0.0f; a.g_rotations[4 * p + 3] = 0.0f;
@@ -74,7 +74,8 @@ __device__ inline void zero_primitive(const PreprocessBackwardArgs& a, uint32_t 
     a.g_precomputed[3 * p] = 0.0f; a.g_precomputed[3 * p + 1] = 0.0f; a.g_precomputed[3 * p + 2] = 0.0f;
 #else
     a.g_base[3 * p] = 0.0f; a.g_base[3 * p + 1] = 0.0f; a.g_base[3 * p + 2] = 0.0f;
-    for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
+    if (residual)
+        for (uint32_t i = 0; i < residual_params; i++) a.g_residual[static_cast<size_t>(p) * residual_params + i] = 0.0f;
 #endif
 }
 
@@ -239,26 +240,39 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             if (pass > 0) __syncthreads();  // every thread has read the previous pass's rows
             stage_residual_rows<preprocess_block>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
             __syncthreads();
+#if EFGS_MODEL == 1 || EFGS_MODEL == 2
             if (work) {
                 const float* row = s_rows + threadIdx.x * row_ld;
 #if EFGS_MODEL == 1
                 dmean_color = sh_residual_backward<EFGS_RES_ACT>(row, dpre, gp, d, norm_rcp, a.cam.degree);
-#elif EFGS_MODEL == 2
-                dmean_color = sv_residual_backward<EFGS_RES_ACT>(row, dpre, gp, d, norm_rcp, a.cam.degree);
 #else
-                const uint32_t na = a.cam.degree > u0 ? min(nu, a.cam.degree - u0) : 0u;
-                const float3 dm = lobe_residual_backward<EFGS_RES_ACT, EFGS_MODEL == 4>(row, dpre, gp + u0 * params_per_unit, d, norm_rcp, na);
+                dmean_color = sv_residual_backward<EFGS_RES_ACT>(row, dpre, gp, d, norm_rcp, a.cam.degree);
+#endif
+            }
+#else
+            // lobes: a lobe's parameters are read before its gradients are written, so the gradients replace the
+            // staged row in place (zero for inactive lobes and for primitives without instances) and leave with
+            // coalesced stores
+            float* row = s_rows + threadIdx.x * row_ld;
+            const uint32_t na = work && a.cam.degree > u0 ? min(nu, a.cam.degree - u0) : 0u;
+            if (work) {
+                const float3 dm = lobe_residual_backward<EFGS_RES_ACT, EFGS_MODEL == 4>(row, dpre, row, d, norm_rcp, na);
                 dmean_color.x += dm.x;
                 dmean_color.y += dm.y;
                 dmean_color.z += dm.z;
-#endif
             }
+            for (uint32_t i = na * params_per_unit; i < nu * params_per_unit; i++) row[i] = 0.0f;
+            __syncthreads();
+            store_residual_rows<preprocess_block>(s_rows, p0, rows, u0 * params_per_unit, nu * params_per_unit, a.g_residual);
+#endif
         }
         if (work) {
+#if EFGS_MODEL == 1 || EFGS_MODEL == 2
             for (uint32_t i = active_residual_params(a.cam.degree); i < residual_params; i++) gp[i] = 0.0f;
+#endif
             geometry_backward(a, p, rec, gi, ig, dmean_color);
         } else if (active) {
-            zero_primitive(a, p);
+            zero_primitive(a, p, EFGS_MODEL == 1 || EFGS_MODEL == 2);
         }
         return;
     }

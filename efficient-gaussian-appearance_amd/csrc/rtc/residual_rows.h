@@ -36,4 +36,20 @@ __device__ __forceinline__ void stage_residual_rows(const float* residual, uint3
     }
 }
 
+// the reverse of stage_residual_rows: s[r * row_ld + c] to rows [p0, p0 + rows), floats [f0, f0 + floats) of `out`
+template <uint32_t BLOCK>
+__device__ __forceinline__ void store_residual_rows(const float* s, uint32_t p0, uint32_t rows, uint32_t f0, uint32_t floats, float* out) {
+    const uint32_t total = rows * floats, dr = BLOCK / floats, dc = BLOCK - dr * floats;
+    uint32_t r = threadIdx.x / floats, c = threadIdx.x - r * floats;
+#pragma unroll 8
+    for (uint32_t i = threadIdx.x; i < total; i += BLOCK) {
+        out[static_cast<size_t>(p0 + r) * residual_params + f0 + c] = s[r * row_ld + c];
+        c += dc;
+        r += dr;
+        const bool wrap = c >= floats;
+        c = wrap ? c - floats : c;
+        r = wrap ? r + 1 : r;
+    }
+}
+
 }  // namespace efgs
