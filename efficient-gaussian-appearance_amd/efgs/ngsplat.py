@@ -27,7 +27,7 @@ from typing import Any
 import numpy as np
 import torch
 
-from ._lib import ALLOC_FN, NgsplatInput, NgsplatOutput, WorkspaceAllocator, check, lib
+from ._lib import NgsplatInput, NgsplatOutput, WorkspaceAllocator, check, lib
 
 SH_C0 = 0.28209479177387814
 TEX_WIDTH = 2048

@@ -16,13 +16,12 @@ Pins of the oracle's restatement of viewer/export_ngsplat.py:
   - header fields written by the oracle come back through the viewer's parser (viewer/utils.js:230-330).
 """
 import math
-import struct
 
 import numpy as np
 import pytest
 
 from efgs import ngsplat as NG
-from efgs.synthetic import NGSPLAT_NEURAL_CASES as NEURAL_CASES, NGSPLAT_OTHER_CASES as OTHER_CASES, mlp_flat
+from efgs.synthetic import NGSPLAT_NEURAL_CASES as NEURAL_CASES, mlp_flat
 from efgs.synthetic import ngsplat_model as make_case
 import ngsplat_oracle as ON
 
