@@ -72,14 +72,15 @@ __device__ __forceinline__ uint32_t pick_group(uint32_t g, uint32_t j0, uint32_t
 }
 
 // Writes each group's surviving Gaussians of the chunk, in order, to list[k * list_len + 0 .. n[k]) (entry:
-// base + lane of the Gaussian); n[k] = popcount(m[k]). A group then walks its list with one LDS read per
-// step instead of scanning a 64-bit mask per lane.
+// (base + lane) << shift for the Gaussian, a batch index or, shifted, a byte offset into 16-byte staged arrays);
+// n[k] = popcount(m[k]). A group then walks its list with one LDS read per step instead of scanning a 64-bit
+// mask per lane.
 __device__ __forceinline__ void build_group_lists(const uint64_t (&m)[4], uint32_t lane, uint32_t base, uint32_t* list,
-                                                  uint32_t list_len, uint32_t (&n)[4]) {
+                                                  uint32_t list_len, uint32_t (&n)[4], uint32_t shift = 0) {
 #pragma unroll
     for (uint32_t k = 0; k < 4; k++) {
         const uint32_t lo = static_cast<uint32_t>(m[k]), hi = static_cast<uint32_t>(m[k] >> 32);
-        if ((m[k] >> lane) & 1u) list[k * list_len + __builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u))] = base + lane;
+        if ((m[k] >> lane) & 1u) list[k * list_len + __builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u))] = (base + lane) << shift;
         n[k] = static_cast<uint32_t>(__popcll(m[k]));
     }
 }
@@ -126,29 +127,33 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
         }
         __syncthreads();
         const uint32_t batch_n = min(tile_pixels, n_total - start);
+        // byte offset of the last Gaussian of this batch the pixel took (~0: none); the last-contributor index
+        // start + offset / 16 + 1 is formed once per batch
+        uint32_t last_off = ~0u;
         for (uint32_t c0 = 0; c0 < batch_n; c0 += 64) {
             uint64_t m[4];
             cull_groups(rect_of(s_xy[c0 + lane]), c0 + lane < batch_n, bx0, by0, by1, m);
             uint32_t n[4];
-            build_group_lists(m, lane, c0, &s_list[wave][0][0], list_len, n);
+            build_group_lists(m, lane, c0, &s_list[wave][0][0], list_len, n, 4u);  // entries: byte offsets of the staged float4s
             wave_lds_fence();
             const uint32_t n_max = max(max(n[0], n[1]), max(n[2], n[3]));
             const uint32_t my_n = pick_group(g, n[0], n[1], n[2], n[3]);
             // two Gaussians of the group's list per step (list_len is even, so entry k + 1 exists; past the
             // group's count it is a stale entry, skipped)
-            const auto walk = [&](uint32_t k, uint32_t jj) {
+            const auto walk = [&](uint32_t k, uint32_t off) {
+                const auto at = [off](const float4* arr) { return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(arr) + off); };
                 // branch-free: a skipped Gaussian gets weight 0, which leaves C and T bit for bit unchanged
                 float dx, dy, G;
-                const float alpha = eval_alpha(s_xy[jj], s_co[jj], pxf, pyf, dx, dy, G);
+                const float alpha = eval_alpha(at(s_xy), at(s_co), pxf, pyf, dx, dy, G);
                 const bool take = k < my_n && !done && alpha >= min_alpha;
                 const float a_t = take ? alpha : 0.0f;
                 const float w = T * a_t;
-                const float4 col = s_col[jj];
+                const float4 col = at(s_col);
                 cr = __builtin_fmaf(w, col.x, cr);
                 cg = __builtin_fmaf(w, col.y, cg);
                 cb = __builtin_fmaf(w, col.z, cb);
                 T = T * (1.0f - a_t);
-                last = take ? start + jj + 1 : last;
+                last_off = take ? off : last_off;
                 done = done || (take && T < transmittance_threshold);
             };
             for (uint32_t k = 0; k < n_max; k += 2) {
@@ -158,6 +163,7 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
             }
             wave_lds_fence();
         }
+        if (last_off != ~0u) last = start + (last_off >> 4) + 1u;
     }
     const uint32_t slot = tile * tile_pixels + tid;
     if (inside) {
