@@ -262,7 +262,8 @@ __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOM
 // Per-tile sort: one wave per tile, four tiles per block, no block barriers. Keys are unique 64-bit values
 // (depth key << 32 | emission index), sorted ascending by bitonic networks:
 //   n <= 64, 128, 256 in registers, K = 1, 2, 4 keys per lane (element x = K lane + i): exchanges at distance
-//                     j < K within a lane, j >= K with the lane at xor distance j / K;
+//                     j < K within a lane, j >= K with the lane at xor distance j / K (128 < n <= 192: a
+//                     128-key and a 64-key network merged by rank);
 //   256 < n <= 512    in the wave's LDS slab;
 //   n > 512           chunks of 512 sorted in the slab and written back to the tile's range, then every key
 //                     placed at (its index in its chunk) + (its rank in each other chunk).
@@ -354,6 +355,38 @@ __device__ __forceinline__ uint32_t rank_in(const uint64_t* run, uint32_t n, uin
     return lo;
 }
 
+// 128 < n <= 192: the first 128 keys (two per lane) and the other n - 128 (one per lane) are sorted by their own
+// register networks and merged: a key's position is its index in its own sorted part plus the number of keys of
+// the other part below it (keys are unique), found by binary search in the wave's slab. About half the work of
+// the 256-key network the run would otherwise be padded to.
+template <typename KeyT>
+__device__ __forceinline__ void sort_run_split192(const uint64_t* run, uint32_t n, uint32_t* out, KeyT* out_keys, uint32_t tile,
+                                                  uint32_t lane, uint64_t* s) {
+    uint64_t a[2], b[1];
+    a[0] = run[2 * lane];
+    a[1] = run[2 * lane + 1];
+    b[0] = 128 + lane < n ? run[128 + lane] : ~0ull;
+    wave_bitonic<2>(a, lane);
+    wave_bitonic<1>(b, lane);
+    s[2 * lane] = a[0];
+    s[2 * lane + 1] = a[1];
+    s[128 + lane] = b[0];
+    wave_lds_fence();
+    const uint32_t nb = n - 128;
+#pragma unroll
+    for (uint32_t i = 0; i < 2; i++) {
+        const uint32_t pos = 2 * lane + i + rank_in(s + 128, nb, a[i]);
+        out[pos] = static_cast<uint32_t>(a[i]);
+        out_keys[pos] = static_cast<KeyT>(tile);
+    }
+    if (lane < nb) {
+        const uint32_t pos = lane + rank_in(s, 128, b[0]);
+        out[pos] = static_cast<uint32_t>(b[0]);
+        out_keys[pos] = static_cast<KeyT>(tile);
+    }
+    wave_lds_fence();  // the slab is free again only after every lane's searches
+}
+
 template <typename KeyT>
 __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* totals, const uint32_t* block_prefix,
                                                                    const uint32_t* local_start, uint2* ranges, uint64_t* bucket,
@@ -378,11 +411,15 @@ __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32
         sort_run_in_registers<2>(run, n, out, out_keys, tile, lane);
         return;
     }
+    uint64_t* s = s_slab[wave];
+    if (n <= 192) {
+        sort_run_split192(run, n, out, out_keys, tile, lane, s);
+        return;
+    }
     if (n <= 256) {
         sort_run_in_registers<4>(run, n, out, out_keys, tile, lane);
         return;
     }
-    uint64_t* s = s_slab[wave];
     if (n <= wave_slab) {
         uint32_t m = 512;
         while (m < n) m <<= 1;
