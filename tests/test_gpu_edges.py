@@ -182,3 +182,30 @@ def test_backward_twice_through_a_retained_graph():
         assert torch.equal(inp[k].grad, first[k]), k
         assert torch.equal(held[k], first[k]), k  # the first call's tensors were not written again
         assert inp[k].grad.data_ptr() != held[k].data_ptr(), k
+
+
+@pytest.mark.parametrize('n_total', [1_500_000, 1_900_000])
+def test_block_count_scan_at_large_primitive_counts(n_total):
+    # The per-block count scan over 5860 / 7422 preprocess blocks (several blocks per scan thread): the same
+    # 400 visible primitives, spread through a scene padded with primitives behind the camera, must render
+    # exactly as the 400 alone (same visible set, order and keys).
+    scene, app, cam = small_case(model='sh', n=400)
+    m = len(scene.means)
+    slots = np.linspace(17, n_total - 5, m).astype(np.int64)
+    src = np.arange(n_total) % m
+
+    def pad(a):
+        out = a[src].copy()
+        out[slots] = a
+        return out
+    means = pad(scene.means)
+    hidden = np.ones(n_total, bool)
+    hidden[slots] = False
+    means[hidden, 2] = -50.0
+    big = O.Scene(means=means, scales=pad(scene.scales), rotations=pad(scene.rotations), opacities=pad(scene.opacities),
+                  base_colors=pad(scene.base_colors), residual_params=pad(scene.residual_params))
+    small_img, small_frame, _ = _render(scene, app, cam)
+    big_img, big_frame, _ = _render(big, app, cam)
+    assert small_frame.n_visible > 0
+    assert (big_frame.n_visible, big_frame.n_instances) == (small_frame.n_visible, small_frame.n_instances)
+    np.testing.assert_array_equal(big_img, small_img)
