@@ -1041,6 +1041,12 @@ void efo_adam_step(int n, const float* grad, float* param, float* m, float* v, i
 /* rest-band SH basis values (15) of a unit direction, band order of appearance_sh.cuh:43-61 */
 int efo_sh_rest_basis(const float* dir, int degree, float* out) { return sh_rest_basis(dir, degree, out); }
 
+/* rotation matrix (row-major 3x3) of an unnormalised (w, x, y, z) quaternion as preprocess forms it, and |q|^2 */
+void efo_quat_to_rot(const float* q, float* out, float* norm_sq) {
+    const mat3 R = quat_to_rot(q, norm_sq);
+    memcpy(out, &R, sizeof(R));
+}
+
 /* activated residual colour of one primitive for the SH / SV / NASG / NASGabor models */
 void efo_residual(const efo_app* a, const float* params, const float* dir, int degree, float* out) {
     switch (a->model) {

@@ -700,6 +700,14 @@ def sh_rest_basis(direction, degree: int) -> np.ndarray:
     return out[:n]
 
 
+def quat_to_rot(q) -> tuple[np.ndarray, float]:
+    """Rotation matrix of an unnormalised (w, x, y, z) quaternion as the preprocess forms it, and |q|^2."""
+    out = np.zeros(9, np.float32)
+    nsq = np.zeros(1, np.float32)
+    lib().efo_quat_to_rot(_p(_f32(q)), _p(out), _p(nsq))
+    return out.reshape(3, 3), float(nsq[0])
+
+
 def residual(app: 'Appearance', params: np.ndarray, direction, degree: int) -> np.ndarray:
     out = np.zeros(3, np.float32)
     lib().efo_residual(ctypes.byref(app.c_struct()), _p(_f32(params).reshape(-1)), _p(_f32(direction)), ctypes.c_int(degree), _p(out))

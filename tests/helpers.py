@@ -50,6 +50,27 @@ def small_case(model='sh', n=500, width=64, height=48, seed=0, scale_shift=2.0, 
     return scene, app, cam
 
 
+def single_tile_state(mean2d, conic_opacity, color, bg):
+    """Forward state of one 16 x 12 tile whose instances are the given 2D Gaussians in order."""
+    import ctypes
+    from types import SimpleNamespace
+    k = mean2d.shape[0]
+    W, H = 16, 12
+    ranges = np.array([0, k], np.uint32)
+    inst = np.arange(k, dtype=np.uint32)
+    bounds = np.tile(np.array([0, W, 0, H], np.uint16), (k, 1))
+    image = np.zeros((3, H, W), np.float32)
+    final_T = np.zeros(H * W, np.float32)
+    n_contrib = np.zeros(H * W, np.uint32)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    O.lib().efo_blend_forward(ctypes.c_int(W), ctypes.c_int(H), ctypes.c_int(1), ctypes.c_int(1), p(ranges), p(inst), p(bounds), p(mean2d),
+                              p(conic_opacity), p(color), p(bg), p(image), p(final_T), p(n_contrib))
+    cam = SimpleNamespace(width=W, height=H, bg=bg, grid=lambda: (1, 1))
+    fw = SimpleNamespace(n_touched=np.ones(k, np.uint32), ranges=ranges, inst_prims=inst, mean2d=mean2d, conic_opacity=conic_opacity,
+                         color=color, image=image, final_T=final_T, n_contrib=n_contrib)
+    return cam, fw
+
+
 def rel_l2(a, b) -> float:
     a = np.asarray(a, np.float64).ravel()
     b = np.asarray(b, np.float64).ravel()

@@ -18,7 +18,7 @@ import torch
 
 import oracle as O
 import torch_ref as TR
-from helpers import small_case, rel_l2
+from helpers import small_case, rel_l2, single_tile_state
 
 
 def _ulps(got, ref):
@@ -414,27 +414,6 @@ def test_relocation_closed_forms():
 # pruning scores (B/rasterization/include/kernels_pruning_scores.cuh:11-171)
 # ---------------------------------------------------------------------------------------------------------
 
-def _single_tile_state(mean2d, conic_opacity, color, bg):
-    """Forward state of one 16 x 12 tile whose instances are the given 2D Gaussians in order."""
-    import ctypes
-    from types import SimpleNamespace
-    k = mean2d.shape[0]
-    W, H = 16, 12
-    ranges = np.array([0, k], np.uint32)
-    inst = np.arange(k, dtype=np.uint32)
-    bounds = np.tile(np.array([0, W, 0, H], np.uint16), (k, 1))
-    image = np.zeros((3, H, W), np.float32)
-    final_T = np.zeros(H * W, np.float32)
-    n_contrib = np.zeros(H * W, np.uint32)
-    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
-    O.lib().efo_blend_forward(ctypes.c_int(W), ctypes.c_int(H), ctypes.c_int(1), ctypes.c_int(1), p(ranges), p(inst), p(bounds), p(mean2d),
-                              p(conic_opacity), p(color), p(bg), p(image), p(final_T), p(n_contrib))
-    cam = SimpleNamespace(width=W, height=H, bg=bg, grid=lambda: (1, 1))
-    fw = SimpleNamespace(n_touched=np.ones(k, np.uint32), ranges=ranges, inst_prims=inst, mean2d=mean2d, conic_opacity=conic_opacity,
-                         color=color, image=image, final_T=final_T, n_contrib=n_contrib)
-    return cam, fw
-
-
 def _random_2d_gaussians(rng, k):
     mean2d = rng.uniform([1.0, 1.0], [15.0, 11.0], (k, 2)).astype(np.float32)
     co = np.zeros((k, 4), np.float32)
@@ -455,7 +434,7 @@ def test_pruning_scores_match_autograd():
     k = 6
     mean2d, co, color = _random_2d_gaussians(rng, k)
     bg = np.array([0.2, 0.5, 0.1], np.float32)
-    cam, fw = _single_tile_state(mean2d, co, color, bg)
+    cam, fw = single_tile_state(mean2d, co, color, bg)
     got = O.pruning_scores(cam, fw)
     log2e = 1.44269504089
     ys, xs = np.mgrid[0:12, 0:16]
@@ -489,7 +468,7 @@ def test_pruning_score_single_gaussian_closed_form():
     co = np.array([[0.3, 0.02, 0.4, 0.7]], np.float32)
     color = np.array([[0.9, 0.4, 0.3]], np.float32)
     bg = np.array([0.1, 0.2, 0.3], np.float32)
-    cam, fw = _single_tile_state(mean2d, co, color, bg)
+    cam, fw = single_tile_state(mean2d, co, color, bg)
     n_pix = int((fw.n_contrib == 1).sum())
     assert 0 < n_pix < 192
     got = O.pruning_scores(cam, fw)
