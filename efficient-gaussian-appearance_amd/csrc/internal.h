@@ -39,7 +39,7 @@ bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,
                             hipStream_t s);
 // (tile key, primitive) at every emission slot
-bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, const uint32_t* n_touched, const PrimRecord* records,
+bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, uint32_t* n_touched, const PrimRecord* records,
                              void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w, uint32_t n_visible,
                              hipStream_t s);
 // Tile binning: per-tile counts from LDS histograms over fixed segments of the emission slots (a table of

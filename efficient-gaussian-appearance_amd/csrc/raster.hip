@@ -61,10 +61,12 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
 // rectangle that passes the contribution test, the first 4 tiles per lane and larger footprints
 // wave-cooperatively (64 tiles per step, positions from ballot prefix counts). Emission slots are
 // [prim_offset, prim_offset + n_touched); a count that disagrees with the preprocess is clamped to that
-// range, the remainder padded with an out-of-range key (never bucketed) and counted in counters[2].
+// range, the remainder padded with an out-of-range key (never bucketed) and counted in counters[2]. A primitive
+// that emitted fewer tiles than counted gets n_touched lowered to the emitted count, so the per-primitive sums of
+// the backward and of the pruning scores cover only slots that a blend kernel writes.
 template <typename KeyT>
 __global__ __launch_bounds__(instance_block) void create_instances_kernel(const uint32_t* visible_prims, const uint32_t* prim_offset,
-                                                                         const uint32_t* n_touched, const PrimRecord* records,
+                                                                         uint32_t* n_touched, const PrimRecord* records,
                                                                          KeyT* keys, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w,
                                                                          uint32_t n_visible) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -122,6 +124,7 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
             keys[off + j] = static_cast<KeyT>(~static_cast<KeyT>(0));
             inst_prim[off + j] = p;
         }
+        if (k < n) n_touched[p] = k;
         atomicAdd(&counters[2], 1u);
     }
 }
@@ -496,7 +499,7 @@ bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_off
     return true;
 }
 
-bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, const uint32_t* n_touched, const PrimRecord* records,
+bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, uint32_t* n_touched, const PrimRecord* records,
                              void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w, uint32_t n_visible,
                              hipStream_t s) {
     if (n_visible == 0) return true;

@@ -1,6 +1,7 @@
 """Seeded synthetic scenes for the benchmark configurations (numpy PCG64, fixed draw order).
 
-Configurations (camera looking along +z from (0, 0, -distance), horizontal field of view 60 degrees,
+c0_inputs gives the colour-only configuration c0. Rasterisation configurations (camera looking along +z from
+(0, 0, -distance), horizontal field of view 60 degrees,
 principal point at the image centre, near 0.2, far 1e4, black background):
   c1          100k Gaussians, means U[-2, 2]^3, 800 x 800, SH degree 3 (none / none / relu)
   c3          1M Gaussians, means U[-10, 10]^3, 1920 x 1080, neural (8 latents, SH degree 1 direction,
@@ -102,6 +103,18 @@ def make_scene(config: str, n: int | None = None, seed: int = 0, width: int | No
     else:
         raise ValueError(model)
     return out
+
+
+def c0_inputs(n: int = 10_000, seed: int = 0) -> dict:
+    """Configuration c0 (the unfused appearance on the host): a camera at the origin looking along +z, means
+    U[-2, 2]^3 + (0, 0, 5), base colours (the SH DC term) N(0, 0.5) (n, 3), SH rest bands N(0, 0.05) (n, 15, 3);
+    draw order as listed. Colour = sigmoid(4 (base + residual(dir))), base and residual activations none."""
+    rng = np.random.default_rng(seed)
+    means = (rng.uniform(-2.0, 2.0, (n, 3)) + np.array([0.0, 0.0, 5.0])).astype(np.float32)
+    base = rng.normal(0.0, 0.5, (n, 3)).astype(np.float32)
+    rest = rng.normal(0.0, 0.05, (n, 15, 3)).astype(np.float32)
+    return dict(means=means, base_colors=base, residual_params=rest, cam_position=np.zeros(3, np.float32),
+                appearance=dict(model='sh', max_degree=3, base_act='none', res_act='none', color_act='sigmoid'))
 
 
 def target_image(width: int, height: int, seed: int = 1) -> np.ndarray:

@@ -206,3 +206,59 @@ def test_ngsplat_layout_validation():
         inp.payload, inp.n_items, inp.n_frequencies, inp.n_neurons, inp.residual_row_stride = 0, 0, 0, 0, 0
         rc, _, _ = plan(**bad)
         assert rc == 1, bad
+
+
+def test_bench_stage_kernels_exist():
+    """Every kernel the bench names for a stage is a kernel of the library's sources (or a hipRTC preprocess kernel)."""
+    import glob
+    import sys
+    sys.path.insert(0, ROOT)
+    import bench
+    src = ''.join(open(f).read() for f in glob.glob(os.path.join(ROOT, 'efficient-gaussian-appearance_amd', 'csrc', '**', '*.hip'),
+                                                      recursive=True))
+    kernels = set(re.findall(r'__global__[^;{]*?\bvoid\s+(\w+)\s*\(', src))
+    assert 'blend_backward_kernel' in kernels and 'adam_kernel' in kernels
+    for stage, names in bench.STAGE_KERNELS.items():
+        for name in names.split(' + '):
+            if '<model>' in name:
+                continue
+            assert name in kernels, (stage, name)
+
+
+def test_bench_line_reports_the_baseline_protocol():
+    """The headline line: BASELINE.json's metric, value = W * H / median step time, the step's timing protocol, and a
+    CPU baseline that is the unfused appearance on the host's torch threads (c0 forward and forward + backward, the CPU
+    model named); the C restatement of the rasterizer stays as an extra key."""
+    import json
+    import sys
+    from types import SimpleNamespace
+    import torch
+    sys.path.insert(0, ROOT)
+    import bench
+    cpu = bench.cpu_unfused_baseline(None, warmup=1, reps=3)
+    assert cpu['unit'] == 'Mprim/s' and cpu['kind'] == 'port' and cpu['value'] > 0
+    assert cpu['cores'] == torch.get_num_threads()
+    assert cpu['cpu_model'] and cpu['cpu_model'] != 'unknown'
+    assert cpu['c0_forward']['value'] > cpu['c0_forward_backward']['value'] > 0
+    assert cpu['value'] == cpu['c0_forward_backward']['value']
+    args = SimpleNamespace(steps=5, warmup=2, config='c3')
+    r = dict(W=1920, H=1080, N=1_000_000, V=698_000.0, I=1_428_000.0, model='neural', step_ms=[0.61, 0.59, 0.6, 0.62, 0.58],
+             wall_ms_per_step=0.605, full_step_ms=0.8, fwd_loss_bwd_ms=0.7, adam_ms=0.1, render_ms=0.22,
+             roofline={'bound': 'hbm', 'achieved': 1.0, 'peak': 8000.0, 'unit': 'GB/s', 'frac': 0.1, 'traffic': None}, stages={})
+    line = bench.headline_line(args, r, cpu, {'value': 0.27, 'unit': 'Mpix/s', 'cores': 1, 'kind': 'port', 'sample': 'x'})
+    baseline = json.load(open(os.path.join(ROOT, 'BASELINE.json')))
+    assert line['metric'] == baseline['metric'] and line['unit'] == 'Mpix/s'
+    assert line['ms_per_step'] == 0.6 and line['value'] == round(1920 * 1080 / 0.6e-3 / 1e6, 3)
+    assert line['steps'] == 5 and line['warmup'] == 2 and line['n_gpus'] == 1 and line['vs_baseline'] is None
+    assert 'median' in line['timing'] and 'forward + backward' in line['config']['workload']
+    assert line['full_step_mpix_s'] == round(1920 * 1080 / 0.8e-3 / 1e6, 3)
+    assert line['cpu_baseline'] is cpu and line['cpu_port_rasterizer']['unit'] == 'Mpix/s'
+    json.dumps(line)
+    defaults = bench.parse_args.__code__  # defaults: 100 timed steps after 10 warm-up steps
+    old = sys.argv
+    sys.argv = ['bench.py']
+    try:
+        a = bench.parse_args()
+    finally:
+        sys.argv = old
+    assert (a.steps, a.warmup) == (100, 10) and defaults is not None

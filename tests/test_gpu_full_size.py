@@ -1,12 +1,13 @@
 """GPU parity at the benchmark configurations' full sizes: the HIP path (through the C ABI) against the CPU
 oracle on the seeded synthetic scenes of c1 (100k Gaussians, 800 x 800, SH degree 3), c3 (1M Gaussians,
 1920 x 1080, neural appearance) and the c4 appearance sweep (c3 geometry, SV / NASG / NASGabor with 8 sites
-or lobes, one colour activation each from {sigmoid, softplus, relu}).
+or lobes, two colour activations each from {sigmoid, softplus, relu}; the third pair of each model runs at
+test size in test_gpu_parity).
 
 Bars (as in test_gpu_parity): counts, per-primitive tile counts and depth keys, projection records, the
 index-ordered emission, tile keys, the tile-sorted primitive order and tile ranges bit-exact; image max-abs <= 1e-4
 (fp32 appearance) or 2e-3 (fp16 MLP); last-contributor indices equal up to near-threshold decisions
-(fp32 appearance: at most 2 + 1e-5 of the pixels); every gradient and
+(at most 2 + 1e-5 of the pixels, the neural path included: alpha comes from the bit-exact fp32 geometry); every gradient and
 densification row rel-L2 <= 1e-3. Size-independent invariants (sorted tile keys, ranges partitioning the
 instance list, per-tile counts summing to the instance count) are checked on the device arrays as well.
 """
@@ -30,6 +31,9 @@ CONFIGS = {
     'c4_sv_sigmoid': ('c4_sv', 'sigmoid'),
     'c4_nasg_softplus': ('c4_nasg', 'softplus'),
     'c4_nasgabor_relu': ('c4_nasgabor', 'relu'),
+    'c4_sv_softplus': ('c4_sv', 'softplus'),
+    'c4_nasg_sigmoid': ('c4_nasg', 'sigmoid'),
+    'c4_nasgabor_sigmoid': ('c4_nasgabor', 'sigmoid'),
 }
 
 
@@ -117,12 +121,11 @@ def test_full_size_parity(name):
     err = float(np.abs(image.cpu().numpy() - fw.image).max())
     print(f'case {name}: image max-abs {err:.3e}', flush=True)
     assert err <= (IMAGE_TOL_FP16 if neural else IMAGE_TOL)
-    if not neural:
-        nc = read_device(bufs, v.n_contributors, gw * gh * 192, np.uint32).reshape(gh, gw, 12, 16)
-        nc = nc.transpose(0, 2, 1, 3).reshape(gh * 12, gw * 16)[:cam.height, :cam.width].reshape(-1)
-        mism = np.count_nonzero(nc != fw.n_contrib)
-        print(f'case {name}: {mism} last-contributor mismatches of {nc.size}', flush=True)
-        assert mism <= contributor_tolerance(nc.size)
+    nc = read_device(bufs, v.n_contributors, gw * gh * 192, np.uint32).reshape(gh, gw, 12, 16)
+    nc = nc.transpose(0, 2, 1, 3).reshape(gh * 12, gw * 16)[:cam.height, :cam.width].reshape(-1)
+    mism = np.count_nonzero(nc != fw.n_contrib)
+    print(f'case {name}: {mism} last-contributor mismatches of {nc.size}', flush=True)
+    assert mism <= contributor_tolerance(nc.size)
     del image, frame, bufs
 
     # gradients through the autograd path

@@ -3,8 +3,8 @@
 Bars: integer / key / index / range arrays bit-exact; per-primitive projection records (mean2d, conic,
 opacity, bounds) bit-exact (shared decision-path arithmetic); image max-abs <= 1e-4 (fp32 path; the blend's
 alpha uses the hardware exp2) and <= 2e-3 (fp16 neural MLP path); last-contributor indices equal up to
-near-threshold decisions (fp32 path: at most 2 + 1e-5 of the pixels); gradients rel-L2 <= 1e-3, including the
-MLP weight gradients.
+near-threshold decisions (at most 2 + 1e-5 of the pixels, every appearance model); gradients rel-L2 <= 1e-3, including the MLP weight
+gradients. The c0 colour configuration: fused preprocess colours against the unfused torch appearance within 1e-5.
 """
 import numpy as np
 import pytest
@@ -32,6 +32,10 @@ CASES = {
     'sv': dict(model='sv'),
     'nasg': dict(model='nasg'),
     'nasgabor': dict(model='nasgabor', acts=('none', 'tanh', 'softplus')),
+    # the remaining model x colour-activation pairs of the c4 sweep (the others run here or at full size)
+    'sv_softplus': dict(model='sv', acts=('none', 'none', 'softplus')),
+    'nasg_sigmoid': dict(model='nasg', acts=('none', 'tanh', 'sigmoid')),
+    'nasgabor_sigmoid': dict(model='nasgabor', acts=('none', 'tanh', 'sigmoid')),
     'ragged_image': dict(model='sh', width=50, height=37),
     'dense_2k': dict(model='sh', n=2000, width=96, height=80, scale_shift=1.5),
     # tiles of 171-632 and of 716-2549 instances: every path of the per-tile sort (registers, LDS slab,
@@ -110,10 +114,10 @@ def test_forward_parity(name):
     nc = nc[:cam.height, :cam.width].reshape(-1)
     mism = np.count_nonzero(nc != fw.n_contrib)
     print(f'case {name}: {mism} last-contributor mismatches of {nc.size}', flush=True)
-    if CASES[name].get('model') != 'neural':
-        # alpha uses the hardware exp2 (the oracle a correctly rounded one): a skip or stop decision can flip
-        # where alpha sits within an ulp of 1/255 or T of 1e-4
-        assert mism <= contributor_tolerance(nc.size), f'{mism} last-contributor mismatches'
+    # alpha uses the hardware exp2 (the oracle a correctly rounded one): a skip or stop decision can flip where
+    # alpha sits within an ulp of 1/255 or T of 1e-4. The decisions depend on the fp32 geometry alone, which is
+    # bit-exact for every appearance model (the neural colours do not enter them).
+    assert mism <= contributor_tolerance(nc.size), f'{mism} last-contributor mismatches'
 
 
 def _check_backward(name, densify_rows):
@@ -186,3 +190,41 @@ def test_backward_is_deterministic():
                                                                                          'base_colors', 'residual_params')])
     for a, b in zip(*outs):
         np.testing.assert_array_equal(a, b)
+
+
+def test_c0_fused_colours_match_the_unfused_appearance():
+    """BASELINE configuration c0: 10k Gaussians with SH degree 3, colour sigmoid(4 (base + residual(dir))), camera at
+    the origin. The fused preprocess colours (every Gaussian visible: small, opaque, inside a wide view) equal the
+    reference's unfused evaluation (AppearanceModel.forward restated in torch on the CPU) and the oracle's."""
+    import math
+    import torch
+    from efgs.rasterization import forward_with_frame, frame_views
+    from efgs.synthetic import c0_inputs
+    import torch_ref as TR
+    c0 = c0_inputs()
+    n = c0['means'].shape[0]
+    a = c0['appearance']
+    app = O.Appearance(model='sh', base_act=a['base_act'], res_act=a['res_act'], color_act=a['color_act'], max_degree=3)
+    width = height = 512
+    f = (width / 2) / 0.7            # |x / z| <= 2 / 3 lands inside the image
+    cam = O.Camera(w2c=np.eye(4, dtype=np.float32), position=c0['cam_position'], width=width, height=height, focal_x=f,
+                   focal_y=f, center_x=width / 2, center_y=height / 2, degree=3)
+    scene = O.Scene(means=c0['means'], scales=np.full((n, 3), math.log(0.01), np.float32),
+                    rotations=np.tile(np.array([1, 0, 0, 0], np.float32), (n, 1)), opacities=np.full((n, 1), 2.0, np.float32),
+                    base_colors=c0['base_colors'], residual_params=c0['residual_params'])
+    unfused = TR.appearance_colors(torch.tensor(c0['means']), torch.tensor(c0['cam_position']), torch.tensor(c0['base_colors']),
+                                   torch.tensor(c0['residual_params']), app, 3).numpy()
+    dev = torch.device('cuda:0')
+    configure(app)
+    inp = torch_inputs(scene, dev)
+    image, frame, bufs = forward_with_frame(inp['means'], inp['scales'], inp['rotations'], inp['opacities'], settings(cam, dev),
+                                            base_colors=inp['base_colors'], residual_params=inp['residual_params'])
+    torch.cuda.synchronize()
+    v = frame_views(frame)
+    assert int(frame.n_visible) == n
+    rec = read_device(bufs, v.records, 12 * n, np.float32).reshape(n, 12)
+    err = float(np.abs(rec[:, 6:9] - unfused).max())
+    print(f'c0: fused vs unfused colour max-abs {err:.3e}', flush=True)
+    assert err <= 1e-5
+    fw = O.render(scene, app, cam)
+    np.testing.assert_allclose(rec[:, 6:9], fw.color, rtol=0, atol=1e-5)
