@@ -261,17 +261,6 @@ def gpu_benchmark(args):
     step_ms = [e[0].elapsed_time(e[1]) for e in step_events]
     log(f'{args.steps} timed forward + backward steps done: median {_median(step_ms):.4f} ms, wall {wall * 1e3 / args.steps:.4f} ms/step')
 
-    # full training iterations (loss and Adam included), reported beside the headline
-    for _ in range(max(args.warmup, 2)):
-        train_step([torch.cuda.Event(enable_timing=True) for _ in range(3)])
-    train_events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    for k in range(args.steps):
-        train_step(train_events[k])
-    torch.cuda.synchronize()
-    full_ms = [e[0].elapsed_time(e[2]) for e in train_events]
-    fwd_loss_bwd_ms = [e[0].elapsed_time(e[1]) for e in train_events]
-    adam_ms = [e[1].elapsed_time(e[2]) for e in train_events]
-    log(f'{args.steps} training iterations done: median {_median(full_ms):.4f} ms')
     # inference renders as the reference's render_image_benchmark calls them: HWC, clamped, no autograd
     render_events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
     with torch.inference_mode():
@@ -286,14 +275,27 @@ def gpu_benchmark(args):
     torch.cuda.synchronize()
     render_ms = _median([e[0].elapsed_time(e[1]) for e in render_events])
     log(f'{args.steps} inference renders done: median {render_ms:.4f} ms')
-    # per-stage breakdown in a separate pass over full training iterations: the library's stage events add host work
-    # to every launch, so the timed steps above run without them
+    # per-stage breakdown: the same forward + backward steps on the same scene, in a separate pass because the
+    # library's stage events add host work to every launch (the timed steps above run without them)
     R._rasterizer.set_stage_timing(True)
     for _ in range(args.steps):
         raster_step()
     stage_times = R._rasterizer.stage_times()
     R._rasterizer.set_stage_timing(False)
     log(f'{args.steps} steps with stage timing done')
+
+    # full training iterations (loss and Adam included), reported beside the headline; they run last because Adam
+    # changes the scene
+    for _ in range(max(args.warmup, 2)):
+        train_step([torch.cuda.Event(enable_timing=True) for _ in range(3)])
+    train_events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for k in range(args.steps):
+        train_step(train_events[k])
+    torch.cuda.synchronize()
+    full_ms = [e[0].elapsed_time(e[2]) for e in train_events]
+    fwd_loss_bwd_ms = [e[0].elapsed_time(e[1]) for e in train_events]
+    adam_ms = [e[1].elapsed_time(e[2]) for e in train_events]
+    log(f'{args.steps} training iterations done: median {_median(full_ms):.4f} ms')
 
     V = sum(c[0] for c in counts) / len(counts)
     I = sum(c[1] for c in counts) / len(counts)
