@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -1069,22 +1070,45 @@ int efgs_neural_decode_forward(efgs_rasterizer* r, int64_t n, const float* featu
     return EFGS_OK;
 }
 
-int efgs_neural_decode_backward(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
-                                const uint16_t* mlp_weights, int degree, const float* grad_out, float* g_features, float* g_base,
-                                float* g_dirs, float* g_mlp_weights, efgs_alloc_fn alloc, void* alloc_ctx, void* stream) {
-    if (int c = check_decode(r, n, features, base, dirs, mlp_weights, degree)) return c;
-    if (!g_mlp_weights || !alloc) return fail(EFGS_ERR_INVALID_ARGUMENT, "null weight gradient output or allocator");
-    if (n > 0 && (!grad_out || (r->mlp_n_features > 0 && !g_features))) return fail(EFGS_ERR_INVALID_ARGUMENT, "null gradient argument");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint32_t params = mlp_params(mlp_shape(r));
-    if (n == 0) return launch_fill_u32(reinterpret_cast<uint32_t*>(g_mlp_weights), 0u, params, s) ? EFGS_OK : EFGS_ERR_HIP;
+}  // extern "C"
+
+// Weight-gradient partials of the allocation-free decode backward: one row of mlp_params floats per block of the
+// backward kernel, 16 MiB on every device the library runs on, held until the process ends. In host code the name
+// `scratch` is a stand-in, not a device address: the host uses only the per-device address that
+// hipGetSymbolAddress returns (scratch_device_address), never the name.
+constexpr size_t scratch_floats = size_t(4) << 20;
+static __device__ __align__(256) float scratch[scratch_floats];
+
+namespace {
+
+constexpr int scratch_max_devices = 64;
+std::mutex scratch_mutex;
+float* scratch_address[scratch_max_devices] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with that device current) on the first call.
+float* scratch_device_address(int device) {
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_address[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fail(EFGS_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+            return nullptr;
+        }
+        scratch_address[device] = static_cast<float*>(p);
+    }
+    return scratch_address[device];
+}
+
+// The decode backward with its partials in `partials` (room for `max_rows` rows of the MLP's parameter count); the
+// block count is min(chunks, neural_backward_blocks, max_rows), so every row the reduction reads is written by the
+// same launch (nothing has to start at zero).
+int decode_backward(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs, const uint16_t* mlp_weights,
+                    int degree, const float* grad_out, float* g_features, float* g_base, float* g_dirs, float* g_mlp_weights,
+                    float* partials, uint32_t blocks, hipStream_t s) {
     RtcKernel fwd;
     hipFunction_t bwd = nullptr;
     if (!get_decode_kernels(r, fwd, bwd)) return EFGS_ERR_RTC;
-    const uint32_t chunks = div_up(static_cast<uint64_t>(n), preprocess_block);
-    const uint32_t blocks = chunks < neural_backward_blocks ? chunks : neural_backward_blocks;
-    float* partials = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(blocks) * params * sizeof(float)));
-    if (!partials) return fail(EFGS_ERR_ALLOC, "allocation of the mlp gradient partials failed");
     NeuralDecodeArgs a = decode_args(n, features, base, dirs, mlp_weights, degree);
     a.grad_out = grad_out;
     a.g_features = g_features;
@@ -1092,8 +1116,61 @@ int efgs_neural_decode_backward(efgs_rasterizer* r, int64_t n, const float* feat
     a.g_dirs = g_dirs;
     a.g_mlp_partials = partials;
     if (!launch_function(bwd, blocks, preprocess_block, mlp_smem_backward(mlp_shape(r)), &a, s)) return EFGS_ERR_HIP;
-    if (!launch_reduce_partials(partials, blocks, params, g_mlp_weights, s)) return EFGS_ERR_HIP;
+    if (!launch_reduce_partials(partials, blocks, mlp_params(mlp_shape(r)), g_mlp_weights, s)) return EFGS_ERR_HIP;
     return EFGS_OK;
+}
+
+int check_decode_backward(const efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                          const uint16_t* mlp_weights, int degree, const float* grad_out, const float* g_features, const float* g_mlp_weights) {
+    if (int c = check_decode(r, n, features, base, dirs, mlp_weights, degree)) return c;
+    if (!g_mlp_weights) return fail(EFGS_ERR_INVALID_ARGUMENT, "null weight gradient output");
+    if (n > 0 && (!grad_out || (r->mlp_n_features > 0 && !g_features))) return fail(EFGS_ERR_INVALID_ARGUMENT, "null gradient argument");
+    return EFGS_OK;
+}
+
+uint32_t decode_backward_blocks(int64_t n) {
+    const uint32_t chunks = div_up(static_cast<uint64_t>(n), preprocess_block);
+    return chunks < neural_backward_blocks ? chunks : neural_backward_blocks;
+}
+
+}  // namespace
+
+extern "C" {
+
+int efgs_neural_decode_backward(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                                const uint16_t* mlp_weights, int degree, const float* grad_out, float* g_features, float* g_base,
+                                float* g_dirs, float* g_mlp_weights, efgs_alloc_fn alloc, void* alloc_ctx, void* stream) {
+    if (int c = check_decode_backward(r, n, features, base, dirs, mlp_weights, degree, grad_out, g_features, g_mlp_weights)) return c;
+    if (!alloc) return fail(EFGS_ERR_INVALID_ARGUMENT, "null allocator");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t params = mlp_params(mlp_shape(r));
+    if (n == 0) return launch_fill_u32(reinterpret_cast<uint32_t*>(g_mlp_weights), 0u, params, s) ? EFGS_OK : EFGS_ERR_HIP;
+    const uint32_t blocks = decode_backward_blocks(n);
+    float* partials = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(blocks) * params * sizeof(float)));
+    if (!partials) return fail(EFGS_ERR_ALLOC, "allocation of the mlp gradient partials failed");
+    return decode_backward(r, n, features, base, dirs, mlp_weights, degree, grad_out, g_features, g_base, g_dirs, g_mlp_weights, partials,
+                           blocks, s);
+}
+
+int efgs_neural_decode_backward_no_alloc(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                                         const uint16_t* mlp_weights, int degree, const float* grad_out, float* g_features,
+                                         float* g_base, float* g_dirs, float* g_mlp_weights, void* stream) {
+    if (int c = check_decode_backward(r, n, features, base, dirs, mlp_weights, degree, grad_out, g_features, g_mlp_weights)) return c;
+    const uint32_t params = mlp_params(mlp_shape(r));
+    if (params > scratch_floats)
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "the mlp's " + std::to_string(params) + " parameters exceed the static scratch of " +
+                                                   std::to_string(scratch_floats) + " floats");
+    int device = 0;
+    if (const hipError_t e = hipGetDevice(&device); e != hipSuccess) return fail(EFGS_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    if (device < 0 || device >= scratch_max_devices) return fail(EFGS_ERR_INVALID_ARGUMENT, "device index beyond the scratch table");
+    float* partials = scratch_device_address(device);
+    if (!partials) return EFGS_ERR_HIP;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n == 0) return launch_fill_u32(reinterpret_cast<uint32_t*>(g_mlp_weights), 0u, params, s) ? EFGS_OK : EFGS_ERR_HIP;
+    const uint32_t rows = static_cast<uint32_t>(scratch_floats / params);
+    const uint32_t blocks = decode_backward_blocks(n) < rows ? decode_backward_blocks(n) : rows;
+    return decode_backward(r, n, features, base, dirs, mlp_weights, degree, grad_out, g_features, g_base, g_dirs, g_mlp_weights, partials,
+                           blocks, s);
 }
 
 int efgs_precompile(const efgs_rasterizer* r, const char* arch) {

@@ -87,7 +87,7 @@ lib = ctypes.CDLL(LIB_PATH)
 EXPORTED = ('efgs_last_error', 'efgs_set_rtc_dirs', 'efgs_rasterizer_create', 'efgs_rasterizer_destroy', 'efgs_set_appearance',
             'efgs_set_residual_mlp', 'efgs_mlp_param_count', 'efgs_forward', 'efgs_backward', 'efgs_adam_step',
             'efgs_get_frame_views', 'efgs_precompile', 'efgs_set_stage_timing', 'efgs_get_stage_times', 'efgs_workspace_alloc',
-            'efgs_neural_decode_forward', 'efgs_neural_decode_backward', 'efgs_add_noise', 'efgs_relocation_adjustment', 'efgs_render', 'efgs_update_pruning_scores',
+            'efgs_neural_decode_forward', 'efgs_neural_decode_backward', 'efgs_neural_decode_backward_no_alloc', 'efgs_add_noise', 'efgs_relocation_adjustment', 'efgs_render', 'efgs_update_pruning_scores',
             'efgs_ngsplat_layout', 'efgs_ngsplat_pack')
 
 # stage ids of efgs_get_stage_times, in order (include/efgs.h)
@@ -120,6 +120,8 @@ lib.efgs_neural_decode_forward.argtypes = [ctypes.c_void_p, ctypes.c_int64] + [c
                                                                                                       ctypes.c_void_p]
 lib.efgs_neural_decode_backward.argtypes = ([ctypes.c_void_p, ctypes.c_int64] + [ctypes.c_void_p] * 4 + [ctypes.c_int] +
                                             [ctypes.c_void_p] * 5 + [ALLOC_FN, ctypes.c_void_p, ctypes.c_void_p])
+lib.efgs_neural_decode_backward_no_alloc.argtypes = ([ctypes.c_void_p, ctypes.c_int64] + [ctypes.c_void_p] * 4 + [ctypes.c_int] +
+                                                     [ctypes.c_void_p] * 6)
 lib.efgs_render.argtypes = [ctypes.c_void_p, ctypes.POINTER(Primitives), ctypes.POINTER(Settings), ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                             ALLOC_FN, ctypes.c_void_p, ctypes.c_void_p]
 lib.efgs_update_pruning_scores.argtypes = [ctypes.c_void_p, ctypes.POINTER(Primitives), ctypes.POINTER(Settings), ctypes.c_void_p, ALLOC_FN,

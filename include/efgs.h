@@ -283,6 +283,19 @@ int efgs_neural_decode_backward(efgs_rasterizer* r, int64_t n, const float* feat
                                 const uint16_t* mlp_weights, int degree, const float* grad_out, float* g_features, float* g_base,
                                 float* g_dirs, float* g_mlp_weights, efgs_alloc_fn alloc, void* alloc_ctx, void* stream);
 
+/* efgs_neural_decode_backward without an allocator, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * per-block weight-gradient partials live in a static 16 MiB device array (4,194,304 floats, one copy per device,
+ * held until the process ends); an MLP whose parameter count exceeds that is rejected (EFGS_ERR_INVALID_ARGUMENT),
+ * and the block count is min(chunks, 512, 4,194,304 / parameters), so MLPs up to 8,192 parameters get the same
+ * blocks, and bit-identical results, as efgs_neural_decode_backward. The first call on a device looks up that
+ * device's copy of the array and loads the decode kernels (as any first decode call does); later calls allocate
+ * nothing and call no hipMalloc / hipFree. Every call on a device shares its array: calls that overlap on one device
+ * (concurrent streams or threads) race and must be serialised by the caller. */
+int efgs_neural_decode_backward_no_alloc(efgs_rasterizer* r, int64_t n, const float* features, const float* base, const float* dirs,
+                                         const uint16_t* mlp_weights, int degree, const float* grad_out, float* g_features,
+                                         float* g_base, float* g_dirs, float* g_mlp_weights, void* stream);
+
 /* Device pointers into a frame's buffers, for inspection (no counterpart in the reference: it lets parity
  * tests compare keys, orders and tile ranges with the CPU oracle). */
 typedef struct efgs_frame_views {
