@@ -267,11 +267,10 @@ __device__ __forceinline__ float group_reduce2(float a, float b) {
 // Per pixel: the nine (eleven with ABS) gradient terms of one Gaussian, zero where the pixel skips it, and the
 // pixel's transmittance and remaining-colour state advanced past it (unchanged bit for bit when skipped).
 template <bool ABS>
-__device__ __forceinline__ void pair_terms(bool contrib, float alpha, float G, float dx, float dy, float4 col, float4 craw,
+__device__ __forceinline__ void pair_terms(bool contrib, float alpha, float dx, float dy, float4 col, float4 conic,
                                            float gr, float gg, float gb, float gbg, float& T, float& A, float* v,
                                            float& wgb, float& e1, float& e2) {
     const float ae = contrib ? alpha : 0.0f;
-    const float Ge = contrib ? G : 0.0f;
     const float w = T * ae;
     const float oma = 1.0f - ae;
     const float rcp = __builtin_amdgcn_rcpf(fmaxf(oma, one_minus_alpha_eps));
@@ -281,13 +280,19 @@ __device__ __forceinline__ void pair_terms(bool contrib, float alpha, float G, f
     const float h = -ae * dalpha;
     const float hdx = h * dx, hdy = h * dy;
     v[0] = hdx; v[1] = hdy; v[2] = hdx * dx; v[3] = hdx * dy; v[4] = hdy * dy;
-    v[5] = Ge * dalpha; v[6] = w * gr; v[7] = w * gg;
+    v[5] = h; v[6] = w * gr; v[7] = w * gg;
     wgb = w * gb;
-    if (ABS) {
-        e1 = fabsf(__builtin_fmaf(craw.x, hdx, craw.y * hdy));
-        e2 = fabsf(__builtin_fmaf(craw.y, hdx, craw.z * hdy));
+    if (ABS) {  // |dL/dmean2d| of the pixel: the raw conic times h d (the exp2-scaled conic divided back)
+        e1 = fabsf(__builtin_fmaf(conic.x, hdx, conic.y * hdy));
+        e2 = fabsf(__builtin_fmaf(conic.y, hdx, conic.z * hdy));
     }
     T = T * oma;
+}
+
+// raw conic (x, y, z) of an exp2-scaled one (scale_conic_for_exp2 inverted)
+__device__ __forceinline__ float4 raw_conic_of(float4 co) {
+    constexpr float ln2 = 0.69314718055994531f;
+    return make_float4(-2.0f * ln2 * co.x, -ln2 * co.y, -2.0f * ln2 * co.z, 0.0f);
 }
 
 // ABS: also reduce |dL/dmean2d| per pixel (needed only for the third densification row).
@@ -297,30 +302,35 @@ __device__ __forceinline__ void pair_terms(bool contrib, float alpha, float G, f
 // forms, branch-free (zero for pixels that skip the Gaussian),
 //   h = -alpha dL/dalpha,  dL/dalpha = T (c . g) - (A - g_bg) / max(1 - alpha, eps)
 // with A = (colour still to come) . g, and the group sums
-//   h dx, h dy, h dx^2, h dx dy, h dy^2, G dL/dalpha, w g_r, w g_g, w g_b   (w = T alpha)
+//   h dx, h dy, h dx^2, h dx dy, h dy^2, h, w g_r, w g_g, w g_b   (w = T alpha)
 // from which the instance's record is dL/dmean2d = (C h d summed), dL/dconic = 0.5 (h d d^T summed),
-// dL/dopacity-term = sum G dL/dalpha, dL/dcolour = sum w g.
+// dL/dopacity-term = sum G dL/dalpha = -(sum h) / o, dL/dcolour = sum w g.
 //
 // Each group walks two Gaussians (a, b) of its list per step, so their first eight values share one
 // 16-value reduction and their ninth values a 2-value one; every (wave, group) stores its sums in its own
-// LDS slot per Gaussian (a group visits a Gaussian at most once per batch). Gaussians are staged 32 at a
-// time (double-buffered, the next batch's records fetched into registers while the current one is
-// walked): one block barrier before the walk, one before the combine, which adds the twelve slots of each
-// value in a fixed order and clears them for the next batch. No atomics: the result is run-to-run
-// deterministic.
-template <bool ABS>
+// LDS slot per Gaussian (a group visits a Gaussian at most once per batch). Gaussians are staged BATCH at a
+// time (double-buffered, the next batch's records fetched into registers while the current one is walked):
+// one block barrier before the walk, one before the combine, which adds the twelve slots of each value in a
+// fixed order and clears them for the next batch. The groups' lists are padded to an even length with a staged
+// dummy of opacity 0 (index BATCH: its alpha is 0, it is never taken, and its sums land in the slots' spare
+// column), so the walk needs no per-entry bounds. No atomics: the result is run-to-run deterministic.
+constexpr uint32_t blend_backward_batch = 32;
+
+template <bool ABS, uint32_t BATCH>
 __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwardArgs a) {
     constexpr uint32_t n_values = ABS ? 11u : 9u;
     constexpr uint32_t n_waves = tile_pixels / 64;
-    constexpr uint32_t batch = 32;
-    constexpr uint32_t list_len = batch;
+    constexpr uint32_t list_len = BATCH;
     constexpr uint32_t n_slots = n_waves * 4;  // (wave, group) pairs
-    // slots [wave][group][value][instance]; value rows 33 floats apart
-    constexpr uint32_t value_stride = batch + 1;
+    constexpr uint32_t dummy = BATCH;          // staged Gaussian of opacity 0 and slot column past the batch
+    // slots [wave][group][value][instance]; value rows BATCH + 1 floats apart
+    constexpr uint32_t value_stride = BATCH + 1;
     constexpr uint32_t slot_stride = n_values * value_stride;
-    // staged per Gaussian: (x, y, packed rect), exp2-scaled conic + opacity, colour, raw conic
-    __shared__ float4 s_stage[2][batch][4];
-    __shared__ uint32_t s_emit[2][batch];
+    constexpr uint32_t n_parts = 6;  // 8-byte parts of the 48-byte record written by the combine
+    static_assert(BATCH <= 64 && BATCH % 2 == 0, "a batch is culled by one wave ballot");
+    // staged per Gaussian: (x, y, packed rect), exp2-scaled conic + opacity, colour
+    __shared__ float4 s_stage[2][BATCH + 1][3];
+    __shared__ uint32_t s_emit[2][BATCH];
     __shared__ uint32_t s_list[n_waves][4][list_len];
     __shared__ float s_part[n_slots * slot_stride];
 
@@ -333,14 +343,13 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
     const bool inside = px < a.width && py < a.height;
     const float pxf = static_cast<float>(px) + 0.5f, pyf = static_cast<float>(py) + 0.5f;
     const uint32_t bx0 = tx * tile_width;
-    const uint32_t by0 = ty * tile_height + wave * 4u, by1 = by0 + 4u;
+    const uint32_t by0 = ty * tile_height + wave * 4u;
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
     const uint32_t n_proc = min(n_total, a.tile_max[tile]);
     const uint32_t* const my_list = &s_list[wave][g][0];
-    // list entries past a group's count are read (and skipped): keep them valid batch indices; slots start at 0
-    for (uint32_t k = tid; k < n_waves * 4 * list_len; k += tile_pixels) (&s_list[0][0][0])[k] = 0;
     for (uint32_t k = tid; k < n_slots * slot_stride; k += tile_pixels) s_part[k] = 0.0f;
+    if (tid < 6) (&s_stage[tid / 3u][dummy][0])[tid % 3u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
     // where this lane stores after the reductions: every lane one of the 16 main values (even quad positions
     // Gaussian a, odd ones b); a few lanes one of the extra values (value 8, with ABS also 9 and 10)
@@ -381,65 +390,65 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
     const uint32_t wave_last = wave_max_u32(last);  // no pixel of the band uses instances at or after this
     float T = 1.0f;
 
-    // staging threads (lanes 0-31 of wave 0) fetch the record of their instance one batch ahead
+    // staging threads (the first BATCH threads) fetch the record of their instance one batch ahead
     uint32_t e_next = 0;
     PrimRecord rec_next{};
     const auto fetch = [&](uint32_t s) {
-        if (tid < batch && s + tid < n_total) {
+        if (tid < BATCH && s + tid < n_total) {
             e_next = a.sorted_inst[range.x + s + tid];
             rec_next = a.records[a.inst_prim[e_next]];
         }
     };
     const auto stage = [&](uint32_t s, uint32_t buf) {
-        if (tid < batch && s + tid < n_total) {
+        if (tid < BATCH && s + tid < n_total) {
             const PrimRecord& rec = rec_next;
             float4* st = s_stage[buf][tid];
+            const float4 co = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
             st[0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
-            st[1] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
+            st[1] = co;
             st[2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
-            st[3] = make_float4(rec.r0.z, rec.r0.w, rec.r1.x, 0.0f);
             s_emit[buf][tid] = e_next;
         }
     };
     if (n_proc > 0) {
         fetch(0);
         stage(0, 0);
-        fetch(batch);
+        fetch(BATCH);
     }
 
     uint32_t covered = 0;
     uint32_t buf = 0;
-    for (uint32_t start = 0; start < n_proc; start += batch, buf ^= 1u) {
+    for (uint32_t start = 0; start < n_proc; start += BATCH, buf ^= 1u) {
         __syncthreads();  // batch staged; the previous combine has read and cleared the slots
-        const uint32_t batch_wave = wave_last > start ? min(min(batch, n_proc - start), wave_last - start) : 0u;
+        const uint32_t batch_wave = wave_last > start ? min(min(BATCH, n_proc - start), wave_last - start) : 0u;
+        const float4(*const stg)[3] = s_stage[buf];
         uint64_t m[4];
-        cull_groups(rect_of(s_stage[buf][lane & (batch - 1)][0]), lane < batch_wave, bx0, by0, by1, m);
+        cull_groups(rect_of(stg[lane < BATCH ? lane : dummy][0]), lane < batch_wave, bx0, by0, by0 + 4u, m);
         uint32_t n[4];
         build_group_lists(m, lane, 0u, &s_list[wave][0][0], list_len, n);
-        wave_lds_fence();
         const uint32_t n_max = __builtin_amdgcn_readfirstlane(max(max(n[0], n[1]), max(n[2], n[3])));
-        const uint32_t my_n = pick_group(g, n[0], n[1], n[2], n[3]);
-        // per-lane step bounds: Gaussian a of step k exists if k < my_n, b if k + 1 < my_n
-        const uint32_t n_main = my_n > main_b ? my_n - main_b : 0u;
-        const uint32_t n_extra = extra_lane && my_n > extra_b ? my_n - extra_b : 0u;
+        const uint32_t n_steps = (n_max + 1u) & ~1u;
+        // pad every list to the even step count with the dummy
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++)
+            if (lane >= n[k] && lane < n_steps) s_list[wave][k][lane] = dummy;
+        wave_lds_fence();
         const uint32_t last_rel = last > start ? last - start : 0u;  // Gaussians j < last_rel are before `last`
-        const float4(*const stg)[4] = s_stage[buf];
-        for (uint32_t k = 0; k < n_max; k += 2) {
-            const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);  // past the count: stale, skipped
+        for (uint32_t k = 0; k < n_steps; k += 2) {
+            const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);
             const uint32_t ja = jab.x, jb = jab.y;
             float dxa, dya, Ga, dxb, dyb, Gb;
             const float alpha_a = eval_alpha(stg[ja][0], stg[ja][1], pxf, pyf, dxa, dya, Ga);
             const float alpha_b = eval_alpha(stg[jb][0], stg[jb][1], pxf, pyf, dxb, dyb, Gb);
-            const bool ca = k < my_n && ja < last_rel && alpha_a >= min_alpha;
-            const bool cb = k + 1 < my_n && jb < last_rel && alpha_b >= min_alpha;
+            const bool ca = ja < last_rel && alpha_a >= min_alpha;
+            const bool cb = jb < last_rel && alpha_b >= min_alpha;
             float v[16], wgb_a, wgb_b, e1a = 0.0f, e2a = 0.0f, e1b = 0.0f, e2b = 0.0f;
             const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            pair_terms<ABS>(ca, alpha_a, Ga, dxa, dya, stg[ja][2], ABS ? stg[ja][3] : zero4, gr, gg, gb, gbg, T, A, v, wgb_a,
-                            e1a, e2a);
-            pair_terms<ABS>(cb, alpha_b, Gb, dxb, dyb, stg[jb][2], ABS ? stg[jb][3] : zero4, gr, gg, gb, gbg, T, A, v + 8, wgb_b,
-                            e1b, e2b);
-            const float s16 = group_reduce16(v, lane);
-            if (k < n_main) part_main[main_b ? jb : ja] = s16;
+            pair_terms<ABS>(ca, alpha_a, dxa, dya, stg[ja][2], ABS ? raw_conic_of(stg[ja][1]) : zero4, gr, gg, gb, gbg, T, A, v,
+                            wgb_a, e1a, e2a);
+            pair_terms<ABS>(cb, alpha_b, dxb, dyb, stg[jb][2], ABS ? raw_conic_of(stg[jb][1]) : zero4, gr, gg, gb, gbg, T, A, v + 8,
+                            wgb_b, e1b, e2b);
+            part_main[main_b ? jb : ja] = group_reduce16(v, lane);
             float sx;
             if (ABS) {
                 const float u[8] = {wgb_a, e1a, e2a, wgb_b, e1b, e2b, 0.0f, 0.0f};
@@ -447,15 +456,16 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
             } else {
                 sx = group_reduce2(wgb_a, wgb_b);
             }
-            if (k < n_extra) part_extra[extra_b ? jb : ja] = sx;
+            if (extra_lane) part_extra[extra_b ? jb : ja] = sx;
         }
         wave_lds_fence();
         __syncthreads();  // every group's sums are in its slots
-        // combine: thread (part p, instance j) adds the twelve slots of its two values in a fixed order,
-        // clears them, and writes its 8 bytes of the 48-byte record
-        const uint32_t j = tid & (batch - 1), p = tid / batch;  // p = 0..5: values 2p, 2p + 1
-        const uint32_t batch_n = min(batch, n_total - start);
-        if (j < batch_n) {
+        // combine: item (part p, instance j) adds the twelve slots of its two values in a fixed order, clears
+        // them, and writes its 8 bytes of the 48-byte record
+        const uint32_t batch_n = min(BATCH, n_total - start);
+        for (uint32_t item = tid; item < n_parts * BATCH; item += tile_pixels) {
+            const uint32_t j = item % BATCH, p = item / BATCH;  // p = 0..5: values 2p, 2p + 1
+            if (j >= batch_n) continue;
             float r[2] = {0.0f, 0.0f};
 #pragma unroll
             for (uint32_t c = 0; c < 2; c++) {
@@ -474,23 +484,23 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
             float2* out = reinterpret_cast<float2*>(a.inst_grads) + 6 * static_cast<size_t>(s_emit[buf][j]) + p;
             float2 o;
             if (p == 0) {
-                const float4 craw = s_stage[buf][j][3];
+                const float4 craw = raw_conic_of(s_stage[buf][j][1]);
                 o = make_float2(__builtin_fmaf(craw.x, r[0], craw.y * r[1]), __builtin_fmaf(craw.y, r[0], craw.z * r[1]));
             } else if (p == 1) {
                 o = make_float2(0.5f * r[0], 0.5f * r[1]);
             } else if (p == 2) {
-                o = make_float2(0.5f * r[0], r[1]);
+                o = make_float2(0.5f * r[0], -r[1] / s_stage[buf][j][1].w);   // sum of G dL/dalpha = -(sum of h) / o
             } else {
                 o = make_float2(r[0], r[1]);  // zero past the last value
             }
             *out = o;
         }
-        covered = min(n_total, start + batch);
+        covered = min(n_total, start + BATCH);
         // stage the next batch into the other buffer (its last readers finished before this batch's first
         // barrier) and fetch the one after it
-        if (start + batch < n_proc) {
-            stage(start + batch, buf ^ 1u);
-            fetch(start + 2 * batch);
+        if (start + BATCH < n_proc) {
+            stage(start + BATCH, buf ^ 1u);
+            fetch(start + 2 * BATCH);
         }
     }
     // instances the tile never reached (after every pixel's last contributor) get zero records
@@ -657,9 +667,9 @@ bool launch_pruning_scores(const BlendBackwardArgs& a, const uint32_t* n_touched
 bool launch_blend_backward(const BlendBackwardArgs& a, hipStream_t s) {
     if (a.n_tiles == 0) return true;
     if (a.abs_grads)
-        blend_backward_kernel<true><<<a.n_tiles, tile_pixels, 0, s>>>(a);
+        blend_backward_kernel<true, blend_backward_batch><<<a.n_tiles, tile_pixels, 0, s>>>(a);
     else
-        blend_backward_kernel<false><<<a.n_tiles, tile_pixels, 0, s>>>(a);
+        blend_backward_kernel<false, blend_backward_batch><<<a.n_tiles, tile_pixels, 0, s>>>(a);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
