@@ -141,9 +141,11 @@ struct efgs_rasterizer {
     int mlp_sh_mask = 0;
     int mlp_n_features = 0;
     bool mlp_base_input = false;
-    uint32_t* host_counters = nullptr;  // pinned, n_counters entries
-    hipEvent_t counters_ready = nullptr;  // recorded after the counter readback, on counters_device
+    uint32_t* host_counters = nullptr;      // pinned and mapped, n_counters entries, written by the preprocess kernel
+    uint32_t* host_counters_dev = nullptr;  // its device address
+    hipEvent_t counters_ready = nullptr;    // recorded after the kernel that writes them, on counters_device
     int counters_device = -1;
+
     // instance count of the last forward and the scene size it was for: sizes the next frame's instance
     // buffers before its counter readback
     uint32_t instance_hint = 0, hint_primitives = 0, hint_tiles = 0;
@@ -602,6 +604,31 @@ int64_t efgs_mlp_param_count(const efgs_rasterizer* r) {
 
 namespace {
 
+// The host's pinned, device-mapped copy of the counters and the event that marks them written (per device).
+int prepare_counters(efgs_rasterizer* r) {
+    int device = 0;
+    if (const hipError_t e = hipGetDevice(&device); e != hipSuccess) return fail(EFGS_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    if (!r->host_counters) {
+        void* host = nullptr;
+        void* dev = nullptr;
+        if (hipHostMalloc(&host, n_counters * sizeof(uint32_t), hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) != hipSuccess)
+            return fail(EFGS_ERR_HIP, "hipHostMalloc of the counter buffer failed");
+        if (hipHostGetDevicePointer(&dev, host, 0) != hipSuccess) {
+            (void)hipHostFree(host);
+            return fail(EFGS_ERR_HIP, "hipHostGetDevicePointer of the counter buffer failed");
+        }
+        r->host_counters = static_cast<uint32_t*>(host);
+        r->host_counters_dev = static_cast<uint32_t*>(dev);
+    }
+    if (r->counters_device != device) {
+        if (r->counters_ready) (void)hipEventDestroy(r->counters_ready);
+        r->counters_ready = nullptr;
+        if (hipEventCreateWithFlags(&r->counters_ready, hipEventDisableTiming) != hipSuccess) return fail(EFGS_ERR_HIP, "hipEventCreate failed");
+        r->counters_device = device;
+    }
+    return EFGS_OK;
+}
+
 // The forward pipeline. A training forward (frame != null) keeps the backward state (final T, last contributors,
 // tile maxima) and writes the image CHW; an inference render (frame == null) writes only the image, in CHW or
 // HWC layout, optionally clamped.
@@ -618,20 +645,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     const uint32_t grid_w = div_up(settings->width, tile_width), grid_h = div_up(settings->height, tile_height);
     const uint32_t n_tiles = grid_w * grid_h;
     const int key_bytes = n_tiles <= 65535u ? 2 : 4;
-    if (!r->host_counters) {
-        if (hipHostMalloc(reinterpret_cast<void**>(&r->host_counters), n_counters * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
-            return fail(EFGS_ERR_HIP, "hipHostMalloc of the counter readback buffer failed");
-    }
-    {
-        int device = 0;
-        EFGS_HIP_CHECK(hipGetDevice(&device));
-        if (r->counters_device != device) {
-            if (r->counters_ready) (void)hipEventDestroy(r->counters_ready);
-            r->counters_ready = nullptr;
-            EFGS_HIP_CHECK(hipEventCreateWithFlags(&r->counters_ready, hipEventDisableTiming));
-            r->counters_device = device;
-        }
-    }
+    if (int c = prepare_counters(r)) return c;
 
     const PrimitiveLayout pl0 = PrimitiveLayout::carve(nullptr, n);
     char* pblob = static_cast<char*>(alloc(alloc_ctx, pl0.bytes));
@@ -671,19 +685,18 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (!launch_rtc(k, blocks, preprocess_block, shared, &a, s)) return EFGS_ERR_HIP;
         t.end(s);
         t.begin(EFGS_STAGE_COMPACT, s);
-        if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, chunks, s)) return EFGS_ERR_HIP;
-    } else {
-        if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
-    }
-    // the counters are final after the block scan: read them back while the compaction runs, and size the
-    // instance buffers meanwhile from the previous frame's count (12.5 % headroom) when the scene size matches,
-    // so that neither the allocation nor the compaction sits between the readback and the next launch
-    if (hipMemcpyAsync(r->host_counters, pl.counters, n_counters * sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipEventRecord(r->counters_ready, s) != hipSuccess)
-        return fail(EFGS_ERR_HIP, std::string("enqueueing the counter readback failed: ") + hipGetErrorString(hipGetLastError()));
-    if (n > 0) {
+        if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, r->host_counters_dev, chunks, s))
+            return EFGS_ERR_HIP;
+        // the scan has written the counters to the pinned host buffer: the host waits for it while the compaction
+        // runs, and sizes the instance buffers meanwhile from the previous frame's count (12.5 % headroom) when the
+        // scene size matches, so that neither the allocation nor the compaction sits between the wait and the next
+        // launch
+        if (hipEventRecord(r->counters_ready, s) != hipSuccess)
+            return fail(EFGS_ERR_HIP, std::string("recording the counter event failed: ") + hipGetErrorString(hipGetLastError()));
         if (!launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
         t.end(s);
+    } else {
+        if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
     }
     char* iblob = nullptr;
     size_t iblob_bytes = 0;
@@ -694,11 +707,11 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
     }
     t.begin(EFGS_STAGE_COUNTER_READ, s);
-    if (hipEventSynchronize(r->counters_ready) != hipSuccess)
+    if (n > 0 && hipEventSynchronize(r->counters_ready) != hipSuccess)
         return fail(EFGS_ERR_HIP, std::string("reading the visible/instance counters failed: ") + hipGetErrorString(hipGetLastError()));
     t.end(s);
-    const uint32_t n_visible = r->host_counters[0];
-    const uint32_t n_instances = r->host_counters[1];
+    const uint32_t n_visible = n > 0 ? __atomic_load_n(&r->host_counters[0], __ATOMIC_ACQUIRE) : 0u;
+    const uint32_t n_instances = n > 0 ? __atomic_load_n(&r->host_counters[1], __ATOMIC_ACQUIRE) : 0u;
     r->instance_hint = n_instances;
     r->hint_primitives = n;
     r->hint_tiles = n_tiles;

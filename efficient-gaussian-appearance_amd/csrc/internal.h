@@ -33,7 +33,7 @@ bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 // [5] ticket of the tile scan's last block
 constexpr uint32_t n_counters = 8;
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
-                              uint32_t n_blocks, hipStream_t s);
+                              uint32_t* host_counters, uint32_t n_blocks, hipStream_t s);
 // visible primitives in index order and their first emission slots (exclusive scan of the tile counts in
 // index order)
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,

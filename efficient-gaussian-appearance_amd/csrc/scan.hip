@@ -39,9 +39,11 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& t
 }
 
 // one block: offsets of the per-preprocess-block (visible, instance) counts; counters[0] = V, counters[1] = I,
-// counters[3] / counters[4] = min / max depth key of the visible primitives
+// counters[3] / counters[4] = min / max depth key of the visible primitives, also written to the host's pinned
+// buffer (device address host_counters; the system-scope fence makes them visible to the host when the kernel
+// completes, so no device-to-host copy is needed)
 __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t* counts, const uint32_t* key_ranges, uint32_t* offsets,
-                                                                 uint32_t* counters, uint32_t n) {
+                                                                 uint32_t* counters, uint32_t* host_counters, uint32_t n) {
     __shared__ uint32_t s_range[2 * 16];
     const uint32_t per = (n + 1023) / 1024;
     const uint32_t base = threadIdx.x * per;
@@ -81,20 +83,22 @@ __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t*
             lo = min(lo, s_range[2 * w]);
             hi = max(hi, s_range[2 * w + 1]);
         }
-        counters[0] = tv;
-        counters[1] = ti;
-        counters[2] = 0;  // instance-emission mismatch counter, see create_instances
-        counters[3] = tv > 0 ? lo : 0u;
-        counters[4] = tv > 0 ? hi : 0u;
+        const uint32_t c[5] = {tv, ti, 0u, tv > 0 ? lo : 0u, tv > 0 ? hi : 0u};  // [2]: emission mismatches, see create_instances
+#pragma unroll
+        for (uint32_t k = 0; k < 5; k++) {
+            counters[k] = c[k];
+            host_counters[k] = c[k];
+        }
         counters[5] = 0;  // ticket of the tile scan's last block
+        __threadfence_system();
     }
 }
 
 }  // namespace
 
-bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters, uint32_t n_blocks,
-                              hipStream_t s) {
-    scan_block_counts_kernel<<<1, 1024, 0, s>>>(block_counts, key_ranges, block_offsets, counters, n_blocks);
+bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
+                              uint32_t* host_counters, uint32_t n_blocks, hipStream_t s) {
+    scan_block_counts_kernel<<<1, 1024, 0, s>>>(block_counts, key_ranges, block_offsets, counters, host_counters, n_blocks);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
