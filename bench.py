@@ -46,8 +46,8 @@ TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'traffic_c3_neural.txt')
 STAGE_KERNELS = {
     'preprocess_forward': 'preprocess_forward_<model>',
     'compact': 'scan_block_counts_kernel + compact_visible_kernel',
-    'create_instances': 'create_instances_kernel',
-    'tile_offsets': 'tile_hist_kernel + tile_block_scan_kernel',
+    'create_instances': 'create_instances_hist_kernel',
+    'tile_offsets': 'tile_column_scan_kernel',
     'tile_buckets': 'tile_buckets_kernel',
     'tile_sort': 'tile_sort_kernel',
     'blend_forward': 'blend_forward_kernel',

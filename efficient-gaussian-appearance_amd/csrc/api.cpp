@@ -220,9 +220,8 @@ struct TileLayout {
     uint32_t* n_contrib;
     uint32_t* tile_max;
     uint32_t* totals;        // instances per tile
-    uint32_t* local_start;   // tile start within its 256-tile block
-    uint32_t* block_sums;    // instances per 256-tile block
-    uint32_t* block_prefix;  // instances of the earlier 256-tile blocks
+    uint32_t* local_start;   // tile start within its 64-tile block
+    uint32_t* block_sums;    // instances per 64-tile block
     uint32_t* cursor;        // per-tile bucket cursor of the global-atomic path
     size_t bytes;
 
@@ -235,8 +234,7 @@ struct TileLayout {
         l.tile_max = c.take<uint32_t>(n_tiles);
         l.totals = c.take<uint32_t>(n_tiles);
         l.local_start = c.take<uint32_t>(n_tiles);
-        l.block_sums = c.take<uint32_t>(div_up(n_tiles > 0 ? n_tiles : 1, 256));
-        l.block_prefix = c.take<uint32_t>(div_up(n_tiles > 0 ? n_tiles : 1, 256));
+        l.block_sums = c.take<uint32_t>(div_up(n_tiles > 0 ? n_tiles : 1, 64));
         l.cursor = c.take<uint32_t>(n_tiles);
         l.bytes = c.offset + buffer_alignment;
         return l;
@@ -246,8 +244,8 @@ struct TileLayout {
 struct InstanceLayout {
     void* keys;              // tile key per emission slot
     uint32_t* inst_prim;     // primitive per emission slot
-    uint32_t* local_rank;    // rank of each instance within its histogram segment's slots of its tile
-    uint32_t* table;         // per histogram segment and tile: the tile's count in the earlier segments
+    uint32_t* local_rank;    // rank of each instance among its segment's instances of its tile | segment << 24
+    uint32_t* table;         // per segment and tile: the tile's count in the earlier segments (rows for every segment)
     uint64_t* bucket;        // sort keys grouped by tile (depth key << 32 | emission index)
     uint32_t* sorted_inst;   // emission slots in (tile, depth, primitive) order
     void* sorted_keys;       // tile key of every sorted instance
@@ -257,11 +255,11 @@ struct InstanceLayout {
         InstanceLayout l;
         Carver c{base};
         const uint64_t ni = n_instances > 0 ? n_instances : 1;
-        const TileBinning plan = tile_binning_plan(static_cast<uint32_t>(n_instances), n_tiles);
+        const bool use_table = tile_binning_plan(1, n_tiles).use_table;
         l.keys = c.take_bytes(key_bytes * ni);
         l.inst_prim = c.take<uint32_t>(ni);
-        l.local_rank = c.take<uint32_t>(plan.use_table ? ni : 1);
-        l.table = c.take<uint32_t>(plan.use_table ? static_cast<uint64_t>(plan.blocks) * n_tiles : 1);
+        l.local_rank = c.take<uint32_t>(use_table ? ni : 1);
+        l.table = c.take<uint32_t>(use_table ? static_cast<uint64_t>(tile_hist_max_blocks) * n_tiles : 1);
         l.bucket = c.take<uint64_t>(ni);
         l.sorted_inst = c.take<uint32_t>(ni);
         l.sorted_keys = c.take_bytes(key_bytes * ni);
@@ -722,15 +720,23 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
     }
     const InstanceLayout il = InstanceLayout::carve(iblob, n_instances, key_bytes, n_tiles);
-    const TileBinning plan = tile_binning_plan(n_instances, n_tiles);
+    const TileBinning plan = tile_binning_plan(n_visible, n_tiles);
+    CreateInstancesArgs ca;
+    ca.visible_prims = pl.visible_prims;
+    ca.prim_offset = pl.prim_offset;
+    ca.n_touched = pl.n_touched;
+    ca.records = pl.records;
+    ca.keys = il.keys;
+    ca.inst_prim = il.inst_prim;
+    ca.counters = pl.counters;
+    ca.grid_w = grid_w;
+    ca.n_visible = n_visible;
     t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
-    if (!launch_create_instances(pl.visible_prims, pl.prim_offset, pl.n_touched, pl.records, il.keys, key_bytes, il.inst_prim, pl.counters, grid_w,
-                                 n_visible, s))
-        return EFGS_ERR_HIP;
+    if (!launch_create_instances(ca, key_bytes, plan, il.local_rank, il.table, n_tiles, s)) return EFGS_ERR_HIP;
     t.end(s);
-    const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.block_prefix, pl.counters + 5, tl.cursor};
+    const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor};
     t.begin(EFGS_STAGE_TILE_OFFSETS, s);
-    if (!launch_tile_counts(plan, il.keys, key_bytes, n_instances, il.local_rank, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
+    if (!launch_tile_counts(plan, il.keys, key_bytes, n_instances, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
     t.end(s);
     t.begin(EFGS_STAGE_TILE_BUCKETS, s);
     if (!launch_tile_buckets(plan, il.keys, key_bytes, il.inst_prim, pl.depth_keys, il.table, il.local_rank, ts, il.bucket, n_instances, n_tiles, s))

@@ -29,8 +29,7 @@ inline uint32_t div_up(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a
 
 // ---- rasterizer stages -------------------------------------------------------------------------------------
 bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
-// counters: [0] V, [1] I, [2] instance-emission mismatches, [3] / [4] min / max depth key of the visible set,
-// [5] ticket of the tile scan's last block
+// counters: [0] V, [1] I, [2] instance-emission mismatches, [3] / [4] min / max depth key of the visible set
 constexpr uint32_t n_counters = 8;
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
                               uint32_t* host_counters, uint32_t n_blocks, hipStream_t s);
@@ -38,37 +37,44 @@ bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_
 // index order)
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,
                             hipStream_t s);
-// (tile key, primitive) at every emission slot
-bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, uint32_t* n_touched, const PrimRecord* records,
-                             void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w, uint32_t n_visible,
-                             hipStream_t s);
-// Tile binning: per-tile counts from LDS histograms over fixed segments of the emission slots (a table of
-// per-segment counts, scanned per tile) when the tile count fits the LDS, else from global atomics.
-constexpr size_t tile_hist_max_lds = 64 * 1024;  // default dynamic LDS limit of a launch
-constexpr uint32_t tile_hist_min_segment = 16384;  // emission slots per histogram block (at least)
-constexpr uint32_t tile_hist_max_blocks = 128;
+// Tile binning: per-tile counts from LDS histograms over segments of contiguous visible primitives (their
+// emission slots are contiguous; a table of per-segment counts, scanned per tile) when the tile count fits the
+// LDS, else from global atomics.
+constexpr size_t tile_hist_max_lds = 64 * 1024;    // default dynamic LDS limit of a launch
+constexpr uint32_t tile_hist_min_segment = 2048;   // visible primitives per histogram block (at least)
+constexpr uint32_t tile_hist_max_blocks = 256;     // segments (the rank word keeps the segment in its top 8 bits)
 struct TileBinning {
     bool use_table;
-    uint32_t blocks;   // histogram blocks (rows of the table)
-    uint32_t segment;  // emission slots per histogram block
+    uint32_t blocks;   // histogram blocks (segments, rows of the table)
+    uint32_t segment;  // visible primitives per segment
 };
-TileBinning tile_binning_plan(uint32_t n_instances, uint32_t n_tiles);
-// Tile scan state (tile arena): totals[t] instances of tile t, local_start[t] exclusive scan of the totals
-// within t's 256-tile block, block_prefix[t / 256] the totals of the earlier blocks (tile t starts at
-// block_prefix[t / 256] + local_start[t]), block_sums per 256-tile block, the ticket of the block that scans
-// them (counters[5], zeroed by scan_block_counts), and a per-tile cursor for the global-atomic path.
+TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles);
+struct CreateInstancesArgs {
+    const uint32_t* visible_prims;
+    const uint32_t* prim_offset;
+    uint32_t* n_touched;
+    const PrimRecord* records;
+    void* keys;                // tile key per emission slot, key_bytes wide
+    uint32_t* inst_prim;
+    uint32_t* counters;
+    uint32_t grid_w, n_visible;
+};
+// (tile key, primitive) at every emission slot; with a table also each instance's rank | segment << 24 and the
+// segments' per-tile counts
+bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const TileBinning& plan, uint32_t* local_rank, uint32_t* table,
+                             uint32_t n_tiles, hipStream_t s);
+// Tile scan state (tile arena): totals[t] instances of tile t, local_start[t] exclusive scan of the totals within
+// t's 64-tile block, block_sums per 64-tile block (tile t starts at the sum of block_sums over the blocks before
+// t / 64 plus local_start[t]), and a per-tile cursor for the global-atomic path.
 struct TileScan {
     uint32_t* totals;
     uint32_t* local_start;
     uint32_t* block_sums;
-    uint32_t* block_prefix;
-    uint32_t* ticket;
     uint32_t* cursor;
 };
-// per-tile counts (LDS histograms over segments of the emission slots with per-instance ranks and the
-// segment table, or global atomics) and the scan above
-bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* local_rank, uint32_t* table,
-                        const TileScan& ts, uint32_t n_tiles, hipStream_t s);
+// per-tile counts (global atomics without a table) and the scan above
+bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* table, const TileScan& ts,
+                        uint32_t n_tiles, hipStream_t s);
 // every instance's sort key (depth key of its primitive << 32 | emission index) into a slot of its tile's range
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
                          const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,

@@ -5,9 +5,10 @@
 //   compact_visible     visible primitives in index order and each one's first emission slot (exclusive
 //                       scan of the tile counts in index order);
 //   create_instances    one thread per visible primitive (index order): the tile test of the preprocess,
-//                       (tile key, primitive) at the emission slots, per-tile instance counts;
-//   tile_offsets        one block: exclusive scan of the tile counts -> [start, end) per tile, cursors;
-//   tile_buckets        every instance claims a slot of its tile's range (atomic cursor; order arbitrary);
+//                       (tile key, primitive) at the emission slots; blocks of contiguous primitives count
+//                       their instances per tile in an LDS histogram (ranks from the atomics' return values);
+//   tile_column_scan    the segments' counts per tile -> prefixes over the segments, tile totals and starts;
+//   tile_buckets        every instance writes its sort key at tile start + earlier segments' count + rank;
 //   tile_sort           one block per tile sorts its slots by (depth key, emission index) in LDS: keys are
 //                       unique, so the order is a deterministic function of the inputs (the emission index
 //                       increases with the primitive index, so ties in depth keep primitive-index order).
@@ -57,27 +58,22 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
     prim_offset[p] = off + inc - touched;
 }
 
-// One thread per visible primitive in index order: emits (tile key, primitive) for every tile of its tile
-// rectangle that passes the contribution test, the first 4 tiles per lane and larger footprints
-// wave-cooperatively (64 tiles per step, positions from ballot prefix counts). Emission slots are
-// [prim_offset, prim_offset + n_touched); a count that disagrees with the preprocess is clamped to that
-// range, the remainder padded with an out-of-range key (never bucketed) and counted in counters[2]. A primitive
-// that emitted fewer tiles than counted gets n_touched lowered to the emitted count, so the per-primitive sums of
-// the backward and of the pruning scores cover only slots that a blend kernel writes.
-template <typename KeyT>
-__global__ __launch_bounds__(instance_block) void create_instances_kernel(const uint32_t* visible_prims, const uint32_t* prim_offset,
-                                                                         uint32_t* n_touched, const PrimRecord* records,
-                                                                         KeyT* keys, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w,
-                                                                         uint32_t n_visible) {
-    const uint32_t lane = threadIdx.x & 63u;
+// Emission of one visible primitive per thread (visible index i, index order): (tile key, primitive) for every
+// tile of its tile rectangle that passes the contribution test, the first 4 tiles per lane and larger
+// footprints wave-cooperatively (64 tiles per step, positions from ballot prefix counts); emit(slot, tile) is
+// called by the lane that writes each instance. Emission slots are [prim_offset, prim_offset + n_touched); a
+// count that disagrees with the preprocess is clamped to that range, the remainder padded with an out-of-range
+// key (never bucketed) and counted in counters[2]. A primitive that emitted fewer tiles than counted gets
+// n_touched lowered to the emitted count, so the per-primitive sums of the backward and of the pruning scores
+// cover only slots that a blend kernel writes. Every lane of the wave must call this (ballots and shuffles).
+template <typename KeyT, typename Emit>
+__device__ __forceinline__ void emit_primitive(const CreateInstancesArgs& a, uint32_t i_raw, bool active, uint32_t lane, Emit&& emit) {
     const uint64_t lanes_below = (1ull << lane) - 1ull;
-    const uint32_t i_raw = blockIdx.x * instance_block + threadIdx.x;
-    const bool active = i_raw < n_visible;
-    const uint32_t i = active ? i_raw : n_visible - 1;
-    const uint32_t p = visible_prims[i];
-    const uint32_t off = prim_offset[p];
-    const uint32_t n = n_touched[p];
-    const PrimRecord rec = records[p];
+    const uint32_t i = active ? i_raw : a.n_visible - 1;
+    const uint32_t p = a.visible_prims[i];
+    const uint32_t off = a.prim_offset[p];
+    const uint32_t n = a.n_touched[p];
+    const PrimRecord rec = a.records[p];
     const uint32_t bx = __float_as_uint(rec.r2.y), by = __float_as_uint(rec.r2.z);
     const TileRect t = screen_to_tile_bounds(bx & 0xffffu, bx >> 16, by & 0xffffu, by >> 16);
     const uint32_t bw = t.x1 - t.x0;
@@ -85,13 +81,16 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
     const float smx = rec.r0.x - 0.5f, smy = rec.r0.y - 0.5f;
     const float cx = rec.r0.z, cy = rec.r0.w, cz = rec.r1.x;
     const float pt = power_threshold_of(rec.r1.y);
+    KeyT* keys = static_cast<KeyT*>(a.keys);
     uint32_t k = 0;
     for (uint32_t j = 0; j < cnt && j < 4; j++) {
         const uint32_t tx = t.x0 + j % bw, ty = t.y0 + j / bw;
         if (will_primitive_contribute(smx, smy, cx, cy, cz, tx, ty, pt)) {
             if (k < n) {
-                keys[off + k] = static_cast<KeyT>(ty * grid_w + tx);
-                inst_prim[off + k] = p;
+                const uint32_t tile = ty * a.grid_w + tx;
+                keys[off + k] = static_cast<KeyT>(tile);
+                a.inst_prim[off + k] = p;
+                emit(off + k, tile);
             }
             k++;
         }
@@ -112,8 +111,10 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
             const uint64_t m = __ballot(hit);
             const uint32_t pos = c_k + static_cast<uint32_t>(__popcll(m & lanes_below));
             if (hit && pos < c_n) {
-                keys[c_off + pos] = static_cast<KeyT>(ty * grid_w + tx);
-                inst_prim[c_off + pos] = c_p;
+                const uint32_t tile = ty * a.grid_w + tx;
+                keys[c_off + pos] = static_cast<KeyT>(tile);
+                a.inst_prim[c_off + pos] = c_p;
+                emit(c_off + pos, tile);
             }
             c_k += static_cast<uint32_t>(__popcll(m));
         }
@@ -122,108 +123,96 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(const 
     if (active && k != n) {
         for (uint32_t j = (k < n ? k : n); j < n; j++) {
             keys[off + j] = static_cast<KeyT>(~static_cast<KeyT>(0));
-            inst_prim[off + j] = p;
+            a.inst_prim[off + j] = p;
         }
-        if (k < n) n_touched[p] = k;
-        atomicAdd(&counters[2], 1u);
+        if (k < n) a.n_touched[p] = k;
+        atomicAdd(&a.counters[2], 1u);
     }
 }
 
-// Per-tile counts without global atomics: block b of tile_hist counts the tiles of emission slots
-// [b seg, (b + 1) seg) in an LDS histogram (ds_add with return gives every instance its rank within the
-// block's slots of its tile, in arbitrary order) and writes its row table[b][tile]; tile_block_scan turns
-// every column into exclusive prefixes over the blocks and the tile totals. Grids too large for an LDS
-// histogram count with global atomics instead (tile_count_global).
-__global__ __launch_bounds__(1024) void tile_hist_kernel(const void* keys_raw, int key_bytes, uint32_t n_instances, uint32_t seg,
-                                                         uint32_t* local_rank, uint32_t* table, uint32_t n_tiles) {
+// One thread per visible primitive (the path for grids whose tile histogram does not fit the LDS).
+template <typename KeyT>
+__global__ __launch_bounds__(instance_block) void create_instances_kernel(CreateInstancesArgs a) {
+    const uint32_t i = blockIdx.x * instance_block + threadIdx.x;
+    emit_primitive<KeyT>(a, i, i < a.n_visible, threadIdx.x & 63u, [](uint32_t, uint32_t) {});
+}
+
+// Emission with the per-tile counts: block s emits the visible primitives [s P, (s + 1) P) (index order, so its
+// emission slots are one contiguous run, its segment), counts them per tile in an LDS histogram whose atomic
+// return values rank every instance among the segment's instances of its tile (in arbitrary order: the per-tile
+// sort fixes the order later), stores rank | s << 24 per instance and writes its histogram row table[s][*].
+template <typename KeyT>
+__global__ __launch_bounds__(1024) void create_instances_hist_kernel(CreateInstancesArgs a, uint32_t per_segment, uint32_t* local_rank,
+                                                                    uint32_t* table, uint32_t n_tiles) {
     extern __shared__ uint32_t hist[];
     for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) hist[t] = 0;
     __syncthreads();
-    const uint32_t e0 = blockIdx.x * seg, e1 = min(n_instances, e0 + seg);
-    for (uint32_t e = e0 + threadIdx.x; e < e1; e += 1024) {
-        const uint32_t t = key_bytes == 2 ? static_cast<const uint16_t*>(keys_raw)[e] : static_cast<const uint32_t*>(keys_raw)[e];
-        if (t < n_tiles) local_rank[e] = atomicAdd(&hist[t], 1u);
+    const uint32_t seg = blockIdx.x;
+    const uint32_t v0 = seg * per_segment, v1 = min(a.n_visible, v0 + per_segment);
+    const uint32_t tag = seg << 24;
+    for (uint32_t base = v0; base < v1; base += 1024) {  // block-uniform trip count
+        const uint32_t i = base + threadIdx.x;
+        emit_primitive<KeyT>(a, i, i < v1, threadIdx.x & 63u, [&](uint32_t slot, uint32_t tile) {
+            local_rank[slot] = tag | atomicAdd(&hist[tile], 1u);
+        });
     }
     __syncthreads();
-    uint32_t* row = table + static_cast<size_t>(blockIdx.x) * n_tiles;
+    uint32_t* row = table + static_cast<size_t>(seg) * n_tiles;
     for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) row[t] = hist[t];
 }
 
-// exclusive scan of one value per thread over a 256-thread block; sum receives the block total
-__device__ __forceinline__ uint32_t block_exclusive_scan_256(uint32_t v, uint32_t* s_waves, uint32_t& sum) {
+// Per-tile offsets, 64 tiles per block, one tile per lane. With a count table (S segment rows): wave w of 16 loads
+// the column entries of its sixteenth of the segments into registers; the sixteen partial sums give each wave its
+// offset and the tile's total; wave 0 scans the block's 64 totals (local_start: the tile's start within the block,
+// and the block total, block_sums); then every entry is rewritten as local_start + the tile's count in the earlier
+// segments, so a bucket slot is block prefix + table entry + rank. Without a table the totals come from the
+// global counts. The start of tile t is the sum of block_sums over the blocks before t / 64 plus local_start[t]:
+// consumers add those few block sums themselves, so no block waits for another and no cross-block fence is needed.
+constexpr uint32_t scan_tiles = 64;
+constexpr uint32_t scan_waves = 16;
+constexpr uint32_t scan_per_wave = tile_hist_max_blocks / scan_waves;
+__global__ __launch_bounds__(64 * scan_waves) void tile_column_scan_kernel(uint32_t* table, uint32_t n_segments, uint32_t n_tiles,
+                                                                          uint32_t* totals, uint32_t* local_start, uint32_t* block_sums) {
+    __shared__ uint32_t s_part[scan_waves][scan_tiles];
+    __shared__ uint32_t s_start[scan_tiles];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    uint32_t inc = v;
+    const uint32_t t = blockIdx.x * scan_tiles + lane;
+    const bool in = t < n_tiles;
+    const uint32_t per = (n_segments + scan_waves - 1) / scan_waves;
+    const uint32_t s0 = wave * per;
+    uint32_t c[scan_per_wave];
+    uint32_t sum = 0;
 #pragma unroll
-    for (uint32_t o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(inc, o);
-        if (lane >= o) inc += t;
+    for (uint32_t k = 0; k < scan_per_wave; k++) {
+        c[k] = (table && in && k < per && s0 + k < n_segments) ? table[static_cast<size_t>(s0 + k) * n_tiles + t] : 0u;
+        sum += c[k];
     }
-    if (lane == 63) s_waves[wave] = inc;
+    s_part[wave][lane] = sum;
     __syncthreads();
-    uint32_t prefix = 0;
-    sum = 0;
+    if (wave == 0) {
+        uint32_t total = 0;
 #pragma unroll
-    for (uint32_t w = 0; w < 4; w++) {
-        const uint32_t x = s_waves[w];
-        if (w < wave) prefix += x;
-        sum += x;
-    }
-    __syncthreads();
-    return prefix + inc - v;
-}
-
-// One thread per tile, 256 tiles per block. With a count table: the tile's column becomes exclusive prefixes
-// over the histogram segments and its sum the tile's total; without one the totals come from the global
-// counts. Then the block's exclusive scan of its totals (local_start) and the block sum; the last block to
-// finish (atomic ticket, zeroed by scan_block_counts) scans the block sums into block_prefix, so the start
-// of tile t is block_prefix[t / 256] + local_start[t].
-__global__ __launch_bounds__(256) void tile_block_scan_kernel(uint32_t* table, uint32_t n_segments, uint32_t n_tiles, uint32_t* totals,
-                                                              uint32_t* local_start, uint32_t* block_sums, uint32_t* block_prefix,
-                                                              uint32_t* ticket) {
-    __shared__ uint32_t s_waves[4];
-    __shared__ bool s_last;
-    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
-    uint32_t count = 0;
-    if (t < n_tiles) {
-        if (table) {
-            // 32 loads in flight (addresses clamped to the last segment, so every load is unconditional): the
-            // grid is small (one thread per tile), so the column walk is bound by load latency
-            constexpr uint32_t in_flight = 32;
-            for (uint32_t b0 = 0; b0 < n_segments; b0 += in_flight) {
-                uint32_t c[in_flight];
+        for (uint32_t w = 0; w < scan_waves; w++) total += s_part[w][lane];
+        if (!table) total = in ? totals[t] : 0u;
+        else if (in) totals[t] = total;
+        uint32_t inc = total;
 #pragma unroll
-                for (uint32_t k = 0; k < in_flight; k++) c[k] = table[static_cast<size_t>(min(b0 + k, n_segments - 1)) * n_tiles + t];
-#pragma unroll
-                for (uint32_t k = 0; k < in_flight; k++) {
-                    if (b0 + k < n_segments) {
-                        table[static_cast<size_t>(b0 + k) * n_tiles + t] = count;
-                        count += c[k];
-                    }
-                }
-            }
-            totals[t] = count;
-        } else {
-            count = totals[t];
+        for (uint32_t o = 1; o < 64; o <<= 1) {
+            const uint32_t x = __shfl_up(inc, o);
+            if (lane >= o) inc += x;
         }
+        if (in) local_start[t] = inc - total;
+        s_start[lane] = inc - total;
+        if (lane == 63) block_sums[blockIdx.x] = inc;
     }
-    uint32_t sum;
-    const uint32_t ex = block_exclusive_scan_256(count, s_waves, sum);
-    if (t < n_tiles) local_start[t] = ex;
-    if (threadIdx.x == 0) block_sums[blockIdx.x] = sum;
-    __threadfence();
+    if (!table) return;
     __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(ticket, 1u) == gridDim.x - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();  // every block's sum is visible to the last block
-    uint32_t carry = 0;
-    for (uint32_t base = 0; base < gridDim.x; base += 256) {
-        const uint32_t i = base + threadIdx.x;
-        const uint32_t v = i < gridDim.x ? block_sums[i] : 0u;
-        uint32_t chunk;
-        const uint32_t e = block_exclusive_scan_256(v, s_waves, chunk);
-        if (i < gridDim.x) block_prefix[i] = carry + e;
-        carry += chunk;
+    uint32_t prefix = s_start[lane];
+    for (uint32_t w = 0; w < wave; w++) prefix += s_part[w][lane];
+#pragma unroll
+    for (uint32_t k = 0; k < scan_per_wave; k++) {
+        if (in && k < per && s0 + k < n_segments) table[static_cast<size_t>(s0 + k) * n_tiles + t] = prefix;
+        prefix += c[k];
     }
 }
 
@@ -235,26 +224,62 @@ __global__ __launch_bounds__(256) void tile_count_global_kernel(const KeyT* keys
     if (t < n_tiles) atomicAdd(&totals[t], 1u);
 }
 
-__device__ __forceinline__ uint32_t tile_start_of(const uint32_t* block_prefix, const uint32_t* local_start, uint32_t t) {
-    return block_prefix[t >> 8] + local_start[t];
+// exclusive prefix of block_sums over the scan blocks before `b`, for one wave (every lane gets it)
+__device__ __forceinline__ uint32_t scan_block_prefix_wave(const uint32_t* block_sums, uint32_t b, uint32_t lane) {
+    uint32_t s = 0;
+    for (uint32_t k = lane; k < b; k += 64) s += block_sums[k];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    return s;
 }
 
 // Every emitted instance goes to a slot of its tile's range: start of the tile + the tile's count in the
-// earlier histogram segments + its rank within its segment (with a table), or + the next slot of an atomic
-// cursor (without one). The slot receives the instance's sort key, the depth key of its primitive above
-// its emission index.
+// earlier segments + its rank within its segment (with a table: the scanned table entry holds the tile's start
+// within its 64-tile block plus that count), or + the next slot of an atomic cursor (without one). The slot receives the instance's sort key, the depth key of its primitive above its emission
+// index. Each block first scans the per-64-tile block sums into LDS (at most tile_hist_max_lds / 4 / 64 of them).
+constexpr uint32_t max_scan_blocks = static_cast<uint32_t>(tile_hist_max_lds / 4 / scan_tiles);
 template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
-                                                          const uint32_t* table, const uint32_t* local_rank, uint32_t seg,
-                                                          const uint32_t* block_prefix, const uint32_t* local_start, uint32_t* cursor,
-                                                          uint64_t* bucket, uint32_t n_instances, uint32_t n_tiles) {
+                                                          const uint32_t* table, const uint32_t* local_rank, const uint32_t* block_sums,
+                                                          const uint32_t* local_start, uint32_t* cursor, uint64_t* bucket, uint32_t n_instances,
+                                                          uint32_t n_tiles) {
+    __shared__ uint32_t s_prefix[max_scan_blocks];
+    __shared__ uint32_t s_waves[4];
+    const uint32_t n_blocks = (n_tiles + scan_tiles - 1) / scan_tiles;
+    if (n_blocks <= max_scan_blocks) {
+        const uint32_t v = threadIdx.x < n_blocks ? block_sums[threadIdx.x] : 0u;
+        const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+        uint32_t inc = v;
+#pragma unroll
+        for (uint32_t o = 1; o < 64; o <<= 1) {
+            const uint32_t x = __shfl_up(inc, o);
+            if (lane >= o) inc += x;
+        }
+        if (lane == 63) s_waves[wave] = inc;
+        __syncthreads();
+        uint32_t off = 0;
+        for (uint32_t w = 0; w < wave; w++) off += s_waves[w];
+        if (threadIdx.x < n_blocks) s_prefix[threadIdx.x] = off + inc - v;
+        __syncthreads();
+    }
     const uint32_t e = blockIdx.x * 256u + threadIdx.x;
     if (e >= n_instances) return;
     const uint32_t t = static_cast<uint32_t>(keys[e]);
     if (t >= n_tiles) return;
     const uint64_t key = (static_cast<uint64_t>(depth_keys[inst_prim[e]]) << 32) | e;
-    const uint32_t pos = tile_start_of(block_prefix, local_start, t) +
-                         (table ? table[static_cast<size_t>(e / seg) * n_tiles + t] + local_rank[e] : atomicAdd(&cursor[t], 1u));
+    const uint32_t b = t / scan_tiles;
+    uint32_t pos = 0;
+    if (n_blocks <= max_scan_blocks) {
+        pos = s_prefix[b];
+    } else {
+        for (uint32_t k = 0; k < b; k++) pos += block_sums[k];
+    }
+    if (table) {  // the table entry already holds the tile's start within its block
+        const uint32_t r = local_rank[e];
+        pos += table[static_cast<size_t>(r >> 24) * n_tiles + t] + (r & 0xffffffu);
+    } else {
+        pos += local_start[t] + atomicAdd(&cursor[t], 1u);
+    }
     bucket[pos] = key;
 }
 
@@ -391,7 +416,7 @@ __device__ __forceinline__ void sort_run_split192(const uint64_t* run, uint32_t 
 }
 
 template <typename KeyT>
-__global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* totals, const uint32_t* block_prefix,
+__global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* totals, const uint32_t* block_sums,
                                                                    const uint32_t* local_start, uint2* ranges, uint64_t* bucket,
                                                                    uint32_t* sorted_inst, KeyT* sorted_keys, uint32_t n_tiles) {
     __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
@@ -399,7 +424,7 @@ __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32
     const uint32_t tile = blockIdx.x * tile_sort_waves + wave;
     if (tile >= n_tiles) return;  // the whole wave (no block barriers below)
     const uint32_t n = totals[tile];
-    const uint32_t start = tile_start_of(block_prefix, local_start, tile);
+    const uint32_t start = scan_block_prefix_wave(block_sums, tile / scan_tiles, lane) + local_start[tile];
     const uint2 r = n > 0 ? make_uint2(start, start + n) : make_uint2(0u, 0u);  // (0, 0) for an empty tile, as the reference
     if (lane == 0) ranges[tile] = r;
     if (n == 0) return;
@@ -499,37 +524,41 @@ bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_off
     return true;
 }
 
-bool launch_create_instances(const uint32_t* visible_prims, const uint32_t* prim_offset, uint32_t* n_touched, const PrimRecord* records,
-                             void* keys, int key_bytes, uint32_t* inst_prim, uint32_t* counters, uint32_t grid_w, uint32_t n_visible,
-                             hipStream_t s) {
-    if (n_visible == 0) return true;
-    const uint32_t blocks = div_up(n_visible, instance_block);
-    if (key_bytes == 2)
-        create_instances_kernel<uint16_t><<<blocks, instance_block, 0, s>>>(visible_prims, prim_offset, n_touched, records, static_cast<uint16_t*>(keys),
-                                                                           inst_prim, counters, grid_w, n_visible);
-    else
-        create_instances_kernel<uint32_t><<<blocks, instance_block, 0, s>>>(visible_prims, prim_offset, n_touched, records, static_cast<uint32_t*>(keys),
-                                                                           inst_prim, counters, grid_w, n_visible);
+bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const TileBinning& plan, uint32_t* local_rank, uint32_t* table,
+                             uint32_t n_tiles, hipStream_t s) {
+    if (a.n_visible == 0) return true;
+    if (plan.use_table) {
+        const size_t lds = static_cast<size_t>(n_tiles) * 4;
+        if (key_bytes == 2)
+            create_instances_hist_kernel<uint16_t><<<plan.blocks, 1024, lds, s>>>(a, plan.segment, local_rank, table, n_tiles);
+        else
+            create_instances_hist_kernel<uint32_t><<<plan.blocks, 1024, lds, s>>>(a, plan.segment, local_rank, table, n_tiles);
+    } else {
+        const uint32_t blocks = div_up(a.n_visible, instance_block);
+        if (key_bytes == 2)
+            create_instances_kernel<uint16_t><<<blocks, instance_block, 0, s>>>(a);
+        else
+            create_instances_kernel<uint32_t><<<blocks, instance_block, 0, s>>>(a);
+    }
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
 
-TileBinning tile_binning_plan(uint32_t n_instances, uint32_t n_tiles) {
+TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles) {
     TileBinning b;
     b.use_table = n_tiles > 0 && static_cast<size_t>(n_tiles) * 4 <= tile_hist_max_lds;
-    b.blocks = b.use_table ? (n_instances > 0 ? div_up(n_instances, tile_hist_min_segment) : 1u) : 0u;
+    b.blocks = b.use_table ? (n_visible > 0 ? div_up(n_visible, tile_hist_min_segment) : 1u) : 0u;
     if (b.blocks > tile_hist_max_blocks) b.blocks = tile_hist_max_blocks;
-    b.segment = b.use_table && n_instances > 0 ? div_up(n_instances, b.blocks) : 1u;
+    b.segment = b.use_table && n_visible > 0 ? div_up(n_visible, b.blocks) : 1u;
+    if (b.use_table && n_visible > 0) b.blocks = div_up(n_visible, b.segment);
     return b;
 }
 
-bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* local_rank, uint32_t* table,
-                        const TileScan& ts, uint32_t n_tiles, hipStream_t s) {
+bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* table, const TileScan& ts,
+                        uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
     const bool with_table = plan.use_table && n_instances > 0;
-    if (with_table) {
-        tile_hist_kernel<<<plan.blocks, 1024, n_tiles * 4, s>>>(keys, key_bytes, n_instances, plan.segment, local_rank, table, n_tiles);
-    } else {
+    if (!with_table) {
         if (!launch_fill_u32(ts.totals, 0u, n_tiles, s) || !launch_fill_u32(ts.cursor, 0u, n_tiles, s)) return false;
         if (n_instances > 0) {
             if (key_bytes == 2)
@@ -540,8 +569,8 @@ bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes
                                                                                            ts.totals, n_tiles);
         }
     }
-    tile_block_scan_kernel<<<div_up(n_tiles, 256), 256, 0, s>>>(with_table ? table : nullptr, with_table ? plan.blocks : 0u, n_tiles, ts.totals,
-                                                                  ts.local_start, ts.block_sums, ts.block_prefix, ts.ticket);
+    tile_column_scan_kernel<<<div_up(n_tiles, scan_tiles), 64 * scan_waves, 0, s>>>(with_table ? table : nullptr, with_table ? plan.blocks : 0u, n_tiles,
+                                                                        ts.totals, ts.local_start, ts.block_sums);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
@@ -553,11 +582,11 @@ bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_byte
     const uint32_t blocks = div_up(n_instances, 256);
     const uint32_t* tab = plan.use_table ? table : nullptr;
     if (key_bytes == 2)
-        tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, plan.segment,
-                                                            ts.block_prefix, ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
+        tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
+                                                            ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
     else
-        tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, plan.segment,
-                                                            ts.block_prefix, ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
+        tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
+                                                            ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
@@ -567,10 +596,10 @@ bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint64_t* bucket, uint3
     if (n_tiles == 0) return true;
     const uint32_t blocks = div_up(n_tiles, tile_sort_waves);
     if (key_bytes == 2)
-        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_prefix, ts.local_start, ranges, bucket, sorted_inst,
+        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ranges, bucket, sorted_inst,
                                                                      static_cast<uint16_t*>(sorted_keys), n_tiles);
     else
-        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_prefix, ts.local_start, ranges, bucket, sorted_inst,
+        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ranges, bucket, sorted_inst,
                                                                      static_cast<uint32_t*>(sorted_keys), n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;

@@ -89,7 +89,6 @@ __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t*
             counters[k] = c[k];
             host_counters[k] = c[k];
         }
-        counters[5] = 0;  // ticket of the tile scan's last block
         __threadfence_system();
     }
 }
