@@ -26,6 +26,10 @@ namespace {
 
 constexpr float log2e = 1.44269504089f;
 
+typedef float native_float4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(3))) char lds_char;
+typedef const __attribute__((address_space(3))) native_float4 lds_float4;
+
 struct Staged {
     float2 xy;
     float4 co;  // exp2-scaled conic (x, y, z) and opacity
@@ -437,17 +441,21 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
         for (uint32_t k = 0; k < n_steps; k += 2) {
             const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);
             const uint32_t ja = jab.x, jb = jab.y;
+            // staged float4 c of instance j, addressed in the LDS address space (32-bit offsets, 24-bit product)
+            const auto at = [stg](uint32_t j, uint32_t c) {
+                lds_char* base = (lds_char*)(stg);
+                const native_float4 v = *reinterpret_cast<lds_float4*>(base + __umul24(j, static_cast<uint32_t>(sizeof(stg[0]))) + 16u * c);
+                return make_float4(v.x, v.y, v.z, v.w);
+            };
             float dxa, dya, Ga, dxb, dyb, Gb;
-            const float alpha_a = eval_alpha(stg[ja][0], stg[ja][1], pxf, pyf, dxa, dya, Ga);
-            const float alpha_b = eval_alpha(stg[jb][0], stg[jb][1], pxf, pyf, dxb, dyb, Gb);
+            const float alpha_a = eval_alpha(at(ja, 0), at(ja, 1), pxf, pyf, dxa, dya, Ga);
+            const float alpha_b = eval_alpha(at(jb, 0), at(jb, 1), pxf, pyf, dxb, dyb, Gb);
             const bool ca = ja < last_rel && alpha_a >= min_alpha;
             const bool cb = jb < last_rel && alpha_b >= min_alpha;
             float v[16], wgb_a, wgb_b, e1a = 0.0f, e2a = 0.0f, e1b = 0.0f, e2b = 0.0f;
             const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            pair_terms<ABS>(ca, alpha_a, dxa, dya, stg[ja][2], ABS ? raw_conic_of(stg[ja][1]) : zero4, gr, gg, gb, gbg, T, A, v,
-                            wgb_a, e1a, e2a);
-            pair_terms<ABS>(cb, alpha_b, dxb, dyb, stg[jb][2], ABS ? raw_conic_of(stg[jb][1]) : zero4, gr, gg, gb, gbg, T, A, v + 8,
-                            wgb_b, e1b, e2b);
+            pair_terms<ABS>(ca, alpha_a, dxa, dya, at(ja, 2), ABS ? raw_conic_of(at(ja, 1)) : zero4, gr, gg, gb, gbg, T, A, v, wgb_a, e1a, e2a);
+            pair_terms<ABS>(cb, alpha_b, dxb, dyb, at(jb, 2), ABS ? raw_conic_of(at(jb, 1)) : zero4, gr, gg, gb, gbg, T, A, v + 8, wgb_b, e1b, e2b);
             part_main[main_b ? jb : ja] = group_reduce16(v, lane);
             float sx;
             if (ABS) {
