@@ -223,6 +223,9 @@ struct TileLayout {
     uint32_t* local_start;   // tile start within its 64-tile block
     uint32_t* block_sums;    // instances per 64-tile block
     uint32_t* cursor;        // per-tile bucket cursor of the global-atomic path
+    uint32_t* order_runs;    // per 64-tile block and size class: tiles, then the run's first position in the order
+    uint32_t* order_rank;    // per tile: size class << 16 | rank in its block's run
+    uint32_t* order;         // tile of each blend block, heaviest first
     size_t bytes;
 
     static TileLayout carve(char* base, uint32_t n_tiles) {
@@ -236,6 +239,9 @@ struct TileLayout {
         l.local_start = c.take<uint32_t>(n_tiles);
         l.block_sums = c.take<uint32_t>(div_up(n_tiles > 0 ? n_tiles : 1, 64));
         l.cursor = c.take<uint32_t>(n_tiles);
+        l.order_runs = c.take<uint32_t>(static_cast<uint64_t>(div_up(n_tiles > 0 ? n_tiles : 1, 64)) * order_classes);
+        l.order_rank = c.take<uint32_t>(n_tiles);
+        l.order = c.take<uint32_t>(n_tiles);
         l.bytes = c.offset + buffer_alignment;
         return l;
     }
@@ -734,7 +740,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
     if (!launch_create_instances(ca, key_bytes, plan, il.local_rank, il.table, n_tiles, s)) return EFGS_ERR_HIP;
     t.end(s);
-    const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor};
+    const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor, tl.order_runs, tl.order_rank, tl.order};
     t.begin(EFGS_STAGE_TILE_OFFSETS, s);
     if (!launch_tile_counts(plan, il.keys, key_bytes, n_instances, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
     t.end(s);
@@ -757,6 +763,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     b.final_T = tl.final_T;
     b.n_contrib = tl.n_contrib;
     b.tile_max = tl.tile_max;
+    b.order = tl.order;
     b.width = static_cast<uint32_t>(settings->width);
     b.height = static_cast<uint32_t>(settings->height);
     b.grid_w = grid_w;
@@ -837,6 +844,7 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     b.final_T = tl.final_T;
     b.n_contrib = tl.n_contrib;
     b.tile_max = tl.tile_max;
+    b.order = tl.order;
     b.inst_grads = inst_grads;
     b.width = static_cast<uint32_t>(settings->width);
     b.height = static_cast<uint32_t>(settings->height);
@@ -972,6 +980,7 @@ int efgs_update_pruning_scores(efgs_rasterizer* r, const efgs_primitives* prims,
     b.final_T = tl.final_T;
     b.n_contrib = tl.n_contrib;
     b.tile_max = tl.tile_max;
+    b.order = tl.order;
     b.inst_grads = inst_scores;
     b.width = static_cast<uint32_t>(settings->width);
     b.height = static_cast<uint32_t>(settings->height);

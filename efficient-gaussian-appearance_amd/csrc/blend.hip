@@ -101,9 +101,9 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
     __shared__ uint32_t s_list[tile_pixels / 64][4][list_len];  // per wave and group: batch indices to walk
     __shared__ uint32_t s_max[tile_pixels / 64];
 
-    const uint32_t tile = blockIdx.x;
-    const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
+    const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
     const uint32_t g = (lane >> 2) & 3u;
     const uint32_t px = tx * tile_width + (lane & 15u);
     const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);
@@ -338,9 +338,9 @@ __global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwa
     __shared__ uint32_t s_list[n_waves][4][list_len];
     __shared__ float s_part[n_slots * slot_stride];
 
-    const uint32_t tile = blockIdx.x;
-    const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
+    const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
     const uint32_t g = (lane >> 2) & 3u;
     const uint32_t px = tx * tile_width + (lane & 15u);
     const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);
@@ -539,9 +539,9 @@ __global__ __launch_bounds__(tile_pixels) void blend_scores_kernel(BlendBackward
     __shared__ uint32_t s_list[n_waves][4][list_len];
     __shared__ float s_part[n_slots][batch + 1];
 
-    const uint32_t tile = blockIdx.x;
-    const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
+    const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
     const uint32_t g = (lane >> 2) & 3u;
     const uint32_t px = tx * tile_width + (lane & 15u);
     const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);

@@ -66,11 +66,21 @@ bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const 
 // Tile scan state (tile arena): totals[t] instances of tile t, local_start[t] exclusive scan of the totals within
 // t's 64-tile block, block_sums per 64-tile block (tile t starts at the sum of block_sums over the blocks before
 // t / 64 plus local_start[t]), and a per-tile cursor for the global-atomic path.
+// Heaviest tile first: the one-block-per-tile blends run their blocks in a permutation of the tiles ordered by
+// instance count, descending (longest-processing-time-first list scheduling, so that a kernel's last blocks are
+// short ones). The count is bucketed into 64 classes (1 + 4 floor(log2 n) + the next two bits, reversed; an empty
+// tile is the last class); the column scan counts each 64-tile block's tiles per class and gives every tile its
+// rank among them (lane order), one small kernel turns the counts into each (block, class) run's first position,
+// and the tile sort writes every tile at its position. Deterministic; a tile's result does not depend on it.
+constexpr uint32_t order_classes = 64;
 struct TileScan {
     uint32_t* totals;
     uint32_t* local_start;
     uint32_t* block_sums;
     uint32_t* cursor;
+    uint32_t* order_runs;  // per 64-tile block and class: the class's tiles in the block, then their first position
+    uint32_t* order_rank;  // per tile: class << 16 | rank among the block's tiles of its class
+    uint32_t* order;       // the tile order (block b of a blend runs tile order[b])
 };
 // per-tile counts (global atomics without a table) and the scan above
 bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* table, const TileScan& ts,
@@ -95,6 +105,7 @@ struct BlendForwardArgs {
     float* final_T;                // (tiles x 192); null for an inference render (no backward state)
     uint32_t* n_contrib;           // (tiles x 192)
     uint32_t* tile_max;            // (tiles)
+    const uint32_t* order;         // tile of each block, heaviest first (null: block index)
     uint32_t width, height, grid_w, n_tiles;
     uint32_t hwc;                  // image layout (H, W, 3)
     uint32_t clamp;                // image clamped to [0, 1] (NaN to 0)
@@ -112,6 +123,7 @@ struct BlendBackwardArgs {
     const float* final_T;
     const uint32_t* n_contrib;
     const uint32_t* tile_max;
+    const uint32_t* order;         // tile of each block, heaviest first (null: block index)
     float* inst_grads;             // (I x 12), emission order (pruning scores: one float per instance)
     uint32_t width, height, grid_w, n_tiles;
     uint32_t abs_grads;            // also reduce |dL/dmean2d| (third densification row)

@@ -171,10 +171,21 @@ __global__ __launch_bounds__(1024) void create_instances_hist_kernel(CreateInsta
 constexpr uint32_t scan_tiles = 64;
 constexpr uint32_t scan_waves = 16;
 constexpr uint32_t scan_per_wave = tile_hist_max_blocks / scan_waves;
+// class of a tile with n instances: 0 for the heaviest, order_classes - 1 for an empty tile
+__device__ __forceinline__ uint32_t order_class(uint32_t n) {
+    if (n == 0) return order_classes - 1;
+    const uint32_t e = 31u - static_cast<uint32_t>(__clz(static_cast<int>(n)));
+    const uint32_t m = e >= 2 ? (n >> (e - 2)) & 3u : (n << (2 - e)) & 3u;
+    return order_classes - 1 - min(1u + 4u * e + m, order_classes - 1);
+}
+
 __global__ __launch_bounds__(64 * scan_waves) void tile_column_scan_kernel(uint32_t* table, uint32_t n_segments, uint32_t n_tiles,
-                                                                          uint32_t* totals, uint32_t* local_start, uint32_t* block_sums) {
+                                                                          uint32_t* totals, uint32_t* local_start, uint32_t* block_sums,
+                                                                          uint32_t* order_runs, uint32_t* order_rank) {
     __shared__ uint32_t s_part[scan_waves][scan_tiles];
     __shared__ uint32_t s_start[scan_tiles];
+    __shared__ uint32_t s_runs[order_classes];
+    static_assert(order_classes == 64 && scan_tiles == 64, "one class and one tile per lane");
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.x * scan_tiles + lane;
     const bool in = t < n_tiles;
@@ -204,6 +215,22 @@ __global__ __launch_bounds__(64 * scan_waves) void tile_column_scan_kernel(uint3
         if (in) local_start[t] = inc - total;
         s_start[lane] = inc - total;
         if (lane == 63) block_sums[blockIdx.x] = inc;
+        // tile order: the block's tiles per class and each tile's rank among its class (the lanes of a class
+        // are found by one ballot per class bit)
+        const uint32_t cls = in ? order_class(total) : order_classes;
+        uint64_t same = __ballot(in);
+#pragma unroll
+        for (uint32_t bit = 1; bit < order_classes; bit <<= 1) {
+            const uint64_t set = __ballot((cls & bit) != 0);
+            same &= (cls & bit) ? set : ~set;
+        }
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(same >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(same), 0u));
+        s_runs[lane] = 0u;  // order_classes == 64: one class per lane
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (in && rank == 0) s_runs[cls] = static_cast<uint32_t>(__popcll(same));
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        order_runs[static_cast<size_t>(blockIdx.x) * order_classes + lane] = s_runs[lane];
+        if (in) order_rank[t] = cls << 16 | rank;
     }
     if (!table) return;
     __syncthreads();
@@ -417,7 +444,8 @@ __device__ __forceinline__ void sort_run_split192(const uint64_t* run, uint32_t 
 
 template <typename KeyT>
 __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* totals, const uint32_t* block_sums,
-                                                                   const uint32_t* local_start, uint2* ranges, uint64_t* bucket,
+                                                                   const uint32_t* local_start, const uint32_t* order_runs,
+                                                                   const uint32_t* order_rank, uint32_t* order, uint2* ranges, uint64_t* bucket,
                                                                    uint32_t* sorted_inst, KeyT* sorted_keys, uint32_t n_tiles) {
     __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -426,7 +454,11 @@ __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32
     const uint32_t n = totals[tile];
     const uint32_t start = scan_block_prefix_wave(block_sums, tile / scan_tiles, lane) + local_start[tile];
     const uint2 r = n > 0 ? make_uint2(start, start + n) : make_uint2(0u, 0u);  // (0, 0) for an empty tile, as the reference
-    if (lane == 0) ranges[tile] = r;
+    if (lane == 0) {
+        ranges[tile] = r;
+        const uint32_t cr = order_rank[tile];
+        order[order_runs[static_cast<size_t>(tile / scan_tiles) * order_classes + (cr >> 16)] + (cr & 0xffffu)] = tile;
+    }
     if (n == 0) return;
     uint64_t* run = bucket + r.x;
     uint32_t* out = sorted_inst + r.x;
@@ -554,6 +586,53 @@ TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles) {
     return b;
 }
 
+// One block: order_runs[b][c] (tiles of class c in 64-tile block b) becomes the first position of that run in
+// the tile order: the tiles of the classes before c, then those of class c in the blocks before b. Lane c of every
+// wave handles class c (a block's 64 counts are one coalesced row); wave w the w-th sixteenth of the blocks, whose
+// rows it holds in registers (16 at a time), so each row is read once and written once.
+__global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_runs, uint32_t n_blocks) {
+    constexpr uint32_t n_waves = 1024 / 64;
+    constexpr uint32_t rows = 16;  // rows per lane in registers per pass
+    __shared__ uint32_t s_part[n_waves][order_classes];
+    const uint32_t c = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t per = (n_blocks + n_waves - 1) / n_waves;
+    const uint32_t b0 = min(wave * per, n_blocks), b1 = min(b0 + per, n_blocks);
+    uint32_t sum = 0;
+    for (uint32_t r0 = b0; r0 < b1; r0 += rows) {
+        uint32_t v[rows];
+#pragma unroll
+        for (uint32_t k = 0; k < rows; k++) v[k] = r0 + k < b1 ? order_runs[static_cast<size_t>(r0 + k) * order_classes + c] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < rows; k++) sum += v[k];
+    }
+    s_part[wave][c] = sum;
+    __syncthreads();
+    uint32_t total = 0, before = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < n_waves; w++) {
+        const uint32_t x = s_part[w][c];
+        total += x;
+        before += w < wave ? x : 0u;
+    }
+    uint32_t inc = total;  // classes in lane order: prefix over the lanes
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t x = static_cast<uint32_t>(__shfl_up(static_cast<int>(inc), o));
+        if (c >= o) inc += x;
+    }
+    uint32_t running = inc - total + before;
+    for (uint32_t r0 = b0; r0 < b1; r0 += rows) {
+        uint32_t v[rows];
+#pragma unroll
+        for (uint32_t k = 0; k < rows; k++) v[k] = r0 + k < b1 ? order_runs[static_cast<size_t>(r0 + k) * order_classes + c] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < rows; k++) {
+            if (r0 + k < b1) order_runs[static_cast<size_t>(r0 + k) * order_classes + c] = running;
+            running += v[k];
+        }
+    }
+}
+
 bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* table, const TileScan& ts,
                         uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
@@ -570,7 +649,9 @@ bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes
         }
     }
     tile_column_scan_kernel<<<div_up(n_tiles, scan_tiles), 64 * scan_waves, 0, s>>>(with_table ? table : nullptr, with_table ? plan.blocks : 0u, n_tiles,
-                                                                        ts.totals, ts.local_start, ts.block_sums);
+                                                                        ts.totals, ts.local_start, ts.block_sums, ts.order_runs, ts.order_rank);
+    EFGS_HIP_CHECK(hipGetLastError());
+    tile_order_runs_kernel<<<1, 1024, 0, s>>>(ts.order_runs, div_up(n_tiles, scan_tiles));
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
@@ -596,10 +677,10 @@ bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint64_t* bucket, uint3
     if (n_tiles == 0) return true;
     const uint32_t blocks = div_up(n_tiles, tile_sort_waves);
     if (key_bytes == 2)
-        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ranges, bucket, sorted_inst,
+        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ranges, bucket, sorted_inst,
                                                                      static_cast<uint16_t*>(sorted_keys), n_tiles);
     else
-        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ranges, bucket, sorted_inst,
+        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ranges, bucket, sorted_inst,
                                                                      static_cast<uint32_t*>(sorted_keys), n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;

@@ -102,4 +102,5 @@ bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_
     return true;
 }
 
+
 }  // namespace efgs
