@@ -148,7 +148,7 @@ struct efgs_rasterizer {
 
     // instance count of the last forward and the scene size it was for: sizes the next frame's instance
     // buffers before its counter readback
-    uint32_t instance_hint = 0, hint_primitives = 0, hint_tiles = 0;
+    uint32_t instance_hint = 0, visible_hint = 0, hint_primitives = 0, hint_tiles = 0;
     efgs::StageTimer timer;
     // specialised preprocess kernels of the current configuration, per variant and direction (forward,
     // backward), for the device they were loaded on; cleared whenever the configuration changes
@@ -273,6 +273,11 @@ struct InstanceLayout {
         return l;
     }
 };
+
+// instances the frame's instance buffers are laid out for (at least its instance count)
+uint64_t instance_capacity(const efgs_frame& f) {
+    return static_cast<uint64_t>(f.instance_capacity > f.n_instances ? f.instance_capacity : f.n_instances);
+}
 
 int fail(int code, const std::string& msg) {
     set_error(msg);
@@ -661,6 +666,14 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     const TileLayout tl = TileLayout::carve(tblob, n_tiles);
     const CameraArgs cam = camera_args(r, settings, variant, grid_w, grid_h);
     StageTimer& t = r->timer;
+    // Instance buffers are laid out for `capacity` instances. With a count from the previous frame of this scene
+    // size, everything after the counter scan is launched at once into buffers with 12.5 % headroom: the scan flags
+    // a count above the capacity, the binning and blend kernels then return at once, and the host, which reads the
+    // counters only after its last launch, re-runs them with exact buffers. Without one the host reads the
+    // counters first.
+    const bool speculate = n > 0 && r->instance_hint > 0 && r->hint_primitives == n && r->hint_tiles == n_tiles;
+    uint64_t capacity = speculate ? static_cast<uint64_t>(r->instance_hint) + r->instance_hint / 8 + 1024 : 0;
+    if (capacity > 0xfffffff0ull) capacity = 0xfffffff0ull;
 
     if (n > 0) {
         RtcKernel k;
@@ -689,12 +702,10 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (!launch_rtc(k, blocks, preprocess_block, shared, &a, s)) return EFGS_ERR_HIP;
         t.end(s);
         t.begin(EFGS_STAGE_COMPACT, s);
-        if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, r->host_counters_dev, chunks, s))
+        if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, r->host_counters_dev,
+                                      speculate ? static_cast<uint32_t>(capacity) : 0xffffffffu, chunks, s))
             return EFGS_ERR_HIP;
-        // the scan has written the counters to the pinned host buffer: the host waits for it while the compaction
-        // runs, and sizes the instance buffers meanwhile from the previous frame's count (12.5 % headroom) when the
-        // scene size matches, so that neither the allocation nor the compaction sits between the wait and the next
-        // launch
+        // the scan writes the counters to the pinned host buffer as well; the event marks them written
         if (hipEventRecord(r->counters_ready, s) != hipSuccess)
             return fail(EFGS_ERR_HIP, std::string("recording the counter event failed: ") + hipGetErrorString(hipGetLastError()));
         if (!launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
@@ -702,13 +713,70 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     } else {
         if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
     }
+
+    // Instance binning and the blend, into instance buffers laid out for `cap` instances (visible_plan: the visible
+    // count the segment plan is made for; max_visible / max_instances: bounds on the counts, the grid sizes).
+    InstanceLayout il{};
+    const auto bin_and_blend = [&](char* iblob, uint64_t cap, uint32_t visible_plan, uint32_t max_visible, uint32_t max_instances) -> int {
+        il = InstanceLayout::carve(iblob, cap, key_bytes, n_tiles);
+        const TileBinning plan = tile_binning_plan(visible_plan, n_tiles);
+        CreateInstancesArgs ca;
+        ca.visible_prims = pl.visible_prims;
+        ca.prim_offset = pl.prim_offset;
+        ca.n_touched = pl.n_touched;
+        ca.records = pl.records;
+        ca.keys = il.keys;
+        ca.inst_prim = il.inst_prim;
+        ca.counters = pl.counters;
+        ca.grid_w = grid_w;
+        ca.max_visible = max_visible;
+        ca.n_visible = 0;
+        t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
+        if (!launch_create_instances(ca, key_bytes, plan, il.local_rank, il.table, n_tiles, s)) return EFGS_ERR_HIP;
+        t.end(s);
+        const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor, tl.order_runs, tl.order_rank, tl.order, pl.counters};
+        t.begin(EFGS_STAGE_TILE_OFFSETS, s);
+        if (!launch_tile_counts(plan, il.keys, key_bytes, max_instances, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
+        t.end(s);
+        t.begin(EFGS_STAGE_TILE_BUCKETS, s);
+        if (!launch_tile_buckets(plan, il.keys, key_bytes, il.inst_prim, pl.depth_keys, il.table, il.local_rank, ts, il.bucket, max_instances,
+                                 n_tiles, s))
+            return EFGS_ERR_HIP;
+        t.end(s);
+        t.begin(EFGS_STAGE_TILE_SORT, s);
+        if (!launch_tile_sort(ts, tl.ranges, il.bucket, il.sorted_inst, il.sorted_keys, key_bytes, n_tiles, s)) return EFGS_ERR_HIP;
+        t.end(s);
+
+        BlendForwardArgs b;
+        b.ranges = tl.ranges;
+        b.sorted_inst = il.sorted_inst;
+        b.inst_prim = il.inst_prim;
+        b.records = pl.records;
+        b.bg = settings->bg_color;
+        b.image = image;
+        b.final_T = tl.final_T;
+        b.n_contrib = tl.n_contrib;
+        b.tile_max = tl.tile_max;
+        b.order = tl.order;
+        b.overflow = pl.counters + counter_overflow;
+        b.width = static_cast<uint32_t>(settings->width);
+        b.height = static_cast<uint32_t>(settings->height);
+        b.grid_w = grid_w;
+        b.n_tiles = n_tiles;
+        b.hwc = hwc ? 1u : 0u;
+        b.clamp = clamp ? 1u : 0u;
+        if (!frame) b.final_T = nullptr;
+        t.begin(EFGS_STAGE_BLEND_FORWARD, s);
+        if (!launch_blend_forward(b, s)) return EFGS_ERR_HIP;
+        t.end(s);
+        return EFGS_OK;
+    };
+
     char* iblob = nullptr;
-    size_t iblob_bytes = 0;
-    if (r->instance_hint > 0 && r->hint_primitives == n && r->hint_tiles == n_tiles) {
-        const uint64_t guess = static_cast<uint64_t>(r->instance_hint) + r->instance_hint / 8 + 1024;
-        iblob_bytes = InstanceLayout::carve(nullptr, guess, key_bytes, n_tiles).bytes;
-        iblob = static_cast<char*>(alloc(alloc_ctx, iblob_bytes));
+    if (speculate) {
+        iblob = static_cast<char*>(alloc(alloc_ctx, InstanceLayout::carve(nullptr, capacity, key_bytes, n_tiles).bytes));
         if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
+        if (int c = bin_and_blend(iblob, capacity, r->visible_hint, n, static_cast<uint32_t>(capacity))) return c;
     }
     t.begin(EFGS_STAGE_COUNTER_READ, s);
     if (n > 0 && hipEventSynchronize(r->counters_ready) != hipSuccess)
@@ -717,63 +785,18 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     const uint32_t n_visible = n > 0 ? __atomic_load_n(&r->host_counters[0], __ATOMIC_ACQUIRE) : 0u;
     const uint32_t n_instances = n > 0 ? __atomic_load_n(&r->host_counters[1], __ATOMIC_ACQUIRE) : 0u;
     r->instance_hint = n_instances;
+    r->visible_hint = n_visible;
     r->hint_primitives = n;
     r->hint_tiles = n_tiles;
-
-    const InstanceLayout il0 = InstanceLayout::carve(nullptr, n_instances, key_bytes, n_tiles);
-    if (!iblob || il0.bytes > iblob_bytes) {
-        iblob = static_cast<char*>(alloc(alloc_ctx, il0.bytes));
+    if (!speculate || n_instances > capacity) {
+        // first frame of this scene size, or more instances than the speculative buffers hold (the device skipped
+        // the binning and the blend): exact buffers, with the overflow flag cleared
+        if (speculate && !launch_fill_u32(pl.counters + counter_overflow, 0u, 1, s)) return EFGS_ERR_HIP;
+        capacity = n_instances;
+        iblob = static_cast<char*>(alloc(alloc_ctx, InstanceLayout::carve(nullptr, capacity, key_bytes, n_tiles).bytes));
         if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
+        if (int c = bin_and_blend(iblob, capacity, n_visible, n_visible, n_instances)) return c;
     }
-    const InstanceLayout il = InstanceLayout::carve(iblob, n_instances, key_bytes, n_tiles);
-    const TileBinning plan = tile_binning_plan(n_visible, n_tiles);
-    CreateInstancesArgs ca;
-    ca.visible_prims = pl.visible_prims;
-    ca.prim_offset = pl.prim_offset;
-    ca.n_touched = pl.n_touched;
-    ca.records = pl.records;
-    ca.keys = il.keys;
-    ca.inst_prim = il.inst_prim;
-    ca.counters = pl.counters;
-    ca.grid_w = grid_w;
-    ca.n_visible = n_visible;
-    t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
-    if (!launch_create_instances(ca, key_bytes, plan, il.local_rank, il.table, n_tiles, s)) return EFGS_ERR_HIP;
-    t.end(s);
-    const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor, tl.order_runs, tl.order_rank, tl.order};
-    t.begin(EFGS_STAGE_TILE_OFFSETS, s);
-    if (!launch_tile_counts(plan, il.keys, key_bytes, n_instances, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
-    t.end(s);
-    t.begin(EFGS_STAGE_TILE_BUCKETS, s);
-    if (!launch_tile_buckets(plan, il.keys, key_bytes, il.inst_prim, pl.depth_keys, il.table, il.local_rank, ts, il.bucket, n_instances, n_tiles, s))
-        return EFGS_ERR_HIP;
-    t.end(s);
-    t.begin(EFGS_STAGE_TILE_SORT, s);
-    if (!launch_tile_sort(ts, tl.ranges, il.bucket, il.sorted_inst, il.sorted_keys, key_bytes, n_tiles, s)) return EFGS_ERR_HIP;
-    t.end(s);
-    const uint32_t* sorted_inst = il.sorted_inst;
-
-    BlendForwardArgs b;
-    b.ranges = tl.ranges;
-    b.sorted_inst = sorted_inst;
-    b.inst_prim = il.inst_prim;
-    b.records = pl.records;
-    b.bg = settings->bg_color;
-    b.image = image;
-    b.final_T = tl.final_T;
-    b.n_contrib = tl.n_contrib;
-    b.tile_max = tl.tile_max;
-    b.order = tl.order;
-    b.width = static_cast<uint32_t>(settings->width);
-    b.height = static_cast<uint32_t>(settings->height);
-    b.grid_w = grid_w;
-    b.n_tiles = n_tiles;
-    b.hwc = hwc ? 1u : 0u;
-    b.clamp = clamp ? 1u : 0u;
-    if (!frame) b.final_T = nullptr;
-    t.begin(EFGS_STAGE_BLEND_FORWARD, s);
-    if (!launch_blend_forward(b, s)) return EFGS_ERR_HIP;
-    t.end(s);
     if (!frame) return EFGS_OK;
 
     frame->primitive_buffers = pblob;
@@ -782,6 +805,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     frame->n_primitives = n;
     frame->n_visible = n_visible;
     frame->n_instances = n_instances;
+    frame->instance_capacity = static_cast<int64_t>(capacity);
     frame->grid_width = static_cast<int32_t>(grid_w);
     frame->grid_height = static_cast<int32_t>(grid_h);
     frame->key_bytes = key_bytes;
@@ -826,7 +850,7 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     const uint32_t n_instances = static_cast<uint32_t>(frame->n_instances);
     const PrimitiveLayout pl = PrimitiveLayout::carve(static_cast<char*>(frame->primitive_buffers), n);
     const TileLayout tl = TileLayout::carve(static_cast<char*>(frame->tile_buffers), n_tiles);
-    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), n_instances, frame->key_bytes, n_tiles);
+    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), instance_capacity(*frame), frame->key_bytes, n_tiles);
     const uint32_t* sorted_inst = il.sorted_inst;
 
     const size_t grad_bytes = static_cast<size_t>(n_instances > 0 ? n_instances : 1) * 12 * sizeof(float);
@@ -966,7 +990,7 @@ int efgs_update_pruning_scores(efgs_rasterizer* r, const efgs_primitives* prims,
     const uint32_t n_instances = static_cast<uint32_t>(frame.n_instances);
     const PrimitiveLayout pl = PrimitiveLayout::carve(static_cast<char*>(frame.primitive_buffers), n);
     const TileLayout tl = TileLayout::carve(static_cast<char*>(frame.tile_buffers), n_tiles);
-    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame.instance_buffers), n_instances, frame.key_bytes, n_tiles);
+    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame.instance_buffers), instance_capacity(frame), frame.key_bytes, n_tiles);
     float* inst_scores = static_cast<float*>(alloc(alloc_ctx, static_cast<size_t>(n_instances) * sizeof(float)));
     if (!inst_scores) return fail(EFGS_ERR_ALLOC, "allocation of the instance score buffer failed");
     BlendBackwardArgs b;
@@ -1033,8 +1057,7 @@ int efgs_get_frame_views(const efgs_frame* frame, efgs_frame_views* v) {
     const uint32_t n_tiles = static_cast<uint32_t>(frame->grid_width) * static_cast<uint32_t>(frame->grid_height);
     const PrimitiveLayout pl = PrimitiveLayout::carve(static_cast<char*>(frame->primitive_buffers), n);
     const TileLayout tl = TileLayout::carve(static_cast<char*>(frame->tile_buffers), n_tiles);
-    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), static_cast<uint64_t>(frame->n_instances),
-                                                    frame->key_bytes, n_tiles);
+    const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), instance_capacity(*frame), frame->key_bytes, n_tiles);
     v->n_touched = pl.n_touched;
     v->depth_keys = pl.depth_keys;
     v->records = reinterpret_cast<const float*>(pl.records);

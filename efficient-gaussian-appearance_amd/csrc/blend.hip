@@ -93,6 +93,7 @@ __device__ __forceinline__ void build_group_lists(const uint64_t (&m)[4], uint32
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
 __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForwardArgs a) {
+    if (a.overflow && *a.overflow != 0) return;  // the binning was skipped: the host re-runs the frame
     constexpr uint32_t list_len = 64;
     // (x, y, packed pixel rectangle): the 16-byte stride of s_co and s_col, so the pair loads share one address
     __shared__ float4 s_xy[tile_pixels];

@@ -29,10 +29,13 @@ inline uint32_t div_up(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a
 
 // ---- rasterizer stages -------------------------------------------------------------------------------------
 bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
-// counters: [0] V, [1] I, [2] instance-emission mismatches, [3] / [4] min / max depth key of the visible set
+// counters: [0] V, [1] I, [2] instance-emission mismatches, [3] / [4] min / max depth key of the visible set,
+// [5] 1 when I exceeds the instance capacity the binning buffers were laid out for (the binning and blend kernels
+// then return at once; the host re-runs them with buffers of the exact size)
 constexpr uint32_t n_counters = 8;
+constexpr uint32_t counter_overflow = 5;
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
-                              uint32_t* host_counters, uint32_t n_blocks, hipStream_t s);
+                              uint32_t* host_counters, uint32_t instance_capacity, uint32_t n_blocks, hipStream_t s);
 // visible primitives in index order and their first emission slots (exclusive scan of the tile counts in
 // index order)
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,
@@ -56,11 +59,13 @@ struct CreateInstancesArgs {
     const PrimRecord* records;
     void* keys;                // tile key per emission slot, key_bytes wide
     uint32_t* inst_prim;
-    uint32_t* counters;
-    uint32_t grid_w, n_visible;
+    uint32_t* counters;        // the visible count is read here ([0]); nothing is emitted when [counter_overflow] is set
+    uint32_t grid_w;
+    uint32_t max_visible;      // bound on the visible count (grid size of the path without a table)
+    uint32_t n_visible;        // set by the kernels from counters[0]
 };
 // (tile key, primitive) at every emission slot; with a table also each instance's rank | segment << 24 and the
-// segments' per-tile counts
+// segments' per-tile counts (plan.blocks segments of ceil(V / plan.blocks) visible primitives)
 bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const TileBinning& plan, uint32_t* local_rank, uint32_t* table,
                              uint32_t n_tiles, hipStream_t s);
 // Tile scan state (tile arena): totals[t] instances of tile t, local_start[t] exclusive scan of the totals within
@@ -81,13 +86,16 @@ struct TileScan {
     uint32_t* order_runs;  // per 64-tile block and class: the class's tiles in the block, then their first position
     uint32_t* order_rank;  // per tile: class << 16 | rank among the block's tiles of its class
     uint32_t* order;       // the tile order (block b of a blend runs tile order[b])
+    const uint32_t* counters;  // instance count ([1]) and overflow flag ([counter_overflow]) on the device
 };
 // per-tile counts (global atomics without a table) and the scan above
-bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* table, const TileScan& ts,
+// (max_instances: bound on the instance count, the grid size of the path without a table; the kernels read the
+// count itself from ts.counters)
+bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t max_instances, uint32_t* table, const TileScan& ts,
                         uint32_t n_tiles, hipStream_t s);
 // every instance's sort key (depth key of its primitive << 32 | emission index) into a slot of its tile's range
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
-                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,
+                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t max_instances,
                          uint32_t n_tiles, hipStream_t s);
 // per tile: [start, end) into ranges and its keys sorted ascending -> emission indices in sorted_inst, tile id
 // in sorted_keys
@@ -106,6 +114,7 @@ struct BlendForwardArgs {
     uint32_t* n_contrib;           // (tiles x 192)
     uint32_t* tile_max;            // (tiles)
     const uint32_t* order;         // tile of each block, heaviest first (null: block index)
+    const uint32_t* overflow;      // nothing is rendered when *overflow != 0 (null: never)
     uint32_t width, height, grid_w, n_tiles;
     uint32_t hwc;                  // image layout (H, W, 3)
     uint32_t clamp;                // image clamped to [0, 1] (NaN to 0)

@@ -133,17 +133,23 @@ __device__ __forceinline__ void emit_primitive(const CreateInstancesArgs& a, uin
 // One thread per visible primitive (the path for grids whose tile histogram does not fit the LDS).
 template <typename KeyT>
 __global__ __launch_bounds__(instance_block) void create_instances_kernel(CreateInstancesArgs a) {
+    if (a.counters[counter_overflow] != 0) return;
+    a.n_visible = a.counters[0];
+    if (blockIdx.x * instance_block >= a.n_visible) return;  // (block-uniform: the grid covers a bound on V)
     const uint32_t i = blockIdx.x * instance_block + threadIdx.x;
     emit_primitive<KeyT>(a, i, i < a.n_visible, threadIdx.x & 63u, [](uint32_t, uint32_t) {});
 }
 
-// Emission with the per-tile counts: block s emits the visible primitives [s P, (s + 1) P) (index order, so its
-// emission slots are one contiguous run, its segment), counts them per tile in an LDS histogram whose atomic
-// return values rank every instance among the segment's instances of its tile (in arbitrary order: the per-tile
-// sort fixes the order later), stores rank | s << 24 per instance and writes its histogram row table[s][*].
+// Emission with the per-tile counts: block s emits the visible primitives [s P, (s + 1) P), P = ceil(V / blocks)
+// (index order, so its emission slots are one contiguous run, its segment), counts them per tile in an LDS
+// histogram whose atomic return values rank every instance among the segment's instances of its tile (in
+// arbitrary order: the per-tile sort fixes the order later), stores rank | s << 24 per instance and writes its
+// histogram row table[s][*].
 template <typename KeyT>
-__global__ __launch_bounds__(1024) void create_instances_hist_kernel(CreateInstancesArgs a, uint32_t per_segment, uint32_t* local_rank,
-                                                                    uint32_t* table, uint32_t n_tiles) {
+__global__ __launch_bounds__(1024) void create_instances_hist_kernel(CreateInstancesArgs a, uint32_t* local_rank, uint32_t* table, uint32_t n_tiles) {
+    if (a.counters[counter_overflow] != 0) return;
+    a.n_visible = a.counters[0];
+    const uint32_t per_segment = (a.n_visible + gridDim.x - 1) / gridDim.x;
     extern __shared__ uint32_t hist[];
     for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) hist[t] = 0;
     __syncthreads();
@@ -181,7 +187,8 @@ __device__ __forceinline__ uint32_t order_class(uint32_t n) {
 
 __global__ __launch_bounds__(64 * scan_waves) void tile_column_scan_kernel(uint32_t* table, uint32_t n_segments, uint32_t n_tiles,
                                                                           uint32_t* totals, uint32_t* local_start, uint32_t* block_sums,
-                                                                          uint32_t* order_runs, uint32_t* order_rank) {
+                                                                          uint32_t* order_runs, uint32_t* order_rank, const uint32_t* counters) {
+    if (counters[counter_overflow] != 0) return;
     __shared__ uint32_t s_part[scan_waves][scan_tiles];
     __shared__ uint32_t s_start[scan_tiles];
     __shared__ uint32_t s_runs[order_classes];
@@ -244,9 +251,10 @@ __global__ __launch_bounds__(64 * scan_waves) void tile_column_scan_kernel(uint3
 }
 
 template <typename KeyT>
-__global__ __launch_bounds__(256) void tile_count_global_kernel(const KeyT* keys, uint32_t n_instances, uint32_t* totals, uint32_t n_tiles) {
+__global__ __launch_bounds__(256) void tile_count_global_kernel(const KeyT* keys, const uint32_t* counters, uint32_t* totals, uint32_t n_tiles) {
+    if (counters[counter_overflow] != 0) return;
     const uint32_t e = blockIdx.x * 256u + threadIdx.x;
-    if (e >= n_instances) return;
+    if (e >= counters[1]) return;
     const uint32_t t = static_cast<uint32_t>(keys[e]);
     if (t < n_tiles) atomicAdd(&totals[t], 1u);
 }
@@ -268,10 +276,13 @@ constexpr uint32_t max_scan_blocks = static_cast<uint32_t>(tile_hist_max_lds / 4
 template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
                                                           const uint32_t* table, const uint32_t* local_rank, const uint32_t* block_sums,
-                                                          const uint32_t* local_start, uint32_t* cursor, uint64_t* bucket, uint32_t n_instances,
+                                                          const uint32_t* local_start, uint32_t* cursor, uint64_t* bucket, const uint32_t* counters,
                                                           uint32_t n_tiles) {
     __shared__ uint32_t s_prefix[max_scan_blocks];
     __shared__ uint32_t s_waves[4];
+    if (counters[counter_overflow] != 0) return;
+    const uint32_t n_instances = counters[1];
+    if (blockIdx.x * 256u >= n_instances) return;  // (block-uniform: the grid covers a bound on I)
     const uint32_t n_blocks = (n_tiles + scan_tiles - 1) / scan_tiles;
     if (n_blocks <= max_scan_blocks) {
         const uint32_t v = threadIdx.x < n_blocks ? block_sums[threadIdx.x] : 0u;
@@ -445,8 +456,9 @@ __device__ __forceinline__ void sort_run_split192(const uint64_t* run, uint32_t 
 template <typename KeyT>
 __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* totals, const uint32_t* block_sums,
                                                                    const uint32_t* local_start, const uint32_t* order_runs,
-                                                                   const uint32_t* order_rank, uint32_t* order, uint2* ranges, uint64_t* bucket,
-                                                                   uint32_t* sorted_inst, KeyT* sorted_keys, uint32_t n_tiles) {
+                                                                   const uint32_t* order_rank, uint32_t* order, const uint32_t* counters, uint2* ranges,
+                                                                   uint64_t* bucket, uint32_t* sorted_inst, KeyT* sorted_keys, uint32_t n_tiles) {
+    if (counters[counter_overflow] != 0) return;
     __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t tile = blockIdx.x * tile_sort_waves + wave;
@@ -558,15 +570,15 @@ bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_off
 
 bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const TileBinning& plan, uint32_t* local_rank, uint32_t* table,
                              uint32_t n_tiles, hipStream_t s) {
-    if (a.n_visible == 0) return true;
+    if (a.max_visible == 0) return true;
     if (plan.use_table) {
         const size_t lds = static_cast<size_t>(n_tiles) * 4;
         if (key_bytes == 2)
-            create_instances_hist_kernel<uint16_t><<<plan.blocks, 1024, lds, s>>>(a, plan.segment, local_rank, table, n_tiles);
+            create_instances_hist_kernel<uint16_t><<<plan.blocks, 1024, lds, s>>>(a, local_rank, table, n_tiles);
         else
-            create_instances_hist_kernel<uint32_t><<<plan.blocks, 1024, lds, s>>>(a, plan.segment, local_rank, table, n_tiles);
+            create_instances_hist_kernel<uint32_t><<<plan.blocks, 1024, lds, s>>>(a, local_rank, table, n_tiles);
     } else {
-        const uint32_t blocks = div_up(a.n_visible, instance_block);
+        const uint32_t blocks = div_up(a.max_visible, instance_block);
         if (key_bytes == 2)
             create_instances_kernel<uint16_t><<<blocks, instance_block, 0, s>>>(a);
         else
@@ -590,7 +602,8 @@ TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles) {
 // the tile order: the tiles of the classes before c, then those of class c in the blocks before b. Lane c of every
 // wave handles class c (a block's 64 counts are one coalesced row); wave w the w-th sixteenth of the blocks, whose
 // rows it holds in registers (16 at a time), so each row is read once and written once.
-__global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_runs, uint32_t n_blocks) {
+__global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_runs, uint32_t n_blocks, const uint32_t* counters) {
+    if (counters[counter_overflow] != 0) return;
     constexpr uint32_t n_waves = 1024 / 64;
     constexpr uint32_t rows = 16;  // rows per lane in registers per pass
     __shared__ uint32_t s_part[n_waves][order_classes];
@@ -633,41 +646,42 @@ __global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_r
     }
 }
 
-bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t n_instances, uint32_t* table, const TileScan& ts,
+bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t max_instances, uint32_t* table, const TileScan& ts,
                         uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
-    const bool with_table = plan.use_table && n_instances > 0;
+    const bool with_table = plan.use_table && max_instances > 0;
     if (!with_table) {
         if (!launch_fill_u32(ts.totals, 0u, n_tiles, s) || !launch_fill_u32(ts.cursor, 0u, n_tiles, s)) return false;
-        if (n_instances > 0) {
+        if (max_instances > 0) {
             if (key_bytes == 2)
-                tile_count_global_kernel<uint16_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint16_t*>(keys), n_instances,
+                tile_count_global_kernel<uint16_t><<<div_up(max_instances, 256), 256, 0, s>>>(static_cast<const uint16_t*>(keys), ts.counters,
                                                                                            ts.totals, n_tiles);
             else
-                tile_count_global_kernel<uint32_t><<<div_up(n_instances, 256), 256, 0, s>>>(static_cast<const uint32_t*>(keys), n_instances,
+                tile_count_global_kernel<uint32_t><<<div_up(max_instances, 256), 256, 0, s>>>(static_cast<const uint32_t*>(keys), ts.counters,
                                                                                            ts.totals, n_tiles);
         }
     }
     tile_column_scan_kernel<<<div_up(n_tiles, scan_tiles), 64 * scan_waves, 0, s>>>(with_table ? table : nullptr, with_table ? plan.blocks : 0u, n_tiles,
-                                                                        ts.totals, ts.local_start, ts.block_sums, ts.order_runs, ts.order_rank);
+                                                                        ts.totals, ts.local_start, ts.block_sums, ts.order_runs, ts.order_rank,
+                                                                        ts.counters);
     EFGS_HIP_CHECK(hipGetLastError());
-    tile_order_runs_kernel<<<1, 1024, 0, s>>>(ts.order_runs, div_up(n_tiles, scan_tiles));
+    tile_order_runs_kernel<<<1, 1024, 0, s>>>(ts.order_runs, div_up(n_tiles, scan_tiles), ts.counters);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
 
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
-                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t n_instances,
+                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t max_instances,
                          uint32_t n_tiles, hipStream_t s) {
-    if (n_instances == 0) return true;
-    const uint32_t blocks = div_up(n_instances, 256);
+    if (max_instances == 0) return true;
+    const uint32_t blocks = div_up(max_instances, 256);
     const uint32_t* tab = plan.use_table ? table : nullptr;
     if (key_bytes == 2)
         tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
-                                                            ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
+                                                            ts.local_start, ts.cursor, bucket, ts.counters, n_tiles);
     else
         tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
-                                                            ts.local_start, ts.cursor, bucket, n_instances, n_tiles);
+                                                            ts.local_start, ts.cursor, bucket, ts.counters, n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
@@ -677,10 +691,10 @@ bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint64_t* bucket, uint3
     if (n_tiles == 0) return true;
     const uint32_t blocks = div_up(n_tiles, tile_sort_waves);
     if (key_bytes == 2)
-        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ranges, bucket, sorted_inst,
+        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ts.counters, ranges, bucket, sorted_inst,
                                                                      static_cast<uint16_t*>(sorted_keys), n_tiles);
     else
-        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ranges, bucket, sorted_inst,
+        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ts.counters, ranges, bucket, sorted_inst,
                                                                      static_cast<uint32_t*>(sorted_keys), n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;

@@ -40,7 +40,7 @@ class Primitives(ctypes.Structure):
 class Frame(ctypes.Structure):
     _fields_ = [('primitive_buffers', ctypes.c_void_p), ('tile_buffers', ctypes.c_void_p), ('instance_buffers', ctypes.c_void_p),
                 ('n_primitives', ctypes.c_int64), ('n_visible', ctypes.c_int64), ('n_instances', ctypes.c_int64),
-                ('grid_width', ctypes.c_int32), ('grid_height', ctypes.c_int32), ('key_bytes', ctypes.c_int32), ('model', ctypes.c_int32)]
+                ('instance_capacity', ctypes.c_int64), ('grid_width', ctypes.c_int32), ('grid_height', ctypes.c_int32), ('key_bytes', ctypes.c_int32), ('model', ctypes.c_int32)]
 
 
 class Gradients(ctypes.Structure):

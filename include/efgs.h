@@ -129,13 +129,16 @@ typedef struct efgs_frame {
     int64_t n_primitives;
     int64_t n_visible;
     int64_t n_instances;
+    int64_t instance_capacity;   /* instances the instance buffers are laid out for (>= n_instances) */
     int32_t grid_width, grid_height;
     int32_t key_bytes;           /* 2 or 4: width of the tile keys */
     int32_t model;               /* variant used (0 = precomputed colours) */
 } efgs_frame;
 
 /* Renders image (device, 3 x H x W fp32, written) and fills *frame. Blocks once on `stream` to read the
- * visible-primitive and instance counts (the reference does the same, B/rasterization/src/forward.cu:82-86).
+ * visible-primitive and instance counts (the reference does the same, B/rasterization/src/forward.cu:82-86);
+ * after the first frame of a scene size the read follows the last launch (instance buffers sized from the
+ * previous count with headroom; a larger count re-runs the binning and the blend with exact buffers).
  * Replaces _C.forward, B/rasterization/src/rasterization_api.cu:16-123. */
 int efgs_forward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_settings* settings, float* image,
                  efgs_alloc_fn alloc, void* alloc_ctx, efgs_frame* frame, void* stream);

@@ -28,7 +28,7 @@ def test_struct_sizes_match_header_layout():
     p = ctypes.sizeof(ctypes.c_void_p)
     assert ctypes.sizeof(_lib.Settings) == 3 * p + 3 * 4 + 6 * 4 + 3 * 4
     assert ctypes.sizeof(_lib.Primitives) == 8 + 8 * p
-    assert ctypes.sizeof(_lib.Frame) == 3 * p + 3 * 8 + 4 * 4
+    assert ctypes.sizeof(_lib.Frame) == 3 * p + 4 * 8 + 4 * 4
     assert ctypes.sizeof(_lib.AdamGroup) == 4 * p + 8 + 8 + 4 + 4 + 7 * 8 + 3 * 8
     assert ctypes.sizeof(_lib.FrameViews) == 13 * p
 

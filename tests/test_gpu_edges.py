@@ -209,3 +209,28 @@ def test_block_count_scan_at_large_primitive_counts(n_total):
     assert small_frame.n_visible > 0
     assert (big_frame.n_visible, big_frame.n_instances) == (small_frame.n_visible, small_frame.n_instances)
     np.testing.assert_array_equal(big_img, small_img)
+
+
+def test_instance_buffers_sized_from_the_previous_frame():
+    # After a frame of a scene size the forward launches the binning and the blend into instance buffers sized
+    # from that frame's count (+12.5 % + 1024) before it reads the counters. A second scene of the same primitive
+    # count and image size with far larger Gaussians overflows them: the device skips the binning and the blend and
+    # the host re-runs them with exact buffers. A third, sparse one fits the (now large) speculative buffers.
+    from efgs.rasterization import frame_views
+    sparse, app, cam = small_case(model='sh', n=600, scale_shift=1.0)
+    dense = O.Scene(means=sparse.means, scales=sparse.scales + 2.5, rotations=sparse.rotations, opacities=sparse.opacities,
+                    base_colors=sparse.base_colors, residual_params=sparse.residual_params)
+    gw, gh = cam.grid()
+    counts = []
+    for scene in (sparse, dense, sparse, dense):
+        image, frame, bufs = _render(scene, app, cam)
+        fw = O.render(scene, app, cam)
+        assert frame.n_instances == len(fw.inst_keys)
+        assert frame.instance_capacity >= frame.n_instances
+        v = frame_views(frame)
+        np.testing.assert_array_equal(read_device(bufs, v.tile_sorted_keys, int(frame.n_instances), np.uint16), fw.inst_keys)
+        np.testing.assert_array_equal(read_device(bufs, v.tile_ranges, 2 * gw * gh, np.uint32).reshape(-1, 2), fw.ranges)
+        assert np.abs(image - fw.image).max() <= 1e-4
+        assert read_device(bufs, v.counters, 8, np.uint32)[5] == 0  # overflow flag cleared by the re-run
+        counts.append(int(frame.n_instances))
+    assert counts[1] > counts[0] + counts[0] // 8 + 1024  # the dense frame did overflow the sparse frame's buffers
