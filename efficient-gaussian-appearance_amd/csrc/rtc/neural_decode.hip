@@ -30,15 +30,34 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::NeuralD
     nn::load_weights<decode_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
     __syncthreads();
     const uint32_t n_chunks = (a.n + decode_block - 1) / decode_block;
+    // the lane's raw inputs (features, base colour, direction) of its primitive in the block's next chunk, loaded
+    // one chunk ahead so that the loads are in flight during the current chunk's MLP
+    constexpr uint32_t NB = EFGS_BASE_INPUT ? 3u : 0u;
+    float nf[nn::FEATURES + NB + 3];
+    const auto load_inputs = [&](uint32_t chunk) {
+        const uint32_t p = chunk * decode_block + threadIdx.x;
+        if (chunk < n_chunks && p < a.n) {
+#pragma unroll
+            for (uint32_t i = 0; i < nn::FEATURES; i++) nf[i] = a.features[static_cast<size_t>(p) * nn::FEATURES + i];
+#pragma unroll
+            for (uint32_t i = 0; i < NB; i++) nf[nn::FEATURES + i] = a.base[3 * static_cast<size_t>(p) + i];
+#pragma unroll
+            for (uint32_t i = 0; i < 3; i++) nf[nn::FEATURES + NB + i] = a.dirs[3 * static_cast<size_t>(p) + i];
+        }
+    };
+    load_inputs(blockIdx.x);
     for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
         const uint32_t p = chunk * decode_block + threadIdx.x;
         const bool active = p < a.n;
+        float cf[nn::FEATURES + NB + 3];
+#pragma unroll
+        for (uint32_t i = 0; i < nn::FEATURES + NB + 3; i++) cf[i] = nf[i];
+        load_inputs(chunk + gridDim.x);
         if (__ballot(active) == 0) continue;  // wave-uniform: the tail of the last chunk
         float x[nn::INP];
         if (active) {
-            const float3 d = make_float3(a.dirs[3 * p], a.dirs[3 * p + 1], a.dirs[3 * p + 2]);
-            nn::mlp_input(a.features + static_cast<size_t>(p) * nn::FEATURES, EFGS_BASE_INPUT ? a.base + 3 * static_cast<size_t>(p) : nullptr,
-                          d, a.degree, x);
+            const float3 d = make_float3(cf[nn::FEATURES + NB], cf[nn::FEATURES + NB + 1], cf[nn::FEATURES + NB + 2]);
+            nn::mlp_input(cf, EFGS_BASE_INPUT ? cf + nn::FEATURES : nullptr, d, a.degree, x);
         } else {
 #pragma unroll
             for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
