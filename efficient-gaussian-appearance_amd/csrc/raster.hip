@@ -282,7 +282,13 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     __shared__ uint32_t s_waves[4];
     if (counters[counter_overflow] != 0) return;
     const uint32_t n_instances = counters[1];
-    if (blockIdx.x * 256u >= n_instances) return;  // (block-uniform: the grid covers a bound on I)
+    const uint32_t n_chunks = (n_instances + 255u) / 256u;
+    if (blockIdx.x >= n_chunks) return;  // (block-uniform: the grid covers a bound on I)
+    // XCD-aware chunk: the hardware deals workgroups to the 8 XCDs round robin (block b on XCD b % 8); XCD x takes
+    // one contiguous run of the chunks, so the table rows of a segment (whose instances are contiguous) are
+    // fetched into one XCD's L2 instead of all eight
+    const uint32_t xcd = blockIdx.x % 8u, per = n_chunks / 8u, extra = n_chunks % 8u;
+    const uint32_t chunk = xcd * per + min(xcd, extra) + blockIdx.x / 8u;
     const uint32_t n_blocks = (n_tiles + scan_tiles - 1) / scan_tiles;
     if (n_blocks <= max_scan_blocks) {
         const uint32_t v = threadIdx.x < n_blocks ? block_sums[threadIdx.x] : 0u;
@@ -300,7 +306,7 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
         if (threadIdx.x < n_blocks) s_prefix[threadIdx.x] = off + inc - v;
         __syncthreads();
     }
-    const uint32_t e = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t e = chunk * 256u + threadIdx.x;
     if (e >= n_instances) return;
     const uint32_t t = static_cast<uint32_t>(keys[e]);
     if (t >= n_tiles) return;
