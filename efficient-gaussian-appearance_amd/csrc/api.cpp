@@ -481,6 +481,17 @@ CameraArgs camera_args(const efgs_rasterizer* r, const efgs_settings* s, int var
     c.center_y = s->center_y;
     c.near_plane = s->near_plane;
     c.far_plane = s->far_plane;
+    {
+#pragma clang fp contract(off)
+        // the operation sequence the kernels used to evaluate per primitive (IEEE fp32, so the same bits)
+        const float wf = static_cast<float>(c.width), hf = static_cast<float>(c.height);
+        const float l = -0.15f * wf - c.center_x, rr = 1.15f * wf - c.center_x;
+        const float t = -0.15f * hf - c.center_y, b = 1.15f * hf - c.center_y;
+        c.clip_left = l / c.focal_x;
+        c.clip_right = rr / c.focal_x;
+        c.clip_top = t / c.focal_y;
+        c.clip_bottom = b / c.focal_y;
+    }
     int degree = s->render_residual ? s->appearance_degree : 0;
     if (degree < 0) degree = 0;
     const int max_deg = variant == 5 ? 0 : r->max_degree;
@@ -590,7 +601,7 @@ int efgs_set_residual_mlp(efgs_rasterizer* r, int n_input_dims, int n_output_dim
     const MlpShape probe{static_cast<uint32_t>((n_input_dims + 15) / 16 * 16), static_cast<uint32_t>(n_neurons),
                          static_cast<uint32_t>(n_hidden_layers)};
     if (mlp_smem_backward(probe) > max_dynamic_lds || mlp_smem_forward(probe) > max_dynamic_lds)
-        return fail(EFGS_ERR_INVALID_ARGUMENT, "the residual mlp exceeds the 64 KiB LDS budget of the fused kernels");
+        return fail(EFGS_ERR_INVALID_ARGUMENT, "the residual mlp exceeds the 160 KiB LDS budget of the fused kernels");
     r->clear_kernels();
     r->mlp_set = true;
     r->mlp_n_in = n_input_dims;

@@ -363,30 +363,43 @@ __device__ __forceinline__ h4 identity_tile(uint32_t lane) {
 // P-tile of the block whose F-tile is f
 __device__ __forceinline__ h4 transpose_tile(h4 f, h4 eye) { return __builtin_convertvector(mfma(f, eye, f4_zero()), h4); }
 
-// the lane's input row (INP floats) to fp16 in the staging area, then the F-tiles X[pb][ib] of the wave's four
-// column blocks
-__device__ inline void stage_input_tiles(_Float16* stage, const float* x, h4 (&X)[4][INP / 16], uint32_t lane) {
-    const uint32_t r = lane & 15u, q = lane >> 4;
+// input row x (INP floats) to fp16 at row `row` of a staging area (rows of XS halves)
+__device__ __forceinline__ void stage_input_row(_Float16* rows, const float* x, uint32_t row) {
 #pragma unroll
     for (uint32_t k = 0; k < INP; k += 4)
-        *reinterpret_cast<h4*>(&stage[lane * XS + k]) =
+        *reinterpret_cast<h4*>(&rows[row * XS + k]) =
             h4{static_cast<_Float16>(x[k]), static_cast<_Float16>(x[k + 1]), static_cast<_Float16>(x[k + 2]), static_cast<_Float16>(x[k + 3])};
-    wave_sync();
+}
+
+// the F-tiles X[pb][ib] of the four column blocks of 64 staged input rows
+__device__ __forceinline__ void load_input_tiles(const _Float16* rows, h4 (&X)[4][INP / 16], uint32_t lane) {
+    const uint32_t r = lane & 15u, q = lane >> 4;
 #pragma unroll
     for (uint32_t pb = 0; pb < 4; pb++)
 #pragma unroll
-        for (uint32_t ib = 0; ib < INP / 16; ib++) X[pb][ib] = *reinterpret_cast<const h4*>(&stage[(16 * pb + r) * XS + 16 * ib + 4 * q]);
+        for (uint32_t ib = 0; ib < INP / 16; ib++) X[pb][ib] = *reinterpret_cast<const h4*>(&rows[(16 * pb + r) * XS + 16 * ib + 4 * q]);
+}
+
+// the lane's input row (INP floats) to fp16 in the staging area, then the F-tiles X[pb][ib] of the wave's four
+// column blocks
+__device__ inline void stage_input_tiles(_Float16* stage, const float* x, h4 (&X)[4][INP / 16], uint32_t lane) {
+    stage_input_row(stage, x, lane);
+    wave_sync();
+    load_input_tiles(stage, X, lane);
     wave_sync();
 }
 
-// Per-wave MLP forward: fp16 MFMA, fp32 accumulation, activations rounded to fp16 between layers. WL: the
-// weights in LDS; stage: this wave's staging area; x: the lane's input row; y: the lane's three raw outputs,
-// rounded to fp16. Column blocks of 16 primitives run one after another (the chain is per primitive).
-__device__ inline void mlp_forward(const _Float16* WL, _Float16* stage, const float* x, float* y, uint32_t lane) {
+// MLP forward of 64 staged input rows (rows of XS halves, written by this wave or, before a block barrier, by
+// any wave of the block): fp16 MFMA, fp32 accumulation, activations rounded to fp16 between layers. WL: the
+// weights in LDS. Row i's three raw outputs, rounded to fp16, then replace the rows as float4 i = (y0, y1, y2,
+// 0) (the first 1 KB of the area). Column blocks of 16 primitives run one after another (the chain is per
+// primitive, so a primitive's outputs do not depend on the other rows).
+__device__ inline void mlp_forward_rows(const _Float16* WL, _Float16* rows, uint32_t lane) {
     const uint32_t r = lane & 15u, q = lane >> 4, ro = opaque_row(lane);
     h4 X[4][INP / 16];
-    stage_input_tiles(stage, x, X, lane);
-    float* ys = reinterpret_cast<float*>(stage);
+    load_input_tiles(rows, X, lane);
+    wave_sync();  // every row read before the outputs overwrite them
+    float* ys = reinterpret_cast<float*>(rows);
 #pragma unroll
     for (uint32_t pp = 0; pp < 2; pp++) {
         h4 H[2][NT], Hn[2][NT];
@@ -423,8 +436,16 @@ __device__ inline void mlp_forward(const _Float16* WL, _Float16* stage, const fl
                     make_float4(round_half(yt[b][0]), round_half(yt[b][1]), round_half(yt[b][2]), 0.0f);
         }
     }
+}
+
+// Per-wave MLP forward of the wave's own 64 primitives: stage: this wave's staging area; x: the lane's input
+// row; y: the lane's three raw outputs, rounded to fp16.
+__device__ inline void mlp_forward(const _Float16* WL, _Float16* stage, const float* x, float* y, uint32_t lane) {
+    stage_input_row(stage, x, lane);
     wave_sync();
-    const float4 v = *reinterpret_cast<const float4*>(&ys[lane * 4]);
+    mlp_forward_rows(WL, stage, lane);
+    wave_sync();
+    const float4 v = *reinterpret_cast<const float4*>(&reinterpret_cast<const float*>(stage)[lane * 4]);
     y[0] = v.x;
     y[1] = v.y;
     y[2] = v.z;

@@ -14,6 +14,9 @@ struct CameraArgs {
     const float* cam_position;  // 3 floats
     uint32_t width, height, grid_w, grid_h;
     float focal_x, focal_y, center_x, center_y, near_plane, far_plane;
+    // limits of the projected x / z and y / z that the EWA Jacobian clamps to (1.15x the image, fixed per camera):
+    // (-0.15 width - center_x) / focal_x, (1.15 width - center_x) / focal_x, the same in y with height, in fp32
+    float clip_left, clip_right, clip_top, clip_bottom;
     uint32_t degree;            // appearance degree used for rendering (0 when the residual is off)
     uint32_t proper_aa;
     uint32_t render_base;

@@ -120,9 +120,7 @@ __device__ inline void geometry_backward(const PreprocessBackwardArgs& a, uint32
     const float c33 = S.m31 * R.m31 + S.m32 * R.m32 + S.m33 * R.m33;
     const float wf = static_cast<float>(a.cam.width), hf = static_cast<float>(a.cam.height);
     const float fx = a.cam.focal_x, fy = a.cam.focal_y, cx = a.cam.center_x, cy = a.cam.center_y;
-    const float cl = (-0.15f * wf - cx) / fx, cr = (1.15f * wf - cx) / fx;
-    const float ct = (-0.15f * hf - cy) / fy, cb = (1.15f * hf - cy) / fy;
-    const float xc = clampf(x, cl, cr), yc = clampf(y, ct, cb);
+    const float xc = clampf(x, a.cam.clip_left, a.cam.clip_right), yc = clampf(y, a.cam.clip_top, a.cam.clip_bottom);
     const float j11 = fx / depth, j13 = -j11 * xc, j22 = fy / depth, j23 = -j22 * yc;
     const float a1x = j11 * W[0] + j13 * W[8], a1y = j11 * W[1] + j13 * W[9], a1z = j11 * W[2] + j13 * W[10];
     const float a2x = j22 * W[4] + j23 * W[8], a2y = j22 * W[5] + j23 * W[9], a2z = j22 * W[6] + j23 * W[10];
@@ -175,7 +173,7 @@ __device__ inline void geometry_backward(const PreprocessBackwardArgs& a, uint32
     }
 
     float mcx = j11 * gmx, mcy = j22 * gmy, mcz = -j11 * x * gmx - j22 * y * gmy;
-    const bool vx = x >= cl && x <= cr, vy = y >= ct && y <= cb;
+    const bool vx = x >= a.cam.clip_left && x <= a.cam.clip_right, vy = y >= a.cam.clip_top && y <= a.cam.clip_bottom;
     if (vx) mcx -= j11 * dj13 / depth;
     if (vy) mcy -= j22 * dj23 / depth;
     const float fxv = 1.0f + static_cast<float>(vx), fyv = 1.0f + static_cast<float>(vy);

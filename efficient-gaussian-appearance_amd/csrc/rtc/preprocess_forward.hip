@@ -8,7 +8,8 @@
 // lane, larger footprints wave-cooperatively 64 tiles per step), activated colour, and the 48-byte record.
 // Each 256-primitive chunk also records its visible and instance counts, which a scan turns into
 // deterministic (primitive-index ordered) compaction offsets. No global atomics. The neural variant runs a
-// persistent grid (chunks strided by the grid size) so its MLP weights are staged into LDS once per block.
+// persistent grid (chunks strided by the grid size) so its MLP weights are staged into LDS once per block, and
+// evaluates the MLP only for the chunk's visible primitives, compacted into as few waves as they fill.
 //
 // Reference: B/rasterization/rtc/preprocess_forward.cu:12-278, preprocess_common.cuh:190-252.
 
@@ -31,17 +32,24 @@ __device__ inline Projected project(const PreprocessForwardArgs& a, uint32_t p, 
     r.sx0 = r.sx1 = r.sy0 = r.sy1 = 0;
     r.tiles = {0, 0, 0, 0};
     const float* W = a.cam.w2c;
-    const float mx = a.means[3 * p], my = a.means[3 * p + 1], mz = a.means[3 * p + 2];
+    // every raw input is loaded before the first cull (p is a valid index for inactive lanes too): the loads are
+    // in flight together, one memory round trip instead of one per cull and per special-cased exp
+    float mx = a.means[3 * p], my = a.means[3 * p + 1], mz = a.means[3 * p + 2];
+    float raw_opacity = a.opacities[p];
+    float ls0 = a.scales[3 * p], ls1 = a.scales[3 * p + 1], ls2 = a.scales[3 * p + 2];
+    float q0 = a.rotations[4 * p], q1 = a.rotations[4 * p + 1], q2 = a.rotations[4 * p + 2], q3 = a.rotations[4 * p + 3];
+    asm volatile("" : "+v"(mx), "+v"(my), "+v"(mz), "+v"(raw_opacity), "+v"(ls0), "+v"(ls1), "+v"(ls2), "+v"(q0), "+v"(q1), "+v"(q2),
+                 "+v"(q3));
     const float depth = W[8] * mx + W[9] * my + W[10] * mz + W[11];
     r.depth = depth;
     if (!active || depth < a.cam.near_plane || depth > a.cam.far_plane) return r;
-    float opacity = ef_sigmoid(a.opacities[p]);
+    float opacity = ef_sigmoid(raw_opacity);
     if (opacity < min_alpha) return r;
-    const float v0 = ef_expf(2.0f * a.scales[3 * p]);
-    const float v1 = ef_expf(2.0f * a.scales[3 * p + 1]);
-    const float v2 = ef_expf(2.0f * a.scales[3 * p + 2]);
+    const float v0 = ef_expf(2.0f * ls0);
+    const float v1 = ef_expf(2.0f * ls1);
+    const float v2 = ef_expf(2.0f * ls2);
     float qn;
-    const Mat3 R = quaternion_to_rotation(a.rotations[4 * p], a.rotations[4 * p + 1], a.rotations[4 * p + 2], a.rotations[4 * p + 3], qn);
+    const Mat3 R = quaternion_to_rotation(q0, q1, q2, q3, qn);
     if (qn < 1e-8f) return r;
     const Mat3 S = {R.m11 * v0, R.m12 * v1, R.m13 * v2, R.m21 * v0, R.m22 * v1, R.m23 * v2, R.m31 * v0, R.m32 * v1, R.m33 * v2};
     const float c11 = S.m11 * R.m11 + S.m12 * R.m12 + S.m13 * R.m13;
@@ -52,11 +60,8 @@ __device__ inline Projected project(const PreprocessForwardArgs& a, uint32_t p, 
     const float c33 = S.m31 * R.m31 + S.m32 * R.m32 + S.m33 * R.m33;
     const float x = (W[0] * mx + W[1] * my + W[2] * mz + W[3]) / depth;
     const float y = (W[4] * mx + W[5] * my + W[6] * mz + W[7]) / depth;
-    const float wf = static_cast<float>(a.cam.width), hf = static_cast<float>(a.cam.height);
     const float fx = a.cam.focal_x, fy = a.cam.focal_y, cx = a.cam.center_x, cy = a.cam.center_y;
-    const float cl = (-0.15f * wf - cx) / fx, cr = (1.15f * wf - cx) / fx;
-    const float ct = (-0.15f * hf - cy) / fy, cb = (1.15f * hf - cy) / fy;
-    const float xc = clampf(x, cl, cr), yc = clampf(y, ct, cb);
+    const float xc = clampf(x, a.cam.clip_left, a.cam.clip_right), yc = clampf(y, a.cam.clip_top, a.cam.clip_bottom);
     const float j11 = fx / depth, j13 = -j11 * xc, j22 = fy / depth, j23 = -j22 * yc;
     const float a1x = j11 * W[0] + j13 * W[8], a1y = j11 * W[1] + j13 * W[9], a1z = j11 * W[2] + j13 * W[10];
     const float a2x = j22 * W[4] + j23 * W[8], a2y = j22 * W[5] + j23 * W[9], a2z = j22 * W[6] + j23 * W[10];
@@ -166,10 +171,10 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
     __shared__ float s_rows[staged_forward ? preprocess_block * row_ld : 1];
 #endif
 #if EFGS_MODEL == 5
-    // residual MLP weights staged once per block (padded rows); per-wave staging area for the input tiles
+    // residual MLP weights staged once per block (padded rows); staging rows of the MLP inputs (64 per wave)
     extern __shared__ __align__(16) unsigned char smem[];
     const _Float16* WL = reinterpret_cast<const _Float16*>(smem);
-    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES) + wave * 64 * nn::XS;
+    _Float16* stage = reinterpret_cast<_Float16*>(smem + nn::WEIGHT_BYTES);
     nn::load_weights<preprocess_block>(a.mlp_weights, reinterpret_cast<uint16_t*>(smem), threadIdx.x);
     __syncthreads();
 #endif
@@ -182,6 +187,41 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
         Projected pr = project(a, p, active);
         uint32_t touched = count_touched_tiles(pr, lane);
         const bool visible = pr.visible && touched > 0;
+        if (!visible) touched = 0;
+
+        // per-chunk visible / instance counts (deterministic compaction offsets come from their scan)
+        const uint64_t visible_mask = __ballot(visible);  // (visible implies active)
+        const uint32_t wave_instances = wave_sum_u32(touched);
+        const uint32_t key = __float_as_uint(pr.depth);
+        const uint32_t wave_kmin = wave_min_u32(visible ? key : 0xffffffffu);
+        const uint32_t wave_kmax = wave_max_u32(visible ? key : 0u);
+        if (lane == 0) {
+            wave_counts[4 * wave] = static_cast<uint32_t>(__popcll(visible_mask));
+            wave_counts[4 * wave + 1] = wave_instances;
+            wave_counts[4 * wave + 2] = wave_kmin;
+            wave_counts[4 * wave + 3] = wave_kmax;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t v = 0, i = 0, kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+            for (uint32_t w = 0; w < preprocess_block / 64; w++) {
+                v += wave_counts[4 * w];
+                i += wave_counts[4 * w + 1];
+                kmin = min(kmin, wave_counts[4 * w + 2]);
+                kmax = max(kmax, wave_counts[4 * w + 3]);
+            }
+            a.block_counts[2 * chunk] = v;
+            a.block_counts[2 * chunk + 1] = i;
+            a.block_key_ranges[2 * chunk] = kmin;
+            a.block_key_ranges[2 * chunk + 1] = kmax;
+        }
+        if (active) {
+            a.n_touched[p] = touched;
+            a.depth_keys[p] = key;
+        }
+        // whether a block barrier follows the last read of wave_counts in this chunk (else one ends the chunk)
+        bool counts_released = false;
 
         float3 color = make_float3(0.0f, 0.0f, 0.0f);
 #if EFGS_MODEL == 0
@@ -194,14 +234,32 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
         const float* rp = a.residual + static_cast<size_t>(p) * residual_params;
         float3 res = make_float3(0.0f, 0.0f, 0.0f);
 #if EFGS_MODEL == 5
-        // the wave's 64 lanes run the MLP together (skipped when none of them is visible)
-        if (a.cam.degree > 0 && __ballot(visible) != 0) {
-            float x[nn::INP];
-            nn::mlp_input(rp, a.base + 3 * p, d, a.cam.degree, x);
-            float y[3];
-            nn::mlp_forward(WL, stage, x, y, lane);
-            res = make_float3(residual_activation<EFGS_RES_ACT>(y[0]), residual_activation<EFGS_RES_ACT>(y[1]),
-                              residual_activation<EFGS_RES_ACT>(y[2]));
+        // The chunk's visible primitives, compacted in thread order into the staging rows, run the MLP on as few
+        // waves as their rows fill (a wave with no row skips it): with about 70 % of a scene's primitives visible,
+        // three waves of the four instead of every wave that holds one visible primitive.
+        if (a.cam.degree > 0) {
+            uint32_t row = static_cast<uint32_t>(__popcll(visible_mask & ((1ull << lane) - 1ull))), n_rows = 0;
+#pragma unroll
+            for (uint32_t w = 0; w < preprocess_block / 64; w++) {
+                const uint32_t c = wave_counts[4 * w];
+                row += w < wave ? c : 0u;
+                n_rows += c;
+            }
+            if (visible) {
+                float x[nn::INP];
+                nn::mlp_input(rp, a.base + 3 * p, d, a.cam.degree, x);
+                nn::stage_input_row(stage, x, row);
+            }
+            __syncthreads();  // rows staged (and every read of wave_counts done)
+            counts_released = true;
+            if (64 * wave < n_rows) nn::mlp_forward_rows(WL, stage + 64 * wave * nn::XS, lane);
+            __syncthreads();  // outputs written over the rows
+            if (visible) {
+                const float* ys = reinterpret_cast<const float*>(stage + (row / 64u) * 64u * nn::XS);
+                const float4 y = *reinterpret_cast<const float4*>(&ys[(row % 64u) * 4u]);
+                res = make_float3(residual_activation<EFGS_RES_ACT>(y.x), residual_activation<EFGS_RES_ACT>(y.y),
+                                  residual_activation<EFGS_RES_ACT>(y.z));
+            }
         }
 #endif
 #if EFGS_MODEL >= 1 && EFGS_MODEL <= 4
@@ -256,46 +314,13 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
         }
 #endif
 
-        if (!visible) touched = 0;
-        if (active) {
-            a.n_touched[p] = touched;
-            a.depth_keys[p] = __float_as_uint(pr.depth);
-            if (visible) {
-                PrimRecord rec;
-                rec.r0 = make_float4(pr.mean2d_x, pr.mean2d_y, pr.conic_x, pr.conic_y);
-                rec.r1 = make_float4(pr.conic_z, pr.opacity, color.x, color.y);
-                rec.r2 = make_float4(color.z, __uint_as_float(pr.sx0 | (pr.sx1 << 16)), __uint_as_float(pr.sy0 | (pr.sy1 << 16)), 0.0f);
-                a.records[p] = rec;
-            }
+        if (visible) {
+            PrimRecord rec;
+            rec.r0 = make_float4(pr.mean2d_x, pr.mean2d_y, pr.conic_x, pr.conic_y);
+            rec.r1 = make_float4(pr.conic_z, pr.opacity, color.x, color.y);
+            rec.r2 = make_float4(color.z, __uint_as_float(pr.sx0 | (pr.sx1 << 16)), __uint_as_float(pr.sy0 | (pr.sy1 << 16)), 0.0f);
+            a.records[p] = rec;
         }
-
-        // per-chunk visible / instance counts (deterministic compaction offsets come from their scan)
-        const uint32_t wave_visible = static_cast<uint32_t>(__popcll(__ballot(visible && active)));
-        const uint32_t wave_instances = wave_sum_u32(active ? touched : 0u);
-        const uint32_t key = __float_as_uint(pr.depth);
-        const uint32_t wave_kmin = wave_min_u32(visible && active ? key : 0xffffffffu);
-        const uint32_t wave_kmax = wave_max_u32(visible && active ? key : 0u);
-        if (lane == 0) {
-            wave_counts[4 * wave] = wave_visible;
-            wave_counts[4 * wave + 1] = wave_instances;
-            wave_counts[4 * wave + 2] = wave_kmin;
-            wave_counts[4 * wave + 3] = wave_kmax;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t v = 0, i = 0, kmin = 0xffffffffu, kmax = 0u;
-#pragma unroll
-            for (uint32_t w = 0; w < preprocess_block / 64; w++) {
-                v += wave_counts[4 * w];
-                i += wave_counts[4 * w + 1];
-                kmin = min(kmin, wave_counts[4 * w + 2]);
-                kmax = max(kmax, wave_counts[4 * w + 3]);
-            }
-            a.block_counts[2 * chunk] = v;
-            a.block_counts[2 * chunk + 1] = i;
-            a.block_key_ranges[2 * chunk] = kmin;
-            a.block_key_ranges[2 * chunk + 1] = kmax;
-        }
-        __syncthreads();
+        if (!counts_released) __syncthreads();  // (block-uniform) wave_counts read before the next chunk writes it
     }
 }
