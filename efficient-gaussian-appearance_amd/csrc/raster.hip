@@ -59,8 +59,9 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
 }
 
 // Emission of one visible primitive per thread (visible index i, index order): (tile key, primitive) for every
-// tile of its tile rectangle that passes the contribution test, the first 4 tiles per lane and larger
-// footprints wave-cooperatively (64 tiles per step, positions from ballot prefix counts); emit(slot, tile) is
+// tile of its tile rectangle that passes the contribution test, the first 4 tiles per lane from the test results
+// the preprocess recorded in the primitive's record, larger footprints' further tiles tested again
+// wave-cooperatively (64 tiles per step, positions from ballot prefix counts); emit(slot, tile) is
 // called by the lane that writes each instance. Emission slots are [prim_offset, prim_offset + n_touched); a
 // count that disagrees with the preprocess is clamped to that range, the remainder padded with an out-of-range
 // key (never bucketed) and counted in counters[2]. A primitive that emitted fewer tiles than counted gets
@@ -80,12 +81,13 @@ __device__ __forceinline__ void emit_primitive(const CreateInstancesArgs& a, uin
     const uint32_t cnt = active ? bw * (t.y1 - t.y0) : 0u;
     const float smx = rec.r0.x - 0.5f, smy = rec.r0.y - 0.5f;
     const float cx = rec.r0.z, cy = rec.r0.w, cz = rec.r1.x;
-    const float pt = power_threshold_of(rec.r1.y);
+    const float pt = cnt > 4 ? power_threshold_of(rec.r1.y) : 0.0f;  // (the tile test of tiles 4 and later)
+    const uint32_t first_tiles = __float_as_uint(rec.r2.w);            // the preprocess's test of tiles 0..3
     KeyT* keys = static_cast<KeyT*>(a.keys);
     uint32_t k = 0;
     for (uint32_t j = 0; j < cnt && j < 4; j++) {
         const uint32_t tx = t.x0 + j % bw, ty = t.y0 + j / bw;
-        if (will_primitive_contribute(smx, smy, cx, cy, cz, tx, ty, pt)) {
+        if ((first_tiles >> j) & 1u) {
             if (k < n) {
                 const uint32_t tile = ty * a.grid_w + tx;
                 keys[off + k] = static_cast<KeyT>(tile);

@@ -33,7 +33,9 @@ constexpr float min_alpha = 1.0f / 255.0f;
 // per-primitive record written by the preprocess for every visible primitive (48 bytes):
 //   r0 = (mean2d.x, mean2d.y, conic.x, conic.y)
 //   r1 = (conic.z, opacity, color.r, color.g)
-//   r2 = (color.b, bits(x_min | x_max << 16), bits(y_min | y_max << 16), 0)
+//   r2 = (color.b, bits(x_min | x_max << 16), bits(y_min | y_max << 16), bits(first-tiles mask))
+// where bit j of the mask (j < 4) records whether tile j of the primitive's tile rectangle (row-major order)
+// passes the contribution test, as the preprocess counted it, so instance emission need not test those again
 struct PrimRecord {
     float4 r0, r1, r2;
 };

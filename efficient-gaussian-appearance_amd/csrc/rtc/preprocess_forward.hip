@@ -107,16 +107,20 @@ __device__ inline Projected project(const PreprocessForwardArgs& a, uint32_t p, 
     return r;
 }
 
-// exact number of tiles in the tile rectangle that the primitive reaches; every lane of the wave must call it
-__device__ inline uint32_t count_touched_tiles(const Projected& pr, uint32_t lane) {
+// exact number of tiles in the tile rectangle that the primitive reaches; first_tiles receives the test results of
+// the rectangle's first n_sequential_tiles tiles (bit i: tile i, row-major). Every lane of the wave must call it.
+__device__ inline uint32_t count_touched_tiles(const Projected& pr, uint32_t lane, uint32_t& first_tiles) {
 #pragma clang fp contract(off)
     const uint32_t bw = pr.tiles.x1 - pr.tiles.x0;
     const uint32_t cnt = pr.visible ? bw * (pr.tiles.y1 - pr.tiles.y0) : 0u;
     const float smx = pr.mean2d_x - 0.5f, smy = pr.mean2d_y - 0.5f;
     uint32_t touched = 0;
+    first_tiles = 0;
     for (uint32_t i = 0; i < cnt && i < n_sequential_tiles; i++) {
         const uint32_t tx = pr.tiles.x0 + i % bw, ty = pr.tiles.y0 + i / bw;
-        touched += will_primitive_contribute(smx, smy, pr.conic_x, pr.conic_y, pr.conic_z, tx, ty, pr.power_threshold) ? 1u : 0u;
+        const bool hit = will_primitive_contribute(smx, smy, pr.conic_x, pr.conic_y, pr.conic_z, tx, ty, pr.power_threshold);
+        touched += hit ? 1u : 0u;
+        first_tiles |= (hit ? 1u : 0u) << i;
     }
     uint64_t coop = __ballot(cnt > n_sequential_tiles);
     while (coop != 0) {
@@ -185,7 +189,8 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
         const uint32_t p = active ? p_raw : a.n - 1;
 
         Projected pr = project(a, p, active);
-        uint32_t touched = count_touched_tiles(pr, lane);
+        uint32_t first_tiles;
+        uint32_t touched = count_touched_tiles(pr, lane, first_tiles);
         const bool visible = pr.visible && touched > 0;
         if (!visible) touched = 0;
 
@@ -318,7 +323,8 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
             PrimRecord rec;
             rec.r0 = make_float4(pr.mean2d_x, pr.mean2d_y, pr.conic_x, pr.conic_y);
             rec.r1 = make_float4(pr.conic_z, pr.opacity, color.x, color.y);
-            rec.r2 = make_float4(color.z, __uint_as_float(pr.sx0 | (pr.sx1 << 16)), __uint_as_float(pr.sy0 | (pr.sy1 << 16)), 0.0f);
+            rec.r2 = make_float4(color.z, __uint_as_float(pr.sx0 | (pr.sx1 << 16)), __uint_as_float(pr.sy0 | (pr.sy1 << 16)),
+                                 __uint_as_float(first_tiles));
             a.records[p] = rec;
         }
         if (!counts_released) __syncthreads();  // (block-uniform) wave_counts read before the next chunk writes it
