@@ -153,3 +153,25 @@ def check_emission(bufs, v, frame, fw, n: int) -> None:
     kt = np.uint16 if frame.key_bytes == 2 else np.uint32
     np.testing.assert_array_equal(read_device(bufs, v.instance_keys, I, kt).astype(np.uint32), fw.inst_keys[order])
     np.testing.assert_array_equal(read_device(bufs, v.instance_primitive, I, np.uint32), fw.inst_prims[order])
+
+
+def check_first_tiles(rec: np.ndarray, fw, vis: np.ndarray, grid_w: int, grid_h: int) -> None:
+    """The record's spare word (column 11): bit j (j < 4) set exactly when tile j of the primitive's tile
+    rectangle (row-major) is one of the tiles the oracle emits for it (the preprocess's tile-test results that
+    instance emission reads instead of testing again). rec: the device records of the visible primitives."""
+    prims = np.nonzero(vis)[0]
+    b = fw.bounds[vis].astype(np.int64)
+    x0, x1 = b[:, 0] // 16, (b[:, 1] + 15) // 16
+    y0, y1 = b[:, 2] // 12, (b[:, 3] + 11) // 12
+    bw = x1 - x0
+    cnt = bw * (y1 - y0)
+    n_tiles_max = int(grid_w) * int(grid_h)
+    emitted = np.sort(fw.inst_prims.astype(np.int64) * n_tiles_max + fw.inst_keys.astype(np.int64))
+    expected = np.zeros(len(prims), np.uint32)
+    for j in range(4):
+        tile = (y0 + j // np.maximum(bw, 1)) * grid_w + x0 + j % np.maximum(bw, 1)
+        code = prims * n_tiles_max + tile
+        pos = np.minimum(np.searchsorted(emitted, code), len(emitted) - 1)
+        hit = (j < cnt) & (emitted[pos] == code) if len(emitted) else np.zeros(len(prims), bool)
+        expected |= hit.astype(np.uint32) << np.uint32(j)
+    np.testing.assert_array_equal(rec[:, 11].view(np.uint32), expected)

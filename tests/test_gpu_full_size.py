@@ -16,7 +16,7 @@ import pytest
 
 import oracle as O
 from efgs.synthetic import make_scene
-from helpers import rel_l2, configure, torch_inputs, settings, read_device, check_emission, contributor_tolerance
+from helpers import rel_l2, configure, torch_inputs, settings, read_device, check_emission, check_first_tiles, contributor_tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -101,6 +101,7 @@ def test_full_size_parity(name):
 
     # index-ordered emission, tile order and ranges
     check_emission(bufs, v, frame, fw, n)
+    check_first_tiles(rec, fw, vis, *cam.grid())
     kdt = np.uint16 if frame.key_bytes == 2 else np.uint32
     keys = read_device(bufs, v.tile_sorted_keys, I, kdt).astype(np.uint32)
     assert np.all(np.diff(keys.astype(np.int64)) >= 0), 'tile keys not sorted'

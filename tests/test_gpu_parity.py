@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from helpers import small_case, rel_l2, configure, torch_inputs, settings, read_device, check_emission, \
+from helpers import small_case, rel_l2, configure, torch_inputs, settings, read_device, check_emission, check_first_tiles, \
     contributor_tolerance
 
 pytestmark = pytest.mark.gpu
@@ -97,6 +97,7 @@ def test_forward_parity(name):
     if V > 0:
         assert counters[3] == fw.depth_key[vis].min() and counters[4] == fw.depth_key[vis].max()
     check_emission(bufs, v, frame, fw, n)
+    check_first_tiles(rec, fw, vis, *cam.grid())
     kt = np.uint16 if frame.key_bytes == 2 else np.uint32
     np.testing.assert_array_equal(read_device(bufs, v.tile_sorted_keys, I, kt).astype(np.uint32), fw.inst_keys)
     sorted_inst = read_device(bufs, v.tile_sorted_instances, I, np.uint32)
