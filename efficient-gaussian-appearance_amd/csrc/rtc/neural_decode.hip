@@ -20,7 +20,9 @@ namespace efgs {
 constexpr uint32_t decode_block = 256;
 }  // namespace efgs
 
-extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::NeuralDecodeArgs a) {
+// (at least two waves per SIMD: a budget of 256 VGPRs, within which the compiler keeps MFMA results in VGPRs
+// instead of accumulation registers that every result tile would have to be copied back from)
+extern "C" __global__ __launch_bounds__(256, 2) void EFGS_KERNEL_NAME(efgs::NeuralDecodeArgs a) {
     using namespace efgs;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
