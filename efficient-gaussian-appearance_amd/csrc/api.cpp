@@ -5,6 +5,7 @@
 // tile ranges -> blend; backward: blend replay -> preprocess backward (per-instance gradient reduction).
 #include "../../include/efgs.h"
 
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -141,10 +142,9 @@ struct efgs_rasterizer {
     int mlp_sh_mask = 0;
     int mlp_n_features = 0;
     bool mlp_base_input = false;
-    uint32_t* host_counters = nullptr;      // pinned and mapped, n_counters entries, written by the preprocess kernel
+    uint32_t* host_counters = nullptr;      // pinned and mapped, n_counters entries, written by the counter scan
     uint32_t* host_counters_dev = nullptr;  // its device address
-    hipEvent_t counters_ready = nullptr;    // recorded after the kernel that writes them, on counters_device
-    int counters_device = -1;
+    uint32_t counter_seq = 0;               // sequence number of the last frame's counters (never 0 once set)
 
     // instance count of the last forward and the scene size it was for: sizes the next frame's instance
     // buffers before its counter readback
@@ -549,7 +549,6 @@ int efgs_rasterizer_create(efgs_rasterizer** out) {
 void efgs_rasterizer_destroy(efgs_rasterizer* r) {
     if (!r) return;
     if (r->host_counters) (void)hipHostFree(r->host_counters);
-    if (r->counters_ready) (void)hipEventDestroy(r->counters_ready);
     delete r;
 }
 
@@ -624,10 +623,8 @@ int64_t efgs_mlp_param_count(const efgs_rasterizer* r) {
 
 namespace {
 
-// The host's pinned, device-mapped copy of the counters and the event that marks them written (per device).
+// The host's pinned, device-mapped copy of the counters (portable: one buffer serves every device).
 int prepare_counters(efgs_rasterizer* r) {
-    int device = 0;
-    if (const hipError_t e = hipGetDevice(&device); e != hipSuccess) return fail(EFGS_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
     if (!r->host_counters) {
         void* host = nullptr;
         void* dev = nullptr;
@@ -637,15 +634,27 @@ int prepare_counters(efgs_rasterizer* r) {
             (void)hipHostFree(host);
             return fail(EFGS_ERR_HIP, "hipHostGetDevicePointer of the counter buffer failed");
         }
+        std::memset(host, 0, n_counters * sizeof(uint32_t));
         r->host_counters = static_cast<uint32_t*>(host);
         r->host_counters_dev = static_cast<uint32_t*>(dev);
     }
-    if (r->counters_device != device) {
-        if (r->counters_ready) (void)hipEventDestroy(r->counters_ready);
-        r->counters_ready = nullptr;
-        if (hipEventCreateWithFlags(&r->counters_ready, hipEventDisableTiming) != hipSuccess) return fail(EFGS_ERR_HIP, "hipEventCreate failed");
-        r->counters_device = device;
+    return EFGS_OK;
+}
+
+// Waits until the counter scan of frame `seq` has written the host's copy of the counters: polls the sequence
+// word (the scan writes it after the counters, behind a system-scope fence), for up to 20 ms, then waits for the
+// stream to drain and looks once more, so an earlier failure on the stream is reported instead of waited on.
+int wait_counters(efgs_rasterizer* r, uint32_t seq, hipStream_t s) {
+    const uint32_t* word = &r->host_counters[counter_sequence];
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint32_t i = 0;; i++) {
+        if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == seq) return EFGS_OK;
+        if ((i & 1023u) == 1023u && std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(20)) break;
+        __builtin_ia32_pause();
     }
+    if (const hipError_t e = hipStreamSynchronize(s); e != hipSuccess)
+        return fail(EFGS_ERR_HIP, std::string("reading the visible/instance counters failed: ") + hipGetErrorString(e));
+    if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != seq) return fail(EFGS_ERR_HIP, "the counter scan did not write the counters");
     return EFGS_OK;
 }
 
@@ -686,6 +695,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     uint64_t capacity = speculate ? static_cast<uint64_t>(r->instance_hint) + r->instance_hint / 8 + 1024 : 0;
     if (capacity > 0xfffffff0ull) capacity = 0xfffffff0ull;
 
+    uint32_t seq = 0;
     if (n > 0) {
         RtcKernel k;
         if (!get_preprocess_kernel(r, variant, "forward", k)) return EFGS_ERR_RTC;
@@ -713,12 +723,11 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (!launch_rtc(k, blocks, preprocess_block, shared, &a, s)) return EFGS_ERR_HIP;
         t.end(s);
         t.begin(EFGS_STAGE_COMPACT, s);
+        // the scan writes the counters to the pinned host buffer as well, then the frame's sequence number
+        seq = ++r->counter_seq == 0 ? ++r->counter_seq : r->counter_seq;
         if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, r->host_counters_dev,
-                                      speculate ? static_cast<uint32_t>(capacity) : 0xffffffffu, chunks, s))
+                                      speculate ? static_cast<uint32_t>(capacity) : 0xffffffffu, seq, chunks, s))
             return EFGS_ERR_HIP;
-        // the scan writes the counters to the pinned host buffer as well; the event marks them written
-        if (hipEventRecord(r->counters_ready, s) != hipSuccess)
-            return fail(EFGS_ERR_HIP, std::string("recording the counter event failed: ") + hipGetErrorString(hipGetLastError()));
         if (!launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
         t.end(s);
     } else {
@@ -790,8 +799,9 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (int c = bin_and_blend(iblob, capacity, r->visible_hint, n, static_cast<uint32_t>(capacity))) return c;
     }
     t.begin(EFGS_STAGE_COUNTER_READ, s);
-    if (n > 0 && hipEventSynchronize(r->counters_ready) != hipSuccess)
-        return fail(EFGS_ERR_HIP, std::string("reading the visible/instance counters failed: ") + hipGetErrorString(hipGetLastError()));
+    if (n > 0) {
+        if (int c = wait_counters(r, seq, s)) return c;
+    }
     t.end(s);
     const uint32_t n_visible = n > 0 ? __atomic_load_n(&r->host_counters[0], __ATOMIC_ACQUIRE) : 0u;
     const uint32_t n_instances = n > 0 ? __atomic_load_n(&r->host_counters[1], __ATOMIC_ACQUIRE) : 0u;

@@ -31,11 +31,13 @@ inline uint32_t div_up(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a
 bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 // counters: [0] V, [1] I, [2] instance-emission mismatches, [3] / [4] min / max depth key of the visible set,
 // [5] 1 when I exceeds the instance capacity the binning buffers were laid out for (the binning and blend kernels
-// then return at once; the host re-runs them with buffers of the exact size)
+// then return at once; the host re-runs them with buffers of the exact size); the host's copy also holds, in
+// [counter_sequence], the sequence number of the frame whose counters it holds (written last)
 constexpr uint32_t n_counters = 8;
 constexpr uint32_t counter_overflow = 5;
+constexpr uint32_t counter_sequence = 7;
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
-                              uint32_t* host_counters, uint32_t instance_capacity, uint32_t n_blocks, hipStream_t s);
+                              uint32_t* host_counters, uint32_t instance_capacity, uint32_t seq, uint32_t n_blocks, hipStream_t s);
 // visible primitives in index order and their first emission slots (exclusive scan of the tile counts in
 // index order)
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,

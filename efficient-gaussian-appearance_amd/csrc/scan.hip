@@ -40,11 +40,12 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& t
 
 // one block: offsets of the per-preprocess-block (visible, instance) counts; counters[0] = V, counters[1] = I,
 // counters[3] / counters[4] = min / max depth key of the visible primitives, also written to the host's pinned
-// buffer (device address host_counters; the system-scope fence makes them visible to the host when the kernel
-// completes, so no device-to-host copy is needed)
+// buffer (device address host_counters), followed, after a system-scope fence, by the frame's sequence number
+// in host_counters[counter_sequence]: the host polls that word instead of waiting for an event or a copy
 constexpr uint32_t scan_regs = 8;  // chunks per thread held in registers (up to 8,192 chunks, 2M primitives)
 __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t* counts, const uint32_t* key_ranges, uint32_t* offsets,
-                                                                 uint32_t* counters, uint32_t* host_counters, uint32_t capacity, uint32_t n) {
+                                                                 uint32_t* counters, uint32_t* host_counters, uint32_t capacity, uint32_t seq,
+                                                                 uint32_t n) {
     __shared__ uint32_t s_range[2 * 16];
     const uint32_t per = (n + 1023) / 1024;
     const uint32_t base = threadIdx.x * per;
@@ -126,14 +127,16 @@ __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t*
             host_counters[k] = c[k];
         }
         __threadfence_system();
+        __hip_atomic_store(&host_counters[counter_sequence], seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        __threadfence_system();
     }
 }
 
 }  // namespace
 
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
-                              uint32_t* host_counters, uint32_t capacity, uint32_t n_blocks, hipStream_t s) {
-    scan_block_counts_kernel<<<1, 1024, 0, s>>>(block_counts, key_ranges, block_offsets, counters, host_counters, capacity, n_blocks);
+                              uint32_t* host_counters, uint32_t capacity, uint32_t seq, uint32_t n_blocks, hipStream_t s) {
+    scan_block_counts_kernel<<<1, 1024, 0, s>>>(block_counts, key_ranges, block_offsets, counters, host_counters, capacity, seq, n_blocks);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
