@@ -1,21 +1,22 @@
-// Alpha blending per 16x12 tile: 192 threads = 3 wave64, wave w owns pixel rows 4w..4w+3 (a 16x4 band),
-// one pixel per lane (lane l: x = l & 15, y = 4w + (l >> 4)). Each band is split into four 4x4 pixel groups:
-// group g = (l >> 2) & 3 holds lanes 4g..4g+3 of every 16-lane row. Gaussians of the tile are staged in LDS;
-// a 64-Gaussian chunk is culled against the four group rectangles with four 64-bit ballots, and every group
-// walks its own surviving list, in order, one Gaussian per loop step (four Gaussians per wave instruction).
-// Small Gaussians cover few pixels: a 4x4 group wastes far fewer lanes than a 16x4 band would.
+// Alpha blending per 16x12 tile.
 //
-// Forward: front-to-back compositing, alpha = o exp2(min(q, 0)) with the conic pre-scaled by -log2(e)/2 and
-// the hardware exp2 (v_exp_f32, as the reference's fast-math exp2f), alpha < 1/255 skipped, stop at
-// T < 1e-4; stores the image, final T and last-contributor index per pixel and the per-tile maximum (an
-// inference render stores only the image, in CHW or HWC layout, optionally clamped). No per-bucket checkpoints.
+// Forward (and pruning scores): 192 threads = 3 wave64, wave w owns pixel rows 4w..4w+3 (a 16x4 band), one pixel
+// per lane (lane l: x = l & 15, y = 4w + (l >> 4)). Each band is split into four 4x4 pixel groups: group
+// g = (l >> 2) & 3 holds lanes 4g..4g+3 of every 16-lane row. Gaussians of the tile are staged in LDS; a
+// 64-Gaussian chunk is culled against the four group rectangles with four 64-bit ballots, and every group walks
+// its own surviving list, in order, one Gaussian per loop step (four Gaussians per wave instruction). Small
+// Gaussians cover few pixels: a 4x4 group wastes far fewer lanes than a 16x4 band would. Front-to-back
+// compositing, alpha = o exp2(min(q, 0)) with the conic pre-scaled by -log2(e)/2 and the hardware exp2
+// (v_exp_f32, as the reference's fast-math exp2f), alpha < 1/255 skipped, stop at T < 1e-4; stores the image,
+// final T and last-contributor index per pixel and the per-tile maximum (an inference render stores only the
+// image, in CHW or HWC layout, optionally clamped). No per-bucket checkpoints.
 //
-// Backward: every pixel replays its forward walk (the evaluation below is shared and compiled with
-// -ffp-contract=off, so T and every skip decision are reproduced bit-exactly) and forms the reference's
-// per-pixel terms; the 9 per-Gaussian values (11 with the |dL/dmean2d| pair) are summed over each 16-lane
-// group with two permlane swaps and two quad DPP steps, each (wave, group) keeps its own LDS slot per
-// Gaussian, and the twelve group sums are added in a fixed order into one 48-byte record per instance at its
-// emission slot. No float atomics; the result is run-to-run deterministic.
+// Backward: one wave per tile, sixteen 4x3 pixel groups, three pixels per lane (see blend_backward_kernel). Every
+// pixel replays its forward walk (the evaluation is shared and compiled with -ffp-contract=off, so T and every
+// skip decision are reproduced bit-exactly; which pixels evaluate a Gaussian differs from the forward only where
+// its alpha is below 1/255, outside its screen rectangle) and forms the reference's per-pixel terms; the
+// per-Gaussian sums of each group are added in a fixed order into one 48-byte record per instance at its emission
+// slot. No float atomics; the result is run-to-run deterministic.
 //
 // Reference: B/rasterization/include/kernels_forward.cuh:26-166, kernels_backward.cuh:12-231.
 #include "internal.h"
@@ -196,9 +197,9 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
     if (tid == 0) a.tile_max[tile] = max(max(s_max[0], s_max[1]), s_max[2]);
 }
 
-// Sums of several per-lane values over each 4x4 pixel group at once ("transposing" reductions). A group's
-// 16 lanes are lanes 4g..4g+3 of the four 16-lane rows. Each exchange step swaps half of the values between
-// lanes so that every lane keeps fewer values, each summed over more lanes of its group:
+// Sums of several per-lane values over the four 16-lane rows (and, in the 4x4 groups of the score kernel, over
+// a row quad) at once ("transposing" reductions). Each exchange step swaps half of the values between lanes so
+// that every lane keeps fewer values, each summed over more lanes:
 //   permlane32 swap: lanes l and l + 32 exchange, a pair of registers becomes one register holding value
 //                    a in rows 0, 1 and value b in rows 2, 3 (sums over 2 rows);
 //   permlane16 swap: rows 1, 3 of the first register exchange with rows 0, 2 of the second; two such
@@ -222,44 +223,6 @@ __device__ __forceinline__ float swap16_add(float a, float b) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Eight values -> lane (r, i) of a group (row r, quad position i) holds the group sum of value
-// 4 (i >> 1) + {0, 2, 1, 3}[r].
-__device__ __forceinline__ float group_reduce8(const float* v, uint32_t lane) {
-    const float w0 = swap32_add(v[0], v[1]), w1 = swap32_add(v[2], v[3]);
-    const float w2 = swap32_add(v[4], v[5]), w3 = swap32_add(v[6], v[7]);
-    const float x0 = swap16_add(w0, w1), x1 = swap16_add(w2, w3);  // rows: v0, v2, v1, v3 / v4, v6, v5, v7
-    const bool hi = (lane & 2u) != 0;
-    float y = (hi ? x1 : x0) + dpp<0x4E, 0xf, true>(0.0f, hi ? x0 : x1);  // quad_perm [2, 3, 0, 1]
-    y += dpp<0xB1, 0xf, true>(0.0f, y);                                     // quad_perm [1, 0, 3, 2]
-    return y;
-}
-
-__device__ __forceinline__ uint32_t group_reduced8_index(uint32_t lane) {
-    const uint32_t r = lane >> 4;
-    return 4u * ((lane >> 1) & 1u) + ((r & 1u) << 1) + (r >> 1);
-}
-
-// Sixteen values -> lane (r, i) of a group holds the group sum of value 4 m + {0, 2, 1, 3}[r] with
-// m = {0, 2, 1, 3}[i]: values 0-7 on even quad positions, 8-15 on odd ones.
-__device__ __forceinline__ float group_reduce16(const float* v, uint32_t lane) {
-    float w[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) w[i] = swap32_add(v[2 * i], v[2 * i + 1]);
-    float x[4];  // rows of x[m]: v[4m], v[4m + 2], v[4m + 1], v[4m + 3]
-#pragma unroll
-    for (int m = 0; m < 4; m++) x[m] = swap16_add(w[2 * m], w[2 * m + 1]);
-    const bool h2 = (lane & 2u) != 0;  // quad positions 2, 3 keep x[1] and x[3]
-    const float y0 = (h2 ? x[1] : x[0]) + dpp<0x4E, 0xf, true>(0.0f, h2 ? x[0] : x[1]);  // quad_perm [2, 3, 0, 1]
-    const float y1 = (h2 ? x[3] : x[2]) + dpp<0x4E, 0xf, true>(0.0f, h2 ? x[2] : x[3]);
-    const bool h1 = (lane & 1u) != 0;  // odd positions keep y1
-    return (h1 ? y1 : y0) + dpp<0xB1, 0xf, true>(0.0f, h1 ? y0 : y1);                  // quad_perm [1, 0, 3, 2]
-}
-
-__device__ __forceinline__ uint32_t group_reduced16_index(uint32_t lane) {
-    const uint32_t r = lane >> 4, i = lane & 3u;
-    return 4u * (2u * (i & 1u) + (i >> 1)) + ((r & 1u) << 1) + (r >> 1);
-}
-
 // Two values -> rows 0, 1 of a group hold the group sum of a, rows 2, 3 that of b.
 __device__ __forceinline__ float group_reduce2(float a, float b) {
     float w = swap32_add(a, b);
@@ -269,252 +232,324 @@ __device__ __forceinline__ float group_reduce2(float a, float b) {
     return w;
 }
 
-// Per pixel: the nine (eleven with ABS) gradient terms of one Gaussian, zero where the pixel skips it, and the
-// pixel's transmittance and remaining-colour state advanced past it (unchanged bit for bit when skipped).
-template <bool ABS>
-__device__ __forceinline__ void pair_terms(bool contrib, float alpha, float dx, float dy, float4 col, float4 conic,
-                                           float gr, float gg, float gb, float gbg, float& T, float& A, float* v,
-                                           float& wgb, float& e1, float& e2) {
-    const float ae = contrib ? alpha : 0.0f;
-    const float w = T * ae;
-    const float oma = 1.0f - ae;
-    const float rcp = __builtin_amdgcn_rcpf(fmaxf(oma, one_minus_alpha_eps));
-    const float cg = __builtin_fmaf(col.z, gb, __builtin_fmaf(col.y, gg, col.x * gr));
-    A = __builtin_fmaf(-w, cg, A);
-    const float dalpha = __builtin_fmaf(T, cg, -rcp * (A - gbg));
-    const float h = -ae * dalpha;
-    const float hdx = h * dx, hdy = h * dy;
-    v[0] = hdx; v[1] = hdy; v[2] = hdx * dx; v[3] = hdx * dy; v[4] = hdy * dy;
-    v[5] = h; v[6] = w * gr; v[7] = w * gg;
-    wgb = w * gb;
-    if (ABS) {  // |dL/dmean2d| of the pixel: the raw conic times h d (the exp2-scaled conic divided back)
-        e1 = fabsf(__builtin_fmaf(conic.x, hdx, conic.y * hdy));
-        e2 = fabsf(__builtin_fmaf(conic.y, hdx, conic.z * hdy));
-    }
-    T = T * oma;
-}
-
 // raw conic (x, y, z) of an exp2-scaled one (scale_conic_for_exp2 inverted)
 __device__ __forceinline__ float4 raw_conic_of(float4 co) {
     constexpr float ln2 = 0.69314718055994531f;
     return make_float4(-2.0f * ln2 * co.x, -ln2 * co.y, -2.0f * ln2 * co.z, 0.0f);
 }
 
-// ABS: also reduce |dL/dmean2d| per pixel (needed only for the third densification row).
-//
-// Only alpha has to reproduce the forward bit for bit (it decides which Gaussians a pixel skips); T and the
-// gradient terms use fused multiply-adds and the hardware reciprocal. Per pixel and Gaussian the kernel
-// forms, branch-free (zero for pixels that skip the Gaussian),
-//   h = -alpha dL/dalpha,  dL/dalpha = T (c . g) - (A - g_bg) / max(1 - alpha, eps)
-// with A = (colour still to come) . g, and the group sums
-//   h dx, h dy, h dx^2, h dx dy, h dy^2, h, w g_r, w g_g, w g_b   (w = T alpha)
+// Four values summed over the four lane rows (lanes l, l + 16, l + 32, l + 48): row k of the result holds the
+// sum of value {0, 2, 1, 3}[k].
+__device__ __forceinline__ float rows_reduce4(float v0, float v1, float v2, float v3) {
+    return swap16_add(swap32_add(v0, v1), swap32_add(v2, v3));
+}
+
+// The maximum over the lane's 16-lane row, in every lane of it (four row rotations).
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x121, 0xf, 0xf, false)));  // row_ror:1
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x122, 0xf, 0xf, false)));  // row_ror:2
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x124, 0xf, 0xf, false)));  // row_ror:4
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, false)));  // row_ror:8
+    return v;
+}
+
+// The sum of one value over the four lane rows, in every row.
+__device__ __forceinline__ float rows_reduce1(float v) {
+    const float w = swap32_add(v, v);
+    return swap16_add(w, w);
+}
+
+// Backward, one wave per tile. Lane l serves column k = l >> 4 of pixel group i = l & 15, a 4x3 block of the tile
+// (columns 4 (i & 3) + 0..3, rows 3 (i >> 2) + 0..2), and that column's three pixels. Every pixel replays its forward
+// walk (alpha bit-identical, the decisions are the forward's) and forms, branch-free (zero where it skips the
+// Gaussian), h = -alpha dL/dalpha with dL/dalpha = T (c . g) - (A - g_bg) / max(1 - alpha, eps), A = (colour still
+// to come) . g, and the Gaussian's group sums
+//   h dx, h dy, h dx^2, h dx dy, h dy^2, h, w g_r, w g_g, w g_b   (w = T alpha; with ABS also |dL/dmean2d|)
 // from which the instance's record is dL/dmean2d = (C h d summed), dL/dconic = 0.5 (h d d^T summed),
-// dL/dopacity-term = sum G dL/dalpha = -(sum h) / o, dL/dcolour = sum w g.
+// dL/dopacity-term = sum G dL/dalpha = -(sum h) / o, dL/dcolour = sum w g. A lane's three pixels share dx, so it
+// accumulates h, h dy, h dy^2 and the colour terms over its rows and forms the dx terms once; the group's four
+// columns are then summed with two permlane swaps per four values (a lane row ends holding one of every four
+// sums), no selects: the three pixels per lane amortise the cross-lane work that a pixel per lane paid alone.
 //
-// Each group walks two Gaussians (a, b) of its list per step, so their first eight values share one
-// 16-value reduction and their ninth values a 2-value one; every (wave, group) stores its sums in its own
-// LDS slot per Gaussian (a group visits a Gaussian at most once per batch). Gaussians are staged BATCH at a
-// time (double-buffered, the next batch's records fetched into registers while the current one is walked):
-// one block barrier before the walk, one before the combine, which adds the twelve slots of each value in a
-// fixed order and clears them for the next batch. The groups' lists are padded to an even length with a staged
-// dummy of opacity 0 (index BATCH: its alpha is 0, it is never taken, and its sums land in the slots' spare
-// column), so the walk needs no per-entry bounds. No atomics: the result is run-to-run deterministic.
-constexpr uint32_t blend_backward_batch = 32;
+// Gaussians are staged BATCH at a time; each of a group's four lanes tests a quarter of the batch against the
+// group's rectangle and a prefix sum over the four places the hits in the group's list, in Gaussian order; each
+// group walks its own list, one Gaussian per step (sixteen different Gaussians per wave instruction), with the
+// list entries read two steps and the staged Gaussians one step ahead, and stores its sums into its slot row of each value
+// (a group visits a Gaussian at most once per batch). The combine then adds each value's sixteen slots in a fixed
+// order, writes the 48-byte record at the instance's emission slot and clears the slots. A single wave needs no
+// block barrier: LDS accesses of a wave complete in order, and a wavefront fence keeps the compiler from
+// reordering them around the list and slot exchanges. No atomics: the result is run-to-run deterministic.
+// Gaussians per batch: the slots take 16 x 9 x (BATCH + 1) floats of LDS, so the batch size trades walk steps
+// (a group's list padded to the longest of the sixteen, per batch) against waves per CU. Measured on the 1M-Gaussian
+// 1080p scene: 8 / 12 / 16 / 20 / 32 Gaussians 215 / 185 / 193 / 206 / 241 us.
+#ifndef EFGS_BACKWARD_BATCH
+#define EFGS_BACKWARD_BATCH 12
+#endif
+constexpr uint32_t blend_backward_batch = EFGS_BACKWARD_BATCH;
+constexpr uint32_t backward_groups = 16;
 
 template <bool ABS, uint32_t BATCH>
-__global__ __launch_bounds__(tile_pixels) void blend_backward_kernel(BlendBackwardArgs a) {
+__global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a) {
     constexpr uint32_t n_values = ABS ? 11u : 9u;
-    constexpr uint32_t n_waves = tile_pixels / 64;
-    constexpr uint32_t list_len = BATCH;
-    constexpr uint32_t n_slots = n_waves * 4;  // (wave, group) pairs
-    constexpr uint32_t dummy = BATCH;          // staged Gaussian of opacity 0 and slot column past the batch
-    // slots [wave][group][value][instance]; value rows BATCH + 1 floats apart
-    constexpr uint32_t value_stride = BATCH + 1;
-    constexpr uint32_t slot_stride = n_values * value_stride;
-    constexpr uint32_t n_parts = 6;  // 8-byte parts of the 48-byte record written by the combine
-    static_assert(BATCH <= 64 && BATCH % 2 == 0, "a batch is culled by one wave ballot");
-    // staged per Gaussian: (x, y, packed rect), exp2-scaled conic + opacity, colour
-    __shared__ float4 s_stage[2][BATCH + 1][3];
-    __shared__ uint32_t s_emit[2][BATCH];
-    __shared__ uint32_t s_list[n_waves][4][list_len];
-    __shared__ float s_part[n_slots * slot_stride];
+    constexpr uint32_t dummy = BATCH;                      // staged Gaussian of opacity 0 past the batch
+    constexpr uint32_t gstride = BATCH + 1;                // one (value, group) slot row, the dummy's column last
+    constexpr uint32_t vstride = backward_groups * gstride;
+    constexpr uint32_t n_part = n_values * vstride;
+    static_assert(BATCH <= 64 && BATCH % 4 == 0 && n_part % 4 == 0, "a group's four lanes cull a quarter of the batch each; slots clear as float4");
+    __shared__ float4 s_stage[BATCH + 1][3];               // (x, y, packed rect), exp2-scaled conic + opacity, colour
+    __shared__ uint32_t s_emit[BATCH];
+    __shared__ uint32_t s_list[backward_groups][BATCH + 1];  // odd row stride: the groups' entries s in distinct banks
+    __shared__ float4 s_part4[n_part / 4];                 // slots [value][group][Gaussian]
+    float* const s_part = reinterpret_cast<float*>(s_part4);
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t lane = threadIdx.x;
     const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
     const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
-    const uint32_t g = (lane >> 2) & 3u;
-    const uint32_t px = tx * tile_width + (lane & 15u);
-    const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);
-    const bool inside = px < a.width && py < a.height;
-    const float pxf = static_cast<float>(px) + 0.5f, pyf = static_cast<float>(py) + 0.5f;
-    const uint32_t bx0 = tx * tile_width;
-    const uint32_t by0 = ty * tile_height + wave * 4u;
+    const uint32_t i = lane & 15u, k = lane >> 4;
+    const uint32_t lx = 4u * (i & 3u) + k, ly0 = 3u * (i >> 2);        // tile-local column, first row
+    const uint32_t bx0 = tx * tile_width, by0 = ty * tile_height;
+    const uint32_t px = bx0 + lx;
+    const float pxf = static_cast<float>(px) + 0.5f;
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
     const uint32_t n_proc = min(n_total, a.tile_max[tile]);
-    const uint32_t* const my_list = &s_list[wave][g][0];
-    for (uint32_t k = tid; k < n_slots * slot_stride; k += tile_pixels) s_part[k] = 0.0f;
-    if (tid < 6) (&s_stage[tid / 3u][dummy][0])[tid % 3u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t q = lane; q < n_part / 4; q += 64) s_part4[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (lane < 3) s_stage[dummy][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
-    // where this lane stores after the reductions: every lane one of the 16 main values (even quad positions
-    // Gaussian a, odd ones b); a few lanes one of the extra values (value 8, with ABS also 9 and 10)
-    const uint32_t row = lane >> 4, qpos = lane & 3u;
-    const uint32_t main_b = qpos & 1u;
-    float* const slot = s_part + (wave * 4u + g) * slot_stride;
-    float* const part_main = slot + (group_reduced16_index(lane) & 7u) * value_stride;
-    bool extra_lane;
-    uint32_t extra_b, extra_k;
-    if (ABS) {  // group_reduce8 of (wgb, e1, e2) of a then b: value u = 4 (i >> 1) + {0, 2, 1, 3}[r]
-        const uint32_t u = group_reduced8_index(lane);
-        extra_lane = (qpos & 1u) == 0 && u < 6u;
-        extra_b = u >= 3u ? 1u : 0u;
-        extra_k = 8u + (u >= 3u ? u - 3u : u);
-    } else {    // group_reduce2: rows 0, 1 hold a, rows 2, 3 hold b
-        extra_lane = qpos == 0 && (row == 0 || row == 2);
-        extra_b = row == 2 ? 1u : 0u;
-        extra_k = 8u;
-    }
-    float* const part_extra = slot + extra_k * value_stride;
-
-    // pixel state: upstream gradient, (colour still to come) . g, background term
-    float gr = 0.0f, gg = 0.0f, gb = 0.0f, A = 0.0f, gbg = 0.0f;
-    uint32_t last = 0;
-    if (inside) {
-        const uint32_t pix = py * a.width + px;
+    // pixel state of the lane's three rows: upstream gradient, (colour still to come) . g, background term. The
+    // loads are unconditional (clamped to the image) so that all of them are in flight together.
+    float pyf[3], T[3], A[3], gr[3], gg[3], gb[3], gbg[3];
+    uint32_t last[3];
+    {
         const uint32_t np = a.width * a.height;
-        const uint32_t pslot = tile * tile_pixels + tid;
-        const float Tf = a.final_T[pslot];
-        last = a.n_contrib[pslot];
-        gr = a.grad_image[pix]; gg = a.grad_image[np + pix]; gb = a.grad_image[2 * np + pix];
-        const float ar = a.image[pix] - Tf * a.bg[0];
-        const float ag = a.image[np + pix] - Tf * a.bg[1];
-        const float ab = a.image[2 * np + pix] - Tf * a.bg[2];
-        A = __builtin_fmaf(ab, gb, __builtin_fmaf(ag, gg, ar * gr));
-        gbg = Tf * -(gr * a.bg[0] + gg * a.bg[1] + gb * a.bg[2]);
-    }
-    const uint32_t wave_last = wave_max_u32(last);  // no pixel of the band uses instances at or after this
-    float T = 1.0f;
-
-    // staging threads (the first BATCH threads) fetch the record of their instance one batch ahead
-    uint32_t e_next = 0;
-    PrimRecord rec_next{};
-    const auto fetch = [&](uint32_t s) {
-        if (tid < BATCH && s + tid < n_total) {
-            e_next = a.sorted_inst[range.x + s + tid];
-            rec_next = a.records[a.inst_prim[e_next]];
-        }
-    };
-    const auto stage = [&](uint32_t s, uint32_t buf) {
-        if (tid < BATCH && s + tid < n_total) {
-            const PrimRecord& rec = rec_next;
-            float4* st = s_stage[buf][tid];
-            const float4 co = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
-            st[0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
-            st[1] = co;
-            st[2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
-            s_emit[buf][tid] = e_next;
-        }
-    };
-    if (n_proc > 0) {
-        fetch(0);
-        stage(0, 0);
-        fetch(BATCH);
-    }
-
-    uint32_t covered = 0;
-    uint32_t buf = 0;
-    for (uint32_t start = 0; start < n_proc; start += BATCH, buf ^= 1u) {
-        __syncthreads();  // batch staged; the previous combine has read and cleared the slots
-        const uint32_t batch_wave = wave_last > start ? min(min(BATCH, n_proc - start), wave_last - start) : 0u;
-        const float4(*const stg)[3] = s_stage[buf];
-        uint64_t m[4];
-        cull_groups(rect_of(stg[lane < BATCH ? lane : dummy][0]), lane < batch_wave, bx0, by0, by0 + 4u, m);
-        uint32_t n[4];
-        build_group_lists(m, lane, 0u, &s_list[wave][0][0], list_len, n);
-        const uint32_t n_max = __builtin_amdgcn_readfirstlane(max(max(n[0], n[1]), max(n[2], n[3])));
-        const uint32_t n_steps = (n_max + 1u) & ~1u;
-        // pad every list to the even step count with the dummy
+        const uint32_t pxc = min(px, a.width - 1u);
+        float Tf[3], im[3][3];
+        uint32_t nc[3];
+        bool inside[3];
 #pragma unroll
-        for (uint32_t k = 0; k < 4; k++)
-            if (lane >= n[k] && lane < n_steps) s_list[wave][k][lane] = dummy;
-        wave_lds_fence();
-        const uint32_t last_rel = last > start ? last - start : 0u;  // Gaussians j < last_rel are before `last`
-        for (uint32_t k = 0; k < n_steps; k += 2) {
-            const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);
-            const uint32_t ja = jab.x, jb = jab.y;
-            // staged float4 c of instance j, addressed in the LDS address space (32-bit offsets, 24-bit product)
-            const auto at = [stg](uint32_t j, uint32_t c) {
-                lds_char* base = (lds_char*)(stg);
-                const native_float4 v = *reinterpret_cast<lds_float4*>(base + __umul24(j, static_cast<uint32_t>(sizeof(stg[0]))) + 16u * c);
+        for (uint32_t r = 0; r < 3; r++) {
+            const uint32_t py = by0 + ly0 + r;
+            pyf[r] = static_cast<float>(py) + 0.5f;
+            inside[r] = px < a.width && py < a.height;
+            const uint32_t pix = min(py, a.height - 1u) * a.width + pxc;
+            const uint32_t pslot = tile * tile_pixels + (ly0 + r) * tile_width + lx;
+            Tf[r] = a.final_T[pslot];
+            nc[r] = a.n_contrib[pslot];
+            gr[r] = a.grad_image[pix]; gg[r] = a.grad_image[np + pix]; gb[r] = a.grad_image[2 * np + pix];
+            im[r][0] = a.image[pix]; im[r][1] = a.image[np + pix]; im[r][2] = a.image[2 * np + pix];
+        }
+        const float bg0 = a.bg[0], bg1 = a.bg[1], bg2 = a.bg[2];
+#pragma unroll
+        for (uint32_t r = 0; r < 3; r++) {
+            T[r] = 1.0f;
+            last[r] = inside[r] ? nc[r] : 0u;
+            gr[r] = inside[r] ? gr[r] : 0.0f;
+            gg[r] = inside[r] ? gg[r] : 0.0f;
+            gb[r] = inside[r] ? gb[r] : 0.0f;
+            const float ar = im[r][0] - Tf[r] * bg0;
+            const float ag = im[r][1] - Tf[r] * bg1;
+            const float ab = im[r][2] - Tf[r] * bg2;
+            A[r] = inside[r] ? __builtin_fmaf(ab, gb[r], __builtin_fmaf(ag, gg[r], ar * gr[r])) : 0.0f;
+            gbg[r] = inside[r] ? Tf[r] * -(gr[r] * bg0 + gg[r] * bg1 + gb[r] * bg2) : 0.0f;
+        }
+    }
+
+    // where the lane stores its sums: value 4m + {0, 2, 1, 3}[k] of group i (m = 0..2, values past n_values none)
+    const uint32_t vk = (k & 1u) * 2u + (k >> 1);
+    float* const slot0 = s_part + vk * vstride + i * gstride;
+
+    // The records of a batch's instances are gathered through a three-stage pipeline over the batches: while
+    // batch b is walked, the emission indices of batch b + 3, the primitive indices of batch b + 2 and the records
+    // of batch b + 1 are loaded, so no load is waited on in the batch that issues it. The loads are unconditional
+    // (indices clamped to the tile's last instance; lanes past BATCH repeat lane BATCH - 1), so the compiler places
+    // each wait at the value's use.
+    const uint32_t gather_lane = min(lane, BATCH - 1u);
+    const uint32_t last_inst = n_total > 0 ? n_total - 1u : 0u;
+    const auto load_e = [&](uint32_t s) { return a.sorted_inst[range.x + min(s + gather_lane, last_inst)]; };
+    const auto stage = [&](uint32_t s, const PrimRecord& rec, uint32_t e) {
+        if (lane < BATCH && s + lane < n_total) {
+            s_stage[lane][0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
+            s_stage[lane][1] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
+            s_stage[lane][2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
+            s_emit[lane] = e;
+        }
+    };
+    // The loads of a batch's top have their consumers a whole batch later (the staging at the end of the batch,
+    // the next batch's top), and no loaded value is copied between loop-carried registers (a copy would make the
+    // loop wait for the load).
+    uint32_t p_next = 0, e_next2 = 0;  // primitive indices of batch b + 1, emission indices of batch b + 2
+    if (n_proc > 0) {
+        const uint32_t e0 = load_e(0), e1 = load_e(BATCH);
+        e_next2 = load_e(2 * BATCH);
+        const uint32_t p0 = a.inst_prim[e0];
+        p_next = a.inst_prim[e1];
+        const PrimRecord rec0 = a.records[p0];
+        stage(0, rec0, e0);
+    }
+    const uint32_t gx0 = bx0 + 4u * (i & 3u), gy0 = by0 + ly0;  // the lane's group rectangle: 4 x 3 pixels
+    uint32_t covered = 0;
+    for (uint32_t start = 0; start < n_proc; start += BATCH) {
+        // advance the gather pipeline: records and emission indices of batch b + 1, primitive indices of b + 2,
+        // emission indices of b + 3
+        const PrimRecord rec_n = a.records[p_next];
+        const uint32_t e_n = load_e(start + BATCH);
+        p_next = a.inst_prim[e_next2];
+        e_next2 = load_e(start + 3 * BATCH);
+        wave_lds_fence();  // the batch is staged
+        const uint32_t batch_n = min(BATCH, n_proc - start);
+        // cull: the four lanes of a group test a quarter of the batch each (lane row k: Gaussians kQ .. kQ + Q - 1)
+        // against the group's rectangle; a prefix sum over the four rows places every hit in the group's list, in
+        // Gaussian order
+        {
+            constexpr uint32_t Q = BATCH / 4;
+            uint32_t hits = 0;
+#pragma unroll
+            for (uint32_t t = 0; t < Q; t++) {
+                const uint32_t j = k * Q + t;
+                const uint2 rect = rect_of(s_stage[j][0]);
+                const uint32_t rx0 = rect.x & 0xffffu, rx1 = rect.x >> 16, ry0 = rect.y & 0xffffu, ry1 = rect.y >> 16;
+                const bool hit = j < batch_n && rx0 < gx0 + 4u && gx0 < rx1 && ry0 < gy0 + 3u && gy0 < ry1;
+                hits |= hit ? 1u << t : 0u;
+            }
+            const uint32_t c = static_cast<uint32_t>(__popc(hits));
+            // inclusive prefix of c over the group's rows (lanes i, i + 16, i + 32, i + 48); every lane runs the
+            // permutes (a lane reading from a lane that does not take part gets nothing), the rows select after
+            const uint32_t up16 = static_cast<uint32_t>(__shfl_up(static_cast<int>(c), 16));
+            uint32_t incl = c + (k >= 1 ? up16 : 0u);
+            const uint32_t up32 = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), 32));
+            incl += k >= 2 ? up32 : 0u;
+            const uint32_t my_n = static_cast<uint32_t>(__shfl(static_cast<int>(incl), static_cast<int>(i + 48u)));
+            uint32_t pos = incl - c;
+#pragma unroll
+            for (uint32_t t = 0; t < Q; t++) {
+                if ((hits >> t) & 1u) s_list[i][pos] = k * Q + t;
+                pos += (hits >> t) & 1u;
+            }
+            wave_lds_fence();
+            const uint32_t n_steps = __builtin_amdgcn_readfirstlane(row_max_u32(my_n));  // rows hold the same counts
+            uint32_t last_rel[3];
+#pragma unroll
+            for (uint32_t r = 0; r < 3; r++) last_rel[r] = last[r] > start ? last[r] - start : 0u;
+
+            // step s walks entry s of the group's list (the dummy past its count); the next step's Gaussian is
+            // read from LDS before the current one is evaluated (two register sets, the loop unrolled by two)
+            const uint32_t* const my_list = s_list[i];
+            const auto entry = [&](uint32_t s) {
+                const uint32_t e = my_list[s < BATCH ? s : BATCH - 1];  // past the count: stale, replaced by the dummy
+                return s < my_n ? e : dummy;
+            };
+            // staged float4 c of Gaussian j, addressed in the LDS address space (32-bit offsets, 24-bit product)
+            const auto at = [&](uint32_t j, uint32_t c) {
+                lds_char* base = (lds_char*)(&s_stage[0][0]);
+                const native_float4 v = *reinterpret_cast<lds_float4*>(base + __umul24(j, static_cast<uint32_t>(sizeof(s_stage[0]))) + 16u * c);
                 return make_float4(v.x, v.y, v.z, v.w);
             };
-            float dxa, dya, Ga, dxb, dyb, Gb;
-            const float alpha_a = eval_alpha(at(ja, 0), at(ja, 1), pxf, pyf, dxa, dya, Ga);
-            const float alpha_b = eval_alpha(at(jb, 0), at(jb, 1), pxf, pyf, dxb, dyb, Gb);
-            const bool ca = ja < last_rel && alpha_a >= min_alpha;
-            const bool cb = jb < last_rel && alpha_b >= min_alpha;
-            float v[16], wgb_a, wgb_b, e1a = 0.0f, e2a = 0.0f, e1b = 0.0f, e2b = 0.0f;
-            const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            pair_terms<ABS>(ca, alpha_a, dxa, dya, at(ja, 2), ABS ? raw_conic_of(at(ja, 1)) : zero4, gr, gg, gb, gbg, T, A, v, wgb_a, e1a, e2a);
-            pair_terms<ABS>(cb, alpha_b, dxb, dyb, at(jb, 2), ABS ? raw_conic_of(at(jb, 1)) : zero4, gr, gg, gb, gbg, T, A, v + 8, wgb_b, e1b, e2b);
-            part_main[main_b ? jb : ja] = group_reduce16(v, lane);
-            float sx;
-            if (ABS) {
-                const float u[8] = {wgb_a, e1a, e2a, wgb_b, e1b, e2b, 0.0f, 0.0f};
-                sx = group_reduce8(u, lane);
-            } else {
-                sx = group_reduce2(wgb_a, wgb_b);
-            }
-            if (extra_lane) part_extra[extra_b ? jb : ja] = sx;
-        }
-        wave_lds_fence();
-        __syncthreads();  // every group's sums are in its slots
-        // combine: item (part p, instance j) adds the twelve slots of its two values in a fixed order, clears
-        // them, and writes its 8 bytes of the 48-byte record
-        const uint32_t batch_n = min(BATCH, n_total - start);
-        for (uint32_t item = tid; item < n_parts * BATCH; item += tile_pixels) {
-            const uint32_t j = item % BATCH, p = item / BATCH;  // p = 0..5: values 2p, 2p + 1
-            if (j >= batch_n) continue;
-            float r[2] = {0.0f, 0.0f};
+            const auto walk = [&](uint32_t j, float4 xy, float4 co, float4 col) {
+                float dx, sh, shdy, shdyy, swr, swg, swb, e1 = 0.0f, e2 = 0.0f;
+                const float4 craw = ABS ? raw_conic_of(co) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (uint32_t c = 0; c < 2; c++) {
-                const uint32_t k = 2u * p + c;
-                if (k < n_values) {
-                    float* src = s_part + k * value_stride + j;
-                    float acc = 0.0f;
-#pragma unroll
-                    for (uint32_t q = 0; q < n_slots; q++) {
-                        acc += src[q * slot_stride];
-                        src[q * slot_stride] = 0.0f;
+                for (uint32_t r = 0; r < 3; r++) {
+                    float dy, G;
+                    const float alpha = eval_alpha(xy, co, pxf, pyf[r], dx, dy, G);
+                    const bool contrib = j < last_rel[r] && alpha >= min_alpha;
+                    const float ae = contrib ? alpha : 0.0f;
+                    const float w = T[r] * ae;
+                    const float oma = 1.0f - ae;
+                    const float rcp = __builtin_amdgcn_rcpf(fmaxf(oma, one_minus_alpha_eps));
+                    const float cg = __builtin_fmaf(col.z, gb[r], __builtin_fmaf(col.y, gg[r], col.x * gr[r]));
+                    A[r] = __builtin_fmaf(-w, cg, A[r]);
+                    const float dalpha = __builtin_fmaf(T[r], cg, -rcp * (A[r] - gbg[r]));
+                    const float h = -ae * dalpha;
+                    const float hdy = h * dy;
+                    if (r == 0) {
+                        sh = h;
+                        shdy = hdy;
+                        shdyy = hdy * dy;
+                        swr = w * gr[r];
+                        swg = w * gg[r];
+                        swb = w * gb[r];
+                    } else {
+                        sh += h;
+                        shdy += hdy;
+                        shdyy = __builtin_fmaf(hdy, dy, shdyy);
+                        swr = __builtin_fmaf(w, gr[r], swr);
+                        swg = __builtin_fmaf(w, gg[r], swg);
+                        swb = __builtin_fmaf(w, gb[r], swb);
                     }
-                    r[c] = acc;
+                    if (ABS) {  // |dL/dmean2d| of the pixel: the raw conic times h d
+                        const float hdx = h * dx;
+                        e1 += fabsf(__builtin_fmaf(craw.x, hdx, craw.y * hdy));
+                        e2 += fabsf(__builtin_fmaf(craw.y, hdx, craw.z * hdy));
+                    }
+                    T[r] = T[r] * oma;
                 }
+                const float shdx = dx * sh;
+                slot0[j] = rows_reduce4(shdx, shdy, dx * shdx, dx * shdy);       // h dx, h dy, h dx^2, h dx dy
+                slot0[4u * vstride + j] = rows_reduce4(shdyy, sh, swr, swg);      // h dy^2, h, w g_r, w g_g
+                if (ABS) {
+                    const float x2 = rows_reduce4(swb, e1, e2, 0.0f);             // w g_b, |.|_x, |.|_y
+                    if (vk < 3u) slot0[8u * vstride + j] = x2;
+                } else {
+                    const float x2 = rows_reduce1(swb);                           // w g_b
+                    if (k == 0u) slot0[8u * vstride + j] = x2;
+                }
+            };
+            // list entries are read two steps ahead, the staged Gaussians one step ahead
+            uint32_t ja = entry(0), jb = entry(1);
+            float4 xya = at(ja, 0), coa = at(ja, 1), cola = at(ja, 2);
+            for (uint32_t s = 0; s < n_steps; s += 2) {
+                const float4 xyb = at(jb, 0), cob = at(jb, 1), colb = at(jb, 2);
+                const uint32_t jc = entry(s + 2);
+                walk(ja, xya, coa, cola);
+                if (s + 1 >= n_steps) break;
+                xya = at(jc, 0);
+                coa = at(jc, 1);
+                cola = at(jc, 2);
+                const uint32_t jd = entry(s + 3);
+                walk(jb, xyb, cob, colb);
+                ja = jc;
+                jb = jd;
             }
-            float2* out = reinterpret_cast<float2*>(a.inst_grads) + 6 * static_cast<size_t>(s_emit[buf][j]) + p;
-            float2 o;
-            if (p == 0) {
-                const float4 craw = raw_conic_of(s_stage[buf][j][1]);
-                o = make_float2(__builtin_fmaf(craw.x, r[0], craw.y * r[1]), __builtin_fmaf(craw.y, r[0], craw.z * r[1]));
-            } else if (p == 1) {
-                o = make_float2(0.5f * r[0], 0.5f * r[1]);
-            } else if (p == 2) {
-                o = make_float2(0.5f * r[0], -r[1] / s_stage[buf][j][1].w);   // sum of G dL/dalpha = -(sum of h) / o
-            } else {
-                o = make_float2(r[0], r[1]);  // zero past the last value
+        }
+        wave_lds_fence();  // every group's sums are in its slots
+        // combine: item (Gaussian j, quarter q) adds the sixteen group slots of values 4q .. 4q + 3 in group order
+        // and writes 16 bytes of the instance's 48-byte record (q = 3 has nothing to do). Every staged instance
+        // gets its record: those after the tile's last contributor, which no group walked, get zeros.
+        const uint32_t batch_staged = min(BATCH, n_total - start);
+        for (uint32_t item = lane; item < 4u * BATCH; item += 64) {
+            const uint32_t jj = item % BATCH, q = item / BATCH;
+            if (jj >= batch_staged || q == 3u) continue;
+            float r[4];
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                const uint32_t v = min(4u * q + c, n_values - 1u);
+                const float* src = s_part + v * vstride + jj;
+                float acc = 0.0f;
+#pragma unroll
+                for (uint32_t g = 0; g < backward_groups; g++) acc += src[g * gstride];
+                r[c] = 4u * q + c < n_values ? acc : 0.0f;
             }
-            *out = o;
+            const float4 co = s_stage[jj][1];
+            const float4 craw = raw_conic_of(co);
+            // q = 0: dL/dmean2d = C (sum h d), 0.5 (sum h dx^2, sum h dx dy); q = 1: 0.5 sum h dy^2, sum G dL/dalpha =
+            // -(sum of h) / o, colour r, g; q = 2: colour b, |dL/dmean2d| (x, y), 0
+            float4 o;
+            if (q == 0u)
+                o = make_float4(__builtin_fmaf(craw.x, r[0], craw.y * r[1]), __builtin_fmaf(craw.y, r[0], craw.z * r[1]), 0.5f * r[2], 0.5f * r[3]);
+            else if (q == 1u)
+                o = make_float4(0.5f * r[0], -r[1] / co.w, r[2], r[3]);
+            else
+                o = make_float4(r[0], r[1], r[2], r[3]);
+            reinterpret_cast<float4*>(a.inst_grads)[3 * static_cast<size_t>(s_emit[jj]) + q] = o;
         }
         covered = min(n_total, start + BATCH);
-        // stage the next batch into the other buffer (its last readers finished before this batch's first
-        // barrier) and fetch the one after it
-        if (start + BATCH < n_proc) {
-            stage(start + BATCH, buf ^ 1u);
-            fetch(start + 2 * BATCH);
-        }
+        wave_lds_fence();  // the combine has read the slots and the stage
+        for (uint32_t q = lane; q < n_part / 4; q += 64) s_part4[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (start + BATCH < n_proc) stage(start + BATCH, rec_n, e_n);  // the next batch
     }
     // instances the tile never reached (after every pixel's last contributor) get zero records
-    for (uint32_t k = covered + tid; k < n_total; k += tile_pixels) {
-        const uint32_t e = a.sorted_inst[range.x + k];
+    for (uint32_t q = covered + lane; q < n_total; q += 64) {
+        const uint32_t e = a.sorted_inst[range.x + q];
         float4* out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(e);
         const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         out[0] = z;
@@ -676,9 +711,9 @@ bool launch_pruning_scores(const BlendBackwardArgs& a, const uint32_t* n_touched
 bool launch_blend_backward(const BlendBackwardArgs& a, hipStream_t s) {
     if (a.n_tiles == 0) return true;
     if (a.abs_grads)
-        blend_backward_kernel<true, blend_backward_batch><<<a.n_tiles, tile_pixels, 0, s>>>(a);
+        blend_backward_kernel<true, blend_backward_batch><<<a.n_tiles, 64, 0, s>>>(a);
     else
-        blend_backward_kernel<false, blend_backward_batch><<<a.n_tiles, tile_pixels, 0, s>>>(a);
+        blend_backward_kernel<false, blend_backward_batch><<<a.n_tiles, 64, 0, s>>>(a);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
