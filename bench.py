@@ -47,7 +47,7 @@ STAGE_KERNELS = {
     'preprocess_forward': 'preprocess_forward_<model>',
     'compact': 'scan_block_counts_kernel + compact_visible_kernel',
     'create_instances': 'create_instances_hist_kernel',
-    'tile_offsets': 'tile_column_scan_kernel',
+    'tile_offsets': 'tile_column_scan_kernel',  # (the tile order's runs are placed by an extra block of tile_buckets_kernel)
     'tile_buckets': 'tile_buckets_kernel',
     'tile_sort': 'tile_sort_kernel',
     'blend_forward': 'blend_forward_kernel',

@@ -7,9 +7,11 @@
 //   create_instances    one thread per visible primitive (index order): the tile test of the preprocess,
 //                       (tile key, primitive) at the emission slots; blocks of contiguous primitives count
 //                       their instances per tile in an LDS histogram (ranks from the atomics' return values);
-//   tile_column_scan    the segments' counts per tile -> prefixes over the segments, tile totals and starts;
-//   tile_buckets        every instance writes its sort key at tile start + earlier segments' count + rank;
-//   tile_sort           one block per tile sorts its slots by (depth key, emission index) in LDS: keys are
+//   tile_column_scan    the segments' counts per tile -> prefixes over the segments, tile totals and starts,
+//                       and each tile's size class for the blends' heaviest-first tile order;
+//   tile_buckets        every instance writes its sort key at tile start + earlier segments' count + rank; one
+//                       extra block turns the size-class counts into the tile order's run positions meanwhile;
+//   tile_sort           one wave per tile sorts its slots by (depth key, emission index): keys are
 //                       unique, so the order is a deterministic function of the inputs (the emission index
 //                       increases with the primitive index, so ties in depth keep primitive-index order).
 // Compiled with -ffp-contract=off: instance emission re-evaluates the tile test of the preprocess and must
@@ -270,6 +272,59 @@ __device__ __forceinline__ uint32_t scan_block_prefix_wave(const uint32_t* block
     return s;
 }
 
+// One block: order_runs[b][c] (tiles of class c in 64-tile block b) becomes the first position of that run in
+// the tile order: the tiles of the classes before c, then those of class c in the blocks before b. Lane c of every
+// wave handles class c (a block's 64 counts are one coalesced row); wave w the w-th part of the blocks, whose
+// rows it holds in registers (16 at a time), so each row is read once and written once.
+template <uint32_t N_WAVES>
+__device__ inline void order_runs_block(uint32_t* order_runs, uint32_t n_blocks, uint32_t (*s_part)[order_classes]) {
+    constexpr uint32_t rows = 16;  // rows per lane in registers per pass
+    const uint32_t c = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t per = (n_blocks + N_WAVES - 1) / N_WAVES;
+    const uint32_t b0 = min(wave * per, n_blocks), b1 = min(b0 + per, n_blocks);
+    uint32_t sum = 0;
+    for (uint32_t r0 = b0; r0 < b1; r0 += rows) {
+        uint32_t v[rows];
+#pragma unroll
+        for (uint32_t k = 0; k < rows; k++) v[k] = r0 + k < b1 ? order_runs[static_cast<size_t>(r0 + k) * order_classes + c] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < rows; k++) sum += v[k];
+    }
+    s_part[wave][c] = sum;
+    __syncthreads();
+    uint32_t total = 0, before = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < N_WAVES; w++) {
+        const uint32_t x = s_part[w][c];
+        total += x;
+        before += w < wave ? x : 0u;
+    }
+    uint32_t inc = total;  // classes in lane order: prefix over the lanes
+#pragma unroll
+    for (uint32_t o = 1; o < 64; o <<= 1) {
+        const uint32_t x = static_cast<uint32_t>(__shfl_up(static_cast<int>(inc), o));
+        if (c >= o) inc += x;
+    }
+    uint32_t running = inc - total + before;
+    for (uint32_t r0 = b0; r0 < b1; r0 += rows) {
+        uint32_t v[rows];
+#pragma unroll
+        for (uint32_t k = 0; k < rows; k++) v[k] = r0 + k < b1 ? order_runs[static_cast<size_t>(r0 + k) * order_classes + c] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < rows; k++) {
+            if (r0 + k < b1) order_runs[static_cast<size_t>(r0 + k) * order_classes + c] = running;
+            running += v[k];
+        }
+    }
+}
+
+// the tile order's run positions alone (frames without instances: no bucket pass to carry them)
+__global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_runs, uint32_t n_blocks, const uint32_t* counters) {
+    if (counters[counter_overflow] != 0) return;
+    __shared__ uint32_t s_part[1024 / 64][order_classes];
+    order_runs_block<1024 / 64>(order_runs, n_blocks, s_part);
+}
+
 // Every emitted instance goes to a slot of its tile's range: start of the tile + the tile's count in the
 // earlier segments + its rank within its segment (with a table: the scanned table entry holds the tile's start
 // within its 64-tile block plus that count), or + the next slot of an atomic cursor (without one). The slot receives the instance's sort key, the depth key of its primitive above its emission
@@ -279,18 +334,24 @@ template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
                                                           const uint32_t* table, const uint32_t* local_rank, const uint32_t* block_sums,
                                                           const uint32_t* local_start, uint32_t* cursor, uint64_t* bucket, const uint32_t* counters,
-                                                          uint32_t n_tiles) {
+                                                          uint32_t n_tiles, uint32_t* order_runs, uint32_t order_blocks) {
     __shared__ uint32_t s_prefix[max_scan_blocks];
     __shared__ uint32_t s_waves[4];
+    __shared__ uint32_t s_order[4][order_classes];
     if (counters[counter_overflow] != 0) return;
+    if (blockIdx.x == 0) {  // the first block (dispatched first): the tile order's run positions, beside the buckets
+        order_runs_block<4>(order_runs, order_blocks, s_order);
+        return;
+    }
+    const uint32_t block = blockIdx.x - 1u;
     const uint32_t n_instances = counters[1];
     const uint32_t n_chunks = (n_instances + 255u) / 256u;
-    if (blockIdx.x >= n_chunks) return;  // (block-uniform: the grid covers a bound on I)
-    // XCD-aware chunk: the hardware deals workgroups to the 8 XCDs round robin (block b on XCD b % 8); XCD x takes
-    // one contiguous run of the chunks, so the table rows of a segment (whose instances are contiguous) are
-    // fetched into one XCD's L2 instead of all eight
-    const uint32_t xcd = blockIdx.x % 8u, per = n_chunks / 8u, extra = n_chunks % 8u;
-    const uint32_t chunk = xcd * per + min(xcd, extra) + blockIdx.x / 8u;
+    if (block >= n_chunks) return;  // (block-uniform: the grid covers a bound on I)
+    // XCD-aware chunk: the hardware deals workgroups to the 8 XCDs round robin (workgroup w on XCD w % 8, so bucket
+    // block b on XCD (b + 1) % 8); the blocks of one XCD take one contiguous run of the chunks, so the table rows of
+    // a segment (whose instances are contiguous) are fetched into one XCD's L2 instead of all eight
+    const uint32_t xcd = block % 8u, per = n_chunks / 8u, extra = n_chunks % 8u;
+    const uint32_t chunk = xcd * per + min(xcd, extra) + block / 8u;
     const uint32_t n_blocks = (n_tiles + scan_tiles - 1) / scan_tiles;
     if (n_blocks <= max_scan_blocks) {
         const uint32_t v = threadIdx.x < n_blocks ? block_sums[threadIdx.x] : 0u;
@@ -606,54 +667,6 @@ TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles) {
     return b;
 }
 
-// One block: order_runs[b][c] (tiles of class c in 64-tile block b) becomes the first position of that run in
-// the tile order: the tiles of the classes before c, then those of class c in the blocks before b. Lane c of every
-// wave handles class c (a block's 64 counts are one coalesced row); wave w the w-th sixteenth of the blocks, whose
-// rows it holds in registers (16 at a time), so each row is read once and written once.
-__global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_runs, uint32_t n_blocks, const uint32_t* counters) {
-    if (counters[counter_overflow] != 0) return;
-    constexpr uint32_t n_waves = 1024 / 64;
-    constexpr uint32_t rows = 16;  // rows per lane in registers per pass
-    __shared__ uint32_t s_part[n_waves][order_classes];
-    const uint32_t c = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t per = (n_blocks + n_waves - 1) / n_waves;
-    const uint32_t b0 = min(wave * per, n_blocks), b1 = min(b0 + per, n_blocks);
-    uint32_t sum = 0;
-    for (uint32_t r0 = b0; r0 < b1; r0 += rows) {
-        uint32_t v[rows];
-#pragma unroll
-        for (uint32_t k = 0; k < rows; k++) v[k] = r0 + k < b1 ? order_runs[static_cast<size_t>(r0 + k) * order_classes + c] : 0u;
-#pragma unroll
-        for (uint32_t k = 0; k < rows; k++) sum += v[k];
-    }
-    s_part[wave][c] = sum;
-    __syncthreads();
-    uint32_t total = 0, before = 0;
-#pragma unroll
-    for (uint32_t w = 0; w < n_waves; w++) {
-        const uint32_t x = s_part[w][c];
-        total += x;
-        before += w < wave ? x : 0u;
-    }
-    uint32_t inc = total;  // classes in lane order: prefix over the lanes
-#pragma unroll
-    for (uint32_t o = 1; o < 64; o <<= 1) {
-        const uint32_t x = static_cast<uint32_t>(__shfl_up(static_cast<int>(inc), o));
-        if (c >= o) inc += x;
-    }
-    uint32_t running = inc - total + before;
-    for (uint32_t r0 = b0; r0 < b1; r0 += rows) {
-        uint32_t v[rows];
-#pragma unroll
-        for (uint32_t k = 0; k < rows; k++) v[k] = r0 + k < b1 ? order_runs[static_cast<size_t>(r0 + k) * order_classes + c] : 0u;
-#pragma unroll
-        for (uint32_t k = 0; k < rows; k++) {
-            if (r0 + k < b1) order_runs[static_cast<size_t>(r0 + k) * order_classes + c] = running;
-            running += v[k];
-        }
-    }
-}
-
 bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t max_instances, uint32_t* table, const TileScan& ts,
                         uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
@@ -673,23 +686,28 @@ bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes
                                                                         ts.totals, ts.local_start, ts.block_sums, ts.order_runs, ts.order_rank,
                                                                         ts.counters);
     EFGS_HIP_CHECK(hipGetLastError());
-    tile_order_runs_kernel<<<1, 1024, 0, s>>>(ts.order_runs, div_up(n_tiles, scan_tiles), ts.counters);
-    EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
 
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
                          const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t max_instances,
                          uint32_t n_tiles, hipStream_t s) {
-    if (max_instances == 0) return true;
-    const uint32_t blocks = div_up(max_instances, 256);
+    if (n_tiles == 0) return true;
+    const uint32_t order_blocks = div_up(n_tiles, scan_tiles);
+    if (max_instances == 0) {
+        tile_order_runs_kernel<<<1, 1024, 0, s>>>(ts.order_runs, order_blocks, ts.counters);
+        EFGS_HIP_CHECK(hipGetLastError());
+        return true;
+    }
+    // one block that places the tile order's runs, then one block per 256 instances (a bound on I)
+    const uint32_t blocks = div_up(max_instances, 256) + 1;
     const uint32_t* tab = plan.use_table ? table : nullptr;
     if (key_bytes == 2)
         tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
-                                                            ts.local_start, ts.cursor, bucket, ts.counters, n_tiles);
+                                                            ts.local_start, ts.cursor, bucket, ts.counters, n_tiles, ts.order_runs, order_blocks);
     else
         tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
-                                                            ts.local_start, ts.cursor, bucket, ts.counters, n_tiles);
+                                                            ts.local_start, ts.cursor, bucket, ts.counters, n_tiles, ts.order_runs, order_blocks);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
