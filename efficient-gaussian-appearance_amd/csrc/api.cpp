@@ -696,6 +696,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     if (capacity > 0xfffffff0ull) capacity = 0xfffffff0ull;
 
     uint32_t seq = 0;
+    const bool fused = n > 0 && fused_binning_fits(n_tiles);
     if (n > 0) {
         RtcKernel k;
         if (!get_preprocess_kernel(r, variant, "forward", k)) return EFGS_ERR_RTC;
@@ -714,6 +715,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         a.records = pl.records;
         a.block_counts = pl.block_counts;
         a.block_key_ranges = pl.block_key_ranges;
+        a.counters = pl.counters;
         a.n = n;
         a.cam = cam;
         const uint32_t chunks = div_up(n, preprocess_block);
@@ -723,12 +725,15 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (!launch_rtc(k, blocks, preprocess_block, shared, &a, s)) return EFGS_ERR_HIP;
         t.end(s);
         t.begin(EFGS_STAGE_COMPACT, s);
-        // the scan writes the counters to the pinned host buffer as well, then the frame's sequence number
+        // The counter scan writes the counters to the pinned host buffer as well, then the frame's sequence number.
+        // With the fused emission (grids whose histogram fits) the emission kernel does the scan and the compaction
+        // itself; the scan still runs before a first frame, whose buffers wait for the counts.
         seq = ++r->counter_seq == 0 ? ++r->counter_seq : r->counter_seq;
-        if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, r->host_counters_dev,
-                                      speculate ? static_cast<uint32_t>(capacity) : 0xffffffffu, seq, chunks, s))
-            return EFGS_ERR_HIP;
-        if (!launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
+        if (!speculate || !fused)
+            if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, r->host_counters_dev,
+                                          speculate ? static_cast<uint32_t>(capacity) : 0xffffffffu, seq, chunks, s))
+                return EFGS_ERR_HIP;
+        if (!fused && !launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
         t.end(s);
     } else {
         if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
@@ -739,10 +744,20 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     InstanceLayout il{};
     const auto bin_and_blend = [&](char* iblob, uint64_t cap, uint32_t visible_plan, uint32_t max_visible, uint32_t max_instances) -> int {
         il = InstanceLayout::carve(iblob, cap, key_bytes, n_tiles);
-        const TileBinning plan = tile_binning_plan(visible_plan, n_tiles);
+        FusedBinningArgs fa{};
+        const TileBinning plan = fused ? fused_binning_plan(n, n_tiles, fa.chunks_per_segment) : tile_binning_plan(visible_plan, n_tiles);
+        fa.block_counts = pl.block_counts;
+        fa.key_ranges = pl.block_key_ranges;
+        fa.host_counters = r->host_counters_dev;
+        fa.n_prims = n;
+        fa.n_chunks = div_up(n, preprocess_block);
+        fa.capacity = static_cast<uint32_t>(cap);
+        fa.seq = seq;
         CreateInstancesArgs ca;
         ca.visible_prims = pl.visible_prims;
         ca.prim_offset = pl.prim_offset;
+        ca.visible_prims_out = pl.visible_prims;
+        ca.prim_offset_out = pl.prim_offset;
         ca.n_touched = pl.n_touched;
         ca.records = pl.records;
         ca.keys = il.keys;
@@ -752,7 +767,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         ca.max_visible = max_visible;
         ca.n_visible = 0;
         t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
-        if (!launch_create_instances(ca, key_bytes, plan, il.local_rank, il.table, n_tiles, s)) return EFGS_ERR_HIP;
+        if (!launch_create_instances(ca, key_bytes, plan, il.local_rank, il.table, n_tiles, fused ? &fa : nullptr, s)) return EFGS_ERR_HIP;
         t.end(s);
         const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor, tl.order_runs, tl.order_rank, tl.order, pl.counters};
         t.begin(EFGS_STAGE_TILE_OFFSETS, s);

@@ -48,6 +48,7 @@ bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_off
 constexpr size_t tile_hist_max_lds = 64 * 1024;    // default dynamic LDS limit of a launch
 constexpr uint32_t tile_hist_min_segment = 2048;   // visible primitives per histogram block (at least)
 constexpr uint32_t tile_hist_max_blocks = 256;     // segments (the rank word keeps the segment in its top 8 bits)
+constexpr uint32_t rank_segment_shift = 24;        // rank word: rank within the segment's instances of the tile | segment << 24
 struct TileBinning {
     bool use_table;
     uint32_t blocks;   // histogram blocks (segments, rows of the table)
@@ -57,6 +58,8 @@ TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles);
 struct CreateInstancesArgs {
     const uint32_t* visible_prims;
     const uint32_t* prim_offset;
+    uint32_t* visible_prims_out;   // the fused path writes the compaction (the same arrays)
+    uint32_t* prim_offset_out;
     uint32_t* n_touched;
     const PrimRecord* records;
     void* keys;                // tile key per emission slot, key_bytes wide
@@ -66,10 +69,23 @@ struct CreateInstancesArgs {
     uint32_t max_visible;      // bound on the visible count (grid size of the path without a table)
     uint32_t n_visible;        // set by the kernels from counters[0]
 };
+// The fused path's inputs: the preprocess's per-chunk counts and depth-key ranges, the instance capacity of the
+// binning buffers, and the host's mapped copy of the counters with the frame's sequence number.
+struct FusedBinningArgs {
+    const uint32_t* block_counts;
+    const uint32_t* key_ranges;
+    uint32_t* host_counters;
+    uint32_t n_prims, n_chunks, chunks_per_segment, capacity, seq;
+};
+// whether the fused emission's LDS (tile histogram and compaction buffers) fits a launch
+bool fused_binning_fits(uint32_t n_tiles);
+// segments of whole preprocess chunks for the fused emission (blocks = segments)
+TileBinning fused_binning_plan(uint32_t n_prims, uint32_t n_tiles, uint32_t& chunks_per_segment);
 // (tile key, primitive) at every emission slot; with a table also each instance's rank | segment << 24 and the
-// segments' per-tile counts (plan.blocks segments of ceil(V / plan.blocks) visible primitives)
+// segments' per-tile counts (plan.blocks segments of ceil(V / plan.blocks) visible primitives). With `fused` the
+// emission also does the counter scan and the compaction (segments of whole preprocess chunks).
 bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const TileBinning& plan, uint32_t* local_rank, uint32_t* table,
-                             uint32_t n_tiles, hipStream_t s);
+                             uint32_t n_tiles, const FusedBinningArgs* fused, hipStream_t s);
 // Tile scan state (tile arena): totals[t] instances of tile t, local_start[t] exclusive scan of the totals within
 // t's 64-tile block, block_sums per 64-tile block (tile t starts at the sum of block_sums over the blocks before
 // t / 64 plus local_start[t]), and a per-tile cursor for the global-atomic path.

@@ -70,11 +70,8 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
 // n_touched lowered to the emitted count, so the per-primitive sums of the backward and of the pruning scores
 // cover only slots that a blend kernel writes. Every lane of the wave must call this (ballots and shuffles).
 template <typename KeyT, typename Emit>
-__device__ __forceinline__ void emit_primitive(const CreateInstancesArgs& a, uint32_t i_raw, bool active, uint32_t lane, Emit&& emit) {
+__device__ __forceinline__ void emit_primitive_at(const CreateInstancesArgs& a, uint32_t p, uint32_t off, bool active, uint32_t lane, Emit&& emit) {
     const uint64_t lanes_below = (1ull << lane) - 1ull;
-    const uint32_t i = active ? i_raw : a.n_visible - 1;
-    const uint32_t p = a.visible_prims[i];
-    const uint32_t off = a.prim_offset[p];
     const uint32_t n = a.n_touched[p];
     const PrimRecord rec = a.records[p];
     const uint32_t bx = __float_as_uint(rec.r2.y), by = __float_as_uint(rec.r2.z);
@@ -134,6 +131,14 @@ __device__ __forceinline__ void emit_primitive(const CreateInstancesArgs& a, uin
     }
 }
 
+// visible primitive i (index order) of the compacted list; inactive lanes repeat the last one
+template <typename KeyT, typename Emit>
+__device__ __forceinline__ void emit_primitive(const CreateInstancesArgs& a, uint32_t i_raw, bool active, uint32_t lane, Emit&& emit) {
+    const uint32_t i = active ? i_raw : a.n_visible - 1;
+    const uint32_t p = a.visible_prims[i];
+    emit_primitive_at<KeyT>(a, p, a.prim_offset[p], active, lane, emit);
+}
+
 // One thread per visible primitive (the path for grids whose tile histogram does not fit the LDS).
 template <typename KeyT>
 __global__ __launch_bounds__(instance_block) void create_instances_kernel(CreateInstancesArgs a) {
@@ -159,7 +164,7 @@ __global__ __launch_bounds__(1024) void create_instances_hist_kernel(CreateInsta
     __syncthreads();
     const uint32_t seg = blockIdx.x;
     const uint32_t v0 = seg * per_segment, v1 = min(a.n_visible, v0 + per_segment);
-    const uint32_t tag = seg << 24;
+    const uint32_t tag = seg << rank_segment_shift;
     for (uint32_t base = v0; base < v1; base += 1024) {  // block-uniform trip count
         const uint32_t i = base + threadIdx.x;
         emit_primitive<KeyT>(a, i, i < v1, threadIdx.x & 63u, [&](uint32_t slot, uint32_t tile) {
@@ -169,6 +174,154 @@ __global__ __launch_bounds__(1024) void create_instances_hist_kernel(CreateInsta
     __syncthreads();
     uint32_t* row = table + static_cast<size_t>(seg) * n_tiles;
     for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) row[t] = hist[t];
+}
+
+// Emission with the per-tile counts, the compaction and the counter scan in one kernel (grids whose histogram
+// leaves room for the queue of visible primitives). Block s takes the primitive chunks [s C, (s + 1) C) of the
+// preprocess (C = f.chunks_per_segment chunks of preprocess_block primitives; its emission slots are one
+// contiguous run, its segment). It first sums the preprocess's per-chunk visible and instance counts: over all
+// chunks (the frame's totals and depth-key range: block 0 publishes the counters, to the host as well, followed
+// by the frame's sequence number) and over the chunks before its own (its first visible index and emission slot).
+// More instances than the buffers hold set the overflow flag and nothing is emitted. Then, 1024 primitives at a
+// time, a block scan of the visible flags and tile counts gives every visible primitive its visible index and
+// first emission slot (visible_prims, prim_offset: the compaction) and appends it to an LDS ring of 2048; whenever
+// the ring holds 1024, they are emitted one per thread (and the rest at the end), counted per tile in the LDS
+// histogram as create_instances_hist_kernel does.
+constexpr uint32_t fused_block = 1024;
+constexpr uint32_t fused_ring = 2 * fused_block;
+constexpr size_t fused_extra_lds = 2 * fused_ring * 4 + 512;  // the ring (primitive, first slot) and scan partials
+template <typename KeyT>
+__global__ __launch_bounds__(fused_block) void create_instances_fused_kernel(CreateInstancesArgs a, FusedBinningArgs f, uint32_t* local_rank,
+                                                                           uint32_t* table, uint32_t n_tiles) {
+    extern __shared__ uint32_t hist[];  // n_tiles counters, then the ring of primitives and of their first slots
+    uint32_t* const q_prim = hist + n_tiles;
+    uint32_t* const q_off = q_prim + fused_ring;
+    __shared__ uint32_t s_red[fused_block / 64][8];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t seg = blockIdx.x;
+    const uint32_t c0 = seg * f.chunks_per_segment, c1 = min(f.n_chunks, c0 + f.chunks_per_segment);
+    const uint32_t p_begin = c0 * preprocess_block, p_end = min(f.n_prims, c1 * preprocess_block);
+    // the tile counts of the segment's first fused_prefetch slices of 1024 primitives, loaded with the chunk counts
+    constexpr uint32_t fused_prefetch = 4;
+    uint32_t touched_pre[fused_prefetch];
+#pragma unroll
+    for (uint32_t it = 0; it < fused_prefetch; it++) {
+        const uint32_t p = p_begin + it * fused_block + tid;
+        touched_pre[it] = p < p_end ? a.n_touched[p] : 0u;
+    }
+
+    // totals, depth-key range and the segment's prefix from the per-chunk counts
+    uint32_t tv = 0, ti = 0, bv = 0, bi = 0, kmin = 0xffffffffu, kmax = 0u;
+    for (uint32_t c = tid; c < f.n_chunks; c += fused_block) {
+        const uint2 cnt = reinterpret_cast<const uint2*>(f.block_counts)[c];
+        const uint2 kr = reinterpret_cast<const uint2*>(f.key_ranges)[c];
+        tv += cnt.x;
+        ti += cnt.y;
+        bv += c < c0 ? cnt.x : 0u;
+        bi += c < c0 ? cnt.y : 0u;
+        kmin = min(kmin, kr.x);
+        kmax = max(kmax, kr.y);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        tv += static_cast<uint32_t>(__shfl_xor(static_cast<int>(tv), o));
+        ti += static_cast<uint32_t>(__shfl_xor(static_cast<int>(ti), o));
+        bv += static_cast<uint32_t>(__shfl_xor(static_cast<int>(bv), o));
+        bi += static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o));
+        kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmin), o)));
+        kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), o)));
+    }
+    if (lane == 0) {
+        s_red[wave][0] = tv; s_red[wave][1] = ti; s_red[wave][2] = bv; s_red[wave][3] = bi; s_red[wave][4] = kmin; s_red[wave][5] = kmax;
+    }
+    for (uint32_t t = tid; t < n_tiles; t += fused_block) hist[t] = 0;
+    __syncthreads();
+    tv = ti = bv = bi = 0;
+    kmin = 0xffffffffu;
+    kmax = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < fused_block / 64; w++) {
+        tv += s_red[w][0]; ti += s_red[w][1]; bv += s_red[w][2]; bi += s_red[w][3];
+        kmin = min(kmin, s_red[w][4]);
+        kmax = max(kmax, s_red[w][5]);
+    }
+    const bool overflow = ti > f.capacity;
+    if (seg == 0 && tid == 0) {
+        // [2] (emission mismatches) was cleared by the preprocess and is counted by the emission below
+        const uint32_t c[6] = {tv, ti, 0u, tv > 0 ? kmin : 0u, tv > 0 ? kmax : 0u, overflow ? 1u : 0u};
+#pragma unroll
+        for (uint32_t k = 0; k < 6; k++) {
+            if (k != 2) a.counters[k] = c[k];
+            f.host_counters[k] = c[k];
+        }
+        __threadfence_system();
+        __hip_atomic_store(&f.host_counters[counter_sequence], f.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        __threadfence_system();
+    }
+    if (overflow) return;  // (block-uniform)
+    __syncthreads();       // every wave has read s_red before the scans reuse it
+
+    const uint32_t tag = seg << rank_segment_shift;
+    const auto emit_ring = [&](uint32_t head, uint32_t count) {  // the ring's entries head .. head + count - 1, count > 0
+        const uint32_t k = (head + min(tid, count - 1u)) & (fused_ring - 1u);
+        emit_primitive_at<KeyT>(a, q_prim[k], q_off[k], tid < count, lane, [&](uint32_t slot, uint32_t tile) {
+            local_rank[slot] = tag | atomicAdd(&hist[tile], 1u);
+        });
+    };
+    uint32_t run_v = bv, run_i = bi;
+    uint32_t head = 0, queued = 0;  // ring state (block-uniform)
+    for (uint32_t base = p_begin, it = 0; base < p_end; base += fused_block, it++) {  // block-uniform trip count
+        const uint32_t p = base + tid;
+        uint32_t touched = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < fused_prefetch; k++) touched = it == k ? touched_pre[k] : touched;
+        if (it >= fused_prefetch) touched = p < p_end ? a.n_touched[p] : 0u;
+        const uint32_t vis = touched > 0 ? 1u : 0u;
+        uint32_t iv = vis, ii = touched;  // inclusive wave scans
+#pragma unroll
+        for (uint32_t o = 1; o < 64; o <<= 1) {
+            const uint32_t xv = static_cast<uint32_t>(__shfl_up(static_cast<int>(iv), o));
+            const uint32_t xi = static_cast<uint32_t>(__shfl_up(static_cast<int>(ii), o));
+            iv += lane >= o ? xv : 0u;
+            ii += lane >= o ? xi : 0u;
+        }
+        if (lane == 63) {
+            s_red[wave][0] = iv;
+            s_red[wave][1] = ii;
+        }
+        __syncthreads();
+        uint32_t pv = 0, pi = 0, nv = 0, ni = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < fused_block / 64; w++) {
+            const uint32_t wv = s_red[w][0], wi = s_red[w][1];
+            pv += w < wave ? wv : 0u;
+            pi += w < wave ? wi : 0u;
+            nv += wv;
+            ni += wi;
+        }
+        const uint32_t vpos = pv + iv - vis, off = run_i + pi + ii - touched;
+        if (vis) {
+            a.visible_prims_out[run_v + vpos] = p;
+            a.prim_offset_out[p] = off;
+            const uint32_t k = (head + queued + vpos) & (fused_ring - 1u);
+            q_prim[k] = p;
+            q_off[k] = off;
+        }
+        run_v += nv;
+        run_i += ni;
+        queued += nv;
+        __syncthreads();  // the ring entries are written; the scan partials may be reused
+        if (queued >= fused_block) {
+            emit_ring(head, fused_block);
+            head = (head + fused_block) & (fused_ring - 1u);
+            queued -= fused_block;
+            __syncthreads();  // the emitted entries have been read before the next primitives overwrite them
+        }
+    }
+    if (queued > 0) emit_ring(head, queued);
+    __syncthreads();
+    uint32_t* row = table + static_cast<size_t>(seg) * n_tiles;
+    for (uint32_t t = tid; t < n_tiles; t += fused_block) row[t] = hist[t];
 }
 
 // Per-tile offsets, 64 tiles per block, one tile per lane. With a count table (S segment rows): wave w of 16 loads
@@ -383,7 +536,7 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     }
     if (table) {  // the table entry already holds the tile's start within its block
         const uint32_t r = local_rank[e];
-        pos += table[static_cast<size_t>(r >> 24) * n_tiles + t] + (r & 0xffffffu);
+        pos += table[static_cast<size_t>(r >> rank_segment_shift) * n_tiles + t] + (r & ((1u << rank_segment_shift) - 1u));
     } else {
         pos += local_start[t] + atomicAdd(&cursor[t], 1u);
     }
@@ -638,9 +791,15 @@ bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_off
 }
 
 bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const TileBinning& plan, uint32_t* local_rank, uint32_t* table,
-                             uint32_t n_tiles, hipStream_t s) {
+                             uint32_t n_tiles, const FusedBinningArgs* fused, hipStream_t s) {
     if (a.max_visible == 0) return true;
-    if (plan.use_table) {
+    if (fused) {
+        const size_t lds = static_cast<size_t>(n_tiles) * 4 + 2 * fused_ring * 4;
+        if (key_bytes == 2)
+            create_instances_fused_kernel<uint16_t><<<plan.blocks, fused_block, lds, s>>>(a, *fused, local_rank, table, n_tiles);
+        else
+            create_instances_fused_kernel<uint32_t><<<plan.blocks, fused_block, lds, s>>>(a, *fused, local_rank, table, n_tiles);
+    } else if (plan.use_table) {
         const size_t lds = static_cast<size_t>(n_tiles) * 4;
         if (key_bytes == 2)
             create_instances_hist_kernel<uint16_t><<<plan.blocks, 1024, lds, s>>>(a, local_rank, table, n_tiles);
@@ -655,6 +814,20 @@ bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const 
     }
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
+}
+
+bool fused_binning_fits(uint32_t n_tiles) { return n_tiles > 0 && static_cast<size_t>(n_tiles) * 4 + fused_extra_lds <= tile_hist_max_lds; }
+
+TileBinning fused_binning_plan(uint32_t n_prims, uint32_t n_tiles, uint32_t& chunks_per_segment) {
+    TileBinning b;
+    b.use_table = true;
+    const uint32_t n_chunks = n_prims > 0 ? div_up(n_prims, preprocess_block) : 1u;
+    const uint32_t want = n_prims > 0 ? div_up(n_prims, tile_hist_min_segment) : 1u;
+    chunks_per_segment = div_up(n_chunks, want < tile_hist_max_blocks ? want : tile_hist_max_blocks);
+    b.blocks = div_up(n_chunks, chunks_per_segment);
+    b.segment = chunks_per_segment * preprocess_block;
+    (void)n_tiles;
+    return b;
 }
 
 TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles) {

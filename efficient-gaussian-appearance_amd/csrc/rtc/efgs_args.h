@@ -37,6 +37,7 @@ struct PreprocessForwardArgs {
     PrimRecord* records;          // (N) written for visible primitives
     uint32_t* block_counts;       // (2 * blocks) visible count and instance count per block
     uint32_t* block_key_ranges;   // (2 * blocks) min and max depth key of the block's visible primitives
+    uint32_t* counters;           // the frame's counters: [2] (instance-emission mismatches) is cleared here
     uint32_t n;
     uint32_t pad_;
     CameraArgs cam;

@@ -220,6 +220,7 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
             a.block_counts[2 * chunk + 1] = i;
             a.block_key_ranges[2 * chunk] = kmin;
             a.block_key_ranges[2 * chunk + 1] = kmax;
+            if (chunk == 0) a.counters[2] = 0u;  // the emission after this kernel counts its mismatches there
         }
         if (active) {
             a.n_touched[p] = touched;
