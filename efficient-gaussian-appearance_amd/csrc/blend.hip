@@ -293,7 +293,9 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
     constexpr uint32_t n_values = ABS ? 11u : 9u;
     constexpr uint32_t dummy = BATCH;                      // staged Gaussian of opacity 0 past the batch
     constexpr uint32_t gstride = BATCH + 1;                // one (value, group) slot row, the dummy's column last
-    constexpr uint32_t vstride = backward_groups * gstride;
+    // one value's slot rows, padded by 4 floats: the combine's lanes read values 4 apart at once, and 4 x vstride
+    // must not be a multiple of the 64 banks (nor the walk's four value rows 1 apart)
+    constexpr uint32_t vstride = backward_groups * gstride + 4;
     constexpr uint32_t n_part = n_values * vstride;
     static_assert(BATCH <= 64 && BATCH % 4 == 0 && n_part % 4 == 0, "a group's four lanes cull a quarter of the batch each; slots clear as float4");
     __shared__ float4 s_stage[BATCH + 1][3];               // (x, y, packed rect), exp2-scaled conic + opacity, colour
