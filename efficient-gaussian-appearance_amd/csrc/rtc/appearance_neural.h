@@ -256,29 +256,53 @@ __host__ __device__ constexpr uint32_t kpos(uint32_t c, uint32_t width) {
     return c < width / 32u * 32u ? (c & ~31u) | (((c >> 2) & 3u) << 3) | (((c >> 4) & 1u) << 2) | (c & 3u) : c;
 }
 
-// copies the flat tcnn-layout weights (fp16 bits, 16-byte aligned) into the W / W^T layout above (whole block
-// of N_THREADS): 8 weights per 16-byte load, up to 8 loads per thread in flight before the LDS stores. Every
-// layer holds a multiple of 256 weights, so a vector never straddles two layers or two rows.
-template <uint32_t N_THREADS>
-__device__ inline void load_weights(const uint16_t* g, uint16_t* WL, uint32_t tid) {
+// the fp16 bits of 8 consecutive flat weights: from fp16 bits (one 16-byte load) or from fp32 master weights (two
+// 16-byte loads, rounded to nearest even, as a cast of the tensor to half would)
+struct WeightVec8 {
+    uint4 lo, hi;
+};
+__device__ __forceinline__ WeightVec8 load_weight_vec(const uint16_t* g, uint32_t v) {
+    return WeightVec8{reinterpret_cast<const uint4*>(g)[v], make_uint4(0u, 0u, 0u, 0u)};
+}
+__device__ __forceinline__ WeightVec8 load_weight_vec(const float* g, uint32_t v) {
+    const uint4* gv = reinterpret_cast<const uint4*>(g);
+    return WeightVec8{gv[2 * v], gv[2 * v + 1]};
+}
+__device__ __forceinline__ void weight_bits(const WeightVec8& w, const uint16_t*, uint16_t (&e)[8]) {
+    const uint32_t x[4] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w};
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+        e[2 * i] = static_cast<uint16_t>(x[i]);
+        e[2 * i + 1] = static_cast<uint16_t>(x[i] >> 16);
+    }
+}
+__device__ __forceinline__ void weight_bits(const WeightVec8& w, const float*, uint16_t (&e)[8]) {
+    const uint32_t x[8] = {w.lo.x, w.lo.y, w.lo.z, w.lo.w, w.hi.x, w.hi.y, w.hi.z, w.hi.w};
+#pragma unroll
+    for (uint32_t i = 0; i < 8; i++) e[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(x[i])));
+}
+
+// copies the flat tcnn-layout weights (fp16 bits or fp32 master weights, 16-byte aligned) into the W / W^T layout
+// above (whole block of N_THREADS): 8 weights per vector, up to 8 vectors per thread in flight before the LDS
+// stores. Every layer holds a multiple of 256 weights, so a vector never straddles two layers or two rows.
+template <uint32_t N_THREADS, typename SRC>
+__device__ inline void load_weights(const SRC* g, uint16_t* WL, uint32_t tid) {
     constexpr uint32_t n_vec = PARAMS / 8;
     constexpr uint32_t batch = 8;
-    const uint4* gv = reinterpret_cast<const uint4*>(g);
     for (uint32_t v0 = 0; v0 < n_vec; v0 += batch * N_THREADS) {
-        uint4 w[batch];
+        WeightVec8 w[batch];
 #pragma unroll
         for (uint32_t k = 0; k < batch; k++) {
             const uint32_t v = v0 + k * N_THREADS + tid;
-            if (v < n_vec) w[k] = gv[v];
+            if (v < n_vec) w[k] = load_weight_vec(g, v);
         }
 #pragma unroll
         for (uint32_t k = 0; k < batch; k++) {
             const uint32_t v = v0 + k * N_THREADS + tid;
             if (v >= n_vec) continue;
             const uint32_t h = 8 * v;
-            const uint16_t e[8] = {static_cast<uint16_t>(w[k].x), static_cast<uint16_t>(w[k].x >> 16), static_cast<uint16_t>(w[k].y),
-                                   static_cast<uint16_t>(w[k].y >> 16), static_cast<uint16_t>(w[k].z), static_cast<uint16_t>(w[k].z >> 16),
-                                   static_cast<uint16_t>(w[k].w), static_cast<uint16_t>(w[k].w >> 16)};
+            uint16_t e[8];
+            weight_bits(w[k], g, e);
 #pragma unroll
             for (uint32_t l = 0; l < NL; l++) {
                 if (h < loff(l) || h >= loff(l) + lout(l) * lin(l)) continue;

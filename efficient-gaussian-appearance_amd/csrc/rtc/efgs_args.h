@@ -31,7 +31,7 @@ struct PreprocessForwardArgs {
     const float* precomputed;
     const float* base;
     const float* residual;
-    const uint16_t* mlp_weights;  // fp16 bits, flat tcnn layout
+    const float* mlp_weights;     // fp32 master weights, flat tcnn layout (rounded to fp16 as they are staged in LDS)
     uint32_t* n_touched;          // (N) 0 for culled primitives
     uint32_t* depth_keys;         // (N) float bits of the view depth
     PrimRecord* records;          // (N) written for visible primitives
@@ -50,7 +50,7 @@ struct PreprocessBackwardArgs {
     const float* opacities;
     const float* base;
     const float* residual;
-    const uint16_t* mlp_weights;
+    const float* mlp_weights;        // fp32 master weights, flat tcnn layout
     const uint32_t* n_touched;
     const uint32_t* prim_offset;     // (N) first emitted instance of each visible primitive
     const PrimRecord* records;

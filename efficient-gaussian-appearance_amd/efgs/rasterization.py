@@ -147,14 +147,14 @@ def _native_settings(s: RasterizerSettings, device: torch.device) -> tuple[_lib.
     return c, [w2c, cam, bg]
 
 
-def _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half):
+def _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32):
     p = _lib.Primitives()
     p.n_primitives = int(means.shape[0])
     p.means, p.scales, p.rotations, p.opacities = means.data_ptr(), scales.data_ptr(), rotations.data_ptr(), opacities.data_ptr()
     p.precomputed_colors = _ptr(precomputed_colors)
     p.base_colors = _ptr(base_colors)
     p.residual_params = _ptr(residual_params)
-    p.mlp_weights = _ptr(mlp_weights_half)
+    p.mlp_weights = _ptr(mlp_weights_f32)
     return p
 
 
@@ -166,25 +166,25 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _check_inputs(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half) -> torch.device:
+def _check_inputs(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32) -> torch.device:
     device = means.device
     if device.type != 'cuda':
         raise ValueError('efgs: the rasterizer runs on a GPU device')
     names = ('means', 'scales', 'rotations', 'opacities', 'precomputed_colors', 'base_colors', 'residual_params')
     for name, t in zip(names, (means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params)):
         _check_param(name, t, device)
-    if mlp_weights_half.numel() > 0:
+    if mlp_weights_f32.numel() > 0:
         expected = _rasterizer.mlp_param_count()
-        if mlp_weights_half.numel() != expected or mlp_weights_half.device != device:
-            raise ValueError(f'efgs: mlp_weights must hold {expected} parameters on {device}, got {mlp_weights_half.numel()}')
+        if mlp_weights_f32.numel() != expected or mlp_weights_f32.device != device:
+            raise ValueError(f'efgs: mlp_weights must hold {expected} parameters on {device}, got {mlp_weights_f32.numel()}')
     return device
 
 
-def _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half, settings):
-    device = _check_inputs(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
+def _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32, settings):
+    device = _check_inputs(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32)
     with torch.cuda.device(device):
         cs, keep = _native_settings(settings, device)
-        prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
+        prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32)
         image = torch.empty((3, int(settings.height), int(settings.width)), dtype=torch.float32, device=device)
         alloc = _lib.WorkspaceAllocator(device, 'forward')
         frame = _lib.Frame()
@@ -200,20 +200,20 @@ class _Rasterize(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights,
                 densification_info, rasterizer_settings: RasterizerSettings) -> torch.Tensor:
-        mlp_weights_half = mlp_weights.detach().half().contiguous() if mlp_weights.numel() > 0 else torch.empty(0, dtype=torch.float16, device=means.device)
+        mlp_weights_f32 = mlp_weights.detach().float().contiguous() if mlp_weights.numel() > 0 else torch.empty(0, dtype=torch.float32, device=means.device)
         image, frame, buffers, _ = _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params,
-                                            mlp_weights_half, rasterizer_settings)
+                                            mlp_weights_f32, rasterizer_settings)
         ctx.rasterizer_settings = rasterizer_settings
         ctx.frame = frame
         ctx.buffers = buffers
         ctx.mlp_numel = mlp_weights.numel()
-        ctx.save_for_backward(image, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
+        ctx.save_for_backward(image, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32)
         ctx.densification_info = densification_info
         ctx.mark_non_differentiable(densification_info)
         # the backward's host-side state is built here, while the GPU still runs the forward, so that the
         # backward only launches
         ctx.prepared = _prepare_backward(ctx, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params,
-                                         mlp_weights_half, densification_info, rasterizer_settings) if any(ctx.needs_input_grad) else None
+                                         mlp_weights_f32, densification_info, rasterizer_settings) if any(ctx.needs_input_grad) else None
         return image
 
     @staticmethod
@@ -256,7 +256,7 @@ def _on_device(device: torch.device):
     return contextlib.nullcontext() if torch.cuda.current_device() == device.index else torch.cuda.device(device)
 
 
-def _prepare_backward(ctx, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half,
+def _prepare_backward(ctx, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32,
                       dinfo, settings) -> _PreparedBackward:
     """Native structs, gradient outputs (every gradient is a view of one allocation, each fully written by the
     backward) and the workspace of the backward of this forward."""
@@ -267,7 +267,7 @@ def _prepare_backward(ctx, means, scales, rotations, opacities, precomputed_colo
         raise ValueError('efgs: densification_info must be a contiguous float32 (2|3, N) tensor on the rendering device')
     with _on_device(device):
         cs, keep = _native_settings(settings, device)
-        prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_half)
+        prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32)
         shapes = [means.shape, scales.shape, rotations.shape, opacities.shape, precomputed_colors.shape, base_colors.shape,
                   residual_params.shape, (ctx.mlp_numel,)]
         sizes = [int(torch.Size(sh).numel()) for sh in shapes]
@@ -313,15 +313,15 @@ def rasterize(means: torch.Tensor, scales: torch.Tensor, rotations: torch.Tensor
     """Inference render (B/torch_bindings/rasterization.py:198-224): (3, H, W) if to_chw else (H, W, 3),
     clamped to [0, 1] if clamp_output; written in that layout by the blend kernel, no backward state."""
     d = means.device
-    mlp_half = mlp_weights.detach().half().contiguous() if mlp_weights is not None else _empty(d, torch.float16)
+    mlp_f32 = mlp_weights.detach().float().contiguous() if mlp_weights is not None else _empty(d)
     pre = precomputed_colors if precomputed_colors is not None else _empty(d)
     base = base_colors if base_colors is not None else _empty(d)
     res = residual_params if residual_params is not None else _empty(d)
-    device = _check_inputs(means, scales, rotations, opacities, pre, base, res, mlp_half)
+    device = _check_inputs(means, scales, rotations, opacities, pre, base, res, mlp_f32)
     h, w = int(rasterizer_settings.height), int(rasterizer_settings.width)
     with torch.cuda.device(device):
         cs, keep = _native_settings(rasterizer_settings, device)
-        prims = _native_primitives(means, scales, rotations, opacities, pre, base, res, mlp_half)
+        prims = _native_primitives(means, scales, rotations, opacities, pre, base, res, mlp_f32)
         image = torch.empty((3, h, w) if to_chw else (h, w, 3), dtype=torch.float32, device=device)
         alloc = _lib.WorkspaceAllocator(device, 'render')
         check(lib.efgs_render(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), image.data_ptr(), int(bool(to_chw)),
@@ -395,16 +395,16 @@ def update_pruning_scores(scores: torch.Tensor, means: torch.Tensor, scales: tor
     """Speedy-Splat pruning scores of one view (B/torch_bindings/rasterization.py:226-250): scores (N,) float32
     += per Gaussian the sum over the view's pixels of (o dL/dalpha)^2 for an all-ones image gradient, in place."""
     d = means.device
-    mlp_half = mlp_weights.detach().half().contiguous() if mlp_weights is not None else _empty(d, torch.float16)
+    mlp_f32 = mlp_weights.detach().float().contiguous() if mlp_weights is not None else _empty(d)
     pre = precomputed_colors if precomputed_colors is not None else _empty(d)
     base = base_colors if base_colors is not None else _empty(d)
     res = residual_params if residual_params is not None else _empty(d)
-    device = _check_inputs(means, scales, rotations, opacities, pre, base, res, mlp_half)
+    device = _check_inputs(means, scales, rotations, opacities, pre, base, res, mlp_f32)
     if scores.dtype != torch.float32 or scores.device != device or not scores.is_contiguous() or scores.numel() != means.shape[0]:
         raise ValueError('efgs: scores must be a contiguous float32 tensor of N entries on the rendering device')
     with torch.cuda.device(device):
         cs, keep = _native_settings(rasterizer_settings, device)
-        prims = _native_primitives(means, scales, rotations, opacities, pre, base, res, mlp_half)
+        prims = _native_primitives(means, scales, rotations, opacities, pre, base, res, mlp_f32)
         alloc = _lib.WorkspaceAllocator(device, 'scores')
         check(lib.efgs_update_pruning_scores(_rasterizer.handle, ctypes.byref(prims), ctypes.byref(cs), scores.data_ptr(), alloc.fn,
                                              alloc.ctx, _stream(device)))
@@ -423,10 +423,10 @@ def forward_with_frame(means, scales, rotations, opacities, rasterizer_settings:
                        base_colors=None, residual_params=None, mlp_weights=None):
     """Forward pass returning (image, frame, buffers): the frame and the buffers that back it, for inspection."""
     d = means.device
-    mlp_half = mlp_weights.detach().half().contiguous() if mlp_weights is not None else _empty(d, torch.float16)
+    mlp_f32 = mlp_weights.detach().float().contiguous() if mlp_weights is not None else _empty(d)
     image, frame, buffers, _ = _forward(means, scales, rotations, opacities,
                                         precomputed_colors if precomputed_colors is not None else _empty(d),
                                         base_colors if base_colors is not None else _empty(d),
                                         residual_params if residual_params is not None else _empty(d),
-                                        mlp_half, rasterizer_settings)
+                                        mlp_f32, rasterizer_settings)
     return image, frame, buffers

@@ -117,7 +117,8 @@ typedef struct efgs_primitives {
     const float* precomputed_colors;  /* (N, 3) or NULL; non-NULL selects the precomputed-colour variant */
     const float* base_colors;         /* (N, 3) or NULL */
     const float* residual_params;     /* model-specific (N, ...) or NULL */
-    const uint16_t* mlp_weights;      /* fp16 bits, efgs_mlp_param_count entries, neural only */
+    const float* mlp_weights;         /* fp32 master weights, efgs_mlp_param_count entries, 16-byte aligned, neural only
+                                         (rounded to fp16, to nearest even, as the kernels stage them) */
 } efgs_primitives;
 
 /* Forward state consumed by the backward. The three buffers are caller-owned allocations made through the
