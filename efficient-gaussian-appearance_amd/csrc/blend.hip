@@ -302,6 +302,7 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
     __shared__ uint32_t s_emit[BATCH];
     __shared__ uint32_t s_list[backward_groups][BATCH + 1];  // odd row stride: the groups' entries s in distinct banks
     __shared__ float4 s_part4[n_part / 4];                 // slots [value][group][Gaussian]
+    __shared__ float s_sum[n_values * BATCH];              // the combine's group sums [value][Gaussian]
     float* const s_part = reinterpret_cast<float*>(s_part4);
 
     const uint32_t lane = threadIdx.x;
@@ -405,10 +406,13 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
         {
             constexpr uint32_t Q = BATCH / 4;
             uint32_t hits = 0;
+            uint2 rects[Q];
+#pragma unroll
+            for (uint32_t t = 0; t < Q; t++) rects[t] = rect_of(s_stage[k * Q + t][0]);  // (all reads in flight at once)
 #pragma unroll
             for (uint32_t t = 0; t < Q; t++) {
                 const uint32_t j = k * Q + t;
-                const uint2 rect = rect_of(s_stage[j][0]);
+                const uint2 rect = rects[t];
                 const uint32_t rx0 = rect.x & 0xffffu, rx1 = rect.x >> 16, ry0 = rect.y & 0xffffu, ry1 = rect.y >> 16;
                 const bool hit = j < batch_n && rx0 < gx0 + 4u && gx0 < rx1 && ry0 < gy0 + 3u && gy0 < ry1;
                 hits |= hit ? 1u << t : 0u;
@@ -514,35 +518,42 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
             }
         }
         wave_lds_fence();  // every group's sums are in its slots
-        // combine: item (Gaussian j, quarter q) adds the sixteen group slots of values 4q .. 4q + 3 in group order
-        // and writes 16 bytes of the instance's 48-byte record (q = 3 has nothing to do). Every staged instance
-        // gets its record: those after the tile's last contributor, which no group walked, get zeros.
+        // combine: item (value v, Gaussian j), spread over all 64 lanes, adds the sixteen group slots in group order
+        // into s_sum; then lane (Gaussian j, quarter q) writes 16 bytes of the instance's 48-byte record (q = 3 has
+        // nothing to do). Every staged instance gets its record: those after the tile's last contributor, which no
+        // group walked, get zeros.
         const uint32_t batch_staged = min(BATCH, n_total - start);
-        for (uint32_t item = lane; item < 4u * BATCH; item += 64) {
-            const uint32_t jj = item % BATCH, q = item / BATCH;
-            if (jj >= batch_staged || q == 3u) continue;
-            float r[4];
+        for (uint32_t item = lane; item < n_values * BATCH; item += 64) {
+            const uint32_t v = item / BATCH, jj = item % BATCH;
+            const float* src = s_part + v * vstride + jj;
+            float acc = 0.0f;
 #pragma unroll
-            for (uint32_t c = 0; c < 4; c++) {
-                const uint32_t v = min(4u * q + c, n_values - 1u);
-                const float* src = s_part + v * vstride + jj;
-                float acc = 0.0f;
+            for (uint32_t g = 0; g < backward_groups; g++) acc += src[g * gstride];
+            s_sum[item] = acc;
+        }
+        wave_lds_fence();
+        if (lane < 3u * BATCH) {
+            const uint32_t jj = lane % BATCH, q = lane / BATCH;
+            if (jj < batch_staged) {
+                float r[4];
 #pragma unroll
-                for (uint32_t g = 0; g < backward_groups; g++) acc += src[g * gstride];
-                r[c] = 4u * q + c < n_values ? acc : 0.0f;
+                for (uint32_t c = 0; c < 4; c++) {
+                    const uint32_t v = 4u * q + c;
+                    r[c] = v < n_values ? s_sum[min(v, n_values - 1u) * BATCH + jj] : 0.0f;
+                }
+                const float4 co = s_stage[jj][1];
+                const float4 craw = raw_conic_of(co);
+                // q = 0: dL/dmean2d = C (sum h d), 0.5 (sum h dx^2, sum h dx dy); q = 1: 0.5 sum h dy^2, sum G dL/dalpha =
+                // -(sum of h) / o, colour r, g; q = 2: colour b, |dL/dmean2d| (x, y), 0
+                float4 o;
+                if (q == 0u)
+                    o = make_float4(__builtin_fmaf(craw.x, r[0], craw.y * r[1]), __builtin_fmaf(craw.y, r[0], craw.z * r[1]), 0.5f * r[2], 0.5f * r[3]);
+                else if (q == 1u)
+                    o = make_float4(0.5f * r[0], -r[1] * __builtin_amdgcn_rcpf(co.w), r[2], r[3]);
+                else
+                    o = make_float4(r[0], r[1], r[2], r[3]);
+                reinterpret_cast<float4*>(a.inst_grads)[3 * static_cast<size_t>(s_emit[jj]) + q] = o;
             }
-            const float4 co = s_stage[jj][1];
-            const float4 craw = raw_conic_of(co);
-            // q = 0: dL/dmean2d = C (sum h d), 0.5 (sum h dx^2, sum h dx dy); q = 1: 0.5 sum h dy^2, sum G dL/dalpha =
-            // -(sum of h) / o, colour r, g; q = 2: colour b, |dL/dmean2d| (x, y), 0
-            float4 o;
-            if (q == 0u)
-                o = make_float4(__builtin_fmaf(craw.x, r[0], craw.y * r[1]), __builtin_fmaf(craw.y, r[0], craw.z * r[1]), 0.5f * r[2], 0.5f * r[3]);
-            else if (q == 1u)
-                o = make_float4(0.5f * r[0], -r[1] / co.w, r[2], r[3]);
-            else
-                o = make_float4(r[0], r[1], r[2], r[3]);
-            reinterpret_cast<float4*>(a.inst_grads)[3 * static_cast<size_t>(s_emit[jj]) + q] = o;
         }
         covered = min(n_total, start + BATCH);
         wave_lds_fence();  // the combine has read the slots and the stage
