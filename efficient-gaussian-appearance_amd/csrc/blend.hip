@@ -319,9 +319,10 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
     for (uint32_t q = lane; q < n_part / 4; q += 64) s_part4[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (lane < 3) s_stage[dummy][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
-    // pixel state of the lane's three rows: upstream gradient, (colour still to come) . g, background term. The
-    // loads are unconditional (clamped to the image) so that all of them are in flight together.
-    float pyf[3], T[3], A[3], gr[3], gg[3], gb[3], gbg[3];
+    // pixel state of the lane's three rows: upstream gradient and Ab = (colour still to come) . g - g_bg, the
+    // background term g_bg = -T_final (bg . g) folded in. The loads are unconditional (clamped to the image) so
+    // that all of them are in flight together.
+    float pyf[3], T[3], Ab[3], gr[3], gg[3], gb[3];
     uint32_t last[3];
     {
         const uint32_t np = a.width * a.height;
@@ -352,8 +353,9 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
             const float ar = im[r][0] - Tf[r] * bg0;
             const float ag = im[r][1] - Tf[r] * bg1;
             const float ab = im[r][2] - Tf[r] * bg2;
-            A[r] = inside[r] ? __builtin_fmaf(ab, gb[r], __builtin_fmaf(ag, gg[r], ar * gr[r])) : 0.0f;
-            gbg[r] = inside[r] ? Tf[r] * -(gr[r] * bg0 + gg[r] * bg1 + gb[r] * bg2) : 0.0f;
+            const float A = __builtin_fmaf(ab, gb[r], __builtin_fmaf(ag, gg[r], ar * gr[r]));
+            const float gbg = Tf[r] * -(gr[r] * bg0 + gg[r] * bg1 + gb[r] * bg2);
+            Ab[r] = inside[r] ? A - gbg : 0.0f;
         }
     }
 
@@ -463,8 +465,8 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
                     const float oma = 1.0f - ae;
                     const float rcp = __builtin_amdgcn_rcpf(fmaxf(oma, one_minus_alpha_eps));
                     const float cg = __builtin_fmaf(col.z, gb[r], __builtin_fmaf(col.y, gg[r], col.x * gr[r]));
-                    A[r] = __builtin_fmaf(-w, cg, A[r]);
-                    const float dalpha = __builtin_fmaf(T[r], cg, -rcp * (A[r] - gbg[r]));
+                    Ab[r] = __builtin_fmaf(-w, cg, Ab[r]);
+                    const float dalpha = __builtin_fmaf(T[r], cg, -rcp * Ab[r]);
                     const float h = -ae * dalpha;
                     const float hdy = h * dy;
                     if (r == 0) {
