@@ -45,8 +45,10 @@ TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'traffic_c3_neural.txt')
 # kernel names (as rocprofv3 lists them) of each timed stage
 STAGE_KERNELS = {
     'preprocess_forward': 'preprocess_forward_<model>',
+    # (with the fused emission the scan runs on a first frame only and the compaction not at all: the compact
+    # stage's time is then its empty event bracket)
     'compact': 'scan_block_counts_kernel + compact_visible_kernel',
-    'create_instances': 'create_instances_hist_kernel',
+    'create_instances': 'create_instances_fused_kernel',
     'tile_offsets': 'tile_column_scan_kernel',  # (the tile order's runs are placed by an extra block of tile_buckets_kernel)
     'tile_buckets': 'tile_buckets_kernel',
     'tile_sort': 'tile_sort_kernel',
