@@ -271,39 +271,63 @@ __device__ __forceinline__ float rows_reduce1(float v) {
 // columns are then summed with two permlane swaps per four values (a lane row ends holding one of every four
 // sums), no selects: the three pixels per lane amortise the cross-lane work that a pixel per lane paid alone.
 //
-// Gaussians are staged BATCH at a time; each of a group's four lanes tests a quarter of the batch against the
-// group's rectangle and a prefix sum over the four places the hits in the group's list, in Gaussian order; each
-// group walks its own list, one Gaussian per step (sixteen different Gaussians per wave instruction), with the
-// list entries read two steps and the staged Gaussians one step ahead, and stores its sums into its slot row of each value
-// (a group visits a Gaussian at most once per batch). The combine then adds each value's sixteen slots in a fixed
-// order, writes the 48-byte record at the instance's emission slot and clears the slots. A single wave needs no
-// block barrier: LDS accesses of a wave complete in order, and a wavefront fence keeps the compiler from
-// reordering them around the list and slot exchanges. No atomics: the result is run-to-run deterministic.
-// Gaussians per batch: the slots take 16 x 9 x (BATCH + 1) floats of LDS, so the batch size trades walk steps
-// (a group's list padded to the longest of the sixteen, per batch) against waves per CU. Measured on the 1M-Gaussian
-// 1080p scene: 8 / 12 / 16 / 20 / 32 Gaussians 215 / 185 / 193 / 206 / 241 us.
-#ifndef EFGS_BACKWARD_BATCH
-#define EFGS_BACKWARD_BATCH 12
+// Gaussians are staged 32 at a time (a chunk). Each of a group's four lanes tests a quarter of the chunk against
+// the group's rectangle, and two lane swaps give every lane of the group the group's 32-bit hit mask. The chunk
+// is then walked in sub-batches: a sub-batch ends before the first Gaussian that would give some group more than
+// LIST hits (or at the chunk's end), so each takes at most LIST wave steps while covering as many Gaussians as
+// the busiest group allows. A group walks its hits in the sub-batch in Gaussian order, one per step (the next
+// one is the mask's lowest set bit; past its hits it walks a staged Gaussian of opacity 0), sixteen different
+// Gaussians per wave instruction, and stores step s's sums at position s of its slot row of each value. The
+// combine then gives two lanes to each Gaussian of the sub-batch; they add the sixteen groups' slots in group
+// order (a per-group byte table holds the Gaussian's position in the group's walk, or an always-zero slot when
+// the group did not walk it) and write the 48-byte record at the instance's emission slot. A single wave needs
+// no block barrier: LDS accesses of a wave complete in order, and a wavefront fence keeps the compiler from
+// reordering them around the table and slot exchanges. No atomics: the result is run-to-run deterministic.
+// LIST trades walk steps against LDS (the slots take (8 + extra) x 16 x LIST floats; at most about 10 KB per
+// wave keeps four waves per SIMD). Against fixed batches of 12 Gaussians per walk (each group's list padded to
+// the batch's longest), the sub-batches take 16 % fewer wave steps and half as many combines on the 1M-Gaussian
+// 1080p scene.
+#ifndef EFGS_BACKWARD_LIST
+#define EFGS_BACKWARD_LIST 12
 #endif
-constexpr uint32_t blend_backward_batch = EFGS_BACKWARD_BATCH;
+constexpr uint32_t backward_list = EFGS_BACKWARD_LIST;
 constexpr uint32_t backward_groups = 16;
+constexpr uint32_t backward_chunk = 32;
 
-template <bool ABS, uint32_t BATCH>
-__global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a) {
-    constexpr uint32_t n_values = ABS ? 11u : 9u;
-    constexpr uint32_t dummy = BATCH;                      // staged Gaussian of opacity 0 past the batch
-    constexpr uint32_t gstride = BATCH + 1;                // one (value, group) slot row, the dummy's column last
-    // one value's slot rows, padded by 4 floats: the combine's lanes read values 4 apart at once, and 4 x vstride
-    // must not be a multiple of the 64 banks (nor the walk's four value rows 1 apart)
-    constexpr uint32_t vstride = backward_groups * gstride + 4;
-    constexpr uint32_t n_part = n_values * vstride;
-    static_assert(BATCH <= 64 && BATCH % 4 == 0 && n_part % 4 == 0, "a group's four lanes cull a quarter of the batch each; slots clear as float4");
-    __shared__ float4 s_stage[BATCH + 1][3];               // (x, y, packed rect), exp2-scaled conic + opacity, colour
-    __shared__ uint32_t s_emit[BATCH];
-    __shared__ uint32_t s_list[backward_groups][BATCH + 1];  // odd row stride: the groups' entries s in distinct banks
-    __shared__ float4 s_part4[n_part / 4];                 // slots [value][group][Gaussian]
-    __shared__ float s_sum[n_values * BATCH];              // the combine's group sums [value][Gaussian]
-    float* const s_part = reinterpret_cast<float*>(s_part4);
+// The bitwise OR of one value over the four lane rows, in every row.
+__device__ __forceinline__ uint32_t rows_or(uint32_t v) {
+    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = a[0] | a[1];
+    const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return b[0] | b[1];
+}
+
+// The minimum over the lane's 16-lane row, in every lane of it (four row rotations).
+__device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
+    v = min(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x121, 0xf, 0xf, false)));  // row_ror:1
+    v = min(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x122, 0xf, 0xf, false)));  // row_ror:2
+    v = min(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x124, 0xf, 0xf, false)));  // row_ror:4
+    v = min(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, false)));  // row_ror:8
+    return v;
+}
+
+template <bool ABS, uint32_t LIST>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void blend_backward_kernel(BlendBackwardArgs a) {
+    constexpr uint32_t CHUNK = backward_chunk;
+    constexpr uint32_t NX = ABS ? 3u : 1u;                 // values after the first eight (w g_b; |dL/dmean2d|)
+    constexpr uint32_t n_values = NX + 8u;
+    constexpr uint32_t dummy = CHUNK;                      // staged Gaussian of opacity 0 after the chunk
+    // One record of VS floats (values 0..7, then the extras) per group and walk step: group g's step s at record
+    // g LIST + s, then one record never written (zero_rec, zeros) and padding that the second combine lane's
+    // reads of the extras' offsets reach past it. VS is odd: a wave step's 64 stores (four values of sixteen
+    // records) and a combine read (sixteen steps of one group, two values four apart) hit distinct banks.
+    constexpr uint32_t VS = n_values;
+    constexpr uint32_t zero_rec = backward_groups * LIST;
+    static_assert(LIST >= 1 && zero_rec < 256u && (VS & 1u), "record indices fit a byte");
+    __shared__ float4 s_stage[CHUNK + 1][3];               // (x, y, packed rect), exp2-scaled conic + opacity, colour
+    __shared__ uint32_t s_emit[CHUNK];
+    __shared__ uint8_t s_pos[backward_groups][CHUNK];      // per group and Gaussian: its record (g LIST + step) or zero_rec
+    __shared__ float s_part[(zero_rec + 1) * VS + 8];
 
     const uint32_t lane = threadIdx.x;
     const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
@@ -316,7 +340,7 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
     const uint32_t n_proc = min(n_total, a.tile_max[tile]);
-    for (uint32_t q = lane; q < n_part / 4; q += 64) s_part4[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (lane < VS) s_part[zero_rec * VS + lane] = 0.0f;
     if (lane < 3) s_stage[dummy][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
     // pixel state of the lane's three rows: upstream gradient and Ab = (colour still to come) . g - g_bg, the
@@ -359,54 +383,60 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
         }
     }
 
-    // where the lane stores its sums: value 4m + {0, 2, 1, 3}[k] of group i (m = 0..2, values past n_values none)
+    // where the lane stores its sums: value 4m + {0, 2, 1, 3}[k] of group i (m = 0, 1; the extras: 8 + the same),
+    // in the record of the walk step
     const uint32_t vk = (k & 1u) * 2u + (k >> 1);
-    float* const slot0 = s_part + vk * vstride + i * gstride;
+    float* const slot0 = s_part + i * LIST * VS + vk;
+    // the combine's lanes: Gaussian cj of the chunk, half ch (values 0..3 and the extras; values 4..7)
+    const uint32_t cj = lane & (CHUNK - 1u), ch = lane / CHUNK;
 
-    // The records of a batch's instances are gathered through a three-stage pipeline over the batches: while
-    // batch b is walked, the emission indices of batch b + 3, the primitive indices of batch b + 2 and the records
-    // of batch b + 1 are loaded, so no load is waited on in the batch that issues it. The loads are unconditional
-    // (indices clamped to the tile's last instance; lanes past BATCH repeat lane BATCH - 1), so the compiler places
+    // The records of a chunk's instances are gathered through a three-stage pipeline over the chunks: while
+    // chunk b is walked, the emission indices of chunk b + 3, the primitive indices of chunk b + 2 and the records
+    // of chunk b + 1 are loaded, so no load is waited on in the chunk that issues it. The loads are unconditional
+    // (indices clamped to the tile's last instance; lanes past CHUNK repeat lane CHUNK - 1), so the compiler places
     // each wait at the value's use.
-    const uint32_t gather_lane = min(lane, BATCH - 1u);
+    const uint32_t gather_lane = min(lane, CHUNK - 1u);
     const uint32_t last_inst = n_total > 0 ? n_total - 1u : 0u;
     const auto load_e = [&](uint32_t s) { return a.sorted_inst[range.x + min(s + gather_lane, last_inst)]; };
     const auto stage = [&](uint32_t s, const PrimRecord& rec, uint32_t e) {
-        if (lane < BATCH && s + lane < n_total) {
+        if (lane < CHUNK && s + lane < n_total) {
             s_stage[lane][0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
             s_stage[lane][1] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
             s_stage[lane][2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
             s_emit[lane] = e;
         }
     };
-    // The loads of a batch's top have their consumers a whole batch later (the staging at the end of the batch,
-    // the next batch's top), and no loaded value is copied between loop-carried registers (a copy would make the
+    // The loads of a chunk's top have their consumers a whole chunk later (the staging at the end of the chunk,
+    // the next chunk's top), and no loaded value is copied between loop-carried registers (a copy would make the
     // loop wait for the load).
-    uint32_t p_next = 0, e_next2 = 0;  // primitive indices of batch b + 1, emission indices of batch b + 2
+    uint32_t p_next = 0, e_next2 = 0;  // primitive indices of chunk b + 1, emission indices of chunk b + 2
     if (n_proc > 0) {
-        const uint32_t e0 = load_e(0), e1 = load_e(BATCH);
-        e_next2 = load_e(2 * BATCH);
+        const uint32_t e0 = load_e(0), e1 = load_e(CHUNK);
+        e_next2 = load_e(2 * CHUNK);
         const uint32_t p0 = a.inst_prim[e0];
         p_next = a.inst_prim[e1];
         const PrimRecord rec0 = a.records[p0];
         stage(0, rec0, e0);
     }
     const uint32_t gx0 = bx0 + 4u * (i & 3u), gy0 = by0 + ly0;  // the lane's group rectangle: 4 x 3 pixels
-    uint32_t covered = 0;
-    for (uint32_t start = 0; start < n_proc; start += BATCH) {
-        // advance the gather pipeline: records and emission indices of batch b + 1, primitive indices of b + 2,
+    for (uint32_t base = 0; base < n_proc; base += CHUNK) {
+        // advance the gather pipeline: records and emission indices of chunk b + 1, primitive indices of b + 2,
         // emission indices of b + 3
         const PrimRecord rec_n = a.records[p_next];
-        const uint32_t e_n = load_e(start + BATCH);
+        const uint32_t e_n = load_e(base + CHUNK);
         p_next = a.inst_prim[e_next2];
-        e_next2 = load_e(start + 3 * BATCH);
-        wave_lds_fence();  // the batch is staged
-        const uint32_t batch_n = min(BATCH, n_proc - start);
-        // cull: the four lanes of a group test a quarter of the batch each (lane row k: Gaussians kQ .. kQ + Q - 1)
-        // against the group's rectangle; a prefix sum over the four rows places every hit in the group's list, in
-        // Gaussian order
+        e_next2 = load_e(base + 3 * CHUNK);
+        wave_lds_fence();  // the chunk is staged
+        const uint32_t n_chunk = min(CHUNK, n_proc - base);
+        uint32_t last_rel[3];
+#pragma unroll
+        for (uint32_t r = 0; r < 3; r++) last_rel[r] = last[r] > base ? last[r] - base : 0u;
+
+        // cull: lane row k tests Gaussians 8k .. 8k + 7 against the group's rectangle; the group's mask (bit j:
+        // Gaussian j overlaps the group) then sits in all four of its lanes
+        uint32_t R;
         {
-            constexpr uint32_t Q = BATCH / 4;
+            constexpr uint32_t Q = CHUNK / 4;
             uint32_t hits = 0;
             uint2 rects[Q];
 #pragma unroll
@@ -416,43 +446,58 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
                 const uint32_t j = k * Q + t;
                 const uint2 rect = rects[t];
                 const uint32_t rx0 = rect.x & 0xffffu, rx1 = rect.x >> 16, ry0 = rect.y & 0xffffu, ry1 = rect.y >> 16;
-                const bool hit = j < batch_n && rx0 < gx0 + 4u && gx0 < rx1 && ry0 < gy0 + 3u && gy0 < ry1;
+                const bool hit = j < n_chunk && rx0 < gx0 + 4u && gx0 < rx1 && ry0 < gy0 + 3u && gy0 < ry1;
                 hits |= hit ? 1u << t : 0u;
             }
-            const uint32_t c = static_cast<uint32_t>(__popc(hits));
-            // inclusive prefix of c over the group's rows (lanes i, i + 16, i + 32, i + 48); every lane runs the
-            // permutes (a lane reading from a lane that does not take part gets nothing), the rows select after
-            const uint32_t up16 = static_cast<uint32_t>(__shfl_up(static_cast<int>(c), 16));
-            uint32_t incl = c + (k >= 1 ? up16 : 0u);
-            const uint32_t up32 = static_cast<uint32_t>(__shfl_up(static_cast<int>(incl), 32));
-            incl += k >= 2 ? up32 : 0u;
-            const uint32_t my_n = static_cast<uint32_t>(__shfl(static_cast<int>(incl), static_cast<int>(i + 48u)));
-            uint32_t pos = incl - c;
+            R = rows_or(hits << (Q * k));
+        }
+
+        for (uint32_t pos0 = 0;;) {
+            // the sub-batch: Gaussians pos0 .. cut - 1, cut the position of the first Gaussian that would be some
+            // group's (LIST + 1)-th hit (the chunk's end if there is none); every group then has at most LIST hits
+            const uint32_t tot = static_cast<uint32_t>(__popc(R));
+            const bool over = __ballot(tot > LIST) != 0;  // (wave-uniform)
+            uint32_t cut = CHUNK, n_steps = LIST;
+            if (over) {
+                uint32_t m = R;
 #pragma unroll
-            for (uint32_t t = 0; t < Q; t++) {
-                if ((hits >> t) & 1u) s_list[i][pos] = k * Q + t;
-                pos += (hits >> t) & 1u;
+                for (uint32_t n = 0; n < LIST; n++) m &= m - 1u;  // the group's hits after its first LIST
+                const uint32_t cand = tot > LIST ? static_cast<uint32_t>(__ffs(m) - 1) : CHUNK;
+                cut = __builtin_amdgcn_readfirstlane(row_min_u32(cand));  // rows hold the same values
+            } else {
+                n_steps = __builtin_amdgcn_readfirstlane(row_max_u32(tot));
+            }
+            const uint32_t sel = cut < 32u ? R & ((1u << cut) - 1u) : R;
+            R ^= sel;
+            // the combine's table: for this lane's eight Gaussians, the record the group stores them in, or zero_rec
+            {
+                constexpr uint32_t Q = CHUNK / 4;
+                const uint32_t own = (sel >> (Q * k)) & ((1u << Q) - 1u);
+                uint32_t rank = i * LIST + static_cast<uint32_t>(__popc(sel & ((1u << (Q * k)) - 1u)));
+#pragma unroll
+                for (uint32_t t = 0; t < Q; t++) {
+                    const bool b = (own >> t) & 1u;
+                    s_pos[i][Q * k + t] = static_cast<uint8_t>(b ? rank : zero_rec);
+                    rank += b ? 1u : 0u;
+                }
             }
             wave_lds_fence();
-            const uint32_t n_steps = __builtin_amdgcn_readfirstlane(row_max_u32(my_n));  // rows hold the same counts
-            uint32_t last_rel[3];
-#pragma unroll
-            for (uint32_t r = 0; r < 3; r++) last_rel[r] = last[r] > start ? last[r] - start : 0u;
 
-            // step s walks entry s of the group's list (the dummy past its count); the next step's Gaussian is
-            // read from LDS before the current one is evaluated (two register sets, the loop unrolled by two)
-            const uint32_t* const my_list = s_list[i];
-            const auto entry = [&](uint32_t s) {
-                const uint32_t e = my_list[s < BATCH ? s : BATCH - 1];  // past the count: stale, replaced by the dummy
-                return s < my_n ? e : dummy;
+            // step s walks the group's s-th hit (the dummy after the last); the next step's Gaussian is read from
+            // LDS before the current one is evaluated (two register sets, the loop unrolled by two)
+            uint32_t M = sel;
+            const auto next = [&]() {
+                const uint32_t j = min(static_cast<uint32_t>(__ffs(M) - 1), dummy);  // (__ffs(0) - 1: all ones)
+                M &= M - 1u;
+                return j;
             };
             // staged float4 c of Gaussian j, addressed in the LDS address space (32-bit offsets, 24-bit product)
             const auto at = [&](uint32_t j, uint32_t c) {
-                lds_char* base = (lds_char*)(&s_stage[0][0]);
-                const native_float4 v = *reinterpret_cast<lds_float4*>(base + __umul24(j, static_cast<uint32_t>(sizeof(s_stage[0]))) + 16u * c);
+                lds_char* sbase = (lds_char*)(&s_stage[0][0]);
+                const native_float4 v = *reinterpret_cast<lds_float4*>(sbase + __umul24(j, static_cast<uint32_t>(sizeof(s_stage[0]))) + 16u * c);
                 return make_float4(v.x, v.y, v.z, v.w);
             };
-            const auto walk = [&](uint32_t j, float4 xy, float4 co, float4 col) {
+            const auto walk = [&](uint32_t j, uint32_t s, float4 xy, float4 co, float4 col) {
                 float dx, sh, shdy, shdyy, swr, swg, swb, e1 = 0.0f, e2 = 0.0f;
                 const float4 craw = ABS ? raw_conic_of(co) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
@@ -492,78 +537,73 @@ __global__ __launch_bounds__(64) void blend_backward_kernel(BlendBackwardArgs a)
                     T[r] = T[r] * oma;
                 }
                 const float shdx = dx * sh;
-                slot0[j] = rows_reduce4(shdx, shdy, dx * shdx, dx * shdy);       // h dx, h dy, h dx^2, h dx dy
-                slot0[4u * vstride + j] = rows_reduce4(shdyy, sh, swr, swg);      // h dy^2, h, w g_r, w g_g
+                float* const sw = slot0 + s * VS;
+                sw[0] = rows_reduce4(shdx, shdy, dx * shdx, dx * shdy);           // h dx, h dy, h dx^2, h dx dy
+                sw[4] = rows_reduce4(shdyy, sh, swr, swg);                         // h dy^2, h, w g_r, w g_g
                 if (ABS) {
-                    const float x2 = rows_reduce4(swb, e1, e2, 0.0f);             // w g_b, |.|_x, |.|_y
-                    if (vk < 3u) slot0[8u * vstride + j] = x2;
+                    const float x2 = rows_reduce4(swb, e1, e2, 0.0f);              // w g_b, |.|_x, |.|_y
+                    if (vk < 3u) sw[8] = x2;
                 } else {
-                    const float x2 = rows_reduce1(swb);                           // w g_b
-                    if (k == 0u) slot0[8u * vstride + j] = x2;
+                    const float x2 = rows_reduce1(swb);                            // w g_b
+                    if (k == 0u) sw[8] = x2;
                 }
             };
-            // list entries are read two steps ahead, the staged Gaussians one step ahead
-            uint32_t ja = entry(0), jb = entry(1);
-            float4 xya = at(ja, 0), coa = at(ja, 1), cola = at(ja, 2);
-            for (uint32_t s = 0; s < n_steps; s += 2) {
-                const float4 xyb = at(jb, 0), cob = at(jb, 1), colb = at(jb, 2);
-                const uint32_t jc = entry(s + 2);
-                walk(ja, xya, coa, cola);
-                if (s + 1 >= n_steps) break;
-                xya = at(jc, 0);
-                coa = at(jc, 1);
-                cola = at(jc, 2);
-                const uint32_t jd = entry(s + 3);
-                walk(jb, xyb, cob, colb);
-                ja = jc;
-                jb = jd;
-            }
-        }
-        wave_lds_fence();  // every group's sums are in its slots
-        // combine: item (value v, Gaussian j), spread over all 64 lanes, adds the sixteen group slots in group order
-        // into s_sum; then lane (Gaussian j, quarter q) writes 16 bytes of the instance's 48-byte record (q = 3 has
-        // nothing to do). Every staged instance gets its record: those after the tile's last contributor, which no
-        // group walked, get zeros.
-        const uint32_t batch_staged = min(BATCH, n_total - start);
-        for (uint32_t item = lane; item < n_values * BATCH; item += 64) {
-            const uint32_t v = item / BATCH, jj = item % BATCH;
-            const float* src = s_part + v * vstride + jj;
-            float acc = 0.0f;
-#pragma unroll
-            for (uint32_t g = 0; g < backward_groups; g++) acc += src[g * gstride];
-            s_sum[item] = acc;
-        }
-        wave_lds_fence();
-        if (lane < 3u * BATCH) {
-            const uint32_t jj = lane % BATCH, q = lane / BATCH;
-            if (jj < batch_staged) {
-                float r[4];
-#pragma unroll
-                for (uint32_t c = 0; c < 4; c++) {
-                    const uint32_t v = 4u * q + c;
-                    r[c] = v < n_values ? s_sum[min(v, n_values - 1u) * BATCH + jj] : 0.0f;
+            {
+                uint32_t ja = next();
+                float4 xya = at(ja, 0), coa = at(ja, 1), cola = at(ja, 2);
+                for (uint32_t s = 0; s < n_steps; s += 2) {
+                    const uint32_t jb = next();
+                    const float4 xyb = at(jb, 0), cob = at(jb, 1), colb = at(jb, 2);
+                    walk(ja, s, xya, coa, cola);
+                    if (s + 1 >= n_steps) break;
+                    ja = next();
+                    xya = at(ja, 0);
+                    coa = at(ja, 1);
+                    cola = at(ja, 2);
+                    walk(jb, s + 1, xyb, cob, colb);
                 }
-                const float4 co = s_stage[jj][1];
-                const float4 craw = raw_conic_of(co);
-                // q = 0: dL/dmean2d = C (sum h d), 0.5 (sum h dx^2, sum h dx dy); q = 1: 0.5 sum h dy^2, sum G dL/dalpha =
-                // -(sum of h) / o, colour r, g; q = 2: colour b, |dL/dmean2d| (x, y), 0
-                float4 o;
-                if (q == 0u)
-                    o = make_float4(__builtin_fmaf(craw.x, r[0], craw.y * r[1]), __builtin_fmaf(craw.y, r[0], craw.z * r[1]), 0.5f * r[2], 0.5f * r[3]);
-                else if (q == 1u)
-                    o = make_float4(0.5f * r[0], -r[1] * __builtin_amdgcn_rcpf(co.w), r[2], r[3]);
-                else
-                    o = make_float4(r[0], r[1], r[2], r[3]);
-                reinterpret_cast<float4*>(a.inst_grads)[3 * static_cast<size_t>(s_emit[jj]) + q] = o;
             }
+            wave_lds_fence();  // every group's sums are in its slots
+
+            // combine: the two lanes of Gaussian cj (of this sub-batch) add its sixteen group slots in group order
+            // (values 0..3 and the extras, resp. values 4..7: the second lane reads four floats on, and its reads
+            // of the extras' offsets land in the next record, unused) and write the instance's 48-byte record:
+            // dL/dmean2d = C (sum h d), 0.5 (sum h dx^2, sum h dx dy); 0.5 sum h dy^2, sum G dL/dalpha = -(sum of
+            // h) / o, colour r, g; colour b, |dL/dmean2d| (x, y), 0. Gaussians that no group walked get zeros.
+            const uint32_t cend = over ? cut : n_chunk;
+            if (cj >= pos0 && cj < cend) {
+                const float* const cb = s_part + ch * 4u;
+                float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ax[NX];
+#pragma unroll
+                for (uint32_t x = 0; x < NX; x++) ax[x] = 0.0f;
+#pragma unroll
+                for (uint32_t g = 0; g < backward_groups; g++) {
+                    const float* const b = cb + s_pos[g][cj] * VS;
+#pragma unroll
+                    for (uint32_t c = 0; c < 4; c++) acc[c] += b[c];
+#pragma unroll
+                    for (uint32_t x = 0; x < NX; x++) ax[x] += b[8 + x];
+                }
+                const float4 co = s_stage[cj][1];
+                float4* const out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(s_emit[cj]);
+                if (ch == 0u) {
+                    const float4 craw = raw_conic_of(co);
+                    out[0] = make_float4(__builtin_fmaf(craw.x, acc[0], craw.y * acc[1]), __builtin_fmaf(craw.y, acc[0], craw.z * acc[1]),
+                                         0.5f * acc[2], 0.5f * acc[3]);
+                    out[2] = make_float4(ax[0], ABS ? ax[NX > 1 ? 1 : 0] : 0.0f, ABS ? ax[NX > 2 ? 2 : 0] : 0.0f, 0.0f);
+                } else {
+                    out[1] = make_float4(0.5f * acc[0], -acc[1] * __builtin_amdgcn_rcpf(co.w), acc[2], acc[3]);
+                }
+            }
+            if (!over) break;
+            pos0 = cend;
+            wave_lds_fence();  // the combine has read the table before the next sub-batch rewrites it
         }
-        covered = min(n_total, start + BATCH);
-        wave_lds_fence();  // the combine has read the slots and the stage
-        for (uint32_t q = lane; q < n_part / 4; q += 64) s_part4[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (start + BATCH < n_proc) stage(start + BATCH, rec_n, e_n);  // the next batch
+        wave_lds_fence();  // the combine has read the stage
+        if (base + CHUNK < n_proc) stage(base + CHUNK, rec_n, e_n);  // the next chunk
     }
     // instances the tile never reached (after every pixel's last contributor) get zero records
-    for (uint32_t q = covered + lane; q < n_total; q += 64) {
+    for (uint32_t q = n_proc + lane; q < n_total; q += 64) {
         const uint32_t e = a.sorted_inst[range.x + q];
         float4* out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(e);
         const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -726,9 +766,9 @@ bool launch_pruning_scores(const BlendBackwardArgs& a, const uint32_t* n_touched
 bool launch_blend_backward(const BlendBackwardArgs& a, hipStream_t s) {
     if (a.n_tiles == 0) return true;
     if (a.abs_grads)
-        blend_backward_kernel<true, blend_backward_batch><<<a.n_tiles, 64, 0, s>>>(a);
+        blend_backward_kernel<true, backward_list><<<a.n_tiles, 64, 0, s>>>(a);
     else
-        blend_backward_kernel<false, blend_backward_batch><<<a.n_tiles, 64, 0, s>>>(a);
+        blend_backward_kernel<false, backward_list><<<a.n_tiles, 64, 0, s>>>(a);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
