@@ -283,14 +283,16 @@ __device__ __forceinline__ float rows_reduce1(float v) {
 // the group did not walk it) and write the 48-byte record at the instance's emission slot. A single wave needs
 // no block barrier: LDS accesses of a wave complete in order, and a wavefront fence keeps the compiler from
 // reordering them around the table and slot exchanges. No atomics: the result is run-to-run deterministic.
-// LIST trades walk steps against LDS (the slots take (8 + extra) x 16 x LIST floats; at most about 10 KB per
-// wave keeps four waves per SIMD). Against fixed batches of 12 Gaussians per walk (each group's list padded to
-// the batch's longest), the sub-batches take 16 % fewer wave steps and half as many combines on the 1M-Gaussian
-// 1080p scene.
+// LIST trades walk steps against LDS (the records take (8 + extra) x 16 x LIST floats; at most 10 KB per wave
+// keeps four waves per SIMD: LIST 14, or 11 with the three extra values of ABS). Against fixed batches of 12
+// Gaussians per walk (each group's list padded to the batch's longest), sub-batches of LIST 14 take 17 % fewer
+// wave steps and 44 % as many combines on the 1M-Gaussian 1080p scene; LIST 12 / 13 / 14 measured 148.6 / 146.4 /
+// 145.2 us there (fixed batches: 176 us).
 #ifndef EFGS_BACKWARD_LIST
-#define EFGS_BACKWARD_LIST 12
+#define EFGS_BACKWARD_LIST 14
 #endif
 constexpr uint32_t backward_list = EFGS_BACKWARD_LIST;
+constexpr uint32_t backward_list_abs = EFGS_BACKWARD_LIST < 11 ? EFGS_BACKWARD_LIST : 11;
 constexpr uint32_t backward_groups = 16;
 constexpr uint32_t backward_chunk = 32;
 
@@ -324,10 +326,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void bl
     constexpr uint32_t VS = n_values;
     constexpr uint32_t zero_rec = backward_groups * LIST;
     static_assert(LIST >= 1 && zero_rec < 256u && (VS & 1u), "record indices fit a byte");
-    __shared__ float4 s_stage[CHUNK + 1][3];               // (x, y, packed rect), exp2-scaled conic + opacity, colour
-    __shared__ uint32_t s_emit[CHUNK];
-    __shared__ uint8_t s_pos[backward_groups][CHUNK];      // per group and Gaussian: its record (g LIST + step) or zero_rec
-    __shared__ float s_part[(zero_rec + 1) * VS + 8];
+    // (x, y, packed rect), exp2-scaled conic + opacity, colour + the instance's emission index (bits)
+    __shared__ float4 s_stage[CHUNK + 1][3];
+    __shared__ __align__(8) uint8_t s_pos[backward_groups][CHUNK];  // per group and Gaussian: its record (g LIST + step) or zero_rec
+    __shared__ float s_part[(zero_rec + 1) * VS + 4];
 
     const uint32_t lane = threadIdx.x;
     const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
@@ -389,6 +391,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void bl
     float* const slot0 = s_part + i * LIST * VS + vk;
     // the combine's lanes: Gaussian cj of the chunk, half ch (values 0..3 and the extras; values 4..7)
     const uint32_t cj = lane & (CHUNK - 1u), ch = lane / CHUNK;
+    const uint32_t below8k = (1u << (8u * k)) - 1u;  // the chunk's Gaussians before the lane's eight
 
     // The records of a chunk's instances are gathered through a three-stage pipeline over the chunks: while
     // chunk b is walked, the emission indices of chunk b + 3, the primitive indices of chunk b + 2 and the records
@@ -402,8 +405,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void bl
         if (lane < CHUNK && s + lane < n_total) {
             s_stage[lane][0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
             s_stage[lane][1] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
-            s_stage[lane][2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
-            s_emit[lane] = e;
+            s_stage[lane][2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, __uint_as_float(e));
         }
     };
     // The loads of a chunk's top have their consumers a whole chunk later (the staging at the end of the chunk,
@@ -443,13 +445,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void bl
             for (uint32_t t = 0; t < Q; t++) rects[t] = rect_of(s_stage[k * Q + t][0]);  // (all reads in flight at once)
 #pragma unroll
             for (uint32_t t = 0; t < Q; t++) {
-                const uint32_t j = k * Q + t;
                 const uint2 rect = rects[t];
                 const uint32_t rx0 = rect.x & 0xffffu, rx1 = rect.x >> 16, ry0 = rect.y & 0xffffu, ry1 = rect.y >> 16;
-                const bool hit = j < n_chunk && rx0 < gx0 + 4u && gx0 < rx1 && ry0 < gy0 + 3u && gy0 < ry1;
+                const bool hit = (rx0 < gx0 + 4u) & (gx0 < rx1) & (ry0 < gy0 + 3u) & (gy0 < ry1);
                 hits |= hit ? 1u << t : 0u;
             }
-            R = rows_or(hits << (Q * k));
+            // (Gaussians past the chunk's count hold stale rectangles: masked off)
+            const uint32_t n_own = n_chunk > Q * k ? min(n_chunk - Q * k, Q) : 0u;
+            R = rows_or((hits & ((1u << n_own) - 1u)) << (Q * k));
         }
 
         for (uint32_t pos0 = 0;;) {
@@ -469,17 +472,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void bl
             }
             const uint32_t sel = cut < 32u ? R & ((1u << cut) - 1u) : R;
             R ^= sel;
-            // the combine's table: for this lane's eight Gaussians, the record the group stores them in, or zero_rec
+            // the combine's table: for this lane's eight Gaussians, the record the group stores them in, or zero_rec.
+            // Per four Gaussians: their bits spread to bytes (b0 + b1 2^8 + ...: one 24-bit product), the bits
+            // below each byte (another product, shifted by a byte), plus the first record in every byte, and a
+            // byte select against zero_rec.
             {
                 constexpr uint32_t Q = CHUNK / 4;
-                const uint32_t own = (sel >> (Q * k)) & ((1u << Q) - 1u);
-                uint32_t rank = i * LIST + static_cast<uint32_t>(__popc(sel & ((1u << (Q * k)) - 1u)));
-#pragma unroll
-                for (uint32_t t = 0; t < Q; t++) {
-                    const bool b = (own >> t) & 1u;
-                    s_pos[i][Q * k + t] = static_cast<uint8_t>(b ? rank : zero_rec);
-                    rank += b ? 1u : 0u;
-                }
+                const uint32_t own = (sel >> (Q * k)) & 0xffu;
+                const uint32_t r0 = static_cast<uint32_t>(__popc(sel & below8k)) + i * LIST;  // the first hit's record
+                const uint32_t lo = own & 15u, hi = own >> 4;
+                const uint32_t bl = __umul24(lo, 0x00204081u) & 0x01010101u, bh = __umul24(hi, 0x00204081u) & 0x01010101u;
+                const uint32_t rl = (__umul24(bl, 0x010101u) << 8) + __builtin_amdgcn_perm(0u, r0, 0u);
+                const uint32_t rh = (__umul24(bh, 0x010101u) << 8) + __builtin_amdgcn_perm(0u, r0 + static_cast<uint32_t>(__popc(lo)), 0u);
+                const uint32_t ml = (bl << 8) - bl, mh = (bh << 8) - bh;  // 0xff in the bytes of hits
+                constexpr uint32_t zb = zero_rec * 0x01010101u;
+                *reinterpret_cast<uint2*>(&s_pos[i][Q * k]) = make_uint2((rl & ml) | (zb & ~ml), (rh & mh) | (zb & ~mh));
             }
             wave_lds_fence();
 
@@ -585,7 +592,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void bl
                     for (uint32_t x = 0; x < NX; x++) ax[x] += b[8 + x];
                 }
                 const float4 co = s_stage[cj][1];
-                float4* const out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(s_emit[cj]);
+                float4* const out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(__float_as_uint(s_stage[cj][2].w));
                 if (ch == 0u) {
                     const float4 craw = raw_conic_of(co);
                     out[0] = make_float4(__builtin_fmaf(craw.x, acc[0], craw.y * acc[1]), __builtin_fmaf(craw.y, acc[0], craw.z * acc[1]),
@@ -766,7 +773,7 @@ bool launch_pruning_scores(const BlendBackwardArgs& a, const uint32_t* n_touched
 bool launch_blend_backward(const BlendBackwardArgs& a, hipStream_t s) {
     if (a.n_tiles == 0) return true;
     if (a.abs_grads)
-        blend_backward_kernel<true, backward_list><<<a.n_tiles, 64, 0, s>>>(a);
+        blend_backward_kernel<true, backward_list_abs><<<a.n_tiles, 64, 0, s>>>(a);
     else
         blend_backward_kernel<false, backward_list><<<a.n_tiles, 64, 0, s>>>(a);
     EFGS_HIP_CHECK(hipGetLastError());
