@@ -28,8 +28,12 @@ namespace {
 constexpr float log2e = 1.44269504089f;
 
 typedef float native_float4 __attribute__((ext_vector_type(4)));
+typedef float native_float3 __attribute__((ext_vector_type(3)));
+typedef float native_float2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(3))) char lds_char;
 typedef const __attribute__((address_space(3))) native_float4 lds_float4;
+typedef const __attribute__((address_space(3))) native_float3 lds_float3;
+typedef const __attribute__((address_space(3))) native_float2 lds_float2;
 
 struct Staged {
     float2 xy;
@@ -498,10 +502,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void bl
                 M &= M - 1u;
                 return j;
             };
-            // staged float4 c of Gaussian j, addressed in the LDS address space (32-bit offsets, 24-bit product)
+            // the staged float4 c of Gaussian j, addressed in the LDS address space (32-bit offsets, 24-bit product),
+            // read only as far as the walk uses it: (x, y), the conic and opacity, the colour. (An unused component
+            // read along would be a register the compiler reuses at once, waiting for the read to land.)
             const auto at = [&](uint32_t j, uint32_t c) {
-                lds_char* sbase = (lds_char*)(&s_stage[0][0]);
-                const native_float4 v = *reinterpret_cast<lds_float4*>(sbase + __umul24(j, static_cast<uint32_t>(sizeof(s_stage[0]))) + 16u * c);
+                lds_char* const p = (lds_char*)(&s_stage[0][0]) + __umul24(j, static_cast<uint32_t>(sizeof(s_stage[0]))) + 16u * c;
+                if (c == 0) {
+                    const native_float2 v = *reinterpret_cast<lds_float2*>(p);
+                    return make_float4(v.x, v.y, 0.0f, 0.0f);
+                }
+                if (c == 2) {
+                    const native_float3 v = *reinterpret_cast<lds_float3*>(p);
+                    return make_float4(v.x, v.y, v.z, 0.0f);
+                }
+                const native_float4 v = *reinterpret_cast<lds_float4*>(p);
                 return make_float4(v.x, v.y, v.z, v.w);
             };
             const auto walk = [&](uint32_t j, uint32_t s, float4 xy, float4 co, float4 col) {
