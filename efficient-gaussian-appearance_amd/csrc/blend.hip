@@ -295,6 +295,9 @@ __device__ __forceinline__ float rows_reduce1(float v) {
 #ifndef EFGS_BACKWARD_LIST
 #define EFGS_BACKWARD_LIST 14
 #endif
+#ifndef EFGS_BACKWARD_WAVES
+#define EFGS_BACKWARD_WAVES 4
+#endif
 constexpr uint32_t backward_list = EFGS_BACKWARD_LIST;
 constexpr uint32_t backward_list_abs = EFGS_BACKWARD_LIST < 11 ? EFGS_BACKWARD_LIST : 11;
 constexpr uint32_t backward_groups = 16;
@@ -318,7 +321,7 @@ __device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
 }
 
 template <bool ABS, uint32_t LIST>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void blend_backward_kernel(BlendBackwardArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWARD_WAVES))) void blend_backward_kernel(BlendBackwardArgs a) {
     constexpr uint32_t CHUNK = backward_chunk;
     constexpr uint32_t NX = ABS ? 3u : 1u;                 // values after the first eight (w g_b; |dL/dmean2d|)
     constexpr uint32_t n_values = NX + 8u;
@@ -605,16 +608,22 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void bl
 #pragma unroll
                     for (uint32_t x = 0; x < NX; x++) ax[x] += b[8 + x];
                 }
+                // (the extras' sums are formed here in both halves, with the reads of the group loop: otherwise the
+                // compiler moves their reads into the first half's branch, recomputing every address)
+#pragma unroll
+                for (uint32_t x = 0; x < NX; x++) asm volatile("" : "+v"(ax[x]));
                 const float4 co = s_stage[cj][1];
-                float4* const out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(__float_as_uint(s_stage[cj][2].w));
-                if (ch == 0u) {
-                    const float4 craw = raw_conic_of(co);
-                    out[0] = make_float4(__builtin_fmaf(craw.x, acc[0], craw.y * acc[1]), __builtin_fmaf(craw.y, acc[0], craw.z * acc[1]),
-                                         0.5f * acc[2], 0.5f * acc[3]);
-                    out[2] = make_float4(ax[0], ABS ? ax[NX > 1 ? 1 : 0] : 0.0f, ABS ? ax[NX > 2 ? 2 : 0] : 0.0f, 0.0f);
-                } else {
-                    out[1] = make_float4(0.5f * acc[0], -acc[1] * __builtin_amdgcn_rcpf(co.w), acc[2], acc[3]);
-                }
+                // the record's 48 bytes at the instance's emission slot: a 32-bit byte offset from the array
+                float4* const out = reinterpret_cast<float4*>(reinterpret_cast<char*>(a.inst_grads) + 48u * __float_as_uint(s_stage[cj][2].w));
+                // first half: quarter 0 (and quarter 2 below), second half: quarter 1, formed by selects so that
+                // both halves run one store path
+                const float4 craw = raw_conic_of(co);
+                const float q1y = -acc[1] * __builtin_amdgcn_rcpf(co.w);
+                const bool first = ch == 0u;
+                out[ch] = make_float4(first ? __builtin_fmaf(craw.x, acc[0], craw.y * acc[1]) : 0.5f * acc[0],
+                                      first ? __builtin_fmaf(craw.y, acc[0], craw.z * acc[1]) : q1y, first ? 0.5f * acc[2] : acc[2],
+                                      first ? 0.5f * acc[3] : acc[3]);
+                if (first) out[2] = make_float4(ax[0], ABS ? ax[NX > 1 ? 1 : 0] : 0.0f, ABS ? ax[NX > 2 ? 2 : 0] : 0.0f, 0.0f);
             }
             if (!over) break;
             pos0 = cend;
