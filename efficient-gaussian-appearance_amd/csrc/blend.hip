@@ -257,6 +257,13 @@ __device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
     return v;
 }
 
+// Two values summed over the four lane rows: rows 0 and 1 of the result hold the sum of a, rows 2 and 3 that of b
+// (each sum in the order of rows_reduce1).
+__device__ __forceinline__ float rows_reduce2(float a, float b) {
+    const float w = swap32_add(a, b);
+    return swap16_add(w, w);
+}
+
 // The sum of one value over the four lane rows, in every row.
 __device__ __forceinline__ float rows_reduce1(float v) {
     const float w = swap32_add(v, v);
@@ -325,7 +332,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
     constexpr uint32_t CHUNK = backward_chunk;
     constexpr uint32_t NX = ABS ? 3u : 1u;                 // values after the first eight (w g_b; |dL/dmean2d|)
     constexpr uint32_t n_values = NX + 8u;
-    constexpr uint32_t dummy = CHUNK;                      // staged Gaussian of opacity 0 after the chunk
     // One record of VS floats (values 0..7, then the extras) per group and walk step: group g's step s at record
     // g LIST + s, then one record never written (zero_rec, zeros) and padding that the second combine lane's
     // reads of the extras' offsets reach past it. VS is odd: a wave step's 64 stores (four values of sixteen
@@ -333,7 +339,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
     constexpr uint32_t VS = n_values;
     constexpr uint32_t zero_rec = backward_groups * LIST;
     static_assert(LIST >= 1 && zero_rec < 256u && (VS & 1u), "record indices fit a byte");
-    // (x, y, packed rect), exp2-scaled conic + opacity, colour + the instance's emission index (bits)
+    // (x, y, packed rect), exp2-scaled conic + opacity, colour + the instance's emission index (bits): Gaussian j
+    // of the chunk at entry j + 1, entry 0 a Gaussian of opacity 0 that a group walks past its hits
     __shared__ float4 s_stage[CHUNK + 1][3];
     __shared__ __align__(8) uint8_t s_pos[backward_groups][CHUNK];  // per group and Gaussian: its record (g LIST + step) or zero_rec
     __shared__ float s_part[(zero_rec + 1) * VS + 4];
@@ -350,7 +357,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
     const uint32_t n_total = range.y - range.x;
     const uint32_t n_proc = min(n_total, a.tile_max[tile]);
     if (lane < VS) s_part[zero_rec * VS + lane] = 0.0f;
-    if (lane < 3) s_stage[dummy][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (lane < 3) s_stage[0][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
     // pixel state of the lane's three rows: upstream gradient and Ab = (colour still to come) . g - g_bg, the
     // background term g_bg = -T_final (bg . g) folded in. The loads are unconditional (clamped to the image) so
@@ -410,9 +417,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
     const auto load_e = [&](uint32_t s) { return a.sorted_inst[range.x + min(s + gather_lane, last_inst)]; };
     const auto stage = [&](uint32_t s, const PrimRecord& rec, uint32_t e) {
         if (lane < CHUNK && s + lane < n_total) {
-            s_stage[lane][0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
-            s_stage[lane][1] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
-            s_stage[lane][2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, __uint_as_float(e));
+            s_stage[lane + 1][0] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
+            s_stage[lane + 1][1] = scale_conic_for_exp2(rec.r0.z, rec.r0.w, rec.r1.x, rec.r1.y);
+            s_stage[lane + 1][2] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, __uint_as_float(e));
         }
     };
     // The loads of a chunk's top have their consumers a whole chunk later (the staging at the end of the chunk,
@@ -449,7 +456,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
             uint32_t hits = 0;
             uint2 rects[Q];
 #pragma unroll
-            for (uint32_t t = 0; t < Q; t++) rects[t] = rect_of(s_stage[k * Q + t][0]);  // (all reads in flight at once)
+            for (uint32_t t = 0; t < Q; t++) rects[t] = rect_of(s_stage[k * Q + t + 1][0]);  // (all reads in flight at once)
 #pragma unroll
             for (uint32_t t = 0; t < Q; t++) {
                 const uint2 rect = rects[t];
@@ -497,11 +504,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
             }
             wave_lds_fence();
 
-            // step s walks the group's s-th hit (the dummy after the last); the next step's Gaussian is read from
-            // LDS before the current one is evaluated (two register sets, the loop unrolled by two)
+            // step s walks the group's s-th hit (after the last: j = all ones, staged entry 0, which also fails every
+            // j < last test); the next step's Gaussian is read from LDS before the current one is evaluated (two
+            // register sets, the loop unrolled by two)
             uint32_t M = sel;
             const auto next = [&]() {
-                const uint32_t j = min(static_cast<uint32_t>(__ffs(M) - 1), dummy);  // (__ffs(0) - 1: all ones)
+                uint32_t j;
+                asm("v_ffbl_b32 %0, %1" : "=v"(j) : "v"(M));  // lowest set bit, all ones for 0 (no select around it)
                 M &= M - 1u;
                 return j;
             };
@@ -509,7 +518,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
             // read only as far as the walk uses it: (x, y), the conic and opacity, the colour. (An unused component
             // read along would be a register the compiler reuses at once, waiting for the read to land.)
             const auto at = [&](uint32_t j, uint32_t c) {
-                lds_char* const p = (lds_char*)(&s_stage[0][0]) + __umul24(j, static_cast<uint32_t>(sizeof(s_stage[0]))) + 16u * c;
+                lds_char* const p = (lds_char*)(&s_stage[0][0]) + __umul24(j + 1u, static_cast<uint32_t>(sizeof(s_stage[0]))) + 16u * c;
                 if (c == 0) {
                     const native_float2 v = *reinterpret_cast<lds_float2*>(p);
                     return make_float4(v.x, v.y, 0.0f, 0.0f);
@@ -521,8 +530,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
                 const native_float4 v = *reinterpret_cast<lds_float4*>(p);
                 return make_float4(v.x, v.y, v.z, v.w);
             };
-            const auto walk = [&](uint32_t j, uint32_t s, float4 xy, float4 co, float4 col) {
-                float dx, sh, shdy, shdyy, swr, swg, swb, e1 = 0.0f, e2 = 0.0f;
+            // (without ABS the step's w g_b sum is returned in swb and reduced with the next step's)
+            const auto walk = [&](uint32_t j, uint32_t s, float4 xy, float4 co, float4 col, float& swb) {
+                float dx, sh, shdy, shdyy, swr, swg, e1 = 0.0f, e2 = 0.0f;
                 const float4 craw = ABS ? raw_conic_of(co) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
                 for (uint32_t r = 0; r < 3; r++) {
@@ -567,24 +577,36 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
                 if (ABS) {
                     const float x2 = rows_reduce4(swb, e1, e2, 0.0f);              // w g_b, |.|_x, |.|_y
                     if (vk < 3u) sw[8] = x2;
-                } else {
-                    const float x2 = rows_reduce1(swb);                            // w g_b
-                    if (k == 0u) sw[8] = x2;
                 }
             };
             {
+                // w g_b of a pair of steps in one reduction: rows 0 and 2 store the first and the second step's sum
+                // (row 2's lanes have vk = 1: their value-8 slot of the next record is VS + 7 floats on)
+                float* const b8 = slot0 + (k == 2u ? VS + 7u : 8u);
+                const bool store8 = (k & 1u) == 0u;
                 uint32_t ja = next();
                 float4 xya = at(ja, 0), coa = at(ja, 1), cola = at(ja, 2);
                 for (uint32_t s = 0; s < n_steps; s += 2) {
                     const uint32_t jb = next();
                     const float4 xyb = at(jb, 0), cob = at(jb, 1), colb = at(jb, 2);
-                    walk(ja, s, xya, coa, cola);
-                    if (s + 1 >= n_steps) break;
+                    float swb_a, swb_b;
+                    walk(ja, s, xya, coa, cola, swb_a);
+                    if (s + 1 >= n_steps) {
+                        if (!ABS) {
+                            const float x = rows_reduce1(swb_a);
+                            if (k == 0u) slot0[s * VS + 8u] = x;
+                        }
+                        break;
+                    }
                     ja = next();
                     xya = at(ja, 0);
                     coa = at(ja, 1);
                     cola = at(ja, 2);
-                    walk(jb, s + 1, xyb, cob, colb);
+                    walk(jb, s + 1, xyb, cob, colb, swb_b);
+                    if (!ABS) {
+                        const float x = rows_reduce2(swb_a, swb_b);
+                        if (store8) b8[s * VS] = x;
+                    }
                 }
             }
             wave_lds_fence();  // every group's sums are in its slots
@@ -612,9 +634,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
                 // compiler moves their reads into the first half's branch, recomputing every address)
 #pragma unroll
                 for (uint32_t x = 0; x < NX; x++) asm volatile("" : "+v"(ax[x]));
-                const float4 co = s_stage[cj][1];
+                const float4 co = s_stage[cj + 1][1];
                 // the record's 48 bytes at the instance's emission slot: a 32-bit byte offset from the array
-                float4* const out = reinterpret_cast<float4*>(reinterpret_cast<char*>(a.inst_grads) + 48u * __float_as_uint(s_stage[cj][2].w));
+                float4* const out = reinterpret_cast<float4*>(reinterpret_cast<char*>(a.inst_grads) + 48u * __float_as_uint(s_stage[cj + 1][2].w));
                 // first half: quarter 0 (and quarter 2 below), second half: quarter 1, formed by selects so that
                 // both halves run one store path
                 const float4 craw = raw_conic_of(co);
