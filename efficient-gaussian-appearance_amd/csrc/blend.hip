@@ -84,13 +84,29 @@ __device__ __forceinline__ uint32_t pick_group(uint32_t g, uint32_t j0, uint32_t
 // (base + lane) << shift for the Gaussian, a batch index or, shifted, a byte offset into 16-byte staged arrays);
 // n[k] = popcount(m[k]). A group then walks its list with one LDS read per step instead of scanning a 64-bit
 // mask per lane.
-__device__ __forceinline__ void build_group_lists(const uint64_t (&m)[4], uint32_t lane, uint32_t base, uint32_t* list,
-                                                  uint32_t list_len, uint32_t (&n)[4], uint32_t shift = 0) {
+template <uint32_t N>
+__device__ __forceinline__ void build_group_lists(const uint64_t (&m)[N], uint32_t lane, uint32_t base, uint32_t* list,
+                                                  uint32_t list_len, uint32_t (&n)[N], uint32_t shift = 0) {
 #pragma unroll
-    for (uint32_t k = 0; k < 4; k++) {
+    for (uint32_t k = 0; k < N; k++) {
         const uint32_t lo = static_cast<uint32_t>(m[k]), hi = static_cast<uint32_t>(m[k] >> 32);
         if ((m[k] >> lane) & 1u) list[k * list_len + __builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u))] = (base + lane) << shift;
         n[k] = static_cast<uint32_t>(__popcll(m[k]));
+    }
+}
+
+// Culls lane's Gaussian against the eight 4x2 groups of the 16x4 band whose pixel columns start at bx0 and rows at
+// by0: m[4h + g] receives the wave's ballot for columns 4g .. 4g + 3, band rows 2h and 2h + 1.
+__device__ __forceinline__ void cull_groups8(uint2 rect, bool in, uint32_t bx0, uint32_t by0, uint64_t (&m)[8]) {
+    const uint32_t rx0 = rect.x & 0xffffu, rx1 = rect.x >> 16, ry0 = rect.y & 0xffffu, ry1 = rect.y >> 16;
+#pragma unroll
+    for (uint32_t h = 0; h < 2; h++) {
+        const bool yov = in && ry0 < by0 + 2u * h + 2u && by0 + 2u * h < ry1;
+#pragma unroll
+        for (uint32_t g = 0; g < 4; g++) {
+            const uint32_t gx0 = bx0 + 4u * g;
+            m[4 * h + g] = __ballot(yov && rx0 < gx0 + 4u && gx0 < rx1);
+        }
     }
 }
 
@@ -100,34 +116,41 @@ __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOM
 __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForwardArgs a) {
     if (a.overflow && *a.overflow != 0) return;  // the binning was skipped: the host re-runs the frame
     constexpr uint32_t list_len = 64;
-    // (x, y, packed pixel rectangle): the 16-byte stride of s_co and s_col, so the pair loads share one address
-    __shared__ float4 s_xy[tile_pixels];
-    __shared__ float4 s_co[tile_pixels];
-    __shared__ float4 s_col[tile_pixels];
-    __shared__ uint32_t s_list[tile_pixels / 64][4][list_len];  // per wave and group: batch indices to walk
+    constexpr uint32_t n_groups = 8;                        // 4x2 pixel groups per wave
+    constexpr uint32_t dummy_off = tile_pixels * 16u;       // byte offset of the staged Gaussian of opacity 0
+    // (x, y, packed pixel rectangle): the 16-byte stride of s_co and s_col, so the pair loads share one address;
+    // entry tile_pixels: a Gaussian of opacity 0 that pads every list
+    __shared__ float4 s_xy[tile_pixels + 1];
+    __shared__ float4 s_co[tile_pixels + 1];
+    __shared__ float4 s_col[tile_pixels + 1];
+    __shared__ __align__(16) uint32_t s_list[tile_pixels / 64][n_groups][list_len];  // per wave and group: offsets to walk
     __shared__ uint32_t s_max[tile_pixels / 64];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
     const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
-    const uint32_t g = (lane >> 2) & 3u;
+    const uint32_t g = ((lane >> 2) & 3u) + 4u * (lane >> 5);  // the lane's 4x2 group within the wave's band
     const uint32_t px = tx * tile_width + (lane & 15u);
     const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);
     const bool inside = px < a.width && py < a.height;
     const float pxf = static_cast<float>(px) + 0.5f, pyf = static_cast<float>(py) + 0.5f;
     const uint32_t bx0 = tx * tile_width;
-    const uint32_t by0 = ty * tile_height + wave * 4u, by1 = by0 + 4u;
+    const uint32_t by0 = ty * tile_height + wave * 4u;
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
     const uint32_t* const my_list = &s_list[wave][g][0];
-    // list entries past a group's count are read (and skipped): keep them valid batch indices
-    for (uint32_t k = tid; k < tile_pixels / 64 * 4 * list_len; k += tile_pixels) (&s_list[0][0][0])[k] = 0;
+    if (tid == 0) {
+        s_xy[tile_pixels] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        s_co[tile_pixels] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        s_col[tile_pixels] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
 
-    float cr = 0.0f, cg = 0.0f, cb = 0.0f, T = 1.0f;
+    // A pixel is done (takes no further Gaussian) exactly when T < transmittance_threshold: T changes only when a
+    // Gaussian is taken and starts at 1; pixels outside the image start at 0, done from the start.
+    float cr = 0.0f, cg = 0.0f, cb = 0.0f, T = inside ? 1.0f : 0.0f;
     uint32_t last = 0;
-    bool done = !inside;
     for (uint32_t start = 0; start < n_total; start += tile_pixels) {
-        if (__syncthreads_and(done)) break;
+        if (__syncthreads_and(T < transmittance_threshold)) break;
         if (start + tid < n_total) {
             const uint32_t e = a.sorted_inst[range.x + start + tid];
             const PrimRecord rec = a.records[a.inst_prim[e]];
@@ -141,21 +164,30 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
         // start + offset / 16 + 1 is formed once per batch
         uint32_t last_off = ~0u;
         for (uint32_t c0 = 0; c0 < batch_n; c0 += 64) {
-            uint64_t m[4];
-            cull_groups(rect_of(s_xy[c0 + lane]), c0 + lane < batch_n, bx0, by0, by1, m);
-            uint32_t n[4];
+            // the wave's lists padded with the opacity-0 Gaussian, then each group's hits of the chunk in order
+            {
+                uint4* const lw = reinterpret_cast<uint4*>(&s_list[wave][0][0]);
+                const uint4 pad = make_uint4(dummy_off, dummy_off, dummy_off, dummy_off);
+#pragma unroll
+                for (uint32_t q = 0; q < n_groups * list_len / 4 / 64; q++) lw[q * 64 + lane] = pad;
+            }
+            wave_lds_fence();
+            uint64_t m[n_groups];
+            cull_groups8(rect_of(s_xy[c0 + lane]), c0 + lane < batch_n, bx0, by0, m);
+            uint32_t n[n_groups];
             build_group_lists(m, lane, c0, &s_list[wave][0][0], list_len, n, 4u);  // entries: byte offsets of the staged float4s
             wave_lds_fence();
-            const uint32_t n_max = max(max(n[0], n[1]), max(n[2], n[3]));
-            const uint32_t my_n = pick_group(g, n[0], n[1], n[2], n[3]);
+            uint32_t n_max = n[0];
+#pragma unroll
+            for (uint32_t k = 1; k < n_groups; k++) n_max = max(n_max, n[k]);
             // two Gaussians of the group's list per step (list_len is even, so entry k + 1 exists; past the
-            // group's count it is a stale entry, skipped)
-            const auto walk = [&](uint32_t k, uint32_t off) {
+            // group's count it is the opacity-0 Gaussian, never taken)
+            const auto walk = [&](uint32_t off) {
                 const auto at = [off](const float4* arr) { return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(arr) + off); };
                 // branch-free: a skipped Gaussian gets weight 0, which leaves C and T bit for bit unchanged
                 float dx, dy, G;
                 const float alpha = eval_alpha(at(s_xy), at(s_co), pxf, pyf, dx, dy, G);
-                const bool take = k < my_n && !done && alpha >= min_alpha;
+                const bool take = T >= transmittance_threshold && alpha >= min_alpha;
                 const float a_t = take ? alpha : 0.0f;
                 const float w = T * a_t;
                 const float4 col = at(s_col);
@@ -164,12 +196,11 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
                 cb = __builtin_fmaf(w, col.z, cb);
                 T = T * (1.0f - a_t);
                 last_off = take ? off : last_off;
-                done = done || (take && T < transmittance_threshold);
             };
             for (uint32_t k = 0; k < n_max; k += 2) {
                 const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);
-                walk(k, jab.x);
-                walk(k + 1, jab.y);
+                walk(jab.x);
+                walk(jab.y);
             }
             wave_lds_fence();
         }
