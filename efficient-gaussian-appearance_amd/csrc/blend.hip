@@ -117,12 +117,14 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
     if (a.overflow && *a.overflow != 0) return;  // the binning was skipped: the host re-runs the frame
     constexpr uint32_t list_len = 64;
     constexpr uint32_t n_groups = 8;                        // 4x2 pixel groups per wave
-    constexpr uint32_t dummy_off = tile_pixels * 16u;       // byte offset of the staged Gaussian of opacity 0
-    // (x, y, packed pixel rectangle): the 16-byte stride of s_co and s_col, so the pair loads share one address;
-    // entry tile_pixels: a Gaussian of opacity 0 that pads every list
-    __shared__ float4 s_xy[tile_pixels + 1];
-    __shared__ float4 s_co[tile_pixels + 1];
-    __shared__ float4 s_col[tile_pixels + 1];
+    constexpr uint32_t fwd_batch = 128;
+    constexpr uint32_t dummy_off = fwd_batch * 16u;       // byte offset of the staged Gaussian of opacity 0
+    // Gaussians are staged fwd_batch at a time (fewer than the block's threads: with the eight groups' lists the
+    // staging area keeps twelve blocks per CU). (x, y, packed pixel rectangle): the 16-byte stride of s_co and
+    // s_col, so the pair loads share one address; entry fwd_batch: a Gaussian of opacity 0 that pads every list
+    __shared__ float4 s_xy[fwd_batch + 1];
+    __shared__ float4 s_co[fwd_batch + 1];
+    __shared__ float4 s_col[fwd_batch + 1];
     __shared__ __align__(16) uint32_t s_list[tile_pixels / 64][n_groups][list_len];  // per wave and group: offsets to walk
     __shared__ uint32_t s_max[tile_pixels / 64];
 
@@ -140,18 +142,18 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
     const uint32_t n_total = range.y - range.x;
     const uint32_t* const my_list = &s_list[wave][g][0];
     if (tid == 0) {
-        s_xy[tile_pixels] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        s_co[tile_pixels] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        s_col[tile_pixels] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        s_xy[fwd_batch] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        s_co[fwd_batch] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        s_col[fwd_batch] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 
     // A pixel is done (takes no further Gaussian) exactly when T < transmittance_threshold: T changes only when a
     // Gaussian is taken and starts at 1; pixels outside the image start at 0, done from the start.
     float cr = 0.0f, cg = 0.0f, cb = 0.0f, T = inside ? 1.0f : 0.0f;
     uint32_t last = 0;
-    for (uint32_t start = 0; start < n_total; start += tile_pixels) {
+    for (uint32_t start = 0; start < n_total; start += fwd_batch) {
         if (__syncthreads_and(T < transmittance_threshold)) break;
-        if (start + tid < n_total) {
+        if (tid < fwd_batch && start + tid < n_total) {
             const uint32_t e = a.sorted_inst[range.x + start + tid];
             const PrimRecord rec = a.records[a.inst_prim[e]];
             s_xy[tid] = make_float4(rec.r0.x, rec.r0.y, rec.r2.y, rec.r2.z);
@@ -159,7 +161,7 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
             s_col[tid] = make_float4(rec.r1.z, rec.r1.w, rec.r2.x, 0.0f);
         }
         __syncthreads();
-        const uint32_t batch_n = min(tile_pixels, n_total - start);
+        const uint32_t batch_n = min(fwd_batch, n_total - start);
         // byte offset of the last Gaussian of this batch the pixel took (~0: none); the last-contributor index
         // start + offset / 16 + 1 is formed once per batch
         uint32_t last_off = ~0u;
