@@ -63,23 +63,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
-// Culls lane's Gaussian (rectangle `rect`, `in` = exists) against the four 4x4 groups of the band whose pixel
-// columns start at bx0 and rows span [by0, by1); m[g] receives the wave's ballot for group g.
-__device__ __forceinline__ void cull_groups(uint2 rect, bool in, uint32_t bx0, uint32_t by0, uint32_t by1, uint64_t (&m)[4]) {
-    const uint32_t rx0 = rect.x & 0xffffu, rx1 = rect.x >> 16, ry0 = rect.y & 0xffffu, ry1 = rect.y >> 16;
-    const bool yov = in && ry0 < by1 && by0 < ry1;
-#pragma unroll
-    for (uint32_t k = 0; k < 4; k++) {
-        const uint32_t gx0 = bx0 + 4u * k;
-        m[k] = __ballot(yov && rx0 < gx0 + 4u && gx0 < rx1);
-    }
-}
-
-// the value of the lane's own group among four wave-uniform ones
-__device__ __forceinline__ uint32_t pick_group(uint32_t g, uint32_t j0, uint32_t j1, uint32_t j2, uint32_t j3) {
-    return (g & 2u) ? ((g & 1u) ? j3 : j2) : ((g & 1u) ? j1 : j0);
-}
-
 // Writes each group's surviving Gaussians of the chunk, in order, to list[k * list_len + 0 .. n[k]) (entry:
 // (base + lane) << shift for the Gaussian, a batch index or, shifted, a byte offset into 16-byte staged arrays);
 // n[k] = popcount(m[k]). A group then walks its list with one LDS read per step instead of scanning a 64-bit
@@ -258,15 +241,6 @@ __device__ __forceinline__ float swap32_add(float a, float b) {
 __device__ __forceinline__ float swap16_add(float a, float b) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Two values -> rows 0, 1 of a group hold the group sum of a, rows 2, 3 that of b.
-__device__ __forceinline__ float group_reduce2(float a, float b) {
-    float w = swap32_add(a, b);
-    w = swap16_add(w, w);
-    w += dpp<0x4E, 0xf, true>(0.0f, w);
-    w += dpp<0xB1, 0xf, true>(0.0f, w);
-    return w;
 }
 
 // raw conic (x, y, z) of an exp2-scaled one (scale_conic_for_exp2 inverted)
@@ -700,42 +674,46 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
 
 // Speedy-Splat pruning scores: per pixel and contributing Gaussian (o dL/dalpha)^2 for the upstream gradient
 // (1, 1, 1), with dL/dalpha formed as in the backward: T (c . 1) - (A - g_bg) / max(1 - alpha, eps), A = (colour
-// still to come) . 1, g_bg = -T_final (bg . 1). Same replay, 4x4 groups and lists as the backward; each group
-// walks two Gaussians per step and sums their scores over its 16 lanes with one two-value reduction; per batch
-// the twelve (wave, group) slots are added in a fixed order into one float per instance at its emission slot
-// (instances after every pixel's last contributor get 0). No atomics (the reference adds per pixel with float
-// atomics). Reference: B/rasterization/include/kernels_pruning_scores.cuh:11-171.
+// still to come) . 1, g_bg = -T_final (bg . 1). Same replay and 4x2 groups as the forward (eight per wave, the
+// lists padded with a staged Gaussian of opacity 0); each group walks two Gaussians per step and sums their
+// scores over its 8 lanes with one row-pair swap and two quad additions; per batch the 24 (wave, group) slots
+// are added in a fixed order into one float per instance at its emission slot (instances after every pixel's
+// last contributor get 0). No atomics (the reference adds per pixel with float atomics).
+// Reference: B/rasterization/include/kernels_pruning_scores.cuh:11-171.
 __global__ __launch_bounds__(tile_pixels) void blend_scores_kernel(BlendBackwardArgs a) {
     constexpr uint32_t n_waves = tile_pixels / 64;
     constexpr uint32_t batch = 32;
     constexpr uint32_t list_len = batch;
-    constexpr uint32_t n_slots = n_waves * 4;
-    __shared__ float4 s_stage[batch][3];  // (x, y, packed rect), exp2-scaled conic + opacity, colour
+    constexpr uint32_t n_groups = 8;
+    constexpr uint32_t n_slots = n_waves * n_groups;
+    constexpr uint32_t dummy = batch;  // staged Gaussian of opacity 0 (its slot column is never read)
+    __shared__ float4 s_stage[batch + 1][3];  // (x, y, packed rect), exp2-scaled conic + opacity, colour
     __shared__ uint32_t s_emit[batch];
-    __shared__ uint32_t s_list[n_waves][4][list_len];
+    __shared__ __align__(16) uint32_t s_list[n_waves][n_groups][list_len];
     __shared__ float s_part[n_slots][batch + 1];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
     const uint32_t tx = tile % a.grid_w, ty = tile / a.grid_w;
-    const uint32_t g = (lane >> 2) & 3u;
+    const uint32_t g = ((lane >> 2) & 3u) + 4u * (lane >> 5);  // the lane's 4x2 group within the wave's band
     const uint32_t px = tx * tile_width + (lane & 15u);
     const uint32_t py = ty * tile_height + wave * 4u + (lane >> 4);
     const bool inside = px < a.width && py < a.height;
     const float pxf = static_cast<float>(px) + 0.5f, pyf = static_cast<float>(py) + 0.5f;
     const uint32_t bx0 = tx * tile_width;
-    const uint32_t by0 = ty * tile_height + wave * 4u, by1 = by0 + 4u;
+    const uint32_t by0 = ty * tile_height + wave * 4u;
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
     const uint32_t n_proc = min(n_total, a.tile_max[tile]);
     const uint32_t* const my_list = &s_list[wave][g][0];
-    for (uint32_t k = tid; k < n_waves * 4 * list_len; k += tile_pixels) (&s_list[0][0][0])[k] = 0;
     for (uint32_t k = tid; k < n_slots * (batch + 1); k += tile_pixels) (&s_part[0][0])[k] = 0.0f;
-    // group_reduce2 leaves Gaussian a's sum in rows 0, 1 and b's in rows 2, 3: lane 4g of rows 0 and 2 store
+    if (tid < 3) s_stage[dummy][tid] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // after the reduction lane row r holds the group sum of Gaussian a (rows 0, 2) or b (rows 1, 3) of the
+    // group of rows r & 2, r | 1: the first lane of each quad stores it
     const uint32_t row = lane >> 4;
-    const bool store_lane = (lane & 3u) == 0 && (row == 0 || row == 2);
-    const uint32_t store_b = row == 2 ? 1u : 0u;
-    float* const slot = &s_part[wave * 4u + g][0];
+    const bool store_lane = (lane & 3u) == 0;
+    const bool store_b = (row & 1u) != 0;
+    float* const slot = &s_part[wave * n_groups + g][0];
 
     float A = 0.0f, gbg = 0.0f;
     uint32_t last = 0;
@@ -764,17 +742,24 @@ __global__ __launch_bounds__(tile_pixels) void blend_scores_kernel(BlendBackward
         }
         __syncthreads();
         const uint32_t batch_wave = wave_last > start ? min(min(batch, n_proc - start), wave_last - start) : 0u;
-        uint64_t m[4];
-        cull_groups(rect_of(s_stage[lane & (batch - 1)][0]), lane < batch_wave, bx0, by0, by1, m);
-        uint32_t n[4];
+        {
+            static_assert(n_groups * list_len == 4 * 64, "one 16-byte store per lane pads the wave's lists");
+            const uint4 pad = make_uint4(dummy, dummy, dummy, dummy);
+            reinterpret_cast<uint4*>(&s_list[wave][0][0])[lane] = pad;
+        }
+        wave_lds_fence();
+        uint64_t m[n_groups];
+        cull_groups8(rect_of(s_stage[lane & (batch - 1)][0]), lane < batch_wave, bx0, by0, m);
+        uint32_t n[n_groups];
         build_group_lists(m, lane, 0u, &s_list[wave][0][0], list_len, n);
         wave_lds_fence();
-        const uint32_t n_max = __builtin_amdgcn_readfirstlane(max(max(n[0], n[1]), max(n[2], n[3])));
-        const uint32_t my_n = pick_group(g, n[0], n[1], n[2], n[3]);
-        const uint32_t n_store = store_lane && my_n > store_b ? my_n - store_b : 0u;
+        uint32_t n_max = n[0];
+#pragma unroll
+        for (uint32_t q = 1; q < n_groups; q++) n_max = max(n_max, n[q]);
+        n_max = __builtin_amdgcn_readfirstlane(n_max);
         const uint32_t last_rel = last > start ? last - start : 0u;
         for (uint32_t k = 0; k < n_max; k += 2) {
-            const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);  // past the count: stale, skipped
+            const uint2 jab = *reinterpret_cast<const uint2*>(my_list + k);  // past the count: the opacity-0 entry
             float sc[2];
 #pragma unroll
             for (uint32_t h = 0; h < 2; h++) {
@@ -782,7 +767,7 @@ __global__ __launch_bounds__(tile_pixels) void blend_scores_kernel(BlendBackward
                 float dx, dy, G;
                 const float4 co = s_stage[j][1];
                 const float alpha = eval_alpha(s_stage[j][0], co, pxf, pyf, dx, dy, G);
-                const bool contrib = k + h < my_n && j < last_rel && alpha >= min_alpha;
+                const bool contrib = j < last_rel && alpha >= min_alpha;
                 const float ae = contrib ? alpha : 0.0f;
                 const float4 col = s_stage[j][2];
                 const float cg = col.x + col.y + col.z;
@@ -793,8 +778,11 @@ __global__ __launch_bounds__(tile_pixels) void blend_scores_kernel(BlendBackward
                 sc[h] = contrib ? dg * dg : 0.0f;
                 T = T * oma;
             }
-            const float sx = group_reduce2(sc[0], sc[1]);
-            if (k < n_store) slot[store_b ? jab.y : jab.x] = sx;
+            // rows 0 + 1 and 2 + 3 (a and b of the upper group, a and b of the lower), then over the quad
+            float sx = swap16_add(sc[0], sc[1]);
+            sx += dpp<0x4E, 0xf, true>(0.0f, sx);
+            sx += dpp<0xB1, 0xf, true>(0.0f, sx);
+            if (store_lane) slot[store_b ? jab.y : jab.x] = sx;
         }
         wave_lds_fence();
         __syncthreads();  // every group's sums are in its slots
