@@ -142,22 +142,31 @@ __device__ inline uint32_t count_touched_tiles(const Projected& pr, uint32_t lan
     return touched;
 }
 
+// Reductions over the wave, the result in every lane, without LDS round trips: four row rotations (DPP) give
+// every lane its 16-lane row's result, then two lane swaps (rows 0 <-> 2 and 1 <-> 3, then 0 <-> 1 and 2 <-> 3)
+// combine the rows. Every lane of the wave must take part.
+template <typename OP>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v, OP op) {
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x121, 0xf, 0xf, false)));  // row_ror:1
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x122, 0xf, 0xf, false)));  // row_ror:2
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x124, 0xf, 0xf, false)));  // row_ror:4
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, false)));  // row_ror:8
+    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return op(b[0], b[1]);
+}
+
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    return wave_reduce_u32(v, [](uint32_t x, uint32_t y) { return x + y; });
 }
 
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = min(v, static_cast<uint32_t>(__shfl_xor(v, o)));
-    return v;
+    return wave_reduce_u32(v, [](uint32_t x, uint32_t y) { return min(x, y); });
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, o)));
-    return v;
+    return wave_reduce_u32(v, [](uint32_t x, uint32_t y) { return max(x, y); });
 }
 
 }  // namespace efgs
