@@ -30,6 +30,35 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t value, uint64_t n) {
 
 // Primitive-index-ordered compaction of the visible primitives with their first emission slots (the
 // preprocess stored per-block visible and instance counts; block_offsets holds their exclusive scans).
+// Wave-wide scans and reductions without LDS round trips (every lane of the wave takes part). Inclusive sum:
+// shifts within each 16-lane row (DPP row_shr, zero filled), then lane 15 of rows 0 and 2 into rows 1 and 3 and
+// lane 31 into rows 2 and 3 (DPP row broadcasts). Reduction: four row rotations give every lane its row's
+// result, two lane swaps combine the rows; the result is in every lane.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, true));  // row_shr:1
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, true));  // row_shr:2
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, true));  // row_shr:4
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, true));  // row_shr:8
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return v;
+}
+template <typename OP>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v, OP op) {
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x121, 0xf, 0xf, false)));  // row_ror:1
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x122, 0xf, 0xf, false)));  // row_ror:2
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x124, 0xf, 0xf, false)));  // row_ror:4
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, false)));  // row_ror:8
+    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return op(b[0], b[1]);
+}
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) { return wave_reduce(v, [](uint32_t x, uint32_t y) { return x + y; }); }
+// a lane's value in every lane; the lane index must be wave-uniform
+__device__ __forceinline__ uint32_t lane_value(uint32_t v, uint32_t src) { return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(src))); }
+__device__ __forceinline__ float lane_value(float v, uint32_t src) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), static_cast<int>(src))); }
+
 __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const uint32_t* n_touched, const uint32_t* block_offsets,
                                                                           uint32_t* visible_out, uint32_t* prim_offset, uint32_t n) {
     __shared__ uint32_t wave_counts[preprocess_block / 64][2];
@@ -38,12 +67,7 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
     const uint32_t touched = p < n ? n_touched[p] : 0u;
     const bool visible = touched > 0;
     const uint64_t mask = __ballot(visible);
-    uint32_t inc = touched;  // inclusive wave scan of the tile counts
-#pragma unroll
-    for (uint32_t o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(inc, o);
-        if (lane >= o) inc += t;
-    }
+    const uint32_t inc = wave_inclusive_sum(touched);  // inclusive wave scan of the tile counts
     if (lane == 63) {
         wave_counts[wave][0] = static_cast<uint32_t>(__popcll(mask));
         wave_counts[wave][1] = inc;
@@ -98,13 +122,13 @@ __device__ __forceinline__ void emit_primitive_at(const CreateInstancesArgs& a, 
     }
     uint64_t coop = __ballot(cnt > 4);
     while (coop != 0) {
-        const uint32_t src = static_cast<uint32_t>(__ffsll(static_cast<long long>(coop)) - 1);
+        const uint32_t src = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__ffsll(static_cast<long long>(coop)) - 1));
         coop &= coop - 1;
-        const uint32_t c_x0 = __shfl(t.x0, src), c_y0 = __shfl(t.y0, src), c_bw = __shfl(bw, src), c_cnt = __shfl(cnt, src);
-        const uint32_t c_off = __shfl(off, src), c_n = __shfl(n, src), c_p = __shfl(p, src);
-        const float c_mx = __shfl(smx, src), c_my = __shfl(smy, src);
-        const float c_cx = __shfl(cx, src), c_cy = __shfl(cy, src), c_cz = __shfl(cz, src), c_pt = __shfl(pt, src);
-        uint32_t c_k = __shfl(k, src);
+        const uint32_t c_x0 = lane_value(t.x0, src), c_y0 = lane_value(t.y0, src), c_bw = lane_value(bw, src), c_cnt = lane_value(cnt, src);
+        const uint32_t c_off = lane_value(off, src), c_n = lane_value(n, src), c_p = lane_value(p, src);
+        const float c_mx = lane_value(smx, src), c_my = lane_value(smy, src);
+        const float c_cx = lane_value(cx, src), c_cy = lane_value(cy, src), c_cz = lane_value(cz, src), c_pt = lane_value(pt, src);
+        uint32_t c_k = lane_value(k, src);
         for (uint32_t base = 4; base < c_cnt; base += 64) {
             const uint32_t j = base + lane;
             const uint32_t tx = c_x0 + j % c_bw, ty = c_y0 + j / c_bw;
@@ -222,15 +246,12 @@ __global__ __launch_bounds__(fused_block) void create_instances_fused_kernel(Cre
         kmin = min(kmin, kr.x);
         kmax = max(kmax, kr.y);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        tv += static_cast<uint32_t>(__shfl_xor(static_cast<int>(tv), o));
-        ti += static_cast<uint32_t>(__shfl_xor(static_cast<int>(ti), o));
-        bv += static_cast<uint32_t>(__shfl_xor(static_cast<int>(bv), o));
-        bi += static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o));
-        kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmin), o)));
-        kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), o)));
-    }
+    tv = wave_sum(tv);
+    ti = wave_sum(ti);
+    bv = wave_sum(bv);
+    bi = wave_sum(bi);
+    kmin = wave_reduce(kmin, [](uint32_t x, uint32_t y) { return min(x, y); });
+    kmax = wave_reduce(kmax, [](uint32_t x, uint32_t y) { return max(x, y); });
     if (lane == 0) {
         s_red[wave][0] = tv; s_red[wave][1] = ti; s_red[wave][2] = bv; s_red[wave][3] = bi; s_red[wave][4] = kmin; s_red[wave][5] = kmax;
     }
@@ -277,14 +298,7 @@ __global__ __launch_bounds__(fused_block) void create_instances_fused_kernel(Cre
         for (uint32_t k = 0; k < fused_prefetch; k++) touched = it == k ? touched_pre[k] : touched;
         if (it >= fused_prefetch) touched = p < p_end ? a.n_touched[p] : 0u;
         const uint32_t vis = touched > 0 ? 1u : 0u;
-        uint32_t iv = vis, ii = touched;  // inclusive wave scans
-#pragma unroll
-        for (uint32_t o = 1; o < 64; o <<= 1) {
-            const uint32_t xv = static_cast<uint32_t>(__shfl_up(static_cast<int>(iv), o));
-            const uint32_t xi = static_cast<uint32_t>(__shfl_up(static_cast<int>(ii), o));
-            iv += lane >= o ? xv : 0u;
-            ii += lane >= o ? xi : 0u;
-        }
+        const uint32_t iv = wave_inclusive_sum(vis), ii = wave_inclusive_sum(touched);  // inclusive wave scans
         if (lane == 63) {
             s_red[wave][0] = iv;
             s_red[wave][1] = ii;
@@ -370,12 +384,7 @@ __global__ __launch_bounds__(64 * scan_waves) void tile_column_scan_kernel(uint3
         for (uint32_t w = 0; w < scan_waves; w++) total += s_part[w][lane];
         if (!table) total = in ? totals[t] : 0u;
         else if (in) totals[t] = total;
-        uint32_t inc = total;
-#pragma unroll
-        for (uint32_t o = 1; o < 64; o <<= 1) {
-            const uint32_t x = __shfl_up(inc, o);
-            if (lane >= o) inc += x;
-        }
+        const uint32_t inc = wave_inclusive_sum(total);
         if (in) local_start[t] = inc - total;
         s_start[lane] = inc - total;
         if (lane == 63) block_sums[blockIdx.x] = inc;
@@ -420,9 +429,7 @@ __global__ __launch_bounds__(256) void tile_count_global_kernel(const KeyT* keys
 __device__ __forceinline__ uint32_t scan_block_prefix_wave(const uint32_t* block_sums, uint32_t b, uint32_t lane) {
     uint32_t s = 0;
     for (uint32_t k = lane; k < b; k += 64) s += block_sums[k];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    return s;
+    return wave_sum(s);
 }
 
 // One block: order_runs[b][c] (tiles of class c in 64-tile block b) becomes the first position of that run in
@@ -509,12 +516,7 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     if (n_blocks <= max_scan_blocks) {
         const uint32_t v = threadIdx.x < n_blocks ? block_sums[threadIdx.x] : 0u;
         const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-        uint32_t inc = v;
-#pragma unroll
-        for (uint32_t o = 1; o < 64; o <<= 1) {
-            const uint32_t x = __shfl_up(inc, o);
-            if (lane >= o) inc += x;
-        }
+        const uint32_t inc = wave_inclusive_sum(v);
         if (lane == 63) s_waves[wave] = inc;
         __syncthreads();
         uint32_t off = 0;
