@@ -124,20 +124,23 @@ __device__ inline uint32_t count_touched_tiles(const Projected& pr, uint32_t lan
     }
     uint64_t coop = __ballot(cnt > n_sequential_tiles);
     while (coop != 0) {
-        const uint32_t src = static_cast<uint32_t>(__ffsll(static_cast<long long>(coop)) - 1);
+        // (the source lane is wave-uniform: its values come by readlane, no LDS permute)
+        const int src = static_cast<int>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__ffsll(static_cast<long long>(coop)) - 1)));
         coop &= coop - 1;
-        const uint32_t c_x0 = __shfl(pr.tiles.x0, src), c_y0 = __shfl(pr.tiles.y0, src);
-        const uint32_t c_bw = __shfl(bw, src), c_cnt = __shfl(cnt, src);
-        const float c_mx = __shfl(smx, src), c_my = __shfl(smy, src);
-        const float c_cx = __shfl(pr.conic_x, src), c_cy = __shfl(pr.conic_y, src), c_cz = __shfl(pr.conic_z, src);
-        const float c_pt = __shfl(pr.power_threshold, src);
+        const auto lane_u = [src](uint32_t v) { return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), src)); };
+        const auto lane_f = [src](float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src)); };
+        const uint32_t c_x0 = lane_u(pr.tiles.x0), c_y0 = lane_u(pr.tiles.y0);
+        const uint32_t c_bw = lane_u(bw), c_cnt = lane_u(cnt);
+        const float c_mx = lane_f(smx), c_my = lane_f(smy);
+        const float c_cx = lane_f(pr.conic_x), c_cy = lane_f(pr.conic_y), c_cz = lane_f(pr.conic_z);
+        const float c_pt = lane_f(pr.power_threshold);
         uint32_t hits = 0;
         for (uint32_t base = n_sequential_tiles; base < c_cnt; base += 64) {
             const uint32_t i = base + lane;
             const bool hit = i < c_cnt && will_primitive_contribute(c_mx, c_my, c_cx, c_cy, c_cz, c_x0 + i % c_bw, c_y0 + i / c_bw, c_pt);
             hits += static_cast<uint32_t>(__popcll(__ballot(hit)));
         }
-        if (lane == src) touched += hits;
+        if (lane == static_cast<uint32_t>(src)) touched += hits;
     }
     return touched;
 }
