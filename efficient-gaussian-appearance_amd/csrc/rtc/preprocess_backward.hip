@@ -202,6 +202,20 @@ __device__ inline void geometry_backward(const PreprocessBackwardArgs& a, uint32
     a.g_rotations[4 * p] = gq.x; a.g_rotations[4 * p + 1] = gq.y; a.g_rotations[4 * p + 2] = gq.z; a.g_rotations[4 * p + 3] = gq.w;
 }
 
+// The maximum of a value over the wave, in every lane, without LDS permutes: four row rotations (DPP), then
+// two lane swaps across the rows. OP: the maximum of two 32-bit patterns.
+template <typename OP>
+__device__ __forceinline__ uint32_t wave_max_bits(uint32_t v, OP op) {
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x121, 0xf, 0xf, false)));  // row_ror:1
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x122, 0xf, 0xf, false)));  // row_ror:2
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x124, 0xf, 0xf, false)));  // row_ror:4
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, false)));  // row_ror:8
+    const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return op(b[0], b[1]);
+}
+
 }  // namespace efgs
 
 #if EFGS_MODEL != 5
@@ -348,8 +362,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
     }
     // bound for the MLP kernel's gradient scale: the residual activations' derivatives are at most 1, so
     // |dL/d(MLP output)| <= max |dpre|; non-negative float bits order like the floats (integer max)
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = __uint_as_float(wave_max_bits(__float_as_uint(m), [](uint32_t x, uint32_t y) { return __float_as_uint(fmaxf(__uint_as_float(x), __uint_as_float(y))); }));
     if ((threadIdx.x & 63u) == 0) atomicMax(&s_max, __float_as_uint(m));
     __syncthreads();
     if (threadIdx.x == 0) a.color_grad_max[blockIdx.x] = s_max;
@@ -394,8 +407,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
 #pragma unroll
             for (uint32_t k = 0; k < 8; k++) m = max(m, v[k]);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(m, o)));
+        m = wave_max_bits(m, [](uint32_t x, uint32_t y) { return max(x, y); });
         if (lane == 0) s_wave_max[wave] = m;
         __syncthreads();
     }
