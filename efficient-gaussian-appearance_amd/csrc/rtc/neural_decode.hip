@@ -110,8 +110,17 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
 #pragma unroll
             for (uint32_t k = 0; k < 8; k++) m = fmaxf(m, v[k]);
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        // the wave's maximum without LDS permutes: four row rotations (DPP), then two lane swaps across the rows
+        const auto fmax_bits = [](uint32_t x, uint32_t y) { return __float_as_uint(fmaxf(__uint_as_float(x), __uint_as_float(y))); };
+        uint32_t mb = __float_as_uint(m);
+        mb = fmax_bits(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x121, 0xf, 0xf, false)));  // row_ror:1
+        mb = fmax_bits(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x122, 0xf, 0xf, false)));  // row_ror:2
+        mb = fmax_bits(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x124, 0xf, 0xf, false)));  // row_ror:4
+        mb = fmax_bits(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x128, 0xf, 0xf, false)));  // row_ror:8
+        const auto sa = __builtin_amdgcn_permlane32_swap(mb, mb, false, false);
+        mb = fmax_bits(sa[0], sa[1]);
+        const auto sb = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+        m = __uint_as_float(fmax_bits(sb[0], sb[1]));
         if (lane == 0) s_wave_max[wave] = m;
     }
     __syncthreads();  // weights staged, wave maxima written
