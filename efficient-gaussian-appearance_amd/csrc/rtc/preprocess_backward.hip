@@ -396,17 +396,22 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
     __shared__ uint32_t s_wave_max[preprocess_block / 64];
     {
         const uint32_t n_geometry_blocks = (a.n + preprocess_block - 1) / preprocess_block;
+        // 16-byte loads, four per thread in flight (one round for up to 4,096 geometry blocks; the array sits 16 n
+        // bytes after the 16-byte aligned colour gradients), then the last few entries one by one
         uint32_t m = 0u;
-        for (uint32_t b0 = 0; b0 < n_geometry_blocks; b0 += 8 * preprocess_block) {  // 8 loads in flight per thread
-            uint32_t v[8];
+        const uint32_t n4 = n_geometry_blocks / 4;
+        const uint4* const bounds4 = reinterpret_cast<const uint4*>(a.color_grad_max);
+        for (uint32_t q0 = 0; q0 < n4; q0 += 4 * preprocess_block) {
+            uint4 v[4];
 #pragma unroll
-            for (uint32_t k = 0; k < 8; k++) {
-                const uint32_t b = b0 + k * preprocess_block + threadIdx.x;
-                v[k] = b < n_geometry_blocks ? a.color_grad_max[b] : 0u;
+            for (uint32_t k = 0; k < 4; k++) {
+                const uint32_t q = q0 + k * preprocess_block + threadIdx.x;
+                v[k] = q < n4 ? bounds4[q] : make_uint4(0u, 0u, 0u, 0u);
             }
 #pragma unroll
-            for (uint32_t k = 0; k < 8; k++) m = max(m, v[k]);
+            for (uint32_t k = 0; k < 4; k++) m = max(m, max(max(v[k].x, v[k].y), max(v[k].z, v[k].w)));
         }
+        for (uint32_t b = 4 * n4 + threadIdx.x; b < n_geometry_blocks; b += preprocess_block) m = max(m, a.color_grad_max[b]);
         m = wave_max_bits(m, [](uint32_t x, uint32_t y) { return max(x, y); });
         if (lane == 0) s_wave_max[wave] = m;
         __syncthreads();
