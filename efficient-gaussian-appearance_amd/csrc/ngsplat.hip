@@ -101,14 +101,30 @@ __device__ __forceinline__ uint32_t ng_quat_code(float4 q) {
     return (angle << 16) | (qv << 8) | qu;
 }
 
-__device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v = fminf(v, __shfl_xor(v, d));
-    return v;
+// Wave reductions and scans without LDS permutes (every lane takes part). Reduction: four DPP row rotations,
+// then two lane swaps across the rows, the result in every lane. Inclusive scan: DPP row shifts (zero filled),
+// then lane 15 of rows 0, 2 into rows 1, 3 and lane 31 into rows 2, 3 (row broadcasts).
+template <typename OP>
+__device__ __forceinline__ float wave_reduce_f(float x, OP op) {
+    int v = __float_as_int(x);
+    v = __float_as_int(op(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x121, 0xf, 0xf, false))));  // row_ror:1
+    v = __float_as_int(op(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x122, 0xf, 0xf, false))));  // row_ror:2
+    v = __float_as_int(op(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false))));  // row_ror:4
+    v = __float_as_int(op(__int_as_float(v), __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false))));  // row_ror:8
+    const auto a = __builtin_amdgcn_permlane32_swap(static_cast<uint32_t>(v), static_cast<uint32_t>(v), false, false);
+    const float w = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(w), __float_as_uint(w), false, false);
+    return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d));
+__device__ __forceinline__ float wave_min(float v) { return wave_reduce_f(v, [](float x, float y) { return fminf(x, y); }); }
+__device__ __forceinline__ float wave_max(float v) { return wave_reduce_f(v, [](float x, float y) { return fmaxf(x, y); }); }
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, true));  // row_shr:1
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, true));  // row_shr:2
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, true));  // row_shr:4
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, true));  // row_shr:8
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false));  // row_bcast:15
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
     return v;
 }
 
@@ -251,12 +267,7 @@ __global__ __launch_bounds__(1024) void ngsplat_combine_kernel(uint32_t* partial
         l2 = fmaxf(l2, __uint_as_float(p[5]));
     }
     // inclusive scan of the per-thread sums within the wave, then over the 16 wave totals
-    uint32_t incl = sum;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t v = __shfl_up(incl, d);
-        if (lane >= static_cast<uint32_t>(d)) incl += v;
-    }
+    const uint32_t incl = wave_inclusive_sum(sum);
     mn = wave_min(mn);
     mx = wave_max(mx);
     l0 = wave_max(l0);
