@@ -820,6 +820,9 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     t.end(s);
     const uint32_t n_visible = n > 0 ? __atomic_load_n(&r->host_counters[0], __ATOMIC_ACQUIRE) : 0u;
     const uint32_t n_instances = n > 0 ? __atomic_load_n(&r->host_counters[1], __ATOMIC_ACQUIRE) : 0u;
+    // instance indices are signed 32-bit in the reference (B/rasterization/src/forward.cu:107-221); the emission
+    // slots, ranges and records here are unsigned 32-bit indices with 64-bit byte offsets
+    if (n_instances > 0x7fffffffu) return fail(EFGS_ERR_INVALID_ARGUMENT, "more than 2^31 - 1 tile instances in one frame");
     r->instance_hint = n_instances;
     r->visible_hint = n_visible;
     r->hint_primitives = n;
@@ -1120,7 +1123,9 @@ int check_decode(const efgs_rasterizer* r, int64_t n, const float* features, con
     if (n < 0 || n >= (1ll << 31)) return fail(EFGS_ERR_INVALID_ARGUMENT, "n out of range");
     if (degree < 0) return fail(EFGS_ERR_INVALID_ARGUMENT, "negative degree");
     if (n > 0) {
-        if (!dirs || !mlp_weights || (r->mlp_n_features > 0 && !features)) return fail(EFGS_ERR_INVALID_ARGUMENT, "null input");
+        // (directions are read only with SH degrees in the encoding)
+        if ((r->mlp_sh_mask != 0 && !dirs) || !mlp_weights || (r->mlp_n_features > 0 && !features))
+            return fail(EFGS_ERR_INVALID_ARGUMENT, "null input");
         if (r->mlp_base_input && !base) return fail(EFGS_ERR_INVALID_ARGUMENT, "base colours are required with base input");
         if ((reinterpret_cast<uintptr_t>(mlp_weights) & 15u) != 0) return fail(EFGS_ERR_INVALID_ARGUMENT, "mlp_weights must be 16-byte aligned");
     }

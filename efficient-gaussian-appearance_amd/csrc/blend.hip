@@ -648,8 +648,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
 #pragma unroll
                 for (uint32_t x = 0; x < NX; x++) asm volatile("" : "+v"(ax[x]));
                 const float4 co = s_stage[cj + 1][1];
-                // the record's 48 bytes at the instance's emission slot: a 32-bit byte offset from the array
-                float4* const out = reinterpret_cast<float4*>(reinterpret_cast<char*>(a.inst_grads) + 48u * __float_as_uint(s_stage[cj + 1][2].w));
+                // the record's 48 bytes at the instance's emission slot (a 64-bit byte offset: 48 e passes 2^32 from
+                // e = 89,478,486 on)
+                float4* const out = reinterpret_cast<float4*>(a.inst_grads) + 3u * static_cast<uint64_t>(__float_as_uint(s_stage[cj + 1][2].w));
                 // first half: quarter 0 (and quarter 2 below), second half: quarter 1, formed by selects so that
                 // both halves run one store path
                 const float4 craw = raw_conic_of(co);

@@ -104,11 +104,11 @@ __device__ __forceinline__ void emit_primitive_at(const CreateInstancesArgs& a, 
     const uint32_t cnt = active ? bw * (t.y1 - t.y0) : 0u;
     const float smx = rec.r0.x - 0.5f, smy = rec.r0.y - 0.5f;
     const float cx = rec.r0.z, cy = rec.r0.w, cz = rec.r1.x;
-    const float pt = cnt > 4 ? power_threshold_of(rec.r1.y) : 0.0f;  // (the tile test of tiles 4 and later)
-    const uint32_t first_tiles = __float_as_uint(rec.r2.w);            // the preprocess's test of tiles 0..3
+    const float pt = cnt > n_sequential_tiles ? power_threshold_of(rec.r1.y) : 0.0f;  // (the tile test of the later tiles)
+    const uint32_t first_tiles = __float_as_uint(rec.r2.w);  // the preprocess's test of the first n_sequential_tiles tiles
     KeyT* keys = static_cast<KeyT*>(a.keys);
     uint32_t k = 0;
-    for (uint32_t j = 0; j < cnt && j < 4; j++) {
+    for (uint32_t j = 0; j < cnt && j < n_sequential_tiles; j++) {
         const uint32_t tx = t.x0 + j % bw, ty = t.y0 + j / bw;
         if ((first_tiles >> j) & 1u) {
             if (k < n) {
@@ -120,7 +120,7 @@ __device__ __forceinline__ void emit_primitive_at(const CreateInstancesArgs& a, 
             k++;
         }
     }
-    uint64_t coop = __ballot(cnt > 4);
+    uint64_t coop = __ballot(cnt > n_sequential_tiles);
     while (coop != 0) {
         const uint32_t src = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__ffsll(static_cast<long long>(coop)) - 1));
         coop &= coop - 1;
@@ -129,7 +129,7 @@ __device__ __forceinline__ void emit_primitive_at(const CreateInstancesArgs& a, 
         const float c_mx = lane_value(smx, src), c_my = lane_value(smy, src);
         const float c_cx = lane_value(cx, src), c_cy = lane_value(cy, src), c_cz = lane_value(cz, src), c_pt = lane_value(pt, src);
         uint32_t c_k = lane_value(k, src);
-        for (uint32_t base = 4; base < c_cnt; base += 64) {
+        for (uint32_t base = n_sequential_tiles; base < c_cnt; base += 64) {
             const uint32_t j = base + lane;
             const uint32_t tx = c_x0 + j % c_bw, ty = c_y0 + j / c_bw;
             const bool hit = j < c_cnt && will_primitive_contribute(c_mx, c_my, c_cx, c_cy, c_cz, tx, ty, c_pt);
@@ -487,15 +487,17 @@ __global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_r
 
 // Every emitted instance goes to a slot of its tile's range: start of the tile + the tile's count in the
 // earlier segments + its rank within its segment (with a table: the scanned table entry holds the tile's start
-// within its 64-tile block plus that count), or + the next slot of an atomic cursor (without one). The slot receives the instance's sort key, the depth key of its primitive above its emission
-// index. Each block first scans the per-64-tile block sums into LDS (at most tile_hist_max_lds / 4 / 64 of them).
-constexpr uint32_t max_scan_blocks = static_cast<uint32_t>(tile_hist_max_lds / 4 / scan_tiles);
+// within its 64-tile block plus that count), or + the next slot of an atomic cursor (without one). The slot
+// receives the instance's sort key, the depth key of its primitive above its emission index. Each block first
+// scans the per-64-tile block sums into dynamic LDS (256 at a time with a running carry), one entry per 64-tile
+// block: up to max_scan_blocks of them (1,015,808 tiles); larger grids add the block sums per instance.
+constexpr uint32_t max_scan_blocks = static_cast<uint32_t>((tile_hist_max_lds - 2048) / 4);
 template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
                                                           const uint32_t* table, const uint32_t* local_rank, const uint32_t* block_sums,
                                                           const uint32_t* local_start, uint32_t* cursor, uint64_t* bucket, const uint32_t* counters,
                                                           uint32_t n_tiles, uint32_t* order_runs, uint32_t order_blocks) {
-    __shared__ uint32_t s_prefix[max_scan_blocks];
+    extern __shared__ uint32_t s_prefix[];  // n_blocks entries (the launch sizes it; none above max_scan_blocks)
     __shared__ uint32_t s_waves[4];
     __shared__ uint32_t s_order[4][order_classes];
     if (counters[counter_overflow] != 0) return;
@@ -514,15 +516,20 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     const uint32_t chunk = xcd * per + min(xcd, extra) + block / 8u;
     const uint32_t n_blocks = (n_tiles + scan_tiles - 1) / scan_tiles;
     if (n_blocks <= max_scan_blocks) {
-        const uint32_t v = threadIdx.x < n_blocks ? block_sums[threadIdx.x] : 0u;
         const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-        const uint32_t inc = wave_inclusive_sum(v);
-        if (lane == 63) s_waves[wave] = inc;
-        __syncthreads();
-        uint32_t off = 0;
-        for (uint32_t w = 0; w < wave; w++) off += s_waves[w];
-        if (threadIdx.x < n_blocks) s_prefix[threadIdx.x] = off + inc - v;
-        __syncthreads();
+        uint32_t carry = 0;  // block-uniform: the sum of the earlier passes
+        for (uint32_t b0 = 0; b0 < n_blocks; b0 += 256) {
+            const uint32_t i = b0 + threadIdx.x;
+            const uint32_t v = i < n_blocks ? block_sums[i] : 0u;
+            const uint32_t inc = wave_inclusive_sum(v);
+            if (lane == 63) s_waves[wave] = inc;
+            __syncthreads();
+            uint32_t off = carry;
+            for (uint32_t w = 0; w < wave; w++) off += s_waves[w];
+            if (i < n_blocks) s_prefix[i] = off + inc - v;
+            carry += s_waves[0] + s_waves[1] + s_waves[2] + s_waves[3];
+            __syncthreads();  // s_waves read by every wave before the next pass writes it (and s_prefix complete)
+        }
     }
     const uint32_t e = chunk * 256u + threadIdx.x;
     if (e >= n_instances) return;
@@ -877,11 +884,12 @@ bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_byte
     // one block that places the tile order's runs, then one block per 256 instances (a bound on I)
     const uint32_t blocks = div_up(max_instances, 256) + 1;
     const uint32_t* tab = plan.use_table ? table : nullptr;
+    const uint32_t prefix_bytes = order_blocks <= max_scan_blocks ? order_blocks * 4u : 0u;  // (order_blocks: the 64-tile blocks)
     if (key_bytes == 2)
-        tile_buckets_kernel<uint16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
+        tile_buckets_kernel<uint16_t><<<blocks, 256, prefix_bytes, s>>>(static_cast<const uint16_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
                                                             ts.local_start, ts.cursor, bucket, ts.counters, n_tiles, ts.order_runs, order_blocks);
     else
-        tile_buckets_kernel<uint32_t><<<blocks, 256, 0, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
+        tile_buckets_kernel<uint32_t><<<blocks, 256, prefix_bytes, s>>>(static_cast<const uint32_t*>(keys), inst_prim, depth_keys, tab, local_rank, ts.block_sums,
                                                             ts.local_start, ts.cursor, bucket, ts.counters, n_tiles, ts.order_runs, order_blocks);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;

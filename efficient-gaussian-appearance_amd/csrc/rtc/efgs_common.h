@@ -40,6 +40,11 @@ struct PrimRecord {
     float4 r0, r1, r2;
 };
 
+// tiles of a primitive's rectangle that the preprocess tests one per lane (and records in the first-tiles mask);
+// further tiles are tested wave-cooperatively, by the preprocess and again by instance emission
+constexpr uint32_t n_sequential_tiles = 4;
+static_assert(n_sequential_tiles <= 32, "the first-tiles mask is one 32-bit word of the record");
+
 // ---------------------------------------------------------------------------------------------------------
 // deterministic exp / log
 // ---------------------------------------------------------------------------------------------------------

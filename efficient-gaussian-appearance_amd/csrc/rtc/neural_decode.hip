@@ -3,6 +3,8 @@
 // feature encoding and the SH degree mask). Inputs are encoded exactly as in the preprocess kernels (frequency
 // encoding of the features, optional base colour input, SH degree values of the direction), so the decode
 // computes the raw MLP outputs that the rasterizer adds (after the residual activation) to the base colour.
+// With no SH degree and no frequency encoding the input rows are the features as they are (the identity-encoded
+// network of the tiny-cuda-nn surface): directions are then neither read nor differentiated.
 //
 //   EFGS_KERNEL_NAME            forward: out = MLP(x), fp16 MFMA with fp32 accumulation, outputs rounded to
 //                               fp16 (one wave per 64 primitives, persistent grid, weights in LDS)
@@ -35,6 +37,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_KERNEL_NAME(efgs::Neur
     // the lane's raw inputs (features, base colour, direction) of its primitive in the block's next chunk, loaded
     // one chunk ahead so that the loads are in flight during the current chunk's MLP
     constexpr uint32_t NB = EFGS_BASE_INPUT ? 3u : 0u;
+    constexpr bool has_dirs = EFGS_SH_DEGREE_MASK != 0;  // without SH degrees the inputs are the features alone (no direction read)
     float nf[nn::FEATURES + NB + 3];
     const auto load_inputs = [&](uint32_t chunk) {
         const uint32_t p = chunk * decode_block + threadIdx.x;
@@ -44,7 +47,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_KERNEL_NAME(efgs::Neur
 #pragma unroll
             for (uint32_t i = 0; i < NB; i++) nf[nn::FEATURES + i] = a.base[3 * static_cast<size_t>(p) + i];
 #pragma unroll
-            for (uint32_t i = 0; i < 3; i++) nf[nn::FEATURES + NB + i] = a.dirs[3 * static_cast<size_t>(p) + i];
+            for (uint32_t i = 0; i < 3; i++) nf[nn::FEATURES + NB + i] = has_dirs ? a.dirs[3 * static_cast<size_t>(p) + i] : 0.0f;
         }
     };
     load_inputs(blockIdx.x);
@@ -137,7 +140,8 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
         const bool active = p < a.n;
         if (__ballot(active) == 0) continue;  // wave-uniform: the tail of the last chunk
         const uint32_t pp = active ? p : 0u;
-        const float3 d = make_float3(a.dirs[3 * pp], a.dirs[3 * pp + 1], a.dirs[3 * pp + 2]);
+        constexpr bool has_dirs = EFGS_SH_DEGREE_MASK != 0;  // without SH degrees no direction is read or differentiated
+        const float3 d = has_dirs ? make_float3(a.dirs[3 * pp], a.dirs[3 * pp + 1], a.dirs[3 * pp + 2]) : make_float3(0.0f, 0.0f, 0.0f);
         const float* feat = a.features + static_cast<size_t>(pp) * nn::FEATURES;
         const float* base = EFGS_BASE_INPUT ? a.base + 3 * static_cast<size_t>(pp) : nullptr;
         float x[nn::INP];
@@ -162,7 +166,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
 #pragma unroll
                 for (uint32_t c = 0; c < 3; c++) a.g_base[3 * p + c] = nn::feature_grad(base[c], dx, nn::FEATURES + c);
             }
-            if (a.g_dirs) {
+            if (has_dirs && a.g_dirs) {
                 const float3 gd = nn::direction_grad(d, a.degree, dx);
                 a.g_dirs[3 * p] = gd.x;
                 a.g_dirs[3 * p + 1] = gd.y;

@@ -16,7 +16,6 @@
 namespace efgs {
 
 constexpr uint32_t preprocess_block = 256;
-constexpr uint32_t n_sequential_tiles = 4;
 
 struct Projected {
     float mean2d_x, mean2d_y, conic_x, conic_y, conic_z, opacity, power_threshold, depth;

@@ -273,8 +273,10 @@ int efgs_ngsplat_pack(const efgs_ngsplat_input* in, efgs_ngsplat_output* out, ef
 
 /* Standalone neural decode: the configured residual MLP (efgs_set_residual_mlp, model 5) on n primitives'
  * features (n x n_features, the learned latents), base colours (n x 3, read with base input only) and unit
- * view directions (n x 3), encoded as in the rasterizer (frequency encoding, SH degree values of the
- * direction gated by `degree`). Forward writes the raw MLP outputs (n x 3, fp16-rounded values) to `out`.
+ * view directions (n x 3; not read, and may be NULL, when the encoding has no SH degree), encoded as in the
+ * rasterizer (frequency encoding, SH degree values of the direction gated by `degree`). With no SH degree, no
+ * frequency encoding and no base input the input rows are the features as given: the identity-encoded network
+ * of tiny-cuda-nn's NetworkWithInputEncoding (Appearance/Neural.py:40-51,102-111), which efgs.tcnn runs here. Forward writes the raw MLP outputs (n x 3, fp16-rounded values) to `out`.
  * Backward takes dL/d(outputs) (n x 3) and writes the feature gradients (n x n_features), the base-input
  * gradients (n x 3, with base input; may be NULL), the direction gradients (n x 3; may be NULL) and the fp32
  * weight gradients (efgs_mlp_param_count entries); it allocates its per-block partials through `alloc`.

@@ -211,24 +211,43 @@ def test_block_count_scan_at_large_primitive_counts(n_total):
     np.testing.assert_array_equal(big_img, small_img)
 
 
-def test_instance_buffers_sized_from_the_previous_frame():
+# (width, height, primitives, sparse and dense scale shifts): the fused-emission grid, a grid of 12,161-16,384
+# tiles (segments of the compacted list with a histogram table) and a 32-bit-key grid (global-atomic counting)
+SPECULATION_GRIDS = {
+    'fused_64x48': (64, 48, 600, 1.0, 3.5),
+    'table_1600x1600': (1600, 1600, 600, 0.5, 2.0),
+    'global_4200x3000': (4200, 3000, 800, 0.5, 1.5),
+}
+
+
+@pytest.mark.parametrize('grid', list(SPECULATION_GRIDS))
+def test_instance_buffers_sized_from_the_previous_frame(grid):
     # After a frame of a scene size the forward launches the binning and the blend into instance buffers sized
     # from that frame's count (+12.5 % + 1024) before it reads the counters. A second scene of the same primitive
     # count and image size with far larger Gaussians overflows them: the device skips the binning and the blend and
-    # the host re-runs them with exact buffers. A third, sparse one fits the (now large) speculative buffers.
+    # the host re-runs them with exact buffers. A third, sparse one fits the (now large) speculative buffers; the
+    # fourth, dense again, fits them too. Every frame's keys, order, ranges and image match the oracle and the
+    # overflow flag ends cleared, on each binning path.
     from efgs.rasterization import frame_views
-    sparse, app, cam = small_case(model='sh', n=600, scale_shift=1.0)
-    dense = O.Scene(means=sparse.means, scales=sparse.scales + 2.5, rotations=sparse.rotations, opacities=sparse.opacities,
-                    base_colors=sparse.base_colors, residual_params=sparse.residual_params)
+    width, height, n, s_sparse, s_dense = SPECULATION_GRIDS[grid]
+    sparse, app, cam = small_case(model='sh', n=n, width=width, height=height, scale_shift=s_sparse)
+    dense = O.Scene(means=sparse.means, scales=sparse.scales + (s_dense - s_sparse), rotations=sparse.rotations,
+                    opacities=sparse.opacities, base_colors=sparse.base_colors, residual_params=sparse.residual_params)
     gw, gh = cam.grid()
     counts = []
-    for scene in (sparse, dense, sparse, dense):
+    for k, scene in enumerate((sparse, dense, sparse, dense)):
+        print(f'speculation {grid}: frame {k}', flush=True)
         image, frame, bufs = _render(scene, app, cam)
         fw = O.render(scene, app, cam)
         assert frame.n_instances == len(fw.inst_keys)
         assert frame.instance_capacity >= frame.n_instances
         v = frame_views(frame)
-        np.testing.assert_array_equal(read_device(bufs, v.tile_sorted_keys, int(frame.n_instances), np.uint16), fw.inst_keys)
+        kt = np.uint16 if frame.key_bytes == 2 else np.uint32
+        assert frame.key_bytes == (2 if gw * gh <= 65535 else 4)
+        np.testing.assert_array_equal(read_device(bufs, v.tile_sorted_keys, int(frame.n_instances), kt).astype(np.uint32), fw.inst_keys)
+        sorted_inst = read_device(bufs, v.tile_sorted_instances, int(frame.n_instances), np.uint32)
+        inst_prim = read_device(bufs, v.instance_primitive, int(frame.n_instances), np.uint32)
+        np.testing.assert_array_equal(inst_prim[sorted_inst], fw.inst_prims)
         np.testing.assert_array_equal(read_device(bufs, v.tile_ranges, 2 * gw * gh, np.uint32).reshape(-1, 2), fw.ranges)
         assert np.abs(image - fw.image).max() <= 1e-4
         assert read_device(bufs, v.counters, 8, np.uint32)[5] == 0  # overflow flag cleared by the re-run
