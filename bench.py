@@ -9,8 +9,10 @@ colours, latents, MLP weights) is timed beside it. Inputs are resident in HBM be
 
 A timed step is the headline quantity W * H / (t_fwd + t_bwd): diff_rasterize forward (preprocess through blend,
 with its counter readback) and backward (blend backward, preprocess backward) with a fixed upstream gradient (the
-L1 gradient of the scene's first render). Output: one JSON line. `value` = W * H / (median HIP-event time of the
-K timed steps) in Mpix/s; `full_step_*` = one training iteration (forward, L1 loss, backward, FusedAdam over every
+L1 gradient of the scene's first render). The step first runs untimed for RAMP_S seconds (the GPU's clocks rise
+over the first tens of milliseconds of load), then W warm-up steps, then the K timed steps between one pair of HIP
+events with device synchronisations on both sides. Output: one JSON line. `value` = W * H / (that time / K) in
+Mpix/s (K more steps, each between its own events, give `step_ms_quartiles`); `full_step_*` = one training iteration (forward, L1 loss, backward, FusedAdam over every
 group); `inference_ms` / `inference_fps` = `rasterize` as the reference's render_image_benchmark calls it (HWC,
 clamped, no autograd). `roofline` covers the step's dominant kernel, timed with HIP events that the library records
 around each stage on the stream it launches on; `stages` lists every stage (Adam: events around FusedAdam.step on
@@ -39,14 +41,16 @@ if PKG not in sys.path:
     sys.path.insert(0, PKG)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+RAMP_S = 0.3                   # untimed clock ramp before the warm-up steps (seconds of the timed step itself)
 MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'traffic_c3_neural.txt')
+KERNELS_FILE = os.path.join(ROOT, 'profiles', 'kernels_c3_neural_train_step.txt')
 
 # kernel names (as rocprofv3 lists them) of each timed stage
 STAGE_KERNELS = {
     'preprocess_forward': 'preprocess_forward_<model>',
-    # (with the fused emission the scan runs on a first frame only and the compaction not at all: the compact
-    # stage's time is then its empty event bracket)
+    # (with the fused emission the scan runs on a first frame only and the compaction not at all: the stage is then
+    # not timed, and create_instances_fused_kernel carries the compaction's bytes)
     'compact': 'scan_block_counts_kernel + compact_visible_kernel',
     'create_instances': 'create_instances_fused_kernel',
     'tile_offsets': 'tile_column_scan_kernel',  # (the tile order's runs are placed by an extra block of tile_buckets_kernel)
@@ -93,10 +97,12 @@ def mlp_flops_per_primitive(n_in: int, n_neurons: int, n_hidden: int, n_out: int
     return 2 * (n_in * n_neurons + (n_hidden - 1) * n_neurons * n_neurons + n_neurons * n_out)
 
 
-def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_fwd_flops: int, adam_elements: int):
+def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_fwd_flops: int, adam_elements: int,
+                compaction_fused: bool = True):
     """(bytes, flops) of one launch of `stage`. Per-unit figures: preprocess N*(60+R) + V*52 split into the
     preprocess kernel (N*(60+R) + V*44) and the compaction (V*8: visible list and emission offsets); instance
-    emission V*40 + I*6, tile ranges T*8; the ordering by (tile, depth) -- the reference's depth sort and
+    emission V*40 + I*6 (with the compaction fused into the emission kernel, as on grids whose tile histogram fits
+    its LDS: V*48 + I*6 for that one kernel, and no compaction stage), tile ranges T*8; the ordering by (tile, depth) -- the reference's depth sort and
     offset scan (V*24) and tile sort (I*12) -- split into the bucketing (I*6: tile key in, emission index
     out) and the per-tile sort (I*6 + V*24); blend forward I*48 + P*20; blend backward P*32 + I*76;
     preprocess backward V*(110+R) + N*(56+R), for the neural model split into the geometry kernel
@@ -106,7 +112,7 @@ def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_
     table = {
         'preprocess_forward': (N * (60 + R) + V * 44, V * mlp_fwd_flops),
         'compact': (V * 8, 0),
-        'create_instances': (V * 40 + I * 6, 0),
+        'create_instances': (V * (48 if compaction_fused else 40) + I * 6, 0),
         'tile_offsets': (T * 8, 0),
         'tile_buckets': (I * 6, 0),
         'tile_sort': (I * 6 + V * 24, 0),
@@ -118,6 +124,19 @@ def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_
         'adam': (28 * adam_elements, 0),
     }
     return table.get(stage, (0, 0))
+
+
+def read_step_kernel_us():
+    """Kernel time of one steady-state c3 step (microseconds) from the committed rocprofv3 kernel-trace summary: its
+    line `step_kernels_us <value>`."""
+    if not os.path.exists(KERNELS_FILE):
+        return None
+    with open(KERNELS_FILE) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) == 2 and parts[0] == 'step_kernels_us':
+                return float(parts[1])
+    return None
 
 
 def read_traffic(kernel: str):
@@ -199,6 +218,13 @@ def l1_loss_fn():
     return L1Loss.apply
 
 
+def _quartiles(xs):
+    """min, lower quartile, median, upper quartile, max (nearest-rank)."""
+    xs = sorted(xs)
+    k = len(xs) - 1
+    return [xs[0], xs[k // 4], _median(xs), xs[(3 * k + 3) // 4], xs[-1]]
+
+
 def _median(xs):
     xs = sorted(xs)
     k = len(xs)
@@ -246,22 +272,42 @@ def gpu_benchmark(args):
         opt.zero_grad(set_to_none=True)
 
     log(f'scene ready: {sc["means"].shape[0]} Gaussians, {sc["camera"]["width"]}x{sc["camera"]["height"]}, {sc["model"]}')
+    # clock ramp: the GPU's clocks rise over the first tens of milliseconds of load (the kernels of the first ~40
+    # steps run up to 8 % slower), so the step runs untimed for RAMP_S seconds before the warm-up steps
+    ramp_steps = 0
+    t_ramp = time.perf_counter()
+    while time.perf_counter() - t_ramp < RAMP_S:
+        raster_step()
+        ramp_steps += 1
+    torch.cuda.synchronize()
     for _ in range(args.warmup):
         raster_step()
     torch.cuda.synchronize()
-    log(f'{args.warmup} warmup steps done')
-    step_events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    log(f'clock ramp ({ramp_steps} untimed steps, {RAMP_S} s) and {args.warmup} warmup steps done')
+    # the K timed steps: one pair of HIP events around all of them, device synchronisations on both sides (no
+    # event between steps: a pair per step adds ~10 us of GPU time to every step)
     counts = []
+    region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for k in range(args.steps):
-        step_events[k][0].record()
+    region[0].record()
+    for _ in range(args.steps):
         counts.append(raster_step())
-        step_events[k][1].record()
+    region[1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    region_ms = region[0].elapsed_time(region[1]) / args.steps
+    # the same K steps again, each between its own pair of events (the per-step spread)
+    step_events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for k in range(args.steps):
+        step_events[k][0].record()
+        raster_step()
+        step_events[k][1].record()
+    torch.cuda.synchronize()
     step_ms = [e[0].elapsed_time(e[1]) for e in step_events]
-    log(f'{args.steps} timed forward + backward steps done: median {_median(step_ms):.4f} ms, wall {wall * 1e3 / args.steps:.4f} ms/step')
+    log(f'{args.steps} timed forward + backward steps done: {region_ms:.4f} ms/step (events around the {args.steps} steps), wall '
+        f'{wall * 1e3 / args.steps:.4f} ms/step; {args.steps} more between per-step events: median {_median(step_ms):.4f} ms')
 
     # inference renders as the reference's render_image_benchmark calls them: HWC, clamped, no autograd
     render_events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
@@ -317,10 +363,11 @@ def gpu_benchmark(args):
         R_bytes = residual_bytes(model, 15 if model == 'sh' else 8)
     adam_elements = sum(p.numel() for p in params.values())
     per_stage = {name: (ms / max(n, 1), n) for name, (ms, n) in stage_times.items() if n > 0}  # per launch
+    fused = 'compact' not in per_stage  # (the compaction stage launches nothing when the emission kernel does it)
     per_stage['adam'] = (_median(adam_ms), args.steps)
     stages = {}
     for name, (ms, n) in per_stage.items():
-        b, f = algorithmic(name, N, V, I, T, W * H, R_bytes, F, adam_elements)
+        b, f = algorithmic(name, N, V, I, T, W * H, R_bytes, F, adam_elements, fused)
         entry = {'ms': round(ms, 5), 'launches': n // args.steps if name != 'adam' else 1}
         if b:
             entry['gb_s'] = round(b / (ms * 1e-3) / 1e9, 1)
@@ -333,7 +380,7 @@ def gpu_benchmark(args):
     kernel_stages = [s for s in per_stage if s not in ('counter_read', 'adam')]   # the step's kernels (Adam is reported apart)
     dominant = max(kernel_stages, key=lambda s: per_stage[s][0])
     dms = per_stage[dominant][0]
-    b, f = algorithmic(dominant, N, V, I, T, W * H, R_bytes, F, adam_elements)
+    b, f = algorithmic(dominant, N, V, I, T, W * H, R_bytes, F, adam_elements, fused)
     hbm_frac = b / (dms * 1e-3) / 1e9 / HBM_PEAK_GBS if b else 0.0
     mfma_frac = f / (dms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS if f else 0.0
     kernel_name = STAGE_KERNELS.get(dominant, dominant).replace('<model>', model)
@@ -346,7 +393,7 @@ def gpu_benchmark(args):
     roofline['traffic'] = read_traffic(kernel_name)
     roofline.update({'kernel': kernel_name, 'stage': dominant, 'avg_launch_ms': round(dms, 5),
                      'algorithmic_bytes': int(b), 'algorithmic_flops': int(f)})
-    return dict(W=W, H=H, N=N, V=V, I=I, model=model, step_ms=step_ms, wall_ms_per_step=wall * 1e3 / args.steps,
+    return dict(W=W, H=H, N=N, V=V, I=I, model=model, step_ms=step_ms, wall_ms_per_step=wall * 1e3 / args.steps, region_ms=region_ms,
                 full_step_ms=_median(full_ms), fwd_loss_bwd_ms=_median(fwd_loss_bwd_ms), adam_ms=_median(adam_ms),
                 render_ms=render_ms, roofline=roofline, stages=stages, scene=sc)
 
@@ -822,11 +869,15 @@ def main() -> None:
 
 
 def headline_line(args, r: dict, cpu: dict | None, port: dict | None) -> dict:
-    """The bench's JSON line. `value` = W * H / t, t = median over the K timed steps of the HIP-event time of one step
-    (the rasterizer's forward and backward, BASELINE.md's headline); `ms_per_step` = t; `wall_ms_per_step` = host
-    wall time of the K steps bracketed by device synchronisations, divided by K."""
+    """The bench's JSON line. `value` = W * H / t, t = the HIP-event time of the K timed steps (one pair of events
+    around all of them, device synchronisations on both sides) divided by K: the rasterizer's forward and backward,
+    BASELINE.md's headline; `ms_per_step` = t; `wall_ms_per_step` = host wall time of the same K steps divided by K;
+    `step_ms_quartiles` = the spread of K more steps, each between its own pair of events (which adds ~10 us per
+    step); `gpu_idle_us_per_step` = t minus the kernel time of one steady-state step of the committed kernel trace of
+    this command (no kernel running on the GPU)."""
     W, H = r['W'], r['H']
-    ms = _median(r['step_ms'])
+    ms = r['region_ms']
+    kernel_us = read_step_kernel_us()
     return {
         'metric': 'fwd+bwd Mpix/s @1M Gaussians 1080p (Neural); % HBM/MFMA roofline per kernel',
         'value': round(W * H / (ms * 1e-3) / 1e6, 3),
@@ -845,9 +896,12 @@ def headline_line(args, r: dict, cpu: dict | None, port: dict | None) -> dict:
                                f'{r["model"]} appearance',
                    'n_gaussians': r['N'], 'width': W, 'height': H, 'appearance': r['model'],
                    'visible': round(r['V']), 'instances': round(r['I'])},
-        'timing': f'HIP events around each of the {args.steps} timed steps after {args.warmup} warm-up steps, median',
-        'mean_ms_per_step': round(sum(r['step_ms']) / len(r['step_ms']), 4),
+        'timing': (f'HIP events around the {args.steps} timed steps (device synchronisations on both sides), after a {RAMP_S} s '
+                   f'untimed clock ramp of the same step and {args.warmup} warm-up steps'),
         'wall_ms_per_step': round(r['wall_ms_per_step'], 4),
+        'step_ms_quartiles': [round(q, 4) for q in _quartiles(r['step_ms'])],
+        'step_kernels_us_rocprof': kernel_us,
+        'gpu_idle_us_per_step': round(ms * 1e3 - kernel_us, 1) if kernel_us is not None else None,
         'full_step_ms': round(r['full_step_ms'], 4),
         'full_step_mpix_s': round(W * H / (r['full_step_ms'] * 1e-3) / 1e6, 3),
         'fwd_loss_bwd_ms': round(r['fwd_loss_bwd_ms'], 4),

@@ -724,17 +724,19 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         t.begin(EFGS_STAGE_PREPROCESS_FORWARD, s);
         if (!launch_rtc(k, blocks, preprocess_block, shared, &a, s)) return EFGS_ERR_HIP;
         t.end(s);
-        t.begin(EFGS_STAGE_COMPACT, s);
         // The counter scan writes the counters to the pinned host buffer as well, then the frame's sequence number.
         // With the fused emission (grids whose histogram fits) the emission kernel does the scan and the compaction
-        // itself; the scan still runs before a first frame, whose buffers wait for the counts.
+        // itself; the scan still runs before a first frame, whose buffers wait for the counts. (The stage is timed
+        // only when it launches a kernel.)
         seq = ++r->counter_seq == 0 ? ++r->counter_seq : r->counter_seq;
-        if (!speculate || !fused)
+        const bool scan = !speculate || !fused;
+        if (scan || !fused) t.begin(EFGS_STAGE_COMPACT, s);
+        if (scan)
             if (!launch_scan_block_counts(pl.block_counts, pl.block_key_ranges, pl.block_offsets, pl.counters, r->host_counters_dev,
                                           speculate ? static_cast<uint32_t>(capacity) : 0xffffffffu, seq, chunks, s))
                 return EFGS_ERR_HIP;
         if (!fused && !launch_compact_visible(pl.n_touched, pl.block_offsets, pl.visible_prims, pl.prim_offset, n, s)) return EFGS_ERR_HIP;
-        t.end(s);
+        if (scan || !fused) t.end(s);
     } else {
         if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
     }

@@ -180,11 +180,16 @@ def _check_inputs(means, scales, rotations, opacities, precomputed_colors, base_
     return device
 
 
-def _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32, settings):
+def _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32, settings,
+             native=None):
+    """native: (settings struct, tensors it points to, primitives struct) already built for these inputs, or None."""
     device = _check_inputs(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32)
     with torch.cuda.device(device):
-        cs, keep = _native_settings(settings, device)
-        prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32)
+        if native is not None:
+            cs, keep, prims = native
+        else:
+            cs, keep = _native_settings(settings, device)
+            prims = _native_primitives(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32)
         image = torch.empty((3, int(settings.height), int(settings.width)), dtype=torch.float32, device=device)
         alloc = _lib.WorkspaceAllocator(device, 'forward')
         frame = _lib.Frame()
@@ -201,19 +206,22 @@ class _Rasterize(torch.autograd.Function):
     def forward(ctx: Any, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights,
                 densification_info, rasterizer_settings: RasterizerSettings) -> torch.Tensor:
         mlp_weights_f32 = mlp_weights.detach().float().contiguous() if mlp_weights.numel() > 0 else torch.empty(0, dtype=torch.float32, device=means.device)
+        ctx.mlp_numel = mlp_weights.numel()
+        # the backward's host-side state is built before the forward launches anything: the host is then still ahead
+        # of the GPU (which runs the previous work), and between the forward's counter read and the backward's first
+        # launch only autograd's own bookkeeping runs on the host while the GPU finishes the binning and the blend
+        prep = _prepare_backward(ctx, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params,
+                                 mlp_weights_f32, densification_info, rasterizer_settings) if any(ctx.needs_input_grad) else None
+        ctx.prepared = prep
         image, frame, buffers, _ = _forward(means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params,
-                                            mlp_weights_f32, rasterizer_settings)
+                                            mlp_weights_f32, rasterizer_settings,
+                                            native=(prep.settings, prep.keep, prep.prims) if prep is not None else None)
         ctx.rasterizer_settings = rasterizer_settings
         ctx.frame = frame
         ctx.buffers = buffers
-        ctx.mlp_numel = mlp_weights.numel()
         ctx.save_for_backward(image, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params, mlp_weights_f32)
         ctx.densification_info = densification_info
         ctx.mark_non_differentiable(densification_info)
-        # the backward's host-side state is built here, while the GPU still runs the forward, so that the
-        # backward only launches
-        ctx.prepared = _prepare_backward(ctx, means, scales, rotations, opacities, precomputed_colors, base_colors, residual_params,
-                                         mlp_weights_f32, densification_info, rasterizer_settings) if any(ctx.needs_input_grad) else None
         return image
 
     @staticmethod
