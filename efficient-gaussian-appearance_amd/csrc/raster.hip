@@ -568,9 +568,18 @@ constexpr uint32_t tile_sort_waves = 4;
 constexpr uint32_t tile_sort_block = 64 * tile_sort_waves;
 constexpr uint32_t wave_slab = 512;
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, uint32_t d) {
-    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(v)), static_cast<int>(d)));
-    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(v >> 32)), static_cast<int>(d)));
+// The value of lane (lane ^ d) (d a power of two below 64, a constant after unrolling): one DPP move within a row
+// for d = 1, 2 (quad permutations) and 8 (row rotation by 8), an LDS permute otherwise (the row swaps of gfx950
+// overwrite both operands: two copies and a select per exchange cost more VALU than the permute).
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v, uint32_t d) {
+    if (d == 1) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xb1, 0xf, 0xf, true));  // quad_perm [1,0,3,2]
+    if (d == 2) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4e, 0xf, 0xf, true));  // quad_perm [2,3,0,1]
+    if (d == 8) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, true));  // row_ror:8
+    return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), static_cast<int>(d)));
+}
+__device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v, uint32_t d) {
+    const uint32_t lo = xor_lane(static_cast<uint32_t>(v), d);
+    const uint32_t hi = xor_lane(static_cast<uint32_t>(v >> 32), d);
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
@@ -584,9 +593,11 @@ __device__ __forceinline__ void wave_bitonic(uint64_t (&k)[K], uint32_t lane) {
 #pragma unroll
                 for (uint32_t i = 0; i < K; i++) {
                     const uint32_t x = K * lane + i;
-                    const uint64_t o = shfl_xor_u64(k[i], j / K);
+                    const uint64_t o = xor_lane_u64(k[i], j / K);
                     const bool keep_min = ((x & size) == 0) == ((x & j) == 0);
-                    k[i] = keep_min ? (k[i] < o ? k[i] : o) : (k[i] < o ? o : k[i]);
+                    // the partner's key belongs here exactly when it is the smaller one where the lane keeps the
+                    // minimum and the larger one elsewhere: one compare and one select (equal keys: either)
+                    k[i] = (o < k[i]) == keep_min ? o : k[i];
                 }
             } else {
 #pragma unroll
