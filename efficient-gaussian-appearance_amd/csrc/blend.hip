@@ -44,16 +44,34 @@ __device__ __forceinline__ float4 scale_conic_for_exp2(float cx, float cy, float
     return make_float4(-0.5f * log2e * cx, -log2e * cy, -0.5f * log2e * cz, opacity);
 }
 
-// alpha of a staged Gaussian at a pixel centre; G receives the Gaussian factor. v_exp_f32 (a quarter-rate
-// instruction: 4 issue slots) replaces an 11-operation polynomial; its result is a fixed function of q, so
-// the backward's replay reproduces the forward's alpha, T and decisions bit for bit.
-__device__ __forceinline__ float eval_alpha(float4 xy, float4 co, float pxf, float pyf, float& dx, float& dy, float& G) {
-    dx = xy.x - pxf;
+// The exponent q = cx dx^2 + cy dx dy + cz dy^2 of an exp2-scaled conic at offset (dx, dy), grouped by dy:
+// (cz dy + cy dx) dy + (cx dx) dx, two fused multiply-adds after the terms in dx alone, which the backward's three
+// pixels of a column share (dx_terms); every blend evaluates it in this order, so the backward's replay reproduces
+// the forward's alpha, T and decisions bit for bit.
+struct DxTerms {
+    float dx, ydx, xdxdx;  // dx, cy dx, (cx dx) dx
+};
+__device__ __forceinline__ DxTerms dx_terms(float4 xy, float4 co, float pxf) {
+    const float dx = xy.x - pxf;
+    return DxTerms{dx, co.y * dx, (co.x * dx) * dx};
+}
+// alpha at the pixel row pyf of a column's dx terms; G receives the Gaussian factor. v_exp_f32 (a quarter-rate
+// instruction: 4 issue slots) replaces an 11-operation polynomial; its result is a fixed function of q.
+__device__ __forceinline__ float eval_alpha_row(const DxTerms& t, float4 xy, float4 co, float pyf, float& dy, float& G) {
     dy = xy.y - pyf;
-    const float q = __builtin_fmaf(dx, __builtin_fmaf(co.x, dx, co.y * dy), co.z * dy * dy);
+    const float q = __builtin_fmaf(__builtin_fmaf(co.z, dy, t.ydx), dy, t.xdxdx);
     G = __builtin_amdgcn_exp2f(fminf(q, 0.0f));
     return co.w * G;
 }
+__device__ __forceinline__ float eval_alpha(float4 xy, float4 co, float pxf, float pyf, float& dx, float& dy, float& G) {
+    const DxTerms t = dx_terms(xy, co, pxf);
+    dx = t.dx;
+    return eval_alpha_row(t, xy, co, pyf, dy, G);
+}
+
+// transmittance after a fragment of opacity a: T (1 - a) with one rounding (one instruction, where T * (1 - a) took
+// two; a = 0 leaves T bit for bit)
+__device__ __forceinline__ float transmit(float T, float a) { return __builtin_fmaf(-T, a, T); }
 
 __device__ __forceinline__ uint2 rect_of(float4 xy) { return make_uint2(__float_as_uint(xy.z), __float_as_uint(xy.w)); }
 
@@ -185,7 +203,7 @@ __global__ __launch_bounds__(tile_pixels) void blend_forward_kernel(BlendForward
                 cr = __builtin_fmaf(w, col.x, cr);
                 cg = __builtin_fmaf(w, col.y, cg);
                 cb = __builtin_fmaf(w, col.z, cb);
-                T = T * (1.0f - a_t);
+                T = transmit(T, a_t);
                 last_off = take ? off : last_off;
             };
             for (uint32_t k = 0; k < n_max; k += 2) {
@@ -527,11 +545,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
                 M &= M - 1u;
                 return j;
             };
-            // the staged float4 c of Gaussian j, addressed in the LDS address space (32-bit offsets, 24-bit product),
-            // read only as far as the walk uses it: (x, y), the conic and opacity, the colour. (An unused component
-            // read along would be a register the compiler reuses at once, waiting for the read to land.)
+            // the staged float4 c of Gaussian j, addressed in the LDS address space (32-bit offsets, one signed 24-bit
+            // multiply-add: j = all ones is -1 in 24 bits, entry 0), read only as far as the walk uses it: (x, y), the
+            // conic and opacity, the colour. (An unused component read along would be a register the compiler reuses
+            // at once, waiting for the read to land.)
             const auto at = [&](uint32_t j, uint32_t c) {
-                lds_char* const p = (lds_char*)(&s_stage[0][0]) + __umul24(j + 1u, static_cast<uint32_t>(sizeof(s_stage[0]))) + 16u * c;
+                lds_char* const p = (lds_char*)(&s_stage[1][0]) + __mul24(static_cast<int>(j), static_cast<int>(sizeof(s_stage[0]))) + 16u * c;
                 if (c == 0) {
                     const native_float2 v = *reinterpret_cast<lds_float2*>(p);
                     return make_float4(v.x, v.y, 0.0f, 0.0f);
@@ -545,12 +564,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
             };
             // (without ABS the step's w g_b sum is returned in swb and reduced with the next step's)
             const auto walk = [&](uint32_t j, uint32_t s, float4 xy, float4 co, float4 col, float& swb) {
-                float dx, sh, shdy, shdyy, swr, swg, e1 = 0.0f, e2 = 0.0f;
+                float sh, shdy, shdyy, swr, swg, e1 = 0.0f, e2 = 0.0f;
                 const float4 craw = ABS ? raw_conic_of(co) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const DxTerms xt = dx_terms(xy, co, pxf);  // (the lane's three pixels share their column)
+                const float dx = xt.dx;
 #pragma unroll
                 for (uint32_t r = 0; r < 3; r++) {
                     float dy, G;
-                    const float alpha = eval_alpha(xy, co, pxf, pyf[r], dx, dy, G);
+                    const float alpha = eval_alpha_row(xt, xy, co, pyf[r], dy, G);
                     const bool contrib = j < last_rel[r] && alpha >= min_alpha;
                     const float ae = contrib ? alpha : 0.0f;
                     const float w = T[r] * ae;
@@ -581,7 +602,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
                         e1 += fabsf(__builtin_fmaf(craw.x, hdx, craw.y * hdy));
                         e2 += fabsf(__builtin_fmaf(craw.y, hdx, craw.z * hdy));
                     }
-                    T[r] = T[r] * oma;
+                    T[r] = transmit(T[r], ae);
                 }
                 const float shdx = dx * sh;
                 float* const sw = slot0 + s * VS;
@@ -783,7 +804,7 @@ __global__ __launch_bounds__(tile_pixels) void blend_scores_kernel(BlendBackward
                 A = __builtin_fmaf(-T * ae, cg, A);
                 const float dg = co.w * __builtin_fmaf(T, cg, -rcp * (A - gbg));
                 sc[h] = contrib ? dg * dg : 0.0f;
-                T = T * oma;
+                T = transmit(T, ae);
             }
             // rows 0 + 1 and 2 + 3 (a and b of the upper group, a and b of the lower), then over the quad
             float sx = swap16_add(sc[0], sc[1]);

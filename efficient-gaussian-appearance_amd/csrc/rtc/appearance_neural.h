@@ -370,8 +370,17 @@ __device__ __forceinline__ uint32_t relu_mask2(uint32_t act) {
     asm("v_and_b32 %0, %1, %2\n\tv_pk_min_u16 %0, %0, %3" : "=&v"(m) : "s"(0x7fff7fffu), "v"(act), "s"(0x00010001u));
     return m;
 }
+// fp16 bits of (a, b), rounded to nearest even by one packed conversion (kept packed: without the register
+// constraint the compiler converts the four values of a tile one by one and packs them with byte permutes)
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t half2_bits(float a, float b) {
+    uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+    asm("" : "+v"(r));
+    return r;
+}
 __device__ __forceinline__ h4 relu_grad(f4 v, h4 act) {
-    const u16x4 x = __builtin_bit_cast(u16x4, __builtin_convertvector(v, h4));
+    const u16x4 x = __builtin_bit_cast(u16x4, make_uint2(half2_bits(v[0], v[1]), half2_bits(v[2], v[3])));
     const uint2 a = __builtin_bit_cast(uint2, act);
     const u16x4 m = __builtin_bit_cast(u16x4, make_uint2(relu_mask2(a.x), relu_mask2(a.y)));
     return __builtin_bit_cast(h4, x * m);
@@ -384,8 +393,15 @@ __device__ __forceinline__ h4 identity_tile(uint32_t lane) {
     return h4{4 * q == r ? one : z, 4 * q + 1 == r ? one : z, 4 * q + 2 == r ? one : z, 4 * q + 3 == r ? one : z};
 }
 
-// P-tile of the block whose F-tile is f
-__device__ __forceinline__ h4 transpose_tile(h4 f, h4 eye) { return __builtin_convertvector(mfma(f, eye, f4_zero()), h4); }
+// P-tile of the block whose F-tile is f: the F-tile taken as the A operand is the block's transpose, so its product
+// with the identity is the P-tile, exact (products x * 1, sums of zeros). One MFMA issue, in a pipe the kernels
+// leave mostly idle. (A store and gfx950's transposing LDS read, ds_read_b64_tr_b16, measured slower: the MLP
+// backward 60.1 -> 63.4 us on the 1M-Gaussian scene; a wave's LDS reads complete in order, so the weight
+// fragments the next MFMAs need wait behind the transposes' LDS traffic.)
+__device__ __forceinline__ h4 transpose_tile(h4 f, h4 eye) {
+    const f4 t = mfma(f, eye, f4_zero());
+    return __builtin_bit_cast(h4, make_uint2(half2_bits(t[0], t[1]), half2_bits(t[2], t[3])));
+}
 
 // input row x (INP floats) to fp16 at row `row` of a staging area (rows of XS halves)
 __device__ __forceinline__ void stage_input_row(_Float16* rows, const float* x, uint32_t row) {
@@ -494,6 +510,13 @@ __device__ inline void mlp_train(const _Float16* WL, _Float16* stage, const floa
     h4 X[4][INP / 16];
     stage_input_tiles(stage, x, X, lane);
     float* fs = reinterpret_cast<float*>(stage);
+    // the upstream gradients of primitive 16 pb + r (column block pb's output tile holds them in lane r), read
+    // before the forward so that the cross-lane reads are not waited on between the forward and the backward
+    float gsrc[4][3];
+#pragma unroll
+    for (uint32_t pb = 0; pb < 4; pb++)
+#pragma unroll
+        for (uint32_t c = 0; c < 3; c++) gsrc[pb][c] = __shfl(g[c], static_cast<int>(16 * pb + r));
 #pragma unroll
     for (uint32_t pp = 0; pp < 2; pp++) {
         // forward: F[l] = input activations of layer l >= 1 (F-tiles), P[l] = their P-tiles (P[0]: the inputs)
@@ -527,10 +550,9 @@ __device__ inline void mlp_train(const _Float16* WL, _Float16* stage, const floa
         h4 G[2][NT], GT[2];
 #pragma unroll
         for (uint32_t b = 0; b < 2; b++) {
-            const uint32_t src = 16 * (2 * pp + b) + r;
-            const float d0 = dy_of(round_half(yt[b][0]), __shfl(g[0], static_cast<int>(src)));
-            const float d1 = dy_of(round_half(yt[b][1]), __shfl(g[1], static_cast<int>(src)));
-            const float d2 = dy_of(round_half(yt[b][2]), __shfl(g[2], static_cast<int>(src)));
+            const float d0 = dy_of(round_half(yt[b][0]), gsrc[2 * pp + b][0]);
+            const float d1 = dy_of(round_half(yt[b][1]), gsrc[2 * pp + b][1]);
+            const float d2 = dy_of(round_half(yt[b][2]), gsrc[2 * pp + b][2]);
             G[b][0] = q == 0 ? h4{static_cast<_Float16>(d0 * s), static_cast<_Float16>(d1 * s), static_cast<_Float16>(d2 * s), z} : zero4;
             GT[b] = transpose_tile(G[b][0], eye);
         }

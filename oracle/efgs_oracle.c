@@ -126,11 +126,16 @@ float ef_exp2f(float x) {
     return p * scale;
 }
 
-/* exponent of the exp2-scaled conic (ex, ey, ez) at offset (dx, dy), with two fused multiply-adds: the
- * contraction nvcc applies to kernels_forward.cuh:124 by default, fixed here so host and device agree */
+/* exponent of the exp2-scaled conic (ex, ey, ez) at offset (dx, dy): the quadratic form of
+ * kernels_forward.cuh:124, ex dx^2 + ey dx dy + ez dy^2, grouped by dy as (ez dy + ey dx) dy + ex dx dx with two
+ * fused multiply-adds. The blends evaluate it in this order (the terms in dx alone are shared by the pixels of a
+ * column), so host and device agree bit for bit; the reference's grouping differs in the last bits of the exponent. */
 static float blend_exponent(float ex, float ey, float ez, float dx, float dy) {
-    return fmaf(dx, fmaf(ex, dx, ey * dy), ez * dy * dy);
+    return fmaf(fmaf(ez, dy, ey * dx), dy, (ex * dx) * dx);
 }
+
+/* transmittance after a fragment of opacity alpha, T (1 - alpha) with one rounding (as the blends compute it) */
+static float transmit(float T, float alpha) { return fmaf(-T, alpha, T); }
 
 
 static float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
@@ -592,7 +597,7 @@ void efo_blend_forward(
                 if (alpha < K_MIN_ALPHA) continue;
                 const float w = T * alpha;
                 for (int c = 0; c < 3; c++) C[c] = fmaf(w, color[3 * p + c], C[c]);
-                T *= 1.0f - alpha;
+                T = transmit(T, alpha);
                 last = i - r0 + 1;
                 if (T < k_transmittance_threshold) break;
             }
@@ -670,7 +675,7 @@ void efo_blend_backward(
                 g_mean2d[2 * p + 1] += gmy;
                 g_mean2d_abs[2 * p] += fabsf(gmx);
                 g_mean2d_abs[2 * p + 1] += fabsf(gmy);
-                T *= oma;
+                T = transmit(T, alpha);
             }
         }
     }
@@ -1213,7 +1218,7 @@ void efo_pruning_scores(
                                      grad_alpha_common * rcp;
                 const float dg = co[3] * dalpha;
                 scores[p] += dg * dg;
-                T *= oma;
+                T = transmit(T, alpha);
             }
         }
     }

@@ -84,6 +84,42 @@ def contributor_tolerance(n_pixels: int) -> int:
     return 2 + n_pixels // 100000
 
 
+# Image difference allowed at a pixel where a near-threshold decision flipped (the device's alpha uses the hardware
+# exp2, the oracle's a correctly rounded one): at the stop, the one fragment taken or skipped has weight T alpha <= 0.99 T
+# with T (1 - alpha) at the 1e-4 threshold (<= 1e-2); at a skip (alpha within an ulp of 1/255, the last contributor
+# unchanged), the fragment's weight is <= 4e-3 T and the later fragments are rescaled by the same factor; times colours
+# and background of magnitude <= 2.
+FLIPPED_PIXEL_TOL = 2e-2
+
+
+def device_contributors(bufs, v, cam) -> np.ndarray:
+    """The device's last-contributor indices in image order (H * W): the blend stores them per tile (16 x 12
+    row-major)."""
+    gw, gh = cam.grid()
+    nc = read_device(bufs, v.n_contributors, gw * gh * 192, np.uint32).reshape(gh, gw, 12, 16).transpose(0, 2, 1, 3)
+    return nc.reshape(gh * 12, gw * 16)[:cam.height, :cam.width].reshape(-1)
+
+
+def check_image(image, fw, nc, tol: float, name: str = '') -> int:
+    """Image parity: max-abs <= tol at every pixel but at most contributor_tolerance ones, where a near-threshold
+    skip or stop decision flipped (those differ by at most FLIPPED_PIXEL_TOL); the last-contributor indices nc (image
+    order) equal the oracle's at all but at most contributor_tolerance pixels. Returns the number of pixels over tol."""
+    image = np.asarray(image)
+    diff = np.abs(image - fw.image).reshape(3, -1).max(axis=0)
+    mism = int(np.count_nonzero(nc != fw.n_contrib))
+    over = diff > tol
+    n_over = int(np.count_nonzero(over))
+    err = float(diff[~over].max()) if diff.size > n_over else 0.0
+    print(f'case {name}: image max-abs {err:.3e} at all but {n_over} of {diff.size} pixels'
+          + (f' (max-abs {float(diff[over].max()):.3e} there)' if n_over else '') + f', {mism} last-contributor mismatches',
+          flush=True)
+    assert mism <= contributor_tolerance(nc.size), f'{mism} last-contributor mismatches'
+    assert n_over <= contributor_tolerance(diff.size), f'{n_over} pixels with image max-abs above {tol}'
+    if n_over:
+        assert float(diff[over].max()) <= FLIPPED_PIXEL_TOL
+    return n_over
+
+
 # ---------------------------------------------------------------------------------------------------------
 # torch side (GPU tests only)
 # ---------------------------------------------------------------------------------------------------------

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from helpers import small_case, configure, torch_inputs, settings, read_device, rel_l2
+from helpers import small_case, configure, torch_inputs, settings, read_device, rel_l2, check_image, device_contributors
 
 pytestmark = pytest.mark.gpu
 
@@ -57,7 +57,8 @@ def test_thirty_two_bit_tile_keys():
     np.testing.assert_array_equal(read_device(bufs, v.tile_sorted_keys, int(frame.n_instances), np.uint32), fw.inst_keys)
     gw, gh = cam.grid()
     np.testing.assert_array_equal(read_device(bufs, v.tile_ranges, 2 * gw * gh, np.uint32).reshape(-1, 2), fw.ranges)
-    assert np.abs(image - fw.image).max() <= 1e-4
+    # (a dense scene: almost every pixel ends within a few fragments of T = 1e-4)
+    check_image(image, fw, device_contributors(bufs, v, cam), 1e-4, '4200x3000')
 
 
 def test_near_plane_straddle():
@@ -249,7 +250,7 @@ def test_instance_buffers_sized_from_the_previous_frame(grid):
         inst_prim = read_device(bufs, v.instance_primitive, int(frame.n_instances), np.uint32)
         np.testing.assert_array_equal(inst_prim[sorted_inst], fw.inst_prims)
         np.testing.assert_array_equal(read_device(bufs, v.tile_ranges, 2 * gw * gh, np.uint32).reshape(-1, 2), fw.ranges)
-        assert np.abs(image - fw.image).max() <= 1e-4
+        check_image(image, fw, device_contributors(bufs, v, cam), 1e-4)
         assert read_device(bufs, v.counters, 8, np.uint32)[5] == 0  # overflow flag cleared by the re-run
         counts.append(int(frame.n_instances))
     assert counts[1] > counts[0] + counts[0] // 8 + 1024  # the dense frame did overflow the sparse frame's buffers

@@ -16,7 +16,7 @@ import pytest
 
 import oracle as O
 from efgs.synthetic import make_scene
-from helpers import rel_l2, configure, torch_inputs, settings, read_device, check_emission, check_first_tiles, contributor_tolerance
+from helpers import rel_l2, configure, torch_inputs, settings, read_device, check_emission, check_first_tiles, check_image, device_contributors
 
 pytestmark = pytest.mark.gpu
 
@@ -119,14 +119,7 @@ def test_full_size_parity(name):
     assert read_device(bufs, v.counters, 4, np.uint32)[2] == 0, 'instance emission disagreed with the preprocess counts'
 
     # image and last contributors
-    err = float(np.abs(image.cpu().numpy() - fw.image).max())
-    print(f'case {name}: image max-abs {err:.3e}', flush=True)
-    assert err <= (IMAGE_TOL_FP16 if neural else IMAGE_TOL)
-    nc = read_device(bufs, v.n_contributors, gw * gh * 192, np.uint32).reshape(gh, gw, 12, 16)
-    nc = nc.transpose(0, 2, 1, 3).reshape(gh * 12, gw * 16)[:cam.height, :cam.width].reshape(-1)
-    mism = np.count_nonzero(nc != fw.n_contrib)
-    print(f'case {name}: {mism} last-contributor mismatches of {nc.size}', flush=True)
-    assert mism <= contributor_tolerance(nc.size)
+    check_image(image.cpu().numpy(), fw, device_contributors(bufs, v, cam), IMAGE_TOL_FP16 if neural else IMAGE_TOL, name)
     del image, frame, bufs
 
     # gradients through the autograd path
