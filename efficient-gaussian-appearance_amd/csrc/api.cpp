@@ -894,7 +894,8 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     const InstanceLayout il = InstanceLayout::carve(static_cast<char*>(frame->instance_buffers), instance_capacity(*frame), frame->key_bytes, n_tiles);
     const uint32_t* sorted_inst = il.sorted_inst;
 
-    const size_t grad_bytes = static_cast<size_t>(n_instances > 0 ? n_instances : 1) * 12 * sizeof(float);
+    const size_t grad_bytes = static_cast<size_t>(n_instances > 0 ? n_instances : 1) *
+                              (grads->densification_rows > 2 ? record_floats_abs : record_floats) * sizeof(float);
     float* inst_grads = static_cast<float*>(alloc(alloc_ctx, grad_bytes));
     if (!inst_grads) return fail(EFGS_ERR_ALLOC, "allocation of the instance gradient buffer failed");
 

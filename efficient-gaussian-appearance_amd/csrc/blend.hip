@@ -15,7 +15,7 @@
 // pixel replays its forward walk (the evaluation is shared and compiled with -ffp-contract=off, so T and every
 // skip decision are reproduced bit-exactly; which pixels evaluate a Gaussian differs from the forward only where
 // its alpha is below 1/255, outside its screen rectangle) and forms the reference's per-pixel terms; the
-// per-Gaussian sums of each group are added in a fixed order into one 48-byte record per instance at its emission
+// per-Gaussian sums of each group are added in a fixed order into one 36-byte record per instance at its emission
 // slot. No float atomics; the result is run-to-run deterministic.
 //
 // Reference: B/rasterization/include/kernels_forward.cuh:26-166, kernels_backward.cuh:12-231.
@@ -56,11 +56,13 @@ __device__ __forceinline__ DxTerms dx_terms(float4 xy, float4 co, float pxf) {
     return DxTerms{dx, co.y * dx, (co.x * dx) * dx};
 }
 // alpha at the pixel row pyf of a column's dx terms; G receives the Gaussian factor. v_exp_f32 (a quarter-rate
-// instruction: 4 issue slots) replaces an 11-operation polynomial; its result is a fixed function of q.
+// instruction: 4 issue slots) replaces an 11-operation polynomial; its result is a fixed function of q. exp2(min(q,
+// 0)) is taken as exp2(q) clamped to [0, 1] (equal for every q that is not NaN), which the exp instruction applies
+// as its output modifier: one instruction fewer per pixel and Gaussian.
 __device__ __forceinline__ float eval_alpha_row(const DxTerms& t, float4 xy, float4 co, float pyf, float& dy, float& G) {
     dy = xy.y - pyf;
     const float q = __builtin_fmaf(__builtin_fmaf(co.z, dy, t.ydx), dy, t.xdxdx);
-    G = __builtin_amdgcn_exp2f(fminf(q, 0.0f));
+    G = fminf(fmaxf(__builtin_amdgcn_exp2f(q), 0.0f), 1.0f);  // exp2(min(q, 0)): the clamp is the exp's output modifier
     return co.w * G;
 }
 __device__ __forceinline__ float eval_alpha(float4 xy, float4 co, float pxf, float pyf, float& dx, float& dy, float& G) {
@@ -322,7 +324,7 @@ __device__ __forceinline__ float rows_reduce1(float v) {
 // Gaussians per wave instruction, and stores step s's sums at position s of its slot row of each value. The
 // combine then gives two lanes to each Gaussian of the sub-batch; they add the sixteen groups' slots in group
 // order (a per-group byte table holds the Gaussian's position in the group's walk, or an always-zero slot when
-// the group did not walk it) and write the 48-byte record at the instance's emission slot. A single wave needs
+// the group did not walk it) and write the 36-byte record at the instance's emission slot. A single wave needs
 // no block barrier: LDS accesses of a wave complete in order, and a wavefront fence keeps the compiler from
 // reordering them around the table and slot exchanges. No atomics: the result is run-to-run deterministic.
 // LIST trades walk steps against LDS (the records take (8 + extra) x 16 x LIST floats; at most 10 KB per wave
@@ -340,6 +342,14 @@ constexpr uint32_t backward_list = EFGS_BACKWARD_LIST;
 constexpr uint32_t backward_list_abs = EFGS_BACKWARD_LIST < 11 ? EFGS_BACKWARD_LIST : 11;
 constexpr uint32_t backward_groups = 16;
 constexpr uint32_t backward_chunk = 32;
+
+// Instance gradient records: dL/dmean2d (x, y), dL/dconic (x, y, z), dL/dopacity, dL/dcolour (r, g, b), then with the
+// absolute-gradient variant |dL/dmean2d| (x, y) and a pad: 9 floats (36 bytes), or 12. A record starts at a 4-byte
+// aligned address, which its 16-byte stores need (dword-aligned vector accesses to global memory).
+struct __attribute__((aligned(4))) Float4A4 {
+    float x, y, z, w;
+};
+__device__ __forceinline__ void store_record4(float* p, float4 v) { *reinterpret_cast<Float4A4*>(p) = Float4A4{v.x, v.y, v.z, v.w}; }
 
 // The bitwise OR of one value over the four lane rows, in every row.
 __device__ __forceinline__ uint32_t rows_or(uint32_t v) {
@@ -368,6 +378,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
     // reads of the extras' offsets reach past it. VS is odd: a wave step's 64 stores (four values of sixteen
     // records) and a combine read (sixteen steps of one group, two values four apart) hit distinct banks.
     constexpr uint32_t VS = n_values;
+    constexpr uint32_t RECORD = ABS ? record_floats_abs : record_floats;  // floats per instance gradient record
     constexpr uint32_t zero_rec = backward_groups * LIST;
     static_assert(LIST >= 1 && zero_rec < 256u && (VS & 1u), "record indices fit a byte");
     // (x, y, packed rect), exp2-scaled conic + opacity, colour + the instance's emission index (bits): Gaussian j
@@ -647,7 +658,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
 
             // combine: the two lanes of Gaussian cj (of this sub-batch) add its sixteen group slots in group order
             // (values 0..3 and the extras, resp. values 4..7: the second lane reads four floats on, and its reads
-            // of the extras' offsets land in the next record, unused) and write the instance's 48-byte record:
+            // of the extras' offsets land in the next record, unused) and write the instance's record (36 bytes, 48 with ABS):
             // dL/dmean2d = C (sum h d), 0.5 (sum h dx^2, sum h dx dy); 0.5 sum h dy^2, sum G dL/dalpha = -(sum of
             // h) / o, colour r, g; colour b, |dL/dmean2d| (x, y), 0. Gaussians that no group walked get zeros.
             const uint32_t cend = over ? cut : n_chunk;
@@ -669,18 +680,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
 #pragma unroll
                 for (uint32_t x = 0; x < NX; x++) asm volatile("" : "+v"(ax[x]));
                 const float4 co = s_stage[cj + 1][1];
-                // the record's 48 bytes at the instance's emission slot (a 64-bit byte offset: 48 e passes 2^32 from
-                // e = 89,478,486 on)
-                float4* const out = reinterpret_cast<float4*>(a.inst_grads) + 3u * static_cast<uint64_t>(__float_as_uint(s_stage[cj + 1][2].w));
-                // first half: quarter 0 (and quarter 2 below), second half: quarter 1, formed by selects so that
-                // both halves run one store path
+                // the record at the instance's emission slot (a 64-bit offset: 36 e passes 2^32 from e = 119,304,648 on)
+                float* const out = a.inst_grads + RECORD * static_cast<uint64_t>(__float_as_uint(s_stage[cj + 1][2].w));
+                // first half: floats 0..3 (and the extras from float 8), second half: floats 4..7, formed by selects so
+                // that both halves run one store path
                 const float4 craw = raw_conic_of(co);
                 const float q1y = -acc[1] * __builtin_amdgcn_rcpf(co.w);
                 const bool first = ch == 0u;
-                out[ch] = make_float4(first ? __builtin_fmaf(craw.x, acc[0], craw.y * acc[1]) : 0.5f * acc[0],
-                                      first ? __builtin_fmaf(craw.y, acc[0], craw.z * acc[1]) : q1y, first ? 0.5f * acc[2] : acc[2],
-                                      first ? 0.5f * acc[3] : acc[3]);
-                if (first) out[2] = make_float4(ax[0], ABS ? ax[NX > 1 ? 1 : 0] : 0.0f, ABS ? ax[NX > 2 ? 2 : 0] : 0.0f, 0.0f);
+                store_record4(out + 4u * ch, make_float4(first ? __builtin_fmaf(craw.x, acc[0], craw.y * acc[1]) : 0.5f * acc[0],
+                                                        first ? __builtin_fmaf(craw.y, acc[0], craw.z * acc[1]) : q1y,
+                                                        first ? 0.5f * acc[2] : acc[2], first ? 0.5f * acc[3] : acc[3]));
+                if (first) {
+                    if (ABS) store_record4(out + 8, make_float4(ax[0], ax[NX > 1 ? 1 : 0], ax[NX > 2 ? 2 : 0], 0.0f));
+                    else out[8] = ax[0];
+                }
             }
             if (!over) break;
             pos0 = cend;
@@ -692,11 +705,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(EFGS_BACKWAR
     // instances the tile never reached (after every pixel's last contributor) get zero records
     for (uint32_t q = n_proc + lane; q < n_total; q += 64) {
         const uint32_t e = a.sorted_inst[range.x + q];
-        float4* out = reinterpret_cast<float4*>(a.inst_grads) + 3 * static_cast<size_t>(e);
+        float* const out = a.inst_grads + RECORD * static_cast<uint64_t>(e);
         const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        out[0] = z;
-        out[1] = z;
-        out[2] = z;
+        store_record4(out, z);
+        store_record4(out + 4, z);
+        if (ABS) store_record4(out + 8, z);
+        else out[8] = 0.0f;
     }
 }
 

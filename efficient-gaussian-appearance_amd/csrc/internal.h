@@ -151,7 +151,7 @@ struct BlendBackwardArgs {
     const uint32_t* n_contrib;
     const uint32_t* tile_max;
     const uint32_t* order;         // tile of each block, heaviest first (null: block index)
-    float* inst_grads;             // (I x 12), emission order (pruning scores: one float per instance)
+    float* inst_grads;             // (I x 9, or I x 12 with abs_grads), emission order (pruning scores: one float per instance)
     uint32_t width, height, grid_w, n_tiles;
     uint32_t abs_grads;            // also reduce |dL/dmean2d| (third densification row)
 };

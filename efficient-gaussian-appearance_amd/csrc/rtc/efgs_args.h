@@ -54,7 +54,7 @@ struct PreprocessBackwardArgs {
     const uint32_t* n_touched;
     const uint32_t* prim_offset;     // (N) first emitted instance of each visible primitive
     const PrimRecord* records;
-    const float* inst_grads;         // (I x 12) per-instance blend gradients, emission order
+    const float* inst_grads;         // (I x 9, or I x 12 with three densification rows) per-instance blend gradients, emission order
     float* g_means;
     float* g_scales;
     float* g_rotations;

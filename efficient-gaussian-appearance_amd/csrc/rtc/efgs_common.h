@@ -44,6 +44,10 @@ struct PrimRecord {
 // further tiles are tested wave-cooperatively, by the preprocess and again by instance emission
 constexpr uint32_t n_sequential_tiles = 4;
 static_assert(n_sequential_tiles <= 32, "the first-tiles mask is one 32-bit word of the record");
+// floats per instance gradient record of the blend backward (dL/dmean2d 2, dL/dconic 3, dL/dopacity, dL/dcolour 3;
+// with |dL/dmean2d| for three densification rows: 2 more and a pad)
+constexpr uint32_t record_floats = 9;
+constexpr uint32_t record_floats_abs = 12;
 
 // ---------------------------------------------------------------------------------------------------------
 // deterministic exp / log

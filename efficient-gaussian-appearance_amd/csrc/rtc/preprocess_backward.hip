@@ -1,8 +1,8 @@
 // Backward preprocess, runtime-specialised with hipRTC (same preamble and headers as the forward).
 //
-// One thread per primitive. The blend backward leaves one 12-float gradient record per emitted instance
-// (dL/dmean2d xy, dL/dconic xyz, dL/dopacity, dL/dcolor rgb, |dL/dmean2d| xy, pad) at the instance's
-// emission slot; a visible primitive's slots are contiguous, so this kernel reduces them in a fixed order
+// One thread per primitive. The blend backward leaves one gradient record per emitted instance (dL/dmean2d xy,
+// dL/dconic xyz, dL/dopacity, dL/dcolor rgb: 9 floats; with three densification rows also |dL/dmean2d| xy and a
+// pad: 12) at the instance's emission slot; a visible primitive's slots are contiguous, so this kernel reduces them in a fixed order
 // (deterministic, no float atomics), applies the opacity chain, backpropagates the colour through the
 // activations and the appearance model, and the 2D mean and conic through the EWA projection to the 3D mean,
 // log-scales and quaternion. Culled primitives get zero gradients.
@@ -33,20 +33,37 @@ __device__ __forceinline__ void add_record(float4& s0, float4& s1, float4& s2, f
     s2.x += t2.x; s2.y += t2.y; s2.z += t2.z;
 }
 
+// four floats of a record at a 4-byte aligned address (one 16-byte load: dword-aligned vector accesses to global
+// memory need no more)
+struct __attribute__((aligned(4))) Float4A4 {
+    float x, y, z, w;
+};
+__device__ __forceinline__ float4 load_record4(const float* p) {
+    const Float4A4 v = *reinterpret_cast<const Float4A4*>(p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // sum of a visible primitive's per-instance gradient records (starting at emission slot `offset`), in
-// emission order; two records are fetched per step so their loads are in flight together
-__device__ inline InstanceGrads reduce_instance_grads(const PreprocessBackwardArgs& a, uint32_t offset, uint32_t touched) {
-    const float4* ig = reinterpret_cast<const float4*>(a.inst_grads) + 3 * static_cast<size_t>(offset);
+// emission order; two records are fetched per step so their loads are in flight together. Records are
+// record_floats_abs floats with three densification rows (|dL/dmean2d| after the colour), record_floats otherwise.
+template <uint32_t RECORD>
+__device__ inline InstanceGrads reduce_instance_grads_of(const PreprocessBackwardArgs& a, uint32_t offset, uint32_t touched) {
+    const float* ig = a.inst_grads + RECORD * static_cast<size_t>(offset);
+    const auto third = [&](uint32_t k) { return RECORD == record_floats ? make_float4(ig[RECORD * k + 8], 0.0f, 0.0f, 0.0f) : load_record4(ig + RECORD * k + 8); };
     float4 s0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = s0, s2 = s0;
     uint32_t k = 0;
     for (; k + 2 <= touched; k += 2) {
-        const float4 t0 = ig[3 * k], t1 = ig[3 * k + 1], t2 = ig[3 * k + 2];
-        const float4 u0 = ig[3 * k + 3], u1 = ig[3 * k + 4], u2 = ig[3 * k + 5];
+        const float4 t0 = load_record4(ig + RECORD * k), t1 = load_record4(ig + RECORD * k + 4), t2 = third(k);
+        const float4 u0 = load_record4(ig + RECORD * (k + 1)), u1 = load_record4(ig + RECORD * (k + 1) + 4), u2 = third(k + 1);
         add_record(s0, s1, s2, t0, t1, t2);
         add_record(s0, s1, s2, u0, u1, u2);
     }
-    if (k < touched) add_record(s0, s1, s2, ig[3 * k], ig[3 * k + 1], ig[3 * k + 2]);
+    if (k < touched) add_record(s0, s1, s2, load_record4(ig + RECORD * k), load_record4(ig + RECORD * k + 4), third(k));
     return {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w, s2.x, s2.y, s2.z};
+}
+__device__ inline InstanceGrads reduce_instance_grads(const PreprocessBackwardArgs& a, uint32_t offset, uint32_t touched) {
+    return a.densification_rows > 2 ? reduce_instance_grads_of<record_floats_abs>(a, offset, touched)
+                                    : reduce_instance_grads_of<record_floats>(a, offset, touched);
 }
 
 // a primitive's parameters, loaded before its instance records are summed so that every load is in flight at once
