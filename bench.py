@@ -140,8 +140,8 @@ def read_step_kernel_us():
 
 
 def read_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, if it lists the kernel:
-    lines `traffic <kernel> <fetch_bytes> <write_bytes>` (already scaled by the copy-kernel calibration)."""
+    """L2-to-fabric bytes per launch of `kernel` (read + write) from the committed rocprofv3 TCC summary, if it lists
+    the kernel: lines `traffic <kernel> <read_bytes> <write_bytes>`, requests counted by size (128 / 64 / 32 bytes)."""
     if not os.path.exists(TRAFFIC_FILE):
         return None
     with open(TRAFFIC_FILE) as f:
