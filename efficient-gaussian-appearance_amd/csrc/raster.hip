@@ -490,8 +490,13 @@ __global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_r
 // within its 64-tile block plus that count), or + the next slot of an atomic cursor (without one). The slot
 // receives the instance's sort key, the depth key of its primitive above its emission index. Each block first
 // scans the per-64-tile block sums into dynamic LDS (256 at a time with a running carry), one entry per 64-tile
-// block: up to max_scan_blocks of them (1,015,808 tiles); larger grids add the block sums per instance.
+// block: up to max_scan_blocks of them (1,015,808 tiles); larger grids add the block sums per instance. A thread
+// takes bucket_per_thread instances (256 apart, so every load stays coalesced) and issues the loads of all of them
+// before their gathers and those before the stores: the kernel waits on memory, and a quarter of the waves then keep
+// four times the requests in flight each (and a quarter of the blocks repeat the block-sum scan).
 constexpr uint32_t max_scan_blocks = static_cast<uint32_t>((tile_hist_max_lds - 2048) / 4);
+constexpr uint32_t bucket_per_thread = 4;
+constexpr uint32_t bucket_chunk = 256 * bucket_per_thread;  // instances per block
 template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
                                                           const uint32_t* table, const uint32_t* local_rank, const uint32_t* block_sums,
@@ -507,13 +512,40 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     }
     const uint32_t block = blockIdx.x - 1u;
     const uint32_t n_instances = counters[1];
-    const uint32_t n_chunks = (n_instances + 255u) / 256u;
+    const uint32_t n_chunks = (n_instances + bucket_chunk - 1u) / bucket_chunk;
     if (block >= n_chunks) return;  // (block-uniform: the grid covers a bound on I)
     // XCD-aware chunk: the hardware deals workgroups to the 8 XCDs round robin (workgroup w on XCD w % 8, so bucket
     // block b on XCD (b + 1) % 8); the blocks of one XCD take one contiguous run of the chunks, so the table rows of
     // a segment (whose instances are contiguous) are fetched into one XCD's L2 instead of all eight
     const uint32_t xcd = block % 8u, per = n_chunks / 8u, extra = n_chunks % 8u;
     const uint32_t chunk = xcd * per + min(xcd, extra) + block / 8u;
+    // the instances' tile keys, primitives and ranks (clamped indices past the count: every load unconditional, all
+    // in flight together), then the depth keys and table entries they select, then the slots
+    uint32_t e[bucket_per_thread], t[bucket_per_thread], prim[bucket_per_thread], rank[bucket_per_thread];
+    const uint32_t last = n_instances - 1u;
+#pragma unroll
+    for (uint32_t k = 0; k < bucket_per_thread; k++) {
+        e[k] = chunk * bucket_chunk + k * 256u + threadIdx.x;
+        const uint32_t ec = min(e[k], last);
+        t[k] = static_cast<uint32_t>(keys[ec]);
+        prim[k] = inst_prim[ec];
+        rank[k] = table ? local_rank[ec] : 0u;
+    }
+    uint32_t depth[bucket_per_thread], pos[bucket_per_thread];
+#pragma unroll
+    for (uint32_t k = 0; k < bucket_per_thread; k++) {
+        // (an instance past the count or padded after an emission mismatch has no rank: table row 0, tile 0)
+        const bool valid = e[k] < n_instances && t[k] < n_tiles;
+        const uint32_t tc = valid ? t[k] : 0u, r = valid ? rank[k] : 0u;
+        depth[k] = depth_keys[prim[k]];
+        pos[k] = 0;
+        if (table) {  // the table entry already holds the tile's start within its block
+            pos[k] = table[static_cast<size_t>(r >> rank_segment_shift) * n_tiles + tc] + (r & ((1u << rank_segment_shift) - 1u));
+        } else if (valid) {
+            pos[k] = local_start[tc] + atomicAdd(&cursor[tc], 1u);
+        }
+    }
+    // the block sums' prefix (after the instances' loads and gathers were issued: those do not wait for it)
     const uint32_t n_blocks = (n_tiles + scan_tiles - 1) / scan_tiles;
     if (n_blocks <= max_scan_blocks) {
         const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -531,25 +563,18 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
             __syncthreads();  // s_waves read by every wave before the next pass writes it (and s_prefix complete)
         }
     }
-    const uint32_t e = chunk * 256u + threadIdx.x;
-    if (e >= n_instances) return;
-    const uint32_t t = static_cast<uint32_t>(keys[e]);
-    if (t >= n_tiles) return;
-    const uint64_t key = (static_cast<uint64_t>(depth_keys[inst_prim[e]]) << 32) | e;
-    const uint32_t b = t / scan_tiles;
-    uint32_t pos = 0;
-    if (n_blocks <= max_scan_blocks) {
-        pos = s_prefix[b];
-    } else {
-        for (uint32_t k = 0; k < b; k++) pos += block_sums[k];
+#pragma unroll
+    for (uint32_t k = 0; k < bucket_per_thread; k++) {
+        if (e[k] >= n_instances || t[k] >= n_tiles) continue;
+        const uint32_t b = t[k] / scan_tiles;
+        uint32_t base = 0;
+        if (n_blocks <= max_scan_blocks) {
+            base = s_prefix[b];
+        } else {
+            for (uint32_t j = 0; j < b; j++) base += block_sums[j];
+        }
+        bucket[base + pos[k]] = (static_cast<uint64_t>(depth[k]) << 32) | e[k];
     }
-    if (table) {  // the table entry already holds the tile's start within its block
-        const uint32_t r = local_rank[e];
-        pos += table[static_cast<size_t>(r >> rank_segment_shift) * n_tiles + t] + (r & ((1u << rank_segment_shift) - 1u));
-    } else {
-        pos += local_start[t] + atomicAdd(&cursor[t], 1u);
-    }
-    bucket[pos] = key;
 }
 
 // orders a wave's own LDS accesses across the steps of a network (the LDS executes a wave's instructions in
@@ -892,8 +917,8 @@ bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_byte
         EFGS_HIP_CHECK(hipGetLastError());
         return true;
     }
-    // one block that places the tile order's runs, then one block per 256 instances (a bound on I)
-    const uint32_t blocks = div_up(max_instances, 256) + 1;
+    // one block that places the tile order's runs, then one block per bucket_chunk instances (a bound on I)
+    const uint32_t blocks = div_up(max_instances, bucket_chunk) + 1;
     const uint32_t* tab = plan.use_table ? table : nullptr;
     const uint32_t prefix_bytes = order_blocks <= max_scan_blocks ? order_blocks * 4u : 0u;  // (order_blocks: the 64-tile blocks)
     if (key_bytes == 2)

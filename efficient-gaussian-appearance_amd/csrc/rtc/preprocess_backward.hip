@@ -451,6 +451,11 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
         const uint32_t p = a.visible_prims[contributes ? v_idx : 0u];
         const float4 dpre = contributes ? reinterpret_cast<const float4*>(a.color_grads)[p] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+        // the geometry kernel's mean and base gradients, which this chunk adds to, loaded with its inputs (their
+        // stores then wait for no load of their own after the MLP)
+        float3 gm = make_float3(0.0f, 0.0f, 0.0f), gb = gm;
+        if (EFGS_DIRECTION_GRADIENT) gm = make_float3(a.g_means[3 * p], a.g_means[3 * p + 1], a.g_means[3 * p + 2]);
+        if (EFGS_BASE_INPUT) gb = make_float3(a.g_base[3 * p], a.g_base[3 * p + 1], a.g_base[3 * p + 2]);
         const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
         float norm_rcp;
         const float3 d = view_direction(mean, cam, norm_rcp);
@@ -470,14 +475,15 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
 #pragma unroll
             for (uint32_t i = 0; i < nn::FEATURES; i++) gp[i] = nn::feature_grad(feat[i], dx, i);
             if (EFGS_BASE_INPUT) {
-#pragma unroll
-                for (uint32_t c = 0; c < 3; c++) a.g_base[3 * p + c] += nn::feature_grad(a.base[3 * p + c], dx, nn::FEATURES + c);
+                a.g_base[3 * p] = gb.x + nn::feature_grad(a.base[3 * p], dx, nn::FEATURES);
+                a.g_base[3 * p + 1] = gb.y + nn::feature_grad(a.base[3 * p + 1], dx, nn::FEATURES + 1);
+                a.g_base[3 * p + 2] = gb.z + nn::feature_grad(a.base[3 * p + 2], dx, nn::FEATURES + 2);
             }
             if (EFGS_DIRECTION_GRADIENT) {
                 const float3 dm = direction_grad_to_mean(nn::direction_grad(d, degree, dx), d, norm_rcp);
-                a.g_means[3 * p] += dm.x;
-                a.g_means[3 * p + 1] += dm.y;
-                a.g_means[3 * p + 2] += dm.z;
+                a.g_means[3 * p] = gm.x + dm.x;
+                a.g_means[3 * p + 1] = gm.y + dm.y;
+                a.g_means[3 * p + 2] = gm.z + dm.z;
             }
         }
     }
