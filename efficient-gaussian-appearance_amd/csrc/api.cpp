@@ -252,9 +252,10 @@ struct InstanceLayout {
     uint32_t* inst_prim;     // primitive per emission slot
     uint32_t* local_rank;    // rank of each instance among its segment's instances of its tile | segment << 24
     uint32_t* table;         // per segment and tile: the tile's count in the earlier segments (rows for every segment)
-    uint64_t* bucket;        // sort keys grouped by tile (depth key << 32 | emission index)
+    uint4* bucket;           // per tile slot: emission index, depth key, primitive, 0 (sort key: the low 8 bytes)
     uint32_t* sorted_inst;   // emission slots in (tile, depth, primitive) order
     void* sorted_keys;       // tile key of every sorted instance
+    uint32_t* sorted_prim;   // primitive of every sorted instance
     size_t bytes;
 
     static InstanceLayout carve(char* base, uint64_t n_instances, int key_bytes, uint32_t n_tiles) {
@@ -266,9 +267,10 @@ struct InstanceLayout {
         l.inst_prim = c.take<uint32_t>(ni);
         l.local_rank = c.take<uint32_t>(use_table ? ni : 1);
         l.table = c.take<uint32_t>(use_table ? static_cast<uint64_t>(tile_hist_max_blocks) * n_tiles : 1);
-        l.bucket = c.take<uint64_t>(ni);
+        l.bucket = c.take<uint4>(ni);
         l.sorted_inst = c.take<uint32_t>(ni);
         l.sorted_keys = c.take_bytes(key_bytes * ni);
+        l.sorted_prim = c.take<uint32_t>(ni);
         l.bytes = c.offset + buffer_alignment;
         return l;
     }
@@ -781,13 +783,12 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
             return EFGS_ERR_HIP;
         t.end(s);
         t.begin(EFGS_STAGE_TILE_SORT, s);
-        if (!launch_tile_sort(ts, tl.ranges, il.bucket, il.sorted_inst, il.sorted_keys, key_bytes, n_tiles, s)) return EFGS_ERR_HIP;
+        if (!launch_tile_sort(ts, tl.ranges, il.bucket, il.sorted_inst, il.sorted_keys, key_bytes, il.inst_prim, il.sorted_prim, n_tiles, s)) return EFGS_ERR_HIP;
         t.end(s);
 
         BlendForwardArgs b;
         b.ranges = tl.ranges;
-        b.sorted_inst = il.sorted_inst;
-        b.inst_prim = il.inst_prim;
+        b.sorted_prim = il.sorted_prim;
         b.records = pl.records;
         b.bg = settings->bg_color;
         b.image = image;
@@ -902,7 +903,7 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     BlendBackwardArgs b;
     b.ranges = tl.ranges;
     b.sorted_inst = sorted_inst;
-    b.inst_prim = il.inst_prim;
+    b.sorted_prim = il.sorted_prim;
     b.records = pl.records;
     b.bg = settings->bg_color;
     b.image = image;
@@ -1039,7 +1040,7 @@ int efgs_update_pruning_scores(efgs_rasterizer* r, const efgs_primitives* prims,
     std::memset(&b, 0, sizeof(b));
     b.ranges = tl.ranges;
     b.sorted_inst = il.sorted_inst;
-    b.inst_prim = il.inst_prim;
+    b.sorted_prim = il.sorted_prim;
     b.records = pl.records;
     b.bg = settings->bg_color;
     b.image = image;

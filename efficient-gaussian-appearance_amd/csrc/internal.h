@@ -111,20 +111,20 @@ struct TileScan {
 // count itself from ts.counters)
 bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes, uint32_t max_instances, uint32_t* table, const TileScan& ts,
                         uint32_t n_tiles, hipStream_t s);
-// every instance's sort key (depth key of its primitive << 32 | emission index) into a slot of its tile's range
+// every instance's bucket entry (emission index, depth key of its primitive, primitive, 0; the low 8 bytes are the
+// sort key depth key << 32 | emission index) into a slot of its tile's range
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
-                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t max_instances,
+                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint4* bucket, uint32_t max_instances,
                          uint32_t n_tiles, hipStream_t s);
-// per tile: [start, end) into ranges and its keys sorted ascending -> emission indices in sorted_inst, tile id
-// in sorted_keys
-bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
-                      uint32_t n_tiles, hipStream_t s);
+// per tile: [start, end) into ranges and its keys sorted ascending -> emission indices in sorted_inst, their
+// primitives (from the bucket entries, or gathered from inst_prim) in sorted_prim, tile id in sorted_keys
+bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint4* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
+                      const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t n_tiles, hipStream_t s);
 bool launch_reduce_partials(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out, hipStream_t s);
 
 struct BlendForwardArgs {
     const uint2* ranges;
-    const uint32_t* sorted_inst;   // emission index per sorted instance
-    const uint32_t* inst_prim;     // primitive per emission index
+    const uint32_t* sorted_prim;   // primitive per sorted instance
     const PrimRecord* records;
     const float* bg;
     float* image;                  // (3, H, W), or (H, W, 3) with hwc
@@ -141,8 +141,8 @@ bool launch_blend_forward(const BlendForwardArgs& a, hipStream_t s);
 
 struct BlendBackwardArgs {
     const uint2* ranges;
-    const uint32_t* sorted_inst;
-    const uint32_t* inst_prim;
+    const uint32_t* sorted_inst;   // emission index per sorted instance
+    const uint32_t* sorted_prim;   // primitive per sorted instance
     const PrimRecord* records;
     const float* bg;
     const float* image;

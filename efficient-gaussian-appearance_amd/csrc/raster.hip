@@ -9,11 +9,14 @@
 //                       their instances per tile in an LDS histogram (ranks from the atomics' return values);
 //   tile_column_scan    the segments' counts per tile -> prefixes over the segments, tile totals and starts,
 //                       and each tile's size class for the blends' heaviest-first tile order;
-//   tile_buckets        every instance writes its sort key at tile start + earlier segments' count + rank; one
-//                       extra block turns the size-class counts into the tile order's run positions meanwhile;
+//   tile_buckets        every instance writes its entry (emission index, depth key, primitive) at tile start +
+//                       earlier segments' count + rank; one extra block turns the size-class counts into the
+//                       tile order's run positions meanwhile;
 //   tile_sort           one wave per tile sorts its slots by (depth key, emission index): keys are
 //                       unique, so the order is a deterministic function of the inputs (the emission index
-//                       increases with the primitive index, so ties in depth keep primitive-index order).
+//                       increases with the primitive index, so ties in depth keep primitive-index order); it
+//                       writes the emission indices and the primitives in that order, so the blends read both
+//                       as coalesced arrays instead of gathering each instance's primitive.
 // Compiled with -ffp-contract=off: instance emission re-evaluates the tile test of the preprocess and must
 // reproduce its counts exactly.
 // Reference: B/rasterization/include/kernels_common.cuh:20-157, B/rasterization/src/forward.cu:82-221.
@@ -500,7 +503,7 @@ constexpr uint32_t bucket_chunk = 256 * bucket_per_thread;  // instances per blo
 template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
                                                           const uint32_t* table, const uint32_t* local_rank, const uint32_t* block_sums,
-                                                          const uint32_t* local_start, uint32_t* cursor, uint64_t* bucket, const uint32_t* counters,
+                                                          const uint32_t* local_start, uint32_t* cursor, uint4* bucket, const uint32_t* counters,
                                                           uint32_t n_tiles, uint32_t* order_runs, uint32_t order_blocks) {
     extern __shared__ uint32_t s_prefix[];  // n_blocks entries (the launch sizes it; none above max_scan_blocks)
     __shared__ uint32_t s_waves[4];
@@ -573,7 +576,7 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
         } else {
             for (uint32_t j = 0; j < b; j++) base += block_sums[j];
         }
-        bucket[base + pos[k]] = (static_cast<uint64_t>(depth[k]) << 32) | e[k];
+        bucket[base + pos[k]] = make_uint4(e[k], depth[k], prim[k], 0u);  // one 16-byte store: key (low 8 bytes) and primitive
     }
 }
 
@@ -639,24 +642,65 @@ __device__ __forceinline__ void wave_bitonic(uint64_t (&k)[K], uint32_t lane) {
     }
 }
 
+// A bucket entry: emission index, depth key, primitive, 0 (the first eight bytes, little-endian, are the sort key
+// depth key << 32 | emission index).
+__device__ __forceinline__ uint64_t key_of(uint4 b) { return (static_cast<uint64_t>(b.y) << 32) | b.x; }
+
+// Where a tile's sorted instances go: the emission index, the instance's primitive and the tile key. The bucket
+// holds each key's primitive beside it. Runs of at most 256 keys whose emission indices fit 24 bits sort the key
+// (depth << 32 | e << 8 | u), u the key's index in the run: e is unique, so the order is that of (depth, e), and
+// the primitive is read back from the wave's slab at u (put_packed). Other runs gather it from inst_prim (put).
+template <typename KeyT>
+struct SortedOut {
+    uint32_t* inst;
+    uint32_t* prim;
+    KeyT* keys;
+    const uint32_t* inst_prim;
+    uint32_t tile;
+    __device__ __forceinline__ void put(uint32_t pos, uint64_t key) const {
+        const uint32_t e = static_cast<uint32_t>(key);
+        inst[pos] = e;
+        prim[pos] = inst_prim[e];
+        keys[pos] = static_cast<KeyT>(tile);
+    }
+    __device__ __forceinline__ void put_packed(uint32_t pos, uint64_t key, const uint32_t* s_prim) const {
+        const uint32_t lo = static_cast<uint32_t>(key);
+        inst[pos] = lo >> 8;
+        prim[pos] = s_prim[lo & 0xffu];
+        keys[pos] = static_cast<KeyT>(tile);
+    }
+};
+// the sort key of run index u (< 256) when every emission index fits 24 bits
+__device__ __forceinline__ uint64_t pack_run_index(uint64_t key, uint32_t u) {
+    return (key & 0xffffffff00000000ull) | (static_cast<uint64_t>(static_cast<uint32_t>(key) << 8)) | u;
+}
+
 // n <= 64 K keys of the tile's run, sorted in registers (K keys per lane, element x = K lane + i), written out
 template <uint32_t K, typename KeyT>
-__device__ __forceinline__ void sort_run_in_registers(const uint64_t* run, uint32_t n, uint32_t* out, KeyT* out_keys, uint32_t tile, uint32_t lane) {
+__device__ __forceinline__ void sort_run_in_registers(const uint4* run, uint32_t n, const SortedOut<KeyT>& o, uint32_t lane, bool packed,
+                                                      uint32_t* s_prim) {
     uint64_t k[K];
 #pragma unroll
     for (uint32_t i = 0; i < K; i++) {
         const uint32_t x = K * lane + i;
-        k[i] = x < n ? run[x] : ~0ull;
+        const uint4 b = x < n ? run[x] : make_uint4(~0u, ~0u, 0u, 0u);
+        k[i] = key_of(b);
+        if (packed && x < n) {
+            s_prim[x] = b.z;
+            k[i] = pack_run_index(k[i], x);
+        }
     }
+    wave_lds_fence();
     wave_bitonic<K>(k, lane);
 #pragma unroll
     for (uint32_t i = 0; i < K; i++) {
         const uint32_t x = K * lane + i;
         if (x < n) {
-            out[x] = static_cast<uint32_t>(k[i]);
-            out_keys[x] = static_cast<KeyT>(tile);
+            if (packed) o.put_packed(x, k[i], s_prim);
+            else o.put(x, k[i]);
         }
     }
+    wave_lds_fence();  // (the slab is free again after every lane's reads)
 }
 
 // ascending bitonic sort of m (a power of two, <= wave_slab) keys in the wave's slab
@@ -688,17 +732,37 @@ __device__ __forceinline__ uint32_t rank_in(const uint64_t* run, uint32_t n, uin
     return lo;
 }
 
+// number of keys below x in the ascending run of bucket entries [0, n)
+__device__ __forceinline__ uint32_t rank_in_bucket(const uint4* run, uint32_t n, uint64_t x) {
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (key_of(run[mid]) < x) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
 // 128 < n <= 192: the first 128 keys (two per lane) and the other n - 128 (one per lane) are sorted by their own
 // register networks and merged: a key's position is its index in its own sorted part plus the number of keys of
 // the other part below it (keys are unique), found by binary search in the wave's slab. About half the work of
 // the 256-key network the run would otherwise be padded to.
 template <typename KeyT>
-__device__ __forceinline__ void sort_run_split192(const uint64_t* run, uint32_t n, uint32_t* out, KeyT* out_keys, uint32_t tile,
-                                                  uint32_t lane, uint64_t* s) {
-    uint64_t a[2], b[1];
-    a[0] = run[2 * lane];
-    a[1] = run[2 * lane + 1];
-    b[0] = 128 + lane < n ? run[128 + lane] : ~0ull;
+__device__ __forceinline__ void sort_run_split192(const uint4* run, uint32_t n, const SortedOut<KeyT>& o, uint32_t lane, uint64_t* s,
+                                                  bool packed) {
+    const uint4 ba0 = run[2 * lane], ba1 = run[2 * lane + 1];
+    const uint4 bb0 = 128 + lane < n ? run[128 + lane] : make_uint4(~0u, ~0u, 0u, 0u);
+    uint64_t a[2] = {key_of(ba0), key_of(ba1)}, b[1] = {key_of(bb0)};
+    uint32_t* const s_prim = reinterpret_cast<uint32_t*>(s + 256);  // (the keys take s[0 .. 192))
+    if (packed) {
+        s_prim[2 * lane] = ba0.z;
+        s_prim[2 * lane + 1] = ba1.z;
+        a[0] = pack_run_index(a[0], 2 * lane);
+        a[1] = pack_run_index(a[1], 2 * lane + 1);
+        if (128 + lane < n) {
+            s_prim[128 + lane] = bb0.z;
+            b[0] = pack_run_index(b[0], 128 + lane);
+        }
+    }
     wave_bitonic<2>(a, lane);
     wave_bitonic<1>(b, lane);
     s[2 * lane] = a[0];
@@ -709,13 +773,13 @@ __device__ __forceinline__ void sort_run_split192(const uint64_t* run, uint32_t 
 #pragma unroll
     for (uint32_t i = 0; i < 2; i++) {
         const uint32_t pos = 2 * lane + i + rank_in(s + 128, nb, a[i]);
-        out[pos] = static_cast<uint32_t>(a[i]);
-        out_keys[pos] = static_cast<KeyT>(tile);
+        if (packed) o.put_packed(pos, a[i], s_prim);
+        else o.put(pos, a[i]);
     }
     if (lane < nb) {
         const uint32_t pos = lane + rank_in(s, 128, b[0]);
-        out[pos] = static_cast<uint32_t>(b[0]);
-        out_keys[pos] = static_cast<KeyT>(tile);
+        if (packed) o.put_packed(pos, b[0], s_prim);
+        else o.put(pos, b[0]);
     }
     wave_lds_fence();  // the slab is free again only after every lane's searches
 }
@@ -724,7 +788,8 @@ template <typename KeyT>
 __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* totals, const uint32_t* block_sums,
                                                                    const uint32_t* local_start, const uint32_t* order_runs,
                                                                    const uint32_t* order_rank, uint32_t* order, const uint32_t* counters, uint2* ranges,
-                                                                   uint64_t* bucket, uint32_t* sorted_inst, KeyT* sorted_keys, uint32_t n_tiles) {
+                                                                   uint4* bucket, uint32_t* sorted_inst, KeyT* sorted_keys,
+                                                                   const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t n_tiles) {
     if (counters[counter_overflow] != 0) return;
     __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -739,59 +804,56 @@ __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32
         order[order_runs[static_cast<size_t>(tile / scan_tiles) * order_classes + (cr >> 16)] + (cr & 0xffffu)] = tile;
     }
     if (n == 0) return;
-    uint64_t* run = bucket + r.x;
-    uint32_t* out = sorted_inst + r.x;
-    KeyT* out_keys = sorted_keys + r.x;
+    uint4* run = bucket + r.x;
+    const SortedOut<KeyT> o{sorted_inst + r.x, sorted_prim + r.x, sorted_keys + r.x, inst_prim, tile};
+    uint64_t* s = s_slab[wave];
+    uint32_t* const s_prim = reinterpret_cast<uint32_t*>(s);
+    const bool packed = counters[1] < (1u << 24) - 1u;  // every emission index fits 24 bits (and no key packs to all ones)
     if (n <= 64) {  // wave-uniform size classes: the smallest network that holds the run
-        sort_run_in_registers<1>(run, n, out, out_keys, tile, lane);
+        sort_run_in_registers<1>(run, n, o, lane, packed, s_prim);
         return;
     }
     if (n <= 128) {
-        sort_run_in_registers<2>(run, n, out, out_keys, tile, lane);
+        sort_run_in_registers<2>(run, n, o, lane, packed, s_prim);
         return;
     }
-    uint64_t* s = s_slab[wave];
     if (n <= 192) {
-        sort_run_split192(run, n, out, out_keys, tile, lane, s);
+        sort_run_split192(run, n, o, lane, s, packed);
         return;
     }
     if (n <= 256) {
-        sort_run_in_registers<4>(run, n, out, out_keys, tile, lane);
+        sort_run_in_registers<4>(run, n, o, lane, packed, s_prim);
         return;
     }
     if (n <= wave_slab) {
         uint32_t m = 512;
         while (m < n) m <<= 1;
-        for (uint32_t x = lane; x < m; x += 64) s[x] = x < n ? run[x] : ~0ull;
+        for (uint32_t x = lane; x < m; x += 64) s[x] = x < n ? key_of(run[x]) : ~0ull;
         wave_lds_fence();
         wave_bitonic_lds(s, m, lane);
-        for (uint32_t x = lane; x < n; x += 64) {
-            out[x] = static_cast<uint32_t>(s[x]);
-            out_keys[x] = static_cast<KeyT>(tile);
-        }
+        for (uint32_t x = lane; x < n; x += 64) o.put(x, s[x]);
         return;
     }
     const uint32_t n_chunks = (n + wave_slab - 1) / wave_slab;
     for (uint32_t c = 0; c < n_chunks; c++) {
         const uint32_t c0 = c * wave_slab, cn = min(wave_slab, n - c0);
-        for (uint32_t x = lane; x < wave_slab; x += 64) s[x] = x < cn ? run[c0 + x] : ~0ull;
+        for (uint32_t x = lane; x < wave_slab; x += 64) s[x] = x < cn ? key_of(run[c0 + x]) : ~0ull;
         wave_lds_fence();
         wave_bitonic_lds(s, wave_slab, lane);
-        for (uint32_t x = lane; x < cn; x += 64) run[c0 + x] = s[x];
+        for (uint32_t x = lane; x < cn; x += 64) run[c0 + x] = make_uint4(static_cast<uint32_t>(s[x]), static_cast<uint32_t>(s[x] >> 32), 0u, 0u);
         wave_lds_fence();
     }
     __threadfence();  // the wave reads back the chunks it wrote
     for (uint32_t idx = lane; idx < n; idx += 64) {
-        const uint64_t key = run[idx];
+        const uint64_t key = key_of(run[idx]);
         const uint32_t c = idx / wave_slab;
         uint32_t pos = idx - c * wave_slab;
-        for (uint32_t o = 0; o < n_chunks; o++) {
-            if (o == c) continue;
-            const uint32_t o0 = o * wave_slab;
-            pos += rank_in(run + o0, min(wave_slab, n - o0), key);
+        for (uint32_t oc = 0; oc < n_chunks; oc++) {
+            if (oc == c) continue;
+            const uint32_t o0 = oc * wave_slab;
+            pos += rank_in_bucket(run + o0, min(wave_slab, n - o0), key);
         }
-        out[pos] = static_cast<uint32_t>(key);
-        out_keys[pos] = static_cast<KeyT>(tile);
+        o.put(pos, key);
     }
 }
 
@@ -908,7 +970,7 @@ bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes
 }
 
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
-                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint64_t* bucket, uint32_t max_instances,
+                         const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint4* bucket, uint32_t max_instances,
                          uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
     const uint32_t order_blocks = div_up(n_tiles, scan_tiles);
@@ -931,16 +993,16 @@ bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_byte
     return true;
 }
 
-bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint64_t* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
-                      uint32_t n_tiles, hipStream_t s) {
+bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint4* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
+                      const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
     const uint32_t blocks = div_up(n_tiles, tile_sort_waves);
     if (key_bytes == 2)
         tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ts.counters, ranges, bucket, sorted_inst,
-                                                                     static_cast<uint16_t*>(sorted_keys), n_tiles);
+                                                                     static_cast<uint16_t*>(sorted_keys), inst_prim, sorted_prim, n_tiles);
     else
         tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ts.counters, ranges, bucket, sorted_inst,
-                                                                     static_cast<uint32_t*>(sorted_keys), n_tiles);
+                                                                     static_cast<uint32_t*>(sorted_keys), inst_prim, sorted_prim, n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }
