@@ -226,6 +226,7 @@ struct TileLayout {
     uint32_t* order_runs;    // per 64-tile block and size class: tiles, then the run's first position in the order
     uint32_t* order_rank;    // per tile: size class << 16 | rank in its block's run
     uint32_t* order;         // tile of each blend block, heaviest first
+    uint32_t* big_tiles;     // tiles whose runs the tile sort sorts (longer than the forward blend sorts)
     size_t bytes;
 
     static TileLayout carve(char* base, uint32_t n_tiles) {
@@ -242,6 +243,7 @@ struct TileLayout {
         l.order_runs = c.take<uint32_t>(static_cast<uint64_t>(div_up(n_tiles > 0 ? n_tiles : 1, 64)) * order_classes);
         l.order_rank = c.take<uint32_t>(n_tiles);
         l.order = c.take<uint32_t>(n_tiles);
+        l.big_tiles = c.take<uint32_t>(n_tiles);
         l.bytes = c.offset + buffer_alignment;
         return l;
     }
@@ -773,7 +775,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
         if (!launch_create_instances(ca, key_bytes, plan, il.local_rank, il.table, n_tiles, fused ? &fa : nullptr, s)) return EFGS_ERR_HIP;
         t.end(s);
-        const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor, tl.order_runs, tl.order_rank, tl.order, pl.counters};
+        const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor, tl.order_runs, tl.order_rank, tl.order, pl.counters, tl.big_tiles};
         t.begin(EFGS_STAGE_TILE_OFFSETS, s);
         if (!launch_tile_counts(plan, il.keys, key_bytes, max_instances, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
         t.end(s);
@@ -788,7 +790,13 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
 
         BlendForwardArgs b;
         b.ranges = tl.ranges;
+        b.bucket = il.bucket;
+        b.sorted_inst = il.sorted_inst;
         b.sorted_prim = il.sorted_prim;
+        b.sorted_keys = il.sorted_keys;
+        b.inst_prim = il.inst_prim;
+        b.counters = pl.counters;
+        b.key_bytes = static_cast<uint32_t>(key_bytes);
         b.records = pl.records;
         b.bg = settings->bg_color;
         b.image = image;

@@ -19,6 +19,7 @@
 //
 // Reference: B/rasterization/include/kernels_forward.cuh:26-166, kernels_backward.cuh:12-231.
 #include "internal.h"
+#include "tile_sort.h"
 
 namespace efgs {
 
@@ -136,8 +137,6 @@ __device__ __forceinline__ void cull_groups8(uint2 rect, uint32_t idx, uint32_t 
     }
 }
 
-// orders a wave's LDS accesses around its list writes (lanes read entries other lanes wrote)
-__device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
 // Sums of several per-lane values over the four 16-lane rows (and, in the 4x4 groups of the score kernel, over
 // a row quad) at once ("transposing" reductions). Each exchange step swaps half of the values between lanes so
@@ -278,12 +277,16 @@ __device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
 // pixel per lane, that this replaced: 14 % fewer VALU instructions and a third of the LDS reads per pixel, at the
 // same time, 70.6 against 70.5 us on the 1M-Gaussian 1080p scene: both waited on the gather chain emission index
 // -> primitive -> record; with the primitives read from the sorted array it takes 57 us.)
+template <typename KeyT>
 __global__ __launch_bounds__(64) void blend_forward_kernel(BlendForwardArgs a) {
     if (a.overflow && *a.overflow != 0) return;  // the binning was skipped: the host re-runs the frame
     constexpr uint32_t CHUNK = 32;
     constexpr uint32_t RING = 2 * CHUNK;
-    // ring entry r: (x, y, packed pixel rectangle), exp2-scaled conic + opacity, colour; entry RING: opacity 0
+    // ring entry r: (x, y, packed pixel rectangle), exp2-scaled conic + opacity, colour; entry RING: opacity 0.
+    // Before the walk its first 3 KB are the sort's scratch.
     __shared__ float4 s_stage[RING + 1][3];
+    __shared__ uint32_t s_sorted_prim[forward_sort_max];  // the run's primitives in sorted order, when sorted here
+    static_assert(sizeof(s_stage) >= 3072, "the sort's scratch fits the stage");
 
     const uint32_t lane = threadIdx.x;
     const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
@@ -295,6 +298,16 @@ __global__ __launch_bounds__(64) void blend_forward_kernel(BlendForwardArgs a) {
     const float pxf = static_cast<float>(px) + 0.5f;
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
+    // A run that fits the register networks is sorted here (the tile sort leaves it): the emission indices,
+    // primitives and tile keys in (depth, primitive) order for the backward, the primitives also into LDS for the walk.
+    const bool own_sort = n_total <= forward_sort_max;  // (wave-uniform)
+    if (own_sort && n_total > 0) {
+        const SortedOut<KeyT> o{a.sorted_inst + range.x, a.sorted_prim + range.x, static_cast<KeyT*>(a.sorted_keys) + range.x, a.inst_prim,
+                                tile, s_sorted_prim};
+        const bool packed = a.counters[1] < (1u << 24) - 1u;  // every emission index fits 24 bits (and no key packs to all ones)
+        sort_small_run(a.bucket + range.x, n_total, o, lane, packed, reinterpret_cast<uint64_t*>(&s_stage[0][0]));
+        wave_lds_fence();
+    }
     if (lane < 3) s_stage[RING][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
     // A pixel is done (takes no further Gaussian) exactly when T < transmittance_threshold: T changes only when a
@@ -313,11 +326,12 @@ __global__ __launch_bounds__(64) void blend_forward_kernel(BlendForwardArgs a) {
     }
 
     // The records of a chunk's instances are gathered through a two-stage pipeline over the chunks: while chunk c
-    // is walked, the primitive indices of chunk c + 3 (the sorted array: coalesced) and the records of chunk c + 2
-    // are loaded (indices clamped to the tile's last instance; lanes past CHUNK repeat lane CHUNK - 1).
+    // is walked, the primitive indices of chunk c + 3 (from LDS, or the sorted array: coalesced) and the records of
+    // chunk c + 2 are loaded (indices clamped to the tile's last instance; lanes past CHUNK repeat lane CHUNK - 1).
     const uint32_t gather_lane = min(lane, CHUNK - 1u);
     const uint32_t last_inst = n_total > 0 ? n_total - 1u : 0u;
-    const auto load_p = [&](uint32_t s) { return a.sorted_prim[range.x + min(s + gather_lane, last_inst)]; };
+    const uint32_t* const prim_src = own_sort ? s_sorted_prim : a.sorted_prim + range.x;
+    const auto load_p = [&](uint32_t s) { return prim_src[min(s + gather_lane, last_inst)]; };
     const auto stage = [&](uint32_t half, uint32_t s, const PrimRecord& rec) {
         if (lane < CHUNK && s + lane < n_total) {
             float4* const d = s_stage[half * CHUNK + lane];
@@ -961,7 +975,10 @@ __global__ __launch_bounds__(256) void accumulate_scores_kernel(const uint32_t* 
 
 bool launch_blend_forward(const BlendForwardArgs& a, hipStream_t s) {
     if (a.n_tiles == 0) return true;
-    blend_forward_kernel<<<a.n_tiles, 64, 0, s>>>(a);
+    if (a.key_bytes == 2)
+        blend_forward_kernel<uint16_t><<<a.n_tiles, 64, 0, s>>>(a);
+    else
+        blend_forward_kernel<uint32_t><<<a.n_tiles, 64, 0, s>>>(a);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

@@ -21,6 +21,7 @@
 // reproduce its counts exactly.
 // Reference: B/rasterization/include/kernels_common.cuh:20-157, B/rasterization/src/forward.cu:82-221.
 #include "internal.h"
+#include "tile_sort.h"
 
 namespace efgs {
 
@@ -278,6 +279,7 @@ __global__ __launch_bounds__(fused_block) void create_instances_fused_kernel(Cre
             if (k != 2) a.counters[k] = c[k];
             f.host_counters[k] = c[k];
         }
+        a.counters[counter_big_tiles] = 0u;
         __threadfence_system();
         __hip_atomic_store(&f.host_counters[counter_sequence], f.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         __threadfence_system();
@@ -580,128 +582,19 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     }
 }
 
-// orders a wave's own LDS accesses across the steps of a network (the LDS executes a wave's instructions in
-// order; the fence keeps the compiler from moving them)
-__device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
-
-// Per-tile sort: one wave per tile, four tiles per block, no block barriers. Keys are unique 64-bit values
-// (depth key << 32 | emission index), sorted ascending by bitonic networks:
+// Per-tile sort: one wave per tile, four tiles per block, no block barriers (the tiles' ranges come from
+// tile_ranges_kernel, launched before). Keys are unique 64-bit values (depth key << 32 | emission index), sorted
+// ascending by bitonic networks:
 //   n <= 64, 128, 256 in registers, K = 1, 2, 4 keys per lane (element x = K lane + i): exchanges at distance
 //                     j < K within a lane, j >= K with the lane at xor distance j / K (128 < n <= 192: a
-//                     128-key and a 64-key network merged by rank);
+//                     128-key and a 64-key network merged by rank); these runs are sorted by the forward blend
+//                     of the tile (tile_sort.h), before its walk, which saves this kernel their loads and writes;
 //   256 < n <= 512    in the wave's LDS slab;
 //   n > 512           chunks of 512 sorted in the slab and written back to the tile's range, then every key
 //                     placed at (its index in its chunk) + (its rank in each other chunk).
 constexpr uint32_t tile_sort_waves = 4;
 constexpr uint32_t tile_sort_block = 64 * tile_sort_waves;
 constexpr uint32_t wave_slab = 512;
-
-// The value of lane (lane ^ d) (d a power of two below 64, a constant after unrolling): one DPP move within a row
-// for d = 1, 2 (quad permutations) and 8 (row rotation by 8), an LDS permute otherwise (the row swaps of gfx950
-// overwrite both operands: two copies and a select per exchange cost more VALU than the permute).
-__device__ __forceinline__ uint32_t xor_lane(uint32_t v, uint32_t d) {
-    if (d == 1) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xb1, 0xf, 0xf, true));  // quad_perm [1,0,3,2]
-    if (d == 2) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4e, 0xf, 0xf, true));  // quad_perm [2,3,0,1]
-    if (d == 8) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xf, 0xf, true));  // row_ror:8
-    return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), static_cast<int>(d)));
-}
-__device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v, uint32_t d) {
-    const uint32_t lo = xor_lane(static_cast<uint32_t>(v), d);
-    const uint32_t hi = xor_lane(static_cast<uint32_t>(v >> 32), d);
-    return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
-template <uint32_t K>
-__device__ __forceinline__ void wave_bitonic(uint64_t (&k)[K], uint32_t lane) {
-#pragma unroll
-    for (uint32_t size = 2; size <= 64 * K; size <<= 1) {
-#pragma unroll
-        for (uint32_t j = size >> 1; j > 0; j >>= 1) {
-            if (j >= K) {
-#pragma unroll
-                for (uint32_t i = 0; i < K; i++) {
-                    const uint32_t x = K * lane + i;
-                    const uint64_t o = xor_lane_u64(k[i], j / K);
-                    const bool keep_min = ((x & size) == 0) == ((x & j) == 0);
-                    // the partner's key belongs here exactly when it is the smaller one where the lane keeps the
-                    // minimum and the larger one elsewhere: one compare and one select (equal keys: either)
-                    k[i] = (o < k[i]) == keep_min ? o : k[i];
-                }
-            } else {
-#pragma unroll
-                for (uint32_t i = 0; i < K; i++) {
-                    if ((i & j) != 0) continue;
-                    const uint32_t x = K * lane + i;
-                    const uint64_t a = k[i], b = k[i ^ j];
-                    const bool swap = (a > b) == ((x & size) == 0);
-                    k[i] = swap ? b : a;
-                    k[i ^ j] = swap ? a : b;
-                }
-            }
-        }
-    }
-}
-
-// A bucket entry: emission index, depth key, primitive, 0 (the first eight bytes, little-endian, are the sort key
-// depth key << 32 | emission index).
-__device__ __forceinline__ uint64_t key_of(uint4 b) { return (static_cast<uint64_t>(b.y) << 32) | b.x; }
-
-// Where a tile's sorted instances go: the emission index, the instance's primitive and the tile key. The bucket
-// holds each key's primitive beside it. Runs of at most 256 keys whose emission indices fit 24 bits sort the key
-// (depth << 32 | e << 8 | u), u the key's index in the run: e is unique, so the order is that of (depth, e), and
-// the primitive is read back from the wave's slab at u (put_packed). Other runs gather it from inst_prim (put).
-template <typename KeyT>
-struct SortedOut {
-    uint32_t* inst;
-    uint32_t* prim;
-    KeyT* keys;
-    const uint32_t* inst_prim;
-    uint32_t tile;
-    __device__ __forceinline__ void put(uint32_t pos, uint64_t key) const {
-        const uint32_t e = static_cast<uint32_t>(key);
-        inst[pos] = e;
-        prim[pos] = inst_prim[e];
-        keys[pos] = static_cast<KeyT>(tile);
-    }
-    __device__ __forceinline__ void put_packed(uint32_t pos, uint64_t key, const uint32_t* s_prim) const {
-        const uint32_t lo = static_cast<uint32_t>(key);
-        inst[pos] = lo >> 8;
-        prim[pos] = s_prim[lo & 0xffu];
-        keys[pos] = static_cast<KeyT>(tile);
-    }
-};
-// the sort key of run index u (< 256) when every emission index fits 24 bits
-__device__ __forceinline__ uint64_t pack_run_index(uint64_t key, uint32_t u) {
-    return (key & 0xffffffff00000000ull) | (static_cast<uint64_t>(static_cast<uint32_t>(key) << 8)) | u;
-}
-
-// n <= 64 K keys of the tile's run, sorted in registers (K keys per lane, element x = K lane + i), written out
-template <uint32_t K, typename KeyT>
-__device__ __forceinline__ void sort_run_in_registers(const uint4* run, uint32_t n, const SortedOut<KeyT>& o, uint32_t lane, bool packed,
-                                                      uint32_t* s_prim) {
-    uint64_t k[K];
-#pragma unroll
-    for (uint32_t i = 0; i < K; i++) {
-        const uint32_t x = K * lane + i;
-        const uint4 b = x < n ? run[x] : make_uint4(~0u, ~0u, 0u, 0u);
-        k[i] = key_of(b);
-        if (packed && x < n) {
-            s_prim[x] = b.z;
-            k[i] = pack_run_index(k[i], x);
-        }
-    }
-    wave_lds_fence();
-    wave_bitonic<K>(k, lane);
-#pragma unroll
-    for (uint32_t i = 0; i < K; i++) {
-        const uint32_t x = K * lane + i;
-        if (x < n) {
-            if (packed) o.put_packed(x, k[i], s_prim);
-            else o.put(x, k[i]);
-        }
-    }
-    wave_lds_fence();  // (the slab is free again after every lane's reads)
-}
 
 // ascending bitonic sort of m (a power of two, <= wave_slab) keys in the wave's slab
 __device__ inline void wave_bitonic_lds(uint64_t* s, uint32_t m, uint32_t lane) {
@@ -722,16 +615,6 @@ __device__ inline void wave_bitonic_lds(uint64_t* s, uint32_t m, uint32_t lane) 
     }
 }
 
-// number of keys below x in the ascending run [0, n)
-__device__ __forceinline__ uint32_t rank_in(const uint64_t* run, uint32_t n, uint64_t x) {
-    uint32_t lo = 0, hi = n;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (run[mid] < x) lo = mid + 1; else hi = mid;
-    }
-    return lo;
-}
-
 // number of keys below x in the ascending run of bucket entries [0, n)
 __device__ __forceinline__ uint32_t rank_in_bucket(const uint4* run, uint32_t n, uint64_t x) {
     uint32_t lo = 0, hi = n;
@@ -742,89 +625,33 @@ __device__ __forceinline__ uint32_t rank_in_bucket(const uint4* run, uint32_t n,
     return lo;
 }
 
-// 128 < n <= 192: the first 128 keys (two per lane) and the other n - 128 (one per lane) are sorted by their own
-// register networks and merged: a key's position is its index in its own sorted part plus the number of keys of
-// the other part below it (keys are unique), found by binary search in the wave's slab. About half the work of
-// the 256-key network the run would otherwise be padded to.
-template <typename KeyT>
-__device__ __forceinline__ void sort_run_split192(const uint4* run, uint32_t n, const SortedOut<KeyT>& o, uint32_t lane, uint64_t* s,
-                                                  bool packed) {
-    const uint4 ba0 = run[2 * lane], ba1 = run[2 * lane + 1];
-    const uint4 bb0 = 128 + lane < n ? run[128 + lane] : make_uint4(~0u, ~0u, 0u, 0u);
-    uint64_t a[2] = {key_of(ba0), key_of(ba1)}, b[1] = {key_of(bb0)};
-    uint32_t* const s_prim = reinterpret_cast<uint32_t*>(s + 256);  // (the keys take s[0 .. 192))
-    if (packed) {
-        s_prim[2 * lane] = ba0.z;
-        s_prim[2 * lane + 1] = ba1.z;
-        a[0] = pack_run_index(a[0], 2 * lane);
-        a[1] = pack_run_index(a[1], 2 * lane + 1);
-        if (128 + lane < n) {
-            s_prim[128 + lane] = bb0.z;
-            b[0] = pack_run_index(b[0], 128 + lane);
-        }
-    }
-    wave_bitonic<2>(a, lane);
-    wave_bitonic<1>(b, lane);
-    s[2 * lane] = a[0];
-    s[2 * lane + 1] = a[1];
-    s[128 + lane] = b[0];
-    wave_lds_fence();
-    const uint32_t nb = n - 128;
-#pragma unroll
-    for (uint32_t i = 0; i < 2; i++) {
-        const uint32_t pos = 2 * lane + i + rank_in(s + 128, nb, a[i]);
-        if (packed) o.put_packed(pos, a[i], s_prim);
-        else o.put(pos, a[i]);
-    }
-    if (lane < nb) {
-        const uint32_t pos = lane + rank_in(s, 128, b[0]);
-        if (packed) o.put_packed(pos, b[0], s_prim);
-        else o.put(pos, b[0]);
-    }
-    wave_lds_fence();  // the slab is free again only after every lane's searches
+// Every tile's range and its place in the blends' tile order, one tile per lane: a wave's 64 tiles are one scan
+// block, so the wave computes the prefix of the block sums once for all of them. Tiles with runs longer than
+// forward_sort_max are listed for the tile sort (in any order: each run's sort is independent of the others).
+__global__ __launch_bounds__(256) void tile_ranges_kernel(const uint32_t* totals, const uint32_t* block_sums, const uint32_t* local_start,
+                                                          const uint32_t* order_runs, const uint32_t* order_rank, uint32_t* order,
+                                                          uint32_t* counters, uint32_t* big_tiles, uint2* ranges, uint32_t n_tiles) {
+    static_assert(scan_tiles == 64, "one scan block per wave");
+    if (counters[counter_overflow] != 0) return;
+    const uint32_t lane = threadIdx.x & 63u, tile = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t tile0 = tile - lane;
+    if (tile0 >= n_tiles) return;  // the whole wave
+    const uint32_t prefix = scan_block_prefix_wave(block_sums, tile0 / scan_tiles, lane);
+    if (tile >= n_tiles) return;
+    const uint32_t n = totals[tile];
+    const uint32_t start = prefix + local_start[tile];
+    ranges[tile] = n > 0 ? make_uint2(start, start + n) : make_uint2(0u, 0u);  // (0, 0) for an empty tile, as the reference
+    const uint32_t cr = order_rank[tile];
+    order[order_runs[static_cast<size_t>(tile / scan_tiles) * order_classes + (cr >> 16)] + (cr & 0xffffu)] = tile;
+    if (n > forward_sort_max) big_tiles[atomicAdd(&counters[counter_big_tiles], 1u)] = tile;
 }
 
+// One run of n > forward_sort_max keys (the wave's slab s: wave_slab keys).
 template <typename KeyT>
-__global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* totals, const uint32_t* block_sums,
-                                                                   const uint32_t* local_start, const uint32_t* order_runs,
-                                                                   const uint32_t* order_rank, uint32_t* order, const uint32_t* counters, uint2* ranges,
-                                                                   uint4* bucket, uint32_t* sorted_inst, KeyT* sorted_keys,
-                                                                   const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t n_tiles) {
-    if (counters[counter_overflow] != 0) return;
-    __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t tile = blockIdx.x * tile_sort_waves + wave;
-    if (tile >= n_tiles) return;  // the whole wave (no block barriers below)
-    const uint32_t n = totals[tile];
-    const uint32_t start = scan_block_prefix_wave(block_sums, tile / scan_tiles, lane) + local_start[tile];
-    const uint2 r = n > 0 ? make_uint2(start, start + n) : make_uint2(0u, 0u);  // (0, 0) for an empty tile, as the reference
-    if (lane == 0) {
-        ranges[tile] = r;
-        const uint32_t cr = order_rank[tile];
-        order[order_runs[static_cast<size_t>(tile / scan_tiles) * order_classes + (cr >> 16)] + (cr & 0xffffu)] = tile;
-    }
-    if (n == 0) return;
+__device__ void sort_big_run(uint4* bucket, uint2 r, uint32_t n, uint32_t tile, uint32_t* sorted_inst, KeyT* sorted_keys,
+                             const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t lane, uint64_t* s) {
     uint4* run = bucket + r.x;
-    const SortedOut<KeyT> o{sorted_inst + r.x, sorted_prim + r.x, sorted_keys + r.x, inst_prim, tile};
-    uint64_t* s = s_slab[wave];
-    uint32_t* const s_prim = reinterpret_cast<uint32_t*>(s);
-    const bool packed = counters[1] < (1u << 24) - 1u;  // every emission index fits 24 bits (and no key packs to all ones)
-    if (n <= 64) {  // wave-uniform size classes: the smallest network that holds the run
-        sort_run_in_registers<1>(run, n, o, lane, packed, s_prim);
-        return;
-    }
-    if (n <= 128) {
-        sort_run_in_registers<2>(run, n, o, lane, packed, s_prim);
-        return;
-    }
-    if (n <= 192) {
-        sort_run_split192(run, n, o, lane, s, packed);
-        return;
-    }
-    if (n <= 256) {
-        sort_run_in_registers<4>(run, n, o, lane, packed, s_prim);
-        return;
-    }
+    const SortedOut<KeyT> o{sorted_inst + r.x, sorted_prim + r.x, sorted_keys + r.x, inst_prim, tile, nullptr};
     if (n <= wave_slab) {
         uint32_t m = 512;
         while (m < n) m <<= 1;
@@ -854,6 +681,24 @@ __global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32
             pos += rank_in_bucket(run + o0, min(wave_slab, n - o0), key);
         }
         o.put(pos, key);
+    }
+}
+
+// The tile_ranges_kernel's list of long runs, one run per wave at a time (a grid of at most 256 blocks: for short
+// runs only, the usual case, the kernel reads the count and ends).
+template <typename KeyT>
+__global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* counters, const uint32_t* big_tiles, const uint2* ranges,
+                                                                   uint4* bucket, uint32_t* sorted_inst, KeyT* sorted_keys,
+                                                                   const uint32_t* inst_prim, uint32_t* sorted_prim) {
+    if (counters[counter_overflow] != 0) return;
+    __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t n_big = counters[counter_big_tiles];
+    for (uint32_t idx = blockIdx.x * tile_sort_waves + wave; idx < n_big; idx += gridDim.x * tile_sort_waves) {
+        const uint32_t tile = big_tiles[idx];
+        const uint2 r = ranges[tile];
+        sort_big_run(bucket, r, r.y - r.x, tile, sorted_inst, sorted_keys, inst_prim, sorted_prim, lane, s_slab[wave]);
+        wave_lds_fence();  // (the slab is reused by the next run)
     }
 }
 
@@ -996,13 +841,16 @@ bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_byte
 bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint4* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
                       const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
-    const uint32_t blocks = div_up(n_tiles, tile_sort_waves);
+    tile_ranges_kernel<<<div_up(n_tiles, 256), 256, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order,
+                                                            ts.counters, ts.big_tiles, ranges, n_tiles);
+    EFGS_HIP_CHECK(hipGetLastError());
+    const uint32_t blocks = min(div_up(n_tiles, tile_sort_waves), 256u);
     if (key_bytes == 2)
-        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ts.counters, ranges, bucket, sorted_inst,
-                                                                     static_cast<uint16_t*>(sorted_keys), inst_prim, sorted_prim, n_tiles);
+        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.counters, ts.big_tiles, ranges, bucket, sorted_inst, static_cast<uint16_t*>(sorted_keys),
+                                                                     inst_prim, sorted_prim);
     else
-        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order, ts.counters, ranges, bucket, sorted_inst,
-                                                                     static_cast<uint32_t*>(sorted_keys), inst_prim, sorted_prim, n_tiles);
+        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.counters, ts.big_tiles, ranges, bucket, sorted_inst, static_cast<uint32_t*>(sorted_keys),
+                                                                     inst_prim, sorted_prim);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

@@ -61,6 +61,28 @@ def test_thirty_two_bit_tile_keys():
     check_image(image, fw, device_contributors(bufs, v, cam), 1e-4, '4200x3000')
 
 
+def test_long_tile_runs():
+    # Tile runs longer than the forward blend sorts itself (256): the tile sort's LDS-slab (<= 512) and chunked paths,
+    # beside runs the forward sorts; the order, ranges, the blend's primitives and the image match the oracle.
+    scene, app, cam = small_case(model='precomputed', n=3000, width=96, height=72, scale_shift=3.0)
+    fw = O.render(scene, app, cam)
+    runs = np.diff(np.asarray(fw.ranges).reshape(-1, 2), axis=1)[:, 0]
+    assert (runs > 512).any() and ((runs > 256) & (runs <= 512)).any() and ((runs > 0) & (runs <= 256)).any()
+    image, frame, bufs = _render(scene, app, cam)
+    from efgs.rasterization import frame_views
+    v = frame_views(frame)
+    I = int(frame.n_instances)
+    assert I == len(fw.inst_keys)
+    gw, gh = cam.grid()
+    np.testing.assert_array_equal(read_device(bufs, v.tile_ranges, 2 * gw * gh, np.uint32).reshape(-1, 2), fw.ranges)
+    kt = np.uint16 if frame.key_bytes == 2 else np.uint32
+    np.testing.assert_array_equal(read_device(bufs, v.tile_sorted_keys, I, kt).astype(np.uint32), fw.inst_keys)
+    sorted_inst = read_device(bufs, v.tile_sorted_instances, I, np.uint32)
+    inst_prim = read_device(bufs, v.instance_primitive, I, np.uint32)
+    np.testing.assert_array_equal(inst_prim[sorted_inst], fw.inst_prims)
+    check_image(image, fw, device_contributors(bufs, v, cam), 1e-4, 'long runs')
+
+
 def test_near_plane_straddle():
     scene, app, cam = small_case(model='sh', n=400, distance=2.0)  # camera inside the cube: many behind / near
     image, frame, _ = _render(scene, app, cam)
