@@ -55,7 +55,7 @@ STAGE_KERNELS = {
     'create_instances': 'create_instances_fused_kernel',
     'tile_offsets': 'tile_column_scan_kernel',  # (the tile order's runs are placed by an extra block of tile_buckets_kernel)
     'tile_buckets': 'tile_buckets_kernel',
-    'tile_sort': 'tile_sort_kernel',
+    'tile_sort': 'tile_ranges_kernel',  # (the tiles' runs are sorted by blend_forward_kernel, before its walk)
     'blend_forward': 'blend_forward_kernel',
     'blend_backward': 'blend_backward_kernel',
     'preprocess_backward': 'preprocess_backward_<model>',
@@ -104,7 +104,8 @@ def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_
     emission V*40 + I*6 (with the compaction fused into the emission kernel, as on grids whose tile histogram fits
     its LDS: V*48 + I*6 for that one kernel, and no compaction stage), tile ranges T*8; the ordering by (tile, depth) -- the reference's depth sort and
     offset scan (V*24) and tile sort (I*12) -- split into the bucketing (I*6: tile key in, emission index
-    out) and the per-tile sort (I*6 + V*24); blend forward I*48 + P*20; blend backward P*32 + I*76;
+    out) and the per-tile sort (I*6 + V*24), which the forward blend runs before its walk; the tiles' ranges and
+    order T*24 (three words in, two out); blend forward I*48 + P*20 (+ the sort); blend backward P*32 + I*76;
     preprocess backward V*(110+R) + N*(56+R), for the neural model split into the geometry kernel
     (V*110 + N*56 + (N-V)*R: culled primitives' zero latent gradients) and the MLP kernel (V*2R: latents in,
     latent gradients out); Adam 28 B per element. MLP FLOPs: forward V*F, backward (input and weight
@@ -115,8 +116,8 @@ def algorithmic(stage: str, N: int, V: int, I: int, T: int, P: int, R: int, mlp_
         'create_instances': (V * (48 if compaction_fused else 40) + I * 6, 0),
         'tile_offsets': (T * 8, 0),
         'tile_buckets': (I * 6, 0),
-        'tile_sort': (I * 6 + V * 24, 0),
-        'blend_forward': (I * 48 + P * 20, 0),
+        'tile_sort': (T * 24, 0),
+        'blend_forward': (I * 48 + P * 20 + I * 6 + V * 24, 0),
         'blend_backward': (P * 32 + I * 76, 0),
         'preprocess_backward': ((V * 110 + N * 56 + (N - V) * R, 0) if mlp_fwd_flops
                                 else (V * (110 + R) + N * (56 + R), 0)),

@@ -226,7 +226,6 @@ struct TileLayout {
     uint32_t* order_runs;    // per 64-tile block and size class: tiles, then the run's first position in the order
     uint32_t* order_rank;    // per tile: size class << 16 | rank in its block's run
     uint32_t* order;         // tile of each blend block, heaviest first
-    uint32_t* big_tiles;     // tiles whose runs the tile sort sorts (longer than the forward blend sorts)
     size_t bytes;
 
     static TileLayout carve(char* base, uint32_t n_tiles) {
@@ -243,7 +242,6 @@ struct TileLayout {
         l.order_runs = c.take<uint32_t>(static_cast<uint64_t>(div_up(n_tiles > 0 ? n_tiles : 1, 64)) * order_classes);
         l.order_rank = c.take<uint32_t>(n_tiles);
         l.order = c.take<uint32_t>(n_tiles);
-        l.big_tiles = c.take<uint32_t>(n_tiles);
         l.bytes = c.offset + buffer_alignment;
         return l;
     }
@@ -775,7 +773,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         t.begin(EFGS_STAGE_CREATE_INSTANCES, s);
         if (!launch_create_instances(ca, key_bytes, plan, il.local_rank, il.table, n_tiles, fused ? &fa : nullptr, s)) return EFGS_ERR_HIP;
         t.end(s);
-        const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor, tl.order_runs, tl.order_rank, tl.order, pl.counters, tl.big_tiles};
+        const TileScan ts{tl.totals, tl.local_start, tl.block_sums, tl.cursor, tl.order_runs, tl.order_rank, tl.order, pl.counters};
         t.begin(EFGS_STAGE_TILE_OFFSETS, s);
         if (!launch_tile_counts(plan, il.keys, key_bytes, max_instances, il.table, ts, n_tiles, s)) return EFGS_ERR_HIP;
         t.end(s);
@@ -785,7 +783,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
             return EFGS_ERR_HIP;
         t.end(s);
         t.begin(EFGS_STAGE_TILE_SORT, s);
-        if (!launch_tile_sort(ts, tl.ranges, il.bucket, il.sorted_inst, il.sorted_keys, key_bytes, il.inst_prim, il.sorted_prim, n_tiles, s)) return EFGS_ERR_HIP;
+        if (!launch_tile_ranges(ts, tl.ranges, n_tiles, s)) return EFGS_ERR_HIP;
         t.end(s);
 
         BlendForwardArgs b;

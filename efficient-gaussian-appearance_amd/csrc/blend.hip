@@ -282,11 +282,12 @@ __global__ __launch_bounds__(64) void blend_forward_kernel(BlendForwardArgs a) {
     if (a.overflow && *a.overflow != 0) return;  // the binning was skipped: the host re-runs the frame
     constexpr uint32_t CHUNK = 32;
     constexpr uint32_t RING = 2 * CHUNK;
-    // ring entry r: (x, y, packed pixel rectangle), exp2-scaled conic + opacity, colour; entry RING: opacity 0.
-    // Before the walk its first 3 KB are the sort's scratch.
-    __shared__ float4 s_stage[RING + 1][3];
-    __shared__ uint32_t s_sorted_prim[forward_sort_max];  // the run's primitives in sorted order, when sorted here
-    static_assert(sizeof(s_stage) >= 3072, "the sort's scratch fits the stage");
+    // The sort's slab (wave_slab keys), which the stage reuses for the walk: ring entry r (x, y, packed pixel
+    // rectangle), exp2-scaled conic + opacity, colour; entry RING: opacity 0.
+    __shared__ __align__(16) uint64_t s_slab[wave_slab];
+    float4 (*const s_stage)[3] = reinterpret_cast<float4 (*)[3]>(s_slab);
+    static_assert(sizeof(s_slab) >= (RING + 1) * 3 * sizeof(float4), "the stage fits the slab");
+    __shared__ uint32_t s_sorted_prim[forward_sort_max];  // a register-sorted run's primitives in sorted order
 
     const uint32_t lane = threadIdx.x;
     const uint32_t tile = a.order ? a.order[blockIdx.x] : blockIdx.x;  // heaviest tiles first
@@ -298,14 +299,21 @@ __global__ __launch_bounds__(64) void blend_forward_kernel(BlendForwardArgs a) {
     const float pxf = static_cast<float>(px) + 0.5f;
     const uint2 range = a.ranges[tile];
     const uint32_t n_total = range.y - range.x;
-    // A run that fits the register networks is sorted here (the tile sort leaves it): the emission indices,
-    // primitives and tile keys in (depth, primitive) order for the backward, the primitives also into LDS for the walk.
-    const bool own_sort = n_total <= forward_sort_max;  // (wave-uniform)
-    if (own_sort && n_total > 0) {
-        const SortedOut<KeyT> o{a.sorted_inst + range.x, a.sorted_prim + range.x, static_cast<KeyT*>(a.sorted_keys) + range.x, a.inst_prim,
-                                tile, s_sorted_prim};
-        const bool packed = a.counters[1] < (1u << 24) - 1u;  // every emission index fits 24 bits (and no key packs to all ones)
-        sort_small_run(a.bucket + range.x, n_total, o, lane, packed, reinterpret_cast<uint64_t*>(&s_stage[0][0]));
+    // The tile's run is sorted here: the emission indices, primitives and tile keys in (depth, primitive) order for
+    // the backward; a run that fits the register networks also leaves its primitives in LDS for the walk, a longer
+    // one (LDS slab, chunks) is read back from the sorted array.
+    const bool in_regs = n_total <= forward_sort_max;  // (wave-uniform)
+    if (n_total > 0) {
+        if (in_regs) {
+            const SortedOut<KeyT> o{a.sorted_inst + range.x, a.sorted_prim + range.x, static_cast<KeyT*>(a.sorted_keys) + range.x,
+                                    a.inst_prim, tile, s_sorted_prim};
+            const bool packed = a.counters[1] < (1u << 24) - 1u;  // every emission index fits 24 bits (and no key packs to all ones)
+            sort_small_run(a.bucket + range.x, n_total, o, lane, packed, s_slab);
+        } else {
+            sort_big_run(a.bucket, range, n_total, tile, a.sorted_inst, static_cast<KeyT*>(a.sorted_keys), a.inst_prim, a.sorted_prim, lane,
+                         s_slab);
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");  // the wave reads back the primitives its lanes wrote
+        }
         wave_lds_fence();
     }
     if (lane < 3) s_stage[RING][lane] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -330,7 +338,7 @@ __global__ __launch_bounds__(64) void blend_forward_kernel(BlendForwardArgs a) {
     // chunk c + 2 are loaded (indices clamped to the tile's last instance; lanes past CHUNK repeat lane CHUNK - 1).
     const uint32_t gather_lane = min(lane, CHUNK - 1u);
     const uint32_t last_inst = n_total > 0 ? n_total - 1u : 0u;
-    const uint32_t* const prim_src = own_sort ? s_sorted_prim : a.sorted_prim + range.x;
+    const uint32_t* const prim_src = in_regs ? s_sorted_prim : a.sorted_prim + range.x;
     const auto load_p = [&](uint32_t s) { return prim_src[min(s + gather_lane, last_inst)]; };
     const auto stage = [&](uint32_t half, uint32_t s, const PrimRecord& rec) {
         if (lane < CHUNK && s + lane < n_total) {

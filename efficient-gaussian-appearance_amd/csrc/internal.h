@@ -32,11 +32,9 @@ bool launch_fill_u32(uint32_t* p, uint32_t value, uint64_t n, hipStream_t s);
 // counters: [0] V, [1] I, [2] instance-emission mismatches, [3] / [4] min / max depth key of the visible set,
 // [5] 1 when I exceeds the instance capacity the binning buffers were laid out for (the binning and blend kernels
 // then return at once; the host re-runs them with buffers of the exact size); the host's copy also holds, in
-// [counter_sequence], the sequence number of the frame whose counters it holds (written last); [6] on the device:
-// the number of tiles whose runs the tile sort sorts (cleared with the others)
+// [counter_sequence], the sequence number of the frame whose counters it holds (written last)
 constexpr uint32_t n_counters = 8;
 constexpr uint32_t counter_overflow = 5;
-constexpr uint32_t counter_big_tiles = 6;
 constexpr uint32_t counter_sequence = 7;
 bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_ranges, uint32_t* block_offsets, uint32_t* counters,
                               uint32_t* host_counters, uint32_t instance_capacity, uint32_t seq, uint32_t n_blocks, hipStream_t s);
@@ -106,8 +104,7 @@ struct TileScan {
     uint32_t* order_runs;  // per 64-tile block and class: the class's tiles in the block, then their first position
     uint32_t* order_rank;  // per tile: class << 16 | rank among the block's tiles of its class
     uint32_t* order;       // the tile order (block b of a blend runs tile order[b])
-    uint32_t* counters;    // instance count ([1]), overflow flag ([counter_overflow]) and big-tile count on the device
-    uint32_t* big_tiles;   // the tiles whose runs are longer than forward_sort_max (the first counters[counter_big_tiles])
+    const uint32_t* counters;  // instance count ([1]) and overflow flag ([counter_overflow]) on the device
 };
 // per-tile counts (global atomics without a table) and the scan above
 // (max_instances: bound on the instance count, the grid size of the path without a table; the kernels read the
@@ -119,18 +116,17 @@ bool launch_tile_counts(const TileBinning& plan, const void* keys, int key_bytes
 bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_bytes, const uint32_t* inst_prim, const uint32_t* depth_keys,
                          const uint32_t* table, const uint32_t* local_rank, const TileScan& ts, uint4* bucket, uint32_t max_instances,
                          uint32_t n_tiles, hipStream_t s);
-// per tile: [start, end) into ranges and its keys sorted ascending -> emission indices in sorted_inst, their
-// primitives (from the bucket entries, or gathered from inst_prim) in sorted_prim, tile id in sorted_keys
-bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint4* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
-                      const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t n_tiles, hipStream_t s);
+// per tile: [start, end) into ranges and its place in the blends' tile order (the runs are sorted by the forward blend)
+bool launch_tile_ranges(const TileScan& ts, uint2* ranges, uint32_t n_tiles, hipStream_t s);
 bool launch_reduce_partials(const float* partials, uint32_t n_blocks, uint32_t n_params, float* out, hipStream_t s);
 
 struct BlendForwardArgs {
     const uint2* ranges;
-    const uint4* bucket;           // per tile slot: emission index, depth key, primitive, 0 (unsorted)
-    uint32_t* sorted_inst;         // emission index per sorted instance (written here for runs of <= 256)
-    uint32_t* sorted_prim;         // primitive per sorted instance (read, or written here for runs of <= 256)
-    void* sorted_keys;             // tile key per sorted instance (key_bytes wide; written here for runs of <= 256)
+    uint4* bucket;                 // per tile slot: emission index, depth key, primitive, 0 (unsorted; runs of more
+                                   // than 512 are sorted in chunks in place)
+    uint32_t* sorted_inst;         // emission index per sorted instance (written here)
+    uint32_t* sorted_prim;         // primitive per sorted instance (written here)
+    void* sorted_keys;             // tile key per sorted instance (key_bytes wide; written here)
     const uint32_t* inst_prim;     // primitive per emission index
     const uint32_t* counters;      // frame counters (counters[1]: the instance count)
     uint32_t key_bytes;

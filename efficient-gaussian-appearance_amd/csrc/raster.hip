@@ -21,7 +21,6 @@
 // reproduce its counts exactly.
 // Reference: B/rasterization/include/kernels_common.cuh:20-157, B/rasterization/src/forward.cu:82-221.
 #include "internal.h"
-#include "tile_sort.h"
 
 namespace efgs {
 
@@ -279,7 +278,6 @@ __global__ __launch_bounds__(fused_block) void create_instances_fused_kernel(Cre
             if (k != 2) a.counters[k] = c[k];
             f.host_counters[k] = c[k];
         }
-        a.counters[counter_big_tiles] = 0u;
         __threadfence_system();
         __hip_atomic_store(&f.host_counters[counter_sequence], f.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         __threadfence_system();
@@ -582,55 +580,12 @@ __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, con
     }
 }
 
-// Per-tile sort: one wave per tile, four tiles per block, no block barriers (the tiles' ranges come from
-// tile_ranges_kernel, launched before). Keys are unique 64-bit values (depth key << 32 | emission index), sorted
-// ascending by bitonic networks:
-//   n <= 64, 128, 256 in registers, K = 1, 2, 4 keys per lane (element x = K lane + i): exchanges at distance
-//                     j < K within a lane, j >= K with the lane at xor distance j / K (128 < n <= 192: a
-//                     128-key and a 64-key network merged by rank); these runs are sorted by the forward blend
-//                     of the tile (tile_sort.h), before its walk, which saves this kernel their loads and writes;
-//   256 < n <= 512    in the wave's LDS slab;
-//   n > 512           chunks of 512 sorted in the slab and written back to the tile's range, then every key
-//                     placed at (its index in its chunk) + (its rank in each other chunk).
-constexpr uint32_t tile_sort_waves = 4;
-constexpr uint32_t tile_sort_block = 64 * tile_sort_waves;
-constexpr uint32_t wave_slab = 512;
-
-// ascending bitonic sort of m (a power of two, <= wave_slab) keys in the wave's slab
-__device__ inline void wave_bitonic_lds(uint64_t* s, uint32_t m, uint32_t lane) {
-    for (uint32_t size = 2; size <= m; size <<= 1) {
-        for (uint32_t j = size >> 1; j > 0; j >>= 1) {
-            for (uint32_t x = lane; x < m; x += 64) {
-                const uint32_t y = x ^ j;
-                if (y > x) {
-                    const uint64_t a = s[x], b = s[y];
-                    if ((a > b) == ((x & size) == 0)) {
-                        s[x] = b;
-                        s[y] = a;
-                    }
-                }
-            }
-            wave_lds_fence();
-        }
-    }
-}
-
-// number of keys below x in the ascending run of bucket entries [0, n)
-__device__ __forceinline__ uint32_t rank_in_bucket(const uint4* run, uint32_t n, uint64_t x) {
-    uint32_t lo = 0, hi = n;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (key_of(run[mid]) < x) lo = mid + 1; else hi = mid;
-    }
-    return lo;
-}
-
 // Every tile's range and its place in the blends' tile order, one tile per lane: a wave's 64 tiles are one scan
-// block, so the wave computes the prefix of the block sums once for all of them. Tiles with runs longer than
-// forward_sort_max are listed for the tile sort (in any order: each run's sort is independent of the others).
+// block, so the wave computes the prefix of the block sums once for all of them. (Each tile's run is sorted by the
+// forward blend of the tile, before its walk.)
 __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint32_t* totals, const uint32_t* block_sums, const uint32_t* local_start,
                                                           const uint32_t* order_runs, const uint32_t* order_rank, uint32_t* order,
-                                                          uint32_t* counters, uint32_t* big_tiles, uint2* ranges, uint32_t n_tiles) {
+                                                          const uint32_t* counters, uint2* ranges, uint32_t n_tiles) {
     static_assert(scan_tiles == 64, "one scan block per wave");
     if (counters[counter_overflow] != 0) return;
     const uint32_t lane = threadIdx.x & 63u, tile = blockIdx.x * 256u + threadIdx.x;
@@ -643,64 +598,8 @@ __global__ __launch_bounds__(256) void tile_ranges_kernel(const uint32_t* totals
     ranges[tile] = n > 0 ? make_uint2(start, start + n) : make_uint2(0u, 0u);  // (0, 0) for an empty tile, as the reference
     const uint32_t cr = order_rank[tile];
     order[order_runs[static_cast<size_t>(tile / scan_tiles) * order_classes + (cr >> 16)] + (cr & 0xffffu)] = tile;
-    if (n > forward_sort_max) big_tiles[atomicAdd(&counters[counter_big_tiles], 1u)] = tile;
 }
 
-// One run of n > forward_sort_max keys (the wave's slab s: wave_slab keys).
-template <typename KeyT>
-__device__ void sort_big_run(uint4* bucket, uint2 r, uint32_t n, uint32_t tile, uint32_t* sorted_inst, KeyT* sorted_keys,
-                             const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t lane, uint64_t* s) {
-    uint4* run = bucket + r.x;
-    const SortedOut<KeyT> o{sorted_inst + r.x, sorted_prim + r.x, sorted_keys + r.x, inst_prim, tile, nullptr};
-    if (n <= wave_slab) {
-        uint32_t m = 512;
-        while (m < n) m <<= 1;
-        for (uint32_t x = lane; x < m; x += 64) s[x] = x < n ? key_of(run[x]) : ~0ull;
-        wave_lds_fence();
-        wave_bitonic_lds(s, m, lane);
-        for (uint32_t x = lane; x < n; x += 64) o.put(x, s[x]);
-        return;
-    }
-    const uint32_t n_chunks = (n + wave_slab - 1) / wave_slab;
-    for (uint32_t c = 0; c < n_chunks; c++) {
-        const uint32_t c0 = c * wave_slab, cn = min(wave_slab, n - c0);
-        for (uint32_t x = lane; x < wave_slab; x += 64) s[x] = x < cn ? key_of(run[c0 + x]) : ~0ull;
-        wave_lds_fence();
-        wave_bitonic_lds(s, wave_slab, lane);
-        for (uint32_t x = lane; x < cn; x += 64) run[c0 + x] = make_uint4(static_cast<uint32_t>(s[x]), static_cast<uint32_t>(s[x] >> 32), 0u, 0u);
-        wave_lds_fence();
-    }
-    __threadfence();  // the wave reads back the chunks it wrote
-    for (uint32_t idx = lane; idx < n; idx += 64) {
-        const uint64_t key = key_of(run[idx]);
-        const uint32_t c = idx / wave_slab;
-        uint32_t pos = idx - c * wave_slab;
-        for (uint32_t oc = 0; oc < n_chunks; oc++) {
-            if (oc == c) continue;
-            const uint32_t o0 = oc * wave_slab;
-            pos += rank_in_bucket(run + o0, min(wave_slab, n - o0), key);
-        }
-        o.put(pos, key);
-    }
-}
-
-// The tile_ranges_kernel's list of long runs, one run per wave at a time (a grid of at most 256 blocks: for short
-// runs only, the usual case, the kernel reads the count and ends).
-template <typename KeyT>
-__global__ __launch_bounds__(tile_sort_block) void tile_sort_kernel(const uint32_t* counters, const uint32_t* big_tiles, const uint2* ranges,
-                                                                   uint4* bucket, uint32_t* sorted_inst, KeyT* sorted_keys,
-                                                                   const uint32_t* inst_prim, uint32_t* sorted_prim) {
-    if (counters[counter_overflow] != 0) return;
-    __shared__ uint64_t s_slab[tile_sort_waves][wave_slab];
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t n_big = counters[counter_big_tiles];
-    for (uint32_t idx = blockIdx.x * tile_sort_waves + wave; idx < n_big; idx += gridDim.x * tile_sort_waves) {
-        const uint32_t tile = big_tiles[idx];
-        const uint2 r = ranges[tile];
-        sort_big_run(bucket, r, r.y - r.x, tile, sorted_inst, sorted_keys, inst_prim, sorted_prim, lane, s_slab[wave]);
-        wave_lds_fence();  // (the slab is reused by the next run)
-    }
-}
 
 // out[i] = sum over blocks b of partials[b][i]. A block covers 64 parameters with 16 groups of 64 lanes;
 // group g sums blocks g, g + 16, ... in order, then the 16 group sums are added in group order (fixed
@@ -838,19 +737,10 @@ bool launch_tile_buckets(const TileBinning& plan, const void* keys, int key_byte
     return true;
 }
 
-bool launch_tile_sort(const TileScan& ts, uint2* ranges, uint4* bucket, uint32_t* sorted_inst, void* sorted_keys, int key_bytes,
-                      const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t n_tiles, hipStream_t s) {
+bool launch_tile_ranges(const TileScan& ts, uint2* ranges, uint32_t n_tiles, hipStream_t s) {
     if (n_tiles == 0) return true;
     tile_ranges_kernel<<<div_up(n_tiles, 256), 256, 0, s>>>(ts.totals, ts.block_sums, ts.local_start, ts.order_runs, ts.order_rank, ts.order,
-                                                            ts.counters, ts.big_tiles, ranges, n_tiles);
-    EFGS_HIP_CHECK(hipGetLastError());
-    const uint32_t blocks = min(div_up(n_tiles, tile_sort_waves), 256u);
-    if (key_bytes == 2)
-        tile_sort_kernel<uint16_t><<<blocks, tile_sort_block, 0, s>>>(ts.counters, ts.big_tiles, ranges, bucket, sorted_inst, static_cast<uint16_t*>(sorted_keys),
-                                                                     inst_prim, sorted_prim);
-    else
-        tile_sort_kernel<uint32_t><<<blocks, tile_sort_block, 0, s>>>(ts.counters, ts.big_tiles, ranges, bucket, sorted_inst, static_cast<uint32_t*>(sorted_keys),
-                                                                     inst_prim, sorted_prim);
+                                                            ts.counters, ranges, n_tiles);
     EFGS_HIP_CHECK(hipGetLastError());
     return true;
 }

@@ -126,7 +126,6 @@ __global__ __launch_bounds__(1024) void scan_block_counts_kernel(const uint32_t*
             counters[k] = c[k];
             host_counters[k] = c[k];
         }
-        counters[counter_big_tiles] = 0u;
         __threadfence_system();
         __hip_atomic_store(&host_counters[counter_sequence], seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         __threadfence_system();

@@ -1,13 +1,19 @@
-// Per-tile sorts of bucket entries shared by the tile sort (raster.hip) and the forward blend (blend.hip), which
-// sorts its own tile's run when it fits the register networks (at most forward_sort_max keys), so that the tile sort
-// only handles the larger runs.
+// The per-tile sort of bucket entries, run by the forward blend of each tile before its walk (no sort kernel: the
+// blend reads its run's primitives from registers and LDS, and the sorted arrays it writes serve the backward).
+// Keys are unique 64-bit values (depth key << 32 | emission index), sorted ascending by bitonic networks:
+//   n <= 64, 128, 256 in registers, K = 1, 2, 4 keys per lane (element x = K lane + i): exchanges at distance
+//                     j < K within a lane, j >= K with the lane at xor distance j / K (128 < n <= 192: a
+//                     128-key and a 64-key network merged by rank);
+//   256 < n <= 512    in the wave's LDS slab;
+//   n > 512           chunks of 512 sorted in the slab and written back to the tile's range, then every key
+//                     placed at (its index in its chunk) + (its rank in each other chunk).
 #pragma once
 
 #include "internal.h"
 
 namespace efgs {
 
-// runs of at most this many instances are sorted by the forward blend of their tile, larger ones by tile_sort
+// runs of at most this many instances are sorted in registers (their primitives also go to LDS for the walk)
 constexpr uint32_t forward_sort_max = 256;
 
 // orders a wave's own LDS accesses across the steps of a network (the LDS executes a wave's instructions in
@@ -187,6 +193,75 @@ __device__ __forceinline__ void sort_small_run(const uint4* run, uint32_t n, con
     else if (n <= 128) sort_run_in_registers<2>(run, n, o, lane, packed, s_prim);
     else if (n <= 192) sort_run_split192(run, n, o, lane, slab, packed);
     else sort_run_in_registers<4>(run, n, o, lane, packed, s_prim);
+}
+
+constexpr uint32_t wave_slab = 512;  // keys of a wave's LDS slab
+
+// ascending bitonic sort of m (a power of two, <= wave_slab) keys in the wave's slab
+__device__ inline void wave_bitonic_lds(uint64_t* s, uint32_t m, uint32_t lane) {
+    for (uint32_t size = 2; size <= m; size <<= 1) {
+        for (uint32_t j = size >> 1; j > 0; j >>= 1) {
+            for (uint32_t x = lane; x < m; x += 64) {
+                const uint32_t y = x ^ j;
+                if (y > x) {
+                    const uint64_t a = s[x], b = s[y];
+                    if ((a > b) == ((x & size) == 0)) {
+                        s[x] = b;
+                        s[y] = a;
+                    }
+                }
+            }
+            wave_lds_fence();
+        }
+    }
+}
+
+// number of keys below x in the ascending run of bucket entries [0, n)
+__device__ __forceinline__ uint32_t rank_in_bucket(const uint4* run, uint32_t n, uint64_t x) {
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (key_of(run[mid]) < x) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+// One run of n > forward_sort_max keys (the wave's slab s: wave_slab keys); the sorted arrays in global memory only.
+template <typename KeyT>
+__device__ inline void sort_big_run(uint4* bucket, uint2 r, uint32_t n, uint32_t tile, uint32_t* sorted_inst, KeyT* sorted_keys,
+                             const uint32_t* inst_prim, uint32_t* sorted_prim, uint32_t lane, uint64_t* s) {
+    uint4* run = bucket + r.x;
+    const SortedOut<KeyT> o{sorted_inst + r.x, sorted_prim + r.x, sorted_keys + r.x, inst_prim, tile, nullptr};
+    if (n <= wave_slab) {
+        uint32_t m = 512;
+        while (m < n) m <<= 1;
+        for (uint32_t x = lane; x < m; x += 64) s[x] = x < n ? key_of(run[x]) : ~0ull;
+        wave_lds_fence();
+        wave_bitonic_lds(s, m, lane);
+        for (uint32_t x = lane; x < n; x += 64) o.put(x, s[x]);
+        return;
+    }
+    const uint32_t n_chunks = (n + wave_slab - 1) / wave_slab;
+    for (uint32_t c = 0; c < n_chunks; c++) {
+        const uint32_t c0 = c * wave_slab, cn = min(wave_slab, n - c0);
+        for (uint32_t x = lane; x < wave_slab; x += 64) s[x] = x < cn ? key_of(run[c0 + x]) : ~0ull;
+        wave_lds_fence();
+        wave_bitonic_lds(s, wave_slab, lane);
+        for (uint32_t x = lane; x < cn; x += 64) run[c0 + x] = make_uint4(static_cast<uint32_t>(s[x]), static_cast<uint32_t>(s[x] >> 32), 0u, 0u);
+        wave_lds_fence();
+    }
+    __threadfence();  // the wave reads back the chunks it wrote
+    for (uint32_t idx = lane; idx < n; idx += 64) {
+        const uint64_t key = key_of(run[idx]);
+        const uint32_t c = idx / wave_slab;
+        uint32_t pos = idx - c * wave_slab;
+        for (uint32_t oc = 0; oc < n_chunks; oc++) {
+            if (oc == c) continue;
+            const uint32_t o0 = oc * wave_slab;
+            pos += rank_in_bucket(run + o0, min(wave_slab, n - o0), key);
+        }
+        o.put(pos, key);
+    }
 }
 
 }  // namespace efgs
