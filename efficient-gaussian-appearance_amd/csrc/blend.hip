@@ -278,7 +278,7 @@ __device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
 // same time, 70.6 against 70.5 us on the 1M-Gaussian 1080p scene: both waited on the gather chain emission index
 // -> primitive -> record; with the primitives read from the sorted array it takes 57 us.)
 template <typename KeyT>
-__global__ __launch_bounds__(64) void blend_forward_kernel(BlendForwardArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(7))) void blend_forward_kernel(BlendForwardArgs a) {
     if (a.overflow && *a.overflow != 0) return;  // the binning was skipped: the host re-runs the frame
     constexpr uint32_t CHUNK = 32;
     constexpr uint32_t RING = 2 * CHUNK;
