@@ -580,32 +580,59 @@ def decode_benchmark(args) -> None:
         tf.grad = td.grad = tw.grad = None
 
     log(f'c2: {n} primitives, MLP {n_in} -> {m["n_neurons"]} x {m["n_hidden_layers"]} -> 3')
+    # eager (autograd) steps: the host's launch and autograd work per step (0.1-0.18 ms on these boxes' cores) is
+    # as long as the step's kernels, so the eager figure follows the host; it is reported beside the value
+    t_ramp = time.perf_counter()
+    while time.perf_counter() - t_ramp < RAMP_S:
+        step()
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
         step(events[k])
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    eager_wall = time.perf_counter() - t0
     fwd_ms = sum(e[0].elapsed_time(e[1]) for e in events) / args.steps
     bwd_ms = sum(e[1].elapsed_time(e[2]) for e in events) / args.steps
+    # the same step (neural_decode and autograd's backward) captured once as a HIP graph and replayed: the step's
+    # kernels without the host's per-launch work; the K replays are timed between one pair of events
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = neural_decode(tf, td, tw, 1)
+        out.backward(tdy)
+    t_ramp = time.perf_counter()
+    while time.perf_counter() - t_ramp < RAMP_S:
+        graph.replay()
+    for _ in range(args.warmup):
+        graph.replay()
+    region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    region[0].record()
+    for _ in range(args.steps):
+        graph.replay()
+    region[1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = region[0].elapsed_time(region[1]) / args.steps
     F = mlp_flops_per_primitive(n_in, m['n_neurons'], m['n_hidden_layers'])
     flops = 3 * F * n                    # forward + backward (input and weight gradients)
     lat = 4 * m['n_feature_dims']
     # forward: latents + directions in, outputs out; backward: latents + directions + upstream in, latent and
     # direction gradients out (156 B per primitive at c2)
     nbytes = n * ((lat + 12 + 12) + (lat + 12 + 12 + lat + 12))
-    ms = fwd_ms + bwd_ms
     line = {
         'metric': 'neural decode fwd+bwd Mprim/s @1M (c2)', 'value': round(n / (ms * 1e-3) / 1e6, 3), 'unit': 'Mprim/s',
         'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(wall * 1e3 / args.steps, 4),
         'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f16 MFMA, f32 accumulation', 'data': 'synthetic',
         'config': {'workload': f'c2: neural decode of {n} primitives ({n_in} -> {m["n_neurons"]} x {m["n_hidden_layers"]} -> 3), '
                                'forward + backward w.r.t. latents, directions and weights', 'n_primitives': n},
-        'forward_ms': round(fwd_ms, 5), 'backward_ms': round(bwd_ms, 5),
+        'timing': (f'HIP events around {args.steps} replays of the step captured as one HIP graph (device synchronisations on '
+                   f'both sides), after a {RAMP_S} s untimed ramp of replays and {args.warmup} warm-up replays'),
+        'eager_ms_per_step': round(eager_wall * 1e3 / args.steps, 4),
+        'eager_forward_ms': round(fwd_ms, 5), 'eager_backward_ms': round(bwd_ms, 5),
         'roofline': {'bound': 'mfma', 'achieved': round(flops / (ms * 1e-3) / 1e12, 3), 'peak': MFMA_FP16_PEAK_TFLOPS,
                      'unit': 'TFLOP/s', 'frac': round(flops / (ms * 1e-3) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 5), 'traffic': None,
                      'kernel': 'neural_decode + neural_decode_backward', 'algorithmic_flops': int(flops),
