@@ -148,7 +148,7 @@ struct efgs_rasterizer {
 
     // instance count of the last forward and the scene size it was for: sizes the next frame's instance
     // buffers before its counter readback
-    uint32_t instance_hint = 0, visible_hint = 0, hint_primitives = 0, hint_tiles = 0;
+    uint32_t instance_hint = 0, hint_primitives = 0, hint_tiles = 0;
     efgs::StageTimer timer;
     // specialised preprocess kernels of the current configuration, per variant and direction (forward,
     // backward), for the device they were loaded on; cleared whenever the configuration changes
@@ -262,7 +262,7 @@ struct InstanceLayout {
         InstanceLayout l;
         Carver c{base};
         const uint64_t ni = n_instances > 0 ? n_instances : 1;
-        const bool use_table = tile_binning_plan(1, n_tiles).use_table;
+        const bool use_table = fused_binning_fits(n_tiles);
         l.keys = c.take_bytes(key_bytes * ni);
         l.inst_prim = c.take<uint32_t>(ni);
         l.local_rank = c.take<uint32_t>(use_table ? ni : 1);
@@ -743,13 +743,13 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         if (!launch_fill_u32(pl.counters, 0u, n_counters, s)) return EFGS_ERR_HIP;
     }
 
-    // Instance binning and the blend, into instance buffers laid out for `cap` instances (visible_plan: the visible
-    // count the segment plan is made for; max_visible / max_instances: bounds on the counts, the grid sizes).
+    // Instance binning and the blend, into instance buffers laid out for `cap` instances (max_visible /
+    // max_instances: bounds on the counts, the grid sizes).
     InstanceLayout il{};
-    const auto bin_and_blend = [&](char* iblob, uint64_t cap, uint32_t visible_plan, uint32_t max_visible, uint32_t max_instances) -> int {
+    const auto bin_and_blend = [&](char* iblob, uint64_t cap, uint32_t max_visible, uint32_t max_instances) -> int {
         il = InstanceLayout::carve(iblob, cap, key_bytes, n_tiles);
         FusedBinningArgs fa{};
-        const TileBinning plan = fused ? fused_binning_plan(n, n_tiles, fa.chunks_per_segment) : tile_binning_plan(visible_plan, n_tiles);
+        const TileBinning plan = fused ? fused_binning_plan(n, n_tiles, fa.chunks_per_segment) : TileBinning{false, 0u, 1u};
         fa.block_counts = pl.block_counts;
         fa.key_ranges = pl.block_key_ranges;
         fa.host_counters = r->host_counters_dev;
@@ -820,7 +820,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     if (speculate) {
         iblob = static_cast<char*>(alloc(alloc_ctx, InstanceLayout::carve(nullptr, capacity, key_bytes, n_tiles).bytes));
         if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
-        if (int c = bin_and_blend(iblob, capacity, r->visible_hint, n, static_cast<uint32_t>(capacity))) return c;
+        if (int c = bin_and_blend(iblob, capacity, n, static_cast<uint32_t>(capacity))) return c;
     }
     t.begin(EFGS_STAGE_COUNTER_READ, s);
     if (n > 0) {
@@ -833,7 +833,6 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
     // slots, ranges and records here are unsigned 32-bit indices with 64-bit byte offsets
     if (n_instances > 0x7fffffffu) return fail(EFGS_ERR_INVALID_ARGUMENT, "more than 2^31 - 1 tile instances in one frame");
     r->instance_hint = n_instances;
-    r->visible_hint = n_visible;
     r->hint_primitives = n;
     r->hint_tiles = n_tiles;
     if (!speculate || n_instances > capacity) {
@@ -843,7 +842,7 @@ int forward_impl(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_se
         capacity = n_instances;
         iblob = static_cast<char*>(alloc(alloc_ctx, InstanceLayout::carve(nullptr, capacity, key_bytes, n_tiles).bytes));
         if (!iblob) return fail(EFGS_ERR_ALLOC, "allocation of the instance buffers failed");
-        if (int c = bin_and_blend(iblob, capacity, n_visible, n_visible, n_instances)) return c;
+        if (int c = bin_and_blend(iblob, capacity, n_visible, n_instances)) return c;
     }
     if (!frame) return EFGS_OK;
 

@@ -42,11 +42,10 @@ bool launch_scan_block_counts(const uint32_t* block_counts, const uint32_t* key_
 // index order)
 bool launch_compact_visible(const uint32_t* n_touched, const uint32_t* block_offsets, uint32_t* visible_out, uint32_t* prim_offset, uint32_t n,
                             hipStream_t s);
-// Tile binning: per-tile counts from LDS histograms over segments of contiguous visible primitives (their
-// emission slots are contiguous; a table of per-segment counts, scanned per tile) when the tile count fits the
-// LDS, else from global atomics.
+// Tile binning: per-tile counts from LDS histograms over segments of contiguous primitives (their emission slots
+// are contiguous; a table of per-segment counts, scanned per tile) when the tile count fits the LDS (the fused
+// emission), else from global atomics.
 constexpr size_t tile_hist_max_lds = 64 * 1024;    // default dynamic LDS limit of a launch
-constexpr uint32_t tile_hist_min_segment = 2048;   // visible primitives per histogram block (at least)
 constexpr uint32_t tile_hist_max_blocks = 256;     // segments (the rank word keeps the segment in its top 8 bits)
 constexpr uint32_t rank_segment_shift = 24;        // rank word: rank within the segment's instances of the tile | segment << 24
 struct TileBinning {
@@ -54,7 +53,6 @@ struct TileBinning {
     uint32_t blocks;   // histogram blocks (segments, rows of the table)
     uint32_t segment;  // visible primitives per segment
 };
-TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles);
 struct CreateInstancesArgs {
     const uint32_t* visible_prims;
     const uint32_t* prim_offset;

@@ -2,21 +2,23 @@
 // 32-bit radix sort of the visible primitives by depth, emission of (tile, primitive) instances in that
 // order, then a stable radix sort by tile. This build reaches the same per-tile order, (depth, primitive
 // index), without a global sort:
-//   compact_visible     visible primitives in index order and each one's first emission slot (exclusive
-//                       scan of the tile counts in index order);
-//   create_instances    one thread per visible primitive (index order): the tile test of the preprocess,
-//                       (tile key, primitive) at the emission slots; blocks of contiguous primitives count
-//                       their instances per tile in an LDS histogram (ranks from the atomics' return values);
+//   create_instances    (fused, grids whose tile histogram fits the LDS) blocks of contiguous primitives scan
+//                       the preprocess's tile counts (the compaction: visible primitives in index order and
+//                       their first emission slots) and emit (tile key, primitive) at the emission slots, the
+//                       tile test of the preprocess for every tile past its recorded first ones; each block
+//                       counts its instances per tile in an LDS histogram (ranks from the atomics' return
+//                       values) and writes its row of the segment x tile table. Larger grids: compact_visible,
+//                       then one thread per visible primitive, counted per tile with global atomics;
 //   tile_column_scan    the segments' counts per tile -> prefixes over the segments, tile totals and starts,
 //                       and each tile's size class for the blends' heaviest-first tile order;
 //   tile_buckets        every instance writes its entry (emission index, depth key, primitive) at tile start +
 //                       earlier segments' count + rank; one extra block turns the size-class counts into the
 //                       tile order's run positions meanwhile;
-//   tile_sort           one wave per tile sorts its slots by (depth key, emission index): keys are
-//                       unique, so the order is a deterministic function of the inputs (the emission index
-//                       increases with the primitive index, so ties in depth keep primitive-index order); it
-//                       writes the emission indices and the primitives in that order, so the blends read both
-//                       as coalesced arrays instead of gathering each instance's primitive.
+//   tile_ranges         every tile's instance range and its place in the tile order.
+// The forward blend then sorts each tile's entries by (depth key, emission index) before it walks them (keys are
+// unique, so the order is a deterministic function of the inputs; the emission index increases with the
+// primitive index, so ties in depth keep primitive-index order) and writes the emission indices and primitives
+// in that order for the backward.
 // Compiled with -ffp-contract=off: instance emission re-evaluates the tile test of the preprocess and must
 // reproduce its counts exactly.
 // Reference: B/rasterization/include/kernels_common.cuh:20-157, B/rasterization/src/forward.cu:82-221.
@@ -88,7 +90,7 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
 }
 
 // Emission of one visible primitive per thread (visible index i, index order): (tile key, primitive) for every
-// tile of its tile rectangle that passes the contribution test, the first 4 tiles per lane from the test results
+// tile of its tile rectangle that passes the contribution test, the first 8 tiles per lane from the test results
 // the preprocess recorded in the primitive's record, larger footprints' further tiles tested again
 // wave-cooperatively (64 tiles per step, positions from ballot prefix counts); emit(slot, tile) is
 // called by the lane that writes each instance. Emission slots are [prim_offset, prim_offset + n_touched); a
@@ -96,19 +98,32 @@ __global__ __launch_bounds__(preprocess_block) void compact_visible_kernel(const
 // key (never bucketed) and counted in counters[2]. A primitive that emitted fewer tiles than counted gets
 // n_touched lowered to the emitted count, so the per-primitive sums of the backward and of the pruning scores
 // cover only slots that a blend kernel writes. Every lane of the wave must call this (ballots and shuffles).
+// The fields of a primitive's 48-byte record that emission reads (nine of its twelve words: not the colour).
+struct EmitRecord {
+    float4 r0;               // mean2d x, y, conic x, y
+    float cz, opacity;       // conic z, opacity
+    uint32_t bx, by, first;  // packed screen bounds x, y; the first-tiles mask
+};
+__device__ __forceinline__ EmitRecord load_emit_record(const PrimRecord* records, uint32_t p) {
+    const float* const r = reinterpret_cast<const float*>(records + p);
+    const float4 r0 = *reinterpret_cast<const float4*>(r);
+    const float2 r1 = *reinterpret_cast<const float2*>(r + 4);
+    return EmitRecord{r0, r1.x, r1.y, __float_as_uint(r[9]), __float_as_uint(r[10]), __float_as_uint(r[11])};
+}
+
+// n: the primitive's tile count from the preprocess, rec: its record's emission fields (both loaded by the caller).
 template <typename KeyT, typename Emit>
-__device__ __forceinline__ void emit_primitive_at(const CreateInstancesArgs& a, uint32_t p, uint32_t off, bool active, uint32_t lane, Emit&& emit) {
+__device__ __forceinline__ void emit_primitive_rec(const CreateInstancesArgs& a, uint32_t p, uint32_t off, uint32_t n, const EmitRecord& rec, bool active,
+                                                   uint32_t lane, Emit&& emit) {
     const uint64_t lanes_below = (1ull << lane) - 1ull;
-    const uint32_t n = a.n_touched[p];
-    const PrimRecord rec = a.records[p];
-    const uint32_t bx = __float_as_uint(rec.r2.y), by = __float_as_uint(rec.r2.z);
+    const uint32_t bx = rec.bx, by = rec.by;
     const TileRect t = screen_to_tile_bounds(bx & 0xffffu, bx >> 16, by & 0xffffu, by >> 16);
     const uint32_t bw = t.x1 - t.x0;
     const uint32_t cnt = active ? bw * (t.y1 - t.y0) : 0u;
     const float smx = rec.r0.x - 0.5f, smy = rec.r0.y - 0.5f;
-    const float cx = rec.r0.z, cy = rec.r0.w, cz = rec.r1.x;
-    const float pt = cnt > n_sequential_tiles ? power_threshold_of(rec.r1.y) : 0.0f;  // (the tile test of the later tiles)
-    const uint32_t first_tiles = __float_as_uint(rec.r2.w);  // the preprocess's test of the first n_sequential_tiles tiles
+    const float cx = rec.r0.z, cy = rec.r0.w, cz = rec.cz;
+    const float pt = cnt > n_sequential_tiles ? power_threshold_of(rec.opacity) : 0.0f;  // (the tile test of the later tiles)
+    const uint32_t first_tiles = rec.first;  // the preprocess's test of the first n_sequential_tiles tiles
     KeyT* keys = static_cast<KeyT*>(a.keys);
     uint32_t k = 0;
     for (uint32_t j = 0; j < cnt && j < n_sequential_tiles; j++) {
@@ -158,6 +173,11 @@ __device__ __forceinline__ void emit_primitive_at(const CreateInstancesArgs& a, 
     }
 }
 
+template <typename KeyT, typename Emit>
+__device__ __forceinline__ void emit_primitive_at(const CreateInstancesArgs& a, uint32_t p, uint32_t off, bool active, uint32_t lane, Emit&& emit) {
+    emit_primitive_rec<KeyT>(a, p, off, a.n_touched[p], load_emit_record(a.records, p), active, lane, emit);
+}
+
 // visible primitive i (index order) of the compacted list; inactive lanes repeat the last one
 template <typename KeyT, typename Emit>
 __device__ __forceinline__ void emit_primitive(const CreateInstancesArgs& a, uint32_t i_raw, bool active, uint32_t lane, Emit&& emit) {
@@ -176,66 +196,41 @@ __global__ __launch_bounds__(instance_block) void create_instances_kernel(Create
     emit_primitive<KeyT>(a, i, i < a.n_visible, threadIdx.x & 63u, [](uint32_t, uint32_t) {});
 }
 
-// Emission with the per-tile counts: block s emits the visible primitives [s P, (s + 1) P), P = ceil(V / blocks)
-// (index order, so its emission slots are one contiguous run, its segment), counts them per tile in an LDS
-// histogram whose atomic return values rank every instance among the segment's instances of its tile (in
-// arbitrary order: the per-tile sort fixes the order later), stores rank | s << 24 per instance and writes its
-// histogram row table[s][*].
-template <typename KeyT>
-__global__ __launch_bounds__(1024) void create_instances_hist_kernel(CreateInstancesArgs a, uint32_t* local_rank, uint32_t* table, uint32_t n_tiles) {
-    if (a.counters[counter_overflow] != 0) return;
-    a.n_visible = a.counters[0];
-    const uint32_t per_segment = (a.n_visible + gridDim.x - 1) / gridDim.x;
-    extern __shared__ uint32_t hist[];
-    for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) hist[t] = 0;
-    __syncthreads();
-    const uint32_t seg = blockIdx.x;
-    const uint32_t v0 = seg * per_segment, v1 = min(a.n_visible, v0 + per_segment);
-    const uint32_t tag = seg << rank_segment_shift;
-    for (uint32_t base = v0; base < v1; base += 1024) {  // block-uniform trip count
-        const uint32_t i = base + threadIdx.x;
-        emit_primitive<KeyT>(a, i, i < v1, threadIdx.x & 63u, [&](uint32_t slot, uint32_t tile) {
-            local_rank[slot] = tag | atomicAdd(&hist[tile], 1u);
-        });
-    }
-    __syncthreads();
-    uint32_t* row = table + static_cast<size_t>(seg) * n_tiles;
-    for (uint32_t t = threadIdx.x; t < n_tiles; t += 1024) row[t] = hist[t];
-}
-
 // Emission with the per-tile counts, the compaction and the counter scan in one kernel (grids whose histogram
-// leaves room for the queue of visible primitives). Block s takes the primitive chunks [s C, (s + 1) C) of the
-// preprocess (C = f.chunks_per_segment chunks of preprocess_block primitives; its emission slots are one
-// contiguous run, its segment). It first sums the preprocess's per-chunk visible and instance counts: over all
-// chunks (the frame's totals and depth-key range: block 0 publishes the counters, to the host as well, followed
-// by the frame's sequence number) and over the chunks before its own (its first visible index and emission slot).
-// More instances than the buffers hold set the overflow flag and nothing is emitted. Then, 1024 primitives at a
-// time, a block scan of the visible flags and tile counts gives every visible primitive its visible index and
-// first emission slot (visible_prims, prim_offset: the compaction) and appends it to an LDS ring of 2048; whenever
-// the ring holds 1024, they are emitted one per thread (and the rest at the end), counted per tile in the LDS
-// histogram as create_instances_hist_kernel does.
+// fits the LDS). Block s takes the primitive chunks [s C, (s + 1) C) of the preprocess (C = f.chunks_per_segment
+// chunks of preprocess_block primitives; its emission slots are one contiguous run, its segment). It first sums the
+// preprocess's per-chunk visible and instance counts: over all chunks (the frame's totals and depth-key range:
+// block 0 publishes the counters, to the host as well, followed by the frame's sequence number) and over the
+// chunks before its own (its first visible index and emission slot). More instances than the buffers hold set the
+// overflow flag and nothing is emitted. Then, 1024 primitives at a time (a round), a block scan of the visible
+// flags and tile counts gives every visible primitive its visible index and first emission slot (visible_prims,
+// prim_offset: the compaction), and the thread that holds the primitive emits it, counted per tile in an LDS
+// histogram whose atomic return values rank every instance among the segment's instances of its tile (in arbitrary
+// order: the per-tile sort fixes the order later); it stores rank | s << 24 per instance and writes its histogram
+// row table[s][*]. The tile counts and records of the first two rounds are loaded
+// before the chunk counts are summed and every later round's during the round two before it, so the rounds wait on
+// no global load of their own (a thread whose primitive is not visible loads a record it does not use).
 constexpr uint32_t fused_block = 1024;
-constexpr uint32_t fused_ring = 2 * fused_block;
-constexpr size_t fused_extra_lds = 2 * fused_ring * 4 + 512;  // the ring (primitive, first slot) and scan partials
 template <typename KeyT>
 __global__ __launch_bounds__(fused_block) void create_instances_fused_kernel(CreateInstancesArgs a, FusedBinningArgs f, uint32_t* local_rank,
                                                                            uint32_t* table, uint32_t n_tiles) {
-    extern __shared__ uint32_t hist[];  // n_tiles counters, then the ring of primitives and of their first slots
-    uint32_t* const q_prim = hist + n_tiles;
-    uint32_t* const q_off = q_prim + fused_ring;
+    extern __shared__ uint32_t hist[];  // n_tiles counters
     __shared__ uint32_t s_red[fused_block / 64][8];
+    __shared__ uint32_t s_scan[2][fused_block / 64][2];  // the rounds' wave totals, alternating between rounds
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t seg = blockIdx.x;
     const uint32_t c0 = seg * f.chunks_per_segment, c1 = min(f.n_chunks, c0 + f.chunks_per_segment);
-    const uint32_t p_begin = c0 * preprocess_block, p_end = min(f.n_prims, c1 * preprocess_block);
-    // the tile counts of the segment's first fused_prefetch slices of 1024 primitives, loaded with the chunk counts
-    constexpr uint32_t fused_prefetch = 4;
-    uint32_t touched_pre[fused_prefetch];
-#pragma unroll
-    for (uint32_t it = 0; it < fused_prefetch; it++) {
+    const uint32_t p_begin = c0 * preprocess_block, p_end = min(f.n_prims, c1 * preprocess_block);  // (p_end > p_begin)
+    // the tile counts and records of a round (threads past the segment: count 0, the segment's last record)
+    const auto load_round = [&](uint32_t it, uint32_t& touched, EmitRecord& rec) {
         const uint32_t p = p_begin + it * fused_block + tid;
-        touched_pre[it] = p < p_end ? a.n_touched[p] : 0u;
-    }
+        touched = p < p_end ? a.n_touched[p] : 0u;
+        rec = load_emit_record(a.records, min(p, p_end - 1u));
+    };
+    uint32_t touched_a, touched_b;
+    EmitRecord rec_a, rec_b;
+    load_round(0, touched_a, rec_a);
+    load_round(1, touched_b, rec_b);
 
     // totals, depth-key range and the segment's prefix from the per-chunk counts
     uint32_t tv = 0, ti = 0, bv = 0, bi = 0, kmin = 0xffffffffu, kmax = 0u;
@@ -283,34 +278,25 @@ __global__ __launch_bounds__(fused_block) void create_instances_fused_kernel(Cre
         __threadfence_system();
     }
     if (overflow) return;  // (block-uniform)
-    __syncthreads();       // every wave has read s_red before the scans reuse it
 
     const uint32_t tag = seg << rank_segment_shift;
-    const auto emit_ring = [&](uint32_t head, uint32_t count) {  // the ring's entries head .. head + count - 1, count > 0
-        const uint32_t k = (head + min(tid, count - 1u)) & (fused_ring - 1u);
-        emit_primitive_at<KeyT>(a, q_prim[k], q_off[k], tid < count, lane, [&](uint32_t slot, uint32_t tile) {
-            local_rank[slot] = tag | atomicAdd(&hist[tile], 1u);
-        });
-    };
     uint32_t run_v = bv, run_i = bi;
-    uint32_t head = 0, queued = 0;  // ring state (block-uniform)
-    for (uint32_t base = p_begin, it = 0; base < p_end; base += fused_block, it++) {  // block-uniform trip count
-        const uint32_t p = base + tid;
-        uint32_t touched = 0;
-#pragma unroll
-        for (uint32_t k = 0; k < fused_prefetch; k++) touched = it == k ? touched_pre[k] : touched;
-        if (it >= fused_prefetch) touched = p < p_end ? a.n_touched[p] : 0u;
+    // A round's scan partials alternate between two buffers: a wave writes round r + 2's partials only after the
+    // barrier of round r + 1, which every wave reaches after its reads of round r's.
+    const auto round = [&](uint32_t it, uint32_t touched, const EmitRecord& rec) {
+        const uint32_t p = p_begin + it * fused_block + tid;
         const uint32_t vis = touched > 0 ? 1u : 0u;
         const uint32_t iv = wave_inclusive_sum(vis), ii = wave_inclusive_sum(touched);  // inclusive wave scans
+        uint32_t(*const sc)[2] = s_scan[it & 1u];
         if (lane == 63) {
-            s_red[wave][0] = iv;
-            s_red[wave][1] = ii;
+            sc[wave][0] = iv;
+            sc[wave][1] = ii;
         }
         __syncthreads();
         uint32_t pv = 0, pi = 0, nv = 0, ni = 0;
 #pragma unroll
         for (uint32_t w = 0; w < fused_block / 64; w++) {
-            const uint32_t wv = s_red[w][0], wi = s_red[w][1];
+            const uint32_t wv = sc[w][0], wi = sc[w][1];
             pv += w < wave ? wv : 0u;
             pi += w < wave ? wi : 0u;
             nv += wv;
@@ -320,22 +306,23 @@ __global__ __launch_bounds__(fused_block) void create_instances_fused_kernel(Cre
         if (vis) {
             a.visible_prims_out[run_v + vpos] = p;
             a.prim_offset_out[p] = off;
-            const uint32_t k = (head + queued + vpos) & (fused_ring - 1u);
-            q_prim[k] = p;
-            q_off[k] = off;
         }
+        emit_primitive_rec<KeyT>(a, p, off, touched, rec, vis != 0u, lane, [&](uint32_t slot, uint32_t tile) {
+            local_rank[slot] = tag | atomicAdd(&hist[tile], 1u);
+        });
         run_v += nv;
         run_i += ni;
-        queued += nv;
-        __syncthreads();  // the ring entries are written; the scan partials may be reused
-        if (queued >= fused_block) {
-            emit_ring(head, fused_block);
-            head = (head + fused_block) & (fused_ring - 1u);
-            queued -= fused_block;
-            __syncthreads();  // the emitted entries have been read before the next primitives overwrite them
-        }
+    };
+    // two register sets, each loaded a round before its use (no loaded value is copied between loop-carried
+    // registers: a copy would wait for the load)
+    const uint32_t n_rounds = (p_end - p_begin + fused_block - 1u) / fused_block;
+    for (uint32_t it = 0; it < n_rounds; it += 2) {  // (block-uniform)
+        round(it, touched_a, rec_a);
+        if (it + 2 < n_rounds) load_round(it + 2, touched_a, rec_a);
+        if (it + 1 >= n_rounds) break;
+        round(it + 1, touched_b, rec_b);
+        if (it + 3 < n_rounds) load_round(it + 3, touched_b, rec_b);
     }
-    if (queued > 0) emit_ring(head, queued);
     __syncthreads();
     uint32_t* row = table + static_cast<size_t>(seg) * n_tiles;
     for (uint32_t t = tid; t < n_tiles; t += fused_block) row[t] = hist[t];
@@ -645,17 +632,11 @@ bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const 
                              uint32_t n_tiles, const FusedBinningArgs* fused, hipStream_t s) {
     if (a.max_visible == 0) return true;
     if (fused) {
-        const size_t lds = static_cast<size_t>(n_tiles) * 4 + 2 * fused_ring * 4;
+        const size_t lds = static_cast<size_t>(n_tiles) * 4;
         if (key_bytes == 2)
             create_instances_fused_kernel<uint16_t><<<plan.blocks, fused_block, lds, s>>>(a, *fused, local_rank, table, n_tiles);
         else
             create_instances_fused_kernel<uint32_t><<<plan.blocks, fused_block, lds, s>>>(a, *fused, local_rank, table, n_tiles);
-    } else if (plan.use_table) {
-        const size_t lds = static_cast<size_t>(n_tiles) * 4;
-        if (key_bytes == 2)
-            create_instances_hist_kernel<uint16_t><<<plan.blocks, 1024, lds, s>>>(a, local_rank, table, n_tiles);
-        else
-            create_instances_hist_kernel<uint32_t><<<plan.blocks, 1024, lds, s>>>(a, local_rank, table, n_tiles);
     } else {
         const uint32_t blocks = div_up(a.max_visible, instance_block);
         if (key_bytes == 2)
@@ -667,27 +648,18 @@ bool launch_create_instances(const CreateInstancesArgs& a, int key_bytes, const 
     return true;
 }
 
-bool fused_binning_fits(uint32_t n_tiles) { return n_tiles > 0 && static_cast<size_t>(n_tiles) * 4 + fused_extra_lds <= tile_hist_max_lds; }
+bool fused_binning_fits(uint32_t n_tiles) { return n_tiles > 0 && static_cast<size_t>(n_tiles) * 4 <= tile_hist_max_lds; }
 
 TileBinning fused_binning_plan(uint32_t n_prims, uint32_t n_tiles, uint32_t& chunks_per_segment) {
     TileBinning b;
     b.use_table = true;
     const uint32_t n_chunks = n_prims > 0 ? div_up(n_prims, preprocess_block) : 1u;
-    const uint32_t want = n_prims > 0 ? div_up(n_prims, tile_hist_min_segment) : 1u;
+    // segments of at least one round of the fused kernel (1024 primitives), at most tile_hist_max_blocks of them
+    const uint32_t want = n_prims > 0 ? div_up(n_prims, fused_block) : 1u;
     chunks_per_segment = div_up(n_chunks, want < tile_hist_max_blocks ? want : tile_hist_max_blocks);
     b.blocks = div_up(n_chunks, chunks_per_segment);
     b.segment = chunks_per_segment * preprocess_block;
     (void)n_tiles;
-    return b;
-}
-
-TileBinning tile_binning_plan(uint32_t n_visible, uint32_t n_tiles) {
-    TileBinning b;
-    b.use_table = n_tiles > 0 && static_cast<size_t>(n_tiles) * 4 <= tile_hist_max_lds;
-    b.blocks = b.use_table ? (n_visible > 0 ? div_up(n_visible, tile_hist_min_segment) : 1u) : 0u;
-    if (b.blocks > tile_hist_max_blocks) b.blocks = tile_hist_max_blocks;
-    b.segment = b.use_table && n_visible > 0 ? div_up(n_visible, b.blocks) : 1u;
-    if (b.use_table && n_visible > 0) b.blocks = div_up(n_visible, b.segment);
     return b;
 }
 

@@ -41,8 +41,10 @@ struct PrimRecord {
 };
 
 // tiles of a primitive's rectangle that the preprocess tests one per lane (and records in the first-tiles mask);
-// further tiles are tested wave-cooperatively, by the preprocess and again by instance emission
-constexpr uint32_t n_sequential_tiles = 4;
+// further tiles are tested wave-cooperatively, by the preprocess and again by instance emission. Eight rather than
+// four: a wave's cooperative loop takes one primitive per step, however few tiles it has past the first ones
+// (100k SH3 Gaussians at 800x800: emission 37.5 -> 21.4 us, preprocess 24.6 -> 21.4 us; neutral on 1M at 1080p)
+constexpr uint32_t n_sequential_tiles = 8;
 static_assert(n_sequential_tiles <= 32, "the first-tiles mask is one 32-bit word of the record");
 // floats per instance gradient record of the blend backward (dL/dmean2d 2, dL/dconic 3, dL/dopacity, dL/dcolour 3;
 // with |dL/dmean2d| for three densification rows: 2 more and a pad)

@@ -4,7 +4,7 @@
 //
 // One thread per primitive, 256 threads = 4 wave64 per block. Per primitive: view-depth cull, opacity cull,
 // 3D covariance from log-scales and quaternion, EWA projection with the 1.15x clip, dilation and determinant
-// cull, conic, screen bounds clamped to the padded tile grid, exact touched-tile count (first 4 tiles per
+// cull, conic, screen bounds clamped to the padded tile grid, exact touched-tile count (first 8 tiles per
 // lane, larger footprints wave-cooperatively 64 tiles per step), activated colour, and the 48-byte record.
 // Each 256-primitive chunk also records its visible and instance counts, which a scan turns into
 // deterministic (primitive-index ordered) compaction offsets. No global atomics. The neural variant runs a

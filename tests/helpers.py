@@ -191,9 +191,13 @@ def check_emission(bufs, v, frame, fw, n: int) -> None:
     np.testing.assert_array_equal(read_device(bufs, v.instance_primitive, I, np.uint32), fw.inst_prims[order])
 
 
+# tiles of a primitive's rectangle whose test results the preprocess records in the record's spare word
+SEQUENTIAL_TILES = 8
+
+
 def check_first_tiles(rec: np.ndarray, fw, vis: np.ndarray, grid_w: int, grid_h: int) -> None:
-    """The record's spare word (column 11): bit j (j < 4) set exactly when tile j of the primitive's tile
-    rectangle (row-major) is one of the tiles the oracle emits for it (the preprocess's tile-test results that
+    """The record's spare word (column 11): bit j (j < SEQUENTIAL_TILES) set exactly when tile j of the primitive's
+    tile rectangle (row-major) is one of the tiles the oracle emits for it (the preprocess's tile-test results that
     instance emission reads instead of testing again). rec: the device records of the visible primitives."""
     prims = np.nonzero(vis)[0]
     b = fw.bounds[vis].astype(np.int64)
@@ -204,7 +208,7 @@ def check_first_tiles(rec: np.ndarray, fw, vis: np.ndarray, grid_w: int, grid_h:
     n_tiles_max = int(grid_w) * int(grid_h)
     emitted = np.sort(fw.inst_prims.astype(np.int64) * n_tiles_max + fw.inst_keys.astype(np.int64))
     expected = np.zeros(len(prims), np.uint32)
-    for j in range(4):
+    for j in range(SEQUENTIAL_TILES):
         tile = (y0 + j // np.maximum(bw, 1)) * grid_w + x0 + j % np.maximum(bw, 1)
         code = prims * n_tiles_max + tile
         pos = np.minimum(np.searchsorted(emitted, code), len(emitted) - 1)

@@ -234,11 +234,11 @@ def test_block_count_scan_at_large_primitive_counts(n_total):
     np.testing.assert_array_equal(big_img, small_img)
 
 
-# (width, height, primitives, sparse and dense scale shifts): the fused-emission grid, a grid of 12,161-16,384
-# tiles (segments of the compacted list with a histogram table) and a 32-bit-key grid (global-atomic counting)
+# (width, height, primitives, sparse and dense scale shifts): fused-emission grids, a small one and one of 13,400
+# tiles (its histogram near the LDS limit of 16,384 tiles), and a 32-bit-key grid (global-atomic counting)
 SPECULATION_GRIDS = {
     'fused_64x48': (64, 48, 600, 1.0, 3.5),
-    'table_1600x1600': (1600, 1600, 600, 0.5, 2.0),
+    'fused_1600x1600': (1600, 1600, 600, 0.5, 2.0),
     'global_4200x3000': (4200, 3000, 800, 0.5, 1.5),
 }
 
