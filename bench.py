@@ -391,7 +391,8 @@ def gpu_benchmark(args):
     else:
         roofline = {'bound': 'hbm', 'achieved': round(b / (dms * 1e-3) / 1e9, 2), 'peak': HBM_PEAK_GBS,
                     'unit': 'GB/s', 'frac': round(hbm_frac, 5)}
-    roofline['traffic'] = read_traffic(kernel_name)
+    # (the committed traffic summary covers the c3 step only)
+    roofline['traffic'] = read_traffic(kernel_name) if args.config == 'c3' else None
     roofline.update({'kernel': kernel_name, 'stage': dominant, 'avg_launch_ms': round(dms, 5),
                      'algorithmic_bytes': int(b), 'algorithmic_flops': int(f)})
     return dict(W=W, H=H, N=N, V=V, I=I, model=model, step_ms=step_ms, wall_ms_per_step=wall * 1e3 / args.steps, region_ms=region_ms,
@@ -905,9 +906,11 @@ def headline_line(args, r: dict, cpu: dict | None, port: dict | None) -> dict:
     this command (no kernel running on the GPU)."""
     W, H = r['W'], r['H']
     ms = r['region_ms']
-    kernel_us = read_step_kernel_us()
+    # the committed kernel trace and BASELINE's metric name are the c3 step's
+    kernel_us = read_step_kernel_us() if args.config == 'c3' else None
     return {
-        'metric': 'fwd+bwd Mpix/s @1M Gaussians 1080p (Neural); % HBM/MFMA roofline per kernel',
+        'metric': ('fwd+bwd Mpix/s @1M Gaussians 1080p (Neural); % HBM/MFMA roofline per kernel' if args.config == 'c3'
+                   else f'fwd+bwd Mpix/s ({args.config})'),
         'value': round(W * H / (ms * 1e-3) / 1e6, 3),
         'unit': 'Mpix/s',
         'n_gpus': 1,
