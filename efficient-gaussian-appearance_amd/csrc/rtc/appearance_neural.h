@@ -519,13 +519,10 @@ __device__ inline void mlp_train(const _Float16* WL, _Float16* stage, const floa
         for (uint32_t c = 0; c < 3; c++) gsrc[pb][c] = __shfl(g[c], static_cast<int>(16 * pb + r));
 #pragma unroll
     for (uint32_t pp = 0; pp < 2; pp++) {
-        // forward: F[l] = input activations of layer l >= 1 (F-tiles), P[l] = their P-tiles (P[0]: the inputs)
-        h4 F[NL][2][NT], P[NL][2][KT];
+        // forward: F[l] = input activations of layer l >= 1 (F-tiles); their P-tiles are taken in the backward, next
+        // to the weight-gradient MFMAs that read them (registers for one layer's P-tiles at a time)
+        h4 F[NL][2][NT];
         f4 yt[2];
-#pragma unroll
-        for (uint32_t b = 0; b < 2; b++)
-#pragma unroll
-            for (uint32_t ib = 0; ib < INP / 16; ib++) P[0][b][ib] = transpose_tile(X[2 * pp + b][ib], eye);
 #pragma unroll
         for (uint32_t l = 0; l < NL; l++) {
             const h4* in0 = l == 0 ? X[2 * pp] : F[l][0];
@@ -537,8 +534,6 @@ __device__ inline void mlp_train(const _Float16* WL, _Float16* stage, const floa
                 if (l < NH) {
                     F[l + 1][0][ob] = relu_h4(a0);
                     F[l + 1][1][ob] = relu_h4(a1);
-                    P[l + 1][0][ob] = transpose_tile(F[l + 1][0][ob], eye);
-                    P[l + 1][1][ob] = transpose_tile(F[l + 1][1][ob], eye);
                 } else if (ob == 0) {
                     yt[0] = a0;
                     yt[1] = a1;
@@ -557,13 +552,26 @@ __device__ inline void mlp_train(const _Float16* WL, _Float16* stage, const floa
             GT[b] = transpose_tile(G[b][0], eye);
         }
         // backward: dW_NH += dY X_NH^T over the pair, then layer by layer the input gradient (F-tiles, through
-        // the ReLU of the input), its P-tiles and dW_{l-1} += dIn X_{l-1}^T over the pair
+        // the ReLU of the input), its P-tiles and dW_{l-1} += dIn X_{l-1}^T over the pair. The P-tiles of a layer's
+        // input are taken right before the layer's weight-gradient MFMAs (they do not depend on the gradients, so
+        // they issue while the gradient chain runs).
+        {
+            h4 PT[2][KT];
 #pragma unroll
-        for (uint32_t ib = 0; ib < lin(NH) / 16; ib++) dW[NH][0][ib] = mfma32(cat(GT[0], GT[1]), cat(P[NH][0][ib], P[NH][1][ib]), dW[NH][0][ib]);
+            for (uint32_t b = 0; b < 2; b++)
+#pragma unroll
+                for (uint32_t ib = 0; ib < lin(NH) / 16; ib++) PT[b][ib] = transpose_tile(F[NH][b][ib], eye);
+#pragma unroll
+            for (uint32_t ib = 0; ib < lin(NH) / 16; ib++) dW[NH][0][ib] = mfma32(cat(GT[0], GT[1]), cat(PT[0][ib], PT[1][ib]), dW[NH][0][ib]);
+        }
 #pragma unroll
         for (int li = static_cast<int>(NH); li >= 1; li--) {
             const uint32_t l = static_cast<uint32_t>(li);
-            h4 Gn[2][NT];
+            h4 Gn[2][NT], PT[2][KT];
+#pragma unroll
+            for (uint32_t b = 0; b < 2; b++)
+#pragma unroll
+                for (uint32_t jb = 0; jb < lin(l - 1) / 16; jb++) PT[b][jb] = transpose_tile(l == 1 ? X[2 * pp + b][jb] : F[l - 1][b][jb], eye);
 #pragma unroll
             for (uint32_t ib = 0; ib < lin(l) / 16; ib++) {
                 f4 a0 = f4_zero(), a1 = f4_zero();
@@ -572,7 +580,7 @@ __device__ inline void mlp_train(const _Float16* WL, _Float16* stage, const floa
                 Gn[1][ib] = relu_grad(a1, F[l][1][ib]);
                 const h8 gt = cat(transpose_tile(Gn[0][ib], eye), transpose_tile(Gn[1][ib], eye));
 #pragma unroll
-                for (uint32_t jb = 0; jb < lin(l - 1) / 16; jb++) dW[l - 1][ib][jb] = mfma32(gt, cat(P[l - 1][0][jb], P[l - 1][1][jb]), dW[l - 1][ib][jb]);
+                for (uint32_t jb = 0; jb < lin(l - 1) / 16; jb++) dW[l - 1][ib][jb] = mfma32(gt, cat(PT[0][jb], PT[1][jb]), dW[l - 1][ib][jb]);
             }
 #pragma unroll
             for (uint32_t ib = 0; ib < NT; ib++) {

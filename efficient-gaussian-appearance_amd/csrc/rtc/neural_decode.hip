@@ -135,36 +135,50 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
     const int e = finite ? max(ilogbf(gmax), -110) : 8;  // the clamp keeps 2^(8 - e) finite for denormal maxima
     const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
 
+    // a chunk's inputs (direction, features, base colour, upstream gradient) are loaded during the chunk before it
+    constexpr bool has_dirs = EFGS_SH_DEGREE_MASK != 0;  // without SH degrees no direction is read or differentiated
+    constexpr uint32_t NB = EFGS_BASE_INPUT ? 3u : 0u;
+    struct ChunkInputs {
+        float3 d;
+        float feat[nn::FEATURES > 0 ? nn::FEATURES : 1], base[3], g[3];
+    };
+    const auto load_inputs = [&](uint32_t chunk, ChunkInputs& in) {
+        const uint32_t p = chunk * decode_block + threadIdx.x;
+        const bool active = p < a.n;
+        const uint32_t pp = active ? p : 0u;
+        in.d = has_dirs ? make_float3(a.dirs[3 * pp], a.dirs[3 * pp + 1], a.dirs[3 * pp + 2]) : make_float3(0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (uint32_t i = 0; i < nn::FEATURES; i++) in.feat[i] = a.features[static_cast<size_t>(pp) * nn::FEATURES + i];
+#pragma unroll
+        for (uint32_t c = 0; c < 3; c++) in.base[c] = c < NB ? a.base[3 * static_cast<size_t>(pp) + c] : 0.0f;
+#pragma unroll
+        for (uint32_t c = 0; c < 3; c++) in.g[c] = active ? a.grad_out[3 * static_cast<size_t>(p) + c] : 0.0f;
+    };
+    ChunkInputs next_in;
+    if (blockIdx.x < n_chunks) load_inputs(blockIdx.x, next_in);
     for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
+        const ChunkInputs in = next_in;  // (loaded during the previous chunk)
+        if (chunk + gridDim.x < n_chunks) load_inputs(chunk + gridDim.x, next_in);
         const uint32_t p = chunk * decode_block + threadIdx.x;
         const bool active = p < a.n;
         if (__ballot(active) == 0) continue;  // wave-uniform: the tail of the last chunk
-        const uint32_t pp = active ? p : 0u;
-        constexpr bool has_dirs = EFGS_SH_DEGREE_MASK != 0;  // without SH degrees no direction is read or differentiated
-        const float3 d = has_dirs ? make_float3(a.dirs[3 * pp], a.dirs[3 * pp + 1], a.dirs[3 * pp + 2]) : make_float3(0.0f, 0.0f, 0.0f);
-        const float* feat = a.features + static_cast<size_t>(pp) * nn::FEATURES;
-        const float* base = EFGS_BASE_INPUT ? a.base + 3 * static_cast<size_t>(pp) : nullptr;
+        const float3 d = in.d;
         float x[nn::INP];
-        nn::mlp_input(feat, base, d, a.degree, x);
+        nn::mlp_input(in.feat, in.base, d, a.degree, x);
         if (!active) {
 #pragma unroll
             for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
         }
-        float g[3] = {0.0f, 0.0f, 0.0f};
-        if (active) {
-            g[0] = a.grad_out[3 * p];
-            g[1] = a.grad_out[3 * p + 1];
-            g[2] = a.grad_out[3 * p + 2];
-        }
+        const float g[3] = {in.g[0], in.g[1], in.g[2]};
         float dx[nn::INP];
         nn::mlp_train(WL, stage, x, g, [](float, float gy) { return gy; }, s, inv_s, dx, dW, lane);
         if (active) {
             float* gf = a.g_features + static_cast<size_t>(p) * nn::FEATURES;
 #pragma unroll
-            for (uint32_t i = 0; i < nn::FEATURES; i++) gf[i] = nn::feature_grad(feat[i], dx, i);
+            for (uint32_t i = 0; i < nn::FEATURES; i++) gf[i] = nn::feature_grad(in.feat[i], dx, i);
             if (EFGS_BASE_INPUT && a.g_base) {
 #pragma unroll
-                for (uint32_t c = 0; c < 3; c++) a.g_base[3 * p + c] = nn::feature_grad(base[c], dx, nn::FEATURES + c);
+                for (uint32_t c = 0; c < 3; c++) a.g_base[3 * p + c] = nn::feature_grad(in.base[c], dx, nn::FEATURES + c);
             }
             if (has_dirs && a.g_dirs) {
                 const float3 gd = nn::direction_grad(d, a.degree, dx);

@@ -442,48 +442,77 @@ extern "C" __global__ __launch_bounds__(256, 2) void EFGS_CAT(EFGS_KERNEL_NAME, 
     const int e = finite ? max(ilogbf(gmax), -110) : 8;  // the clamp keeps 2^(8 - e) finite for denormal maxima
     const float s = ldexpf(1.0f, 8 - e), inv_s = ldexpf(1.0f, e - 8);
     // work list: the visible primitives in index order (every other primitive's MLP gradients are zero), so
-    // the MFMA tiles are full and the gathers nearly contiguous
+    // the MFMA tiles are full and the gathers nearly contiguous. A chunk's inputs are loaded during the chunk before
+    // it, and its primitive indices two chunks ahead, so no chunk waits on a load of its own.
     const uint32_t n_chunks = (a.n_visible + preprocess_block - 1) / preprocess_block;
+    struct ChunkInputs {
+        uint32_t p;
+        float4 dpre;      // upstream gradient of the activated colour (zero past the list)
+        float3 mean, gm, gb;  // the mean; the geometry kernel's mean and base gradients, which this chunk adds to
+        float feat[nn::FEATURES > 0 ? nn::FEATURES : 1], base[3];
+    };
+    // (chunks past the list read entry 0: the list is not empty when a chunk is processed)
+    const auto prim_of = [&](uint32_t chunk) {
+        const uint32_t v_idx = chunk * preprocess_block + threadIdx.x;
+        return a.visible_prims[v_idx < a.n_visible ? v_idx : 0u];
+    };
+    const auto load_inputs = [&](uint32_t chunk, uint32_t p, ChunkInputs& in) {
+        const bool contributes = chunk * preprocess_block + threadIdx.x < a.n_visible;
+        in.p = p;
+        in.dpre = contributes ? reinterpret_cast<const float4*>(a.color_grads)[p] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        in.mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
+        in.gm = EFGS_DIRECTION_GRADIENT ? make_float3(a.g_means[3 * p], a.g_means[3 * p + 1], a.g_means[3 * p + 2]) : make_float3(0.0f, 0.0f, 0.0f);
+        in.gb = EFGS_BASE_INPUT ? make_float3(a.g_base[3 * p], a.g_base[3 * p + 1], a.g_base[3 * p + 2]) : make_float3(0.0f, 0.0f, 0.0f);
+        const float* feat = a.residual + static_cast<size_t>(p) * residual_params;
+#pragma unroll
+        for (uint32_t i = 0; i < nn::FEATURES; i++) in.feat[i] = feat[i];
+#pragma unroll
+        for (uint32_t c = 0; c < 3; c++) in.base[c] = EFGS_BASE_INPUT ? a.base[3 * p + c] : 0.0f;
+    };
+    const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
+    ChunkInputs next_in;
+    uint32_t p_after = 0u;
+    if (blockIdx.x < n_chunks) {
+        load_inputs(blockIdx.x, prim_of(blockIdx.x), next_in);
+        p_after = prim_of(blockIdx.x + gridDim.x);
+    }
     for (uint32_t chunk = blockIdx.x; chunk < n_chunks; chunk += gridDim.x) {
+        const ChunkInputs in = next_in;  // (loaded during the previous chunk)
+        const uint32_t later = chunk + gridDim.x;
+        if (later < n_chunks) {
+            load_inputs(later, p_after, next_in);
+            p_after = prim_of(later + gridDim.x);
+        }
         const uint32_t v_idx = chunk * preprocess_block + threadIdx.x;
         const bool contributes = v_idx < a.n_visible;
         if (__ballot(contributes) == 0) continue;  // wave-uniform: the tail of the list
-        const uint32_t p = a.visible_prims[contributes ? v_idx : 0u];
-        const float4 dpre = contributes ? reinterpret_cast<const float4*>(a.color_grads)[p] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const float3 mean = make_float3(a.means[3 * p], a.means[3 * p + 1], a.means[3 * p + 2]);
-        // the geometry kernel's mean and base gradients, which this chunk adds to, loaded with its inputs (their
-        // stores then wait for no load of their own after the MLP)
-        float3 gm = make_float3(0.0f, 0.0f, 0.0f), gb = gm;
-        if (EFGS_DIRECTION_GRADIENT) gm = make_float3(a.g_means[3 * p], a.g_means[3 * p + 1], a.g_means[3 * p + 2]);
-        if (EFGS_BASE_INPUT) gb = make_float3(a.g_base[3 * p], a.g_base[3 * p + 1], a.g_base[3 * p + 2]);
-        const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
+        const uint32_t p = in.p;
         float norm_rcp;
-        const float3 d = view_direction(mean, cam, norm_rcp);
-        const float* feat = a.residual + static_cast<size_t>(p) * residual_params;
+        const float3 d = view_direction(in.mean, cam, norm_rcp);
         float x[nn::INP];
-        nn::mlp_input(feat, a.base + 3 * p, d, degree, x);
+        nn::mlp_input(in.feat, in.base, d, degree, x);
         if (!contributes) {
 #pragma unroll
             for (uint32_t k = 0; k < nn::INP; k++) x[k] = 0.0f;
         }
-        const float g[3] = {dpre.x, dpre.y, dpre.z};
+        const float g[3] = {in.dpre.x, in.dpre.y, in.dpre.z};
         float dx[nn::INP];
         nn::mlp_train(WL, stage, x, g, [](float y, float gy) { return gy * nn::residual_activation_slope<EFGS_RES_ACT>(y); }, s, inv_s, dx,
                       dW, lane);
         if (contributes) {
             float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
 #pragma unroll
-            for (uint32_t i = 0; i < nn::FEATURES; i++) gp[i] = nn::feature_grad(feat[i], dx, i);
+            for (uint32_t i = 0; i < nn::FEATURES; i++) gp[i] = nn::feature_grad(in.feat[i], dx, i);
             if (EFGS_BASE_INPUT) {
-                a.g_base[3 * p] = gb.x + nn::feature_grad(a.base[3 * p], dx, nn::FEATURES);
-                a.g_base[3 * p + 1] = gb.y + nn::feature_grad(a.base[3 * p + 1], dx, nn::FEATURES + 1);
-                a.g_base[3 * p + 2] = gb.z + nn::feature_grad(a.base[3 * p + 2], dx, nn::FEATURES + 2);
+                a.g_base[3 * p] = in.gb.x + nn::feature_grad(in.base[0], dx, nn::FEATURES);
+                a.g_base[3 * p + 1] = in.gb.y + nn::feature_grad(in.base[1], dx, nn::FEATURES + 1);
+                a.g_base[3 * p + 2] = in.gb.z + nn::feature_grad(in.base[2], dx, nn::FEATURES + 2);
             }
             if (EFGS_DIRECTION_GRADIENT) {
                 const float3 dm = direction_grad_to_mean(nn::direction_grad(d, degree, dx), d, norm_rcp);
-                a.g_means[3 * p] = gm.x + dm.x;
-                a.g_means[3 * p + 1] = gm.y + dm.y;
-                a.g_means[3 * p + 2] = gm.z + dm.z;
+                a.g_means[3 * p] = in.gm.x + dm.x;
+                a.g_means[3 * p + 1] = in.gm.y + dm.y;
+                a.g_means[3 * p + 2] = in.gm.z + dm.z;
             }
         }
     }
