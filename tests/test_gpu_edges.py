@@ -83,6 +83,47 @@ def test_long_tile_runs():
     check_image(image, fw, device_contributors(bufs, v, cam), 1e-4, 'long runs')
 
 
+def test_sort_beyond_24_bit_emission_indices():
+    # 60k large Gaussians at 4200x3000 (65,750 tiles, 32-bit tile keys, global-atomic binning): 19.3M instances, more
+    # than the 2^24 - 1 emission indices that the forward's packed sort keys hold, so runs of <= 256 are sorted with
+    # (depth, emission index) keys and their primitives gathered, beside the LDS-slab sorts of longer runs.
+    # Too large for the oracle's blend: checked by the properties that define the result. Emission: primitives in
+    # index order, each one's tiles ascending, as many as its count. Sorted arrays: the same (tile, primitive) pairs,
+    # grouped by the tile ranges, and within each tile strictly increasing in (depth key, primitive index).
+    scene, app, cam = small_case(model='precomputed', n=60000, width=4200, height=3000, scale_shift=1.5)
+    print('case sort beyond 24-bit emission indices: n=60000 4200x3000', flush=True)
+    _, frame, bufs = _render(scene, app, cam)
+    from efgs.rasterization import frame_views
+    v = frame_views(frame)
+    I, n = int(frame.n_instances), 60000
+    gw, gh = cam.grid()
+    T = gw * gh
+    assert frame.key_bytes == 4 and I >= (1 << 24)
+    inst_key = read_device(bufs, v.instance_keys, I, np.uint32).astype(np.int64)
+    inst_prim = read_device(bufs, v.instance_primitive, I, np.uint32).astype(np.int64)
+    n_touched = read_device(bufs, v.n_touched, n, np.uint32).astype(np.int64)
+    depth = read_device(bufs, v.depth_keys, n, np.uint32).astype(np.int64)
+    ranges = read_device(bufs, v.tile_ranges, 2 * T, np.uint32).reshape(-1, 2).astype(np.int64)
+    sorted_key = read_device(bufs, v.tile_sorted_keys, I, np.uint32).astype(np.int64)
+    sorted_inst = read_device(bufs, v.tile_sorted_instances, I, np.uint32).astype(np.int64)
+    # emission
+    assert np.all(np.diff(inst_prim) >= 0)
+    same = np.diff(inst_prim) == 0
+    assert np.all(np.diff(inst_key)[same] > 0)
+    np.testing.assert_array_equal(np.bincount(inst_prim, minlength=n), n_touched)
+    # ranges partition the instances in tile order; every tile's run sorted by (depth key, primitive)
+    runs = ranges[:, 1] - ranges[:, 0]
+    assert ranges[0, 0] == 0 and ranges[-1, 1] == I and np.all(ranges[1:, 0] == ranges[:-1, 1])
+    assert ((runs > 0) & (runs <= 256)).sum() > 1000 and (runs > 256).sum() > 1000
+    np.testing.assert_array_equal(sorted_key, np.repeat(np.arange(T), runs))
+    sorted_prim = inst_prim[sorted_inst]
+    np.testing.assert_array_equal(np.sort(sorted_key * n + sorted_prim), np.sort(inst_key * n + inst_prim))
+    d = depth[sorted_prim]
+    within = sorted_key[1:] == sorted_key[:-1]
+    increasing = (d[1:] > d[:-1]) | ((d[1:] == d[:-1]) & (sorted_prim[1:] > sorted_prim[:-1]))
+    assert np.all(increasing[within])
+
+
 def test_near_plane_straddle():
     scene, app, cam = small_case(model='sh', n=400, distance=2.0)  # camera inside the cube: many behind / near
     image, frame, _ = _render(scene, app, cam)
