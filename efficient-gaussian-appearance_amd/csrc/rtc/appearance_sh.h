@@ -47,24 +47,14 @@ __device__ inline float3 sh_residual(const float* coef, float3 d, uint32_t degre
     return make_float3(residual_activation<RES_ACT>(r), residual_activation<RES_ACT>(g), residual_activation<RES_ACT>(bl));
 }
 
-// writes dL/dcoef for the active bases and returns dL/dmean through the view direction
+// writes dL/dcoef for the active bases and returns dL/dmean through the view direction. Every coefficient is read
+// before the first gradient is written, so gcoef may be coef itself (the gradients replace the coefficients).
 template <int RES_ACT>
 __device__ inline float3 sh_residual_backward(const float* coef, float3 dpre, float* gcoef, float3 d, float norm_rcp, uint32_t degree) {
     if (degree == 0) return make_float3(0.0f, 0.0f, 0.0f);
     const float3 res = sh_residual<RES_ACT>(coef, d, degree);
     const float3 ds = make_float3(dpre.x * residual_activation_grad<RES_ACT>(res.x), dpre.y * residual_activation_grad<RES_ACT>(res.y),
                                   dpre.z * residual_activation_grad<RES_ACT>(res.z));
-    float b[15];
-    sh_rest_basis(d.x, d.y, d.z, degree, b);
-    const uint32_t nb = sh_bases_of_degree(degree);
-#pragma unroll
-    for (uint32_t i = 0; i < 15; i++) {
-        if (i < nb) {
-            gcoef[3 * i] = b[i] * ds.x;
-            gcoef[3 * i + 1] = b[i] * ds.y;
-            gcoef[3 * i + 2] = b[i] * ds.z;
-        }
-    }
     const float x = d.x, y = d.y, z = d.z;
     float gx[3], gy[3], gz[3];
 #pragma unroll
@@ -89,6 +79,17 @@ __device__ inline float3 sh_residual_backward(const float* coef, float3 dpre, fl
     }
     const float3 gd = make_float3(gx[0] * ds.x + gx[1] * ds.y + gx[2] * ds.z, gy[0] * ds.x + gy[1] * ds.y + gy[2] * ds.z,
                                   gz[0] * ds.x + gz[1] * ds.y + gz[2] * ds.z);
+    float b[15];
+    sh_rest_basis(d.x, d.y, d.z, degree, b);
+    const uint32_t nb = sh_bases_of_degree(degree);
+#pragma unroll
+    for (uint32_t i = 0; i < 15; i++) {
+        if (i < nb) {
+            gcoef[3 * i] = b[i] * ds.x;
+            gcoef[3 * i + 1] = b[i] * ds.y;
+            gcoef[3 * i + 2] = b[i] * ds.z;
+        }
+    }
     return direction_grad_to_mean(gd, d, norm_rcp);
 }
 

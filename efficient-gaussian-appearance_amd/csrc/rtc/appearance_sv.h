@@ -29,6 +29,8 @@ __device__ inline float3 sv_residual(const float* p, float3 d, uint32_t sites) {
     return make_float3(wr * r, wr * g, wr * b);
 }
 
+// writes dL/d(site parameters) of the active sites and returns dL/dmean through the view direction. A site's
+// parameters are read before its gradients are written, and no later step reads them, so gp may be p0 itself.
 template <int RES_ACT>
 __device__ inline float3 sv_residual_backward(const float* p0, float3 gc, float* gp, float3 d, float norm_rcp, uint32_t sites) {
     if (sites == 0) return make_float3(0.0f, 0.0f, 0.0f);

@@ -262,7 +262,6 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             d = view_direction(gi.mean, cam, norm_rcp);
         }
         const uint32_t rows = p0 < a.n ? min(preprocess_block, a.n - p0) : 0u;
-        float* gp = a.g_residual + static_cast<size_t>(p) * residual_params;
         for (uint32_t pass = 0; pass < n_passes; pass++) {
             const uint32_t u0 = pass * pass_units;
             const uint32_t nu = min(pass_units, static_cast<uint32_t>(EFGS_N_UNITS) - u0);
@@ -270,14 +269,20 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             stage_residual_rows<preprocess_block>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
             __syncthreads();
 #if EFGS_MODEL == 1 || EFGS_MODEL == 2
+            // (one pass: every coefficient / site of the row) the gradients replace the staged row in place (each
+            // parameter is read before its gradient is written) and leave with coalesced stores; the units past the
+            // active degree and the rows of primitives without instances get zeros
+            float* row = s_rows + threadIdx.x * row_ld;
             if (work) {
-                const float* row = s_rows + threadIdx.x * row_ld;
 #if EFGS_MODEL == 1
-                dmean_color = sh_residual_backward<EFGS_RES_ACT>(row, dpre, gp, d, norm_rcp, a.cam.degree);
+                dmean_color = sh_residual_backward<EFGS_RES_ACT>(row, dpre, row, d, norm_rcp, a.cam.degree);
 #else
-                dmean_color = sv_residual_backward<EFGS_RES_ACT>(row, dpre, gp, d, norm_rcp, a.cam.degree);
+                dmean_color = sv_residual_backward<EFGS_RES_ACT>(row, dpre, row, d, norm_rcp, a.cam.degree);
 #endif
             }
+            for (uint32_t i = work ? active_residual_params(a.cam.degree) : 0u; i < residual_params; i++) row[i] = 0.0f;
+            __syncthreads();
+            store_residual_rows<preprocess_block>(s_rows, p0, rows, 0u, residual_params, a.g_residual);
 #else
             // lobes: a lobe's parameters are read before its gradients are written, so the gradients replace the
             // staged row in place (zero for inactive lobes and for primitives without instances) and leave with
@@ -296,12 +301,9 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
 #endif
         }
         if (work) {
-#if EFGS_MODEL == 1 || EFGS_MODEL == 2
-            for (uint32_t i = active_residual_params(a.cam.degree); i < residual_params; i++) gp[i] = 0.0f;
-#endif
             geometry_backward(a, p, rec, gi, ig, dmean_color);
         } else if (active) {
-            zero_primitive(a, p, EFGS_MODEL == 1 || EFGS_MODEL == 2);
+            zero_primitive(a, p, false);  // (its residual gradients were stored as zeros with the block's rows)
         }
         return;
     }
