@@ -240,7 +240,8 @@ __device__ __forceinline__ uint32_t wave_max_bits(uint32_t v, OP op) {
 extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
     using namespace efgs;
 #if EFGS_MODEL != 0
-    if constexpr (staged_rows) {
+    if constexpr (BackwardRows::staged) {
+        constexpr uint32_t row_ld = BackwardRows::row_ld, pass_units = BackwardRows::pass_units, n_passes = BackwardRows::n_passes;
         __shared__ float s_rows[preprocess_block * row_ld];
         const uint32_t p0 = blockIdx.x * preprocess_block, p = p0 + threadIdx.x;
         const bool active = p < a.n;
@@ -266,7 +267,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             const uint32_t u0 = pass * pass_units;
             const uint32_t nu = min(pass_units, static_cast<uint32_t>(EFGS_N_UNITS) - u0);
             if (pass > 0) __syncthreads();  // every thread has read the previous pass's rows
-            stage_residual_rows<preprocess_block>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
+            stage_residual_rows<preprocess_block, row_ld>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
             __syncthreads();
 #if EFGS_MODEL == 1 || EFGS_MODEL == 2
             // (one pass: every coefficient / site of the row) the gradients replace the staged row in place (each
@@ -282,7 +283,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             }
             for (uint32_t i = work ? active_residual_params(a.cam.degree) : 0u; i < residual_params; i++) row[i] = 0.0f;
             __syncthreads();
-            store_residual_rows<preprocess_block>(s_rows, p0, rows, 0u, residual_params, a.g_residual);
+            store_residual_rows<preprocess_block, row_ld>(s_rows, p0, rows, 0u, residual_params, a.g_residual);
 #else
             // lobes: a lobe's parameters are read before its gradients are written, so the gradients replace the
             // staged row in place (zero for inactive lobes and for primitives without instances) and leave with
@@ -297,7 +298,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             }
             for (uint32_t i = na * params_per_unit; i < nu * params_per_unit; i++) row[i] = 0.0f;
             __syncthreads();
-            store_residual_rows<preprocess_block>(s_rows, p0, rows, u0 * params_per_unit, nu * params_per_unit, a.g_residual);
+            store_residual_rows<preprocess_block, row_ld>(s_rows, p0, rows, u0 * params_per_unit, nu * params_per_unit, a.g_residual);
 #endif
         }
         if (work) {

@@ -182,7 +182,8 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
 #if EFGS_MODEL >= 1 && EFGS_MODEL <= 4
     // the forward stages its rows only for the lobe models: SH and SV read each row once and keep more waves per
     // SIMD without the LDS
-    constexpr bool staged_forward = staged_rows && (EFGS_MODEL == 3 || EFGS_MODEL == 4);
+    constexpr bool staged_forward = ForwardRows::staged && (EFGS_MODEL == 3 || EFGS_MODEL == 4);
+    constexpr uint32_t row_ld = ForwardRows::row_ld, pass_units = ForwardRows::pass_units, n_passes = ForwardRows::n_passes;
     __shared__ float s_rows[staged_forward ? preprocess_block * row_ld : 1];
 #endif
 #if EFGS_MODEL == 5
@@ -288,7 +289,7 @@ extern "C" __global__ __launch_bounds__(256, 4) void EFGS_KERNEL_NAME(efgs::Prep
                 const uint32_t u0 = pass * pass_units;
                 const uint32_t nu = min(pass_units, static_cast<uint32_t>(EFGS_N_UNITS) - u0);
                 if (pass > 0) __syncthreads();  // every thread has read the previous pass's rows
-                stage_residual_rows<preprocess_block>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
+                stage_residual_rows<preprocess_block, row_ld>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
                 __syncthreads();
                 if (visible) {
                     const float* row = s_rows + threadIdx.x * row_ld;
