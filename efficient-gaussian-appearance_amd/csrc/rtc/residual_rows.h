@@ -11,8 +11,9 @@ constexpr uint32_t residual_params = EFGS_MODEL == 0 ? 0u : params_per_unit * EF
 // its neighbours', so direct per-thread reads spread every load instruction of a wave over 64 cache lines). Whole
 // units per pass: SH (coefficients) and SV (sites: the backward's softmax needs them all) in one pass, lobes in
 // passes of at most MAX_FLOATS floats; a layout that does not fit reads its rows directly. Fewer floats per pass
-// mean less LDS per block and more waves per SIMD, at one barrier and one staging round more per pass: the lobe
-// forward runs best at 18 (2 lobes per pass; NASG 149 -> 109 us, NASGabor 233 -> 151 us on 1M Gaussians against
+// mean less LDS per block and more waves per SIMD, at one barrier and one staging round more per pass (the SV
+// forward in passes of two sites, its softmax carried online, measured 105 -> 131 us: it stays unstaged): the lobe
+// forward runs best at 18 (2 lobes per pass; NASG 149 -> 119 us, NASGabor 233 -> 162 us on 1M Gaussians against
 // 40), the lobe backward, which also writes its gradients back through the rows, at 40 (24: 221 -> 310 us).
 template <uint32_t MAX_FLOATS>
 struct RowStaging {
