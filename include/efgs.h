@@ -337,7 +337,8 @@ enum {
     EFGS_STAGE_CREATE_INSTANCES = 3,   /* (tile, primitive) instances at their emission slots, per-tile counts */
     EFGS_STAGE_TILE_OFFSETS = 4,       /* scan of the per-tile counts: tile ranges */
     EFGS_STAGE_TILE_BUCKETS = 5,       /* instances into their tiles' ranges */
-    EFGS_STAGE_TILE_SORT = 6,          /* per-tile (depth, primitive) order */
+    EFGS_STAGE_TILE_SORT = 6,          /* the tiles' ranges and the blends' tile order (the per-tile (depth, primitive)
+                                          sort itself runs inside the forward blend, EFGS_STAGE_BLEND_FORWARD) */
     EFGS_STAGE_BLEND_FORWARD = 7,
     EFGS_STAGE_BLEND_BACKWARD = 8,
     EFGS_STAGE_PREPROCESS_BACKWARD = 9,
