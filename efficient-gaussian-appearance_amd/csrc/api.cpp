@@ -443,6 +443,9 @@ bool get_preprocess_kernel(efgs_rasterizer* r, int model, const char* kind, RtcK
 constexpr uint32_t neural_forward_blocks = 1024;
 constexpr uint32_t neural_backward_blocks = 512;
 
+// threads per block of the non-neural preprocess backward of `model` (the kernel's backward_block)
+uint32_t preprocess_backward_block(int model) { return model >= 1 && model <= 4 ? 128u : 256u; }
+
 // 0 (precomputed colours) when colours are supplied, else the configured model; -1 if none is configured
 int variant_of(const efgs_rasterizer* r, const efgs_primitives* prims) {
     if (prims->precomputed_colors != nullptr) return 0;
@@ -957,8 +960,9 @@ int efgs_backward(efgs_rasterizer* r, const efgs_primitives* prims, const efgs_s
     a.cam = camera_args(r, settings, variant, grid_w, grid_h);
     const uint32_t chunks = div_up(n, preprocess_block);
     if (variant != 5) {
+        const uint32_t bb = preprocess_backward_block(variant);
         t.begin(EFGS_STAGE_PREPROCESS_BACKWARD, s);
-        if (!launch_rtc(k, chunks, preprocess_block, 0u, &a, s)) return EFGS_ERR_HIP;
+        if (!launch_rtc(k, div_up(n, bb), bb, 0u, &a, s)) return EFGS_ERR_HIP;
         t.end(s);
         return EFGS_OK;
     }

@@ -237,13 +237,21 @@ __device__ __forceinline__ uint32_t wave_max_bits(uint32_t v, OP op) {
 
 #if EFGS_MODEL != 5
 
-extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
+namespace efgs {
+// Threads per block of the non-neural backward: 128 for the appearance models, whose rows are staged through LDS
+// (a CU holds whole blocks, so halving a block's LDS lets more of the CU's LDS hold rows: SV with 8 sites from 2 to
+// 2.5 waves per SIMD, NASG from 3 to 3.5; on the 1M c4 scene SV 192.5 -> 174.7 us, NASG 219.5 -> 212.4 us), 256 for
+// precomputed colours. The host launches the kernel with the same count (api.cpp, preprocess_backward_block).
+constexpr uint32_t backward_block = EFGS_MODEL >= 1 && EFGS_MODEL <= 4 ? 128u : 256u;
+}  // namespace efgs
+
+extern "C" __global__ __launch_bounds__(efgs::backward_block) void EFGS_KERNEL_NAME(efgs::PreprocessBackwardArgs a) {
     using namespace efgs;
 #if EFGS_MODEL != 0
     if constexpr (BackwardRows::staged) {
         constexpr uint32_t row_ld = BackwardRows::row_ld, pass_units = BackwardRows::pass_units, n_passes = BackwardRows::n_passes;
-        __shared__ float s_rows[preprocess_block * row_ld];
-        const uint32_t p0 = blockIdx.x * preprocess_block, p = p0 + threadIdx.x;
+        __shared__ float s_rows[backward_block * row_ld];
+        const uint32_t p0 = blockIdx.x * backward_block, p = p0 + threadIdx.x;
         const bool active = p < a.n;
         const uint32_t touched = active ? a.n_touched[p] : 0u;
         const uint32_t offset = active ? a.prim_offset[p] : 0u;
@@ -262,12 +270,12 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             const float3 cam = make_float3(a.cam.cam_position[0], a.cam.cam_position[1], a.cam.cam_position[2]);
             d = view_direction(gi.mean, cam, norm_rcp);
         }
-        const uint32_t rows = p0 < a.n ? min(preprocess_block, a.n - p0) : 0u;
+        const uint32_t rows = p0 < a.n ? min(backward_block, a.n - p0) : 0u;
         for (uint32_t pass = 0; pass < n_passes; pass++) {
             const uint32_t u0 = pass * pass_units;
             const uint32_t nu = min(pass_units, static_cast<uint32_t>(EFGS_N_UNITS) - u0);
             if (pass > 0) __syncthreads();  // every thread has read the previous pass's rows
-            stage_residual_rows<preprocess_block, row_ld>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
+            stage_residual_rows<backward_block, row_ld>(a.residual, p0, rows, u0 * params_per_unit, nu * params_per_unit, s_rows);
             __syncthreads();
 #if EFGS_MODEL == 1 || EFGS_MODEL == 2
             // (one pass: every coefficient / site of the row) the gradients replace the staged row in place (each
@@ -283,7 +291,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             }
             for (uint32_t i = work ? active_residual_params(a.cam.degree) : 0u; i < residual_params; i++) row[i] = 0.0f;
             __syncthreads();
-            store_residual_rows<preprocess_block, row_ld>(s_rows, p0, rows, 0u, residual_params, a.g_residual);
+            store_residual_rows<backward_block, row_ld>(s_rows, p0, rows, 0u, residual_params, a.g_residual);
 #else
             // lobes: a lobe's parameters are read before its gradients are written, so the gradients replace the
             // staged row in place (zero for inactive lobes and for primitives without instances) and leave with
@@ -298,7 +306,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
             }
             for (uint32_t i = na * params_per_unit; i < nu * params_per_unit; i++) row[i] = 0.0f;
             __syncthreads();
-            store_residual_rows<preprocess_block, row_ld>(s_rows, p0, rows, u0 * params_per_unit, nu * params_per_unit, a.g_residual);
+            store_residual_rows<backward_block, row_ld>(s_rows, p0, rows, u0 * params_per_unit, nu * params_per_unit, a.g_residual);
 #endif
         }
         if (work) {
@@ -309,7 +317,7 @@ extern "C" __global__ __launch_bounds__(256) void EFGS_KERNEL_NAME(efgs::Preproc
         return;
     }
 #endif
-    const uint32_t p = blockIdx.x * preprocess_block + threadIdx.x;
+    const uint32_t p = blockIdx.x * backward_block + threadIdx.x;
     if (p >= a.n) return;
     const uint32_t touched = a.n_touched[p];
     const uint32_t offset = a.prim_offset[p];
