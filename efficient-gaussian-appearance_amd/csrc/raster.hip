@@ -482,10 +482,11 @@ __global__ __launch_bounds__(1024) void tile_order_runs_kernel(uint32_t* order_r
 // scans the per-64-tile block sums into dynamic LDS (256 at a time with a running carry), one entry per 64-tile
 // block: up to max_scan_blocks of them (1,015,808 tiles); larger grids add the block sums per instance. A thread
 // takes bucket_per_thread instances (256 apart, so every load stays coalesced) and issues the loads of all of them
-// before their gathers and those before the stores: the kernel waits on memory, and a quarter of the waves then keep
-// four times the requests in flight each (and a quarter of the blocks repeat the block-sum scan).
+// before their gathers and those before the stores: the kernel waits on memory, and half the waves then keep twice
+// the requests in flight each (and half the blocks repeat the block-sum scan). Two per thread measured best on the
+// 1M-Gaussian 1080p step (bucket stage 21.3-22.2 us with four, 19.8 with two, 22.2 with eight).
 constexpr uint32_t max_scan_blocks = static_cast<uint32_t>((tile_hist_max_lds - 2048) / 4);
-constexpr uint32_t bucket_per_thread = 4;
+constexpr uint32_t bucket_per_thread = 2;
 constexpr uint32_t bucket_chunk = 256 * bucket_per_thread;  // instances per block
 template <typename KeyT>
 __global__ __launch_bounds__(256) void tile_buckets_kernel(const KeyT* keys, const uint32_t* inst_prim, const uint32_t* depth_keys,
