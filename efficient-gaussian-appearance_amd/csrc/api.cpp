@@ -440,7 +440,13 @@ bool get_preprocess_kernel(efgs_rasterizer* r, int model, const char* kind, RtcK
 }
 
 
-constexpr uint32_t neural_forward_blocks = 1024;
+// persistent grids of the neural kernels: the preprocess forward in 2,048 blocks, two per resident slot (four blocks
+// of 256 per CU): each block stages the MLP weights once and takes every 2,048th chunk, which balances the tail better
+// than one block per slot (61.1 -> 59.4 us on 1M Gaussians at 1080p, twice); the decode forward, whose blocks do
+// little besides the MLP, in 1,024; the backward in 512 blocks, one per slot of its two waves per SIMD, whose
+// weight-gradient partials are reduced after it
+constexpr uint32_t neural_forward_blocks = 2048;
+constexpr uint32_t decode_forward_blocks = 1024;
 constexpr uint32_t neural_backward_blocks = 512;
 
 // threads per block of the non-neural preprocess backward of `model` (the kernel's backward_block)
@@ -1170,7 +1176,7 @@ int efgs_neural_decode_forward(efgs_rasterizer* r, int64_t n, const float* featu
     NeuralDecodeArgs a = decode_args(n, features, base, dirs, mlp_weights, degree);
     a.out = out;
     const uint32_t chunks = div_up(static_cast<uint64_t>(n), preprocess_block);
-    const uint32_t blocks = chunks < neural_forward_blocks ? chunks : neural_forward_blocks;
+    const uint32_t blocks = chunks < decode_forward_blocks ? chunks : decode_forward_blocks;
     if (!launch_rtc(fwd, blocks, preprocess_block, mlp_smem_forward(mlp_shape(r)), &a, static_cast<hipStream_t>(stream))) return EFGS_ERR_HIP;
     return EFGS_OK;
 }
